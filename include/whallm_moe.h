@@ -1,0 +1,143 @@
+/* C interface of the MI355X (gfx950) MoE expert-path library, libwhallm_moe.so.
+ *
+ * Conventions (mirroring Native/QwenNative/capi.h:1-5 and capi.mm:20-37):
+ *  - every entry point returns int: 0 on success, 1 on an error whose message
+ *    wm_last_error() returns (per calling thread); nothing is launched when an
+ *    argument check fails;
+ *  - pointers are device pointers unless named host_*; sizes are element counts;
+ *  - `stream` is a hipStream_t (NULL = the default stream); work is enqueued,
+ *    not waited for. Outputs are caller-owned and valid once the stream reaches
+ *    them; inputs must stay valid until then;
+ *  - calls that share a workspace or a slot arena from more than one thread
+ *    at a time race: one thread per handle / workspace, as in the reference.
+ *
+ * Weight layout (HBM): each expert is the reference's Qwen blob regions
+ * (runtime/deepseek_v4_ssd/manifest.py:37-42): gate_up [2I, H/8] u32 words of
+ * eight E2M1 nibbles (value i = nibble i % 8, low first), gate_up scales
+ * [2I, H/32] E8M0 bytes, down [H, I/8] u32, down scales [H, I/32] u8.
+ * An expert table locates expert e's regions at base + slot(e) * stride, which
+ * covers both per-slot blobs (stride = blob size) and the region-major layer
+ * buffers of expert_layout.py:83-119 (stride = region size).
+ */
+#ifndef WHALLM_MOE_H
+#define WHALLM_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+#define WM_EXPORT __attribute__((visibility("default")))
+extern "C" {
+#else
+#define WM_EXPORT
+#endif
+
+/* MXFP4 expert set. gate rows first (Qwen, qwen4_exp.py:816-818) unless up_first
+ * (DeepSeek w13 = [w3; w1], expert_layout.py:43-51, model.py:516-523). */
+typedef struct wm_mxfp4_experts {
+  const void* gate_up;
+  const void* gate_up_scales;
+  const void* down;
+  const void* down_scales;
+  int64_t gate_up_stride;        /* bytes between consecutive slots */
+  int64_t gate_up_scales_stride;
+  int64_t down_stride;
+  int64_t down_scales_stride;
+  const int32_t* slots;          /* device map expert -> slot, or NULL for slot = expert */
+  int32_t experts;               /* routed experts addressable through `slots` */
+  int32_t hidden;                /* H: multiple of 32 */
+  int32_t inter;                 /* I: multiple of 32 */
+  int32_t up_first;
+  float swiglu_limit;            /* 0: plain SwiGLU; > 0: clamped (deepseek_v41/moe.py:30-43) */
+} wm_mxfp4_experts;
+
+/* FP8-E4M3 expert set with fp32 128x128 block scales (mimo/weights.py:17-43):
+ * w13 [2I, H] bytes (gate rows first unless up_first), scales [ceil(2I/128), ceil(H/128)];
+ * w2 [H, I] bytes, scales [ceil(H/128), ceil(I/128)]. I must be a multiple of 128. */
+typedef struct wm_fp8_experts {
+  const void* w13;
+  const void* w13_scales;
+  const void* w2;
+  const void* w2_scales;
+  int64_t w13_stride, w13_scales_stride, w2_stride, w2_scales_stride;
+  const int32_t* slots;
+  int32_t experts;
+  int32_t hidden;
+  int32_t inter;
+  int32_t up_first;
+  float swiglu_limit;
+} wm_fp8_experts;
+
+/* Message of the last failed call on this thread ("" when none). */
+WM_EXPORT const char* wm_last_error(void);
+/* Library version string; no device work. */
+WM_EXPORT const char* wm_version(void);
+
+/* ---- formats --------------------------------------------------------------
+ * out[r, i] = e2m1(nibble) * 2^(scale[r, i/32] - 127) as fp32 (bf16 when out_bf16);
+ * scale byte 0 -> 2^-127 (a denormal), 255 -> NaN (OCP MX). Replaces the reference's unpack_fp4 /
+ * dequant_fp4 / e8m0_to_float (deepseek_v41/dequant.py:33-68) and mx.dequantize. */
+WM_EXPORT int wm_dequant_mxfp4(const void* packed, const void* scales, int64_t rows, int64_t cols,
+                               void* out, int out_bf16, void* stream);
+/* out[r, c] = e4m3(w[r, c]) * scales[r/128, c/128] (fp32); decode_fp8_blocks
+ * (mimo/weights.py:17-43) without the bf16 rounding. */
+WM_EXPORT int wm_dequant_fp8_blocks(const void* weight, const float* scales, int64_t rows, int64_t cols,
+                                    float* out, void* stream);
+
+/* ---- routing --------------------------------------------------------------
+ * logits [T, E] fp32 -> indices [T, K] int32 (descending, ties -> lower index)
+ * and weights [T, K] fp32 = softmax over the kept logits (norm_topk_prob) or the
+ * full softmax probability; probabilities (nullable) receives the full softmax [T, E].
+ * SparseMoE.route/_gates (qwen4_exp.py:1009-1046), native host top-k
+ * (Native/QwenNative/engine.mm:2086-2100). E <= 1024, K <= 32. */
+WM_EXPORT int wm_route_softmax_topk(const float* logits, int32_t tokens, int32_t experts, int32_t k,
+                                    int32_t norm_topk_prob, int32_t* indices, float* weights, float* probabilities,
+                                    void* stream);
+/* DeepSeek routing: s = f(logits) (func 0 softmax, 1 sigmoid, 2 sqrt-softplus),
+ * select on s + bias (bias may be NULL), w = s[idx] / (sum + 1e-20) * route_scale.
+ * Gate.__call__ (deepseek_v41/moe.py:58-74), native route (Native/DeepSeekNative/engine.mm:1863-1889).
+ * n_groups > 1 adds DeepSeek-V3 group-limited selection (no reference counterpart). */
+WM_EXPORT int wm_route_scored(const float* logits, const float* bias, int32_t tokens, int32_t experts,
+                              int32_t k, int32_t func, float route_scale, int32_t norm_topk_prob,
+                              int32_t n_groups, int32_t topk_groups, int32_t* indices, float* weights,
+                              void* stream);
+/* logits[t, e] = x[t] . w[e] for bf16 x [T, H] and bf16 w [E, H], fp32 out: the
+ * router linear (SparseMoE.gate, qwen4_exp.py:1000; linear_bf16,
+ * Native/QwenNative/kernels.metal:18-67). */
+WM_EXPORT int wm_linear_bf16(const void* x, const void* w, int32_t tokens, int32_t hidden, int32_t outputs,
+                             float* out, void* stream);
+
+/* ---- permute --------------------------------------------------------------
+ * Stable sort of the T*K (token, k) pairs by expert (mlx-lm _gather_sort as used at
+ * qwen4_exp.py:865-868; native tile build Native/QwenNative/engine.mm:2104-2126).
+ * order[r] = pair of permuted row r, inverse[p] = row of pair p, offsets[E+1],
+ * tiles[n][2] = (expert, first row) of each tile_rows-row tile, tile_count[1].
+ * max tiles = ceil(T*K / tile_rows) + E. workspace: wm_permute_workspace_size bytes. */
+WM_EXPORT size_t wm_permute_workspace_size(int64_t pairs, int32_t experts);
+WM_EXPORT int wm_permute(const int32_t* indices, int64_t pairs, int32_t experts, int32_t tile_rows,
+                         int32_t* order, int32_t* inverse, int32_t* offsets, int32_t* tiles,
+                         int32_t* tile_count, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- MXFP4 expert FFN -----------------------------------------------------
+ * One MoE layer, Qwen form (SparseMoE.__call__, qwen4_exp.py:1015-1051):
+ *   y[t] = sum_k weights[t,k] * FFN_{indices[t,k]}(x[t]) + sigmoid(x[t] . shared_gate) * FFN_shared(x[t])
+ * x, y bf16 [T, H]; shared may be NULL (no shared term) and shared_gate NULL
+ * (ungated shared expert, the DeepSeek form, model.py:540-541).
+ * Decode path (fused dequant-GEMV) for T*K <= 256, MFMA grouped GEMM otherwise.
+ * workspace: wm_moe_mxfp4_workspace_size bytes. */
+WM_EXPORT size_t wm_moe_mxfp4_workspace_size(int32_t tokens, int32_t k, const wm_mxfp4_experts* experts);
+WM_EXPORT int wm_moe_mxfp4(const void* x, int32_t tokens, const int32_t* indices, const float* weights,
+                           int32_t k, const wm_mxfp4_experts* experts, const wm_mxfp4_experts* shared,
+                           const void* shared_gate, void* y, void* workspace, size_t workspace_bytes,
+                           void* stream);
+/* Per-pair expert outputs in router order, out bf16 [T, K, H]: the
+ * StreamingExperts.__call__ contract (qwen4_exp.py:853-904) and
+ * _StreamingSwitchGLU.__call__ (model.py:325-385). Same workspace size. */
+WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* indices, int32_t k,
+                               const wm_mxfp4_experts* experts, void* out, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,202 @@
+"""Weight formats of the expert path, restated in numpy (test oracle only).
+
+Pinning (how each function here is checked, see tests/test_oracle_formats.py):
+
+* ``quantize_mxfp4_bf16`` / ``quantize_mxfp4_fp8`` — the reference's four Swift
+  known-answer tests (Tests/DeepSeekRepackTests/DeepSeekRepackTests.swift:336-412),
+  bytes and SHA-256, plus the C restatement in ``oracle/c/oracle.c``.
+* ``e2m1_value`` / ``e8m0_value`` / ``dequant_mxfp4`` — closed form over all
+  16 codes x 256 scale bytes, and the round trip encode -> decode on exact values.
+* ``e4m3_value`` — all 256 bytes against torch.float8_e4m3fn (an independent
+  library decoder), NaN codes included.
+* ``dequant_fp8_blocks`` — closed form on hand-built blocks (crop at ragged
+  edges, NaN-code and bad-scale rejection).
+* ``bf16_round`` — against torch's float32 -> bfloat16 conversion.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# E2M1 magnitudes, code & 7 -> value; bit 3 is the sign.
+# deepseek_v41/dequant.py:29-30, Native/QwenNative/kernels.metal:140-144.
+E2M1_MAGNITUDES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float32)
+E2M1_VALUES = np.concatenate([E2M1_MAGNITUDES, -E2M1_MAGNITUDES]).astype(np.float32)
+
+GROUP = 32          # MXFP4: values per E8M0 scale (deepseek_v41/dequant.py:27)
+FP8_BLOCK = 128     # FP8 checkpoint: 128 x 128 blocks per fp32 scale (mimo/weights.py:27-41)
+
+
+def e2m1_value(codes: np.ndarray) -> np.ndarray:
+    """E2M1 nibble -> float32. Code 8 ("negative zero") decodes to -0.0, which
+    compares equal to +0.0 (deepseek_v41/dequant.py:29-30 maps it to +0.0; the
+    Metal table at Native/QwenNative/kernels.metal:701-702 gives -0.0)."""
+    return E2M1_VALUES[np.asarray(codes) & 15]
+
+
+def e8m0_value(scale_bytes: np.ndarray) -> np.ndarray:
+    """E8M0 byte b -> 2**(b-127) as float32 (deepseek_v41/dequant.py:33-36).
+
+    Edge bytes, fixed for this build: b == 0 is 2**-127 exactly (a float32
+    denormal: what dequant.py's fp32 ``power`` gives and what OCP MX defines;
+    the Metal bit trick at Native/QwenNative/kernels.metal:727 gives 0 instead),
+    and b == 255 is NaN (OCP MX; dequant.py's fp32 power would give inf). The
+    gfx950 scaled FP4 converts decode the same way, measured over all bytes.
+    """
+    b = np.asarray(scale_bytes).astype(np.int32)
+    out = np.ldexp(np.ones(b.shape, np.float32), b - 127).astype(np.float32)
+    return np.where(b == 255, np.float32(np.nan), out).astype(np.float32)
+
+
+def unpack_mxfp4_codes(packed: np.ndarray) -> np.ndarray:
+    """[O, K/8] uint32 (or [O, K/2] uint8) -> [O, K] codes; value i of a word is
+    nibble i % 8, low nibble first (deepseek_v41/dequant.py:53-60,
+    Native/QwenNative/kernels.metal:157-165)."""
+    b = np.ascontiguousarray(packed).view(np.uint8)
+    lo = b & 0x0F
+    hi = b >> 4
+    return np.stack([lo, hi], axis=-1).reshape(*b.shape[:-1], b.shape[-1] * 2)
+
+
+def pack_mxfp4_codes(codes: np.ndarray) -> np.ndarray:
+    """[O, K] codes -> [O, K/8] uint32 words (inverse of ``unpack_mxfp4_codes``)."""
+    c = np.asarray(codes, np.uint8)
+    pairs = c.reshape(*c.shape[:-1], c.shape[-1] // 2, 2)
+    bytes_ = (pairs[..., 0] & 15) | ((pairs[..., 1] & 15) << 4)
+    return np.ascontiguousarray(bytes_.astype(np.uint8)).view(np.uint32)
+
+
+def dequant_mxfp4(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """Packed E2M1 [O, K/8] u32 + E8M0 [O, K/32] u8 -> float32 [O, K].
+
+    w[o, i] = e2m1(nibble) * 2**(scale[o, i // 32] - 127), exact in fp32
+    (deepseek_v41/dequant.py:63-68, Native/QwenNative/kernels.metal:511-518).
+    """
+    codes = unpack_mxfp4_codes(packed)
+    values = e2m1_value(codes)
+    s = e8m0_value(np.asarray(scales, np.uint8))
+    return (values.reshape(*values.shape[:-1], -1, GROUP) * s[..., None]).reshape(values.shape)
+
+
+def e4m3_value(bytes_: np.ndarray) -> np.ndarray:
+    """FP8 E4M3FN byte -> float32 (Sources/DeepSeekRepack/MXFP4.swift:96-107).
+
+    exponent 0: sign * m * 2**-9; (exponent, mantissa) == (15, 7): NaN;
+    else sign * (1 + m/8) * 2**(e - 7).
+    """
+    b = np.asarray(bytes_, np.uint8).astype(np.int32)
+    sign = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0x0F
+    m = b & 0x07
+    sub = sign * m * 2.0 ** -9
+    norm = sign * (1.0 + m / 8.0) * np.exp2(e - 7.0)
+    out = np.where(e == 0, sub, norm)
+    out = np.where((e == 15) & (m == 7), np.nan, out)
+    return out.astype(np.float32)
+
+
+def dequant_fp8_blocks(weight: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """FP8 E4M3 [rows, cols] bytes + fp32 [ceil(rows/128), ceil(cols/128)] -> fp32.
+
+    Restates runtime/deepseek_v4_ssd/mimo/weights.py:17-43 with one source shard:
+    shape checks, reserved NaN codes rejected (:33-34), non-finite or negative
+    scales rejected (:35-36), each value times its block's scale, blocks cropped
+    at ragged edges (:41). The reference then rounds to bf16; the expert path
+    keeps fp32 (the MoE oracle's ``dequant-then-matmul`` is fp32).
+    """
+    w = np.asarray(weight)
+    s = np.asarray(scales)
+    if w.ndim != 2 or s.ndim != 2 or w.dtype != np.uint8:
+        raise ValueError("FP8 weights must be a 2-D uint8 tensor with 2-D scales")
+    if s.dtype != np.float32:
+        raise ValueError("FP8 block scales must be float32")
+    rows, cols = w.shape
+    if rows < 1 or cols < 1:
+        raise ValueError("FP8 tensor cannot be empty")
+    if s.shape != (-(-rows // FP8_BLOCK), -(-cols // FP8_BLOCK)):
+        raise ValueError("FP8 scale shape does not match 128x128 block padding")
+    if np.any((w & 127) == 127):
+        raise ValueError("FP8 checkpoint contains reserved NaN codes")
+    if np.any(~np.isfinite(s) | (s < 0)):
+        raise ValueError("FP8 checkpoint contains invalid block scales")
+    expanded = np.repeat(np.repeat(s, FP8_BLOCK, axis=0), FP8_BLOCK, axis=1)[:rows, :cols]
+    return (e4m3_value(w) * expanded).astype(np.float32)
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(values: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits by round-to-nearest-even of the bit pattern
+    (Sources/DeepSeekRepack/MXFP4.swift:109-113; NaN not special-cased, as there)."""
+    bits = np.ascontiguousarray(values, np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000
+    return (rounded >> 16).astype(np.uint16)
+
+
+def bf16_round_f32(values: np.ndarray) -> np.ndarray:
+    """float32 rounded to the nearest bf16, returned as float32."""
+    return bf16_bits_to_f32(bf16_round(values))
+
+
+def _fp4_code(values: np.ndarray) -> np.ndarray:
+    """Nearest E2M1 code with ties to the even index, sign from the sign bit
+    (Sources/DeepSeekRepack/MXFP4.swift:115-131). Magnitudes above 6 clamp to 6;
+    a NaN magnitude keeps code 0 (no candidate compares less)."""
+    v = np.asarray(values, np.float32)
+    negative = np.signbit(v)
+    magnitude = np.minimum(np.abs(v), np.float32(6.0))
+    selected = np.zeros(v.shape, np.uint8)
+    best = np.full(v.shape, np.inf, np.float32)
+    for index, candidate in enumerate(E2M1_MAGNITUDES):
+        d = np.abs(magnitude - candidate)
+        take = (d < best) | ((d == best) & (index % 2 == 0))
+        selected = np.where(take, np.uint8(index), selected)
+        best = np.where(take, d, best)
+    return selected | np.where(negative, np.uint8(8), np.uint8(0))
+
+
+def _quantize_groups(values: np.ndarray, rows: int, columns: int) -> tuple[np.ndarray, np.ndarray]:
+    """Shared tail of both Swift encoders (MXFP4.swift:22-37 and :68-85):
+    per 32-value group, scale exponent = exponent(max|v|) - 2 clamped to
+    [-127, 128]; an all-zero group keeps scale byte 0 and zero codes."""
+    g = values.reshape(rows, columns // GROUP, GROUP).astype(np.float32)
+    maximum = np.abs(g).max(axis=-1)
+    zero = maximum == 0
+    _, exp = np.frexp(np.where(zero, np.float32(1.0), maximum))
+    exponent = np.clip(exp.astype(np.int32) - 1 - 2, -127, 128)   # Float.exponent == frexp - 1
+    scales = np.where(zero, 0, exponent + 127).astype(np.uint8)
+    factor = np.ldexp(np.float32(1.0), -exponent).astype(np.float32)
+    codes = _fp4_code((g * factor[..., None]).astype(np.float32))
+    codes = np.where(zero[..., None], np.uint8(0), codes)
+    packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)
+    return packed.reshape(rows, columns // 2), scales
+
+
+def quantize_mxfp4_bf16(bf16_bits: np.ndarray, rows: int, columns: int) -> tuple[np.ndarray, np.ndarray]:
+    """BF16 [rows, columns] -> (MXFP4 bytes [rows, columns/2], E8M0 [rows, columns/32]).
+
+    Restates MXFP4.quantizeBF16 (Sources/DeepSeekRepack/MXFP4.swift:4-40).
+    """
+    if rows <= 0 or columns <= 0 or columns % GROUP or np.size(bf16_bits) != rows * columns:
+        raise ValueError("MXFP4 source must contain complete BF16 rows")
+    values = bf16_bits_to_f32(np.asarray(bf16_bits, np.uint16).reshape(rows, columns))
+    return _quantize_groups(values, rows, columns)
+
+
+def quantize_mxfp4_fp8(fp8: np.ndarray, inverse_scales_bf16: np.ndarray,
+                       rows: int, columns: int) -> tuple[np.ndarray, np.ndarray]:
+    """FP8 E4M3 [rows, columns] with BF16 128x128 inverse scales -> MXFP4.
+
+    Restates MXFP4.quantizeFP8 (Sources/DeepSeekRepack/MXFP4.swift:42-88): each
+    value is e4m3 * scale rounded to bf16 (:66), then encoded as quantizeBF16.
+    """
+    if (rows <= 0 or columns <= 0 or rows % FP8_BLOCK or columns % FP8_BLOCK
+            or np.size(fp8) != rows * columns
+            or np.size(inverse_scales_bf16) != (rows // FP8_BLOCK) * (columns // FP8_BLOCK)):
+        raise ValueError("MXFP4 FP8 source must contain complete 128 by 128 scale blocks")
+    w = e4m3_value(np.asarray(fp8, np.uint8).reshape(rows, columns))
+    s = bf16_bits_to_f32(np.asarray(inverse_scales_bf16, np.uint16).reshape(rows // FP8_BLOCK, columns // FP8_BLOCK))
+    s = np.repeat(np.repeat(s, FP8_BLOCK, axis=0), FP8_BLOCK, axis=1)
+    values = bf16_round_f32((w * s).astype(np.float32))
+    return _quantize_groups(values, rows, columns)

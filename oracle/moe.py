@@ -1,0 +1,382 @@
+"""MoE expert-path arithmetic restated in numpy (test oracle only; see oracle/__init__.py).
+
+Pinning (tests/test_oracle_moe.py):
+
+* ``route_softmax_topk`` — brute-force sort on tiny inputs; the reference's tie
+  KAT (runtime/tests/test_runtime.py:2680-2683); softmax-over-kept equals
+  renormalised full softmax (the two forms in qwen4_exp.py:1038-1042 and
+  Native/QwenNative/engine.mm:2091-2096).
+* ``route_scored`` (DeepSeek sqrt-softplus / sigmoid / softmax with bias-select)
+  — closed form on hand-built rows; bias selects but does not weight.
+  Group-limited selection (n_groups > 1) has no reference implementation:
+  PARITY UNPINNED against the reference; pinned only by brute force over all
+  group subsets on tiny E.
+* ``permute`` — invariants of Scripts/diagnose_qwen_grouped_experts.py:34-40
+  (permutation, stable per-expert token order, inverse round trip) and the
+  wave/pair tests of runtime/tests/portable/test_qwen_flash_portable.py:32-92.
+* ``expert_ffn`` / ``moe_layer`` — constant-valued MXFP4 experts with a closed
+  form (the reference's own test shape, runtime/tests/test_runtime.py:2507-2745),
+  and a float64 per-pair loop on small shapes.
+* ``verify_greedy`` / ``verify_rejection`` — the reference's distribution test
+  (runtime/tests/test_native_qwen.py:71-87) and hand cases.
+* ``SlotArena`` — state-machine cases read off Native/QwenNative/engine.mm:679-778.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .formats import dequant_mxfp4, dequant_fp8_blocks, bf16_round_f32
+
+
+# ----------------------------------------------------------------------------- routing
+
+def topk_desc(scores: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest values per row, descending, ties -> lower index.
+
+    The reference has no single rule: the Qwen native engine partial-sorts fp32
+    logits (Native/QwenNative/engine.mm:2086-2090), MLX uses an unordered
+    argpartition (qwen4_exp.py:1012), DeepSeek breaks ties toward the lower
+    index (Native/DeepSeekNative/engine.mm:1881, model.py:590-602). This build
+    fixes: value descending, ties to the lower index.
+    """
+    s = np.asarray(scores, np.float32)
+    if np.isnan(s).any():
+        raise ValueError("router scores contain NaN")
+    order = np.argsort(-s, axis=-1, kind="stable")
+    return order[..., :k].astype(np.int32)
+
+
+def route_softmax_topk(logits: np.ndarray, k: int, norm_topk_prob: bool = True):
+    """Qwen router: p = softmax(l); idx = topk(p, k); w = p[idx] (/ sum if norm).
+
+    SparseMoE.route/_gates (qwen4_exp.py:1009-1046); the native engine's form
+    exp(l_k - l_max) / sum_kept (Native/QwenNative/engine.mm:2091-2096) is the
+    same quantity. Top-k is taken on the fp32 logits (monotone in p). Returns
+    (indices int32 [T, k], weights float32 [T, k]); weights computed in float64.
+    """
+    l = np.asarray(logits, np.float32)
+    idx = topk_desc(l, k)
+    ld = l.astype(np.float64)
+    top = ld.max(axis=-1, keepdims=True)
+    e = np.exp(ld - top)
+    kept = np.take_along_axis(e, idx, axis=-1)
+    if norm_topk_prob:
+        w = kept / kept.sum(axis=-1, keepdims=True)
+    else:
+        w = kept / e.sum(axis=-1, keepdims=True)
+    return idx, w.astype(np.float32)
+
+
+def score_function(logits: np.ndarray, func: str) -> np.ndarray:
+    """DeepSeek gate scores (deepseek_v41/moe.py:61-67; native sqrt-softplus at
+    Native/DeepSeekNative/engine.mm:1875-1876), float64."""
+    l = np.asarray(logits, np.float64)
+    if func == "softmax":
+        e = np.exp(l - l.max(axis=-1, keepdims=True))
+        return e / e.sum(axis=-1, keepdims=True)
+    if func == "sigmoid":
+        return 1.0 / (1.0 + np.exp(-l))
+    if func == "sqrtsoftplus":
+        return np.sqrt(np.maximum(l, 0.0) + np.log1p(np.exp(-np.abs(l))))
+    raise ValueError(f"unknown score function {func!r}")
+
+
+def route_scored(logits: np.ndarray, bias: np.ndarray | None, k: int, func: str = "sigmoid",
+                 route_scale: float = 1.0, norm_topk_prob: bool = True,
+                 n_groups: int = 1, topk_groups: int = 1):
+    """DeepSeek-style routing: the bias picks the experts but does not weight them.
+
+    Gate.__call__ (deepseek_v41/moe.py:58-74): s = f(l); selection on s + bias;
+    w = s[idx] / (sum + 1e-20) * route_scale. With n_groups > 1, the DeepSeek-V3
+    group-limited rule (not in the reference): a group's score is the sum of
+    its two largest biased scores, the topk_groups best groups are kept, and
+    top-k runs over their experts. Ties go to the lower index (group or expert).
+    """
+    s = score_function(logits, func)
+    biased = s + (0.0 if bias is None else np.asarray(bias, np.float64))
+    biased32 = biased.astype(np.float32)
+    T, E = biased32.shape
+    if n_groups > 1:
+        if E % n_groups:
+            raise ValueError("experts must divide into groups")
+        g = biased32.reshape(T, n_groups, E // n_groups)
+        two = -np.sort(-g, axis=-1)[..., :2]
+        group_scores = (two[..., 0].astype(np.float32) + two[..., 1].astype(np.float32)).astype(np.float32)
+        keep = topk_desc(group_scores, topk_groups)
+        mask = np.ones((T, n_groups), bool)
+        np.put_along_axis(mask, keep, False, axis=-1)
+        biased32 = np.where(np.repeat(mask, E // n_groups, axis=-1), np.float32(-np.inf), biased32)
+    idx = topk_desc(biased32, k)
+    w = np.take_along_axis(s, idx, axis=-1)
+    if norm_topk_prob and k > 1:
+        w = w / (w.sum(axis=-1, keepdims=True) + 1e-20)
+    return idx, (w * route_scale).astype(np.float32)
+
+
+# ----------------------------------------------------------------------------- permute
+
+@dataclass
+class Permutation:
+    order: np.ndarray      # [P] pair index t*K+k at each permuted row
+    inverse: np.ndarray    # [P] permuted row of each pair
+    offsets: np.ndarray    # [E+1] first permuted row of each expert
+    tiles: np.ndarray      # [n_tiles, 2] (expert, first permuted row) of each row tile
+
+
+def permute(indices: np.ndarray, experts: int, tile_rows: int = 128) -> Permutation:
+    """Stable sort of the flattened (token, k) pairs by expert.
+
+    mlx-lm _gather_sort as restated at Scripts/diagnose_qwen_grouped_experts.py:34-40
+    (order = argsort(flat), inverse = argsort(order)) with the stability of the
+    native tile build (std::stable_sort, Native/QwenNative/engine.mm:2104-2126);
+    per-expert row tiles of ``tile_rows`` as the native 16-row tiles
+    (:2111-2122), described by (expert, first row) instead of padded row lists.
+    """
+    flat = np.asarray(indices).reshape(-1)
+    if flat.size and (flat.min() < 0 or flat.max() >= experts):
+        raise ValueError("expert ID is outside the model")
+    order = np.argsort(flat, kind="stable").astype(np.int32)
+    inverse = np.empty_like(order)
+    inverse[order] = np.arange(order.size, dtype=np.int32)
+    counts = np.bincount(flat, minlength=experts).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    tiles = [(e, offsets[e] + r) for e in range(experts) for r in range(0, counts[e], tile_rows)]
+    return Permutation(order, inverse, offsets, np.array(tiles, np.int32).reshape(-1, 2))
+
+
+# ----------------------------------------------------------------------------- expert FFN
+
+def silu(x: np.ndarray) -> np.ndarray:
+    return x / (1.0 + np.exp(-x))
+
+
+@dataclass
+class MXFP4Expert:
+    """One expert in the reference's Qwen blob regions (manifest.py:37-42):
+    gate_up [2I, H/8] u32 + [2I, H/32] u8 with gate rows 0..I-1 and up rows
+    I..2I-1 (qwen4_exp.py:816-818), down [H, I/8] u32 + [H, I/32] u8."""
+    gate_up: np.ndarray
+    gate_up_scales: np.ndarray
+    down: np.ndarray
+    down_scales: np.ndarray
+
+
+def expert_ffn(x: np.ndarray, e: MXFP4Expert, limit: float = 0.0, up_first: bool = False) -> np.ndarray:
+    """fp32 dequant-then-matmul expert: silu(x Wg^T) * (x Wu^T) then @ Wd^T.
+
+    StreamingExperts._one (qwen4_exp.py:815-818). With ``up_first`` the fused
+    projection is DeepSeek's w13 = [w3 (up); w1 (gate)] (model.py:516-523,
+    expert_layout.py:43-51). ``limit`` > 0 is the clamped SwiGLU
+    (deepseek_v41/moe.py:30-43): up clamped to +-limit, gate clamped above.
+    """
+    wgu = dequant_mxfp4(e.gate_up, e.gate_up_scales)
+    wd = dequant_mxfp4(e.down, e.down_scales)
+    return ffn_dense(np.asarray(x, np.float32), wgu, wd, limit, up_first)
+
+
+def ffn_dense(x: np.ndarray, wgu: np.ndarray, wd: np.ndarray, limit: float = 0.0,
+              up_first: bool = False) -> np.ndarray:
+    I = wgu.shape[0] // 2
+    proj = x.astype(np.float32) @ wgu.T
+    if up_first:
+        up, gate = proj[..., :I], proj[..., I:]
+    else:
+        gate, up = proj[..., :I], proj[..., I:]
+    if limit > 0:
+        up = np.clip(up, -limit, limit)
+        gate = np.minimum(gate, limit)
+    return (silu(gate) * up).astype(np.float32) @ wd.T
+
+
+@dataclass
+class FP8Expert:
+    """DeepSeek-style FP8 expert: w1 (gate) / w3 (up) [I, H] and w2 [H, I]
+    E4M3 bytes with fp32 128x128 block scales (mimo/weights.py:17-43)."""
+    w1: np.ndarray
+    w1_scales: np.ndarray
+    w3: np.ndarray
+    w3_scales: np.ndarray
+    w2: np.ndarray
+    w2_scales: np.ndarray
+
+
+def fp8_expert_ffn(x: np.ndarray, e: FP8Expert, limit: float = 0.0) -> np.ndarray:
+    """SharedExpert / routed expert of deepseek_v41/moe.py:77-93 in fp32."""
+    w1 = dequant_fp8_blocks(e.w1, e.w1_scales)
+    w3 = dequant_fp8_blocks(e.w3, e.w3_scales)
+    w2 = dequant_fp8_blocks(e.w2, e.w2_scales)
+    return ffn_dense(x, np.concatenate([w1, w3], axis=0), w2, limit, up_first=False)
+
+
+def routed_outputs(x: np.ndarray, indices: np.ndarray, experts, ffn=expert_ffn, **kw) -> np.ndarray:
+    """StreamingExperts.__call__ contract (qwen4_exp.py:853-904): per-pair expert
+    outputs [T, K, H] in router order, grouped by expert for the math
+    (the grouped/ungrouped equivalence of runtime/tests/test_qwen_grouped_experts.py:23-45)."""
+    x = np.asarray(x, np.float32).reshape(-1, x.shape[-1])
+    idx = np.asarray(indices).reshape(x.shape[0], -1)
+    T, K = idx.shape
+    flat = idx.reshape(-1)
+    out = None
+    for expert in np.unique(flat):
+        positions = np.flatnonzero(flat == expert)
+        y = ffn(x[positions // K], experts[int(expert)], **kw)
+        if out is None:
+            out = np.zeros((T * K, y.shape[-1]), np.float32)
+        out[positions] = y
+    if out is None:
+        return np.zeros((T, K, x.shape[-1]), np.float32)
+    return out.reshape(T, K, -1)
+
+
+def combine(routed: np.ndarray, weights: np.ndarray, shared: np.ndarray | None = None,
+            shared_gate: np.ndarray | None = None) -> np.ndarray:
+    """y[t] = sum_k w[t,k] * routed[t,k] + sigmoid(g[t]) * shared[t].
+
+    SparseMoE._combine (qwen4_exp.py:1048-1051) with the shared term of
+    _gates (:1045); moe_combine (Native/QwenNative/kernels.metal:185-194).
+    ``shared_gate`` None means an ungated shared expert (DeepSeek, model.py:540-541).
+    Accumulated in float64, returned float32.
+    """
+    y = (np.asarray(routed, np.float64) * np.asarray(weights, np.float64)[..., None]).sum(axis=-2)
+    if shared is not None:
+        s = np.asarray(shared, np.float64)
+        if shared_gate is not None:
+            s = s / (1.0 + np.exp(-np.asarray(shared_gate, np.float64).reshape(-1, 1)))
+        y = y + s
+    return y.astype(np.float32)
+
+
+def moe_layer(x: np.ndarray, logits: np.ndarray, experts, k: int, shared=None,
+              shared_gate_weight: np.ndarray | None = None, norm_topk_prob: bool = True):
+    """Whole Qwen-style MoE layer: route, routed experts, gated shared expert, combine.
+
+    SparseMoE.__call__ (qwen4_exp.py:1015-1018). ``x`` is the bf16 input as
+    float32 [T, H]; ``logits`` fp32 [T, E]; ``shared_gate_weight`` bf16 [H] as
+    float32 (shared_expert_gate, :1003). Returns (y [T, H] f32, indices, weights).
+    """
+    idx, w = route_softmax_topk(logits, k, norm_topk_prob)
+    routed = routed_outputs(x, idx, experts)
+    sh = sg = None
+    if shared is not None:
+        sh = expert_ffn(np.asarray(x, np.float32), shared)
+        if shared_gate_weight is not None:
+            sg = np.asarray(x, np.float64) @ np.asarray(shared_gate_weight, np.float64)
+    return combine(routed, w, sh, sg), idx, w
+
+
+def rms_norm(r: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """Unit-weight RMSNorm, rounded to bf16: the pre-norm glue between MoE layers
+    of the decode stack (a decoder layer's post-attention norm with the
+    attention half removed)."""
+    r = np.asarray(r, np.float64)
+    inv = 1.0 / np.sqrt((r * r).mean(axis=-1, keepdims=True) + eps)
+    return bf16_round_f32((r * inv).astype(np.float32))
+
+
+# ----------------------------------------------------------------------------- MTP acceptance
+
+def verify_greedy(drafts: np.ndarray, target_logits: np.ndarray) -> tuple[int, int]:
+    """Greedy acceptance (native_qwen.py:395-400, dspark.py:862-873): accept
+    drafts while each equals the argmax of its target row; return (accepted,
+    next token). argmax ties go to the lower index (np.argmax)."""
+    t = np.asarray(target_logits, np.float32)
+    for index, token in enumerate(np.asarray(drafts).reshape(-1)):
+        target = int(np.argmax(t[index]))
+        if int(token) != target:
+            return index, target
+    return len(drafts), int(np.argmax(t[len(drafts)]))
+
+
+def verify_rejection(drafts, draft_logp: np.ndarray, target_logp: np.ndarray,
+                     uniforms: np.ndarray, residual_pick) -> tuple[int, int]:
+    """Rejection acceptance (native_qwen.py:401-408, dspark.py:875-898):
+    accept draft i when u_i <= min(1, exp(t[tok] - d[tok])); on reject, sample
+    from the residual max(p - q, 0) (``residual_pick(probs)`` draws). With all
+    drafts accepted the bonus token comes from the last target row."""
+    for index, token in enumerate(drafts):
+        accept = min(1.0, float(np.exp(target_logp[index][token] - draft_logp[index][token])))
+        if uniforms[index] > accept:
+            residual = np.maximum(np.exp(target_logp[index]) - np.exp(draft_logp[index]), 0)
+            total = residual.sum()
+            if total > 0:
+                return index, int(residual_pick(residual / total))
+            return index, int(residual_pick(np.exp(target_logp[index])))
+    return len(drafts), int(residual_pick(np.exp(target_logp[len(drafts)])))
+
+
+# ----------------------------------------------------------------------------- slot cache policy
+
+@dataclass
+class SlotArena:
+    """The native expert arena's replacement policy (Native/QwenNative/engine.mm:649-778).
+
+    LFU: the victim is the least-used slot, oldest stamp among equals, never a
+    slot handed out in the current plan (stamp == clock). Use counts halve
+    (floor 1) every max(8 * slots, 64) touches. Free slots fill in order.
+    """
+    slots: int
+    experts_per_layer: int
+    owner: list = field(default_factory=list)
+    stamp: list = field(default_factory=list)
+    uses: list = field(default_factory=list)
+    where: dict = field(default_factory=dict)
+    used: int = 0
+    clock: int = 0
+    touches: int = 0
+    hits: int = 0
+    misses: int = 0
+
+    def __post_init__(self):
+        self.owner = [-1] * self.slots
+        self.stamp = [0] * self.slots
+        self.uses = [0] * self.slots
+
+    def _victim(self) -> int:
+        if self.used < self.slots:
+            self.used += 1
+            return self.used - 1
+        best = -1
+        for s in range(self.slots):
+            if self.stamp[s] == self.clock:
+                continue
+            if (best < 0 or self.uses[s] < self.uses[best]
+                    or (self.uses[s] == self.uses[best] and self.stamp[s] < self.stamp[best])):
+                best = s
+        if best < 0:
+            raise RuntimeError("the expert cache is too small for one step")
+        return best
+
+    def _touch(self):
+        self.touches += 1
+        if self.touches < max(self.slots * 8, 64):
+            return
+        self.touches = 0
+        self.uses = [max(1, u // 2) for u in self.uses]
+
+    def plan(self, layer: int, experts: list[int]):
+        """(slots, missing[(expert, slot)]) as ExpertArena::plan (:679-707)."""
+        self.clock += 1
+        slots, missing = [], []
+        for expert in experts:
+            key = layer * self.experts_per_layer + expert
+            self._touch()
+            if key in self.where:
+                s = self.where[key]
+                self.stamp[s] = self.clock
+                self.uses[s] += 1
+                self.hits += 1
+                slots.append(s)
+                continue
+            s = self._victim()
+            if self.owner[s] >= 0:
+                del self.where[self.owner[s]]
+            self.owner[s] = key
+            self.where[key] = s
+            self.stamp[s] = self.clock
+            self.uses[s] = 1
+            slots.append(s)
+            missing.append((expert, s))
+            self.misses += 1
+        return slots, missing

@@ -1,0 +1,49 @@
+"""The C-ABI library loads and exports what include/*.h declares (CPU: no kernel launches)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from whallm_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = header.read_text()
+        names.update(re.findall(r"WM_EXPORT\s+[\w\s\*]+?\b(wm_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert "wm_moe_mxfp4" in names and "wm_permute" in names and len(names) >= 10
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert missing == []
+
+
+def test_binding_covers_every_declared_symbol():
+    assert set(declared_symbols()) <= set(_lib.exported_symbols())
+
+
+def test_version_and_argument_checks_fail_before_any_launch():
+    lib = _lib.load()
+    assert b"gfx950" in lib.wm_version()
+    with pytest.raises(_lib.WhallmError, match="experts must be in"):
+        _lib.call("wm_route_softmax_topk", None, 1, 0, 1, 1, None, None, None, None)
+    with pytest.raises(_lib.WhallmError, match="k must be"):
+        _lib.call("wm_route_softmax_topk", None, 1, 8, 9, 1, None, None, None, None)
+    with pytest.raises(_lib.WhallmError, match="workspace too small"):
+        _lib.call("wm_permute", None, 10, 4, 16, None, None, None, None, None, None, 0, None)
+    table = _lib.MXFP4ExpertsC()
+    with pytest.raises(_lib.WhallmError, match="expert region pointer is null"):
+        _lib.call("wm_moe_mxfp4", None, 1, None, None, 2, ctypes.byref(table), None, None, None, None, 0, None)
+    # The error message is per thread and clears on the next good call.
+    assert lib.wm_last_error() != b""

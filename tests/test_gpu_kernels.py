@@ -1,0 +1,153 @@
+"""GPU parity of the format, routing and permute kernels against the oracle.
+
+Bar: bit-exact for dequantised weights, top-k indices and permutation lists;
+routing weights (fp32 transcendental math) within 2e-6 relative.
+"""
+import numpy as np
+import pytest
+import torch
+
+import whallm_amd as wa
+from oracle import formats as F
+from oracle import moe as M
+from whallm_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+# ----------------------------------------------------------------------------- formats
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_dequant_mxfp4_every_code_and_scale_bit_exact(device, out_dtype):
+    # 256 rows (one per scale byte) x 64 values: every code appears at every scale.
+    rng = np.random.default_rng(0)
+    codes = np.tile(np.arange(16, dtype=np.uint8), 4)
+    packed = np.stack([F.pack_mxfp4_codes(rng.permutation(codes)) for _ in range(256)])   # [256, 8] u32
+    scales = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 2, axis=1)               # [256, 2]
+    want = F.dequant_mxfp4(packed, scales)
+    got = wa.dequant_mxfp4(torch.from_numpy(packed.view(np.int32)).to(device), torch.from_numpy(scales).to(device),
+                           out_dtype)
+    got = _np(got.float())
+    if out_dtype == torch.bfloat16:
+        want = F.bf16_round_f32(want)  # exact: every decoded value is a bf16
+        want = np.where(np.isnan(F.dequant_mxfp4(packed, scales)), np.nan, want)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+
+
+def test_dequant_mxfp4_baseline_distribution(device):
+    rng = np.random.default_rng(1)
+    a = S.mxfp4_experts_np(rng, 2, 2048, 512)
+    for name, sname in (("gate_up", "gate_up_scales"), ("down", "down_scales")):
+        p, s = a[name].reshape(-1, a[name].shape[-1]), a[sname].reshape(-1, a[sname].shape[-1])
+        got = wa.dequant_mxfp4(torch.from_numpy(p.view(np.int32)).to(device), torch.from_numpy(s).to(device))
+        np.testing.assert_array_equal(_np(got), F.dequant_mxfp4(p, s))
+
+
+def test_dequant_fp8_blocks_bit_exact_with_ragged_edges(device):
+    rng = np.random.default_rng(2)
+    w = rng.integers(0, 256, size=(300, 200)).astype(np.uint8)
+    w = np.where((w & 0x7F) == 0x7F, w ^ 1, w).astype(np.uint8)
+    s = (rng.random((3, 2)) * 2).astype(np.float32)
+    got = wa.dequant_fp8_blocks(torch.from_numpy(w).to(device), torch.from_numpy(s).to(device))
+    np.testing.assert_array_equal(_np(got), F.dequant_fp8_blocks(w, s))
+
+
+# ----------------------------------------------------------------------------- routing
+
+@pytest.mark.parametrize("tokens,experts,k", [(16, 64, 4), (1, 512, 10), (333, 512, 10), (64, 1000, 32), (5, 7, 7)])
+def test_route_softmax_topk_indices_exact(device, tokens, experts, k):
+    rng = np.random.default_rng(tokens + experts)
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    logits[:, ::5] = np.round(logits[:, ::5])            # plant exact ties
+    for norm in (True, False):
+        idx, w, probs = wa.route_softmax_topk(torch.from_numpy(logits).to(device), k, norm, probabilities=True)
+        want_idx, want_w = M.route_softmax_topk(logits, k, norm)
+        np.testing.assert_array_equal(_np(idx), want_idx)
+        np.testing.assert_allclose(_np(w), want_w, rtol=2e-6, atol=1e-7)
+        p = np.exp(logits.astype(np.float64) - logits.max(-1, keepdims=True))
+        np.testing.assert_allclose(_np(probs), p / p.sum(-1, keepdims=True), rtol=2e-6, atol=1e-8)
+
+
+def test_route_softmax_c1_router_linear(device):
+    # C1: router weight bf16 N(0, 0.02) [64, 1024], x bf16 N(0, 1) [16, 1024], seed 0.
+    rng = np.random.default_rng(0)
+    x_bits = S.bf16_normal_np(rng, (16, 1024))
+    wr_bits = S.bf16_normal_np(rng, (64, 1024), 0.02)
+    x = S.bf16_bits_to_tensor(x_bits, device)
+    wr = S.bf16_bits_to_tensor(wr_bits, device)
+    logits = wa.linear_bf16(x, wr)
+    want = S.bf16_bits_to_f32(x_bits).astype(np.float64) @ S.bf16_bits_to_f32(wr_bits).astype(np.float64).T
+    np.testing.assert_allclose(_np(logits), want, rtol=1e-5, atol=1e-5)
+    idx, w = wa.route_softmax_topk(logits, 4)
+    want_idx, want_w = M.route_softmax_topk(_np(logits), 4)
+    np.testing.assert_array_equal(_np(idx), want_idx)
+    np.testing.assert_allclose(_np(w), want_w, rtol=2e-6)
+
+
+def _scored_case(rng, tokens, experts, func, groups, topk_groups, k):
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    bias = (rng.standard_normal(experts) * 0.05).astype(np.float32)
+    return logits, bias
+
+
+@pytest.mark.parametrize("func,groups,topk_groups,k,experts",
+                         [("sigmoid", 8, 4, 8, 256), ("sigmoid", 1, 1, 8, 256), ("sqrtsoftplus", 1, 1, 6, 384),
+                          ("softmax", 1, 1, 6, 64), ("sigmoid", 4, 2, 3, 16)])
+def test_route_scored_matches_oracle(device, func, groups, topk_groups, k, experts):
+    rng = np.random.default_rng(experts + k)
+    logits, bias = _scored_case(rng, 512, experts, func, groups, topk_groups, k)
+    idx, w = wa.route_scored(torch.from_numpy(logits).to(device), torch.from_numpy(bias).to(device), k, func,
+                             route_scale=2.5, n_groups=groups, topk_groups=topk_groups)
+    want_idx, want_w = M.route_scored(logits, bias, k, func, 2.5, True, groups, topk_groups)
+    got_idx = _np(idx)
+    # Scores are transcendental: device and oracle round differently in the last
+    # bits, so a token may differ only where its selection sits on a near-tie.
+    same = np.all(got_idx == want_idx, axis=1)
+    assert same.mean() > 0.99
+    s = M.score_function(logits, func) + bias
+    for t in np.flatnonzero(~same):
+        kth = np.sort(s[t])[::-1]
+        gaps = np.abs(np.diff(kth))
+        assert gaps.min() < 1e-5, f"token {t} differs without a near tie"
+    np.testing.assert_allclose(_np(w)[same], want_w[same], rtol=1e-5)
+
+
+# ----------------------------------------------------------------------------- permute
+
+@pytest.mark.parametrize("tokens,k,experts,skew", [(1, 10, 512, False), (16, 4, 64, False), (1000, 10, 512, True),
+                                                    (16384, 10, 512, True), (7, 3, 1, False)])
+def test_permute_exact(device, tokens, k, experts, skew):
+    rng = np.random.default_rng(tokens)
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    if skew:
+        logits += S.zipf_bias(experts, 1.1, rng)
+    idx = M.topk_desc(logits, k) if k <= experts else rng.integers(0, experts, (tokens, k))
+    if experts == 1:
+        idx = np.zeros((tokens, k), np.int32)
+    p = wa.permute(torch.from_numpy(idx.astype(np.int32)).to(device), experts, 128)
+    want = M.permute(idx, experts, 128)
+    np.testing.assert_array_equal(_np(p.order), want.order)
+    np.testing.assert_array_equal(_np(p.inverse), want.inverse)
+    np.testing.assert_array_equal(_np(p.offsets), want.offsets)
+    n = int(_np(p.tile_count)[0])
+    assert n == len(want.tiles)
+    np.testing.assert_array_equal(_np(p.tiles)[:n], want.tiles)
+
+
+def test_permute_skips_invalid_ids(device):
+    idx = np.array([[0, 5], [9, 1], [-1, 0]], np.int32)
+    p = wa.permute(torch.from_numpy(idx).to(device), 8, 4)
+    inv = _np(p.inverse)
+    assert inv[2] == -1 and inv[4] == -1
+    assert _np(p.offsets)[-1] == 4
+    np.testing.assert_array_equal(_np(p.order)[:4], [0, 5, 3, 1])
+
+
+def test_permute_empty(device):
+    p = wa.permute(torch.empty(0, 10, dtype=torch.int32, device=device), 512)
+    assert int(_np(p.tile_count)[0]) == 0 and int(_np(p.offsets)[-1]) == 0

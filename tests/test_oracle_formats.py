@@ -1,0 +1,171 @@
+"""Pins the format oracle (oracle/formats.py, oracle/c/oracle.c) — CPU only.
+
+Known-answer vectors come from the reference's Swift tests
+(Tests/DeepSeekRepackTests/DeepSeekRepackTests.swift:336-412); the rest are
+closed forms and an independent library decoder (torch.float8_e4m3fn).
+"""
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as F
+from oracle import c_oracle as C
+
+
+def _bf16_bits(values):
+    return (np.asarray(values, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+KAT2_BITS = [
+    49381, 49134, 16475, 49335, 48859, 16539, 49289, 16256, 16585, 49207, 16411, 49367, 49079, 16503, 49321, 0,
+    16553, 49271, 16311, 16599, 49179, 16439, 49353, 49024, 16521, 49307, 16091, 16567, 49243, 16366, 16613, 49152,
+    16466, 49339, 48914, 16535, 49294, 16219, 16581, 49216, 16402, 49371, 49097, 16494, 49326, 48658, 16549, 49280,
+    16293, 16594, 49189, 16430, 49358, 49042, 16517, 49312, 16018, 16562, 49253, 16347, 16608, 49161, 16457, 49344,
+]
+KAT2_WEIGHTS = [
+    207, 245, 105, 46, 215, 244, 107, 15, 231, 115, 92, 175, 230, 113, 77, 199,
+    245, 105, 46, 215, 244, 107, 143, 231, 115, 93, 175, 230, 113, 62, 199, 245,
+]
+
+
+def _kat4_source():
+    idx = np.arange(128 * 128)
+    v = ((idx * 37 + 11) & 0xFF).astype(np.uint8)
+    return np.where((v & 0x7F) == 0x7F, v ^ 1, v).astype(np.uint8)
+
+
+@pytest.mark.parametrize("impl", ["numpy", "c"])
+def test_kat_fixed_vector(impl):
+    # DeepSeekRepackTests.swift:336-351
+    bits = _bf16_bits([0.5, 1, 1.5, 2, 3, 4, 6, -0.5, -1, -1.5, -2, -3, -4, -6] + [0] * 18)
+    q = F.quantize_mxfp4_bf16 if impl == "numpy" else C.quantize_bf16
+    w, s = q(bits, 1, 32)
+    assert list(w.ravel()) == [0x21, 0x43, 0x65, 0x97, 0xBA, 0xDC, 0xFE] + [0] * 9
+    assert list(s.ravel()) == [127]
+
+
+@pytest.mark.parametrize("impl", ["numpy", "c"])
+def test_kat_bf16_rows(impl):
+    # DeepSeekRepackTests.swift:353-375
+    q = F.quantize_mxfp4_bf16 if impl == "numpy" else C.quantize_bf16
+    w, s = q(np.array(KAT2_BITS, np.uint16), 2, 32)
+    assert list(w.ravel()) == KAT2_WEIGHTS
+    assert list(s.ravel()) == [127, 127]
+
+
+@pytest.mark.parametrize("impl", ["numpy", "c"])
+def test_kat_official_fp8_blocks(impl):
+    # DeepSeekRepackTests.swift:377-393
+    first = [0x30, 0x38, 0x3C, 0x40, 0x44, 0x48, 0x4C, 0xB0, 0xB8, 0xBC, 0xC0, 0xC4, 0xC8, 0xCC] + [0] * 114
+    src = np.array(first + [0] * (127 * 128), np.uint8)
+    q = F.quantize_mxfp4_fp8 if impl == "numpy" else C.quantize_fp8
+    w, s = q(src, np.array([0x3F80], np.uint16), 128, 128)
+    assert list(w.ravel()[:16]) == [0x21, 0x43, 0x65, 0x97, 0xBA, 0xDC, 0xFE] + [0] * 9
+    assert list(s.ravel()[:4]) == [127, 0, 0, 0]
+
+
+@pytest.mark.parametrize("impl", ["numpy", "c"])
+def test_kat_fp8_sha256(impl):
+    # DeepSeekRepackTests.swift:395-412: pins e4m3 decode, x scale, bf16 RNE and the encoder end to end.
+    q = F.quantize_mxfp4_fp8 if impl == "numpy" else C.quantize_fp8
+    w, s = q(_kat4_source(), np.array([0x3F40], np.uint16), 128, 128)
+    assert hashlib.sha256(w.tobytes()).hexdigest() == "7c332f3b69c7e580b8f3dd7c89bf44d18f81debfb17a648a7d131e28907a3b71"
+    assert hashlib.sha256(s.tobytes()).hexdigest() == "0fecfb3515a322ce43dca1e7d6115fcf2c1f34d474774097fb4eededdcc6cf49"
+
+
+def test_encoders_reject_incomplete_plans():
+    with pytest.raises(ValueError):
+        F.quantize_mxfp4_bf16(np.zeros(31, np.uint16), 1, 31)
+    with pytest.raises(ValueError):
+        F.quantize_mxfp4_fp8(np.zeros(64 * 128, np.uint8), np.zeros(1, np.uint16), 64, 128)
+
+
+def test_numpy_and_c_encoders_agree_on_random_rows():
+    rng = np.random.default_rng(5)
+    for scale in (1e-3, 1.0, 300.0):
+        bits = _bf16_bits(rng.standard_normal((16, 256)).astype(np.float32) * scale)
+        a = F.quantize_mxfp4_bf16(bits, 16, 256)
+        b = C.quantize_bf16(bits, 16, 256)
+        np.testing.assert_array_equal(a[0], b[0])
+        np.testing.assert_array_equal(a[1], b[1])
+
+
+def test_e2m1_e8m0_closed_form_every_code_and_scale():
+    # Every (scale byte, code) pair: value = sign * magnitude * 2**(b - 127); 255 is NaN.
+    codes = np.arange(16, dtype=np.uint8)
+    words = np.zeros((256, 4), np.uint32)
+    for j in range(4):
+        words[:, j] = sum(((int(codes[(2 * j * 4 + n) % 16])) << (4 * n)) for n in range(8))
+    packed = np.tile(words, (1, 1))  # [256, 4] -> 32 values per row, codes cycling
+    scales = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    got = F.dequant_mxfp4(packed, scales)
+    mags = [0, 0.5, 1, 1.5, 2, 3, 4, 6]
+    for b in range(256):
+        for i in range(32):
+            code = (int(packed[b, i // 8]) >> (4 * (i % 8))) & 15
+            m = mags[code & 7] * (-1 if code & 8 else 1)
+            want = np.nan if b == 255 else np.float32(m) * np.float32(2.0 ** (b - 127))
+            if b == 255:
+                assert np.isnan(got[b, i])
+            else:
+                assert got[b, i] == want, (b, i, code)
+    np.testing.assert_array_equal(got, C.dequant_mxfp4(packed, scales))
+
+
+def test_mxfp4_round_trip_on_exact_values():
+    # Values already on the MXFP4 grid encode and decode to themselves.
+    rng = np.random.default_rng(9)
+    codes = rng.integers(0, 16, size=(8, 64)).astype(np.uint8)
+    codes[:, ::32] = 7  # each group holds +6, so the encoder picks exponent(6) - 2 = 0 relative
+    exps = rng.integers(-8, 3, size=(8, 2))
+    vals = F.e2m1_value(codes).reshape(8, 2, 32) * (2.0 ** exps)[..., None]
+    vals = vals.reshape(8, 64).astype(np.float32)
+    w, s = F.quantize_mxfp4_bf16(F.bf16_round(vals), 8, 64)
+    back = F.dequant_mxfp4(np.ascontiguousarray(w).view(np.uint32), s)
+    np.testing.assert_array_equal(back, vals)
+
+
+def test_e4m3_matches_torch_float8_every_byte():
+    b = np.arange(256, dtype=np.uint8)
+    ours = F.e4m3_value(b)
+    theirs = torch.from_numpy(b).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    nan = np.isnan(theirs)
+    assert list(np.flatnonzero(nan)) == [0x7F, 0xFF]
+    np.testing.assert_array_equal(np.isnan(ours), nan)
+    np.testing.assert_array_equal(ours[~nan], theirs[~nan])
+    c = np.array([C.e4m3(int(v)) for v in b], np.float32)
+    np.testing.assert_array_equal(c[~nan], theirs[~nan])
+
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(3)
+    v = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 10000),
+                        np.array([0.0, -0.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8], np.float32)]).astype(np.float32)
+    ours = F.bf16_round(v)
+    theirs = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, theirs)
+
+
+def test_fp8_blocks_crop_and_reject():
+    rng = np.random.default_rng(1)
+    w = rng.integers(0, 256, size=(130, 200)).astype(np.uint8)
+    w = np.where((w & 0x7F) == 0x7F, w ^ 1, w).astype(np.uint8)
+    s = rng.random((2, 2)).astype(np.float32)
+    out = F.dequant_fp8_blocks(w, s)
+    assert out.shape == (130, 200)
+    # Ragged edge: row 129 / column 199 use block (1, 1).
+    assert out[129, 199] == F.e4m3_value(w[129, 199]) * s[1, 1]
+    assert out[127, 127] == F.e4m3_value(w[127, 127]) * s[0, 0]
+    assert out[128, 5] == F.e4m3_value(w[128, 5]) * s[1, 0]
+    bad = w.copy()
+    bad[3, 3] = 0x7F
+    with pytest.raises(ValueError):
+        F.dequant_fp8_blocks(bad, s)
+    with pytest.raises(ValueError):
+        F.dequant_fp8_blocks(w, np.array([[1, -1], [1, 1]], np.float32))
+    with pytest.raises(ValueError):
+        F.dequant_fp8_blocks(w, np.ones((1, 2), np.float32))
+    with pytest.raises(ValueError):
+        F.dequant_fp8_blocks(w, s.astype(np.float64))

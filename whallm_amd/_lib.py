@@ -1,0 +1,88 @@
+"""ctypes binding of libwhallm_moe.so (the C ABI declared in include/whallm_moe.h).
+
+The library is loaded from the package's own ``lib/`` folder. There is no
+fallback: when it is missing or fails to load, every operation raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int32, c_int64, c_size_t, c_void_p, c_char_p, POINTER
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libwhallm_moe.so"
+
+
+class MXFP4ExpertsC(ctypes.Structure):
+    """wm_mxfp4_experts (include/whallm_moe.h)."""
+    _fields_ = [
+        ("gate_up", c_void_p), ("gate_up_scales", c_void_p), ("down", c_void_p), ("down_scales", c_void_p),
+        ("gate_up_stride", c_int64), ("gate_up_scales_stride", c_int64),
+        ("down_stride", c_int64), ("down_scales_stride", c_int64),
+        ("slots", c_void_p), ("experts", c_int32), ("hidden", c_int32), ("inter", c_int32),
+        ("up_first", c_int32), ("swiglu_limit", c_float),
+    ]
+
+
+class FP8ExpertsC(ctypes.Structure):
+    """wm_fp8_experts (include/whallm_moe.h)."""
+    _fields_ = [
+        ("w13", c_void_p), ("w13_scales", c_void_p), ("w2", c_void_p), ("w2_scales", c_void_p),
+        ("w13_stride", c_int64), ("w13_scales_stride", c_int64), ("w2_stride", c_int64), ("w2_scales_stride", c_int64),
+        ("slots", c_void_p), ("experts", c_int32), ("hidden", c_int32), ("inter", c_int32),
+        ("up_first", c_int32), ("swiglu_limit", c_float),
+    ]
+
+
+_P = c_void_p
+_SIGNATURES = {
+    "wm_last_error": (c_char_p, []),
+    "wm_version": (c_char_p, []),
+    "wm_dequant_mxfp4": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
+    "wm_dequant_fp8_blocks": (c_int, [_P, _P, c_int64, c_int64, _P, _P]),
+    "wm_route_softmax_topk": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P]),
+    "wm_route_scored": (c_int, [_P, _P, c_int32, c_int32, c_int32, c_int32, c_float, c_int32, c_int32, c_int32,
+                                _P, _P, _P]),
+    "wm_linear_bf16": (c_int, [_P, _P, c_int32, c_int32, c_int32, _P, _P]),
+    "wm_permute_workspace_size": (c_size_t, [c_int64, c_int32]),
+    "wm_permute": (c_int, [_P, c_int64, c_int32, c_int32, _P, _P, _P, _P, _P, _P, c_size_t, _P]),
+    "wm_moe_mxfp4_workspace_size": (c_size_t, [c_int32, c_int32, POINTER(MXFP4ExpertsC)]),
+    "wm_moe_mxfp4": (c_int, [_P, c_int32, _P, _P, c_int32, POINTER(MXFP4ExpertsC), POINTER(MXFP4ExpertsC), _P,
+                             _P, _P, c_size_t, _P]),
+    "wm_experts_mxfp4": (c_int, [_P, c_int32, _P, c_int32, POINTER(MXFP4ExpertsC), _P, _P, c_size_t, _P]),
+}
+
+_lib = None
+
+
+class WhallmError(RuntimeError):
+    """A libwhallm_moe call returned a nonzero status."""
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises when it is not built or cannot load."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m whallm_amd.build` "
+            "(there is no CPU fallback for the expert path)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Calls an int-status entry point, raising WhallmError with wm_last_error()."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        raise WhallmError(f"{name}: {lib.wm_last_error().decode(errors='replace')}")
+
+
+def exported_symbols() -> list[str]:
+    return sorted(_SIGNATURES)

@@ -1,0 +1,378 @@
+// Decode-time MXFP4 expert FFN: fused dequant + GEMV, HBM-bound.
+//
+// Replaces the reference's expert_linear4 + expert_act_pairs + expert_linear4 +
+// moe_combine dispatch chain (Native/QwenNative/kernels.metal:1190-1220,
+// :1333-1339, :185-194; driven from engine.mm:2198-2235) with two kernels:
+//
+//   gate_up_act : one workgroup = (pair, block of intermediate rows i). Each wave
+//                 streams the gate row i and the up row I+i of its expert; a row of
+//                 H/2 bytes is read by H/32 lanes, 16 bytes (one 32-value E8M0
+//                 group) per lane per load, so a wave load is 64 x 16 B, fully
+//                 coalesced. Nibbles -> bf16 with the gfx950 scaled convert
+//                 (scale folded in), dot2 against the bf16 input held in registers,
+//                 segment reduction, then silu(gate) * up in the epilogue -> act (fp32).
+//   down_combine: one workgroup = (token, block of output rows o). The four waves
+//                 split the token's experts (routed + shared); each lane keeps its
+//                 partial sums already scaled by the routing weight, so the
+//                 cross-lane and cross-wave reductions happen once per output row:
+//                 y[t,o] = sum_k w[t,k] * act_k . Wd_k[o] + gate(t) * act_s . Wd_s[o].
+//                 The same kernel in per-pair mode writes each pair's row unweighted
+//                 (the StreamingExperts [T, K, H] contract, qwen4_exp.py:853-904).
+#include <cmath>
+
+#include "wm_common.h"
+#include "moe_internal.h"
+
+namespace wm {
+
+// ---------------------------------------------------------------------------------
+// The input row of a decode token as bf16 pairs: lane group `g` needs values
+// [32 g, 32 g + 32) = 16 words.
+template <int GPL, int LPR>
+__device__ __forceinline__ void load_x_groups(const uint32_t* __restrict__ xrow, int gl, uint32_t (&xw)[GPL][16]) {
+#pragma unroll
+  for (int gp = 0; gp < GPL; ++gp) {
+    const uint4* src = reinterpret_cast<const uint4*>(xrow + (gl + gp * LPR) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint4 v = src[q];
+      xw[gp][4 * q + 0] = v.x;
+      xw[gp][4 * q + 1] = v.y;
+      xw[gp][4 * q + 2] = v.z;
+      xw[gp][4 * q + 3] = v.w;
+    }
+  }
+}
+
+// dot of one 32-value group: 16 weight bytes (4 words) against 16 bf16-pair words.
+__device__ __forceinline__ float group_dot_bf16(uint4 w, float scale, const uint32_t (&xw)[16], float acc) {
+  uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    wm_bf16x2 wv[4];
+    fp4x8_to_bf16(words[j], scale, wv);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc = dot2_bf16(wv[m], bits_to_bf16x2(xw[4 * j + m]), acc);
+  }
+  return acc;
+}
+
+// One pair of the decode list: its token row and expert (or the shared expert).
+__device__ __forceinline__ bool decode_pair(int p, int tokens, int k, const int32_t* __restrict__ indices,
+                                            const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared_opt,
+                                            const wm_mxfp4_experts& shared, int& t, ExpertRegions& r) {
+  if (p < tokens * k) {
+    t = p / k;
+    int e = indices[p];
+    if (e < 0 || e >= routed.experts) return false;
+    r = expert_regions(routed, e);
+    return true;
+  }
+  t = p - tokens * k;
+  if (!shared_opt) return false;
+  r = expert_regions(shared, 0);
+  return true;
+}
+
+// grid: (ceil(I / (4 * RPW)), pairs). act[p, i] fp32.
+template <int LPR, int GPL, int RPW>
+__global__ void __launch_bounds__(256) gate_up_act_kernel(const uint16_t* __restrict__ x, int tokens, int k,
+                                                          const int32_t* __restrict__ indices, wm_mxfp4_experts routed,
+                                                          wm_mxfp4_experts shared, int has_shared,
+                                                          float* __restrict__ act) {
+  constexpr int NS = 64 / LPR;              // rows a wave reads at once
+  constexpr int ROWS = 2 * RPW;             // gate and up rows of RPW intermediate indices
+  constexpr int STEPS = (ROWS + NS - 1) / NS;
+  __shared__ float sums[4][ROWS];
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int slot = lane / LPR, gl = lane % LPR;
+  const int p = blockIdx.y;
+  const int H = routed.hidden, I = routed.inter;
+  int t;
+  ExpertRegions r;
+  if (!decode_pair(p, tokens, k, indices, routed, has_shared ? &shared : nullptr, shared, t, r)) {
+    // Unknown expert id: its act row is zero (the index check of the host layer reports it).
+    for (int i = blockIdx.x * 4 * RPW + threadIdx.x; i < min(I, (int)(blockIdx.x + 1) * 4 * RPW); i += 256)
+      act[(int64_t)p * I + i] = 0.0f;
+    return;
+  }
+  const int up_first = has_shared && p >= tokens * k ? shared.up_first : routed.up_first;
+  const float limit = has_shared && p >= tokens * k ? shared.swiglu_limit : routed.swiglu_limit;
+  const int i_base = blockIdx.x * 4 * RPW + wave * RPW;
+
+  uint32_t xw[GPL][16];
+  load_x_groups<GPL, LPR>(reinterpret_cast<const uint32_t*>(x) + (int64_t)t * (H / 2), gl, xw);
+
+  const int G = H / 32;
+  uint4 wq[STEPS][GPL];
+  uint32_t sb[STEPS][GPL];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    int q = st * NS + slot;
+    int i = i_base + q / 2;
+    bool ok = q < ROWS && i < I;
+    // q even: gate row, q odd: up row (their order in the blob follows up_first).
+    int row = ((q & 1) ^ up_first) ? I + i : i;
+#pragma unroll
+    for (int gp = 0; gp < GPL; ++gp) {
+      int g = gl + gp * LPR;
+      if (ok) {
+        wq[st][gp] = reinterpret_cast<const uint4*>(r.gate_up + (int64_t)row * (H / 2))[g];
+        sb[st][gp] = r.gate_up_scales[(int64_t)row * G + g];
+      } else {
+        wq[st][gp] = make_uint4(0, 0, 0, 0);
+        sb[st][gp] = 127;
+      }
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int gp = 0; gp < GPL; ++gp) acc = group_dot_bf16(wq[st][gp], e8m0_scale_operand(sb[st][gp]), xw[gp], acc);
+    acc = segment_sum<LPR>(acc);
+    int q = st * NS + slot;
+    if (gl == 0 && q < ROWS) sums[wave][q] = acc;
+  }
+  __syncthreads();
+  if (lane < RPW) {
+    int i = i_base + lane;
+    if (i < I) {
+      float g = sums[wave][2 * lane], u = sums[wave][2 * lane + 1];
+      if (limit > 0.0f) {
+        g = fminf(g, limit);
+        u = fminf(fmaxf(u, -limit), limit);
+      }
+      act[(int64_t)p * I + i] = silu(g) * u;
+    }
+  }
+}
+
+// grid: combine mode (ceil(H / (NS * STEPS)), tokens); per-pair mode (ceil(H / (4 * NS * STEPS)), pairs).
+// In combine mode the four waves split the token's experts; in per-pair mode they split the rows.
+template <int LPR, int GPL, int STEPS, bool COMBINE>
+__global__ void __launch_bounds__(256) down_kernel(const float* __restrict__ act, int tokens, int k,
+                                                   const int32_t* __restrict__ indices,
+                                                   const float* __restrict__ weights, wm_mxfp4_experts routed,
+                                                   wm_mxfp4_experts shared, int has_shared,
+                                                   const uint16_t* __restrict__ x,
+                                                   const uint16_t* __restrict__ shared_gate,
+                                                   uint16_t* __restrict__ y) {
+  constexpr int NS = 64 / LPR;
+  constexpr int OPW = NS * STEPS;           // output rows per wave
+  __shared__ float partial[4][OPW];
+  __shared__ float gate_value;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int slot = lane / LPR, gl = lane % LPR;
+  const int H = routed.hidden, I = routed.inter;
+  const int G = I / 32;
+
+  int o_base, first_entry, entry_step, n_entries, t;
+  if (COMBINE) {
+    t = blockIdx.y;
+    o_base = blockIdx.x * OPW;
+    n_entries = k + (has_shared ? 1 : 0);
+    first_entry = wave;
+    entry_step = 4;
+  } else {
+    t = blockIdx.y;  // the pair
+    o_base = (blockIdx.x * 4 + wave) * OPW;
+    n_entries = 1;
+    first_entry = 0;
+    entry_step = 1;
+  }
+  if (COMBINE && has_shared) {
+    if (threadIdx.x < 64) {
+      float gv = 1.0f;
+      if (shared_gate) {
+        const uint32_t* xr = reinterpret_cast<const uint32_t*>(x) + (int64_t)t * (H / 2);
+        const uint32_t* gr = reinterpret_cast<const uint32_t*>(shared_gate);
+        float a = 0.0f;
+        for (int q = lane; q < H / 2; q += 64) a = dot2_bf16(bits_to_bf16x2(xr[q]), bits_to_bf16x2(gr[q]), a);
+        a = segment_sum<64>(a);
+        gv = 1.0f / (1.0f + __expf(-a));
+      }
+      if (lane == 0) gate_value = gv;
+    }
+    __syncthreads();
+  }
+
+  float acc[STEPS];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) acc[st] = 0.0f;
+
+  for (int entry = first_entry; entry < n_entries; entry += entry_step) {
+    int p;          // act row
+    float w;        // weight of this expert's output
+    ExpertRegions r;
+    if (COMBINE) {
+      if (entry < k) {
+        p = t * k + entry;
+        int e = indices[p];
+        if (e < 0 || e >= routed.experts) continue;
+        r = expert_regions(routed, e);
+        w = weights[p];
+      } else {
+        p = tokens * k + t;
+        r = expert_regions(shared, 0);
+        w = gate_value;
+      }
+    } else {
+      p = t;
+      if (p < tokens * k) {
+        int e = indices[p];
+        if (e < 0 || e >= routed.experts) break;  // zero row
+        r = expert_regions(routed, e);
+      } else {
+        r = expert_regions(shared, 0);
+      }
+      w = 1.0f;
+    }
+    // act values of this lane's groups: 32 floats per group.
+    const float* arow = act + (int64_t)p * I;
+    uint4 wq[STEPS][GPL];
+    uint32_t sb[STEPS][GPL];
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+      int o = o_base + st * NS + slot;
+#pragma unroll
+      for (int gp = 0; gp < GPL; ++gp) {
+        int g = gl + gp * LPR;
+        if (o < H) {
+          wq[st][gp] = reinterpret_cast<const uint4*>(r.down + (int64_t)o * (I / 2))[g];
+          sb[st][gp] = r.down_scales[(int64_t)o * G + g];
+        } else {
+          wq[st][gp] = make_uint4(0, 0, 0, 0);
+          sb[st][gp] = 127;
+        }
+      }
+    }
+#pragma unroll
+    for (int gp = 0; gp < GPL; ++gp) {
+      const float4* a4 = reinterpret_cast<const float4*>(arow + (gl + gp * LPR) * 32);
+      float av[32];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        float4 v = a4[q];
+        av[4 * q] = v.x; av[4 * q + 1] = v.y; av[4 * q + 2] = v.z; av[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        float scale = e8m0_scale_operand(sb[st][gp]);
+        uint32_t words[4] = {wq[st][gp].x, wq[st][gp].y, wq[st][gp].z, wq[st][gp].w};
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            wm_f32x2 wf;
+            switch (b) {
+              case 0: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[j], scale, 0); break;
+              case 1: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[j], scale, 1); break;
+              case 2: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[j], scale, 2); break;
+              default: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[j], scale, 3); break;
+            }
+            s = fmaf(wf[0], av[8 * j + 2 * b], s);
+            s = fmaf(wf[1], av[8 * j + 2 * b + 1], s);
+          }
+        }
+        acc[st] = fmaf(w, s, acc[st]);
+      }
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    float v = segment_sum<LPR>(acc[st]);
+    if (gl == 0) partial[wave][st * NS + slot] = v;
+  }
+  __syncthreads();
+  if (COMBINE) {
+    if (threadIdx.x < OPW) {
+      int o = o_base + threadIdx.x;
+      if (o < H) {
+        float v = partial[0][threadIdx.x] + partial[1][threadIdx.x] + partial[2][threadIdx.x] + partial[3][threadIdx.x];
+        y[(int64_t)t * H + o] = f32_to_bf16_bits(v);
+      }
+    }
+  } else {
+    if (lane < OPW) {
+      int o = o_base + lane;
+      if (o < H) y[(int64_t)t * H + o] = f32_to_bf16_bits(partial[wave][lane]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Launchers. LPR (lanes per row) = min(64, groups); GPL = groups / LPR.
+
+template <int RPW>
+static void launch_gate_up(int lpr, int gpl, dim3 grid, hipStream_t s, const uint16_t* x, int tokens, int k,
+                           const int32_t* indices, const wm_mxfp4_experts& routed, const wm_mxfp4_experts& shared,
+                           int has_shared, float* act) {
+#define WM_GU(L, G)                                                                                           \
+  if (lpr == L && gpl == G) {                                                                                  \
+    hipLaunchKernelGGL((gate_up_act_kernel<L, G, RPW>), grid, dim3(256), 0, s, x, tokens, k, indices, routed, \
+                       shared, has_shared, act);                                                              \
+    return;                                                                                                    \
+  }
+  WM_GU(2, 1) WM_GU(4, 1) WM_GU(8, 1) WM_GU(16, 1) WM_GU(32, 1) WM_GU(64, 1) WM_GU(64, 2) WM_GU(64, 3) WM_GU(64, 4)
+#undef WM_GU
+  fail("decode gate_up: unsupported hidden size");
+}
+
+template <int STEPS, bool COMBINE>
+static void launch_down(int lpr, int gpl, dim3 grid, hipStream_t s, const float* act, int tokens, int k,
+                        const int32_t* indices, const float* weights, const wm_mxfp4_experts& routed,
+                        const wm_mxfp4_experts& shared, int has_shared, const uint16_t* x, const uint16_t* sg,
+                        uint16_t* y) {
+#define WM_DN(L, G)                                                                                            \
+  if (lpr == L && gpl == G) {                                                                                   \
+    hipLaunchKernelGGL((down_kernel<L, G, STEPS, COMBINE>), grid, dim3(256), 0, s, act, tokens, k, indices,     \
+                       weights, routed, shared, has_shared, x, sg, y);                                          \
+    return;                                                                                                     \
+  }
+  WM_DN(2, 1) WM_DN(4, 1) WM_DN(8, 1) WM_DN(16, 1) WM_DN(32, 1) WM_DN(64, 1) WM_DN(64, 2) WM_DN(64, 3) WM_DN(64, 4)
+#undef WM_DN
+  fail("decode down: unsupported intermediate size");
+}
+
+static void lanes_for(int dim, int& lpr, int& gpl) {
+  int groups = dim / 32;
+  if (groups >= 64) {
+    lpr = 64;
+    gpl = groups / 64;
+    if (groups % 64 || gpl > 4) fail("decode: size must be a multiple of 2048 up to 8192, or a power of two below");
+  } else {
+    lpr = groups;
+    gpl = 1;
+    if (groups & (groups - 1)) fail("decode: sizes below 2048 must be powers of two");
+  }
+}
+
+void decode_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                  const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared, const uint16_t* shared_gate,
+                  uint16_t* y, bool combine, float* act, hipStream_t s) {
+  const int H = routed.hidden, I = routed.inter;
+  const int pairs = tokens * k + (shared ? tokens : 0);
+  wm_mxfp4_experts sh = shared ? *shared : routed;
+  int lpr, gpl;
+  constexpr int RPW = 4;
+  lanes_for(H, lpr, gpl);
+  dim3 g1((I + 4 * RPW - 1) / (4 * RPW), pairs);
+  launch_gate_up<RPW>(lpr, gpl, g1, s, x, tokens, k, indices, routed, sh, shared ? 1 : 0, act);
+  check_launch("gate_up_act");
+  lanes_for(I, lpr, gpl);
+  constexpr int STEPS = 2;
+  int opw = (64 / lpr) * STEPS;
+  if (combine) {
+    dim3 g2((H + opw - 1) / opw, tokens);
+    launch_down<STEPS, true>(lpr, gpl, g2, s, act, tokens, k, indices, weights, routed, sh, shared ? 1 : 0, x,
+                             shared_gate, y);
+  } else {
+    dim3 g2((H + 4 * opw - 1) / (4 * opw), tokens * k);
+    launch_down<STEPS, false>(lpr, gpl, g2, s, act, tokens, k, indices, weights, routed, sh, 0, x, nullptr, y);
+  }
+  check_launch("down");
+}
+
+}  // namespace wm

@@ -1,0 +1,96 @@
+// C-ABI entry points of the MXFP4 MoE layer: argument checks, path choice
+// (fused dequant-GEMV for decode, MFMA grouped GEMM for prefill) and workspace sizing.
+#include "moe_internal.h"
+
+namespace wm {
+
+void validate_experts(const wm_mxfp4_experts* e, const char* what, bool shared) {
+  std::string w(what);
+  if (!e) fail(w + ": expert table is null");
+  if (!e->gate_up || !e->gate_up_scales || !e->down || !e->down_scales) fail(w + ": expert region pointer is null");
+  if (e->hidden < 32 || e->hidden % 32) fail(w + ": hidden must be a positive multiple of 32");
+  if (e->inter < 32 || e->inter % 32) fail(w + ": intermediate must be a positive multiple of 32");
+  if (!shared && (e->experts < 1 || e->experts > 1024)) fail(w + ": expert count must be in 1..1024");
+  if (e->gate_up_stride < 0 || e->gate_up_scales_stride < 0 || e->down_stride < 0 || e->down_scales_stride < 0)
+    fail(w + ": negative stride");
+  if (e->swiglu_limit < 0.0f) fail(w + ": swiglu_limit must be >= 0");
+  // 16-byte weight loads and 2-byte scale loads.
+  auto aligned = [](const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; };
+  if (!aligned(e->gate_up, 16) || !aligned(e->down, 16) || e->gate_up_stride % 16 || e->down_stride % 16)
+    fail(w + ": weight regions and strides must be 16-byte aligned");
+  if (!aligned(e->gate_up_scales, 2) || !aligned(e->down_scales, 2) || e->gate_up_scales_stride % 2 ||
+      e->down_scales_stride % 2)
+    fail(w + ": scale regions and strides must be 2-byte aligned");
+}
+
+static void validate_pair(const wm_mxfp4_experts* routed, const wm_mxfp4_experts* shared) {
+  validate_experts(routed, "routed experts", false);
+  if (shared) {
+    validate_experts(shared, "shared expert", true);
+    if (shared->hidden != routed->hidden) fail("shared expert: hidden differs from the routed experts");
+    if (shared->inter != routed->inter)
+      fail("shared expert: intermediate must equal the routed experts' (one act buffer layout)");
+  }
+}
+
+static bool use_decode(int tokens, int k) { return (int64_t)tokens * k <= DECODE_MAX_PAIRS; }
+
+static size_t decode_workspace(int tokens, int k, const wm_mxfp4_experts& e) {
+  return sizeof(float) * (size_t)(tokens * k + tokens) * e.inter;
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+WM_EXPORT size_t wm_moe_mxfp4_workspace_size(int32_t tokens, int32_t k, const wm_mxfp4_experts* experts) {
+  if (!experts || tokens < 0 || k < 1) return 0;
+  if (use_decode(tokens, k)) return decode_workspace(tokens, k, *experts) + 256;
+  return prefill_workspace_size(tokens, k, *experts, true) + 256;
+}
+
+WM_EXPORT int wm_moe_mxfp4(const void* x, int32_t tokens, const int32_t* indices, const float* weights, int32_t k,
+                           const wm_mxfp4_experts* experts, const wm_mxfp4_experts* shared, const void* shared_gate,
+                           void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    if (tokens < 0) fail("wm_moe_mxfp4: negative token count");
+    if (k < 1 || k > 32) fail("wm_moe_mxfp4: k must be in 1..32");
+    validate_pair(experts, shared);
+    if (tokens == 0) return;
+    if (!x || !indices || !weights || !y) fail("wm_moe_mxfp4: null pointer");
+    if (workspace_bytes < wm_moe_mxfp4_workspace_size(tokens, k, experts) - 256 || !workspace)
+      fail("wm_moe_mxfp4: workspace too small");
+    hipStream_t s = as_stream(stream);
+    if (use_decode(tokens, k))
+      decode_mxfp4((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
+                    (uint16_t*)y, true, (float*)workspace, s);
+    else
+      prefill_mxfp4((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
+                    (uint16_t*)y, true, workspace, workspace_bytes, s);
+  });
+}
+
+WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* indices, int32_t k,
+                               const wm_mxfp4_experts* experts, void* out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  return guarded([&] {
+    if (tokens < 0) fail("wm_experts_mxfp4: negative token count");
+    if (k < 1 || k > 32) fail("wm_experts_mxfp4: k must be in 1..32");
+    validate_pair(experts, nullptr);
+    if (tokens == 0) return;
+    if (!x || !indices || !out) fail("wm_experts_mxfp4: null pointer");
+    if (workspace_bytes < wm_moe_mxfp4_workspace_size(tokens, k, experts) - 256 || !workspace)
+      fail("wm_experts_mxfp4: workspace too small");
+    hipStream_t s = as_stream(stream);
+    if (use_decode(tokens, k))
+      decode_mxfp4((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out, false,
+                   (float*)workspace, s);
+    else
+      prefill_mxfp4((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out,
+                    false, workspace, workspace_bytes, s);
+  });
+}
+
+}  // extern "C"

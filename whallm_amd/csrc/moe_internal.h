@@ -1,0 +1,44 @@
+// Internal interfaces between the MoE kernel files of libwhallm_moe.
+#pragma once
+
+#include "wm_common.h"
+
+namespace wm {
+
+// Device addresses of one expert's four regions.
+struct ExpertRegions {
+  const uint8_t* gate_up;
+  const uint8_t* gate_up_scales;
+  const uint8_t* down;
+  const uint8_t* down_scales;
+};
+
+__device__ __forceinline__ ExpertRegions expert_regions(const wm_mxfp4_experts& t, int e) {
+  int64_t slot = t.slots ? t.slots[e] : e;
+  ExpertRegions r;
+  r.gate_up = (const uint8_t*)t.gate_up + slot * t.gate_up_stride;
+  r.gate_up_scales = (const uint8_t*)t.gate_up_scales + slot * t.gate_up_scales_stride;
+  r.down = (const uint8_t*)t.down + slot * t.down_stride;
+  r.down_scales = (const uint8_t*)t.down_scales + slot * t.down_scales_stride;
+  return r;
+}
+
+// Host-side checks of an expert table; raises on a bad shape.
+void validate_experts(const wm_mxfp4_experts* e, const char* what, bool shared);
+
+// Decode path (small T): gate_up_act into `act` [(T*K + T_shared), I] fp32, then
+// down (combined into y [T, H] bf16, or per pair into y [T*K, H] bf16).
+void decode_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                  const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared, const uint16_t* shared_gate,
+                  uint16_t* y, bool combine, float* act, hipStream_t s);
+
+// Prefill path (grouped GEMM). `ws` holds the permute and activation buffers.
+size_t prefill_workspace_size(int tokens, int k, const wm_mxfp4_experts& e, bool has_shared);
+void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                   const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared, const uint16_t* shared_gate,
+                   uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s);
+
+// Pairs at or below this count take the decode path.
+constexpr int DECODE_MAX_PAIRS = 256;
+
+}  // namespace wm

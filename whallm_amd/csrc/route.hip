@@ -1,0 +1,258 @@
+// Router kernels: softmax top-k (Qwen), scored top-k with bias-select and
+// group-limited selection (DeepSeek), and the bf16 router linear.
+//
+// One wave64 per token. Expert e lives in lane e % 64, register e / 64, so a
+// row of up to 1024 logits is 16 registers per lane. Top-k is K rounds of a
+// wave-wide arg-max (value descending, ties to the lower index), the rule
+// fixed for this build (Native/DeepSeekNative/engine.mm:1881 breaks ties the
+// same way; Native/QwenNative/engine.mm:2086-2090 partial-sorts fp32 logits).
+#include <cmath>
+
+#include "wm_common.h"
+
+namespace wm {
+
+constexpr int ROUTE_MAX_PER_LANE = 16;  // E <= 1024
+constexpr int ROUTE_MAX_K = 32;
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// Wave-wide arg-max of (v, i); every lane gets the winner.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    float ov = __shfl_xor(v, offset, 64);
+    int oi = __shfl_xor(i, offset, 64);
+    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return segment_sum<64>(v); }
+
+// Selects k experts from vals (lane-strided, n_valid per lane implicit through -inf/NaN-free
+// masking by `taken`). Writes indices into sel[0..k) (uniform across lanes).
+__device__ __forceinline__ void wave_topk(const float (&vals)[ROUTE_MAX_PER_LANE], int per_lane, int experts,
+                                          int k, int lane, int (&sel)[ROUTE_MAX_K]) {
+  uint32_t taken = 0;
+  for (int j = 0; j < k; ++j) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int r = 0; r < per_lane; ++r) {
+      int e = r * 64 + lane;
+      if (e >= experts || (taken >> r) & 1u) continue;
+      if (better(vals[r], e, bv, bi)) { bv = vals[r]; bi = e; }
+    }
+    wave_argmax(bv, bi);
+    sel[j] = bi;
+    if ((bi & 63) == lane && bi < experts) taken |= 1u << (bi >> 6);
+  }
+}
+
+__global__ void __launch_bounds__(64) route_softmax_topk_kernel(const float* __restrict__ logits, int tokens,
+                                                               int experts, int k, int norm,
+                                                               int32_t* __restrict__ indices,
+                                                               float* __restrict__ weights,
+                                                               float* __restrict__ probabilities) {
+  int t = blockIdx.x, lane = threadIdx.x;
+  if (t >= tokens) return;
+  const float* row = logits + (int64_t)t * experts;
+  int per_lane = (experts + 63) / 64;
+  float vals[ROUTE_MAX_PER_LANE];
+#pragma unroll
+  for (int r = 0; r < ROUTE_MAX_PER_LANE; ++r) {
+    int e = r * 64 + lane;
+    vals[r] = (r < per_lane && e < experts) ? row[e] : -INFINITY;
+  }
+  int sel[ROUTE_MAX_K];
+  wave_topk(vals, per_lane, experts, k, lane, sel);
+  // The first selected logit is the row maximum.
+  float top = row[sel[0]];
+  float denom = 0.0f;
+  if (probabilities) {
+    float part = 0.0f;
+    for (int r = 0; r < per_lane; ++r) {
+      int e = r * 64 + lane;
+      if (e < experts) part += __expf(vals[r] - top);
+    }
+    float full = wave_sum(part);
+    for (int r = 0; r < per_lane; ++r) {
+      int e = r * 64 + lane;
+      if (e < experts) probabilities[(int64_t)t * experts + e] = __expf(vals[r] - top) / full;
+    }
+  }
+  if (norm) {
+    for (int j = 0; j < k; ++j) denom += __expf(row[sel[j]] - top);
+  } else {
+    float part = 0.0f;
+    for (int r = 0; r < per_lane; ++r) {
+      int e = r * 64 + lane;
+      if (e < experts) part += __expf(vals[r] - top);
+    }
+    denom = wave_sum(part);
+  }
+  if (lane < k) {
+    int j = lane;
+    indices[(int64_t)t * k + j] = sel[j];
+    weights[(int64_t)t * k + j] = __expf(row[sel[j]] - top) / denom;
+  }
+}
+
+__device__ __forceinline__ float score_fn(float l, int func) {
+  if (func == 1) return 1.0f / (1.0f + __expf(-l));
+  // sqrt(softplus(l)) = sqrt(max(l, 0) + log1p(exp(-|l|))) (Native/DeepSeekNative/engine.mm:1875-1876)
+  return sqrtf(fmaxf(l, 0.0f) + log1pf(__expf(-fabsf(l))));
+}
+
+__global__ void __launch_bounds__(64) route_scored_kernel(const float* __restrict__ logits,
+                                                         const float* __restrict__ bias, int tokens, int experts,
+                                                         int k, int func, float route_scale, int norm, int n_groups,
+                                                         int topk_groups, int32_t* __restrict__ indices,
+                                                         float* __restrict__ weights) {
+  __shared__ float biased_lds[1024];
+  __shared__ float score_lds[1024];
+  __shared__ float group_score[64];
+  int t = blockIdx.x, lane = threadIdx.x;
+  if (t >= tokens) return;
+  const float* row = logits + (int64_t)t * experts;
+  int per_lane = (experts + 63) / 64;
+  float vals[ROUTE_MAX_PER_LANE];
+  float top = -INFINITY, denom = 1.0f;
+  if (func == 0) {  // softmax scores: need the row max and sum
+    float m = -INFINITY;
+    for (int r = 0; r < per_lane; ++r) {
+      int e = r * 64 + lane;
+      if (e < experts) m = fmaxf(m, row[e]);
+    }
+    int dummy = 0;
+    wave_argmax(m, dummy);
+    top = m;
+    float part = 0.0f;
+    for (int r = 0; r < per_lane; ++r) {
+      int e = r * 64 + lane;
+      if (e < experts) part += __expf(row[e] - top);
+    }
+    denom = wave_sum(part);
+  }
+#pragma unroll
+  for (int r = 0; r < ROUTE_MAX_PER_LANE; ++r) {
+    int e = r * 64 + lane;
+    if (r < per_lane && e < experts) {
+      float s = func == 0 ? __expf(row[e] - top) / denom : score_fn(row[e], func);
+      float b = s + (bias ? bias[e] : 0.0f);
+      score_lds[e] = s;
+      biased_lds[e] = b;
+      vals[r] = b;
+    } else {
+      vals[r] = -INFINITY;
+    }
+  }
+  __syncthreads();
+  if (n_groups > 1) {
+    int gsize = experts / n_groups;
+    // Group score: the sum of its two largest biased scores (DeepSeek-V3 rule).
+    float gs = -INFINITY;
+    if (lane < n_groups) {
+      float a = -INFINITY, b = -INFINITY;
+      for (int j = 0; j < gsize; ++j) {
+        float v = biased_lds[lane * gsize + j];
+        if (v > a) { b = a; a = v; }
+        else if (v > b) b = v;
+      }
+      gs = a + b;
+      group_score[lane] = gs;
+    }
+    // Keep the topk_groups best groups (ties -> lower group).
+    uint64_t keep = 0;
+    float gv[ROUTE_MAX_PER_LANE];
+    for (int r = 0; r < ROUTE_MAX_PER_LANE; ++r) gv[r] = (r == 0 && lane < n_groups) ? gs : -INFINITY;
+    int gsel[ROUTE_MAX_K];
+    wave_topk(gv, 1, n_groups, topk_groups, lane, gsel);
+    for (int j = 0; j < topk_groups; ++j) keep |= 1ull << gsel[j];
+    for (int r = 0; r < per_lane; ++r) {
+      int e = r * 64 + lane;
+      if (e < experts && !((keep >> (e / gsize)) & 1ull)) vals[r] = -INFINITY;
+    }
+  }
+  int sel[ROUTE_MAX_K];
+  wave_topk(vals, per_lane, experts, k, lane, sel);
+  float sum = 0.0f;
+  for (int j = 0; j < k; ++j) sum += score_lds[sel[j]];
+  if (lane < k) {
+    float w = score_lds[sel[lane]];
+    if (norm && k > 1) w = w / (sum + 1e-20f);
+    indices[(int64_t)t * k + lane] = sel[lane];
+    weights[(int64_t)t * k + lane] = w * route_scale;
+  }
+}
+
+// logits[t, e] = sum_h x[t, h] * w[e, h]; one wave per (e, t), lanes stride h in bf16 pairs.
+__global__ void __launch_bounds__(256) linear_bf16_kernel(const uint32_t* __restrict__ x, const uint32_t* __restrict__ w,
+                                                         int tokens, int hidden, int outputs, float* __restrict__ out) {
+  int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  int e = blockIdx.x * 4 + wave, t = blockIdx.y;
+  if (e >= outputs || t >= tokens) return;
+  int pairs = hidden / 2;
+  const uint32_t* xr = x + (int64_t)t * pairs;
+  const uint32_t* wr = w + (int64_t)e * pairs;
+  float acc = 0.0f;
+  for (int p = lane; p < pairs; p += 64) acc = dot2_bf16(bits_to_bf16x2(xr[p]), bits_to_bf16x2(wr[p]), acc);
+  acc = segment_sum<64>(acc);
+  if (lane == 0) out[(int64_t)t * outputs + e] = acc;
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+WM_EXPORT int wm_route_softmax_topk(const float* logits, int32_t tokens, int32_t experts, int32_t k,
+                                    int32_t norm_topk_prob, int32_t* indices, float* weights, float* probabilities,
+                                    void* stream) {
+  return guarded([&] {
+    if (tokens < 0) fail("wm_route_softmax_topk: negative token count");
+    if (experts < 1 || experts > 64 * ROUTE_MAX_PER_LANE) fail("wm_route_softmax_topk: experts must be in 1..1024");
+    if (k < 1 || k > ROUTE_MAX_K || k > experts) fail("wm_route_softmax_topk: k must be in 1..min(32, experts)");
+    if (tokens == 0) return;
+    if (!logits || !indices || !weights) fail("wm_route_softmax_topk: null pointer");
+    hipLaunchKernelGGL(route_softmax_topk_kernel, dim3(tokens), dim3(64), 0, as_stream(stream), logits, tokens,
+                       experts, k, norm_topk_prob, indices, weights, probabilities);
+    check_launch("route_softmax_topk");
+  });
+}
+
+WM_EXPORT int wm_route_scored(const float* logits, const float* bias, int32_t tokens, int32_t experts, int32_t k,
+                              int32_t func, float route_scale, int32_t norm_topk_prob, int32_t n_groups,
+                              int32_t topk_groups, int32_t* indices, float* weights, void* stream) {
+  return guarded([&] {
+    if (tokens < 0) fail("wm_route_scored: negative token count");
+    if (experts < 1 || experts > 64 * ROUTE_MAX_PER_LANE) fail("wm_route_scored: experts must be in 1..1024");
+    if (k < 1 || k > ROUTE_MAX_K || k > experts) fail("wm_route_scored: k must be in 1..min(32, experts)");
+    if (func < 0 || func > 2) fail("wm_route_scored: func must be 0 (softmax), 1 (sigmoid) or 2 (sqrt-softplus)");
+    if (n_groups < 1 || n_groups > 64 || experts % n_groups) fail("wm_route_scored: n_groups must divide experts (<= 64)");
+    if (n_groups > 1 && experts / n_groups < 2) fail("wm_route_scored: groups need at least two experts");
+    if (topk_groups < 1 || topk_groups > n_groups) fail("wm_route_scored: topk_groups must be in 1..n_groups");
+    if (n_groups > 1 && k > topk_groups * (experts / n_groups)) fail("wm_route_scored: k exceeds the kept groups' experts");
+    if (tokens == 0) return;
+    if (!logits || !indices || !weights) fail("wm_route_scored: null pointer");
+    hipLaunchKernelGGL(route_scored_kernel, dim3(tokens), dim3(64), 0, as_stream(stream), logits, bias, tokens, experts,
+                       k, func, route_scale, norm_topk_prob, n_groups, topk_groups, indices, weights);
+    check_launch("route_scored");
+  });
+}
+
+WM_EXPORT int wm_linear_bf16(const void* x, const void* w, int32_t tokens, int32_t hidden, int32_t outputs, float* out,
+                             void* stream) {
+  return guarded([&] {
+    if (tokens < 0 || outputs < 0 || hidden < 2 || hidden % 2) fail("wm_linear_bf16: bad shape");
+    if (tokens == 0 || outputs == 0) return;
+    if (!x || !w || !out) fail("wm_linear_bf16: null pointer");
+    hipLaunchKernelGGL(linear_bf16_kernel, dim3((outputs + 3) / 4, tokens), dim3(256), 0, as_stream(stream),
+                       (const uint32_t*)x, (const uint32_t*)w, tokens, hidden, outputs, out);
+    check_launch("linear_bf16");
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// Shared device/host helpers of libwhallm_moe (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/whallm_moe.h"
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 wm_bf16x2;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 wm_bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float wm_f32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float wm_f32x2;
+
+namespace wm {
+
+// ------------------------------------------------------------------ host error state
+void set_error(const std::string& message);
+void clear_error();
+
+// Runs `body`; a thrown std::exception becomes status 1 with its message
+// (Native/QwenNative/capi.mm:20-37 turns exceptions into a status the same way).
+template <typename Body>
+int guarded(Body body) {
+  try {
+    clear_error();
+    body();
+    return 0;
+  } catch (const std::exception& e) {
+    set_error(e.what());
+    return 1;
+  } catch (...) {
+    set_error("unknown error");
+    return 1;
+  }
+}
+
+[[noreturn]] void fail(const std::string& message);
+void check_hip(hipError_t status, const char* what);
+// Raises if the last launch failed (bad configuration, missing code object).
+void check_launch(const char* kernel);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------------ device helpers
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// E8M0 byte -> 2^(b - 127) as the float whose exponent field is b. Used only as
+// the scale operand of the gfx950 scaled converts, which read its exponent field:
+// byte 0 decodes to 2^-127 and 255 to NaN (OCP MX), bit-exact with
+// oracle/formats.py e8m0_value over all 256 bytes.
+__device__ __forceinline__ float e8m0_scale_operand(uint32_t b) { return __uint_as_float(b << 23); }
+
+// E2M1 magnitude table as fp32 bit patterns, index = code & 7.
+__device__ __forceinline__ float e2m1_to_f32(uint32_t code) {
+  // 0, .5, 1, 1.5, 2, 3, 4, 6: exponent/mantissa built from the 3 magnitude bits.
+  uint32_t m = code & 7u;
+  uint32_t e = m >> 1, man = m & 1u;
+  // e == 0: subnormal E2M1 (0 or 0.5); else (1 + man/2) * 2^(e-1).
+  uint32_t bits = e ? (((e + 126u) << 23) | (man << 22)) : (man ? 0x3f000000u : 0u);
+  return __uint_as_float(bits | ((code & 8u) << 28));
+}
+
+// Eight E2M1 nibbles of one word as four bf16 pairs (nibbles 2j, 2j+1 in pair j),
+// each times `scale` (a power of two). gfx950 V_CVT_SCALEF32_PK_BF16_FP4.
+__device__ __forceinline__ void fp4x8_to_bf16(uint32_t word, float scale, wm_bf16x2 out[4]) {
+  out[0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+  out[1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+  out[2] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+  out[3] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+}
+
+// bf16 pair . bf16 pair + acc (fp32), gfx950 V_DOT2_F32_BF16.
+__device__ __forceinline__ float dot2_bf16(wm_bf16x2 a, wm_bf16x2 b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
+}
+
+__device__ __forceinline__ wm_bf16x2 bits_to_bf16x2(uint32_t u) { return __builtin_bit_cast(wm_bf16x2, u); }
+__device__ __forceinline__ uint32_t bf16x2_to_bits(wm_bf16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// E4M3FN byte -> fp32 (Sources/DeepSeekRepack/MXFP4.swift:96-107): built from bits,
+// subnormals exact; 0x7f / 0xff -> NaN.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float mag;
+  if (e == 0) mag = (float)m * (1.0f / 512.0f);
+  else if (e == 15 && m == 7) mag = __uint_as_float(0x7fc00000u);
+  else mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (b & 0x80u) ? -mag : mag;
+}
+
+// Sum over `width` consecutive lanes (width a power of two <= 64), result in every lane.
+template <int WIDTH>
+__device__ __forceinline__ float segment_sum(float v) {
+#pragma unroll
+  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+  return v;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+}  // namespace wm

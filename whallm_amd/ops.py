@@ -1,0 +1,275 @@
+"""Torch-facing calls into libwhallm_moe: device tensors in, device tensors out.
+
+Every function requires CUDA (HIP) tensors and enqueues on the current torch
+stream; nothing here computes on the CPU or falls back to torch math.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import MXFP4ExpertsC
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _require_device(*tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("whallm_amd ops take device (HIP) tensors")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError("all tensors must be on one device")
+    if device is None:
+        raise ValueError("no device tensor given")
+    return device
+
+
+def _contig(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    return t.contiguous()
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ----------------------------------------------------------------------------- expert tables
+
+@dataclass(frozen=True)
+class MXFP4Experts:
+    """Device regions of a set of MXFP4 experts, addressed as base + slot * stride.
+
+    The four tensors are the reference's Qwen blob regions (manifest.py:37-42):
+    gate_up u32 [.., 2I, H/8], gate_up_scales u8 [.., 2I, H/32], down u32
+    [.., H, I/8], down_scales u8 [.., H, I/32], with a leading expert/slot axis
+    (QwenBatchedExperts, expert_cache.py:70-75) or none for a single expert
+    (QwenExpertWeights, :62-67). ``slots`` (int32 [E]) maps expert -> slot when
+    the regions are a slot pool rather than a whole layer.
+    """
+    gate_up: torch.Tensor
+    gate_up_scales: torch.Tensor
+    down: torch.Tensor
+    down_scales: torch.Tensor
+    slots: torch.Tensor | None = None
+    experts: int | None = None
+    up_first: bool = False
+    swiglu_limit: float = 0.0
+
+    @property
+    def hidden(self) -> int:
+        return self.gate_up.shape[-1] * 8
+
+    @property
+    def inter(self) -> int:
+        return self.gate_up.shape[-2] // 2
+
+    @property
+    def count(self) -> int:
+        if self.experts is not None:
+            return self.experts
+        return self.gate_up.shape[0] if self.gate_up.dim() == 3 else 1
+
+    def c_struct(self) -> MXFP4ExpertsC:
+        def stride(t: torch.Tensor) -> int:
+            return t.stride(0) * t.element_size() if t.dim() == 3 else 0
+
+        for name, t, dt in (("gate_up", self.gate_up, torch.int32), ("down", self.down, torch.int32)):
+            if t.dtype not in (torch.int32, torch.uint32):
+                raise ValueError(f"{name} must hold 32-bit words, got {t.dtype}")
+            if t.stride(-1) != 1 or t.stride(-2) != t.shape[-1]:
+                raise ValueError(f"{name} rows must be contiguous")
+        for name, t in (("gate_up_scales", self.gate_up_scales), ("down_scales", self.down_scales)):
+            if t.dtype != torch.uint8:
+                raise ValueError(f"{name} must be uint8")
+            if t.stride(-1) != 1 or t.stride(-2) != t.shape[-1]:
+                raise ValueError(f"{name} rows must be contiguous")
+        H, I = self.hidden, self.inter
+        if self.down.shape[-2:] != (H, I // 8) or self.gate_up_scales.shape[-2:] != (2 * I, H // 32) \
+                or self.down_scales.shape[-2:] != (H, I // 32):
+            raise ValueError("expert region shapes do not agree")
+        return MXFP4ExpertsC(
+            self.gate_up.data_ptr(), self.gate_up_scales.data_ptr(), self.down.data_ptr(), self.down_scales.data_ptr(),
+            stride(self.gate_up), stride(self.gate_up_scales), stride(self.down), stride(self.down_scales),
+            0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
+            float(self.swiglu_limit))
+
+    def tensors(self):
+        return (self.gate_up, self.gate_up_scales, self.down, self.down_scales, self.slots)
+
+
+# ----------------------------------------------------------------------------- formats
+
+def dequant_mxfp4(packed: torch.Tensor, scales: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """[.., O, K/8] words + [.., O, K/32] E8M0 -> [.., O, K] (dequant.py:63-68, exact)."""
+    device = _require_device(packed, scales)
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("dtype must be float32 or bfloat16")
+    packed = packed.contiguous()
+    scales = _contig(scales, torch.uint8, "scales")
+    cols = packed.shape[-1] * 8
+    rows = packed.numel() // packed.shape[-1] if packed.numel() else 0
+    if scales.shape[-1] * 32 != cols or scales.numel() != rows * (cols // 32):
+        raise ValueError("scales do not match the packed weights")
+    out = torch.empty(*packed.shape[:-1], cols, dtype=dtype, device=device)
+    _lib.call("wm_dequant_mxfp4", _ptr(packed), _ptr(scales), rows, cols, _ptr(out),
+              int(dtype == torch.bfloat16), _stream(device))
+    return out
+
+
+def dequant_fp8_blocks(weight: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """FP8 E4M3 [R, C] + fp32 [ceil(R/128), ceil(C/128)] -> fp32 (mimo/weights.py:17-43)."""
+    device = _require_device(weight, scales)
+    weight = _contig(weight, torch.uint8, "weight")
+    scales = _contig(scales, torch.float32, "scales")
+    R, C = weight.shape
+    if scales.shape != (-(-R // 128), -(-C // 128)):
+        raise ValueError("FP8 scale shape does not match 128x128 block padding")
+    out = torch.empty(R, C, dtype=torch.float32, device=device)
+    _lib.call("wm_dequant_fp8_blocks", _ptr(weight), _ptr(scales), R, C, _ptr(out), _stream(device))
+    return out
+
+
+# ----------------------------------------------------------------------------- routing
+
+def route_softmax_topk(logits: torch.Tensor, k: int, norm_topk_prob: bool = True, probabilities: bool = False):
+    """logits [.., E] fp32 -> (indices int32 [.., k], weights fp32 [.., k][, probabilities [.., E]])."""
+    device = _require_device(logits)
+    logits = _contig(logits, torch.float32, "logits")
+    E = logits.shape[-1]
+    T = logits.numel() // E if E else 0
+    idx = torch.empty(*logits.shape[:-1], k, dtype=torch.int32, device=device)
+    w = torch.empty(*logits.shape[:-1], k, dtype=torch.float32, device=device)
+    probs = torch.empty_like(logits) if probabilities else None
+    _lib.call("wm_route_softmax_topk", _ptr(logits), T, E, k, int(norm_topk_prob), _ptr(idx), _ptr(w), _ptr(probs),
+              _stream(device))
+    return (idx, w, probs) if probabilities else (idx, w)
+
+
+SCORE_FUNCS = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
+
+
+def route_scored(logits: torch.Tensor, bias: torch.Tensor | None, k: int, func: str = "sigmoid",
+                 route_scale: float = 1.0, norm_topk_prob: bool = True, n_groups: int = 1, topk_groups: int = 1):
+    """DeepSeek routing (deepseek_v41/moe.py:58-74, + DeepSeek-V3 group-limited selection)."""
+    device = _require_device(logits, bias)
+    logits = _contig(logits, torch.float32, "logits")
+    if bias is not None:
+        bias = _contig(bias, torch.float32, "bias")
+    E = logits.shape[-1]
+    T = logits.numel() // E if E else 0
+    idx = torch.empty(*logits.shape[:-1], k, dtype=torch.int32, device=device)
+    w = torch.empty(*logits.shape[:-1], k, dtype=torch.float32, device=device)
+    _lib.call("wm_route_scored", _ptr(logits), _ptr(bias), T, E, k, SCORE_FUNCS[func], float(route_scale),
+              int(norm_topk_prob), n_groups, topk_groups, _ptr(idx), _ptr(w), _stream(device))
+    return idx, w
+
+
+def linear_bf16(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """x [.., H] bf16 @ weight [O, H]^T bf16 -> fp32 [.., O] (the router linear)."""
+    device = _require_device(x, weight)
+    x = _contig(x, torch.bfloat16, "x")
+    weight = _contig(weight, torch.bfloat16, "weight")
+    H = x.shape[-1]
+    O = weight.shape[0]
+    if weight.shape[1] != H:
+        raise ValueError("weight does not match x")
+    T = x.numel() // H if H else 0
+    out = torch.empty(*x.shape[:-1], O, dtype=torch.float32, device=device)
+    _lib.call("wm_linear_bf16", _ptr(x), _ptr(weight), T, H, O, _ptr(out), _stream(device))
+    return out
+
+
+# ----------------------------------------------------------------------------- permute
+
+@dataclass
+class Permutation:
+    order: torch.Tensor
+    inverse: torch.Tensor
+    offsets: torch.Tensor
+    tiles: torch.Tensor
+    tile_count: torch.Tensor
+
+
+def permute(indices: torch.Tensor, experts: int, tile_rows: int = 128) -> Permutation:
+    """Stable expert sort of the flattened (token, k) pairs (see wm_permute)."""
+    device = _require_device(indices)
+    flat = _contig(indices, torch.int32, "indices").reshape(-1)
+    P = flat.numel()
+    order = torch.empty(P, dtype=torch.int32, device=device)
+    inverse = torch.empty(P, dtype=torch.int32, device=device)
+    offsets = torch.empty(experts + 1, dtype=torch.int32, device=device)
+    max_tiles = -(-P // tile_rows) + experts
+    tiles = torch.empty(max_tiles, 2, dtype=torch.int32, device=device)
+    count = torch.empty(1, dtype=torch.int32, device=device)
+    ws_bytes = _lib.load().wm_permute_workspace_size(P, experts)
+    ws = _workspace(ws_bytes, device)
+    _lib.call("wm_permute", _ptr(flat), P, experts, tile_rows, _ptr(order), _ptr(inverse), _ptr(offsets),
+              _ptr(tiles), _ptr(count), _ptr(ws), ws_bytes, _stream(device))
+    return Permutation(order, inverse, offsets, tiles, count)
+
+
+# ----------------------------------------------------------------------------- expert FFN
+
+def _check_indices(indices: torch.Tensor, experts: int, validate: bool) -> None:
+    if validate and indices.numel():
+        bad = (indices < 0) | (indices >= experts)
+        if bool(bad.any()):
+            raise ValueError("expert ID is outside the model")
+
+
+def moe_mxfp4(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, experts: MXFP4Experts,
+              shared: MXFP4Experts | None = None, shared_gate: torch.Tensor | None = None,
+              validate: bool = False) -> torch.Tensor:
+    """One MoE layer: y = sum_k w_k FFN_k(x) + sigmoid(x . g) FFN_shared(x); bf16 [.., H]."""
+    device = _require_device(x, indices, weights, *experts.tensors(), *(shared.tensors() if shared else ()),
+                             shared_gate)
+    x = _contig(x, torch.bfloat16, "x")
+    H = x.shape[-1]
+    T = x.numel() // H if H else 0
+    k = indices.shape[-1]
+    idx = _contig(indices, torch.int32, "indices").reshape(T, k)
+    w = _contig(weights, torch.float32, "weights").reshape(T, k)
+    _check_indices(idx, experts.count, validate)
+    sg = None if shared_gate is None else _contig(shared_gate, torch.bfloat16, "shared_gate").reshape(-1)
+    table = experts.c_struct()
+    sh = shared.c_struct() if shared is not None else None
+    ws_bytes = _lib.load().wm_moe_mxfp4_workspace_size(T, k, ctypes.byref(table))
+    ws = _workspace(ws_bytes, device)
+    y = torch.empty_like(x)
+    _lib.call("wm_moe_mxfp4", _ptr(x), T, _ptr(idx), _ptr(w), k, ctypes.byref(table),
+              ctypes.byref(sh) if sh is not None else None, _ptr(sg), _ptr(y), _ptr(ws), ws_bytes, _stream(device))
+    return y
+
+
+def experts_mxfp4(x: torch.Tensor, indices: torch.Tensor, experts: MXFP4Experts,
+                  validate: bool = False) -> torch.Tensor:
+    """Per-pair expert outputs in router order: [.., K, H] bf16 (StreamingExperts contract)."""
+    device = _require_device(x, indices, *experts.tensors())
+    x = _contig(x, torch.bfloat16, "x")
+    H = x.shape[-1]
+    T = x.numel() // H if H else 0
+    k = indices.shape[-1]
+    idx = _contig(indices, torch.int32, "indices").reshape(T, k)
+    _check_indices(idx, experts.count, validate)
+    table = experts.c_struct()
+    ws_bytes = _lib.load().wm_moe_mxfp4_workspace_size(T, k, ctypes.byref(table))
+    ws = _workspace(ws_bytes, device)
+    out = torch.empty(*x.shape[:-1], k, H, dtype=torch.bfloat16, device=device)
+    _lib.call("wm_experts_mxfp4", _ptr(x), T, _ptr(idx), k, ctypes.byref(table), _ptr(out), _ptr(ws), ws_bytes,
+              _stream(device))
+    return out

@@ -1,0 +1,78 @@
+"""Synthetic inputs of the benchmark configurations (random-init weights, no checkpoints).
+
+MXFP4 expert weights: E2M1 codes uniform over the 16 values (so packed bytes are
+uniform), E8M0 scale exponents uniform in [-8, -2] (bytes 119..125); activations
+bf16 N(0, 1); router logits N(0, 1). ``*_np`` builders use numpy's
+``default_rng(seed)`` (parity tests compare them against the oracle);
+``*_device`` builders fill HBM directly with a seeded torch generator (the
+full-size benchmark layers are tens of GB).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .ops import MXFP4Experts
+
+SCALE_LOW, SCALE_HIGH = 119, 125  # 2**-8 .. 2**-2
+
+
+def mxfp4_experts_np(rng: np.random.Generator, experts: int, hidden: int, inter: int) -> dict:
+    """Region-major arrays of ``experts`` experts (QwenBatchedExperts layout)."""
+    return {
+        "gate_up": rng.integers(0, 2**32, size=(experts, 2 * inter, hidden // 8), dtype=np.uint32),
+        "gate_up_scales": rng.integers(SCALE_LOW, SCALE_HIGH + 1, size=(experts, 2 * inter, hidden // 32),
+                                       dtype=np.uint8),
+        "down": rng.integers(0, 2**32, size=(experts, hidden, inter // 8), dtype=np.uint32),
+        "down_scales": rng.integers(SCALE_LOW, SCALE_HIGH + 1, size=(experts, hidden, inter // 32), dtype=np.uint8),
+    }
+
+
+def experts_to_device(arrays: dict, device, **kw) -> MXFP4Experts:
+    def t(a):
+        a = np.ascontiguousarray(a)
+        if a.dtype == np.uint32:
+            a = a.view(np.int32)
+        return torch.from_numpy(a).to(device)
+
+    return MXFP4Experts(t(arrays["gate_up"]), t(arrays["gate_up_scales"]), t(arrays["down"]),
+                        t(arrays["down_scales"]), **kw)
+
+
+def mxfp4_experts_device(experts: int, hidden: int, inter: int, device, generator: torch.Generator) -> MXFP4Experts:
+    """Region-major MXFP4 experts generated on the device."""
+    def words(*shape):
+        return torch.randint(-2**31, 2**31, shape, dtype=torch.int32, device=device, generator=generator)
+
+    def scales(*shape):
+        return torch.randint(SCALE_LOW, SCALE_HIGH + 1, shape, dtype=torch.uint8, device=device, generator=generator)
+
+    return MXFP4Experts(words(experts, 2 * inter, hidden // 8), scales(experts, 2 * inter, hidden // 32),
+                        words(experts, hidden, inter // 8), scales(experts, hidden, inter // 32))
+
+
+def bf16_normal_np(rng: np.random.Generator, shape, std: float = 1.0) -> np.ndarray:
+    """bf16 N(0, std) values as uint16 bit patterns (round to nearest even)."""
+    v = (rng.standard_normal(shape) * std).astype(np.float32)
+    bits = v.view(np.uint32).astype(np.uint64)
+    return (((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+
+
+def bf16_bits_to_tensor(bits: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device).view(torch.bfloat16)
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def zipf_bias(experts: int, s: float = 1.1, rng: np.random.Generator | None = None) -> np.ndarray:
+    """Per-expert logit bias log(p_e) for a Zipf(s) popularity over a random expert order:
+    adding it to N(0,1) logits makes the routed load imbalanced (prefill config)."""
+    ranks = np.arange(1, experts + 1, dtype=np.float64)
+    p = ranks ** -s
+    p /= p.sum()
+    bias = np.log(p).astype(np.float32)
+    if rng is not None:
+        bias = bias[rng.permutation(experts)]
+    return bias
