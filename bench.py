@@ -1,0 +1,336 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE expert path (one JSON line on stdout).
+
+Default workload ("c2-decode"): a Qwen3-Next-style
+48-layer stack of MXFP4 MoE layers (H 2048, 512 experts, I 512, top-10 + one
+always-on MXFP4 shared expert), one token per step, router logits N(0, 1), all
+weights resident in HBM (41 GB). A step = one token through the 48 layers,
+replayed from one HIP graph. ``--config c3-prefill`` runs one layer at a
+16,384-token prefill with Zipf(1.1)-skewed routing.
+
+Synthetic data (random-init weights of the configured shapes; no checkpoints).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
+FP4_PEAK_TFLOPS = 10100.0      # dense MXFP4 MFMA
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------------- workloads
+
+class DecodeStack:
+    """C2: 48-layer MXFP4 MoE decode, 1 token per step."""
+    name = "c2-decode"
+
+    def __init__(self, device, layers=48, hidden=2048, experts=512, inter=512, k=10, tokens=1, seed=0,
+                 impl="persistent"):
+        import whallm_amd as wa
+        from whallm_amd import synthetic as S
+        from whallm_amd.ops import MoEStack, PersistentDecodeStack
+        self.L, self.H, self.E, self.I, self.K, self.T = layers, hidden, experts, inter, k, tokens
+        self.device = device
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        log(f"[bench] generating {layers} layers x {experts} MXFP4 experts on device")
+        self.layers = [S.mxfp4_experts_device(experts, hidden, inter, device, g) for _ in range(layers)]
+        self.shared = [S.mxfp4_experts_device(1, hidden, inter, device, g) for _ in range(layers)]
+        self.gates = [(torch.randn(hidden, device=device, generator=g) * 0.02).to(torch.bfloat16)
+                      for _ in range(layers)]
+        self.impl = impl
+        if impl == "persistent":
+            self.stack = PersistentDecodeStack(self.layers, self.shared, self.gates, k=k)
+        else:
+            self.stack = MoEStack(self.layers, self.shared, self.gates, k=k)
+        self.logits = torch.empty(layers, tokens, experts, dtype=torch.float32, device=device)
+        self.residual = torch.empty(tokens, hidden, dtype=torch.float32, device=device)
+        self.x_out = torch.empty(tokens, hidden, dtype=torch.bfloat16, device=device)
+        self.gen = g
+        self.graph = None
+
+    # Bytes every step must move: 11 expert blobs per layer-token (10 routed + shared)
+    # plus the logits row (fp32) and the token's input and output rows (bf16).
+    def expert_bytes(self):
+        return 2 * self.I * self.H // 2 + 2 * self.I * self.H // 32 + self.H * self.I // 2 + self.H * self.I // 32
+
+    def algorithmic_bytes(self):
+        per_layer_token = (self.K + 1) * self.expert_bytes() + self.E * 4 + 2 * self.H * 2
+        return per_layer_token * self.L * self.T
+
+    def flops(self):
+        return 2 * 3 * self.H * self.I * (self.K + 1) * self.L * self.T
+
+    def tokens_per_step(self):
+        return self.T
+
+    def prepare_inputs(self, steps):
+        self.step_logits = torch.randn(steps, self.L, self.T, self.E, device=self.device, generator=self.gen)
+        self.step_embed = torch.randn(steps, self.T, self.H, device=self.device, generator=self.gen)
+
+    def _body(self):
+        if self.impl == "persistent":
+            self.stack(self.logits, self.residual.view(-1), self.x_out.view(-1))
+        else:
+            self.stack(self.logits, self.residual, self.x_out)
+
+    def check(self):
+        if self.impl == "persistent" and self.stack.status() != 0:
+            raise RuntimeError("persistent decode: a message exchange stalled (status word set)")
+
+    def capture(self):
+        self.logits.copy_(self.step_logits[0])
+        self.residual.copy_(self.step_embed[0])
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._body()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body()
+        torch.cuda.synchronize(self.device)
+
+    def step(self, i):
+        self.logits.copy_(self.step_logits[i])
+        self.residual.copy_(self.step_embed[i])
+        self.graph.replay()
+
+    def config(self):
+        return {"workload": "c2-decode: Qwen3-Next-style MXFP4 MoE decode, 48-layer stack, 1 token/step",
+                "hidden": self.H, "experts": self.E, "moe_intermediate": self.I, "top_k": self.K,
+                "shared_experts": 1, "shared_intermediate": self.I, "layers": self.L, "tokens_per_step": self.T,
+                "weights": "MXFP4 E2M1 + E8M0/32, codes uniform, scale exponents uniform [-8,-2]",
+                "router_logits": "N(0,1) per layer per step", "activations": "bf16",
+                "hbm_resident_weight_gb": round(self.L * (self.E + 1) * self.expert_bytes() / 1e9, 2)}
+
+    # -- CPU baseline: the numpy oracle on a bounded sample (one token, `layers` layers)
+    def cpu_baseline(self, budget_s: float):
+        from oracle import moe as M
+        from oracle import formats as F
+        from whallm_amd import synthetic as S
+        threads = len(os.sched_getaffinity(0))
+        logits = self.step_logits[0].cpu().numpy()       # [L, T, E]
+        x = F.bf16_round_f32(self.step_embed[0].cpu().numpy())
+        r = x.astype(np.float64)
+
+        def fetch(t: torch.Tensor, e):
+            a = t[e].cpu().numpy()
+            return a.view(np.uint32) if a.dtype == np.int32 else a
+
+        done = 0
+        elapsed = 0.0
+        with ThreadPoolExecutor(threads) as pool:
+            for l in range(self.L):
+                ids = [int(e) for e in M.topk_desc(logits[l], self.K)[0]]
+                ex = {e: M.MXFP4Expert(fetch(self.layers[l].gate_up, e), fetch(self.layers[l].gate_up_scales, e),
+                                       fetch(self.layers[l].down, e), fetch(self.layers[l].down_scales, e))
+                      for e in ids}
+                sh = M.MXFP4Expert(fetch(self.shared[l].gate_up, 0), fetch(self.shared[l].gate_up_scales, 0),
+                                   fetch(self.shared[l].down, 0), fetch(self.shared[l].down_scales, 0))
+                g = S.bf16_bits_to_f32(self.gates[l].view(torch.int16).cpu().numpy().view(np.uint16))
+                t0 = time.perf_counter()   # compute only: routing, 11 expert FFNs, combine, residual
+                xin = M.rms_norm(r)
+                idx, w = M.route_softmax_topk(logits[l], self.K)
+                outs = list(pool.map(lambda e: M.expert_ffn(xin, ex[e]), [int(e) for e in idx[0]]))
+                shared_out = M.expert_ffn(xin, sh)
+                gate = xin.astype(np.float64) @ g.astype(np.float64)
+                y = M.combine(np.stack(outs, axis=1), w, shared_out, gate)
+                r = r + F.bf16_round_f32(y)
+                elapsed += time.perf_counter() - t0
+                done += 1
+                if elapsed > budget_s:
+                    break
+        # The sample is `done` layer-tokens of the 48-layer stack (expert bytes fetched beforehand).
+        per_token_s = elapsed / done * self.L
+        return {"value": round(1.0 / per_token_s, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"1 token through {done} of {self.L} layers (numpy fp32 dequant-then-matmul oracle, "
+                          f"{threads} threads over experts), scaled to the 48-layer stack"}
+
+
+class Prefill:
+    """C3: one MXFP4 MoE layer at a 16,384-token prefill, Zipf(1.1)-skewed routing."""
+    name = "c3-prefill"
+
+    def __init__(self, device, hidden=2048, experts=512, inter=512, k=10, tokens=16384, seed=0):
+        from whallm_amd import synthetic as S
+        self.H, self.E, self.I, self.K, self.T = hidden, experts, inter, k, tokens
+        self.device = device
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        self.experts = S.mxfp4_experts_device(experts, hidden, inter, device, g)
+        self.shared = S.mxfp4_experts_device(1, hidden, inter, device, g)
+        self.gate = (torch.randn(hidden, device=device, generator=g) * 0.02).to(torch.bfloat16)
+        rng = np.random.default_rng(seed)
+        bias = torch.from_numpy(S.zipf_bias(experts, 1.1, rng)).to(device)
+        self.logits = torch.randn(tokens, experts, device=device, generator=g) + bias
+        self.x = torch.randn(tokens, hidden, device=device, generator=g).to(torch.bfloat16)
+        self.graph = None
+
+    def flops(self):
+        return 2 * 3 * self.H * self.I * (self.K + 1) * self.T
+
+    def algorithmic_bytes(self):
+        blob = 3 * self.H * self.I // 2 + 3 * self.H * self.I // 32
+        return (self.E + 1) * blob + self.T * self.H * 2 * 2 + self.T * self.E * 4
+
+    def tokens_per_step(self):
+        return self.T
+
+    def prepare_inputs(self, steps):
+        pass
+
+    def _body(self):
+        import whallm_amd as wa
+        idx, w = wa.route_softmax_topk(self.logits, self.K)
+        self.y = wa.moe_mxfp4(self.x, idx, w, self.experts, self.shared, self.gate)
+
+    def capture(self):
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._body()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body()
+        torch.cuda.synchronize(self.device)
+
+    def step(self, i):
+        self.graph.replay()
+
+    def config(self):
+        return {"workload": "c3-prefill: Qwen3-Next-style MXFP4 MoE layer, 16384-token prefill, Zipf(1.1) routing",
+                "hidden": self.H, "experts": self.E, "moe_intermediate": self.I, "top_k": self.K,
+                "shared_experts": 1, "tokens": self.T, "activations": "bf16",
+                "compute": "bf16 MFMA (16x16x32) with FP4->bf16 dequant in registers"}
+
+    def cpu_baseline(self, budget_s: float):
+        from oracle import moe as M
+        from whallm_amd import synthetic as S
+        threads = len(os.sched_getaffinity(0))
+        # Sample: the first tokens of the prompt, one expert group at a time, within the budget.
+        sample = 64
+        logits = self.logits[:sample].cpu().numpy()
+        x = self.x[:sample].float().cpu().numpy()
+        idx, w = M.route_softmax_topk(logits, self.K)
+
+        def fetch(t, e):
+            a = t[e].cpu().numpy()
+            return a.view(np.uint32) if a.dtype == np.int32 else a
+
+        experts = {int(e): M.MXFP4Expert(fetch(self.experts.gate_up, e), fetch(self.experts.gate_up_scales, e),
+                                         fetch(self.experts.down, e), fetch(self.experts.down_scales, e))
+                   for e in np.unique(idx)}
+        started = time.perf_counter()
+        with ThreadPoolExecutor(threads) as pool:
+            flat = idx.reshape(-1)
+            groups = [(e, np.flatnonzero(flat == e)) for e in np.unique(flat)]
+            list(pool.map(lambda g: M.expert_ffn(x[g[1] // self.K], experts[int(g[0])]), groups))
+        elapsed = time.perf_counter() - started
+        return {"value": round(sample / elapsed, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"{sample} prompt tokens x top-{self.K} routed experts (numpy fp32 dequant-then-matmul "
+                          f"oracle, {threads} threads), shared expert excluded"}
+
+
+WORKLOADS = {"c2-decode": DecodeStack, "c3-prefill": Prefill}
+
+
+# ----------------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2-decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-impl", default="persistent", choices=["persistent", "layers"],
+                    help="c2-decode: one persistent kernel per token, or the per-layer kernel chain")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    wl = (DecodeStack(device, impl=args.decode_impl) if args.config == "c2-decode"
+          else WORKLOADS[args.config](device))
+    total = args.warmup + args.steps
+    wl.prepare_inputs(total)
+    wl.capture()
+    for i in range(args.warmup):
+        wl.step(i)
+    torch.cuda.synchronize(device)
+
+    stream = torch.cuda.current_stream(device)
+    start_ev = torch.cuda.Event(enable_timing=True)
+    end_ev = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start_ev.record(stream)
+    for i in range(args.warmup, total):
+        wl.step(i)
+    end_ev.record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    gpu_ms = start_ev.elapsed_time(end_ev)
+    if hasattr(wl, "check"):
+        wl.check()
+    ms_per_step = gpu_ms / args.steps
+    value = wl.tokens_per_step() / (ms_per_step / 1e3)
+
+    if isinstance(wl, DecodeStack):
+        achieved = wl.algorithmic_bytes() / (ms_per_step / 1e3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": ("decode_persistent_kernel (one launch = one token through 48 layers)"
+                               if wl.impl == "persistent" else
+                               "decode step: 48 x (route, gate_up_act, down_combine, residual_rmsnorm)"),
+                    "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
+        metric = "MoE decode tok/s (48-layer MXFP4 stack, 1 token/step)"
+    else:
+        tflops = wl.flops() / (ms_per_step / 1e3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                    "frac_of_fp4_peak": round(tflops / FP4_PEAK_TFLOPS, 4),
+                    "kernel": "prefill layer: route, permute, grouped gate_up, grouped down, combine",
+                    "algorithmic_flops_per_launch": wl.flops()}
+        metric = "MoE prefill tok/s (one MXFP4 layer, 16K tokens)"
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU baseline")
+        cpu = wl.cpu_baseline(args.cpu_budget)
+        cpu["host"] = platform.processor() or platform.machine()
+
+    line = {
+        "metric": metric, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init MXFP4 weights, N(0,1) logits/inputs)",
+        "config": wl.config(), "roofline": roofline, "cpu_baseline": cpu,
+        "wall_s_timed_region": round(wall, 4),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -137,6 +137,70 @@ WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* ind
                                const wm_mxfp4_experts* experts, void* out, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* ---- decode stack ---------------------------------------------------------
+ * r[t] += y[t] (y nullable), x[t] = bf16(r[t] / sqrt(mean(r[t]^2) + eps)): the
+ * pre-norm residual between MoE layers (DecoderLayer.feed_forward, qwen4_exp.py:1127-1149,
+ * without attention). residual fp32 [T, H], y and x bf16 [T, H]. */
+WM_EXPORT int wm_residual_rmsnorm(float* residual, const void* y, int32_t tokens, int32_t hidden, float eps,
+                                  void* x, void* stream);
+/* `layers` MoE layers chained as x_l = rmsnorm(r_l), r_{l+1} = r_l + MoE_l(x_l), routing
+ * from logits [layers, T, E] on the device (no host synchronisation; graph-capturable).
+ * experts / shared / shared_gates are host arrays of `layers` entries (shared and
+ * shared_gates nullable). The per-layer loop of the native engine
+ * (Native/QwenNative/engine.mm:1567-1588, experts() at :2073-2236). x_out (nullable)
+ * receives the last rmsnorm(r_L). */
+WM_EXPORT size_t wm_moe_stack_mxfp4_workspace_size(int32_t tokens, int32_t k, const wm_mxfp4_experts* experts);
+WM_EXPORT int wm_moe_stack_mxfp4(const float* logits, int32_t layers, int32_t tokens, int32_t k,
+                                 int32_t norm_topk_prob, const wm_mxfp4_experts* experts,
+                                 const wm_mxfp4_experts* shared, const void* const* shared_gates,
+                                 float* residual, float eps, void* x_out, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* ---- persistent decode (one kernel per token through every layer) ----------
+ * Per-layer descriptor of the persistent decode kernel. Routed experts keep the
+ * reference gate_up region ([2I, H/8] u32 + [2I, H/32] u8 per expert); the down
+ * region is repacked slice-major for it (wm_repack_down_slices): [8][H][I/16 bytes]
+ * words and [8][H][I/256] scale bytes per expert, slice s holding columns
+ * [s*I/8, (s+1)*I/8). The shared expert (one, always on) uses the same layouts and
+ * is gated by sigmoid(x . shared_gate) (NULL gate: weight 1). */
+typedef struct wm_decode_layer {
+  const void* gate_up;
+  const void* gate_up_scales;
+  const void* down;               /* slice-major */
+  const void* down_scales;        /* slice-major */
+  int64_t gate_up_stride, gate_up_scales_stride, down_stride, down_scales_stride;
+  const int32_t* slots;           /* NULL: slot = expert */
+  const void* shared_gate_up;
+  const void* shared_gate_up_scales;
+  const void* shared_down;        /* slice-major */
+  const void* shared_down_scales; /* slice-major */
+  const void* shared_gate;        /* bf16 [H] or NULL */
+} wm_decode_layer;
+
+/* Repacks `experts` down regions from the reference row-major layout ([H, I/8] u32 +
+ * [H, I/32] u8, consecutive experts `src_stride` / `src_scales_stride` bytes apart) into
+ * the slice-major layout above (dst experts dense: H*I/2 and H*I/32 bytes apart). */
+WM_EXPORT int wm_repack_down_slices(const void* src, const void* src_scales, int64_t src_stride,
+                                    int64_t src_scales_stride, int32_t experts, int32_t hidden, int32_t inter,
+                                    void* dst, void* dst_scales, void* stream);
+
+/* Bytes of the persistent decode state (message buffers and per-workgroup epochs);
+ * the caller zero-fills it once and passes the same buffer to every call. */
+WM_EXPORT size_t wm_decode_state_size(int32_t layers, int32_t experts);
+/* One token through `layers` MoE layers in one persistent launch of 256 workgroups
+ * (8 XCDs x 32): x_l = rmsnorm(r_l); r_{l+1} = r_l + bf16(MoE_l(x_l)) with top-k
+ * softmax routing from logits [layers, E] (fp32). layers_dev: device array of
+ * wm_decode_layer. residual fp32 [H] in/out; x_out (nullable) bf16 rmsnorm(r_L).
+ * Supports hidden 2048, inter 512, k <= 11, one token. A stalled
+ * exchange ends the kernel after a bounded wait and makes wm_decode_status report it.
+ * Calls that share a state buffer must be stream-ordered. */
+WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers, int32_t experts, int32_t k,
+                                             int32_t hidden, int32_t inter, const wm_decode_layer* layers_dev,
+                                             float* residual, float eps, void* x_out, void* state,
+                                             size_t state_bytes, void* stream);
+/* Device word of the state buffer that a stalled exchange sets (0 = healthy). */
+WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts);
+
 #ifdef __cplusplus
 }
 #endif

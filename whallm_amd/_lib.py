@@ -33,6 +33,18 @@ class FP8ExpertsC(ctypes.Structure):
     ]
 
 
+class DecodeLayerC(ctypes.Structure):
+    """wm_decode_layer (include/whallm_moe.h)."""
+    _fields_ = [
+        ("gate_up", c_void_p), ("gate_up_scales", c_void_p), ("down", c_void_p), ("down_scales", c_void_p),
+        ("gate_up_stride", c_int64), ("gate_up_scales_stride", c_int64),
+        ("down_stride", c_int64), ("down_scales_stride", c_int64),
+        ("slots", c_void_p),
+        ("shared_gate_up", c_void_p), ("shared_gate_up_scales", c_void_p),
+        ("shared_down", c_void_p), ("shared_down_scales", c_void_p), ("shared_gate", c_void_p),
+    ]
+
+
 _P = c_void_p
 _SIGNATURES = {
     "wm_last_error": (c_char_p, []),
@@ -49,6 +61,15 @@ _SIGNATURES = {
     "wm_moe_mxfp4": (c_int, [_P, c_int32, _P, _P, c_int32, POINTER(MXFP4ExpertsC), POINTER(MXFP4ExpertsC), _P,
                              _P, _P, c_size_t, _P]),
     "wm_experts_mxfp4": (c_int, [_P, c_int32, _P, c_int32, POINTER(MXFP4ExpertsC), _P, _P, c_size_t, _P]),
+    "wm_residual_rmsnorm": (c_int, [_P, _P, c_int32, c_int32, c_float, _P, _P]),
+    "wm_moe_stack_mxfp4_workspace_size": (c_size_t, [c_int32, c_int32, POINTER(MXFP4ExpertsC)]),
+    "wm_moe_stack_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, POINTER(MXFP4ExpertsC),
+                                   POINTER(MXFP4ExpertsC), _P, _P, c_float, _P, _P, c_size_t, _P]),
+    "wm_repack_down_slices": (c_int, [_P, _P, c_int64, c_int64, c_int32, c_int32, c_int32, _P, _P, _P]),
+    "wm_decode_state_size": (c_size_t, [c_int32, c_int32]),
+    "wm_decode_status_offset": (c_size_t, [c_int32, c_int32]),
+    "wm_moe_decode_persistent_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, c_float,
+                                               _P, _P, c_size_t, _P]),
 }
 
 _lib = None

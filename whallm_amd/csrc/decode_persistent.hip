@@ -1,0 +1,659 @@
+// Persistent decode: one launch carries one token through every MoE layer.
+//
+// The per-layer kernel chain (decode.hip, stack.hip) is latency-bound at one token:
+// each kernel boundary and each dependent HBM round trip costs microseconds while
+// a layer's 18 MB of weights streams in ~2.3 us. Here 256 workgroups (8 XCDs x 32,
+// the hardware XCC of block b is b % 8) stay resident and exchange small messages:
+//
+//   A  (per XCD x): act[k][i] = silu(x . Wg_k[i]) * (x . Wu_k[i]) for i in the XCD's
+//      64-wide slice [64x, 64x+64) of every selected expert k (10 routed + shared).
+//      A tile is 8 gate rows + the 8 matching up rows; one wave reduces it over the
+//      full hidden width with 16 scaled MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4):
+//      the weights enter as stored (E2M1 codes, one E8M0 scale per 32 = one MFMA
+//      lane's block), x enters as two E4M3 terms (hi + lo, each with its own E8M0
+//      scale) which together reproduce every bf16 x exactly when |x| >= 2^-13 max|x|.
+//   B  (per XCD x, rows 64j..64j+63 per workgroup j): split-K partial of the down
+//      projection over the slice, weighted by the routing weight:
+//      p_x[o] = sum_k w_k act_k[slice] . Wd_k[o][slice], again on scaled MFMAs, with
+//      w_k act_k split into three E4M3 terms (12 significant bits) under a per-32
+//      scale; the down weights are repacked slice-major so each row-slice is 32
+//      contiguous bytes.
+//   R  r[o] += bf16(sum_x p_x[o]) (fixed x order, so every XCD gets the same r),
+//      then the XCD gathers the full r and its rmsnorm statistics for the next layer.
+//
+// Each exchange has low fan-in (act: within the XCD; partials: the 8 workgroups
+// sharing a row block; r: within the XCD). Messages are 64-bit words carrying the
+// value and an epoch, written and read with agent-scope relaxed atomics, so a
+// reader polls the data itself: no flags, no grid barriers, no L2-wide fences.
+// Weight loads run a phase ahead: the A tile of layer l+1 is in flight from the end
+// of phase A(l), the down rows of layer l+1 from the end of layer l's phase B.
+//
+// Replaces, for the decode case, the per-layer host loop of the native engine
+// (Native/QwenNative/engine.mm:1567-1588 -> experts() :2073-2236) and its host
+// top-k (:2086-2100); routing runs in the launch prologue from the given logits.
+#include <cmath>
+
+#include "moe_internal.h"
+#include "route_device.h"
+
+namespace wm {
+
+constexpr int DS_H = 2048;            // hidden
+constexpr int DS_I = 512;             // expert intermediate
+constexpr int DS_X = 8;               // XCDs
+constexpr int DS_J = 32;              // workgroups per XCD
+constexpr int DS_WGS = DS_X * DS_J;   // 256
+constexpr int DS_SLICE = DS_I / DS_X; // 64 intermediate columns per XCD
+constexpr int DS_ROWS = DS_H / DS_J;  // 64 output rows per workgroup
+constexpr int DS_NE_MAX = 12;         // routed + shared experts per layer
+constexpr int DS_KB = DS_H / 128;     // K-steps of a phase-A tile (128 per MFMA)
+constexpr int DS_KB_B = DS_NE_MAX / 2;  // K-steps of phase B (two 64-wide expert slices each)
+constexpr uint32_t DS_SPIN_LIMIT = 1u << 20;
+constexpr int DS_MAX_LAYERS = 128;    // layer descriptors kept in LDS
+constexpr int DS_CW = 3;                      // compute waves (prefetch weights and compute)
+constexpr int DS_THREADS = (DS_CW + 1) * 64;  // + one message wave (polls and publishes)
+constexpr int DS_FMT_FP8 = 0, DS_FMT_FP4 = 4;  // MFMA operand formats (E4M3, E2M1)
+
+typedef int ds_v8i __attribute__((ext_vector_type(8)));
+typedef float ds_v4f __attribute__((ext_vector_type(4)));
+
+struct DSLayout {
+  size_t route, act, part, r, epoch, status, total;
+};
+
+__host__ __device__ inline DSLayout ds_layout(int layers) {
+  DSLayout d;
+  size_t at = 0;
+  d.route = at;  at += (size_t)layers * 32 * 8;
+  d.act = at;    at += (size_t)2 * DS_X * DS_NE_MAX * DS_SLICE * 8;
+  d.part = at;   at += (size_t)2 * DS_X * DS_H * 8;
+  d.r = at;      at += (size_t)2 * DS_X * DS_H * 8;
+  d.epoch = at;  at += (size_t)DS_WGS * 4;
+  d.status = at; at += 256;
+  d.total = at;
+  return d;
+}
+
+__device__ __forceinline__ void ll_put(uint64_t* p, uint32_t bits, uint32_t epoch) {
+  __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reads base[first + m * stride] (m < N, index < limit) with all N loads in flight,
+// re-polls only the words that do not carry `epoch` yet, then hands each value to
+// store(index, bits). Bounded: after DS_SPIN_LIMIT rounds it raises the status word.
+template <int N, typename Store>
+__device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int stride, int limit, uint32_t epoch,
+                                          uint32_t* status, bool& ok, Store store) {
+  uint64_t v[N];
+#pragma unroll
+  for (int m = 0; m < N; ++m) {
+    int i = first + m * stride;
+    v[m] = i < limit ? __hip_atomic_load(&base[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)epoch << 32;
+  }
+  uint32_t spins = 0;
+  while (ok) {
+    bool ready = true;
+#pragma unroll
+    for (int m = 0; m < N; ++m) ready &= (uint32_t)(v[m] >> 32) == epoch;
+    if (ready) break;
+    if (++spins > DS_SPIN_LIMIT) {
+      __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = false;
+      break;
+    }
+    if ((spins & 255) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);  // leave the CU's memory pipeline to the weight streams
+#pragma unroll
+    for (int m = 0; m < N; ++m) {
+      int i = first + m * stride;
+      if (i < limit && (uint32_t)(v[m] >> 32) != epoch)
+        v[m] = __hip_atomic_load(&base[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < N; ++m) {
+    int i = first + m * stride;
+    if (i < limit) store(i, (uint32_t)v[m]);
+  }
+}
+
+// Phase timestamps for a profiling build (expands to nothing in the library).
+#ifndef WM_DS_TRACE
+#define WM_DS_TRACE(layer, point)
+#endif
+
+__device__ __forceinline__ float bf16_round_f(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// ---- E4M3 term splitting -------------------------------------------------------
+// E8M0 exponent s that puts amax / 2^(s-127) in [128, 256) (E4M3's largest finite is
+// 448); at least 1 so the scale stays a normal number. amax 0 gives 1.
+__device__ __forceinline__ int e4m3_term_exponent(float amax) {
+  int be = (int)((__float_as_uint(amax) >> 23) & 0xff);
+  return be - 7 > 1 ? be - 7 : 1;
+}
+// 2^(e-127) for a biased exponent e in 1..254.
+__device__ __forceinline__ float pow2_biased(int e) { return __uint_as_float((uint32_t)e << 23); }
+// Two f32 -> E4M3 (round to nearest even) into bytes 0..1 of a word.
+__device__ __forceinline__ uint32_t e4m3_pair(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+}
+template <int SEL>
+__device__ __forceinline__ float e4m3_byte(uint32_t w) { return __builtin_amdgcn_cvt_f32_fp8((int)w, SEL); }
+
+// Workgroup state shared by the two roles.
+struct DSShared {
+  __attribute__((aligned(16))) float r[DS_H];
+  // x as E4M3 terms in MFMA B-operand order: [term hi/lo][K-step][lane group][32 bytes]
+  __attribute__((aligned(16))) uint8_t xb[2][DS_KB][4][32];
+  __attribute__((aligned(16))) float act[DS_NE_MAX][DS_SLICE];
+  // phase-B operand staging per compute wave and K-step: [term][lane group][32 bytes]
+  __attribute__((aligned(16))) uint8_t bstage[DS_CW][2][3][4][32];
+  __attribute__((aligned(16))) float tile_out[DS_CW][16];
+  __attribute__((aligned(16))) float partb[DS_CW][3][DS_ROWS];
+  int slot[DS_MAX_LAYERS][16];
+  float w[DS_MAX_LAYERS][16];
+  wm_decode_layer desc[DS_MAX_LAYERS];
+  float gate;   // sigmoid(x . g) of the current layer
+  float eps;
+  float inv;    // 1 / rms(r) of the current layer
+  float xmax;   // max |bf16(r * inv)|
+  int failures;
+};
+
+// Per-launch constants of one workgroup.
+struct DSCtx {
+  int L, K, NE, x, j, lane, wave;
+  uint32_t base;
+  uint64_t *route_ll, *act_ll, *part_ll, *r_ll;
+  uint32_t* status;
+};
+
+// Workgroup barrier over LDS only: this wave's LDS operations complete (lgkmcnt 0),
+// then the hardware barrier. __syncthreads() would also wait for this wave's global
+// stores, and since the vector memory counter drains in order, for every weight load
+// still in flight; message words need no such wait (their epochs order them).
+__device__ __forceinline__ void ds_barrier() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
+
+// x = bf16(r * inv) as two E4M3 terms: hi = e4m3(x / 2^(s-127)), lo = e4m3((x / 2^(s-127)
+// - hi) * 16) under scale 2^(s-131). Thread t handles x[8t .. 8t+7]; x[n] with
+// n = 128 kb + 64 h + 16 g + e sits at byte 16 h + e of xb[term][kb][g], the order in
+// which the MFMA's B lanes of group g pair with the A lanes (block 4 kb + a, a = 0..3).
+__device__ __forceinline__ void ds_build_x(DSShared& sh, int tid) {
+  const float inv = sh.inv;
+  const int s_hi = e4m3_term_exponent(sh.xmax);
+  const float f = pow2_biased(254 - s_hi);
+  const int n0 = tid * 8;
+  const float4 ra = *reinterpret_cast<const float4*>(&sh.r[n0]);
+  const float4 rb = *reinterpret_cast<const float4*>(&sh.r[n0 + 4]);
+  const float rv[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+  uint32_t hw[2], lw[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    float h[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) h[t] = bf16_round_f(rv[4 * p + t] * inv) * f;
+    uint32_t w01 = e4m3_pair(h[0], h[1]), w23 = e4m3_pair(h[2], h[3]);
+    float l0 = (h[0] - e4m3_byte<0>(w01)) * 16.0f, l1 = (h[1] - e4m3_byte<1>(w01)) * 16.0f;
+    float l2 = (h[2] - e4m3_byte<0>(w23)) * 16.0f, l3 = (h[3] - e4m3_byte<1>(w23)) * 16.0f;
+    hw[p] = (w01 & 0xffffu) | (w23 << 16);
+    lw[p] = (e4m3_pair(l0, l1) & 0xffffu) | (e4m3_pair(l2, l3) << 16);
+  }
+  const int kb = n0 >> 7, h = (n0 >> 6) & 1, g = (n0 >> 4) & 3, e = n0 & 15;
+  const int off = (kb * 4 + g) * 32 + 16 * h + e;
+  *reinterpret_cast<uint2*>(&sh.xb[0][0][0][0] + off) = make_uint2(hw[0], hw[1]);
+  *reinterpret_cast<uint2*>(&sh.xb[1][0][0][0] + off) = make_uint2(lw[0], lw[1]);
+}
+
+// The two roles run separate loops (so their registers do not overlap) and meet at
+// the same four barriers per layer:
+//   S0: r_l and its rmsnorm statistics in LDS -> every wave builds a quarter of x
+//   S0b: x terms in LDS -> compute waves: phase A (one tile each), publish act,
+//                          prefetch the A tile of l+1
+//                          message wave: shared gate, gather the XCD's act slice
+//   S1: act ready  -> compute waves: phase B partials into LDS, prefetch B(l+1)
+//   S2: partials   -> (every wave leaves here if a message wait ran out)
+//                     message wave: publish the row block's partial, gather the 8
+//                     XCDs' partials, r += bf16(sum), publish r, gather the XCD's r
+// Compute waves never wait on a message. One wave per SIMD.
+__device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
+  const int lane = c.lane, wave = c.wave, x = c.x, j = c.j, K = c.K, NE = c.NE;
+  const int tiles = 8 * NE;                     // phase-A tiles of the XCD
+  const int col = lane & 15, grp = lane >> 4;   // MFMA lane: row / column and K group
+
+  auto expert_base = [&](int l, int k, const uint8_t*& gu, const uint8_t*& gus, const uint8_t*& dn,
+                         const uint8_t*& dns) {
+    const wm_decode_layer& D = sh.desc[l];
+    if (k < K) {
+      int64_t slot = sh.slot[l][k];
+      gu = (const uint8_t*)D.gate_up + slot * D.gate_up_stride;
+      gus = (const uint8_t*)D.gate_up_scales + slot * D.gate_up_scales_stride;
+      dn = (const uint8_t*)D.down + slot * D.down_stride;
+      dns = (const uint8_t*)D.down_scales + slot * D.down_scales_stride;
+    } else {
+      gu = (const uint8_t*)D.shared_gate_up;
+      gus = (const uint8_t*)D.shared_gate_up_scales;
+      dn = (const uint8_t*)D.shared_down;
+      dns = (const uint8_t*)D.shared_down_scales;
+    }
+  };
+
+  // Phase-A tile t of this wave: expert t / 8, slice rows 8 (t % 8) .. +7 (gate, then up).
+  // Lanes beyond the XCD's tiles re-read a valid tile (a cache hit) so every load is
+  // unconditional; a branch among in-flight loads would make the compiler wait for all.
+  int t_mine = j + DS_J * wave;
+  const bool tile_valid = t_mine < tiles;
+  if (!tile_valid) t_mine = t_mine % tiles;
+  const int tk = t_mine >> 3, tq = t_mine & 7;
+  const int arow = col < 8 ? DS_SLICE * x + 8 * tq + col : DS_I + DS_SLICE * x + 8 * tq + (col - 8);
+  uint4 aw[DS_KB];
+  uint4 as4[4];
+  auto issue_a = [&](int l) {
+    const uint8_t *gu, *gus, *dn, *dns;
+    expert_base(l, tk, gu, gus, dn, dns);
+    const uint8_t* rp = gu + (size_t)arow * (DS_H / 2) + 16 * grp;
+#pragma unroll
+    for (int kb = 0; kb < DS_KB; ++kb) aw[kb] = gload16(rp + 64 * kb);
+    const uint8_t* sp = gus + (size_t)arow * (DS_H / 32);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) as4[m] = gload16(sp + 16 * m);
+  };
+
+  // Phase-B K-steps 2 wave + i (i = 0, 1): experts 2 kb and 2 kb + 1 of the slice.
+  // Lane (row r, group a) reads half a % 2 of expert 2 kb + a / 2's row-slice for each
+  // of the four 16-row tiles; missing experts re-read the step's first expert.
+  uint4 bw[2][4];
+  uint32_t bs[2][4];
+  const int bshift = 8 * (2 * (col & 1) + (grp & 1));  // byte of the scale word
+  auto issue_b = [&](int l) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kb = 2 * wave + i;
+      int e = 2 * kb + (grp >> 1);
+      if (e >= NE) e = 2 * kb < NE ? 2 * kb : 0;
+      const uint8_t *gu, *gus, *dn, *dns;
+      expert_base(l, e, gu, gus, dn, dns);
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        const size_t row = (size_t)x * DS_H + j * DS_ROWS + 16 * rt + col;
+        bw[i][rt] = gload16(dn + row * (DS_SLICE / 2) + 16 * (grp & 1));
+        bs[i][rt] = gload<uint32_t>(dns + ((row * (DS_SLICE / 32)) & ~(size_t)3));
+      }
+    }
+  };
+
+  issue_a(0);
+  issue_b(0);
+  for (int l = 0; l < c.L; ++l) {
+    const uint32_t e_act = c.base + 2 + 3 * l;
+    uint64_t* act_buf = c.act_ll + ((size_t)(l & 1) * DS_X + x) * DS_NE_MAX * DS_SLICE;
+    ds_barrier();  // S0: r_l, inv, xmax in LDS
+    WM_DS_TRACE(l, 0);
+    ds_build_x(sh, c.wave * 64 + lane);
+    ds_barrier();  // S0b: x terms in LDS
+    WM_DS_TRACE(l, 1);
+    // ---- phase A: one 16-row tile over the hidden width
+    {
+      const int s_hi = e4m3_term_exponent(sh.xmax);
+      // lanes of columns >= 2 feed unused outputs; a scale below 2^-127 only arises for
+      // x below 2^-113, so clamping it changes nothing measurable
+      const int sb = (col & 1) ? (s_hi > 4 ? s_hi - 4 : 0) : s_hi;
+      const uint8_t* xp = &sh.xb[col & 1][0][grp][0];
+      ds_v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < DS_KB; ++kb) {
+        const uint4 blo = *reinterpret_cast<const uint4*>(xp + kb * 128);
+        const uint4 bhi = *reinterpret_cast<const uint4*>(xp + kb * 128 + 16);
+        const ds_v8i bv = {(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w,
+                           (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
+        const ds_v8i av = {(int)aw[kb].x, (int)aw[kb].y, (int)aw[kb].z, (int)aw[kb].w, 0, 0, 0, 0};
+        const uint32_t sw = kb % 4 == 0 ? as4[kb / 4].x : kb % 4 == 1 ? as4[kb / 4].y : kb % 4 == 2 ? as4[kb / 4].z : as4[kb / 4].w;
+        const int sa = (int)((sw >> (8 * grp)) & 0xffu);
+        if (kb & 1)
+          acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc1, DS_FMT_FP4, DS_FMT_FP8, 0, sa, 0, sb);
+        else
+          acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc0, DS_FMT_FP4, DS_FMT_FP8, 0, sa, 0, sb);
+      }
+      // column 0 holds the hi term's dot products, column 1 the lo term's
+      float d[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = acc0[i] + acc1[i];
+        d[i] = v + dpp_f<0xB1>(v);
+      }
+      if (col == 0) *reinterpret_cast<float4*>(&sh.tile_out[wave][4 * grp]) = make_float4(d[0], d[1], d[2], d[3]);
+      if (tile_valid && lane < 8) {
+        const float g = sh.tile_out[wave][lane], u = sh.tile_out[wave][8 + lane];
+        ll_put(&act_buf[tk * DS_SLICE + 8 * tq + lane], __float_as_uint(silu(g) * u), e_act);
+      }
+    }
+    WM_DS_TRACE(l, 3);
+    issue_a(l + 1 < c.L ? l + 1 : l);
+    WM_DS_TRACE(l, 4);
+    ds_barrier();  // S1: act slice and shared gate in LDS
+    WM_DS_TRACE(l, 5);
+    // ---- phase B: split-K partials of rows 64 j .. 64 j + 63 over this wave's K-steps
+    {
+      ds_v4f accb[4];
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) accb[rt] = ds_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int kb = 2 * wave + i;
+        if (2 * kb < NE) {
+          // B operand: w_e act_e as three E4M3 terms. A B lane's scale covers the same
+          // 32-value K block as the A lanes of its group (block a = expert 2 kb + a / 2,
+          // columns 32 (a % 2) ..), which the register layout spreads over two B lane
+          // groups: element t of block a sits in group 2 (a % 2) + t / 16 at byte
+          // 16 (a / 2) + t % 16. Row a of this wave splits block a, two values a lane.
+          const int t2 = 2 * (lane & 15);
+          const int e = 2 * kb + (grp >> 1);
+          const int cc = 32 * (grp & 1) + t2;
+          const float we = e < K ? sh.w[l][e] : (e < NE ? sh.gate : 0.0f);
+          float2 av = *reinterpret_cast<const float2*>(&sh.act[e][cc]);
+          const float v0 = e < NE ? av.x * we : 0.0f, v1 = e < NE ? av.y * we : 0.0f;
+          const float gmax = segment_max<16>(fmaxf(fabsf(v0), fabsf(v1)));
+          const int s = e4m3_term_exponent(gmax);
+          const float f = pow2_biased(254 - s);
+          const float h0 = v0 * f, h1 = v1 * f;
+          const uint32_t c0 = e4m3_pair(h0, h1);
+          const float m0 = (h0 - e4m3_byte<0>(c0)) * 16.0f, m1 = (h1 - e4m3_byte<1>(c0)) * 16.0f;
+          const uint32_t c1 = e4m3_pair(m0, m1);
+          const float n0 = (m0 - e4m3_byte<0>(c1)) * 16.0f, n1 = (m1 - e4m3_byte<1>(c1)) * 16.0f;
+          const uint32_t c2 = e4m3_pair(n0, n1);
+          uint8_t* st = &sh.bstage[wave][i][0][0][0];
+          const int at = (2 * (grp & 1) + (t2 >> 4)) * 32 + 16 * (grp >> 1) + (t2 & 15);
+          *reinterpret_cast<uint16_t*>(st + 0 * 128 + at) = (uint16_t)c0;
+          *reinterpret_cast<uint16_t*>(st + 1 * 128 + at) = (uint16_t)c1;
+          *reinterpret_cast<uint16_t*>(st + 2 * 128 + at) = (uint16_t)c2;
+          const int term = col < 3 ? col : 0;  // columns >= 3 feed unused outputs
+          const uint4 blo = *reinterpret_cast<const uint4*>(st + term * 128 + grp * 32);
+          const uint4 bhi = *reinterpret_cast<const uint4*>(st + term * 128 + grp * 32 + 16);
+          const ds_v8i bv = {(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w,
+                             (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
+          const int sb = s > 4 * term ? s - 4 * term : 0;
+#pragma unroll
+          for (int rt = 0; rt < 4; ++rt) {
+            const ds_v8i aop = {(int)bw[i][rt].x, (int)bw[i][rt].y, (int)bw[i][rt].z, (int)bw[i][rt].w, 0, 0, 0, 0};
+            accb[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop, bv, accb[rt], DS_FMT_FP4, DS_FMT_FP8, 0,
+                                                                        (int)((bs[i][rt] >> bshift) & 0xffu), 0, sb);
+          }
+        }
+      }
+      // rows 4 g .. 4 g + 3 of each tile, column = term; the message wave adds the terms
+      if (col < 3) {
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+          *reinterpret_cast<float4*>(&sh.partb[wave][col][16 * rt + 4 * grp]) =
+              make_float4(accb[rt][0], accb[rt][1], accb[rt][2], accb[rt][3]);
+      }
+    }
+    WM_DS_TRACE(l, 6);
+    ds_barrier();  // S2: partials in LDS
+    if (sh.failures != 0) break;  // a message wait ran out (every wave leaves here)
+    issue_b(l + 1 < c.L ? l + 1 : l);
+  }
+}
+
+// rmsnorm statistics of r in LDS -> sh.inv, sh.xmax (lane 0 writes; read after the next barrier).
+__device__ __forceinline__ void ds_publish_norm(DSShared& sh, float ss, float mx, int lane) {
+  ss = segment_sum<64>(ss);
+  mx = segment_max<64>(mx);
+  const float inv = rsqrtf(ss / (float)DS_H + sh.eps);
+  if (lane == 0) {
+    sh.inv = inv;
+    sh.xmax = bf16_round_f(mx * inv);
+  }
+}
+
+__device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, float& r_own) {
+  const int lane = c.lane, x = c.x, j = c.j;
+  bool ok = true;
+  for (int l = 0; l < c.L; ++l) {
+    const int par = l & 1;
+    const uint32_t e_act = c.base + 2 + 3 * l, e_part = c.base + 3 + 3 * l, e_r = c.base + 4 + 3 * l;
+    uint64_t* act_buf = c.act_ll + ((size_t)par * DS_X + x) * DS_NE_MAX * DS_SLICE;
+    uint64_t* part_buf = c.part_ll + (size_t)par * DS_X * DS_H;
+    uint64_t* r_buf = c.r_ll + ((size_t)par * DS_X + x) * DS_H;
+    const uint8_t* sg = (const uint8_t*)sh.desc[l].shared_gate;
+    uint4 gw[4] = {};
+    if (sg) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) gw[m] = gload16(sg + (lane + 64 * m) * 16);
+    }
+    ds_barrier();  // S0
+    WM_DS_TRACE(l, 8);
+    ds_build_x(sh, DS_CW * 64 + lane);
+    ds_barrier();  // S0b
+    // ---- shared-expert gate sigmoid(x . g); lane: x[8 (lane + 64 m) .. + 7]
+    {
+      float gv = 1.0f;
+      if (sg) {
+        const float inv = sh.inv;
+        float a = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int n = 8 * (lane + 64 * m);
+          const float4 ra = *reinterpret_cast<const float4*>(&sh.r[n]);
+          const float4 rb = *reinterpret_cast<const float4*>(&sh.r[n + 4]);
+          const float rv[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+          const uint32_t g4[4] = {gw[m].x, gw[m].y, gw[m].z, gw[m].w};
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            uint32_t xv = f32_to_bf16_bits(rv[2 * h] * inv) | ((uint32_t)f32_to_bf16_bits(rv[2 * h + 1] * inv) << 16);
+            a = dot2_bf16(bits_to_bf16x2(xv), bits_to_bf16x2(g4[h]), a);
+          }
+        }
+        a = segment_sum<64>(a);
+        gv = 1.0f / (1.0f + __expf(-a));
+      }
+      if (lane == 0) sh.gate = gv;
+    }
+    // ---- the XCD's act slice (every expert's 64 columns)
+    ll_gather<DS_NE_MAX * DS_SLICE / 64>(act_buf, lane, 64, c.NE * DS_SLICE, e_act, c.status, ok,
+                                         [&](int w, uint32_t v) { sh.act[w / DS_SLICE][w % DS_SLICE] = __uint_as_float(v); });
+    WM_DS_TRACE(l, 9);
+    if (!ok) sh.failures = 1;
+    ds_barrier();  // S1
+    WM_DS_TRACE(l, 10);
+    ds_barrier();  // S2
+    if (sh.failures != 0) break;
+    WM_DS_TRACE(l, 11);
+    // ---- row block partial -> the 8 XCDs; sum them (x order); r += bf16(sum); gather r_{l+1}
+    float p = 0.0f;
+#pragma unroll
+    for (int w = 0; w < DS_CW; ++w)
+      p += (sh.partb[w][0][lane] + sh.partb[w][1][lane]) + sh.partb[w][2][lane];
+    ll_put(&part_buf[(size_t)x * DS_H + j * DS_ROWS + lane], __float_as_uint(p), e_part);
+    float y = 0.0f;
+    ll_gather<DS_X>(part_buf + j * DS_ROWS, lane, DS_H, DS_X * DS_H, e_part, c.status, ok,
+                    [&](int i, uint32_t v) { y += __uint_as_float(v); });
+    WM_DS_TRACE(l, 12);
+    r_own += bf16_bits_to_f32(f32_to_bf16_bits(y));
+    ll_put(&r_buf[j * DS_ROWS + lane], __float_as_uint(r_own), e_r);
+    float ss = 0.0f, mx = 0.0f;
+    for (int half = 0; half < 2; ++half)
+      ll_gather<DS_H / 128>(r_buf, half * (DS_H / 2) + lane, 64, (half + 1) * (DS_H / 2), e_r, c.status, ok,
+                            [&](int w, uint32_t v) {
+                              const float rv = __uint_as_float(v);
+                              sh.r[w] = rv;
+                              ss += rv * rv;
+                              mx = fmaxf(mx, fabsf(rv));
+                            });
+    ds_publish_norm(sh, ss, mx, lane);
+    if (!ok) sh.failures = 1;
+    WM_DS_TRACE(l, 13);
+  }
+}
+
+template <int PER_LANE>
+__global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
+    const float* __restrict__ logits, int L, int E, int K, int norm_topk, const wm_decode_layer* layers,
+    float* __restrict__ residual, float eps, uint16_t* __restrict__ x_out, uint8_t* state) {
+  __shared__ DSShared sh;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const DSLayout lay = ds_layout(L);
+  DSCtx c;
+  c.L = L;
+  c.K = K;
+  c.NE = K + 1;
+  c.x = b % DS_X;
+  c.j = b / DS_X;
+  c.lane = tid % 64;
+  c.wave = tid / 64;
+  c.route_ll = (uint64_t*)(state + lay.route);
+  c.act_ll = (uint64_t*)(state + lay.act);
+  c.part_ll = (uint64_t*)(state + lay.part);
+  c.r_ll = (uint64_t*)(state + lay.r);
+  c.status = (uint32_t*)(state + lay.status);
+  uint32_t* wg_epoch = (uint32_t*)(state + lay.epoch);
+  c.base = wg_epoch[b];
+  const uint32_t e_route = c.base + 1;
+  const bool msg = c.wave == DS_CW;
+  bool ok = true;
+  if (tid == 0) sh.failures = 0;
+  if (tid == 0) sh.eps = eps;
+  ds_barrier();  // failures is cleared before any wave can raise it
+
+  // ---- prologue: routes of layers b, b + 256, ... (message wave), descriptors, r_0
+  if (msg) {
+    for (int l = b; l < L; l += DS_WGS) {
+      int sel;
+      float w;
+      wave_route_softmax<PER_LANE>(logits + (size_t)l * E, E, K, norm_topk != 0, c.lane, sel, w, nullptr);
+      if (c.lane < 16) {
+        ll_put(&c.route_ll[(size_t)l * 32 + c.lane], c.lane < K ? (uint32_t)sel : 0u, e_route);
+        ll_put(&c.route_ll[(size_t)l * 32 + 16 + c.lane], c.lane < K ? __float_as_uint(w) : 0u, e_route);
+      }
+    }
+  }
+  for (int i = tid; i < L * (int)(sizeof(wm_decode_layer) / 8); i += DS_THREADS)
+    reinterpret_cast<uint64_t*>(sh.desc)[i] = reinterpret_cast<const uint64_t*>(layers)[i];
+  for (int i = tid; i < DS_H; i += DS_THREADS) sh.r[i] = residual[i];
+  float r_own = msg ? residual[c.j * DS_ROWS + c.lane] : 0.0f;  // the message wave owns rows 64j + lane
+  if (msg) {
+    for (int s = 0; s < L * 32; s += 64 * 16)
+      ll_gather<16>(c.route_ll, s + c.lane, 64, L * 32, e_route, c.status, ok, [&](int i, uint32_t v) {
+        int l = i / 32, s_ = i % 32;
+        if (s_ < 16) sh.slot[l][s_] = (int)v;
+        else sh.w[l][s_ - 16] = __uint_as_float(v);
+      });
+  }
+  if (!ok) sh.failures = 1;
+  ds_barrier();
+  if (sh.failures != 0) return;
+  // Expert ids -> slots once, so the prefetch loops read only LDS.
+  for (int i = tid; i < L * 16; i += DS_THREADS) {
+    int l = i / 16, k = i % 16;
+    const int32_t* slots = sh.desc[l].slots;
+    if (k < K && slots) sh.slot[l][k] = gload<int32_t>(slots + sh.slot[l][k]);
+  }
+  if (msg) {  // rmsnorm statistics of r_0
+    float ss = 0.0f, mx = 0.0f;
+    for (int i = c.lane; i < DS_H; i += 64) {
+      ss += sh.r[i] * sh.r[i];
+      mx = fmaxf(mx, fabsf(sh.r[i]));
+    }
+    ds_publish_norm(sh, ss, mx, c.lane);
+  }
+  ds_barrier();
+
+  if (msg) ds_message_role(sh, c, r_own);
+  else ds_compute_role(sh, c);
+  if (sh.failures != 0) return;
+
+  // ---- outputs (XCD 0's message waves): r_L and rmsnorm(r_L); sh.inv is r_L's
+  if (msg && c.x == 0) {
+    residual[c.j * DS_ROWS + c.lane] = r_own;
+    if (x_out) x_out[c.j * DS_ROWS + c.lane] = f32_to_bf16_bits(r_own * sh.inv);
+  }
+  if (tid == 0) wg_epoch[b] = c.base + 3 * (uint32_t)L + 5;
+}
+
+// Repack of down regions into the slice-major layout: one thread per (expert, slice, row).
+__global__ void __launch_bounds__(256) repack_down_kernel(const uint8_t* __restrict__ src,
+                                                          const uint8_t* __restrict__ src_scales, int64_t src_stride,
+                                                          int64_t src_scales_stride, int experts, int H, int I,
+                                                          uint8_t* __restrict__ dst, uint8_t* __restrict__ dst_scales) {
+  int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t total = (int64_t)experts * DS_X * H;
+  if (n >= total) return;
+  int o = (int)(n % H);
+  int s = (int)((n / H) % DS_X);
+  int e = (int)(n / ((int64_t)H * DS_X));
+  const int row_bytes = I / 2, slice_bytes = I / 16;             // packed bytes per row / per slice-row
+  const int row_scales = I / 32, slice_scales = I / 256;
+  const uint8_t* sp = src + e * src_stride + (int64_t)o * row_bytes + s * slice_bytes;
+  uint8_t* dp = dst + (int64_t)e * H * row_bytes + ((int64_t)s * H + o) * slice_bytes;
+  for (int q = 0; q < slice_bytes / 16; ++q) reinterpret_cast<uint4*>(dp)[q] = reinterpret_cast<const uint4*>(sp)[q];
+  const uint8_t* ss = src_scales + e * src_scales_stride + (int64_t)o * row_scales + s * slice_scales;
+  uint8_t* ds = dst_scales + (int64_t)e * H * row_scales + ((int64_t)s * H + o) * slice_scales;
+  for (int q = 0; q < slice_scales; ++q) ds[q] = ss[q];
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+WM_EXPORT int wm_repack_down_slices(const void* src, const void* src_scales, int64_t src_stride,
+                                    int64_t src_scales_stride, int32_t experts, int32_t hidden, int32_t inter, void* dst,
+                                    void* dst_scales, void* stream) {
+  return guarded([&] {
+    if (experts < 0 || hidden < 1 || inter % 256) fail("wm_repack_down_slices: inter must be a multiple of 256");
+    if (experts == 0) return;
+    if (!src || !src_scales || !dst || !dst_scales) fail("wm_repack_down_slices: null pointer");
+    if (((uintptr_t)src | (uintptr_t)dst | (uintptr_t)src_stride) % 16)
+      fail("wm_repack_down_slices: weight regions must be 16-byte aligned");
+    int64_t total = (int64_t)experts * DS_X * hidden;
+    hipLaunchKernelGGL(repack_down_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       (const uint8_t*)src, (const uint8_t*)src_scales, src_stride, src_scales_stride, experts, hidden,
+                       inter, (uint8_t*)dst, (uint8_t*)dst_scales);
+    check_launch("repack_down");
+  });
+}
+
+WM_EXPORT size_t wm_decode_state_size(int32_t layers, int32_t experts) {
+  (void)experts;
+  return layers > 0 ? ds_layout(layers).total : 0;
+}
+
+WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts) {
+  (void)experts;
+  return layers > 0 ? ds_layout(layers).status : 0;
+}
+
+WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers, int32_t experts, int32_t k,
+                                             int32_t hidden, int32_t inter, const wm_decode_layer* layers_dev,
+                                             float* residual, float eps, void* x_out, void* state, size_t state_bytes,
+                                             void* stream) {
+  return guarded([&] {
+    if (hidden != DS_H || inter != DS_I)
+      fail("wm_moe_decode_persistent_mxfp4: supports hidden 2048 and intermediate 512");
+    if (layers < 1 || layers > DS_MAX_LAYERS) fail("wm_moe_decode_persistent_mxfp4: layers must be in 1..128");
+    if (k < 1 || k + 1 > DS_NE_MAX || k > experts) fail("wm_moe_decode_persistent_mxfp4: k must be in 1..11");
+    if (experts < 1 || experts > 1024) fail("wm_moe_decode_persistent_mxfp4: experts must be in 1..1024");
+    if (!logits || !layers_dev || !residual || !state) fail("wm_moe_decode_persistent_mxfp4: null pointer");
+    if (state_bytes < ds_layout(layers).total || (uintptr_t)state % 8)
+      fail("wm_moe_decode_persistent_mxfp4: state buffer too small or misaligned");
+    hipStream_t s = as_stream(stream);
+    int per_lane = (experts + 63) / 64;
+    if (per_lane <= 8)
+      hipLaunchKernelGGL(decode_persistent_kernel<8>, dim3(DS_WGS), dim3(DS_THREADS), 0, s, logits, layers, experts, k, 1,
+                         layers_dev, residual, eps, (uint16_t*)x_out, (uint8_t*)state);
+    else
+      hipLaunchKernelGGL(decode_persistent_kernel<16>, dim3(DS_WGS), dim3(DS_THREADS), 0, s, logits, layers, experts, k, 1,
+                         layers_dev, residual, eps, (uint16_t*)x_out, (uint8_t*)state);
+    check_launch("decode_persistent");
+  });
+}
+
+}  // extern "C"

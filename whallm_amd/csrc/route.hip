@@ -1,55 +1,15 @@
 // Router kernels: softmax top-k (Qwen), scored top-k with bias-select and
 // group-limited selection (DeepSeek), and the bf16 router linear.
-//
-// One wave64 per token. Expert e lives in lane e % 64, register e / 64, so a
-// row of up to 1024 logits is 16 registers per lane. Top-k is K rounds of a
-// wave-wide arg-max (value descending, ties to the lower index), the rule
-// fixed for this build (Native/DeepSeekNative/engine.mm:1881 breaks ties the
-// same way; Native/QwenNative/engine.mm:2086-2090 partial-sorts fp32 logits).
+// One wave64 per token; the top-k rule and register layout are in route_device.h.
 #include <cmath>
 
-#include "wm_common.h"
+#include "route_device.h"
 
 namespace wm {
 
-constexpr int ROUTE_MAX_PER_LANE = 16;  // E <= 1024
 constexpr int ROUTE_MAX_K = 32;
 
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
-}
-
-// Wave-wide arg-max of (v, i); every lane gets the winner.
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    float ov = __shfl_xor(v, offset, 64);
-    int oi = __shfl_xor(i, offset, 64);
-    if (better(ov, oi, v, i)) { v = ov; i = oi; }
-  }
-}
-
-__device__ __forceinline__ float wave_sum(float v) { return segment_sum<64>(v); }
-
-// Selects k experts from vals (lane-strided, n_valid per lane implicit through -inf/NaN-free
-// masking by `taken`). Writes indices into sel[0..k) (uniform across lanes).
-__device__ __forceinline__ void wave_topk(const float (&vals)[ROUTE_MAX_PER_LANE], int per_lane, int experts,
-                                          int k, int lane, int (&sel)[ROUTE_MAX_K]) {
-  uint32_t taken = 0;
-  for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int r = 0; r < per_lane; ++r) {
-      int e = r * 64 + lane;
-      if (e >= experts || (taken >> r) & 1u) continue;
-      if (better(vals[r], e, bv, bi)) { bv = vals[r]; bi = e; }
-    }
-    wave_argmax(bv, bi);
-    sel[j] = bi;
-    if ((bi & 63) == lane && bi < experts) taken |= 1u << (bi >> 6);
-  }
-}
-
+template <int PER_LANE>
 __global__ void __launch_bounds__(64) route_softmax_topk_kernel(const float* __restrict__ logits, int tokens,
                                                                int experts, int k, int norm,
                                                                int32_t* __restrict__ indices,
@@ -58,44 +18,20 @@ __global__ void __launch_bounds__(64) route_softmax_topk_kernel(const float* __r
   int t = blockIdx.x, lane = threadIdx.x;
   if (t >= tokens) return;
   const float* row = logits + (int64_t)t * experts;
-  int per_lane = (experts + 63) / 64;
-  float vals[ROUTE_MAX_PER_LANE];
-#pragma unroll
-  for (int r = 0; r < ROUTE_MAX_PER_LANE; ++r) {
-    int e = r * 64 + lane;
-    vals[r] = (r < per_lane && e < experts) ? row[e] : -INFINITY;
-  }
-  int sel[ROUTE_MAX_K];
-  wave_topk(vals, per_lane, experts, k, lane, sel);
-  // The first selected logit is the row maximum.
-  float top = row[sel[0]];
-  float denom = 0.0f;
-  if (probabilities) {
-    float part = 0.0f;
-    for (int r = 0; r < per_lane; ++r) {
-      int e = r * 64 + lane;
-      if (e < experts) part += __expf(vals[r] - top);
-    }
-    float full = wave_sum(part);
-    for (int r = 0; r < per_lane; ++r) {
-      int e = r * 64 + lane;
-      if (e < experts) probabilities[(int64_t)t * experts + e] = __expf(vals[r] - top) / full;
-    }
-  }
-  if (norm) {
-    for (int j = 0; j < k; ++j) denom += __expf(row[sel[j]] - top);
-  } else {
-    float part = 0.0f;
-    for (int r = 0; r < per_lane; ++r) {
-      int e = r * 64 + lane;
-      if (e < experts) part += __expf(vals[r] - top);
-    }
-    denom = wave_sum(part);
-  }
+  int sel;
+  float w, full;
+  wave_route_softmax<PER_LANE>(row, experts, k, norm != 0, lane, sel, w, probabilities ? &full : nullptr);
   if (lane < k) {
-    int j = lane;
-    indices[(int64_t)t * k + j] = sel[j];
-    weights[(int64_t)t * k + j] = __expf(row[sel[j]] - top) / denom;
+    indices[(int64_t)t * k + lane] = sel;
+    weights[(int64_t)t * k + lane] = w;
+  }
+  if (probabilities) {
+    float top = row[__shfl(sel, 0, 64)];
+#pragma unroll
+    for (int r = 0; r < PER_LANE; ++r) {
+      int e = r * 64 + lane;
+      if (e < experts) probabilities[(int64_t)t * experts + e] = __expf(row[e] - top) / full;
+    }
   }
 }
 
@@ -105,23 +41,23 @@ __device__ __forceinline__ float score_fn(float l, int func) {
   return sqrtf(fmaxf(l, 0.0f) + log1pf(__expf(-fabsf(l))));
 }
 
+template <int PER_LANE>
 __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restrict__ logits,
                                                          const float* __restrict__ bias, int tokens, int experts,
                                                          int k, int func, float route_scale, int norm, int n_groups,
                                                          int topk_groups, int32_t* __restrict__ indices,
                                                          float* __restrict__ weights) {
-  __shared__ float biased_lds[1024];
-  __shared__ float score_lds[1024];
-  __shared__ float group_score[64];
+  __shared__ float biased_lds[64 * PER_LANE];
+  __shared__ float score_lds[64 * PER_LANE];
   int t = blockIdx.x, lane = threadIdx.x;
   if (t >= tokens) return;
   const float* row = logits + (int64_t)t * experts;
-  int per_lane = (experts + 63) / 64;
-  float vals[ROUTE_MAX_PER_LANE];
-  float top = -INFINITY, denom = 1.0f;
-  if (func == 0) {  // softmax scores: need the row max and sum
+  float vals[PER_LANE];
+  float top = 0.0f, denom = 1.0f;
+  if (func == 0) {  // softmax scores need the row max and sum
     float m = -INFINITY;
-    for (int r = 0; r < per_lane; ++r) {
+#pragma unroll
+    for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
       if (e < experts) m = fmaxf(m, row[e]);
     }
@@ -129,16 +65,17 @@ __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restric
     wave_argmax(m, dummy);
     top = m;
     float part = 0.0f;
-    for (int r = 0; r < per_lane; ++r) {
+#pragma unroll
+    for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
       if (e < experts) part += __expf(row[e] - top);
     }
-    denom = wave_sum(part);
+    denom = segment_sum<64>(part);
   }
 #pragma unroll
-  for (int r = 0; r < ROUTE_MAX_PER_LANE; ++r) {
+  for (int r = 0; r < PER_LANE; ++r) {
     int e = r * 64 + lane;
-    if (r < per_lane && e < experts) {
+    if (e < experts) {
       float s = func == 0 ? __expf(row[e] - top) / denom : score_fn(row[e], func);
       float b = s + (bias ? bias[e] : 0.0f);
       score_lds[e] = s;
@@ -151,8 +88,8 @@ __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restric
   __syncthreads();
   if (n_groups > 1) {
     int gsize = experts / n_groups;
-    // Group score: the sum of its two largest biased scores (DeepSeek-V3 rule).
-    float gs = -INFINITY;
+    // A group's score is the sum of its two largest biased scores (DeepSeek-V3 rule).
+    float gs[1] = {-INFINITY};
     if (lane < n_groups) {
       float a = -INFINITY, b = -INFINITY;
       for (int j = 0; j < gsize; ++j) {
@@ -160,29 +97,28 @@ __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restric
         if (v > a) { b = a; a = v; }
         else if (v > b) b = v;
       }
-      gs = a + b;
-      group_score[lane] = gs;
+      gs[0] = a + b;
     }
-    // Keep the topk_groups best groups (ties -> lower group).
+    int gsel;
+    float gval;
+    wave_topk<1>(gs, n_groups, topk_groups, lane, gsel, gval);
     uint64_t keep = 0;
-    float gv[ROUTE_MAX_PER_LANE];
-    for (int r = 0; r < ROUTE_MAX_PER_LANE; ++r) gv[r] = (r == 0 && lane < n_groups) ? gs : -INFINITY;
-    int gsel[ROUTE_MAX_K];
-    wave_topk(gv, 1, n_groups, topk_groups, lane, gsel);
-    for (int j = 0; j < topk_groups; ++j) keep |= 1ull << gsel[j];
-    for (int r = 0; r < per_lane; ++r) {
+    for (int j = 0; j < topk_groups; ++j) keep |= 1ull << __shfl(gsel, j, 64);
+#pragma unroll
+    for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
       if (e < experts && !((keep >> (e / gsize)) & 1ull)) vals[r] = -INFINITY;
     }
   }
-  int sel[ROUTE_MAX_K];
-  wave_topk(vals, per_lane, experts, k, lane, sel);
-  float sum = 0.0f;
-  for (int j = 0; j < k; ++j) sum += score_lds[sel[j]];
+  int sel;
+  float sel_val;
+  wave_topk<PER_LANE>(vals, experts, k, lane, sel, sel_val);
+  float mine = lane < k ? score_lds[lane < k ? sel : 0] : 0.0f;
+  float sum = segment_sum<64>(mine);
   if (lane < k) {
-    float w = score_lds[sel[lane]];
+    float w = mine;
     if (norm && k > 1) w = w / (sum + 1e-20f);
-    indices[(int64_t)t * k + lane] = sel[lane];
+    indices[(int64_t)t * k + lane] = sel;
     weights[(int64_t)t * k + lane] = w * route_scale;
   }
 }
@@ -213,12 +149,20 @@ WM_EXPORT int wm_route_softmax_topk(const float* logits, int32_t tokens, int32_t
                                     void* stream) {
   return guarded([&] {
     if (tokens < 0) fail("wm_route_softmax_topk: negative token count");
-    if (experts < 1 || experts > 64 * ROUTE_MAX_PER_LANE) fail("wm_route_softmax_topk: experts must be in 1..1024");
+    if (experts < 1 || experts > 1024) fail("wm_route_softmax_topk: experts must be in 1..1024");
     if (k < 1 || k > ROUTE_MAX_K || k > experts) fail("wm_route_softmax_topk: k must be in 1..min(32, experts)");
     if (tokens == 0) return;
     if (!logits || !indices || !weights) fail("wm_route_softmax_topk: null pointer");
-    hipLaunchKernelGGL(route_softmax_topk_kernel, dim3(tokens), dim3(64), 0, as_stream(stream), logits, tokens,
-                       experts, k, norm_topk_prob, indices, weights, probabilities);
+    hipStream_t s = as_stream(stream);
+    int per_lane = (experts + 63) / 64;
+#define WM_RS(P) hipLaunchKernelGGL(route_softmax_topk_kernel<P>, dim3(tokens), dim3(64), 0, s, logits, tokens, experts, \
+                                    k, norm_topk_prob, indices, weights, probabilities)
+    if (per_lane <= 1) WM_RS(1);
+    else if (per_lane <= 2) WM_RS(2);
+    else if (per_lane <= 4) WM_RS(4);
+    else if (per_lane <= 8) WM_RS(8);
+    else WM_RS(16);
+#undef WM_RS
     check_launch("route_softmax_topk");
   });
 }
@@ -228,7 +172,7 @@ WM_EXPORT int wm_route_scored(const float* logits, const float* bias, int32_t to
                               int32_t topk_groups, int32_t* indices, float* weights, void* stream) {
   return guarded([&] {
     if (tokens < 0) fail("wm_route_scored: negative token count");
-    if (experts < 1 || experts > 64 * ROUTE_MAX_PER_LANE) fail("wm_route_scored: experts must be in 1..1024");
+    if (experts < 1 || experts > 1024) fail("wm_route_scored: experts must be in 1..1024");
     if (k < 1 || k > ROUTE_MAX_K || k > experts) fail("wm_route_scored: k must be in 1..min(32, experts)");
     if (func < 0 || func > 2) fail("wm_route_scored: func must be 0 (softmax), 1 (sigmoid) or 2 (sqrt-softplus)");
     if (n_groups < 1 || n_groups > 64 || experts % n_groups) fail("wm_route_scored: n_groups must divide experts (<= 64)");
@@ -237,8 +181,16 @@ WM_EXPORT int wm_route_scored(const float* logits, const float* bias, int32_t to
     if (n_groups > 1 && k > topk_groups * (experts / n_groups)) fail("wm_route_scored: k exceeds the kept groups' experts");
     if (tokens == 0) return;
     if (!logits || !indices || !weights) fail("wm_route_scored: null pointer");
-    hipLaunchKernelGGL(route_scored_kernel, dim3(tokens), dim3(64), 0, as_stream(stream), logits, bias, tokens, experts,
-                       k, func, route_scale, norm_topk_prob, n_groups, topk_groups, indices, weights);
+    hipStream_t s = as_stream(stream);
+    int per_lane = (experts + 63) / 64;
+#define WM_RS(P) hipLaunchKernelGGL(route_scored_kernel<P>, dim3(tokens), dim3(64), 0, s, logits, bias, tokens, experts, \
+                                    k, func, route_scale, norm_topk_prob, n_groups, topk_groups, indices, weights)
+    if (per_lane <= 1) WM_RS(1);
+    else if (per_lane <= 2) WM_RS(2);
+    else if (per_lane <= 4) WM_RS(4);
+    else if (per_lane <= 8) WM_RS(8);
+    else WM_RS(16);
+#undef WM_RS
     check_launch("route_scored");
   });
 }

@@ -44,6 +44,19 @@ void check_launch(const char* kernel);
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // ------------------------------------------------------------------ device helpers
+// Load through a pointer known to address global memory. Pointers read from LDS or
+// from memory are generic to the compiler, which then emits FLAT accesses; those
+// also count against the LDS wait counter, so every LDS wait would wait for them.
+template <typename T>
+__device__ __forceinline__ T gload(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+typedef uint32_t wm_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 gload16(const void* p) {
+  wm_u32x4 v = *(const __attribute__((address_space(1))) wm_u32x4*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
 // float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
@@ -97,11 +110,53 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
   return (b & 0x80u) ? -mag : mag;
 }
 
-// Sum over `width` consecutive lanes (width a power of two <= 64), result in every lane.
+// DPP move of a float within 16-lane rows (gfx9 DPP controls).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over `WIDTH` consecutive lanes (a power of two <= 64), result in every lane of
+// the segment. 16- and 64-lane sums use DPP (quad permutes and row mirrors) and,
+// across rows, lane reads into scalar registers; no LDS round trips.
 template <int WIDTH>
 __device__ __forceinline__ float segment_sum(float v) {
+  if constexpr (WIDTH == 16 || WIDTH == 64) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: pairs
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: quads
+    v += dpp_f<0x141>(v);  // row_half_mirror: 8 lanes
+    v += dpp_f<0x140>(v);  // row_mirror: 16 lanes
+    if constexpr (WIDTH == 64) {
+      float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+      float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+      float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+      float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+      v = (r0 + r1) + (r2 + r3);
+    }
+    return v;
+  } else {
 #pragma unroll
-  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    for (int offset = WIDTH / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+  }
+}
+
+// Maximum over each aligned group of WIDTH lanes (16 or 64); every lane of the group
+// receives it. Same DPP steps as segment_sum.
+template <int WIDTH>
+__device__ __forceinline__ float segment_max(float v) {
+  static_assert(WIDTH == 16 || WIDTH == 64, "segment_max: width 16 or 64");
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  if constexpr (WIDTH == 64) {
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    v = fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+  }
   return v;
 }
 

@@ -273,3 +273,131 @@ def experts_mxfp4(x: torch.Tensor, indices: torch.Tensor, experts: MXFP4Experts,
     _lib.call("wm_experts_mxfp4", _ptr(x), T, _ptr(idx), k, ctypes.byref(table), _ptr(out), _ptr(ws), ws_bytes,
               _stream(device))
     return out
+
+
+# ----------------------------------------------------------------------------- decode stack
+
+def residual_rmsnorm(residual: torch.Tensor, y: torch.Tensor | None, eps: float = 1e-6) -> torch.Tensor:
+    """residual += y (in place), returns bf16 rmsnorm(residual)."""
+    device = _require_device(residual, y)
+    if residual.dtype != torch.float32 or not residual.is_contiguous():
+        raise ValueError("residual must be a contiguous float32 tensor")
+    H = residual.shape[-1]
+    T = residual.numel() // H if H else 0
+    if y is not None:
+        y = _contig(y, torch.bfloat16, "y")
+    x = torch.empty(residual.shape, dtype=torch.bfloat16, device=device)
+    _lib.call("wm_residual_rmsnorm", _ptr(residual), _ptr(y), T, H, float(eps), _ptr(x), _stream(device))
+    return x
+
+
+class MoEStack:
+    """L chained MXFP4 MoE layers run by one wm_moe_stack_mxfp4 call (device routing,
+    no host synchronisation, graph-capturable). Holds the C tables of every layer."""
+
+    def __init__(self, layers: list[MXFP4Experts], shared: list[MXFP4Experts] | None = None,
+                 shared_gates: list[torch.Tensor] | None = None, k: int = 10, norm_topk_prob: bool = True,
+                 eps: float = 1e-6):
+        self.layers, self.shared, self.shared_gates = layers, shared, shared_gates
+        self.k, self.norm, self.eps = k, norm_topk_prob, eps
+        n = len(layers)
+        self._tables = (MXFP4ExpertsC * n)(*[e.c_struct() for e in layers])
+        self._shared = (MXFP4ExpertsC * n)(*[e.c_struct() for e in shared]) if shared else None
+        self._gates = (ctypes.c_void_p * n)(*[g.data_ptr() for g in shared_gates]) if shared_gates else None
+        self.device = layers[0].gate_up.device
+        self._ws = None
+
+    def workspace_bytes(self, tokens: int) -> int:
+        return _lib.load().wm_moe_stack_mxfp4_workspace_size(tokens, self.k, ctypes.byref(self._tables[0]))
+
+    def __call__(self, logits: torch.Tensor, residual: torch.Tensor, x_out: torch.Tensor | None = None):
+        """logits fp32 [L, T, E]; residual fp32 [T, H] updated in place; x_out bf16 [T, H] (optional)."""
+        _require_device(logits, residual, x_out)
+        L = len(self.layers)
+        T = residual.shape[0]
+        if logits.shape[0] != L or logits.shape[1] != T or logits.dtype != torch.float32 or not logits.is_contiguous():
+            raise ValueError("logits must be contiguous float32 [layers, tokens, experts]")
+        need = self.workspace_bytes(T)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = _workspace(need, self.device)
+        _lib.call("wm_moe_stack_mxfp4", _ptr(logits), L, T, self.k, int(self.norm), self._tables, self._shared,
+                  self._gates, _ptr(residual), float(self.eps), _ptr(x_out), _ptr(self._ws), self._ws.numel(),
+                  _stream(self.device))
+        return residual
+
+
+# ----------------------------------------------------------------------------- persistent decode
+
+def repack_down_slices(experts: MXFP4Experts) -> tuple[torch.Tensor, torch.Tensor]:
+    """Down regions of every expert in the slice-major layout of the persistent decode
+    kernel: words [E, 8, H, I/64] int32 and scales [E, 8, H, I/256] uint8."""
+    device = _require_device(*experts.tensors())
+    E, H, I = experts.count, experts.hidden, experts.inter
+    down = experts.down if experts.down.dim() == 3 else experts.down.unsqueeze(0)
+    scales = experts.down_scales if experts.down_scales.dim() == 3 else experts.down_scales.unsqueeze(0)
+    dst = torch.empty(E, 8, H, I // 64, dtype=torch.int32, device=device)
+    dst_s = torch.empty(E, 8, H, I // 256, dtype=torch.uint8, device=device)
+    _lib.call("wm_repack_down_slices", _ptr(down), _ptr(scales), down.stride(0) * 4, scales.stride(0), E, H, I,
+              _ptr(dst), _ptr(dst_s), _stream(device))
+    return dst, dst_s
+
+
+class PersistentDecodeStack:
+    """One-token decode through L MXFP4 MoE layers in one persistent kernel launch
+    (wm_moe_decode_persistent_mxfp4). Repacks the down regions slice-major once,
+    keeps the per-layer descriptor table and the message state on the device."""
+
+    def __init__(self, layers: list[MXFP4Experts], shared: list[MXFP4Experts],
+                 shared_gates: list[torch.Tensor] | None = None, k: int = 10, eps: float = 1e-6):
+        if not layers or len(shared) != len(layers):
+            raise ValueError("one shared expert per layer is required")
+        self.device = layers[0].gate_up.device
+        self.k, self.eps = k, eps
+        self.L, self.E = len(layers), layers[0].count
+        self.H, self.I = layers[0].hidden, layers[0].inter
+        self.layers, self.shared, self.shared_gates = layers, shared, shared_gates
+        self._keep = []
+        descs = []
+        for l, (e, s) in enumerate(zip(layers, shared)):
+            if e.hidden != self.H or e.inter != self.I or e.count != self.E or s.hidden != self.H or s.inter != self.I:
+                raise ValueError("layers differ in shape")
+            if e.gate_up.dim() != 3:
+                raise ValueError("routed experts need a leading expert axis")
+            d, ds = repack_down_slices(e)
+            sd, sds = repack_down_slices(s)
+            g = shared_gates[l] if shared_gates is not None else None
+            if g is not None and (g.dtype != torch.bfloat16 or g.numel() != self.H):
+                raise ValueError("shared gate must be bf16 [H]")
+            self._keep += [d, ds, sd, sds]
+            descs.append(_lib.DecodeLayerC(
+                e.gate_up.data_ptr(), e.gate_up_scales.data_ptr(), d.data_ptr(), ds.data_ptr(),
+                e.gate_up.stride(0) * 4, e.gate_up_scales.stride(0), d.stride(0) * 4, ds.stride(0),
+                0 if e.slots is None else e.slots.data_ptr(),
+                s.gate_up.data_ptr(), s.gate_up_scales.data_ptr(), sd.data_ptr(), sds.data_ptr(),
+                0 if g is None else g.data_ptr()))
+        table = (_lib.DecodeLayerC * self.L)(*descs)
+        raw = bytes(table)
+        self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
+        lib = _lib.load()
+        self.state = torch.zeros(lib.wm_decode_state_size(self.L, self.E), dtype=torch.uint8, device=self.device)
+        self.status_offset = lib.wm_decode_status_offset(self.L, self.E)
+
+    def __call__(self, logits: torch.Tensor, residual: torch.Tensor, x_out: torch.Tensor | None = None):
+        """logits fp32 [L, E] (or [L, 1, E]); residual fp32 [H] (or [1, H]) updated in place."""
+        _require_device(logits, residual, x_out)
+        if logits.dtype != torch.float32 or not logits.is_contiguous() or logits.numel() != self.L * self.E:
+            raise ValueError("logits must be contiguous float32 [layers, experts]")
+        if residual.dtype != torch.float32 or not residual.is_contiguous() or residual.numel() != self.H:
+            raise ValueError("residual must be contiguous float32 [hidden] (one token)")
+        _lib.call("wm_moe_decode_persistent_mxfp4", _ptr(logits), self.L, self.E, self.k, self.H, self.I,
+                  _ptr(self.table), _ptr(residual), float(self.eps), _ptr(x_out), _ptr(self.state),
+                  self.state.numel(), _stream(self.device))
+        return residual
+
+    def status(self) -> int:
+        """0 when every exchange completed; nonzero after a stalled exchange ended a
+        launch (then call reset() before the next one). Synchronises the device."""
+        return int(self.state[self.status_offset:self.status_offset + 4].view(torch.int32).item())
+
+    def reset(self):
+        self.state.zero_()
