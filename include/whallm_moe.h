@@ -200,6 +200,12 @@ WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers
                                              size_t state_bytes, void* stream);
 /* Device word of the state buffer that a stalled exchange sets (0 = healthy). */
 WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts);
+/* 1 when the current device runs block b of the persistent launch on XCC b % 8, so
+ * messages read only within one XCD use XCD-local stores; 0 when it does not (the
+ * persistent launch then uses device-scope stores throughout); -1 on error. Checked
+ * once per device with a probe launch on `stream`. No counterpart in the reference
+ * (an MI355X placement detail of the persistent decode). */
+WM_EXPORT int wm_decode_xcd_local(void* stream);
 
 #ifdef __cplusplus
 }

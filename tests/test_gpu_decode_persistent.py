@@ -80,6 +80,7 @@ class Chain:
 @pytest.mark.parametrize("layers,experts", [(1, 16), (6, 64), (3, 512)])
 def test_persistent_decode_matches_oracle_chain(device, layers, experts):
     chain = Chain(device, layers, experts, seed=layers * 7 + experts)
+    print(f"xcd_local={chain.stack.xcd_local()}", flush=True)
     for call in range(3):  # successive launches advance the message epochs
         logits, r0 = chain.inputs()
         residual = torch.from_numpy(r0.copy()).to(device)

@@ -32,6 +32,7 @@
 // (Native/QwenNative/engine.mm:1567-1588 -> experts() :2073-2236) and its host
 // top-k (:2086-2100); routing runs in the launch prologue from the given logits.
 #include <cmath>
+#include <mutex>
 
 #include "moe_internal.h"
 #include "route_device.h"
@@ -53,6 +54,7 @@ constexpr int DS_MAX_LAYERS = 128;    // layer descriptors kept in LDS
 constexpr int DS_CW = 3;                      // compute waves (prefetch weights and compute)
 constexpr int DS_THREADS = (DS_CW + 1) * 64;  // + one message wave (polls and publishes)
 constexpr int DS_FMT_FP8 = 0, DS_FMT_FP4 = 4;  // MFMA operand formats (E4M3, E2M1)
+constexpr int DS_RW = (DS_ROWS + 2) / 3;      // words carrying one workgroup's 64 r rows as bf16 triples
 
 typedef int ds_v8i __attribute__((ext_vector_type(8)));
 typedef float ds_v4f __attribute__((ext_vector_type(4)));
@@ -67,7 +69,7 @@ __host__ __device__ inline DSLayout ds_layout(int layers) {
   d.route = at;  at += (size_t)layers * 32 * 8;
   d.act = at;    at += (size_t)2 * DS_X * DS_NE_MAX * DS_SLICE * 8;
   d.part = at;   at += (size_t)2 * DS_X * DS_H * 8;
-  d.r = at;      at += (size_t)2 * DS_X * DS_H * 8;
+  d.r = at;      at += (size_t)2 * DS_X * DS_J * DS_RW * 8;
   d.epoch = at;  at += (size_t)DS_WGS * 4;
   d.status = at; at += 256;
   d.total = at;
@@ -78,23 +80,38 @@ __device__ __forceinline__ void ll_put(uint64_t* p, uint32_t bits, uint32_t epoc
   __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Store of a message word read only by workgroups of the writer's own XCD. With
+// LOCAL, a workgroup-scope store: it is written through the CU's L1 into the XCD's
+// L2, where the readers' agent-scope loads find it, and goes no further (measured
+// on MI355X; the launcher enables LOCAL only after checking that block b runs on
+// XCC b % 8). Without LOCAL, an agent-scope store.
+template <bool LOCAL>
+__device__ __forceinline__ void ll_put_xcd(uint64_t* p, uint64_t word) {
+  if constexpr (LOCAL) __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Reads base[first + m * stride] (m < N, index < limit) with all N loads in flight,
-// re-polls only the words that do not carry `epoch` yet, then hands each value to
-// store(index, bits). Bounded: after DS_SPIN_LIMIT rounds it raises the status word.
-template <int N, typename Store>
+// re-polls only the words whose top EBITS bits do not equal `epoch` (mod 2^EBITS)
+// yet, then hands each word to store(index, word). Bounded: after DS_SPIN_LIMIT
+// rounds it raises the status word.
+template <int N, int EBITS = 32, typename Store>
 __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int stride, int limit, uint32_t epoch,
                                           uint32_t* status, bool& ok, Store store) {
+  const uint32_t want = EBITS == 32 ? epoch : (epoch & ((1u << EBITS) - 1));
+  auto tag = [](uint64_t v) { return (uint32_t)(v >> (64 - EBITS)); };
   uint64_t v[N];
 #pragma unroll
   for (int m = 0; m < N; ++m) {
     int i = first + m * stride;
-    v[m] = i < limit ? __hip_atomic_load(&base[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)epoch << 32;
+    v[m] = i < limit ? __hip_atomic_load(&base[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : (uint64_t)want << (64 - EBITS);
   }
   uint32_t spins = 0;
   while (ok) {
     bool ready = true;
 #pragma unroll
-    for (int m = 0; m < N; ++m) ready &= (uint32_t)(v[m] >> 32) == epoch;
+    for (int m = 0; m < N; ++m) ready &= tag(v[m]) == want;
     if (ready) break;
     if (++spins > DS_SPIN_LIMIT) {
       __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -109,14 +126,14 @@ __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int s
 #pragma unroll
     for (int m = 0; m < N; ++m) {
       int i = first + m * stride;
-      if (i < limit && (uint32_t)(v[m] >> 32) != epoch)
+      if (i < limit && tag(v[m]) != want)
         v[m] = __hip_atomic_load(&base[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 #pragma unroll
   for (int m = 0; m < N; ++m) {
     int i = first + m * stride;
-    if (i < limit) store(i, (uint32_t)v[m]);
+    if (i < limit) store(i, v[m]);
   }
 }
 
@@ -153,6 +170,7 @@ struct DSShared {
   __attribute__((aligned(16))) uint8_t bstage[DS_CW][2][3][4][32];
   __attribute__((aligned(16))) float tile_out[DS_CW][16];
   __attribute__((aligned(16))) float partb[DS_CW][3][DS_ROWS];
+  uint16_t rpack[3 * DS_RW];  // bf16 of this workgroup's r rows (+ zero pad) for packing
   int slot[DS_MAX_LAYERS][16];
   float w[DS_MAX_LAYERS][16];
   wm_decode_layer desc[DS_MAX_LAYERS];
@@ -223,6 +241,7 @@ __device__ __forceinline__ void ds_build_x(DSShared& sh, int tid) {
 //                     message wave: publish the row block's partial, gather the 8
 //                     XCDs' partials, r += bf16(sum), publish r, gather the XCD's r
 // Compute waves never wait on a message. One wave per SIMD.
+template <bool LOCAL>
 __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
   const int lane = c.lane, wave = c.wave, x = c.x, j = c.j, K = c.K, NE = c.NE;
   const int tiles = 8 * NE;                     // phase-A tiles of the XCD
@@ -258,12 +277,13 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
   auto issue_a = [&](int l) {
     const uint8_t *gu, *gus, *dn, *dns;
     expert_base(l, tk, gu, gus, dn, dns);
-    const uint8_t* rp = gu + (size_t)arow * (DS_H / 2) + 16 * grp;
-#pragma unroll
-    for (int kb = 0; kb < DS_KB; ++kb) aw[kb] = gload16(rp + 64 * kb);
+    // scales first: the first MFMA needs them with the first weight load
     const uint8_t* sp = gus + (size_t)arow * (DS_H / 32);
 #pragma unroll
     for (int m = 0; m < 4; ++m) as4[m] = gload16(sp + 16 * m);
+    const uint8_t* rp = gu + (size_t)arow * (DS_H / 2) + 16 * grp;
+#pragma unroll
+    for (int kb = 0; kb < DS_KB; ++kb) aw[kb] = gload16(rp + 64 * kb);
   };
 
   // Phase-B K-steps 2 wave + i (i = 0, 1): experts 2 kb and 2 kb + 1 of the slice.
@@ -306,13 +326,24 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
       // x below 2^-113, so clamping it changes nothing measurable
       const int sb = (col & 1) ? (s_hi > 4 ? s_hi - 4 : 0) : s_hi;
       const uint8_t* xp = &sh.xb[col & 1][0][grp][0];
+      // B operands come from LDS three K-steps ahead of their MFMA, so LDS latency
+      // overlaps the MFMA chain instead of adding to every step
+      constexpr int PF = 3;
+      uint4 blo[PF], bhi[PF];
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        blo[q] = *reinterpret_cast<const uint4*>(xp + q * 128);
+        bhi[q] = *reinterpret_cast<const uint4*>(xp + q * 128 + 16);
+      }
       ds_v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < DS_KB; ++kb) {
-        const uint4 blo = *reinterpret_cast<const uint4*>(xp + kb * 128);
-        const uint4 bhi = *reinterpret_cast<const uint4*>(xp + kb * 128 + 16);
-        const ds_v8i bv = {(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w,
-                           (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
+        const uint4 lo = blo[kb % PF], hi = bhi[kb % PF];
+        if (kb + PF < DS_KB) {
+          blo[kb % PF] = *reinterpret_cast<const uint4*>(xp + (kb + PF) * 128);
+          bhi[kb % PF] = *reinterpret_cast<const uint4*>(xp + (kb + PF) * 128 + 16);
+        }
+        const ds_v8i bv = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         const ds_v8i av = {(int)aw[kb].x, (int)aw[kb].y, (int)aw[kb].z, (int)aw[kb].w, 0, 0, 0, 0};
         const uint32_t sw = kb % 4 == 0 ? as4[kb / 4].x : kb % 4 == 1 ? as4[kb / 4].y : kb % 4 == 2 ? as4[kb / 4].z : as4[kb / 4].w;
         const int sa = (int)((sw >> (8 * grp)) & 0xffu);
@@ -320,6 +351,7 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
           acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc1, DS_FMT_FP4, DS_FMT_FP8, 0, sa, 0, sb);
         else
           acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc0, DS_FMT_FP4, DS_FMT_FP8, 0, sa, 0, sb);
+        __builtin_amdgcn_sched_barrier(0);  // keep the read-ahead where it is written
       }
       // column 0 holds the hi term's dot products, column 1 the lo term's
       float d[4];
@@ -331,7 +363,8 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
       if (col == 0) *reinterpret_cast<float4*>(&sh.tile_out[wave][4 * grp]) = make_float4(d[0], d[1], d[2], d[3]);
       if (tile_valid && lane < 8) {
         const float g = sh.tile_out[wave][lane], u = sh.tile_out[wave][8 + lane];
-        ll_put(&act_buf[tk * DS_SLICE + 8 * tq + lane], __float_as_uint(silu(g) * u), e_act);
+        ll_put_xcd<LOCAL>(&act_buf[tk * DS_SLICE + 8 * tq + lane],
+                          ((uint64_t)e_act << 32) | __float_as_uint(silu(g) * u));
       }
     }
     WM_DS_TRACE(l, 3);
@@ -413,6 +446,7 @@ __device__ __forceinline__ void ds_publish_norm(DSShared& sh, float ss, float mx
   }
 }
 
+template <bool LOCAL>
 __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, float& r_own) {
   const int lane = c.lane, x = c.x, j = c.j;
   bool ok = true;
@@ -421,7 +455,7 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     const uint32_t e_act = c.base + 2 + 3 * l, e_part = c.base + 3 + 3 * l, e_r = c.base + 4 + 3 * l;
     uint64_t* act_buf = c.act_ll + ((size_t)par * DS_X + x) * DS_NE_MAX * DS_SLICE;
     uint64_t* part_buf = c.part_ll + (size_t)par * DS_X * DS_H;
-    uint64_t* r_buf = c.r_ll + ((size_t)par * DS_X + x) * DS_H;
+    uint64_t* r_buf = c.r_ll + ((size_t)par * DS_X + x) * DS_J * DS_RW;
     const uint8_t* sg = (const uint8_t*)sh.desc[l].shared_gate;
     uint4 gw[4] = {};
     if (sg) {
@@ -456,9 +490,9 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
       }
       if (lane == 0) sh.gate = gv;
     }
-    // ---- the XCD's act slice (every expert's 64 columns)
+    // ---- the XCD's act slice (every expert's 64 columns); tile t wrote words 8t .. 8t+7
     ll_gather<DS_NE_MAX * DS_SLICE / 64>(act_buf, lane, 64, c.NE * DS_SLICE, e_act, c.status, ok,
-                                         [&](int w, uint32_t v) { sh.act[w / DS_SLICE][w % DS_SLICE] = __uint_as_float(v); });
+                                         [&](int w, uint64_t v) { sh.act[w / DS_SLICE][w % DS_SLICE] = __uint_as_float((uint32_t)v); });
     WM_DS_TRACE(l, 9);
     if (!ok) sh.failures = 1;
     ds_barrier();  // S1
@@ -474,26 +508,39 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     ll_put(&part_buf[(size_t)x * DS_H + j * DS_ROWS + lane], __float_as_uint(p), e_part);
     float y = 0.0f;
     ll_gather<DS_X>(part_buf + j * DS_ROWS, lane, DS_H, DS_X * DS_H, e_part, c.status, ok,
-                    [&](int i, uint32_t v) { y += __uint_as_float(v); });
+                    [&](int i, uint64_t v) { y += __uint_as_float((uint32_t)v); });
     WM_DS_TRACE(l, 12);
     r_own += bf16_bits_to_f32(f32_to_bf16_bits(y));
-    ll_put(&r_buf[j * DS_ROWS + lane], __float_as_uint(r_own), e_r);
+    // publish the row block as bf16 triples under a 16-bit epoch (the hidden state that
+    // feeds the next rmsnorm is bf16, as in the reference's bf16 residual stream; the
+    // owner keeps accumulating r in fp32)
+    sh.rpack[lane] = f32_to_bf16_bits(r_own);
+    if (lane < 3 * DS_RW - DS_ROWS) sh.rpack[DS_ROWS + lane] = 0;
+    if (lane < DS_RW) {
+      const uint64_t word = ((uint64_t)(e_r & 0xffffu) << 48) | ((uint64_t)sh.rpack[3 * lane + 2] << 32) |
+                            ((uint64_t)sh.rpack[3 * lane + 1] << 16) | sh.rpack[3 * lane];
+      ll_put_xcd<LOCAL>(&r_buf[j * DS_RW + lane], word);
+    }
     float ss = 0.0f, mx = 0.0f;
-    for (int half = 0; half < 2; ++half)
-      ll_gather<DS_H / 128>(r_buf, half * (DS_H / 2) + lane, 64, (half + 1) * (DS_H / 2), e_r, c.status, ok,
-                            [&](int w, uint32_t v) {
-                              const float rv = __uint_as_float(v);
-                              sh.r[w] = rv;
-                              ss += rv * rv;
-                              mx = fmaxf(mx, fabsf(rv));
-                            });
+    ll_gather<(DS_J * DS_RW + 63) / 64, 16>(r_buf, lane, 64, DS_J * DS_RW, e_r, c.status, ok, [&](int w, uint64_t v) {
+      const int jj = w / DS_RW, t = 3 * (w % DS_RW);
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        if (t + u < DS_ROWS) {
+          const float rv = bf16_bits_to_f32((uint32_t)(v >> (16 * u)) & 0xffffu);
+          sh.r[jj * DS_ROWS + t + u] = rv;
+          ss += rv * rv;
+          mx = fmaxf(mx, fabsf(rv));
+        }
+      }
+    });
     ds_publish_norm(sh, ss, mx, lane);
     if (!ok) sh.failures = 1;
     WM_DS_TRACE(l, 13);
   }
 }
 
-template <int PER_LANE>
+template <int PER_LANE, bool LOCAL>
 __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
     const float* __restrict__ logits, int L, int E, int K, int norm_topk, const wm_decode_layer* layers,
     float* __restrict__ residual, float eps, uint16_t* __restrict__ x_out, uint8_t* state) {
@@ -540,7 +587,8 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   float r_own = msg ? residual[c.j * DS_ROWS + c.lane] : 0.0f;  // the message wave owns rows 64j + lane
   if (msg) {
     for (int s = 0; s < L * 32; s += 64 * 16)
-      ll_gather<16>(c.route_ll, s + c.lane, 64, L * 32, e_route, c.status, ok, [&](int i, uint32_t v) {
+      ll_gather<16>(c.route_ll, s + c.lane, 64, L * 32, e_route, c.status, ok, [&](int i, uint64_t word) {
+        const uint32_t v = (uint32_t)word;
         int l = i / 32, s_ = i % 32;
         if (s_ < 16) sh.slot[l][s_] = (int)v;
         else sh.w[l][s_ - 16] = __uint_as_float(v);
@@ -565,8 +613,8 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   }
   ds_barrier();
 
-  if (msg) ds_message_role(sh, c, r_own);
-  else ds_compute_role(sh, c);
+  if (msg) ds_message_role<LOCAL>(sh, c, r_own);
+  else ds_compute_role<LOCAL>(sh, c);
   if (sh.failures != 0) return;
 
   // ---- outputs (XCD 0's message waves): r_L and rmsnorm(r_L); sh.inv is r_L's
@@ -598,11 +646,54 @@ __global__ void __launch_bounds__(256) repack_down_kernel(const uint8_t* __restr
   for (int q = 0; q < slice_scales; ++q) ds[q] = ss[q];
 }
 
+// XCC of each block of a DS_WGS-block launch (the hardware register, low 4 bits).
+__global__ void __launch_bounds__(64) xcc_map_kernel(uint32_t* out) {
+  if (threadIdx.x == 0) {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    out[blockIdx.x] = v & 0xfu;
+  }
+}
+
+// Whether block b of a DS_WGS-block launch runs on XCC b % DS_X on the current
+// device, checked once per device with a probe launch on `s`. Only then are the
+// messages that stay within one XCD written with XCD-local stores.
+static bool xcd_local_ok(hipStream_t s) {
+  static std::mutex mu;
+  static int known[64];  // 0 unknown, 1 yes, 2 no
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  if (known[dev] == 0) {
+    bool ok = false;
+    uint32_t* d = nullptr;
+    if (hipMalloc(&d, DS_WGS * sizeof(uint32_t)) == hipSuccess) {
+      uint32_t h[DS_WGS] = {};
+      hipLaunchKernelGGL(xcc_map_kernel, dim3(DS_WGS), dim3(64), 0, s, d);
+      if (hipGetLastError() == hipSuccess &&
+          hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, s) == hipSuccess &&
+          hipStreamSynchronize(s) == hipSuccess) {
+        ok = true;
+        for (int b = 0; b < DS_WGS; ++b) ok &= h[b] == (uint32_t)(b % DS_X);
+      }
+      (void)hipFree(d);
+    }
+    known[dev] = ok ? 1 : 2;
+  }
+  return known[dev] == 1;
+}
+
 }  // namespace wm
 
 using namespace wm;
 
 extern "C" {
+
+WM_EXPORT int wm_decode_xcd_local(void* stream) {
+  int r = 0;
+  int rc = guarded([&] { r = xcd_local_ok(as_stream(stream)) ? 1 : 0; });
+  return rc != 0 ? -1 : r;
+}
 
 WM_EXPORT int wm_repack_down_slices(const void* src, const void* src_scales, int64_t src_stride,
                                     int64_t src_scales_stride, int32_t experts, int32_t hidden, int32_t inter, void* dst,
@@ -645,13 +736,16 @@ WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers
     if (state_bytes < ds_layout(layers).total || (uintptr_t)state % 8)
       fail("wm_moe_decode_persistent_mxfp4: state buffer too small or misaligned");
     hipStream_t s = as_stream(stream);
-    int per_lane = (experts + 63) / 64;
-    if (per_lane <= 8)
-      hipLaunchKernelGGL(decode_persistent_kernel<8>, dim3(DS_WGS), dim3(DS_THREADS), 0, s, logits, layers, experts, k, 1,
-                         layers_dev, residual, eps, (uint16_t*)x_out, (uint8_t*)state);
-    else
-      hipLaunchKernelGGL(decode_persistent_kernel<16>, dim3(DS_WGS), dim3(DS_THREADS), 0, s, logits, layers, experts, k, 1,
-                         layers_dev, residual, eps, (uint16_t*)x_out, (uint8_t*)state);
+    const int per_lane = (experts + 63) / 64;
+    const bool local = xcd_local_ok(s);
+#define WM_DP(P, LOC) hipLaunchKernelGGL((decode_persistent_kernel<P, LOC>), dim3(DS_WGS), dim3(DS_THREADS), 0, s, logits, \
+                                         layers, experts, k, 1, layers_dev, residual, eps, (uint16_t*)x_out, (uint8_t*)state)
+    if (per_lane <= 8) {
+      if (local) WM_DP(8, true); else WM_DP(8, false);
+    } else {
+      if (local) WM_DP(16, true); else WM_DP(16, false);
+    }
+#undef WM_DP
     check_launch("decode_persistent");
   });
 }

@@ -401,3 +401,12 @@ class PersistentDecodeStack:
 
     def reset(self):
         self.state.zero_()
+
+    def xcd_local(self) -> bool:
+        """Whether the device places block b of the launch on XCC b % 8, so that
+        messages read within one XCD use XCD-local stores (checked once per device)."""
+        lib = _lib.load()
+        r = lib.wm_decode_xcd_local(_stream(self.device))
+        if r < 0:
+            raise _lib.WhallmError(f"wm_decode_xcd_local: {lib.wm_last_error().decode(errors='replace')}")
+        return bool(r)
