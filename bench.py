@@ -25,7 +25,10 @@ import torch
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0       # dense fp8 MFMA
 FP4_PEAK_TFLOPS = 10100.0      # dense MXFP4 MFMA
+METRIC = "MoE-layer tok/s (decode, 16K prefill) + % of HBM / MFMA roofline"
+HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def log(msg: str) -> None:
@@ -37,6 +40,9 @@ def log(msg: str) -> None:
 class DecodeStack:
     """C2: 48-layer MXFP4 MoE decode, 1 token per step."""
     name = "c2-decode"
+    # MXFP4 weights straight into scaled MFMAs against E4M3 terms of the bf16 activations,
+    # fp32 accumulation
+    dtype = "mxfp4"
 
     def __init__(self, device, layers=48, hidden=2048, experts=512, inter=512, k=10, tokens=1, seed=0,
                  impl="persistent"):
@@ -91,6 +97,23 @@ class DecodeStack:
     def check(self):
         if self.impl == "persistent" and self.stack.status() != 0:
             raise RuntimeError("persistent decode: a message exchange stalled (status word set)")
+
+    def kernel_ms(self, launches: int) -> float:
+        """Average duration of the persistent kernel itself: HIP events recorded on the
+        stream it is launched on, around each launch (outside the graph)."""
+        stream = torch.cuda.current_stream(self.device)
+        total = 0.0
+        for i in range(launches):
+            self.logits.copy_(self.step_logits[i % len(self.step_logits)])
+            self.residual.copy_(self.step_embed[i % len(self.step_embed)])
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            self._body()
+            b.record(stream)
+            b.synchronize()
+            total += a.elapsed_time(b)
+        self.check()
+        return total / launches
 
     def capture(self):
         self.logits.copy_(self.step_logits[0])
@@ -166,6 +189,7 @@ class DecodeStack:
 class Prefill:
     """C3: one MXFP4 MoE layer at a 16,384-token prefill, Zipf(1.1)-skewed routing."""
     name = "c3-prefill"
+    dtype = "bf16"
 
     def __init__(self, device, hidden=2048, experts=512, inter=512, k=10, tokens=16384, seed=0):
         from whallm_amd import synthetic as S
@@ -254,6 +278,21 @@ WORKLOADS = {"c2-decode": DecodeStack, "c3-prefill": Prefill}
 
 # ----------------------------------------------------------------------------- main
 
+def profiled_traffic(name: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter
+    summary profiles/<name>_traffic.txt (FETCH_SIZE + WRITE_SIZE, each scaled by the
+    factor a copy kernel of known size gives), or None when it has not been profiled."""
+    path = os.path.join(HERE, "profiles", f"{name}_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -299,14 +338,17 @@ def main():
     value = wl.tokens_per_step() / (ms_per_step / 1e3)
 
     if isinstance(wl, DecodeStack):
-        achieved = wl.algorithmic_bytes() / (ms_per_step / 1e3) / 1e9
+        if wl.impl == "persistent":
+            k_ms = wl.kernel_ms(args.steps)
+            kernel = "decode_persistent_kernel (one launch = one token through 48 layers)"
+        else:
+            k_ms = ms_per_step
+            kernel = "decode step: 48 x (route, gate_up_act, down_combine, residual_rmsnorm)"
+        achieved = wl.algorithmic_bytes() / (k_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": ("decode_persistent_kernel (one launch = one token through 48 layers)"
-                               if wl.impl == "persistent" else
-                               "decode step: 48 x (route, gate_up_act, down_combine, residual_rmsnorm)"),
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_persistent_c2"),
+                    "kernel": kernel, "kernel_ms": round(k_ms, 5),
                     "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
-        metric = "MoE decode tok/s (48-layer MXFP4 stack, 1 token/step)"
     else:
         tflops = wl.flops() / (ms_per_step / 1e3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -314,7 +356,6 @@ def main():
                     "frac_of_fp4_peak": round(tflops / FP4_PEAK_TFLOPS, 4),
                     "kernel": "prefill layer: route, permute, grouped gate_up, grouped down, combine",
                     "algorithmic_flops_per_launch": wl.flops()}
-        metric = "MoE prefill tok/s (one MXFP4 layer, 16K tokens)"
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -323,9 +364,9 @@ def main():
         cpu["host"] = platform.processor() or platform.machine()
 
     line = {
-        "metric": metric, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init MXFP4 weights, N(0,1) logits/inputs)",
+        "vs_baseline": None, "dtype": wl.dtype, "data": "synthetic (random-init MXFP4 weights, N(0,1) logits/inputs)",
         "config": wl.config(), "roofline": roofline, "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }
