@@ -207,6 +207,24 @@ WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts);
  * (an MI355X placement detail of the persistent decode). */
 WM_EXPORT int wm_decode_xcd_local(void* stream);
 
+/* ---- MTP acceptance ----------------------------------------------------------
+ * Verify n draft tokens (n <= 15) against n + 1 target rows [n + 1, vocab] fp32.
+ * out: device int32[2] = (accepted drafts, next token).
+ * Greedy: Sampler.verify at temperature 0 (runtime/deepseek_v4_ssd/native_qwen.py:395-400;
+ * dspark._verify, dspark.py:862-873): argmax ties go to the lower index, a NaN wins.
+ * Rejection (native_qwen.py:401-408; dspark.py:875-898): target_logp / draft_logp are
+ * log-probabilities; uniforms[n + 1] are the caller's draws (u_0..u_{n-1} the accept
+ * tests, u_n the sampling draw, inverse CDF as numpy Generator.choice). A draft id
+ * outside [0, vocab) counts as rejected. workspace: wm_mtp_workspace_size bytes,
+ * 16-byte aligned. */
+WM_EXPORT size_t wm_mtp_workspace_size(int32_t drafts, int32_t vocab);
+WM_EXPORT int wm_mtp_verify_greedy(const float* target_logits, const int32_t* drafts, int32_t n_drafts,
+                                   int32_t vocab, int32_t* out, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+WM_EXPORT int wm_mtp_verify_rejection(const float* target_logp, const float* draft_logp, const int32_t* drafts,
+                                      int32_t n_drafts, int32_t vocab, const float* uniforms, int32_t* out,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,5 +45,9 @@ def test_version_and_argument_checks_fail_before_any_launch():
     table = _lib.MXFP4ExpertsC()
     with pytest.raises(_lib.WhallmError, match="expert region pointer is null"):
         _lib.call("wm_moe_mxfp4", None, 1, None, None, 2, ctypes.byref(table), None, None, None, None, 0, None)
+    with pytest.raises(_lib.WhallmError, match="drafts must be in"):
+        _lib.call("wm_mtp_verify_greedy", None, None, 16, 100, None, None, 0, None)
+    with pytest.raises(_lib.WhallmError, match="workspace too small"):
+        _lib.call("wm_mtp_verify_rejection", 1, 1, 1, 3, 100, 1, 1, 1, 0, None)
     # The error message is per thread and clears on the next good call.
     assert lib.wm_last_error() != b""

@@ -69,6 +69,9 @@ _SIGNATURES = {
     "wm_decode_state_size": (c_size_t, [c_int32, c_int32]),
     "wm_decode_status_offset": (c_size_t, [c_int32, c_int32]),
     "wm_decode_xcd_local": (c_int, [_P]),
+    "wm_mtp_workspace_size": (c_size_t, [c_int32, c_int32]),
+    "wm_mtp_verify_greedy": (c_int, [_P, _P, c_int32, c_int32, _P, _P, c_size_t, _P]),
+    "wm_mtp_verify_rejection": (c_int, [_P, _P, _P, c_int32, c_int32, _P, _P, _P, c_size_t, _P]),
     "wm_moe_decode_persistent_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, c_float,
                                                _P, _P, c_size_t, _P]),
 }

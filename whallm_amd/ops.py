@@ -410,3 +410,59 @@ class PersistentDecodeStack:
         if r < 0:
             raise _lib.WhallmError(f"wm_decode_xcd_local: {lib.wm_last_error().decode(errors='replace')}")
         return bool(r)
+
+
+# ----------------------------------------------------------------------------- MTP acceptance
+
+def _mtp_rows(t: torch.Tensor, name: str) -> tuple[torch.Tensor, int, int]:
+    t = _contig(t, torch.float32, name)
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be [rows, vocab]")
+    return t, t.shape[0], t.shape[1]
+
+
+def mtp_verify_greedy(target_logits: torch.Tensor, drafts: torch.Tensor) -> torch.Tensor:
+    """Greedy MTP acceptance (Sampler.verify at temperature 0, native_qwen.py:395-400).
+
+    target_logits fp32 [n + 1, V], drafts int32 [n] -> device int32 [2] =
+    (accepted drafts, next token). Enqueued; no host synchronisation."""
+    device = _require_device(target_logits, drafts)
+    target_logits, rows, vocab = _mtp_rows(target_logits, "target_logits")
+    drafts = _contig(drafts.reshape(-1), torch.int32, "drafts")
+    n = drafts.numel()
+    if rows != n + 1:
+        raise ValueError("target_logits needs one row per draft plus the bonus row")
+    out = torch.empty(2, dtype=torch.int32, device=device)
+    ws = _workspace(_lib.load().wm_mtp_workspace_size(n, vocab), device)
+    _lib.call("wm_mtp_verify_greedy", _ptr(target_logits), _ptr(drafts), n, vocab, _ptr(out), _ptr(ws), ws.numel(),
+              _stream(device))
+    return out
+
+
+def mtp_verify_rejection(target_logp: torch.Tensor, draft_logp: torch.Tensor, drafts: torch.Tensor,
+                         uniforms: torch.Tensor) -> torch.Tensor:
+    """Rejection-sampling MTP acceptance (native_qwen.py:401-408, dspark.py:875-898).
+
+    target_logp fp32 [n + 1, V], draft_logp fp32 [n, V] (log-probabilities), drafts
+    int32 [n], uniforms fp32 [n + 1] (u_0..u_{n-1} accept tests, u_n the sampling draw)
+    -> device int32 [2] = (accepted drafts, next token)."""
+    device = _require_device(target_logp, draft_logp, drafts, uniforms)
+    target_logp, rows, vocab = _mtp_rows(target_logp, "target_logp")
+    drafts = _contig(drafts.reshape(-1), torch.int32, "drafts")
+    n = drafts.numel()
+    if rows != n + 1:
+        raise ValueError("target_logp needs one row per draft plus the bonus row")
+    if n > 0:
+        draft_logp, drows, dvocab = _mtp_rows(draft_logp, "draft_logp")
+        if drows != n or dvocab != vocab:
+            raise ValueError("draft_logp must be [n, vocab]")
+    else:
+        draft_logp = None
+    uniforms = _contig(uniforms.reshape(-1), torch.float32, "uniforms")
+    if uniforms.numel() != n + 1:
+        raise ValueError("uniforms must hold n + 1 draws")
+    out = torch.empty(2, dtype=torch.int32, device=device)
+    ws = _workspace(_lib.load().wm_mtp_workspace_size(n, vocab), device)
+    _lib.call("wm_mtp_verify_rejection", _ptr(target_logp), _ptr(draft_logp), _ptr(drafts), n, vocab, _ptr(uniforms),
+              _ptr(out), _ptr(ws), ws.numel(), _stream(device))
+    return out
