@@ -207,6 +207,40 @@ WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts);
  * (an MI355X placement detail of the persistent decode). */
 WM_EXPORT int wm_decode_xcd_local(void* stream);
 
+/* ---- HBM expert slot cache ----------------------------------------------------
+ * The reference's expert arena (Native/QwenNative/engine.mm:649-778; ExpertCache,
+ * runtime/deepseek_v4_ssd/expert_cache.py:1465-1945) on MI355X: `slots` expert blobs of
+ * blob_bytes (the Qwen blob, manifest.py:41-45: gate_up | gate_up scales | down |
+ * down scales) in caller-owned device memory, filled from a caller-owned pinned host pool
+ * [files][experts][blob_bytes] (hipHostMalloc; the stand-in for the SSD expert files).
+ * Replacement: LFU (use count, then oldest stamp), never a slot handed out by the same
+ * plan; use counts halve every max(8 * slots, 64) touches (ExpertArena::victim/touch).
+ * Opaque handle; errors as in the reference's C ABI (capi.h): int status, message at
+ * wm_slot_cache_error(handle). One thread per handle. */
+typedef struct wm_slot_cache wm_slot_cache;
+/* device_slots NULL: policy only (plan works, acquire fails; no device calls at all).
+ * device_map (nullable): device int32 [files * experts], expert -> slot of each file,
+ * refreshed by acquire for the experts it hands out (the `slots` of wm_mxfp4_experts).
+ * Returns NULL on failure with the message in err. Replaces ExpertArena's constructor
+ * (engine.mm:653-659) and ExpertCache's slot pool (expert_cache.py:488-610). */
+WM_EXPORT wm_slot_cache* wm_slot_cache_open(int32_t slots, int64_t blob_bytes, int32_t files, int32_t experts,
+                                            void* device_slots, int32_t* device_map, const void* host_pool,
+                                            char* err, size_t err_size);
+WM_EXPORT void wm_slot_cache_close(wm_slot_cache* cache);
+WM_EXPORT const char* wm_slot_cache_error(const wm_slot_cache* cache);
+/* Slots for experts[n] (host ids) of `file`; out_filled[i] = 1 where the expert was missing
+ * and took a slot (ExpertArena::plan, engine.mm:679-707). No copies. Host arrays. */
+WM_EXPORT int wm_slot_cache_plan(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
+                                 int32_t* out_slots, int32_t* out_filled);
+/* plan + fill the misses from the host pool with hipMemcpyAsync on the cache's copy stream
+ * (ExpertArena::acquire/load, engine.mm:671-722; ExpertCache.get_many, expert_cache.py:1465-1530).
+ * The copy stream waits for the work already on compute_stream; compute_stream then waits
+ * for the fills, so work enqueued after this call sees the experts resident. */
+WM_EXPORT int wm_slot_cache_acquire(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
+                                    int32_t* out_slots, void* compute_stream);
+/* out4 = (hits, misses, bytes copied, fills) since open. */
+WM_EXPORT int wm_slot_cache_stats(const wm_slot_cache* cache, int64_t* out4);
+
 /* ---- MTP acceptance ----------------------------------------------------------
  * Verify n draft tokens (n <= 15) against n + 1 target rows [n + 1, vocab] fp32.
  * out: device int32[2] = (accepted drafts, next token).

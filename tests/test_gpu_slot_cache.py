@@ -1,0 +1,98 @@
+"""GPU tests of the HBM slot cache: fills from the pinned host pool land bit-exact in
+their slots with the expert -> slot map refreshed, slots follow the oracle policy,
+the MoE layer computed through the cache table matches the oracle, and a fill never
+overwrites slots that work enqueued before it still reads."""
+import numpy as np
+import pytest
+import torch
+
+import whallm_amd as wa
+from oracle import moe as M
+from whallm_amd import synthetic as S
+from whallm_amd.slot_cache import SlotCache, qwen_blob_bytes
+
+pytestmark = pytest.mark.gpu
+
+H, I = 256, 128
+
+
+def blob_of(a, e):
+    return np.concatenate([a["gate_up"][e].view(np.uint8).reshape(-1), a["gate_up_scales"][e].reshape(-1),
+                           a["down"][e].view(np.uint8).reshape(-1), a["down_scales"][e].reshape(-1)])
+
+
+def make_pool(files, experts, seed):
+    rng = np.random.default_rng(seed)
+    arrays = [S.mxfp4_experts_np(rng, experts, H, I) for _ in range(files)]
+    blob = qwen_blob_bytes(H, I)
+    pool = torch.empty(files * experts * blob, dtype=torch.uint8).pin_memory()
+    host = pool.numpy().reshape(files, experts, blob)
+    for f in range(files):
+        for e in range(experts):
+            host[f, e] = blob_of(arrays[f], e)
+    return arrays, pool
+
+
+def test_fills_are_bit_exact_and_follow_the_policy(device):
+    files, experts, slots = 3, 24, 12
+    arrays, pool = make_pool(files, experts, 1)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    oracle = M.SlotArena(slots=slots, experts_per_layer=experts)
+    rng = np.random.default_rng(2)
+    blob = cache.blob
+    for step in range(40):
+        f = int(rng.integers(files))
+        ids = [int(v) for v in rng.choice(experts, size=5, replace=False)]
+        got = cache.acquire(f, ids)
+        want, _ = oracle.plan(f, ids)
+        assert got == want, step
+        torch.cuda.current_stream(device).synchronize()
+        mem = cache.slot_memory.view(slots, blob).cpu().numpy()
+        row = cache.map[f].cpu().numpy()
+        for e, s in zip(ids, got):
+            assert np.array_equal(mem[s], blob_of(arrays[f], e)), (step, e, s)
+            assert row[e] == s
+    st = cache.stats()
+    assert st["hits"] == oracle.hits and st["misses"] == oracle.misses and st["bytes"] == st["fills"] * blob
+
+
+def test_moe_through_the_cache_matches_oracle(device):
+    files, experts, slots, K, T = 2, 16, 16, 4, 8
+    arrays, pool = make_pool(files, experts, 3)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    rng = np.random.default_rng(4)
+    for f in range(files):
+        logits = rng.standard_normal((T, experts)).astype(np.float32)
+        idx, w = M.route_softmax_topk(logits, K)
+        cache.acquire(f, sorted(set(int(v) for v in idx.reshape(-1))))   # every routed expert resident
+        x = S.bf16_normal_np(rng, (T, H))
+        xt = S.bf16_bits_to_tensor(x, device)
+        y = wa.moe_mxfp4(xt, torch.from_numpy(idx.astype(np.int32)).to(device), torch.from_numpy(w.astype(np.float32)).to(device),
+                         cache.table(f))
+        ex = {e: M.MXFP4Expert(arrays[f]["gate_up"][e], arrays[f]["gate_up_scales"][e], arrays[f]["down"][e],
+                               arrays[f]["down_scales"][e]) for e in range(experts)}
+        want = M.moe_layer(S.bf16_bits_to_f32(x), logits, ex, K)[0]
+        got = y.float().cpu().numpy()
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel <= 1e-2 and np.abs(got - want).max() <= 2e-2 * np.abs(want).max(), rel
+
+
+def test_fill_waits_for_work_that_reads_the_evicted_slots(device):
+    files, experts, slots, K, T = 2, 16, 8, 8, 4096
+    arrays, pool = make_pool(files, experts, 5)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    ids0 = list(range(8))
+    cache.acquire(0, ids0)
+    rng = np.random.default_rng(6)
+    idx = np.tile(np.arange(8, dtype=np.int32), (T, 1))
+    w = np.full((T, K), 1.0 / K, np.float32)
+    x = S.bf16_normal_np(rng, (T, H))
+    y = wa.moe_mxfp4(S.bf16_bits_to_tensor(x, device), torch.from_numpy(idx).to(device), torch.from_numpy(w).to(device),
+                     cache.table(0))                                    # reads slots 0..7
+    cache.acquire(1, list(range(8, 16)))                                 # evicts every one of them
+    got = y.float().cpu().numpy()
+    ex = {e: M.MXFP4Expert(arrays[0]["gate_up"][e], arrays[0]["gate_up_scales"][e], arrays[0]["down"][e],
+                           arrays[0]["down_scales"][e]) for e in range(experts)}
+    want = M.combine(M.routed_outputs(S.bf16_bits_to_f32(x[:64]), idx[:64], ex), w[:64])
+    rel = np.linalg.norm(got[:64] - want) / np.linalg.norm(want)
+    assert rel <= 1e-2, rel

@@ -69,6 +69,12 @@ _SIGNATURES = {
     "wm_decode_state_size": (c_size_t, [c_int32, c_int32]),
     "wm_decode_status_offset": (c_size_t, [c_int32, c_int32]),
     "wm_decode_xcd_local": (c_int, [_P]),
+    "wm_slot_cache_open": (c_void_p, [c_int32, c_int64, c_int32, c_int32, _P, _P, _P, c_char_p, c_size_t]),
+    "wm_slot_cache_close": (None, [_P]),
+    "wm_slot_cache_error": (c_char_p, [_P]),
+    "wm_slot_cache_plan": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
+    "wm_slot_cache_acquire": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
+    "wm_slot_cache_stats": (c_int, [_P, _P]),
     "wm_mtp_workspace_size": (c_size_t, [c_int32, c_int32]),
     "wm_mtp_verify_greedy": (c_int, [_P, _P, c_int32, c_int32, _P, _P, c_size_t, _P]),
     "wm_mtp_verify_rejection": (c_int, [_P, _P, _P, c_int32, c_int32, _P, _P, _P, c_size_t, _P]),

@@ -601,7 +601,7 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   for (int i = tid; i < L * 16; i += DS_THREADS) {
     int l = i / 16, k = i % 16;
     const int32_t* slots = sh.desc[l].slots;
-    if (k < K && slots) sh.slot[l][k] = gload<int32_t>(slots + sh.slot[l][k]);
+    if (k < K && slots) sh.slot[l][k] = max(0, gload<int32_t>(slots + sh.slot[l][k]));  // -1: not resident
   }
   if (msg) {  // rmsnorm statistics of r_0
     float ss = 0.0f, mx = 0.0f;

@@ -15,6 +15,7 @@ struct ExpertRegions {
 
 __device__ __forceinline__ ExpertRegions expert_regions(const wm_mxfp4_experts& t, int e) {
   int64_t slot = t.slots ? t.slots[e] : e;
+  if (slot < 0) slot = 0;  // an expert that is not resident (map entry -1): never address outside the pool
   ExpertRegions r;
   r.gate_up = (const uint8_t*)t.gate_up + slot * t.gate_up_stride;
   r.gate_up_scales = (const uint8_t*)t.gate_up_scales + slot * t.gate_up_scales_stride;
