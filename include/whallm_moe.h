@@ -137,6 +137,23 @@ WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* ind
                                const wm_mxfp4_experts* experts, void* out, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* ---- FP8-E4M3 expert FFN (fp32 128x128 block scales) ----------------------
+ * The DeepSeek-V3 expert format (runtime/deepseek_v4_ssd/mimo/weights.py:17-43):
+ * SharedExpert / routed experts of deepseek_v41/moe.py:77-93, y = W2(swiglu(W1 x, W3 x)),
+ * clamped when swiglu_limit > 0 (moe.py:30-43). Same contract as wm_moe_mxfp4 /
+ * wm_experts_mxfp4 (shared_gate NULL = the ungated DeepSeek shared expert, model.py:540-541).
+ * Fused dequant-GEMV for T*K <= 256 when hidden and intermediate are multiples of 1024;
+ * grouped MFMA GEMM otherwise (multiples of 128). Replaces the FP8 expert linears
+ * (Native/DeepSeekNative/kernels.metal:82-124) and the install-time FP8 decode
+ * (Sources/DeepSeekRepack/Repacker.swift:622-627). */
+WM_EXPORT size_t wm_moe_fp8_workspace_size(int32_t tokens, int32_t k, const wm_fp8_experts* experts);
+WM_EXPORT int wm_moe_fp8(const void* x, int32_t tokens, const int32_t* indices, const float* weights, int32_t k,
+                         const wm_fp8_experts* experts, const wm_fp8_experts* shared, const void* shared_gate,
+                         void* y, void* workspace, size_t workspace_bytes, void* stream);
+WM_EXPORT int wm_experts_fp8(const void* x, int32_t tokens, const int32_t* indices, int32_t k,
+                             const wm_fp8_experts* experts, void* out, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* ---- decode stack ---------------------------------------------------------
  * r[t] += y[t] (y nullable), x[t] = bf16(r[t] / sqrt(mean(r[t]^2) + eps)): the
  * pre-norm residual between MoE layers (DecoderLayer.feed_forward, qwen4_exp.py:1127-1149,

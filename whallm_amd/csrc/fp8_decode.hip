@@ -1,0 +1,293 @@
+// Decode-time FP8-E4M3 expert FFN with fp32 128x128 block scales (the DeepSeek-V3
+// expert format, mimo/weights.py:17-43): fused dequant + GEMV, HBM-bound.
+//
+// Replaces the reference's FP8 expert linears (Native/DeepSeekNative/kernels.metal:82-124,
+// linear_fp8 of the shared expert; the routed experts decode FP8 only at install time,
+// Sources/DeepSeekRepack/Repacker.swift:622-627) with two kernels:
+//
+//   fp8_gate_up_act : one workgroup = (pair, 8 intermediate rows); a wave streams the
+//                     gate and up rows of 2 rows i: each lane reads 16 bytes of a row per
+//                     1024-byte chunk (fully coalesced), converts them to bf16 exactly
+//                     (v_cvt_scalef32_pk_bf16_fp8 with scale 1), dots them with the bf16
+//                     input (v_dot2_f32_bf16) and multiplies the 16-column partial by the
+//                     fp32 scale of its 128 x 128 block; silu(gate) * up (clamped when the
+//                     table sets a SwiGLU limit) -> act (fp32).
+//   fp8_down        : one workgroup = (token, 8 output rows); the four waves split the
+//                     token's experts (routed + shared) and keep routing-weighted partial
+//                     sums per row, reduced once: y[t, o] = sum_k w_k act_k . Wd_k[o]
+//                     (+ gate(t) act_s . Wd_s[o]). The per-pair mode writes each pair's
+//                     row unweighted (router order, the StreamingExperts contract).
+#include <cmath>
+
+#include "wm_common.h"
+#include "moe_internal.h"
+
+namespace wm {
+
+// 16 E4M3 bytes dotted with 16 bf16 values (8 words); products exact, fp32 sum.
+__device__ __forceinline__ float e4m3x16_dot_bf16(uint4 w, const uint32_t* xw, float acc) {
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const wm_bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(words[j], 1.0f, false);
+    const wm_bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(words[j], 1.0f, true);
+    acc = dot2_bf16(lo, bits_to_bf16x2(xw[2 * j]), acc);
+    acc = dot2_bf16(hi, bits_to_bf16x2(xw[2 * j + 1]), acc);
+  }
+  return acc;
+}
+
+// 16 E4M3 bytes dotted with 16 fp32 values.
+__device__ __forceinline__ float e4m3x16_dot_f32(uint4 w, const float* a, float acc) {
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const wm_f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[j], false);
+    const wm_f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[j], true);
+    acc = fmaf(lo[0], a[4 * j], acc);
+    acc = fmaf(lo[1], a[4 * j + 1], acc);
+    acc = fmaf(hi[0], a[4 * j + 2], acc);
+    acc = fmaf(hi[1], a[4 * j + 3], acc);
+  }
+  return acc;
+}
+
+// The pair's token and expert (or the shared expert); false for an unknown expert id.
+__device__ __forceinline__ bool fp8_pair(int p, int tokens, int k, const int32_t* __restrict__ indices,
+                                         const wm_fp8_experts& routed, bool has_shared, const wm_fp8_experts& shared,
+                                         int& t, Fp8Regions& r, bool& is_shared) {
+  is_shared = p >= tokens * k;
+  if (!is_shared) {
+    t = p / k;
+    const int e = indices[p];
+    if (e < 0 || e >= routed.experts) return false;
+    r = fp8_regions(routed, e);
+    return true;
+  }
+  t = p - tokens * k;
+  if (!has_shared) return false;
+  r = fp8_regions(shared, 0);
+  return true;
+}
+
+constexpr int FP8_RPW = 2;  // intermediate rows per wave (4 weight rows: gate and up of each)
+
+// grid: (I / (4 * FP8_RPW), pairs). CPL = H / 1024 chunks of 16 bytes per lane per row.
+template <int CPL>
+__global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __restrict__ x, int tokens, int k,
+                                                              const int32_t* __restrict__ indices,
+                                                              wm_fp8_experts routed, wm_fp8_experts shared,
+                                                              int has_shared, float* __restrict__ act) {
+  constexpr int ROWS = 2 * FP8_RPW;
+  __shared__ float sums[4][ROWS];
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int p = blockIdx.y;
+  const int H = routed.hidden, I = routed.inter, HB = H / 128;
+  int t;
+  Fp8Regions r;
+  bool is_shared;
+  if (!fp8_pair(p, tokens, k, indices, routed, has_shared != 0, shared, t, r, is_shared)) {
+    // unknown expert id: its act rows are zero (the host layer's index check reports it)
+    for (int i = blockIdx.x * 4 * FP8_RPW + threadIdx.x; i < (int)(blockIdx.x + 1) * 4 * FP8_RPW; i += 256)
+      act[(int64_t)p * I + i] = 0.0f;
+    return;
+  }
+  const wm_fp8_experts& tab = is_shared ? shared : routed;
+  const int up_first = tab.up_first;
+  const float limit = tab.swiglu_limit;
+  const int i_base = blockIdx.x * 4 * FP8_RPW + wave * FP8_RPW;
+
+  uint32_t xw[CPL][8];  // x[1024 m + 16 lane .. +15] as bf16 pairs
+  const uint16_t* xr = x + (int64_t)t * H;
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    const uint4* src = reinterpret_cast<const uint4*>(xr + 1024 * m + 16 * lane);
+    const uint4 a = src[0], b = src[1];
+    xw[m][0] = a.x; xw[m][1] = a.y; xw[m][2] = a.z; xw[m][3] = a.w;
+    xw[m][4] = b.x; xw[m][5] = b.y; xw[m][6] = b.z; xw[m][7] = b.w;
+  }
+  uint4 wq[ROWS][CPL];
+  float sc[ROWS][CPL];
+#pragma unroll
+  for (int q = 0; q < ROWS; ++q) {
+    const int i = i_base + q / 2;  // I is a multiple of 8: always in range
+    const int row = ((q & 1) ^ up_first) ? I + i : i;  // q even: gate, odd: up
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+      wq[q][m] = gload16(r.w13 + (int64_t)row * H + 1024 * m + 16 * lane);
+      sc[q][m] = gload<float>(r.w13_scales + (int64_t)(row / 128) * HB + 8 * m + lane / 8);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < ROWS; ++q) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) acc = fmaf(sc[q][m], e4m3x16_dot_bf16(wq[q][m], xw[m], 0.0f), acc);
+    acc = segment_sum<64>(acc);
+    if (lane == 0) sums[wave][q] = acc;
+  }
+  // sums[wave] is written and read by this wave only (LDS operations of a wave are ordered)
+  if (lane < FP8_RPW) {
+    float g = sums[wave][2 * lane], u = sums[wave][2 * lane + 1];
+    if (limit > 0.0f) {
+      g = fminf(g, limit);
+      u = fminf(fmaxf(u, -limit), limit);
+    }
+    act[(int64_t)p * I + i_base + lane] = silu(g) * u;
+  }
+}
+
+constexpr int FP8_OPW = 8;  // output rows per wave step
+
+// grid: combine (H / FP8_OPW, tokens); per pair (H / (4 * FP8_OPW), pairs). CPL = I / 1024.
+template <int CPL, bool COMBINE>
+__global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__ act, int tokens, int k,
+                                                       const int32_t* __restrict__ indices,
+                                                       const float* __restrict__ weights, wm_fp8_experts routed,
+                                                       wm_fp8_experts shared, int has_shared,
+                                                       const uint16_t* __restrict__ x,
+                                                       const uint16_t* __restrict__ shared_gate,
+                                                       uint16_t* __restrict__ y) {
+  __shared__ float partial[4][FP8_OPW];
+  __shared__ float gate_value;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int H = routed.hidden, I = routed.inter, IB = I / 128;
+  int t, o_base, first, step, n_entries;
+  if (COMBINE) {
+    t = blockIdx.y;
+    o_base = blockIdx.x * FP8_OPW;
+    n_entries = k + (has_shared ? 1 : 0);
+    first = wave;
+    step = 4;
+  } else {
+    t = blockIdx.y;  // the pair
+    o_base = (blockIdx.x * 4 + wave) * FP8_OPW;
+    n_entries = 1;
+    first = 0;
+    step = 1;
+  }
+  if (COMBINE && has_shared) {
+    if (threadIdx.x < 64) {
+      float gv = 1.0f;
+      if (shared_gate) {
+        const uint32_t* xr = reinterpret_cast<const uint32_t*>(x) + (int64_t)t * (H / 2);
+        const uint32_t* gr = reinterpret_cast<const uint32_t*>(shared_gate);
+        float a = 0.0f;
+        for (int q = lane; q < H / 2; q += 64) a = dot2_bf16(bits_to_bf16x2(xr[q]), bits_to_bf16x2(gr[q]), a);
+        a = segment_sum<64>(a);
+        gv = 1.0f / (1.0f + __expf(-a));
+      }
+      if (lane == 0) gate_value = gv;
+    }
+    __syncthreads();
+  }
+  float acc[FP8_OPW];
+#pragma unroll
+  for (int q = 0; q < FP8_OPW; ++q) acc[q] = 0.0f;
+  for (int entry = first; entry < n_entries; entry += step) {
+    int p;
+    float w;
+    Fp8Regions r;
+    if (COMBINE) {
+      if (entry < k) {
+        p = t * k + entry;
+        const int e = indices[p];
+        if (e < 0 || e >= routed.experts) continue;
+        r = fp8_regions(routed, e);
+        w = weights[p];
+      } else {
+        p = tokens * k + t;
+        r = fp8_regions(shared, 0);
+        w = gate_value;
+      }
+    } else {
+      p = t;
+      const int e = indices[p];
+      if (e < 0 || e >= routed.experts) break;  // zero row
+      r = fp8_regions(routed, e);
+      w = 1.0f;
+    }
+    float av[CPL][16];
+    const float* arow = act + (int64_t)p * I;
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+      const float4* a4 = reinterpret_cast<const float4*>(arow + 1024 * m + 16 * lane);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = a4[q];
+        av[m][4 * q] = v.x; av[m][4 * q + 1] = v.y; av[m][4 * q + 2] = v.z; av[m][4 * q + 3] = v.w;
+      }
+    }
+    uint4 wq[FP8_OPW][CPL];
+    float sc[FP8_OPW][CPL];
+#pragma unroll
+    for (int q = 0; q < FP8_OPW; ++q) {
+      const int o = o_base + q;  // H is a multiple of 32: always in range
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) {
+        wq[q][m] = gload16(r.w2 + (int64_t)o * I + 1024 * m + 16 * lane);
+        sc[q][m] = gload<float>(r.w2_scales + (int64_t)(o / 128) * IB + 8 * m + lane / 8);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < FP8_OPW; ++q) {
+      float s = 0.0f;
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) s = fmaf(sc[q][m], e4m3x16_dot_f32(wq[q][m], av[m], 0.0f), s);
+      acc[q] = fmaf(w, s, acc[q]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < FP8_OPW; ++q) {
+    const float v = segment_sum<64>(acc[q]);
+    if (lane == 0) partial[wave][q] = v;
+  }
+  __syncthreads();
+  if (COMBINE) {
+    if (threadIdx.x < FP8_OPW) {
+      const int q = threadIdx.x;
+      const float v = (partial[0][q] + partial[1][q]) + (partial[2][q] + partial[3][q]);
+      y[(int64_t)t * H + o_base + q] = f32_to_bf16_bits(v);
+    }
+  } else {
+    if (lane < FP8_OPW) y[(int64_t)t * H + o_base + lane] = f32_to_bf16_bits(partial[wave][lane]);
+  }
+}
+
+void decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
+                uint16_t* y, bool combine, float* act, hipStream_t s) {
+  const int H = routed.hidden, I = routed.inter;
+  if (H % 1024 || I % 1024 || H / 1024 > 8 || I / 1024 > 8)
+    fail("FP8 decode: hidden and intermediate must be multiples of 1024 up to 8192");
+  const int pairs = tokens * k + (shared ? tokens : 0);
+  const wm_fp8_experts sh = shared ? *shared : routed;
+  const dim3 g1(I / (4 * FP8_RPW), pairs);
+  switch (H / 1024) {
+#define WM_F8GU(C) case C: hipLaunchKernelGGL(fp8_gate_up_act_kernel<C>, g1, dim3(256), 0, s, x, tokens, k, indices, \
+                                              routed, sh, shared ? 1 : 0, act); break;
+    WM_F8GU(1) WM_F8GU(2) WM_F8GU(3) WM_F8GU(4) WM_F8GU(5) WM_F8GU(6) WM_F8GU(7) WM_F8GU(8)
+#undef WM_F8GU
+  }
+  check_launch("fp8_gate_up_act");
+  if (combine) {
+    const dim3 g2(H / FP8_OPW, tokens);
+    switch (I / 1024) {
+#define WM_F8DN(C) case C: hipLaunchKernelGGL((fp8_down_kernel<C, true>), g2, dim3(256), 0, s, act, tokens, k, indices, \
+                                              weights, routed, sh, shared ? 1 : 0, x, shared_gate, y); break;
+      WM_F8DN(1) WM_F8DN(2) WM_F8DN(3) WM_F8DN(4) WM_F8DN(5) WM_F8DN(6) WM_F8DN(7) WM_F8DN(8)
+#undef WM_F8DN
+    }
+  } else {
+    const dim3 g2(H / (4 * FP8_OPW), tokens * k);
+    switch (I / 1024) {
+#define WM_F8DP(C) case C: hipLaunchKernelGGL((fp8_down_kernel<C, false>), g2, dim3(256), 0, s, act, tokens, k, indices, \
+                                              weights, routed, sh, 0, x, nullptr, y); break;
+      WM_F8DP(1) WM_F8DP(2) WM_F8DP(3) WM_F8DP(4) WM_F8DP(5) WM_F8DP(6) WM_F8DP(7) WM_F8DP(8)
+#undef WM_F8DP
+    }
+  }
+  check_launch("fp8_down");
+}
+
+}  // namespace wm

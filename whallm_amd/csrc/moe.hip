@@ -35,6 +35,38 @@ static void validate_pair(const wm_mxfp4_experts* routed, const wm_mxfp4_experts
 
 static bool use_decode(int tokens, int k) { return (int64_t)tokens * k <= DECODE_MAX_PAIRS; }
 
+static void validate_fp8(const wm_fp8_experts* e, const char* what, bool shared) {
+  std::string w(what);
+  if (!e) fail(w + ": expert table is null");
+  if (!e->w13 || !e->w13_scales || !e->w2 || !e->w2_scales) fail(w + ": expert region pointer is null");
+  if (e->hidden < 128 || e->hidden % 128) fail(w + ": hidden must be a positive multiple of 128");
+  if (e->inter < 128 || e->inter % 128) fail(w + ": intermediate must be a positive multiple of 128");
+  if (!shared && (e->experts < 1 || e->experts > 1024)) fail(w + ": expert count must be in 1..1024");
+  if (e->w13_stride < 0 || e->w13_scales_stride < 0 || e->w2_stride < 0 || e->w2_scales_stride < 0)
+    fail(w + ": negative stride");
+  if (e->swiglu_limit < 0.0f) fail(w + ": swiglu_limit must be >= 0");
+  auto aligned = [](const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; };
+  if (!aligned(e->w13, 16) || !aligned(e->w2, 16) || e->w13_stride % 16 || e->w2_stride % 16)
+    fail(w + ": weight regions and strides must be 16-byte aligned");
+  if (!aligned(e->w13_scales, 4) || !aligned(e->w2_scales, 4) || e->w13_scales_stride % 4 || e->w2_scales_stride % 4)
+    fail(w + ": scale regions and strides must be 4-byte aligned");
+}
+
+static void validate_fp8_pair(const wm_fp8_experts* routed, const wm_fp8_experts* shared) {
+  validate_fp8(routed, "routed experts", false);
+  if (shared) {
+    validate_fp8(shared, "shared expert", true);
+    if (shared->hidden != routed->hidden || shared->inter != routed->inter)
+      fail("shared expert: hidden and intermediate must equal the routed experts'");
+  }
+}
+
+// The fused GEMV handles hidden / intermediate multiples of 1024; other shapes and
+// larger batches take the grouped GEMM.
+static bool use_decode_fp8(int tokens, int k, const wm_fp8_experts& e) {
+  return use_decode(tokens, k) && e.hidden % 1024 == 0 && e.inter % 1024 == 0 && e.hidden <= 8192 && e.inter <= 8192;
+}
+
 static size_t decode_workspace(int tokens, int k, const wm_mxfp4_experts& e) {
   return sizeof(float) * (size_t)(tokens * k + tokens) * e.inter;
 }
@@ -90,6 +122,54 @@ WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* ind
     else
       prefill_mxfp4((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out,
                     false, workspace, workspace_bytes, s);
+  });
+}
+
+WM_EXPORT size_t wm_moe_fp8_workspace_size(int32_t tokens, int32_t k, const wm_fp8_experts* experts) {
+  if (!experts || tokens < 0 || k < 1) return 0;
+  if (use_decode_fp8(tokens, k, *experts)) return sizeof(float) * (size_t)(tokens * k + tokens) * experts->inter + 256;
+  return prefill_fp8_workspace_size(tokens, k, *experts, true) + 256;
+}
+
+WM_EXPORT int wm_moe_fp8(const void* x, int32_t tokens, const int32_t* indices, const float* weights, int32_t k,
+                         const wm_fp8_experts* experts, const wm_fp8_experts* shared, const void* shared_gate, void* y,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    if (tokens < 0) fail("wm_moe_fp8: negative token count");
+    if (k < 1 || k > 32) fail("wm_moe_fp8: k must be in 1..32");
+    validate_fp8_pair(experts, shared);
+    if (tokens == 0) return;
+    if (!x || !indices || !weights || !y) fail("wm_moe_fp8: null pointer");
+    if (workspace_bytes < wm_moe_fp8_workspace_size(tokens, k, experts) - 256 || !workspace)
+      fail("wm_moe_fp8: workspace too small");
+    hipStream_t s = as_stream(stream);
+    if (use_decode_fp8(tokens, k, *experts))
+      decode_fp8((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
+                 (uint16_t*)y, true, (float*)workspace, s);
+    else
+      prefill_fp8((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
+                  (uint16_t*)y, true, workspace, workspace_bytes, s);
+  });
+}
+
+WM_EXPORT int wm_experts_fp8(const void* x, int32_t tokens, const int32_t* indices, int32_t k,
+                             const wm_fp8_experts* experts, void* out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  return guarded([&] {
+    if (tokens < 0) fail("wm_experts_fp8: negative token count");
+    if (k < 1 || k > 32) fail("wm_experts_fp8: k must be in 1..32");
+    validate_fp8_pair(experts, nullptr);
+    if (tokens == 0) return;
+    if (!x || !indices || !out) fail("wm_experts_fp8: null pointer");
+    if (workspace_bytes < wm_moe_fp8_workspace_size(tokens, k, experts) - 256 || !workspace)
+      fail("wm_experts_fp8: workspace too small");
+    hipStream_t s = as_stream(stream);
+    if (use_decode_fp8(tokens, k, *experts))
+      decode_fp8((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out, false,
+                 (float*)workspace, s);
+    else
+      prefill_fp8((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out, false,
+                  workspace, workspace_bytes, s);
   });
 }
 

@@ -24,6 +24,25 @@ __device__ __forceinline__ ExpertRegions expert_regions(const wm_mxfp4_experts& 
   return r;
 }
 
+// Device addresses of one FP8 expert (w13 = gate/up rows, w2 = down; fp32 128x128 block scales).
+struct Fp8Regions {
+  const uint8_t* w13;
+  const float* w13_scales;
+  const uint8_t* w2;
+  const float* w2_scales;
+};
+
+__device__ __forceinline__ Fp8Regions fp8_regions(const wm_fp8_experts& t, int e) {
+  int64_t slot = t.slots ? t.slots[e] : e;
+  if (slot < 0) slot = 0;  // not resident: never address outside the pool
+  Fp8Regions r;
+  r.w13 = (const uint8_t*)t.w13 + slot * t.w13_stride;
+  r.w13_scales = (const float*)((const uint8_t*)t.w13_scales + slot * t.w13_scales_stride);
+  r.w2 = (const uint8_t*)t.w2 + slot * t.w2_stride;
+  r.w2_scales = (const float*)((const uint8_t*)t.w2_scales + slot * t.w2_scales_stride);
+  return r;
+}
+
 // Host-side checks of an expert table; raises on a bad shape.
 void validate_experts(const wm_mxfp4_experts* e, const char* what, bool shared);
 
@@ -38,6 +57,15 @@ size_t prefill_workspace_size(int tokens, int k, const wm_mxfp4_experts& e, bool
 void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                    const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared, const uint16_t* shared_gate,
                    uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s);
+
+// FP8 expert FFN (hidden and intermediate multiples of 1024 for decode, of 128 for prefill).
+void decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
+                uint16_t* y, bool combine, float* act, hipStream_t s);
+size_t prefill_fp8_workspace_size(int tokens, int k, const wm_fp8_experts& e, bool has_shared);
+void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                 const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
+                 uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s);
 
 // Pairs at or below this count take the decode path.
 constexpr int DECODE_MAX_PAIRS = 256;

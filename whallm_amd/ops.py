@@ -275,6 +275,105 @@ def experts_mxfp4(x: torch.Tensor, indices: torch.Tensor, experts: MXFP4Experts,
     return out
 
 
+@dataclass(frozen=True)
+class FP8Experts:
+    """Device regions of a set of FP8-E4M3 experts with fp32 128x128 block scales
+    (the DeepSeek-V3 expert format, mimo/weights.py:17-43), addressed as base + slot * stride.
+
+    w13 uint8 [.., 2I, H] (W1 = gate rows first, then W3 = up; ``up_first`` swaps them),
+    w13_scales fp32 [.., 2I/128, H/128], w2 uint8 [.., H, I], w2_scales fp32 [.., H/128, I/128].
+    """
+    w13: torch.Tensor
+    w13_scales: torch.Tensor
+    w2: torch.Tensor
+    w2_scales: torch.Tensor
+    slots: torch.Tensor | None = None
+    experts: int | None = None
+    up_first: bool = False
+    swiglu_limit: float = 0.0
+
+    @property
+    def hidden(self) -> int:
+        return self.w13.shape[-1]
+
+    @property
+    def inter(self) -> int:
+        return self.w13.shape[-2] // 2
+
+    @property
+    def count(self) -> int:
+        if self.experts is not None:
+            return self.experts
+        return self.w13.shape[0] if self.w13.dim() == 3 else 1
+
+    def c_struct(self) -> _lib.FP8ExpertsC:
+        def stride(t: torch.Tensor) -> int:
+            return t.stride(0) * t.element_size() if t.dim() == 3 else 0
+
+        for name, t, dt in (("w13", self.w13, torch.uint8), ("w2", self.w2, torch.uint8),
+                            ("w13_scales", self.w13_scales, torch.float32), ("w2_scales", self.w2_scales, torch.float32)):
+            if t.dtype != dt:
+                raise ValueError(f"{name} must be {dt}, got {t.dtype}")
+            if t.stride(-1) != 1 or t.stride(-2) != t.shape[-1]:
+                raise ValueError(f"{name} rows must be contiguous")
+        H, I = self.hidden, self.inter
+        if H % 128 or I % 128:
+            raise ValueError("FP8 experts need hidden and intermediate multiples of 128")
+        if self.w2.shape[-2:] != (H, I) or self.w13_scales.shape[-2:] != (2 * I // 128, H // 128) \
+                or self.w2_scales.shape[-2:] != (H // 128, I // 128):
+            raise ValueError("FP8 expert region shapes do not agree")
+        return _lib.FP8ExpertsC(
+            self.w13.data_ptr(), self.w13_scales.data_ptr(), self.w2.data_ptr(), self.w2_scales.data_ptr(),
+            stride(self.w13), stride(self.w13_scales), stride(self.w2), stride(self.w2_scales),
+            0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
+            float(self.swiglu_limit))
+
+    def tensors(self):
+        return (self.w13, self.w13_scales, self.w2, self.w2_scales, self.slots)
+
+
+def moe_fp8(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, experts: FP8Experts,
+            shared: FP8Experts | None = None, shared_gate: torch.Tensor | None = None,
+            validate: bool = False) -> torch.Tensor:
+    """One FP8 MoE layer (DeepSeek form: shared_gate None = ungated shared expert); bf16 [.., H]."""
+    device = _require_device(x, indices, weights, *experts.tensors(), *(shared.tensors() if shared else ()),
+                             shared_gate)
+    x = _contig(x, torch.bfloat16, "x")
+    H = x.shape[-1]
+    T = x.numel() // H if H else 0
+    k = indices.shape[-1]
+    idx = _contig(indices, torch.int32, "indices").reshape(T, k)
+    w = _contig(weights, torch.float32, "weights").reshape(T, k)
+    _check_indices(idx, experts.count, validate)
+    sg = None if shared_gate is None else _contig(shared_gate, torch.bfloat16, "shared_gate").reshape(-1)
+    table = experts.c_struct()
+    sh = shared.c_struct() if shared is not None else None
+    ws_bytes = _lib.load().wm_moe_fp8_workspace_size(T, k, ctypes.byref(table))
+    ws = _workspace(ws_bytes, device)
+    y = torch.empty_like(x)
+    _lib.call("wm_moe_fp8", _ptr(x), T, _ptr(idx), _ptr(w), k, ctypes.byref(table),
+              ctypes.byref(sh) if sh is not None else None, _ptr(sg), _ptr(y), _ptr(ws), ws_bytes, _stream(device))
+    return y
+
+
+def experts_fp8(x: torch.Tensor, indices: torch.Tensor, experts: FP8Experts, validate: bool = False) -> torch.Tensor:
+    """Per-pair FP8 expert outputs in router order: [.., K, H] bf16 (_StreamingSwitchGLU contract)."""
+    device = _require_device(x, indices, *experts.tensors())
+    x = _contig(x, torch.bfloat16, "x")
+    H = x.shape[-1]
+    T = x.numel() // H if H else 0
+    k = indices.shape[-1]
+    idx = _contig(indices, torch.int32, "indices").reshape(T, k)
+    _check_indices(idx, experts.count, validate)
+    table = experts.c_struct()
+    ws_bytes = _lib.load().wm_moe_fp8_workspace_size(T, k, ctypes.byref(table))
+    ws = _workspace(ws_bytes, device)
+    out = torch.empty(*x.shape[:-1], k, H, dtype=torch.bfloat16, device=device)
+    _lib.call("wm_experts_fp8", _ptr(x), T, _ptr(idx), k, ctypes.byref(table), _ptr(out), _ptr(ws), ws_bytes,
+              _stream(device))
+    return out
+
+
 # ----------------------------------------------------------------------------- decode stack
 
 def residual_rmsnorm(residual: torch.Tensor, y: torch.Tensor | None, eps: float = 1e-6) -> torch.Tensor:

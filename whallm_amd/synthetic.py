@@ -12,7 +12,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .ops import MXFP4Experts
+from .ops import FP8Experts, MXFP4Experts
 
 SCALE_LOW, SCALE_HIGH = 119, 125  # 2**-8 .. 2**-2
 
@@ -76,3 +76,39 @@ def zipf_bias(experts: int, s: float = 1.1, rng: np.random.Generator | None = No
     if rng is not None:
         bias = bias[rng.permutation(experts)]
     return bias
+
+
+def fp8_experts_np(rng: np.random.Generator, experts: int, hidden: int, inter: int,
+                   scale_low: float = 2.0 ** -7, scale_high: float = 2.0 ** -5) -> dict:
+    """FP8-E4M3 experts as uint8 codes of N(0, 1) clipped to +-448 (round to nearest even,
+    via torch's float8_e4m3fn) with fp32 128x128 block scales uniform in [low, high)."""
+    def codes(*shape):
+        v = np.clip(rng.standard_normal(shape).astype(np.float32), -448, 448)
+        return torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+    def scales(*shape):
+        return rng.uniform(scale_low, scale_high, size=shape).astype(np.float32)
+
+    return {
+        "w13": codes(experts, 2 * inter, hidden), "w13_scales": scales(experts, 2 * inter // 128, hidden // 128),
+        "w2": codes(experts, hidden, inter), "w2_scales": scales(experts, hidden // 128, inter // 128),
+    }
+
+
+def fp8_experts_to_device(arrays: dict, device, **kw) -> FP8Experts:
+    return FP8Experts(*(torch.from_numpy(np.ascontiguousarray(arrays[n])).to(device)
+                        for n in ("w13", "w13_scales", "w2", "w2_scales")), **kw)
+
+
+def fp8_experts_device(experts: int, hidden: int, inter: int, device, generator: torch.Generator,
+                       scale_low: float = 2.0 ** -7, scale_high: float = 2.0 ** -5) -> FP8Experts:
+    """FP8 experts generated on the device (bench sizes)."""
+    def codes(*shape):
+        v = torch.randn(shape, device=device, generator=generator).clamp_(-448, 448)
+        return v.to(torch.float8_e4m3fn).view(torch.uint8)
+
+    def scales(*shape):
+        return torch.rand(shape, device=device, generator=generator) * (scale_high - scale_low) + scale_low
+
+    return FP8Experts(codes(experts, 2 * inter, hidden), scales(experts, 2 * inter // 128, hidden // 128),
+                      codes(experts, hidden, inter), scales(experts, hidden // 128, inter // 128))
