@@ -43,6 +43,7 @@ class DecodeStack:
     # MXFP4 weights straight into scaled MFMAs against E4M3 terms of the bf16 activations,
     # fp32 accumulation
     dtype = "mxfp4"
+    data = "synthetic (random-init MXFP4 weights, N(0,1) router logits and residual inputs)"
 
     def __init__(self, device, layers=48, hidden=2048, experts=512, inter=512, k=10, tokens=1, seed=0,
                  impl="persistent"):
@@ -190,6 +191,7 @@ class Prefill:
     """C3: one MXFP4 MoE layer at a 16,384-token prefill, Zipf(1.1)-skewed routing."""
     name = "c3-prefill"
     dtype = "bf16"
+    data = "synthetic (random-init MXFP4 weights, N(0,1) bf16 tokens, N(0,1) + Zipf(1.1) bias router logits)"
 
     def __init__(self, device, hidden=2048, experts=512, inter=512, k=10, tokens=16384, seed=0):
         from whallm_amd import synthetic as S
@@ -273,7 +275,227 @@ class Prefill:
                           f"oracle, {threads} threads), shared expert excluded"}
 
 
-WORKLOADS = {"c2-decode": DecodeStack, "c3-prefill": Prefill}
+class FP8Layer:
+    """C4: one DeepSeek-V3-style FP8 MoE layer (H 7168, 256 routed + 1 shared expert, I 2048,
+    top-8 sigmoid routing with group-limited selection: 8 groups, top 4), at 1 decode
+    token or a 4096-token prefill."""
+    dtype = "fp8-e4m3"
+    data = "synthetic (random-init FP8 weights + fp32 block scales, N(0,1) bf16 tokens and router logits)"
+
+    def __init__(self, device, tokens=1, hidden=7168, experts=256, inter=2048, k=8, seed=0):
+        from whallm_amd import synthetic as S
+        self.H, self.E, self.I, self.K, self.T = hidden, experts, inter, k, tokens
+        self.name = "c4-decode" if tokens == 1 else "c4-prefill"
+        self.device = device
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        log(f"[bench] generating {experts} + 1 FP8 experts (H {hidden}, I {inter}) on device")
+        self.experts = S.fp8_experts_device(experts, hidden, inter, device, g)
+        self.shared = S.fp8_experts_device(1, hidden, inter, device, g)
+        self.bias = torch.randn(experts, device=device, generator=g) * 0.1
+        self.gen = g
+        self.graph = None
+
+    def expert_bytes(self):
+        return 3 * self.H * self.I + 4 * (2 * self.I // 128) * (self.H // 128) + 4 * (self.H // 128) * (self.I // 128)
+
+    def algorithmic_bytes(self):
+        if self.T == 1:   # the routed experts and the shared one, plus logits, x and y
+            return (self.K + 1) * self.expert_bytes() + self.E * 4 + 2 * self.H * 2
+        return (self.E + 1) * self.expert_bytes() + self.T * self.H * 2 * 2 + self.T * self.E * 4
+
+    def flops(self):
+        return 2 * 3 * self.H * self.I * (self.K + 1) * self.T
+
+    def tokens_per_step(self):
+        return self.T
+
+    def prepare_inputs(self, steps):
+        n = min(steps, 4) if self.T > 1 else steps
+        self.step_logits = torch.randn(n, self.T, self.E, device=self.device, generator=self.gen)
+        self.step_x = torch.randn(n, self.T, self.H, device=self.device, generator=self.gen).to(torch.bfloat16)
+        self.logits = torch.empty(self.T, self.E, device=self.device)
+        self.x = torch.empty(self.T, self.H, dtype=torch.bfloat16, device=self.device)
+
+    def _body(self):
+        import whallm_amd as wa
+        idx, w = wa.route_scored(self.logits, self.bias, self.K, func="sigmoid", route_scale=2.5, n_groups=8,
+                                 topk_groups=4)
+        self.y = wa.moe_fp8(self.x, idx, w, self.experts, self.shared, None)
+
+    def capture(self):
+        self.logits.copy_(self.step_logits[0])
+        self.x.copy_(self.step_x[0])
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._body()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body()
+        torch.cuda.synchronize(self.device)
+
+    def step(self, i):
+        j = i % len(self.step_logits)
+        self.logits.copy_(self.step_logits[j])
+        self.x.copy_(self.step_x[j])
+        self.graph.replay()
+
+    def config(self):
+        return {"workload": f"{self.name}: DeepSeek-V3-style FP8 MoE layer, {self.T} token(s)/step",
+                "hidden": self.H, "experts": self.E, "moe_intermediate": self.I, "top_k": self.K,
+                "shared_experts": 1, "routing": "sigmoid + bias select, 8 groups / top-4 groups, route_scale 2.5",
+                "weights": "FP8-E4M3 of N(0,1) clipped to +-448, fp32 128x128 block scales",
+                "tokens": self.T, "activations": "bf16",
+                "hbm_resident_weight_gb": round((self.E + 1) * self.expert_bytes() / 1e9, 2)}
+
+    def cpu_baseline(self, budget_s: float):
+        from oracle import moe as M
+        from whallm_amd import synthetic as S
+        threads = len(os.sched_getaffinity(0))
+        logits = self.step_logits[0][:1].cpu().numpy()
+        x = self.step_x[0][:1].float().cpu().numpy()
+        idx, w = M.route_scored(logits, self.bias.cpu().numpy(), self.K, func="sigmoid", route_scale=2.5,
+                                n_groups=8, topk_groups=4)
+        I = self.I
+
+        def expert(tab, e):
+            w13, s13 = tab.w13[e].cpu().numpy(), tab.w13_scales[e].cpu().numpy()
+            return M.FP8Expert(w13[:I], s13[:I // 128], w13[I:], s13[I // 128:], tab.w2[e].cpu().numpy(),
+                               tab.w2_scales[e].cpu().numpy())
+
+        ids = [int(e) for e in idx[0]]
+        ex = {e: expert(self.experts, e) for e in ids}
+        sh = expert(self.shared, 0)
+        started = time.perf_counter()
+        with ThreadPoolExecutor(threads) as pool:
+            outs = list(pool.map(lambda e: M.fp8_expert_ffn(x, ex[e]), ids))
+        s_out = M.fp8_expert_ffn(x, sh)
+        M.combine(np.stack(outs, axis=1), w, s_out, None)
+        elapsed = time.perf_counter() - started
+        return {"value": round(1.0 / elapsed, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"1 token through the layer ({self.K} routed + shared FP8 experts; numpy fp32 "
+                          f"dequant-then-matmul oracle, {threads} threads over experts)"}
+
+
+class MtpVerify:
+    """C5: MTP verify step: 1 accepted + 3 draft tokens (M 4) through a 4-layer FP8 MoE stack
+    (C4 layers with the rmsnorm residual glue), a random bf16 LM head to fp32 logits over a
+    129,280-token vocabulary, then greedy acceptance on the device."""
+    name = "c5-verify"
+    dtype = "fp8-e4m3"
+    data = "synthetic (random-init FP8 experts and bf16 LM head, N(0,1) residual inputs and router logits)"
+
+    def __init__(self, device, layers=4, hidden=7168, experts=256, inter=2048, k=8, tokens=4, vocab=129280, seed=0):
+        from whallm_amd import synthetic as S
+        self.L, self.H, self.E, self.I, self.K, self.T, self.V = layers, hidden, experts, inter, k, tokens, vocab
+        self.device = device
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        log(f"[bench] generating {layers} x ({experts} + 1) FP8 experts and a {vocab} x {hidden} LM head")
+        self.layers = [S.fp8_experts_device(experts, hidden, inter, device, g) for _ in range(layers)]
+        self.shared = [S.fp8_experts_device(1, hidden, inter, device, g) for _ in range(layers)]
+        self.bias = [torch.randn(experts, device=device, generator=g) * 0.1 for _ in range(layers)]
+        self.head = (torch.randn(vocab, hidden, device=device, generator=g) * hidden ** -0.5).to(torch.bfloat16)
+        self.gen = g
+        self.graph = None
+
+    def expert_bytes(self):
+        return 3 * self.H * self.I + 4 * (2 * self.I // 128) * (self.H // 128) + 4 * (self.H // 128) * (self.I // 128)
+
+    def algorithmic_bytes(self):
+        # distinct experts a 4-token step can touch: at most T*K routed + 1 shared per layer
+        return self.L * (min(self.E, self.T * self.K) + 1) * self.expert_bytes() + self.V * self.H * 2 \
+            + self.T * self.V * 4
+
+    def tokens_per_step(self):
+        return self.T
+
+    def prepare_inputs(self, steps):
+        self.step_logits = torch.randn(steps, self.L, self.T, self.E, device=self.device, generator=self.gen)
+        self.step_r = torch.randn(steps, self.T, self.H, device=self.device, generator=self.gen)
+        self.logits = torch.empty(self.L, self.T, self.E, device=self.device)
+        self.r = torch.empty(self.T, self.H, device=self.device)
+        self.drafts = torch.zeros(self.T - 1, dtype=torch.int32, device=self.device)
+
+    def _layers(self):
+        import whallm_amd as wa
+        x = wa.ops.residual_rmsnorm(self.r, None)
+        for l in range(self.L):
+            idx, w = wa.route_scored(self.logits[l], self.bias[l], self.K, func="sigmoid", route_scale=2.5,
+                                     n_groups=8, topk_groups=4)
+            y = wa.moe_fp8(x, idx, w, self.layers[l], self.shared[l], None)
+            x = wa.ops.residual_rmsnorm(self.r, y)
+        self.x_last = x
+
+    def _head_and_accept(self):
+        import whallm_amd as wa
+        self.vocab_logits = torch.matmul(self.x_last, self.head.t()).float()
+        self.accept = wa.mtp_verify_greedy(self.vocab_logits, self.drafts)
+
+    def _body(self):
+        self._layers()
+        self._head_and_accept()
+
+    def capture(self):
+        self.logits.copy_(self.step_logits[0])
+        self.r.copy_(self.step_r[0])
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._body()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body()
+        torch.cuda.synchronize(self.device)
+
+    def step(self, i):
+        self.logits.copy_(self.step_logits[i])
+        self.r.copy_(self.step_r[i])
+        self.graph.replay()
+
+    def accept_ms(self, launches: int) -> float:
+        """Device time of the acceptance kernels alone (HIP events around direct launches)."""
+        import whallm_amd as wa
+        stream = torch.cuda.current_stream(self.device)
+        total = 0.0
+        for _ in range(launches):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            wa.mtp_verify_greedy(self.vocab_logits, self.drafts)
+            b.record(stream)
+            b.synchronize()
+            total += a.elapsed_time(b)
+        return total / launches
+
+    def config(self):
+        return {"workload": "c5-verify: MTP verify, 4 tokens (1 accepted + 3 drafts) through a 4-layer FP8 MoE "
+                            "stack, bf16 LM head to 129280 fp32 logits, greedy acceptance on the device",
+                "hidden": self.H, "experts": self.E, "moe_intermediate": self.I, "top_k": self.K, "layers": self.L,
+                "tokens": self.T, "vocab": self.V}
+
+    def cpu_baseline(self, budget_s: float):
+        from oracle import moe as M
+        threads = len(os.sched_getaffinity(0))
+        logits = self.vocab_logits.cpu().numpy()
+        drafts = self.drafts.cpu().numpy()
+        started = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - started < min(budget_s, 5.0):
+            M.verify_greedy(drafts, logits)
+            reps += 1
+        elapsed = (time.perf_counter() - started) / reps
+        return {"value": round(1.0 / elapsed, 3), "unit": "verifications/s", "cores": 1, "kind": "port",
+                "sample": f"greedy acceptance of {self.T - 1} drafts over [{self.T}, {self.V}] fp32 logits "
+                          f"(numpy oracle, {reps} repeats); the MoE layers are not part of this sample"}
+
+
+WORKLOADS = {"c2-decode": DecodeStack, "c3-prefill": Prefill, "c4-decode": FP8Layer, "c4-prefill": FP8Layer,
+             "c5-verify": MtpVerify}
 
 
 # ----------------------------------------------------------------------------- main
@@ -312,8 +534,12 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    wl = (DecodeStack(device, impl=args.decode_impl) if args.config == "c2-decode"
-          else WORKLOADS[args.config](device))
+    if args.config == "c2-decode":
+        wl = DecodeStack(device, impl=args.decode_impl)
+    elif args.config == "c4-prefill":
+        wl = FP8Layer(device, tokens=4096)
+    else:
+        wl = WORKLOADS[args.config](device)
     total = args.warmup + args.steps
     wl.prepare_inputs(total)
     wl.capture()
@@ -349,6 +575,22 @@ def main():
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("decode_persistent_c2"),
                     "kernel": kernel, "kernel_ms": round(k_ms, 5),
                     "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
+    elif isinstance(wl, FP8Layer):
+        achieved = wl.algorithmic_bytes() / (ms_per_step / 1e3) / 1e9
+        tflops = wl.flops() / (ms_per_step / 1e3) / 1e12
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "tflops": round(tflops, 2), "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
+                    "kernel": "FP8 MoE layer step (route_scored, FP8 expert kernels, combine) from one graph",
+                    "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
+    elif isinstance(wl, MtpVerify):
+        achieved = wl.algorithmic_bytes() / (ms_per_step / 1e3) / 1e9
+        a_ms = wl.accept_ms(20)
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": "verify step: 4 FP8 MoE layers + LM head + greedy acceptance, one graph",
+                    "verify_latency_ms": round(ms_per_step, 4), "acceptance_kernel_ms": round(a_ms, 5),
+                    "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
     else:
         tflops = wl.flops() / (ms_per_step / 1e3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -366,7 +608,7 @@ def main():
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": wl.dtype, "data": "synthetic (random-init MXFP4 weights, N(0,1) logits/inputs)",
+        "vs_baseline": None, "dtype": wl.dtype, "data": wl.data,
         "config": wl.config(), "roofline": roofline, "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }
