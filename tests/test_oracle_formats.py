@@ -1,10 +1,13 @@
 """Pins the format oracle (oracle/formats.py, oracle/c/oracle.c) — CPU only.
 
 Known-answer vectors come from the reference's Swift tests
-(Tests/DeepSeekRepackTests/DeepSeekRepackTests.swift:336-412); the rest are
-closed forms and an independent library decoder (torch.float8_e4m3fn).
+(Tests/DeepSeekRepackTests/DeepSeekRepackTests.swift:336-412), kept as data in
+tests/golden/reference_kats.json; the rest are closed forms and an independent
+library decoder (torch.float8_e4m3fn).
 """
 import hashlib
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -18,16 +21,7 @@ def _bf16_bits(values):
     return (np.asarray(values, np.float32).view(np.uint32) >> 16).astype(np.uint16)
 
 
-KAT2_BITS = [
-    49381, 49134, 16475, 49335, 48859, 16539, 49289, 16256, 16585, 49207, 16411, 49367, 49079, 16503, 49321, 0,
-    16553, 49271, 16311, 16599, 49179, 16439, 49353, 49024, 16521, 49307, 16091, 16567, 49243, 16366, 16613, 49152,
-    16466, 49339, 48914, 16535, 49294, 16219, 16581, 49216, 16402, 49371, 49097, 16494, 49326, 48658, 16549, 49280,
-    16293, 16594, 49189, 16430, 49358, 49042, 16517, 49312, 16018, 16562, 49253, 16347, 16608, 49161, 16457, 49344,
-]
-KAT2_WEIGHTS = [
-    207, 245, 105, 46, 215, 244, 107, 15, 231, 115, 92, 175, 230, 113, 77, 199,
-    245, 105, 46, 215, 244, 107, 143, 231, 115, 93, 175, 230, 113, 62, 199, 245,
-]
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 
 
 def _kat4_source():
@@ -38,41 +32,41 @@ def _kat4_source():
 
 @pytest.mark.parametrize("impl", ["numpy", "c"])
 def test_kat_fixed_vector(impl):
-    # DeepSeekRepackTests.swift:336-351
-    bits = _bf16_bits([0.5, 1, 1.5, 2, 3, 4, 6, -0.5, -1, -1.5, -2, -3, -4, -6] + [0] * 18)
+    kat = KATS["mxfp4_fixed_vector"]
     q = F.quantize_mxfp4_bf16 if impl == "numpy" else C.quantize_bf16
-    w, s = q(bits, 1, 32)
-    assert list(w.ravel()) == [0x21, 0x43, 0x65, 0x97, 0xBA, 0xDC, 0xFE] + [0] * 9
-    assert list(s.ravel()) == [127]
+    w, s = q(_bf16_bits(kat["values"]), kat["rows"], kat["columns"])
+    assert list(w.ravel()) == kat["weights"]
+    assert list(s.ravel()) == kat["scales"]
 
 
 @pytest.mark.parametrize("impl", ["numpy", "c"])
 def test_kat_bf16_rows(impl):
-    # DeepSeekRepackTests.swift:353-375
+    kat = KATS["mxfp4_bf16_rows"]
     q = F.quantize_mxfp4_bf16 if impl == "numpy" else C.quantize_bf16
-    w, s = q(np.array(KAT2_BITS, np.uint16), 2, 32)
-    assert list(w.ravel()) == KAT2_WEIGHTS
-    assert list(s.ravel()) == [127, 127]
+    w, s = q(np.array(kat["bf16_bits"], np.uint16), kat["rows"], kat["columns"])
+    assert list(w.ravel()) == kat["weights"]
+    assert list(s.ravel()) == kat["scales"]
 
 
 @pytest.mark.parametrize("impl", ["numpy", "c"])
 def test_kat_official_fp8_blocks(impl):
-    # DeepSeekRepackTests.swift:377-393
-    first = [0x30, 0x38, 0x3C, 0x40, 0x44, 0x48, 0x4C, 0xB0, 0xB8, 0xBC, 0xC0, 0xC4, 0xC8, 0xCC] + [0] * 114
-    src = np.array(first + [0] * (127 * 128), np.uint8)
+    kat = KATS["fp8_official_blocks"]
+    first = kat["first_bytes"]
+    src = np.array(first + [0] * (kat["rows"] * kat["columns"] - len(first)), np.uint8)
     q = F.quantize_mxfp4_fp8 if impl == "numpy" else C.quantize_fp8
-    w, s = q(src, np.array([0x3F80], np.uint16), 128, 128)
-    assert list(w.ravel()[:16]) == [0x21, 0x43, 0x65, 0x97, 0xBA, 0xDC, 0xFE] + [0] * 9
-    assert list(s.ravel()[:4]) == [127, 0, 0, 0]
+    w, s = q(src, np.array([kat["inverse_scale_bf16"]], np.uint16), kat["rows"], kat["columns"])
+    assert list(w.ravel()[:16]) == kat["weights_head"]
+    assert list(s.ravel()[:4]) == kat["scales_head"]
 
 
 @pytest.mark.parametrize("impl", ["numpy", "c"])
 def test_kat_fp8_sha256(impl):
-    # DeepSeekRepackTests.swift:395-412: pins e4m3 decode, x scale, bf16 RNE and the encoder end to end.
+    # Pins e4m3 decode, x scale, bf16 RNE and the encoder end to end.
+    kat = KATS["fp8_pattern_sha256"]
     q = F.quantize_mxfp4_fp8 if impl == "numpy" else C.quantize_fp8
-    w, s = q(_kat4_source(), np.array([0x3F40], np.uint16), 128, 128)
-    assert hashlib.sha256(w.tobytes()).hexdigest() == "7c332f3b69c7e580b8f3dd7c89bf44d18f81debfb17a648a7d131e28907a3b71"
-    assert hashlib.sha256(s.tobytes()).hexdigest() == "0fecfb3515a322ce43dca1e7d6115fcf2c1f34d474774097fb4eededdcc6cf49"
+    w, s = q(_kat4_source(), np.array([kat["inverse_scale_bf16"]], np.uint16), kat["rows"], kat["columns"])
+    assert hashlib.sha256(w.tobytes()).hexdigest() == kat["weights_sha256"]
+    assert hashlib.sha256(s.tobytes()).hexdigest() == kat["scales_sha256"]
 
 
 def test_encoders_reject_incomplete_plans():

@@ -1,0 +1,465 @@
+"""The reference runtime's expert-FFN operators, over the HIP kernels of libwhallm_moe.
+
+Same names, constructor arguments, call signatures, cache protocol and error
+behaviour as:
+
+* ``SparseMoE`` / ``StreamingExperts`` / ``MLP`` (runtime/deepseek_v4_ssd/qwen4_exp.py:763-1051),
+* ``_StreamingSwitchGLU`` and the DeepSeek gate / shared expert / activation
+  (runtime/deepseek_v4_ssd/model.py:318-546, deepseek_v41/moe.py:30-112),
+* the weight containers of expert_cache.py:32-75,
+
+with torch device tensors in place of mlx arrays. The cache is duck-typed as in the
+reference: ``current_batched(layer)`` (a whole-layer table: no host sync, the fused
+kernels index experts on the device), ``get_many(layer, ids)`` / ``iter_ready(layer, ids)``
+(individual resident experts: their regions are gathered into one table), plus the
+optional recording hooks. Routed experts always run on the library's kernels; a
+bf16 shared ``MLP`` and an activation other than (clamped) SwiGLU run as library GEMMs
+(hipBLASLt through torch) over weights that the library dequantizes.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, replace
+
+import torch
+
+from .ops import (FP8Experts, MXFP4Experts, dequant_fp8_blocks, dequant_mxfp4, experts_fp8, experts_mxfp4,
+                  linear_bf16, moe_fp8, moe_mxfp4, route_scored, route_softmax_topk)
+
+# Whole-layer prefill groups rows by expert from this many rows (qwen4_exp.py:789).
+GROUPED_PREFILL_ROWS = 64
+# MTP verification rows handled by the ready path (qwen4_exp.py:787).
+READY_VERIFICATION_ROWS = 16
+
+
+# ----------------------------------------------------------------------------- containers (expert_cache.py:32-75)
+
+@dataclass(frozen=True)
+class ExpertWeights:
+    """One DeepSeek expert: MXFP4 w1 (gate), w2 (down), w3 (up) regions, optionally the
+    fused w13 = [w3; w1] (expert_layout.py:43-51)."""
+    w1: torch.Tensor
+    w1_scales: torch.Tensor
+    w2: torch.Tensor
+    w2_scales: torch.Tensor
+    w3: torch.Tensor
+    w3_scales: torch.Tensor
+    w13: torch.Tensor | None = None
+    w13_scales: torch.Tensor | None = None
+
+
+@dataclass(frozen=True)
+class BatchedExperts(ExpertWeights):
+    """ExpertWeights with a leading expert axis (expert_cache.py:51-59)."""
+
+
+@dataclass(frozen=True)
+class QwenExpertWeights:
+    """One Qwen expert blob: gate_up = [gate; up] rows, down (expert_cache.py:62-67)."""
+    gate_up: torch.Tensor
+    gate_up_scales: torch.Tensor
+    down: torch.Tensor
+    down_scales: torch.Tensor
+
+
+@dataclass(frozen=True)
+class QwenBatchedExperts(QwenExpertWeights):
+    """QwenExpertWeights with a leading expert axis (expert_cache.py:70-75)."""
+
+
+@dataclass(frozen=True)
+class ResidentExperts:
+    """Experts made resident for one call; slots maps expert id -> index into
+    individual_weights (expert_cache.py:44-47)."""
+    individual_weights: tuple
+    slots: dict
+
+
+# ----------------------------------------------------------------------------- activations
+
+class ClampedSwiGLU:
+    """activation(up, gate) = silu(min(gate, limit)) * clip(up, -limit, limit); limit 0 is
+    plain SwiGLU (deepseek_v41/moe.py:30-43). Fused into the expert kernels."""
+
+    def __init__(self, limit: float = 0.0):
+        self.limit = float(limit)
+
+    def __call__(self, up: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        up, gate = up.float(), gate.float()
+        if self.limit > 0:
+            up = up.clamp(-self.limit, self.limit)
+            gate = gate.clamp(max=self.limit)
+        return torch.nn.functional.silu(gate) * up
+
+
+class SwiGLU(ClampedSwiGLU):
+    """mlx-lm SwitchGLU's default activation: silu(gate) * up."""
+
+    def __init__(self):
+        super().__init__(0.0)
+
+
+def _fused_limit(activation) -> float | None:
+    """The swiglu_limit the kernels apply for ``activation``, or None when it is not SwiGLU."""
+    if activation is None:
+        return 0.0
+    if isinstance(activation, ClampedSwiGLU):
+        return activation.limit
+    return None
+
+
+# ----------------------------------------------------------------------------- tables
+
+def _as_table(weights, activation_limit: float = 0.0):
+    """A batched weight container -> the library's expert table (MXFP4Experts / FP8Experts)."""
+    if isinstance(weights, (MXFP4Experts, FP8Experts)):
+        return weights
+    if isinstance(weights, QwenExpertWeights):   # gate rows first (qwen4_exp.py:816-818)
+        return MXFP4Experts(weights.gate_up, weights.gate_up_scales, weights.down, weights.down_scales,
+                            swiglu_limit=activation_limit)
+    if isinstance(weights, ExpertWeights):       # w13 = [w3 (up); w1 (gate)] (model.py:516-523)
+        if weights.w13 is not None and weights.w13_scales is not None:
+            w13, w13s = weights.w13, weights.w13_scales
+        else:
+            axis = weights.w1.dim() - 2
+            w13 = torch.cat([weights.w3, weights.w1], dim=axis)
+            w13s = torch.cat([weights.w3_scales, weights.w1_scales], dim=axis)
+        return MXFP4Experts(w13, w13s, weights.w2, weights.w2_scales, up_first=True,
+                            swiglu_limit=activation_limit)
+    raise TypeError(f"unsupported expert weights {type(weights).__name__}")
+
+
+def _stack_tables(tables: list):
+    """One table over the experts of ``tables`` (each a single expert, in order)."""
+    first = tables[0]
+    fields = [torch.stack([t.tensors()[i] for t in tables]) for i in range(4)]
+    return type(first)(*fields, up_first=first.up_first, swiglu_limit=first.swiglu_limit)
+
+
+def _resident_table(resident: ResidentExperts, experts: list[int], limit: float):
+    """Gather the individual experts of ``experts`` (unique ids) into one compact table."""
+    singles = []
+    for e in experts:
+        if e not in resident.slots:
+            raise ValueError(f"expert {e} is not resident")
+        singles.append(_as_table(resident.individual_weights[resident.slots[e]], limit))
+    return _stack_tables(singles)
+
+
+def _compact(indices: torch.Tensor, experts: list[int]) -> torch.Tensor:
+    """Expert ids -> positions in ``experts`` (sorted unique ids), on the device."""
+    lut = torch.full((max(experts) + 1,), -1, dtype=torch.int32, device=indices.device)
+    lut[torch.tensor(experts, dtype=torch.long, device=indices.device)] = torch.arange(
+        len(experts), dtype=torch.int32, device=indices.device)
+    return lut[indices.long()]
+
+
+def _host_ids(indices: torch.Tensor, expert_count: int | None):
+    flat = indices.reshape(-1).to("cpu", torch.int64)
+    if flat.numel() and (int(flat.min()) < 0 or (expert_count is not None and int(flat.max()) >= expert_count)):
+        raise ValueError("expert ID is outside the model")
+    return flat
+
+
+def _generic_experts(x: torch.Tensor, indices: torch.Tensor, table, activation) -> torch.Tensor:
+    """Per-pair outputs [T, K, H] for an activation the kernels do not fuse: the library
+    dequantizes each touched expert, the projections run as library GEMMs (the
+    _StreamingSwitchGLU arithmetic of model.py:395-426 with mx.quantized_matmul's
+    dequant-then-matmul)."""
+    T, K = indices.shape
+    H, I = table.hidden, table.inter
+    flat = indices.reshape(-1).long()
+    out = torch.empty(T * K, H, dtype=torch.bfloat16, device=x.device)
+    slots = None if table.slots is None else table.slots.to("cpu", torch.int64)
+    fp8 = isinstance(table, FP8Experts)
+    for e in torch.unique(flat).tolist():
+        rows = (flat == e).nonzero().squeeze(1)
+        slot = e if slots is None else int(slots[e])
+        w13, w13s, w2, w2s = (t[slot] if t.dim() == 3 else t for t in table.tensors()[:4])
+        if fp8:
+            wa, wd, src = dequant_fp8_blocks(w13, w13s), dequant_fp8_blocks(w2, w2s), x[rows // K].float()
+        else:
+            wa, wd = dequant_mxfp4(w13, w13s, torch.bfloat16), dequant_mxfp4(w2, w2s, torch.bfloat16)
+            src = x[rows // K]
+        first, second = (src @ wa.T).split(I, dim=-1)
+        up, gate = (first, second) if table.up_first else (second, first)
+        h = activation(up, gate).to(wd.dtype)
+        out[rows] = (h @ wd.T).to(torch.bfloat16)
+    return out.view(T, K, H)
+
+
+def resolve_table(cache, layer: int, indices: torch.Tensor, limit: float = 0.0):
+    """(expert table, indices into it) for one call: the whole-layer table when the cache
+    has one (no host synchronisation: the kernels map ids to slots on the device), else the
+    resident experts from iter_ready (single-token decode with ready_expert_decode) or
+    get_many, gathered into one table (qwen4_exp.py:857-944, model.py:325-371)."""
+    current = getattr(cache, "current_batched", None)
+    batched = current(layer) if callable(current) else None
+    if batched is not None:
+        capture = getattr(cache, "capture_prefill_seed_routes", None)
+        if capture is not None:
+            capture(layer, indices)
+        if getattr(cache, "route_cache_enabled", False):
+            cache.observe_batched_routes(layer, indices.to("cpu", torch.int32).numpy())
+        record = getattr(cache, "record_gather_qmm", None)
+        if callable(record):   # separate w1 / w3 regions cost the reference a third gather_qmm
+            record(3 if isinstance(batched, ExpertWeights) and batched.w13 is None else 2)
+        return replace(_as_table(batched), swiglu_limit=limit), indices
+    started = time.perf_counter()
+    model = getattr(cache, "model", None)
+    flat = _host_ids(indices, getattr(model, "expert_count", None))
+    record_sync = getattr(cache, "record_routing_sync", None)
+    if record_sync is not None:
+        record_sync(time.perf_counter() - started)
+    ids = flat.tolist()
+    unique = sorted(set(ids))
+    rows = indices.numel() // indices.shape[-1]
+    if rows == 1 and getattr(cache, "ready_expert_decode", False) and hasattr(cache, "iter_ready"):
+        ready = cache.iter_ready(layer, ids)
+        try:
+            got = dict(ready)
+        finally:
+            close = getattr(ready, "close", None)
+            if close is not None:
+                close()
+        resident = ResidentExperts(tuple(got[e] for e in unique), {e: i for i, e in enumerate(unique)})
+    else:
+        resident = cache.get_many(layer, ids)
+    return _resident_table(resident, unique, limit), _compact(indices, unique)
+
+
+# ----------------------------------------------------------------------------- Qwen operators
+
+class Linear:
+    """A bias-free bf16 linear (mlx nn.Linear(in, out, bias=False)); weight [out, in]."""
+
+    def __init__(self, inputs: int, outputs: int, device="cuda", weight: torch.Tensor | None = None):
+        self.weight = weight if weight is not None else torch.zeros(outputs, inputs, dtype=torch.bfloat16,
+                                                                    device=device)
+
+    def __call__(self, value: torch.Tensor) -> torch.Tensor:
+        return torch.nn.functional.linear(value, self.weight)
+
+
+class MLP:
+    """The bf16 shared expert: down(silu(gate(x)) * up(x)) (qwen4_exp.py:763-771)."""
+
+    def __init__(self, dimensions: int, intermediate: int, device="cuda"):
+        self.gate_proj = Linear(dimensions, intermediate, device)
+        self.up_proj = Linear(dimensions, intermediate, device)
+        self.down_proj = Linear(intermediate, dimensions, device)
+
+    def __call__(self, value: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(torch.nn.functional.silu(self.gate_proj(value)) * self.up_proj(value))
+
+
+class StreamingExperts:
+    """Routed Qwen experts: __call__(value [.., H], indices [.., K]) -> [.., K, H] in router
+    order (qwen4_exp.py:796-904).
+
+    The reference's flags are kept. ``grouped_prefill`` / ``sorted_prefill`` / ``wave_slots`` /
+    ``ready_verification`` choose how it submits MLX work; here every call is one launch
+    sequence whose rows the library groups by expert itself (the decode GEMV for up to
+    256 (token, expert) pairs, the grouped GEMM above that), so they change no result.
+    """
+
+    def __init__(self, layer: int, cache):
+        self.layer = layer
+        self.cache = cache
+        self.grouped_prefill = False
+        self.sorted_prefill = False
+        self.ready_verification = False
+        self.wave_slots = 0
+        self.wave_count = 0
+        self.wave_pairs = 0
+        self.wave_peak_experts = 0
+
+    @staticmethod
+    def _one(value: torch.Tensor, weights) -> torch.Tensor:
+        """One expert over rows ``value`` [n, H] (qwen4_exp.py:814-818)."""
+        table = _as_table(weights)
+        n = value.reshape(-1, value.shape[-1]).shape[0]
+        idx = torch.zeros(n, 1, dtype=torch.int32, device=value.device)
+        return experts_mxfp4(value.reshape(n, -1), idx, table)[:, 0].reshape(*value.shape[:-1], -1)
+
+    def table(self, indices: torch.Tensor, limit: float = 0.0):
+        """(expert table, indices into it) for one call; see ``resolve_table``."""
+        return resolve_table(self.cache, self.layer, indices, limit)
+
+    def __call__(self, value: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        if value.shape[:-1] != indices.shape[:-1]:
+            raise ValueError("value and indices disagree on the token axes")
+        if getattr(self.cache, "route_trace_enabled", False):
+            self.cache.record_routes(self.layer, indices.to("cpu", torch.int32).numpy())
+        table, idx = self.table(indices)
+        return experts_mxfp4(value, idx, table)
+
+
+class SparseMoE:
+    """Qwen MoE block (qwen4_exp.py:997-1051): softmax top-k router, streamed routed experts,
+    sigmoid-gated shared expert, routing-weighted combine.
+
+    ``shared_expert`` is the reference's bf16 ``MLP`` by default; set it to a one-expert
+    ``MXFP4Experts`` to run the shared expert inside the fused layer kernels, or to None
+    for a layer without one.
+    """
+
+    def __init__(self, args, layer: int, cache, device="cuda"):
+        H, E = args.hidden_size, args.num_experts
+        self.gate = Linear(H, E, device)
+        self.experts = StreamingExperts(layer, cache)
+        self.shared_expert = MLP(H, args.shared_expert_intermediate_size, device)
+        self.shared_expert_gate = Linear(H, 1, device)
+        self.top_k = args.num_experts_per_tok
+        self.norm_topk_prob = args.norm_topk_prob
+        self.cache = cache
+        self.layer = layer
+
+    def route(self, value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """(probabilities [.., E] fp32, indices [.., K] int32) of the router (qwen4_exp.py:1009-1013).
+        The router linear accumulates in fp32 as the native engine's GEMV does
+        (Native/QwenNative/engine.mm:2080-2091)."""
+        logits = linear_bf16(value, self.gate.weight)
+        indices, _, probabilities = route_softmax_topk(logits, self.top_k, True, probabilities=True)
+        return probabilities, indices
+
+    def _gates(self, value: torch.Tensor, routes=None):
+        """(indices, scores, shared) as qwen4_exp.py:1036-1046; shared is None when the shared
+        expert runs inside the layer kernel."""
+        if routes is None:
+            logits = linear_bf16(value, self.gate.weight)
+            indices, scores = route_softmax_topk(logits, self.top_k, self.norm_topk_prob)
+        else:
+            probabilities, indices = routes
+            indices = indices.to(torch.int32)
+            scores = torch.gather(probabilities.float(), -1, indices.long())
+            if self.norm_topk_prob:
+                scores = scores / scores.sum(dim=-1, keepdim=True)
+        if getattr(self.cache, "route_trace_enabled", False):
+            self.cache.record_routes(self.layer, indices.to("cpu", torch.int32).numpy())
+        shared = None
+        if self.shared_expert is not None and not isinstance(self.shared_expert, MXFP4Experts):
+            gate = torch.sigmoid(self.shared_expert_gate(value).float())
+            shared = (gate * self.shared_expert(value).float()).to(torch.bfloat16)
+        return indices, scores, shared
+
+    def _layer(self, value: torch.Tensor, indices, scores, shared) -> torch.Tensor:
+        table, idx = self.experts.table(indices)
+        if isinstance(self.shared_expert, MXFP4Experts):
+            return moe_mxfp4(value, idx, scores.contiguous(), table, self.shared_expert,
+                             self.shared_expert_gate.weight.reshape(-1))
+        y = moe_mxfp4(value, idx, scores.contiguous(), table)
+        return y if shared is None else (y.float() + shared.float()).to(torch.bfloat16)
+
+    def __call__(self, value: torch.Tensor, routes=None) -> torch.Tensor:
+        indices, scores, shared = self._gates(value, routes)
+        return self._layer(value, indices, scores, shared)
+
+    def merged(self, values: list[torch.Tensor]) -> list[torch.Tensor]:
+        """Each value through this block with one routed-expert call for all of them
+        (qwen4_exp.py:1020-1034)."""
+        gates = [self._gates(value) for value in values]
+        axis = values[0].dim() - 2
+        joined = torch.cat(values, dim=axis)
+        indices = torch.cat([g[0] for g in gates], dim=axis)
+        scores = torch.cat([g[1] for g in gates], dim=axis)
+        shared = None if gates[0][2] is None else torch.cat([g[2] for g in gates], dim=axis)
+        y = self._layer(joined, indices, scores, shared)
+        return list(torch.split(y, [v.shape[axis] for v in values], dim=axis))
+
+    @staticmethod
+    def _combine(routed: torch.Tensor, scores: torch.Tensor, shared: torch.Tensor) -> torch.Tensor:
+        """sum_k scores_k * routed_k + shared (qwen4_exp.py:1048-1051), fp32 accumulation."""
+        return ((routed.float() * scores[..., None].float()).sum(dim=-2) + shared.float()).to(routed.dtype)
+
+
+# ----------------------------------------------------------------------------- DeepSeek operators
+
+class _StreamingSwitchGLU:
+    """DeepSeek routed experts: __call__(x [.., H], indices [.., K]) -> [.., K, H] in router
+    order (model.py:318-385). ``activation(up, gate)``: ClampedSwiGLU / SwiGLU (or None)
+    run fused in the expert kernels; any other callable takes the dequantize-then-GEMM
+    path (the reference tests' ``lambda up, _gate: up``, test_runtime.py:2509-2745)."""
+
+    def __init__(self, layer: int, cache, activation=None):
+        self.layer = layer
+        self.cache = cache
+        self.activation = activation
+
+    def _table(self, indices: torch.Tensor, limit: float):
+        return resolve_table(self.cache, self.layer, indices, limit)
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        if x.shape[:-1] != indices.shape[:-1]:
+            raise ValueError("x and indices disagree on the token axes")
+        if getattr(self.cache, "route_trace_enabled", False):
+            self.cache.record_routes(self.layer, indices.to("cpu", torch.int32).numpy())
+        limit = _fused_limit(self.activation)
+        table, idx = self._table(indices, 0.0 if limit is None else limit)
+        if limit is None:
+            H = x.shape[-1]
+            T = x.numel() // H
+            out = _generic_experts(x.reshape(T, H), idx.reshape(T, -1), table, self.activation)
+            return out.reshape(*indices.shape, H)
+        if isinstance(table, FP8Experts):
+            return experts_fp8(x, idx, table)
+        return experts_mxfp4(x, idx, table)
+
+    def forward_with_resident(self, x: torch.Tensor, indices: torch.Tensor, resident: ResidentExperts):
+        """Token-shaped expert math from one pre-acquired union (model.py:387-395)."""
+        flat = _host_ids(indices, None)
+        unique = sorted(set(flat.tolist()))
+        limit = _fused_limit(self.activation)
+        table = _resident_table(resident, unique, 0.0 if limit is None else limit)
+        idx = _compact(indices, unique)
+        if limit is None:
+            H = x.shape[-1]
+            T = x.numel() // H
+            return _generic_experts(x.reshape(T, H), idx.reshape(T, -1), table, self.activation).reshape(
+                *indices.shape, H)
+        return (experts_fp8 if isinstance(table, FP8Experts) else experts_mxfp4)(x, idx, table)
+
+
+class Gate:
+    """DeepSeek router over precomputed logits-producing weight (deepseek_v41/moe.py:46-74):
+    scores f(x . W^T / temp), selection on scores + bias (ties -> lower index), weights
+    from the unbiased scores, normalised (sum + 1e-20) and scaled by route_scale. ``n_groups``
+    > 1 adds DeepSeek-V3 group-limited selection."""
+
+    def __init__(self, dim: int, experts: int, topk: int, score_func: str = "sqrtsoftplus",
+                 route_scale: float = 1.0, norm_topk_prob: bool = True, gate_temp: float = 1.0,
+                 n_groups: int = 1, topk_groups: int = 1, device="cuda"):
+        self.weight = torch.zeros(experts, dim, dtype=torch.bfloat16, device=device)
+        self.bias = torch.zeros(experts, dtype=torch.float32, device=device)
+        self.topk, self.score_func, self.route_scale = topk, score_func, route_scale
+        self.norm_topk_prob, self.gate_temp = norm_topk_prob, gate_temp
+        self.n_groups, self.topk_groups = n_groups, topk_groups
+
+    def __call__(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        logits = linear_bf16(x, self.weight)
+        if self.gate_temp != 1.0:
+            logits = logits / self.gate_temp
+        indices, weights = route_scored(logits, self.bias, self.topk, self.score_func, self.route_scale,
+                                        self.norm_topk_prob and self.topk > 1, self.n_groups, self.topk_groups)
+        return weights, indices
+
+
+def route_reduce(routed: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+    """sum_k routed_k * scores_k (model.py:544-546), fp32 accumulation, routed dtype out."""
+    return (routed.float() * scores[..., None].float()).sum(dim=-2).to(routed.dtype)
+
+
+def streaming_moe(gate: Gate, switch_mlp: _StreamingSwitchGLU, shared, x: torch.Tensor) -> torch.Tensor:
+    """The DeepSeek MoE forward (model.py:526-541): routed experts reduced by the routing
+    weights, plus the ungated shared expert. ``shared`` is a one-expert table (fused into
+    the layer kernel when the activation is SwiGLU) or a callable on x."""
+    weights, indices = gate(x)
+    limit = _fused_limit(switch_mlp.activation)
+    if limit is not None and isinstance(shared, (MXFP4Experts, FP8Experts)):
+        table, idx = switch_mlp._table(indices, limit)
+        shared = replace(shared, swiglu_limit=limit)
+        if isinstance(table, FP8Experts):
+            return moe_fp8(x, idx, weights, table, shared, None)
+        return moe_mxfp4(x, idx, weights, table, shared, None)
+    routed = route_reduce(switch_mlp(x, indices), weights)
+    return (routed.float() + shared(x).float()).to(x.dtype)
