@@ -35,6 +35,7 @@
 //
 // The shared expert is one more row group after the routed ones (rows P .. P+T-1). Work
 // tiles are mapped XCD-major so the column tiles of one row tile share an L2.
+#include <algorithm>
 #include <cmath>
 
 #include "wm_common.h"
@@ -221,6 +222,10 @@ __device__ __forceinline__ const_f32_ptr uniform_ptr(const float* p) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return (const_f32_ptr)(((uint64_t)hi << 32) | lo);
 }
+__device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uniform_f(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
 __device__ __forceinline__ const uint8_t* uniform_u8(const uint8_t* p) {
   const uint64_t v = (uint64_t)(uintptr_t)p;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
@@ -280,45 +285,34 @@ __device__ __forceinline__ void step_mfma(const Stage<W>& st, const LaneOffsets&
       sa[mi] = 127;
     }
   }
-  // B fragments one row tile ahead of their MFMAs
-  v8i bh[2], bl[2];
-  int sbh[2], sbl[2];
-  auto read_b = [&](int ni, int slot) {
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
     const int db = 16 * ni * CHUNK;
     const uint4 h0 = *reinterpret_cast<const uint4*>(st.b + lo.b[0] + db);
     const uint4 h1 = *reinterpret_cast<const uint4*>(st.b + lo.b[1] + db);
     const uint4 l0 = *reinterpret_cast<const uint4*>(st.b + lo.b[2] + db);
     const uint4 l1 = *reinterpret_cast<const uint4*>(st.b + lo.b[3] + db);
-    bh[slot] = v8i{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-    bl[slot] = v8i{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
-    sbh[slot] = st.bs[lo.bs + 16 * ni * 8];
-    sbl[slot] = st.bs[lo.bs + 16 * ni * 8 + 4];
-  };
-  read_b(0, 0);
-#pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    const int cur = ni & 1;
-    if (ni + 1 < NI) read_b(ni + 1, cur ^ 1);
-    // the next row tile's reads are issued before this one's MFMAs, and only one is in flight
-    __builtin_amdgcn_sched_barrier(0);
+    const v8i bh = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+    const v8i bl = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+    const int sbh = st.bs[lo.bs + 16 * ni * 8], sbl = st.bs[lo.bs + 16 * ni * 8 + 4];
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       if constexpr (W::FMT == FMT_FP4) {
-        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bh[cur], acc[mi][ni], FMT_FP4, FMT_FP8,
-                                                                       0, sa[mi], 0, sbh[cur]);
-        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bl[cur], acc[mi][ni], FMT_FP4, FMT_FP8,
-                                                                       0, sa[mi], 0, sbl[cur]);
+        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bh, acc[mi][ni], FMT_FP4, FMT_FP8, 0,
+                                                                       sa[mi], 0, sbh);
+        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bl, acc[mi][ni], FMT_FP4, FMT_FP8, 0,
+                                                                       sa[mi], 0, sbl);
       } else {
         v4f blk = {0.0f, 0.0f, 0.0f, 0.0f};
-        blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bh[cur], blk, FMT_FP8, FMT_FP8, 0, 127, 0,
-                                                               sbh[cur]);
-        blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bl[cur], blk, FMT_FP8, FMT_FP8, 0, 127, 0,
-                                                               sbl[cur]);
+        blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bh, blk, FMT_FP8, FMT_FP8, 0, 127, 0, sbh);
+        blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bl, blk, FMT_FP8, FMT_FP8, 0, 127, 0, sbl);
         const float s = bscale(mi);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[mi][ni][r] = fmaf(s, blk[r], acc[mi][ni][r]);
       }
     }
+    // one row tile's fragment live at a time (the scheduler would otherwise hoist all four
+    // reads and run out of registers)
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -389,27 +383,65 @@ struct Loader {
 // it, and no memory fence.
 __device__ __forceinline__ void ring_wait_all() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// The tile's K loop over `steps` 128-wide steps through two LDS stages (stage k % 2 holds
-// step k). At the top of step k every wave has the loads of step k landed and is done
-// with stage k - 1, which then takes the loads of step k + 1. The loop is unrolled over
-// the two stages so each stage's address is static.
-template <typename W, typename MRow, typename BScale>
-__device__ __forceinline__ void k_loop(Loader<W>& ld, Stage<W>& s0, Stage<W>& s1, int steps, v4f (&acc)[MI][NI],
-                                       const LaneOffsets& lo, MRow mrow, BScale bscale) {
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  ld.issue(s0, 0);
-  auto body = [&](int k, Stage<W>& stage_k, Stage<W>& stage_next) {
-    if (k >= steps) return;
+// The tiles of this workgroup in a persistent launch: XCD x takes the contiguous range
+// [x * share, (x + 1) * share) of the (row tile, column tile) list, and its workgroups
+// take every (gridDim / 8)-th tile of it, so the column tiles of a row tile (which read
+// the same rows) and the row tiles of an expert (the same weights) meet in one L2.
+struct TileRange {
+  int first, stride, count;
+};
+__device__ __forceinline__ TileRange tile_range(int active) {
+  const int xcd = blockIdx.x % XCDS, local = blockIdx.x / XCDS, per = gridDim.x / XCDS;
+  const int share = (active + XCDS - 1) / XCDS;
+  const int hi = min(xcd * share + share, active);
+  TileRange t{xcd * share + local, per, 0};
+  if (t.first < hi) t.count = (hi - t.first + per - 1) / per;
+  return t;
+}
+
+// Persistent K loop over this workgroup's tiles, as one flat sequence of 128-wide steps
+// through two LDS stages (global step g uses stage g % 2; the loop is unrolled over the
+// two stages so their addresses are static). At the top of each step every wave has the
+// step's loads landed and is done with the other stage, which then takes the next step's
+// loads: the tile's next K step, or at a tile's last step the next tile's first step. The
+// next tile is set up (index loads, load offsets) after the MFMAs of the tile's
+// second-to-last step, and its first loads fly during this tile's epilogue.
+//   setup(j, tile) -> bool: fills tile j's state; false for a tile with no rows
+//   mfma(tile, stage, k): step k of a tile
+//   epilogue(tile): after a tile's last step
+template <typename W, typename Tile, typename Setup, typename Mfma, typename Epilogue>
+__device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps, Stage<W>& s0, Stage<W>& s1,
+                                                 Setup setup, Mfma mfma, Epilogue epilogue) {
+  if (tr.count == 0) return;
+  Tile cur, nxt;
+  bool cur_ok = setup(0, cur), nxt_ok = false;
+  if (cur_ok) cur.ld.issue(s0, 0);
+  const int total = tr.count * steps;
+  auto body = [&](int g, Stage<W>& stage, Stage<W>& other) {
+    if (g >= total) return;
+    const int j = g / steps, k = g - j * steps;
     ring_wait_all();
-    if (k + 1 < steps) ld.issue(stage_next, k + 1);
-    step_mfma<W>(stage_k, lo, acc, mrow, [&](int mi) { return bscale(k, mi); });
+    if (k + 1 < steps) {
+      if (cur_ok) cur.ld.issue(other, k + 1);
+    } else if (j + 1 < tr.count && steps > 1 && nxt_ok) {
+      nxt.ld.issue(other, 0);
+    }
+    if (cur_ok) mfma(cur, stage, k);
+    if (k == steps - 2 && j + 1 < tr.count) nxt_ok = setup(j + 1, nxt);
+    if (k == steps - 1) {
+      if (cur_ok) epilogue(cur);
+      if (steps == 1 && j + 1 < tr.count) {
+        nxt_ok = setup(j + 1, nxt);
+        if (nxt_ok) nxt.ld.issue(other, 0);
+      }
+      cur = nxt;
+      cur_ok = nxt_ok;
+      nxt_ok = false;
+    }
   };
-  for (int ks = 0; ks < steps; ks += 2) {
-    body(ks, s0, s1);
-    body(ks + 1, s1, s0);
+  for (int g = 0; g < total; g += 2) {
+    body(g, s0, s1);
+    body(g + 1, s1, s0);
   }
 }
 
@@ -451,11 +483,18 @@ __device__ __forceinline__ void act_terms(float v0, float v1, float v2, float v3
 }
 
 // ---------------------------------------------------------------------------------
-// gate_up: act rows of the tile's TW / 2 intermediate columns. Weight tile rows
-// [0, TW/2) are the gate rows nt * TW/2 + j, [TW/2, TW) the matching up rows; wave wn owns
-// gate rows 64 wn + [0, 64) (mi 0..3) and the same up rows (mi 4..7). When I is not a
-// multiple of TW / 2, the last tile's columns past I are computed on repeated rows and not
-// written.
+// gate_up: act rows of a tile's TW / 2 intermediate columns. Weight tile rows [0, TW/2)
+// are the gate rows nt * TW/2 + j, [TW/2, TW) the matching up rows; wave wn owns gate rows
+// 64 wn + [0, 64) (mi 0..3) and the same up rows (mi 4..7). When I is not a multiple of
+// TW / 2, the last tile's columns past I are computed on repeated rows and not written.
+
+template <typename W>
+struct GateUpTile {
+  Loader<W> ld;
+  int begin, end, nt, valid;
+  float limit;
+  const_f32_ptr sg, su;   // FP8 block scales of the wave's gate and up rows (per K step)
+};
 
 template <typename W, typename Table>
 __global__ void __launch_bounds__(64 * W::WAVES) gate_up_kernel(const uint8_t* __restrict__ x8,
@@ -465,104 +504,132 @@ __global__ void __launch_bounds__(64 * W::WAVES) gate_up_kernel(const uint8_t* _
   constexpr int TG = W::TW / 2;  // gate (and up) rows per tile
   const int H = routed.hidden, I = routed.inter;
   const int n_tiles = (I + TG - 1) / TG;
-  int logical;
-  if (!map_work(active_row_tiles(L) * n_tiles, logical)) return;
-  const int mt = logical / n_tiles, nt = logical % n_tiles;
-  int expert, begin, end;
-  if (!resolve_tile(L, mt, expert, begin, end)) return;
-  const TileWeights tw = tile_weights(routed, shared, expert);
+  const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-
-  auto token_of = [&](int pr) { return pr < L.pairs ? L.order[pr] / L.k : pr - L.pairs; };
-  const int valid = min(TG, I - nt * TG);  // a multiple of 128
-  const int gate0 = (tw.up_first ? I : 0) + nt * TG;
-  const int up0 = (tw.up_first ? 0 : I) + nt * TG;
-  auto weight_row = [gate0, up0, valid](int j) {
-    const int jj = j % TG;
-    return (j < TG ? gate0 : up0) + (jj < valid ? jj : jj % valid);
-  };
-  const int64_t wrow_bytes = (int64_t)H * W::STEP_BYTES / 128;
-  Loader<W> ld;
-  ld.init(
-      x8, xs, H / 128, tw.w13, tw.w13s,
-      // pad rows repeat the tile's first row; their results are never written
-      [&](int r) { return token_of(begin + r < end ? begin + r : begin); },
-      [&](int j) { return (uint32_t)(weight_row(j) * wrow_bytes); },
-      [&](int j) { return (uint32_t)(weight_row(j) * (H / 32)); });
-
   const int wm = wave & 1, wn = wave >> 1;
-  // FP8: the wave's 64 gate (up) rows lie in one 128-row scale block
-  const const_f32_ptr sg =
-      uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(weight_row(64 * wn) / 128) * (H / 128));
-  const const_f32_ptr su =
-      uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(weight_row(TG + 64 * wn) / 128) * (H / 128));
-  v4f acc[MI][NI];
   const LaneOffsets lo = lane_offsets<W>(64 * wn, wm);
-  auto loop = [&](Stage<W>& s0, Stage<W>& s1) {
-    k_loop<W>(ld, s0, s1, H / 128, acc, lo, [](int mi) { return (mi < 4 ? 0 : TG) + 16 * (mi & 3); },
-              [&](int ks, int mi) { return W::FMT == FMT_FP8 ? (mi < 4 ? sg[ks] : su[ks]) : 1.0f; });
+  const int64_t wrow_bytes = (int64_t)H * W::STEP_BYTES / 128;
+  using Tile = GateUpTile<W>;
+
+  auto setup = [&](int j, Tile& t) {
+    const int logical = tr.first + tr.stride * j;
+    const int mt = logical / n_tiles;
+    t.nt = logical - mt * n_tiles;
+    int expert, begin_, end_;
+    if (!resolve_tile(L, mt, expert, begin_, end_)) return false;
+    t.begin = uniform_i(begin_);
+    t.end = uniform_i(end_);
+    const TileWeights tw = tile_weights(routed, shared, uniform_i(expert));
+    t.limit = uniform_f(tw.limit);
+    t.valid = min(TG, I - t.nt * TG);  // a multiple of 128
+    const int gate0 = (tw.up_first ? I : 0) + t.nt * TG;
+    const int up0 = (tw.up_first ? 0 : I) + t.nt * TG;
+    const int valid = t.valid;
+    auto weight_row = [gate0, up0, valid](int r) {
+      const int rr = r % TG;
+      return (r < TG ? gate0 : up0) + (rr < valid ? rr : rr % valid);
+    };
+    const int begin = t.begin, end = t.end;
+    auto token_of = [&](int pr) { return pr < L.pairs ? L.order[pr] / L.k : pr - L.pairs; };
+    t.ld.init(
+        x8, xs, H / 128, tw.w13, tw.w13s,
+        // pad rows repeat the tile's first row; their results are never written
+        [&](int r) { return token_of(begin + r < end ? begin + r : begin); },
+        [&](int r) { return (uint32_t)(weight_row(r) * wrow_bytes); },
+        [&](int r) { return (uint32_t)(weight_row(r) * (H / 32)); });
+    // FP8: the wave's 64 gate (up) rows lie in one 128-row scale block
+    t.sg = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(weight_row(64 * wn) / 128) * (H / 128));
+    t.su = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(weight_row(TG + 64 * wn) / 128) * (H / 128));
+    return true;
   };
-  __shared__ Stage<W> s0, s1;
-  loop(s0, s1);
-  if (64 * wn >= valid) return;  // after the K loop: every wave takes part in its barriers
+
+  v4f acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto mfma = [&](const Tile& t, const Stage<W>& st, int k) {
+    step_mfma<W>(st, lo, acc, [](int mi) { return (mi < 4 ? 0 : TG) + 16 * (mi & 3); },
+                 [&](int mi) { return W::FMT == FMT_FP8 ? (mi < 4 ? t.sg[k] : t.su[k]) : 1.0f; });
+  };
 
   // Epilogue: lane holds act columns col0 + 16 mi + 4 g + r (mi 0..3) of row
   // 64 wm + 16 ni + c, col0 = nt * TG + 64 wn: 128-wide act chunk col0 / 128, K offset
   // kin0 = col0 % 128 (0 or 64). E8M0 block (kin0 + 32 half) / 32 holds mi 2 half, 2 half + 1.
-  const int c = lane % 16, g = lane / 16;
-  const int chunks = I / 128;
-  const int col0 = nt * TG + 64 * wn;
-  const int chunk = col0 / 128, kin0 = col0 % 128;
+  auto epilogue = [&](const Tile& t) {
+    if (64 * wn < t.valid) {
+      const int c = lane % 16, g = lane / 16;
+      const int chunks = I / 128;
+      const int col0 = t.nt * TG + 64 * wn;
+      const int chunk = col0 / 128, kin0 = col0 % 128;
 #pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    const int row = begin + 64 * wm + 16 * ni + c;
+      for (int ni = 0; ni < NI; ++ni) {
+        const int row = t.begin + 64 * wm + 16 * ni + c;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      float h[2][4];
-      float amax = 0.0f;
+        for (int half = 0; half < 2; ++half) {
+          float h[2][4];
+          float amax = 0.0f;
 #pragma unroll
-      for (int m = 0; m < 2; ++m)
+          for (int m = 0; m < 2; ++m)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int mi = 2 * half + m;
-          float gv = acc[mi][ni][r], uv = acc[mi + 4][ni][r];
-          if (tw.limit > 0.0f) {
-            gv = fminf(gv, tw.limit);
-            uv = fminf(fmaxf(uv, -tw.limit), tw.limit);
+            for (int r = 0; r < 4; ++r) {
+              const int mi = 2 * half + m;
+              float gv = acc[mi][ni][r], uv = acc[mi + 4][ni][r];
+              if (t.limit > 0.0f) {
+                gv = fminf(gv, t.limit);
+                uv = fminf(fmaxf(uv, -t.limit), t.limit);
+              }
+              h[m][r] = silu(gv) * uv;
+              amax = fmaxf(amax, fabsf(h[m][r]));
+            }
+          amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+          amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+          if (row >= t.end) continue;
+          const int s = term_exponent(amax);
+          const float f = pow2_biased(254 - s);
+          uint8_t* dst = a8 + ((int64_t)row * chunks + chunk) * CHUNK;
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            uint32_t hi, lo_;
+            act_terms(h[m][0] * f, h[m][1] * f, h[m][2] * f, h[m][3] * f, hi, lo_);
+            // K = kin0 + 32 half + 16 m + 4 g + r -> B-operand position 32 (K/16 % 4) + 16 (K/64) + K % 16
+            const int K = kin0 + 32 * half + 16 * m + 4 * g;
+            const int pos = 32 * ((K >> 4) & 3) + 16 * (K >> 6) + (K & 15);
+            *reinterpret_cast<uint32_t*>(dst + pos) = hi;
+            *reinterpret_cast<uint32_t*>(dst + 128 + pos) = lo_;
           }
-          h[m][r] = silu(gv) * uv;
-          amax = fmaxf(amax, fabsf(h[m][r]));
+          if (g == 0) {
+            const int blk = (kin0 >> 5) + half;
+            uint8_t* sd = as8 + ((int64_t)row * chunks + chunk) * 8;
+            sd[blk] = (uint8_t)s;
+            sd[4 + blk] = (uint8_t)(s > 4 ? s - 4 : 0);
+          }
         }
-      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-      if (row >= end) continue;
-      const int s = term_exponent(amax);
-      const float f = pow2_biased(254 - s);
-      uint8_t* dst = a8 + ((int64_t)row * chunks + chunk) * CHUNK;
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        uint32_t hi, lo;
-        act_terms(h[m][0] * f, h[m][1] * f, h[m][2] * f, h[m][3] * f, hi, lo);
-        // K = kin0 + 32 half + 16 m + 4 g + r -> B-operand position 32 (K/16 % 4) + 16 (K/64) + K % 16
-        const int K = kin0 + 32 * half + 16 * m + 4 * g;
-        const int pos = 32 * ((K >> 4) & 3) + 16 * (K >> 6) + (K & 15);
-        *reinterpret_cast<uint32_t*>(dst + pos) = hi;
-        *reinterpret_cast<uint32_t*>(dst + 128 + pos) = lo;
-      }
-      if (g == 0) {
-        const int blk = (kin0 >> 5) + half;
-        uint8_t* sd = as8 + ((int64_t)row * chunks + chunk) * 8;
-        sd[blk] = (uint8_t)s;
-        sd[4 + blk] = (uint8_t)(s > 4 ? s - 4 : 0);
       }
     }
-  }
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  };
+
+  __shared__ Stage<W> s0, s1;
+  persistent_tiles<W, Tile>(tr, H / 128, s0, s1, setup, mfma, epilogue);
 }
 
 // ---------------------------------------------------------------------------------
 // down: out[row, n] = w(row) * act[row] . W2[n], bf16, permuted rows; tile = 128 rows x
 // TW output columns, wave wn owns columns 128 wn + [0, 128). When H is not a multiple of
 // TW, the last tile's columns past H are computed on repeated rows and not written.
+
+template <typename W>
+struct DownTile {
+  Loader<W> ld;
+  int begin, end, nt, valid;
+  int slot;               // LDS slot of the tile's row weights (tiles alternate)
+  const_f32_ptr sd;       // FP8 block scales of the wave's 128 columns (per K step)
+};
 
 template <typename W, typename Table>
 __global__ void __launch_bounds__(64 * W::WAVES) down_kernel(const uint8_t* __restrict__ a8,
@@ -571,54 +638,82 @@ __global__ void __launch_bounds__(64 * W::WAVES) down_kernel(const uint8_t* __re
                                                              Table routed, Table shared, uint16_t* __restrict__ out) {
   const int H = routed.hidden, I = routed.inter;
   const int n_tiles = (H + W::TW - 1) / W::TW;
-  int logical;
-  if (!map_work(active_row_tiles(L) * n_tiles, logical)) return;
-  const int mt = logical / n_tiles, nt = logical % n_tiles;
-  int expert, begin, end;
-  if (!resolve_tile(L, mt, expert, begin, end)) return;
-  const TileWeights tw = tile_weights(routed, shared, expert);
+  const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int valid = min(W::TW, H - nt * W::TW);  // a multiple of 128
-  auto col_row = [&](int j) { return nt * W::TW + (j < valid ? j : j % valid); };  // never addresses past H
-
-  const int64_t wrow_bytes = (int64_t)I * W::STEP_BYTES / 128;
-  Loader<W> ld;
-  ld.init(
-      a8, as8, I / 128, tw.w2, tw.w2s, [&](int r) { return begin + r < end ? begin + r : begin; },
-      [&](int j) { return (uint32_t)(col_row(j) * wrow_bytes); },
-      [&](int j) { return (uint32_t)(col_row(j) * (I / 32)); });
   const int wm = wave & 1, wn = wave >> 1;
-  // FP8: the wave's 128 columns are one 128-row scale block
-  const const_f32_ptr sd =
-      uniform_ptr(reinterpret_cast<const float*>(tw.w2s) + (int64_t)(col_row(128 * wn) / 128) * (I / 128));
+  const LaneOffsets lo = lane_offsets<W>(128 * wn, wm);
+  const int64_t wrow_bytes = (int64_t)I * W::STEP_BYTES / 128;
+  using Tile = DownTile<W>;
+  __shared__ float row_weight[2][BM];
+
+  auto setup = [&](int j, Tile& t) {
+    const int logical = tr.first + tr.stride * j;
+    const int mt = logical / n_tiles;
+    t.nt = logical - mt * n_tiles;
+    int expert, begin_, end_;
+    if (!resolve_tile(L, mt, expert, begin_, end_)) return false;
+    t.begin = uniform_i(begin_);
+    t.end = uniform_i(end_);
+    const TileWeights tw = tile_weights(routed, shared, uniform_i(expert));
+    t.valid = min(W::TW, H - t.nt * W::TW);  // a multiple of 128
+    const int nt = t.nt, valid = t.valid, begin = t.begin, end = t.end;
+    auto col_row = [nt, valid](int r) { return nt * W::TW + (r < valid ? r : r % valid); };  // never past H
+    t.ld.init(
+        a8, as8, I / 128, tw.w2, tw.w2s, [&](int r) { return begin + r < end ? begin + r : begin; },
+        [&](int r) { return (uint32_t)(col_row(r) * wrow_bytes); },
+        [&](int r) { return (uint32_t)(col_row(r) * (I / 32)); });
+    // routing weight (or shared gate) of the tile's rows, kept in LDS until the epilogue (at
+    // least one barrier later; the two slots alternate between consecutive tiles)
+    t.slot = j & 1;
+    if (threadIdx.x < BM) {
+      const int row = begin + (int)threadIdx.x;
+      float w = 1.0f;
+      if (weighted && row < end) w = row < L.pairs ? weights[L.order[row]] : L.shared_gate[row - L.pairs];
+      row_weight[t.slot][threadIdx.x] = w;
+    }
+    // FP8: the wave's 128 columns are one 128-row scale block
+    t.sd = uniform_ptr(reinterpret_cast<const float*>(tw.w2s) + (int64_t)(col_row(128 * wn) / 128) * (I / 128));
+    return true;
+  };
 
   v4f acc[MI][NI];
-  const LaneOffsets lo = lane_offsets<W>(128 * wn, wm);
-  auto loop = [&](Stage<W>& s0, Stage<W>& s1) {
-    k_loop<W>(ld, s0, s1, I / 128, acc, lo, [](int mi) { return 16 * mi; },
-              [&](int ks, int) { return W::FMT == FMT_FP8 ? sd[ks] : 1.0f; });
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto mfma = [&](const Tile& t, const Stage<W>& st, int k) {
+    step_mfma<W>(st, lo, acc, [](int mi) { return 16 * mi; },
+                 [&](int) { return W::FMT == FMT_FP8 ? t.sd[k] : 1.0f; });
   };
-  __shared__ Stage<W> s0, s1;
-  loop(s0, s1);
-  if (128 * wn >= valid) return;  // after the K loop: every wave takes part in its barriers
 
   // lane holds output columns nt*TW + 128 wn + 16 mi + 4 g + r of row 64 wm + 16 ni + c
-  const int c = lane % 16, g = lane / 16;
+  auto epilogue = [&](const Tile& t) {
+    if (128 * wn < t.valid) {
+      const int c = lane % 16, g = lane / 16;
 #pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    const int row = begin + 64 * wm + 16 * ni + c;
-    if (row >= end) continue;
-    float w = 1.0f;
-    if (weighted) w = row < L.pairs ? weights[L.order[row]] : L.shared_gate[row - L.pairs];
+      for (int ni = 0; ni < NI; ++ni) {
+        const int row = t.begin + 64 * wm + 16 * ni + c;
+        if (row >= t.end) continue;
+        const float w = row_weight[t.slot][64 * wm + 16 * ni + c];
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      const int col = nt * W::TW + 128 * wn + 16 * mi + 4 * g;
-      uint2 o;
-      o.x = f32_to_bf16_bits(w * acc[mi][ni][0]) | ((uint32_t)f32_to_bf16_bits(w * acc[mi][ni][1]) << 16);
-      o.y = f32_to_bf16_bits(w * acc[mi][ni][2]) | ((uint32_t)f32_to_bf16_bits(w * acc[mi][ni][3]) << 16);
-      *reinterpret_cast<uint2*>(out + (int64_t)row * H + col) = o;
+        for (int mi = 0; mi < MI; ++mi) {
+          const int col = t.nt * W::TW + 128 * wn + 16 * mi + 4 * g;
+          uint2 o;
+          o.x = f32_to_bf16_bits(w * acc[mi][ni][0]) | ((uint32_t)f32_to_bf16_bits(w * acc[mi][ni][1]) << 16);
+          o.y = f32_to_bf16_bits(w * acc[mi][ni][2]) | ((uint32_t)f32_to_bf16_bits(w * acc[mi][ni][3]) << 16);
+          *reinterpret_cast<uint2*>(out + (int64_t)row * H + col) = o;
+        }
+      }
     }
-  }
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  };
+
+  __shared__ Stage<W> s0, s1;
+  persistent_tiles<W, Tile>(tr, I / 128, s0, s1, setup, mfma, epilogue);
 }
 
 // ---------------------------------------------------------------------------------
@@ -682,6 +777,20 @@ __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __res
 // Host side.
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Compute units of the current device (queried once per device).
+static int compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) fail("prefill: device index out of range");
+  if (!cached[dev]) {
+    int n = 0;
+    check_hip(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    cached[dev] = n > 0 ? n : 1;
+  }
+  return cached[dev];
+}
 
 struct Layout {
   size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, x8, xs, a8, as8, rows, total;
@@ -757,10 +866,12 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
   check_launch("split_rows");
   const Table sh = shared ? *shared : routed;
   const int64_t max_row_tiles = (pairs + BM - 1) / BM + routed.experts + (has_shared ? (tokens + BM - 1) / BM : 0);
-  // Upper bound of the work tiles, rounded up so every XCD's share fits the grid.
+  // Persistent launches: one workgroup per CU (the LDS stages allow one), a multiple of the
+  // 8 XCDs, and no more than the work tiles can use.
+  const int cus = compute_units();
   auto grid_for = [&](int n_tiles) {
     const int64_t work = max_row_tiles * n_tiles;
-    const int64_t per_xcd = (work + XCDS - 1) / XCDS;
+    const int64_t per_xcd = std::min<int64_t>((work + XCDS - 1) / XCDS, std::max(cus / XCDS, 1));
     return dim3((unsigned)(per_xcd * XCDS));
   };
   uint8_t* a8 = base + p.a8;

@@ -160,6 +160,10 @@ __device__ __forceinline__ float segment_max(float v) {
   return v;
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// x * sigmoid(x) with the native exp2 and reciprocal (each ~1 ulp): large negative x gives
+// exp2 -> inf, rcp -> 0, result -0; large positive x gives x; NaN stays NaN.
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 }  // namespace wm
