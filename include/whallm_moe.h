@@ -154,6 +154,15 @@ WM_EXPORT int wm_experts_fp8(const void* x, int32_t tokens, const int32_t* indic
                              const wm_fp8_experts* experts, void* out, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* ---- measurement ----------------------------------------------------------
+ * When enabled, every later wm_moe_mxfp4 / wm_experts_mxfp4 / wm_moe_fp8 / wm_experts_fp8
+ * call that takes the grouped-GEMM path records events on its stream around the gate_up
+ * and the down GEMM; wm_kernel_timing_ms waits for the latest call's events and returns
+ * (gate_up ms, down ms). No counterpart in the reference (a benchmark hook; one set of
+ * events per device, so concurrent calls overwrite each other's). */
+WM_EXPORT int wm_set_kernel_timing(int enable);
+WM_EXPORT int wm_kernel_timing_ms(float* out2);
+
 /* ---- decode stack ---------------------------------------------------------
  * r[t] += y[t] (y nullable), x[t] = bf16(r[t] / sqrt(mean(r[t]^2) + eps)): the
  * pre-norm residual between MoE layers (DecoderLayer.feed_forward, qwen4_exp.py:1127-1149,

@@ -82,6 +82,8 @@ _SIGNATURES = {
     "wm_mtp_workspace_size": (c_size_t, [c_int32, c_int32]),
     "wm_mtp_verify_greedy": (c_int, [_P, _P, c_int32, c_int32, _P, _P, c_size_t, _P]),
     "wm_mtp_verify_rejection": (c_int, [_P, _P, _P, c_int32, c_int32, _P, _P, _P, c_size_t, _P]),
+    "wm_set_kernel_timing": (c_int, [c_int]),
+    "wm_kernel_timing_ms": (c_int, [_P]),
     "wm_moe_decode_persistent_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, c_float,
                                                _P, _P, c_size_t, _P]),
 }

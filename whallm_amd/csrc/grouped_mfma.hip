@@ -36,7 +36,9 @@
 // The shared expert is one more row group after the routed ones (rows P .. P+T-1). Work
 // tiles are mapped XCD-major so the column tiles of one row tile share an L2.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <mutex>
 
 #include "wm_common.h"
 #include "moe_internal.h"
@@ -778,6 +780,25 @@ __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __res
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// Optional event timing of the two grouped GEMMs (off unless wm_set_kernel_timing(1)):
+// events recorded on the call's stream around gate_up and down; one set per device.
+static std::atomic<int> g_timing{0};
+struct TimingEvents {
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+};
+static TimingEvents* timing_events() {
+  static TimingEvents per_device[64];
+  static std::mutex lock;
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) fail("prefill timing: device index out of range");
+  std::lock_guard<std::mutex> g(lock);
+  TimingEvents& t = per_device[dev];
+  for (auto& e : t.ev)
+    if (!e) check_hip(hipEventCreate(&e), "hipEventCreate");
+  return &t;
+}
+
 // Compute units of the current device (queried once per device).
 static int compute_units() {
   static int cached[64] = {0};
@@ -877,13 +898,17 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
   uint8_t* a8 = base + p.a8;
   uint8_t* as8 = base + p.as8;
   uint16_t* out_rows = (uint16_t*)(base + p.rows);
+  TimingEvents* te = g_timing.load() ? timing_events() : nullptr;
+  if (te) check_hip(hipEventRecord(te->ev[0], s), "hipEventRecord");
   hipLaunchKernelGGL((gate_up_kernel<W, Table>), grid_for((I + W::TW / 2 - 1) / (W::TW / 2)), dim3(64 * W::WAVES), 0,
                      s, x8, xs, L, routed, sh, a8, as8);
   check_launch("gate_up");
+  if (te) check_hip(hipEventRecord(te->ev[1], s), "hipEventRecord");
   hipLaunchKernelGGL((down_kernel<W, Table>), grid_for((H + W::TW - 1) / W::TW), dim3(64 * W::WAVES), 0, s, a8, as8, L,
                      weights,
                      combine ? 1 : 0, routed, sh, out_rows);
   check_launch("down");
+  if (te) check_hip(hipEventRecord(te->ev[2], s), "hipEventRecord");
   if (combine)
     hipLaunchKernelGGL(combine_rows_kernel, dim3(tokens, (H / 8 + 255) / 256), dim3(256), 0, s, out_rows, inverse,
                        tokens, k, H, has_shared ? 1 : 0, 1, y);
@@ -916,3 +941,22 @@ void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const fl
 }
 
 }  // namespace wm
+
+extern "C" {
+
+WM_EXPORT int wm_set_kernel_timing(int enable) {
+  wm::mf::g_timing.store(enable ? 1 : 0);
+  return 0;
+}
+
+WM_EXPORT int wm_kernel_timing_ms(float* out2) {
+  return wm::guarded([&] {
+    if (!out2) wm::fail("wm_kernel_timing_ms: null output");
+    wm::mf::TimingEvents* te = wm::mf::timing_events();
+    wm::check_hip(hipEventSynchronize(te->ev[2]), "hipEventSynchronize");
+    wm::check_hip(hipEventElapsedTime(&out2[0], te->ev[0], te->ev[1]), "hipEventElapsedTime");
+    wm::check_hip(hipEventElapsedTime(&out2[1], te->ev[1], te->ev[2]), "hipEventElapsedTime");
+  });
+}
+
+}  // extern "C"
