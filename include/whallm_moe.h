@@ -49,6 +49,8 @@ typedef struct wm_mxfp4_experts {
   int32_t inter;                 /* I: multiple of 32 */
   int32_t up_first;
   float swiglu_limit;            /* 0: plain SwiGLU; > 0: clamped (deepseek_v41/moe.py:30-43) */
+  int32_t tiled;                 /* 0: the reference's row layout; 1: prefill tile layout
+                                    (wm_repack_prefill_mxfp4), grouped-GEMM path only */
 } wm_mxfp4_experts;
 
 /* FP8-E4M3 expert set with fp32 128x128 block scales (mimo/weights.py:17-43):
@@ -136,6 +138,20 @@ WM_EXPORT int wm_moe_mxfp4(const void* x, int32_t tokens, const int32_t* indices
 WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* indices, int32_t k,
                                const wm_mxfp4_experts* experts, void* out, void* workspace,
                                size_t workspace_bytes, void* stream);
+/* Prefill tile layout: writes every expert of src (resolved through src->slots) into the
+ * caller's four device regions, one expert after another with the region sizes of the
+ * row layout (2I*H/2, 2I*H/32, H*I/2, H*I/32 bytes), the same bytes reordered so that the
+ * grouped GEMM reads each 16-row group's 128-wide K step as one contiguous KB and each
+ * step's scale bytes of all rows as one run:
+ *   weights [K/128 steps][rows/16 groups][4 x 16 bytes of the step][16 rows][16 bytes]
+ *   scales  [K/128 steps][rows][4 E8M0 bytes of the step]
+ * (gate_up: rows 2I, K = H; down: rows H, K = I; H and I multiples of 128). Describe the
+ * result with slots = NULL, the region sizes as strides and tiled = 1; such a table always
+ * takes the grouped-GEMM path. The counterpart of the reference's install-time expert blob
+ * repack (Repacker.run / convert, Sources/DeepSeekRepack/Repacker.swift:17-124, :601-715),
+ * for this GPU's loads. */
+WM_EXPORT int wm_repack_prefill_mxfp4(const wm_mxfp4_experts* src, void* gate_up, void* gate_up_scales,
+                                      void* down, void* down_scales, void* stream);
 
 /* ---- FP8-E4M3 expert FFN (fp32 128x128 block scales) ----------------------
  * The DeepSeek-V3 expert format (runtime/deepseek_v4_ssd/mimo/weights.py:17-43):

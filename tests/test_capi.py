@@ -51,3 +51,30 @@ def test_version_and_argument_checks_fail_before_any_launch():
         _lib.call("wm_mtp_verify_rejection", 1, 1, 1, 3, 100, 1, 1, 1, 0, None)
     # The error message is per thread and clears on the next good call.
     assert lib.wm_last_error() != b""
+
+
+def _fake_table(tiled: int, hidden=256, inter=128):
+    """A table with aligned non-null (never dereferenced) addresses: argument checks only."""
+    t = _lib.MXFP4ExpertsC()
+    t.gate_up = t.gate_up_scales = t.down = t.down_scales = 0x10000
+    t.experts, t.hidden, t.inter, t.tiled = 8, hidden, inter, tiled
+    return t
+
+
+def test_prefill_tile_layout_argument_checks():
+    routed, shared = _fake_table(1), _fake_table(0)
+    with pytest.raises(_lib.WhallmError, match="both tiled"):
+        _lib.call("wm_moe_mxfp4", 1, 1, 1, 1, 2, ctypes.byref(routed), ctypes.byref(shared), None, 1, 1, 1 << 40, None)
+    with pytest.raises(_lib.WhallmError, match="multiples of 128"):
+        _lib.call("wm_moe_mxfp4", 1, 1, 1, 1, 2, ctypes.byref(_fake_table(1, hidden=96)), None, None, 1, 1, 1 << 40,
+                  None)
+    with pytest.raises(_lib.WhallmError, match="prefill tile layout"):
+        _lib.call("wm_moe_stack_mxfp4", 1, 1, 1, 2, 1, ctypes.byref(routed), None, None, 1, 1e-6, None, 1, 1 << 40,
+                  None)
+    with pytest.raises(_lib.WhallmError, match="already in the prefill tile layout"):
+        _lib.call("wm_repack_prefill_mxfp4", ctypes.byref(routed), 16, 16, 16, 16, None)
+    # a tiled table always takes the grouped GEMM: its workspace is the prefill one, not the
+    # (smaller) decode buffer of a single-token call
+    lib = _lib.load()
+    assert lib.wm_moe_mxfp4_workspace_size(1, 2, ctypes.byref(routed)) > \
+        lib.wm_moe_mxfp4_workspace_size(1, 2, ctypes.byref(_fake_table(0)))

@@ -153,3 +153,71 @@ def test_edges_empty_k1_and_invalid_ids(device):
     out = wa.experts_mxfp4(layer.x, bad, layer.dev)
     torch.cuda.synchronize()
     assert torch.count_nonzero(out[0, 0]).item() == 0
+
+
+# ----------------------------------------------------------------------------- prefill tile layout
+
+def _tile_layout_np(region: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """The tile layout of one expert's weight region as a numpy reindexing (the layout the
+    header states): bytes [k/128 steps][rows/16 groups][4 pieces][16 rows][16 bytes]."""
+    b = np.ascontiguousarray(region).view(np.uint8).reshape(rows // 16, 16, k // 128, 4, 16)
+    return b.transpose(2, 0, 3, 1, 4).reshape(-1)
+
+
+def _tile_scales_np(region: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """[k/128 steps][rows][4 bytes] from [rows][k/32]."""
+    return np.ascontiguousarray(region).reshape(rows, k // 128, 4).transpose(1, 0, 2).reshape(-1)
+
+
+def test_prefill_layout_bytes(device):
+    E, H, I = 3, 256, 384
+    arrays = S.mxfp4_experts_np(np.random.default_rng(11), E, H, I)
+    dev = S.experts_to_device(arrays, device)
+    tiled = wa.prefill_layout(dev)
+    torch.cuda.synchronize()
+    assert tiled.tiled and tiled.gate_up.shape == dev.gate_up.shape
+    for e in range(E):
+        got = tiled.gate_up[e].cpu().numpy().view(np.uint8).reshape(-1)
+        assert np.array_equal(got, _tile_layout_np(arrays["gate_up"][e], 2 * I, H)), f"gate_up {e}"
+        got = tiled.gate_up_scales[e].cpu().numpy().reshape(-1)
+        assert np.array_equal(got, _tile_scales_np(arrays["gate_up_scales"][e], 2 * I, H)), f"gate_up scales {e}"
+        got = tiled.down[e].cpu().numpy().view(np.uint8).reshape(-1)
+        assert np.array_equal(got, _tile_layout_np(arrays["down"][e], H, I)), f"down {e}"
+        got = tiled.down_scales[e].cpu().numpy().reshape(-1)
+        assert np.array_equal(got, _tile_scales_np(arrays["down_scales"][e], H, I)), f"down scales {e}"
+
+
+@pytest.mark.parametrize("name,tokens,experts,hidden,inter,k", [
+    ("decode-sized", 4, 64, 1024, 512, 4),       # T*K <= 256: a tiled table still takes the GEMM path
+    ("prefill-small", 100, 64, 1024, 512, 4),
+    ("prefill-c3-shape", 512, 512, 2048, 512, 10),
+    ("odd-tiles", 200, 32, 256, 384, 3),           # a partial intermediate tile (384 = 256 + 128)
+])
+def test_prefill_layout_matches_oracle(device, name, tokens, experts, hidden, inter, k):
+    layer = Layer(device, 21, tokens, experts, hidden, inter, k)
+    tiled, tiled_shared = wa.prefill_layout(layer.dev), wa.prefill_layout(layer.dev_shared)
+    y = wa.moe_mxfp4(layer.x, layer.idx_d, layer.w_d, tiled, tiled_shared, layer.gate)
+    torch.cuda.synchronize()
+    assert_close(y.float().cpu().numpy(), layer.oracle_layer(), name)
+    out = wa.experts_mxfp4(layer.x, layer.idx_d, tiled)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), layer.oracle_routed(), name + " router order")
+
+
+def test_prefill_layout_deepseek_form(device):
+    layer = Layer(device, 22, 150, 16, 256, 128, 4, shared=True, up_first=True, limit=10.0)
+    y = wa.moe_mxfp4(layer.x, layer.idx_d, layer.w_d, wa.prefill_layout(layer.dev),
+                     wa.prefill_layout(layer.dev_shared), layer.gate)
+    torch.cuda.synchronize()
+    assert_close(y.float().cpu().numpy(), layer.oracle_layer(), "deepseek tiled")
+
+
+def test_prefill_layout_zipf_agrees_with_row_layout(device):
+    layer = Layer(device, 23, 2048, 512, 2048, 512, 10, skew=True)
+    y_rows = layer.run()
+    y_tiled = wa.moe_mxfp4(layer.x, layer.idx_d, layer.w_d, wa.prefill_layout(layer.dev),
+                           wa.prefill_layout(layer.dev_shared), layer.gate)
+    torch.cuda.synchronize()
+    # the two layouts feed the same bytes to the same MFMAs: identical results
+    assert torch.equal(y_rows, y_tiled)
+    assert_close(y_tiled.float().cpu().numpy(), layer.oracle_layer(), "zipf tiled")

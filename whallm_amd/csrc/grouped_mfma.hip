@@ -55,6 +55,7 @@ constexpr int FMT_FP4 = 4;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 struct Lists {
   const int32_t* order;       // [P] pair of each permuted row
@@ -410,16 +411,17 @@ __device__ __forceinline__ TileRange tile_range(int active) {
 // second-to-last step, and its first loads fly during this tile's epilogue.
 //   setup(j, tile) -> bool: fills tile j's state; false for a tile with no rows
 //   mfma(tile, stage, k): step k of a tile
-//   epilogue(tile): after a tile's last step
-template <typename W, typename Tile, typename Setup, typename Mfma, typename Epilogue>
-__device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps, Stage<W>& s0, Stage<W>& s1,
-                                                 Setup setup, Mfma mfma, Epilogue epilogue) {
+//   epilogue(tile, stage): after a tile's last step (stage: the one just consumed, free
+//     until the next step's loads are issued once every wave has passed its top barrier)
+template <typename Tile, typename S, typename Setup, typename Mfma, typename Epilogue>
+__device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps, S& s0, S& s1, Setup setup, Mfma mfma,
+                                                 Epilogue epilogue) {
   if (tr.count == 0) return;
   Tile cur, nxt;
   bool cur_ok = setup(0, cur), nxt_ok = false;
   if (cur_ok) cur.ld.issue(s0, 0);
   const int total = tr.count * steps;
-  auto body = [&](int g, Stage<W>& stage, Stage<W>& other) {
+  auto body = [&](int g, S& stage, S& other) {
     if (g >= total) return;
     const int j = g / steps, k = g - j * steps;
     ring_wait_all();
@@ -431,7 +433,7 @@ __device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps,
     if (cur_ok) mfma(cur, stage, k);
     if (k == steps - 2 && j + 1 < tr.count) nxt_ok = setup(j + 1, nxt);
     if (k == steps - 1) {
-      if (cur_ok) epilogue(cur);
+      if (cur_ok) epilogue(cur, stage);
       if (steps == 1 && j + 1 < tr.count) {
         nxt_ok = setup(j + 1, nxt);
         if (nxt_ok) nxt.ld.issue(other, 0);
@@ -559,7 +561,7 @@ __global__ void __launch_bounds__(64 * W::WAVES) gate_up_kernel(const uint8_t* _
   // Epilogue: lane holds act columns col0 + 16 mi + 4 g + r (mi 0..3) of row
   // 64 wm + 16 ni + c, col0 = nt * TG + 64 wn: 128-wide act chunk col0 / 128, K offset
   // kin0 = col0 % 128 (0 or 64). E8M0 block (kin0 + 32 half) / 32 holds mi 2 half, 2 half + 1.
-  auto epilogue = [&](const Tile& t) {
+  auto epilogue = [&](const Tile& t, Stage<W>&) {
     if (64 * wn < t.valid) {
       const int c = lane % 16, g = lane / 16;
       const int chunks = I / 128;
@@ -617,7 +619,7 @@ __global__ void __launch_bounds__(64 * W::WAVES) gate_up_kernel(const uint8_t* _
   };
 
   __shared__ Stage<W> s0, s1;
-  persistent_tiles<W, Tile>(tr, H / 128, s0, s1, setup, mfma, epilogue);
+  persistent_tiles<Tile>(tr, H / 128, s0, s1, setup, mfma, epilogue);
 }
 
 // ---------------------------------------------------------------------------------
@@ -690,7 +692,7 @@ __global__ void __launch_bounds__(64 * W::WAVES) down_kernel(const uint8_t* __re
   };
 
   // lane holds output columns nt*TW + 128 wn + 16 mi + 4 g + r of row 64 wm + 16 ni + c
-  auto epilogue = [&](const Tile& t) {
+  auto epilogue = [&](const Tile& t, Stage<W>&) {
     if (128 * wn < t.valid) {
       const int c = lane % 16, g = lane / 16;
 #pragma unroll
@@ -715,7 +717,615 @@ __global__ void __launch_bounds__(64 * W::WAVES) down_kernel(const uint8_t* __re
   };
 
   __shared__ Stage<W> s0, s1;
-  persistent_tiles<W, Tile>(tr, I / 128, s0, s1, setup, mfma, epilogue);
+  persistent_tiles<Tile>(tr, I / 128, s0, s1, setup, mfma, epilogue);
+}
+
+// ---------------------------------------------------------------------------------
+// MXFP4 weights on v_mfma_scale_f32_32x32x64_f8f6f4 with the activations as two E2M3
+// (fp6) terms. This MFMA shape runs fp4 x fp6 at twice the rate of any fp8 operand
+// (measured on MI355X: 33 against 64 cycles per instruction; the 16x16x128 shape runs
+// every format at the fp8 rate).
+//
+// Operand layout (32 x 32 x 64; lane l, r = l % 32, g = l / 32):
+//   fp4 operand: lane holds row r's K values [32g, 32g+32) as nibbles (low first), 16 bytes;
+//   fp6 operand: lane holds row r's K values [32g, 32g+32) as 32 contiguous 6-bit fields
+//                (bit 6f of the lane's 24 bytes is K value 32g + f), 24 bytes;
+//   scale     : lane (r, g) gives the E8M0 scale of row r, K block g;
+//   result    : lane holds D[8 (i / 4) + 4 g + i % 4][r] in its register i (16 registers).
+//
+// Terms: a 32-value block gets hi = e2m3(x / 2^(s - 127)) with s = e(max |x|) - 2, so the
+// block maximum lands in [4, 8); the residual x - hi (exact in fp32) gets its own block
+// exponent the same way, lo = e2m3(residual / 2^(t - 127)). Rounding is to nearest even,
+// saturating at 7.5 (the hardware conversion's behaviour). Per element the pair keeps an
+// absolute error within about 2^-7 of the block maximum's binade.
+//
+// Split rows (x, and act for the down GEMM): per row, per 128-wide K step, 208 bytes: the
+// 4 blocks' terms (hi fields 24 bytes, lo fields 24 bytes, each), then the 4 blocks' hi
+// E8M0 bytes, their lo bytes, and 8 bytes of padding. The GEMMs load whole 256-byte row
+// steps, so a buffer of split rows ends with XSLACK spare bytes.
+
+constexpr int FMT_FP6 = 2;
+constexpr int XSTEP = 208;
+constexpr int XSLACK = 256;
+
+// E8M0 exponent that maps a block maximum into [4, 8) (never below 1, so 2^(127 - s) stays
+// a normal float).
+__device__ __forceinline__ int fp6_exponent(float amax) {
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xff);
+  return e - 2 > 1 ? e - 2 : 1;
+}
+
+// Round |q| to an E2M3 magnitude code (nearest even, saturating at 7.5) and return the code
+// with its sign; `value` gets the signed E2M3 value. Each binade's offset is subtracted
+// exactly (Sterbenz), so the only rounding is the rint.
+__device__ __forceinline__ uint32_t e2m3_encode(float q, float& value) {
+  const float a = fabsf(q);
+  const float t0 = rintf(a * 8.0f);                               // [0, 2): step 1/8
+  const float t1 = 16.0f + rintf((a - 2.0f) * 4.0f);              // [2, 4): step 1/4
+  const float t2 = 24.0f + rintf((fminf(a, 8.0f) - 4.0f) * 2.0f);  // [4, 8): step 1/2
+  const bool b0 = a < 2.0f, b1 = a < 4.0f;
+  const float t = fminf(b0 ? t0 : (b1 ? t1 : t2), 31.0f);
+  // value of code t in the binade the rounding started from (a carry into the next binade
+  // gives the same value: 16 / 8 = (16 - 8) / 4 = 2, (24 - 8) / 4 = (24 - 16) / 2 = 4)
+  const float step = b0 ? 0.125f : (b1 ? 0.25f : 0.5f);
+  const float base = b0 ? 0.0f : (b1 ? 8.0f : 16.0f);
+  const float mag = (t - base) * step;
+  const uint32_t neg = __float_as_uint(q) >> 31;
+  value = neg ? -mag : mag;
+  return (uint32_t)t | (neg << 5);
+}
+
+// Codes of 32 values (v[i], block maximum amax) into 6 words of contiguous 6-bit fields,
+// and the block exponent; `resid` gets v - hi (exact).
+__device__ __forceinline__ void fp6_term32(const float (&v)[32], float amax, uint32_t (&w)[6], int& s,
+                                           float (&resid)[32]) {
+  s = fp6_exponent(amax);
+  const float down = pow2_biased(254 - s), up = pow2_biased(s);
+#pragma unroll
+  for (int k = 0; k < 6; ++k) w[k] = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    float hv;
+    const uint32_t code = e2m3_encode(v[i] * down, hv);
+    resid[i] = v[i] - hv * up;
+    const int bit = 6 * i;
+    w[bit / 32] |= code << (bit % 32);
+    if (bit % 32 > 26) w[bit / 32 + 1] |= code >> (32 - bit % 32);
+  }
+}
+
+// x [rows, H] bf16 -> split rows [rows][H/128][208 bytes]. One lane per 32-value block.
+__global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __restrict__ x, int rows, int hidden,
+                                                          uint8_t* __restrict__ x6) {
+  const int blocks = hidden / 32;
+  const int64_t job = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, block)
+  if (job >= (int64_t)rows * blocks) return;
+  const int64_t row = job / blocks;
+  const int blk = (int)(job % blocks);
+  const uint4* src = reinterpret_cast<const uint4*>(x + row * hidden + blk * 32);
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint4 u = src[q];
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[8 * q + 2 * j] = bf16_bits_to_f32(w[j] & 0xffffu);
+      v[8 * q + 2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  uint32_t hi[6], lo[6];
+  float r[32], r2[32];
+  int s_hi, s_lo;
+  fp6_term32(v, amax, hi, s_hi, r);
+  float rmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) rmax = fmaxf(rmax, fabsf(r[i]));
+  fp6_term32(r, rmax, lo, s_lo, r2);
+  uint8_t* step = x6 + (row * (hidden / 128) + blk / 4) * XSTEP;
+  uint4* dst = reinterpret_cast<uint4*>(step + (blk % 4) * 48);
+  dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  dst[1] = make_uint4(hi[4], hi[5], lo[0], lo[1]);
+  dst[2] = make_uint4(lo[2], lo[3], lo[4], lo[5]);
+  step[192 + blk % 4] = (uint8_t)s_hi;
+  step[196 + blk % 4] = (uint8_t)s_lo;
+}
+
+// ---------------------------------------------------------------------------------
+// Prefill tile layout of MXFP4 weights (one expert region; rows R, K values per row):
+//   weights [K/128 steps][R/16 groups][4 pieces][16 rows][16 bytes]: piece p of a row's step
+//           is its bytes [16p, 16p + 16) of the 64 the step takes in the row layout;
+//   scales  [K/128 steps][R rows][4 bytes]: the row's 4 E8M0 bytes of the step.
+// One 16-byte piece (or one 4-byte scale word) per thread.
+__global__ void __launch_bounds__(256) repack_prefill_kernel(const uint8_t* __restrict__ src,
+                                                             const uint8_t* __restrict__ src_s, int64_t stride,
+                                                             int64_t stride_s, const int32_t* __restrict__ slots,
+                                                             int experts, int rows, int k, uint8_t* __restrict__ dst,
+                                                             uint8_t* __restrict__ dst_s) {
+  const int64_t pieces = (int64_t)rows * (k / 32);  // 16-byte pieces per expert
+  const int64_t words = (int64_t)rows * (k / 128);  // scale words per expert
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)experts * (pieces + words)) return;
+  const int e = (int)(i / (pieces + words));
+  const int64_t j = i - (int64_t)e * (pieces + words);
+  int64_t slot = slots ? slots[e] : e;
+  if (slot < 0) slot = 0;
+  if (j < pieces) {
+    const int64_t row = j / (k / 32);
+    const int pr = (int)(j % (k / 32)), step = pr / 4, p = pr % 4;
+    const uint4 v = *reinterpret_cast<const uint4*>(src + slot * stride + row * (k / 2) + 16 * pr);
+    *reinterpret_cast<uint4*>(dst + (int64_t)e * rows * (k / 2) + (int64_t)step * rows * 64 + (row / 16) * 1024 +
+                              p * 256 + (row % 16) * 16) = v;
+  } else {
+    const int64_t w = j - pieces;
+    const int64_t row = w / (k / 128);
+    const int step = (int)(w % (k / 128));
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(src_s + slot * stride_s + row * (k / 32) + 4 * step);
+    *reinterpret_cast<uint32_t*>(dst_s + (int64_t)e * rows * (k / 32) + (int64_t)step * rows * 4 + row * 4) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Grouped GEMMs for MXFP4 weights. A workgroup computes a 128-row x 512-weight-row tile
+// with 8 waves: wave w = (wm, wn) = (w & 1, w >> 1) owns 64 rows (2 tiles of 32) and
+// 4 weight tiles of 32 rows. Each 128-wide K step's operands go straight from global memory
+// into LDS (global_load_lds: lane i of a wave writes LDS base + 16 i) in a ring of two
+// stages; step k + 1's loads are issued when step k starts.
+//
+// LDS stage:
+//   split rows: 256 bytes per row, piece p of the row's 208-byte step in slot p ^ (row & 15)
+//     (the 16 rows a ds_read_b128 phase serves fall on distinct banks); one load takes 4
+//     rows (lane: row 4q + lane / 16, slot lane % 16), so each row's step arrives as one run;
+//   weight rows: 16-row groups [4 pieces][16 rows][16 bytes], one load per group: in the
+//     tile layout one contiguous KB, in the row layout 64 contiguous bytes of each row;
+//   weight scales: one dword per row (its 4 E8M0 bytes of the step).
+// A uniform int32 read through the scalar cache (data written by an earlier launch).
+__device__ __forceinline__ int32_t scalar_i32(const int32_t* p, int idx) {
+  typedef const __attribute__((address_space(4))) int32_t* cptr;
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((cptr)(((uint64_t)hi << 32) | lo))[idx];
+}
+
+// Row range and expert of logical row tile m through scalar loads only (a per-lane vector
+// load would make the compiler wait for every load in flight, the ring's included).
+__device__ __forceinline__ bool resolve_tile_s(const Lists& L, int m, int& expert, int& begin, int& end) {
+  const int routed_tiles = scalar_i32(L.tile_count, 0);
+  if (m < routed_tiles) {
+    expert = scalar_i32(L.tiles, 2 * m);
+    begin = scalar_i32(L.tiles, 2 * m + 1);
+    end = min(begin + BM, scalar_i32(L.offsets, expert + 1));
+    return true;
+  }
+  const int j = m - routed_tiles;
+  if (!L.has_shared || j * BM >= L.tokens) return false;
+  expert = -1;
+  begin = L.pairs + j * BM;
+  end = min(begin + BM, L.pairs + L.tokens);
+  return true;
+}
+
+__device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& routed, const wm_mxfp4_experts& shared,
+                                                      int expert) {
+  const wm_mxfp4_experts& t = expert < 0 ? shared : routed;
+  const int e = expert < 0 ? 0 : expert;
+  int64_t slot = t.slots ? scalar_i32(t.slots, e) : e;
+  if (slot < 0) slot = 0;  // an expert that is not resident: never address outside the pool
+  return {(const uint8_t*)t.gate_up + slot * t.gate_up_stride,
+          (const uint8_t*)t.gate_up_scales + slot * t.gate_up_scales_stride,
+          (const uint8_t*)t.down + slot * t.down_stride, (const uint8_t*)t.down_scales + slot * t.down_scales_stride,
+          t.up_first, t.swiglu_limit};
+}
+
+struct TileWeightsRegion {
+  const uint8_t* w;  // weight region of the expert
+  const uint8_t* s;  // its scale region
+};
+
+constexpr int TW4 = 512;
+constexpr int WAVES4 = 8;
+constexpr int MI4 = 4;      // 32-row weight tiles per wave
+constexpr int NI4 = 2;      // 32-row row tiles per wave
+
+struct Stage4 {
+  __attribute__((aligned(16))) uint8_t b[BM * 256];
+  __attribute__((aligned(16))) uint8_t a[TW4 * 64];
+  __attribute__((aligned(16))) uint8_t as[TW4 * 4];
+};
+
+// Per-lane LDS read offsets. Weight tile mi of the wave is rows wave_row0 + mrow(mi) + r
+// (multiples of 32 plus the lane's row); row tile ni is rows 64 wm + 32 ni + r. Half h of
+// the step is K [64h, 64h + 64); the lane's K block in it is 2h + g.
+struct Lane4 {
+  uint32_t a;        // + 64 mrow(mi) + 512 h
+  uint32_t as;       // + 4 mrow(mi)
+  uint32_t b[2][3];  // [h][piece of the lane's 48 bytes] + 8192 ni
+  uint32_t bs;       // the row's scale piece (bytes 192..207 of the step) + 8192 ni
+  uint32_t shift;    // 8 g
+};
+
+__device__ __forceinline__ Lane4 lane4(int wave_row0, int wm) {
+  const int lane = threadIdx.x % 64, r = lane % 32, g = lane / 32;
+  Lane4 o;
+  o.a = (uint32_t)((wave_row0 / 16 + r / 16) * 1024 + 256 * g + 16 * (r % 16));
+  o.as = (uint32_t)(4 * (wave_row0 + r));
+  const int row = 64 * wm + r, z = r & 15;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 3; ++e) o.b[h][e] = (uint32_t)(row * 256 + 16 * ((6 * h + 3 * g + e) ^ z));
+  o.bs = (uint32_t)(row * 256 + 16 * (12 ^ z));
+  o.shift = (uint32_t)(8 * g);
+  return o;
+}
+
+// One 128-wide K step of the wave's sub-tile. Per half: the 4 A fragments, then per row
+// tile its hi B fragment feeds 4 MFMAs and its lo fragment 4 more, so no MFMA waits on the
+// one before it.
+template <typename MRow>
+__device__ __forceinline__ void step4(const Stage4& st, const Lane4& lo, v16f (&acc)[MI4][NI4], MRow mrow) {
+  uint32_t sa[MI4];
+  uint2 sb[NI4];
+#pragma unroll
+  for (int mi = 0; mi < MI4; ++mi) sa[mi] = *reinterpret_cast<const uint32_t*>(st.as + lo.as + 4 * mrow(mi));
+#pragma unroll
+  for (int ni = 0; ni < NI4; ++ni) sb[ni] = *reinterpret_cast<const uint2*>(st.b + lo.bs + 8192 * ni);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t sh = lo.shift + 16u * (uint32_t)h;
+    v8i a[MI4];
+#pragma unroll
+    for (int mi = 0; mi < MI4; ++mi) {
+      const uint4 v = *reinterpret_cast<const uint4*>(st.a + lo.a + 64 * mrow(mi) + 512 * h);
+      a[mi] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int ni = 0; ni < NI4; ++ni) {
+      const uint4 b0 = *reinterpret_cast<const uint4*>(st.b + lo.b[h][0] + 8192 * ni);
+      const uint4 b1 = *reinterpret_cast<const uint4*>(st.b + lo.b[h][1] + 8192 * ni);
+      const uint4 b2 = *reinterpret_cast<const uint4*>(st.b + lo.b[h][2] + 8192 * ni);
+      const v8i bh = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, 0, 0};
+      const v8i bl = {(int)b1.z, (int)b1.w, (int)b2.x, (int)b2.y, (int)b2.z, (int)b2.w, 0, 0};
+      const int sbh = (int)(sb[ni].x >> sh), sbl = (int)(sb[ni].y >> sh);
+#pragma unroll
+      for (int mi = 0; mi < MI4; ++mi)
+        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
+                                                                      (int)(sa[mi] >> sh), 0, sbh);
+#pragma unroll
+      for (int mi = 0; mi < MI4; ++mi)
+        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
+                                                                      (int)(sa[mi] >> sh), 0, sbl);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// Per-lane sources of one K step's loads (9 per wave): split rows, loads q = w + 8i
+// (i = 0..3), rows 4q + lane / 16; weight groups q = w + 8i; weight scales rows 64 w + lane.
+// Offsets are taken at step 0; step ks adds ks * XSTEP, ks * a_step and ks * s_step.
+struct Loader4 {
+  const uint8_t* b;
+  const uint8_t* wbase;
+  const uint8_t* sbase;
+  uint32_t boff[4];
+  uint32_t aoff[4];
+  uint32_t soff;
+  uint32_t a_step, s_step;
+
+  __device__ __forceinline__ void issue(Stage4& st, int ks) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(st.b + (w + WAVES4 * i) * 1024));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(st.a + (w + WAVES4 * i) * 1024));
+    dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(st.as + 256 * w));
+  }
+};
+
+// The split-row part of a loader: row_off(r) is the byte offset of tile row r's split row.
+template <typename RowOff>
+__device__ __forceinline__ void split_row_offsets(Loader4& ld, RowOff row_off) {
+  const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * (w + WAVES4 * i) + lane / 16;
+    ld.boff[i] = row_off(i, r) + 16u * (uint32_t)((lane % 16) ^ (r & 15));
+  }
+}
+
+// The weight part: tile rows [0, TW4) are expert rows row_of(j) (multiples of 16 in runs of
+// 16, so a tile group is an expert group); rows is the expert region's row count, k its K.
+template <typename RowOf>
+__device__ __forceinline__ void weight_offsets(Loader4& ld, const TileWeightsRegion& tr_, int rows, int k, int tiled,
+                                               RowOf row_of) {
+  const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  ld.wbase = uniform_u8(tr_.w);
+  ld.sbase = uniform_u8(tr_.s);
+  if (tiled) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + WAVES4 * i)) / 16 * 1024 + 16 * lane);
+    ld.soff = (uint32_t)(row_of(64 * w + lane) * 4);
+    ld.a_step = (uint32_t)(rows * 64);
+    ld.s_step = (uint32_t)(rows * 4);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ld.aoff[i] = (uint32_t)(row_of(16 * (w + WAVES4 * i) + lane % 16) * (k / 2) + 16 * (lane / 16));
+    ld.soff = (uint32_t)(row_of(64 * w + lane) * (k / 32));
+    ld.a_step = 64;
+    ld.s_step = 4;
+  }
+}
+
+struct Tile4 {
+  Loader4 ld;
+  int begin, end, nt, valid;
+  float limit;
+};
+
+__device__ __forceinline__ void zero_acc4(v16f (&acc)[MI4][NI4]) {
+#pragma unroll
+  for (int mi = 0; mi < MI4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI4; ++ni)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.0f;
+}
+
+// Every wave's LDS reads of the stage have returned (the epilogue may overwrite it).
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// This wave's LDS writes are done before its next LDS reads (and its reads before its writes).
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// 16 codes of a lane (its rows 8j + 4 half + 0..3 of a block, j = 0..3) as four 24-bit groups.
+__device__ __forceinline__ void fp6_groups16(const float (&v)[16], float scale_down, uint32_t (&grp)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t gword = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float unused;
+      gword |= e2m3_encode(v[4 * j + q] * scale_down, unused) << (6 * q);
+    }
+    grp[j] = gword;
+  }
+}
+
+// gate_up: act rows of a tile's 256 intermediate columns; weight tile rows [0, 256) are the
+// gate rows nt * 256 + j, [256, 512) the matching up rows; wave wn owns gate rows
+// 64 wn + [0, 64) (mi 0, 1) and the same up rows (mi 2, 3).
+template <typename Table>
+__global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __restrict__ x6,
+                                                               const int32_t* __restrict__ row_token, Lists L,
+                                                               Table routed, Table shared, uint8_t* __restrict__ a6) {
+  constexpr int TG = TW4 / 2;
+  const int H = routed.hidden, I = routed.inter;
+  const int n_tiles = (I + TG - 1) / TG;
+  const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int wm = wave & 1, wn = wave >> 1;
+  const Lane4 lo = lane4(64 * wn, wm);
+  const uint32_t x_row = (uint32_t)(H / 128 * XSTEP);
+  const int64_t a_row = (int64_t)(I / 128) * XSTEP;
+
+  auto setup = [&](int j, Tile4& t) {
+    const int logical = tr.first + tr.stride * j;
+    const int mt = logical / n_tiles;
+    t.nt = logical - mt * n_tiles;
+    int expert = 0, begin = 0, end = 0;
+    if (!resolve_tile_s(L, mt, expert, begin, end)) return false;
+    t.begin = begin;
+    t.end = end;
+    const TileWeights tw = tile_weights_s(routed, shared, expert);
+    const Table& tab = expert < 0 ? shared : routed;
+    t.limit = tw.limit;
+    t.valid = min(TG, I - t.nt * TG);  // a multiple of 128
+    const int gate0 = (tw.up_first ? I : 0) + t.nt * TG;
+    const int up0 = (tw.up_first ? 0 : I) + t.nt * TG;
+    const int valid = t.valid;
+    weight_offsets(t.ld, TileWeightsRegion{tw.w13, tw.w13s}, 2 * I, H, tab.tiled, [gate0, up0, valid](int r) {
+      const int rr = r % TG;
+      return (r < TG ? gate0 : up0) + (rr < valid ? rr : rr % valid);
+    });
+    t.ld.b = uniform_u8(x6);
+    // tokens of this lane's split rows 4q + 0..3 (q = w + 8i), through scalar loads
+    split_row_offsets(t.ld, [&](int i, int r) {
+      const int q0 = 4 * (__builtin_amdgcn_readfirstlane(threadIdx.x / 64) + WAVES4 * i);
+      int tok = 0;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int pr = begin + q0 + d < end ? begin + q0 + d : begin;
+        const int td = scalar_i32(row_token, pr);
+        tok = r == q0 + d ? td : tok;
+      }
+      return (uint32_t)tok * x_row;
+    });
+    return true;
+  };
+
+  v16f acc[MI4][NI4];
+  zero_acc4(acc);
+  auto mrow = [](int mi) { return (mi < 2 ? 0 : TG) + 32 * (mi & 1); };
+  auto mfma = [&](const Tile4&, const Stage4& st, int) { step4(st, lo, acc, mrow); };
+
+  // Epilogue: lane (r, half) holds act rows 8 j + 4 half + q (j, q = 0..3; register 4 j + q)
+  // of 32-column block kb = 2 wn + b of the tile (b = 0, 1: gate mi b, up mi b + 2) for row
+  // 64 wm + 32 ni + r. The two lanes of a block exchange 24-bit field groups so that lane
+  // half 0 writes the block's hi fields and half 1 its lo fields, into the consumed stage as
+  // the tile's act rows (416 bytes: 2 steps), which all threads then copy out row by row.
+  auto epilogue = [&](const Tile4& t, Stage4& st) {
+    stage_barrier();
+    uint8_t* stg = reinterpret_cast<uint8_t*>(&st);
+    if (64 * wn < t.valid) {
+      const int r = lane % 32, half = lane / 32;
+#pragma unroll
+      for (int ni = 0; ni < NI4; ++ni) {
+        const int lr = 64 * wm + 32 * ni + r;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          float v[16];
+          float amax = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            float gv = acc[b][ni][i], uv = acc[b + 2][ni][i];
+            if (t.limit > 0.0f) {
+              gv = fminf(gv, t.limit);
+              uv = fminf(fmaxf(uv, -t.limit), t.limit);
+            }
+            v[i] = silu(gv) * uv;
+            amax = fmaxf(amax, fabsf(v[i]));
+          }
+          amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+          const int s_hi = fp6_exponent(amax);
+          const float down_hi = pow2_biased(254 - s_hi), up_hi = pow2_biased(s_hi);
+          float res[16];
+          float rmax = 0.0f;
+          uint32_t ghi[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            uint32_t gword = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float hv;
+              gword |= e2m3_encode(v[4 * j + q] * down_hi, hv) << (6 * q);
+              res[4 * j + q] = v[4 * j + q] - hv * up_hi;
+              rmax = fmaxf(rmax, fabsf(res[4 * j + q]));
+            }
+            ghi[j] = gword;
+          }
+          rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+          const int s_lo = fp6_exponent(rmax);
+          uint32_t glo[4];
+          fp6_groups16(res, pow2_biased(254 - s_lo), glo);
+          uint32_t g0[4], g1[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t recv = __shfl_xor(half ? ghi[j] : glo[j], 32, 64);
+            g0[j] = half ? recv : ghi[j];   // rows 8 j + 0..3 of the term this lane writes
+            g1[j] = half ? glo[j] : recv;   // rows 8 j + 4..7
+          }
+          // group pair j = 48 bits at bit 48 j of the 24-byte term
+          uint32_t d[6];
+          d[0] = g0[0] | (g1[0] << 24);
+          d[1] = (g1[0] >> 8) | (g0[1] << 16);
+          d[2] = (g0[1] >> 16) | (g1[1] << 8);
+          d[3] = g0[2] | (g1[2] << 24);
+          d[4] = (g1[2] >> 8) | (g0[3] << 16);
+          d[5] = (g0[3] >> 16) | (g1[3] << 8);
+          const int kb = 2 * wn + b;  // block of the tile: step kb / 4, block kb % 4 of the step
+          uint8_t* step = stg + lr * 416 + (kb / 4) * XSTEP;
+          uint2* dst = reinterpret_cast<uint2*>(step + (kb % 4) * 48 + half * 24);
+          dst[0] = make_uint2(d[0], d[1]);
+          dst[1] = make_uint2(d[2], d[3]);
+          dst[2] = make_uint2(d[4], d[5]);
+          step[192 + 4 * half + kb % 4] = (uint8_t)(half ? s_lo : s_hi);
+        }
+      }
+    }
+    stage_barrier();
+    const int chunks = t.valid / 128 * (XSTEP / 16);  // 16-byte pieces of a row's act steps
+    const int n = (t.end - t.begin) * chunks;
+    for (int idx = threadIdx.x; idx < n; idx += 64 * WAVES4) {
+      const int lr = idx / chunks, c = idx - lr * chunks;
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + lr * 416 + 16 * c);
+      *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(2 * t.nt) * XSTEP + 16 * c) = v;
+    }
+    zero_acc4(acc);
+  };
+
+  __shared__ Stage4 s0, s1;
+  persistent_tiles<Tile4>(tr, H / 128, s0, s1, setup, mfma, epilogue);
+}
+
+// down: out[row, n] = act[row] . W2[n], bf16, permuted rows (the combine applies the routing
+// weights); tile = 128 rows x 512 output columns, wave wn owns columns 128 wn + [0, 128).
+template <typename Table>
+__global__ void __launch_bounds__(64 * WAVES4) down4_kernel(const uint8_t* __restrict__ a6, Lists L, Table routed,
+                                                            Table shared, uint16_t* __restrict__ out) {
+  const int H = routed.hidden, I = routed.inter;
+  const int n_tiles = (H + TW4 - 1) / TW4;
+  const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int wm = wave & 1, wn = wave >> 1;
+  const Lane4 lo = lane4(128 * wn, wm);
+  const uint32_t a_row = (uint32_t)(I / 128 * XSTEP);
+
+  auto setup = [&](int j, Tile4& t) {
+    const int logical = tr.first + tr.stride * j;
+    const int mt = logical / n_tiles;
+    t.nt = logical - mt * n_tiles;
+    int expert = 0, begin = 0, end = 0;
+    if (!resolve_tile_s(L, mt, expert, begin, end)) return false;
+    t.begin = begin;
+    t.end = end;
+    const TileWeights tw = tile_weights_s(routed, shared, expert);
+    const Table& tab = expert < 0 ? shared : routed;
+    t.valid = min(TW4, H - t.nt * TW4);  // a multiple of 128
+    const int nt = t.nt, valid = t.valid;
+    weight_offsets(t.ld, TileWeightsRegion{tw.w2, tw.w2s}, H, I, tab.tiled,
+                   [nt, valid](int r) { return nt * TW4 + (r < valid ? r : r % valid); });  // never past H
+    t.ld.b = uniform_u8(a6);
+    split_row_offsets(t.ld, [&](int, int r) { return (uint32_t)(begin + r < end ? begin + r : begin) * a_row; });
+    return true;
+  };
+
+  v16f acc[MI4][NI4];
+  zero_acc4(acc);
+  auto mfma = [&](const Tile4&, const Stage4& st, int) { step4(st, lo, acc, [](int mi) { return 32 * mi; }); };
+
+  // Epilogue: lane (r, half) holds output columns nt * 512 + 128 wn + 32 mi + 8 j + 4 half + q
+  // (register 4 j + q) of row 64 wm + 32 ni + r. Each wave turns 32 rows x 64 columns at a
+  // time around in its own slice of the consumed stage (rows of 144 bytes) and stores each
+  // row's 128 bytes as 8 lanes x 16.
+  auto epilogue = [&](const Tile4& t, Stage4& st) {
+    stage_barrier();
+    if (128 * wn < t.valid) {
+      uint8_t* slice = reinterpret_cast<uint8_t*>(&st) + wave * 4608;
+      const int r = lane % 32, half = lane / 32;
+#pragma unroll
+      for (int ni = 0; ni < NI4; ++ni)
+#pragma unroll
+        for (int mp = 0; mp < 2; ++mp) {
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const v16f& a = acc[2 * mp + m][ni];
+              uint2 o;
+              o.x = f32_to_bf16_bits(a[4 * j]) | ((uint32_t)f32_to_bf16_bits(a[4 * j + 1]) << 16);
+              o.y = f32_to_bf16_bits(a[4 * j + 2]) | ((uint32_t)f32_to_bf16_bits(a[4 * j + 3]) << 16);
+              *reinterpret_cast<uint2*>(slice + r * 144 + 64 * m + 16 * j + 8 * half) = o;
+            }
+          wave_lds_fence();
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            const int rr = lane / 8 + 8 * it, c = lane % 8;
+            const uint4 v = *reinterpret_cast<const uint4*>(slice + rr * 144 + 16 * c);
+            const int row = t.begin + 64 * wm + 32 * ni + rr;
+            if (row < t.end)
+              *reinterpret_cast<uint4*>(out + (int64_t)row * H + t.nt * TW4 + 128 * wn + 64 * mp + 8 * c) = v;
+          }
+          wave_lds_fence();
+        }
+    }
+    zero_acc4(acc);
+  };
+
+  __shared__ Stage4 s0, s1;
+  persistent_tiles<Tile4>(tr, I / 128, s0, s1, setup, mfma, epilogue);
+}
+
+// Token of every permuted row: order[p] / K for routed rows, p - P for the shared rows.
+__global__ void __launch_bounds__(256) row_tokens_kernel(const int32_t* __restrict__ order, int pairs, int k,
+                                                         int rows, int32_t* __restrict__ row_token) {
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p < rows) row_token[p] = p < pairs ? order[p] / k : p - pairs;
 }
 
 // ---------------------------------------------------------------------------------
@@ -736,10 +1346,13 @@ __global__ void __launch_bounds__(64) shared_gate_kernel(const uint16_t* __restr
   if (lane == 0) gate[t] = v;
 }
 
-// combine: y[t, c] = sum_k rows[inverse[t*K + k], c] (+ rows[P + t, c]), fp32 sum, bf16 out.
+// combine: y[t, c] = sum_k w[t, k] rows[inverse[t*K + k], c] (+ gate[t] rows[P + t, c]), fp32
+// sum in k order, bf16 out (the expert rows are unweighted).
 // per-pair (combine = 0): out[p, c] = rows[inverse[p], c]. 8 columns per thread.
 __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __restrict__ rows,
-                                                           const int32_t* __restrict__ inverse, int tokens, int k,
+                                                           const int32_t* __restrict__ inverse,
+                                                           const float* __restrict__ weights,
+                                                           const float* __restrict__ gate, int tokens, int k,
                                                            int hidden, int has_shared, int combine,
                                                            uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
@@ -753,20 +1366,29 @@ __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __res
     return;
   }
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  auto add = [&](int row) {
-    const uint4 v = reinterpret_cast<const uint4*>(rows + (int64_t)row * hidden)[c8];
+  auto add = [&](const uint4 v, float s) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      acc[2 * q] += bf16_bits_to_f32(w[q] & 0xffffu);
-      acc[2 * q + 1] += bf16_bits_to_f32(w[q] >> 16);
+      acc[2 * q] = fmaf(s, bf16_bits_to_f32(w[q] & 0xffffu), acc[2 * q]);
+      acc[2 * q + 1] = fmaf(s, bf16_bits_to_f32(w[q] >> 16), acc[2 * q + 1]);
     }
   };
-  for (int j = 0; j < k; ++j) {
-    const int row = inverse[t * k + j];
-    if (row >= 0) add(row);
+  // the rows of up to 8 pairs are loaded before any is summed (sums stay in k order)
+  constexpr int BATCH = 8;
+  for (int j0 = 0; j0 < k; j0 += BATCH) {
+    int row[BATCH];
+    uint4 v[BATCH];
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) row[q] = j0 + q < k ? inverse[t * k + j0 + q] : -1;
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q)
+      if (row[q] >= 0) v[q] = reinterpret_cast<const uint4*>(rows + (int64_t)row[q] * hidden)[c8];
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q)
+      if (row[q] >= 0) add(v[q], weights[t * k + j0 + q]);
   }
-  if (has_shared) add(pairs + t);
+  if (has_shared) add(reinterpret_cast<const uint4*>(rows + (int64_t)(pairs + t) * hidden)[c8], gate[t]);
   uint4 o;
   o.x = f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16);
   o.y = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
@@ -814,10 +1436,12 @@ static int compute_units() {
 }
 
 struct Layout {
-  size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, x8, xs, a8, as8, rows, total;
+  size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, row_token, x8, xs, a8, as8, rows, total;
 };
 
-static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool has_shared) {
+// rowb: bytes of one row's 128-wide K step in the split format (E4M3 terms 256 with separate
+// scales, E2M3 terms XSTEP with the scales inside); split buffers end with XSLACK spare bytes.
+static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool has_shared, int rowb) {
   const int64_t pairs = (int64_t)tokens * k;
   const int64_t rows = pairs + (has_shared ? tokens : 0);
   const int64_t max_tiles = (pairs + BM - 1) / BM + experts;
@@ -830,9 +1454,10 @@ static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool
   p.tiles = at;      at += align256(sizeof(int32_t) * 2 * (size_t)max_tiles);
   p.tile_count = at; at += align256(sizeof(int32_t));
   p.gate = at;       at += align256(sizeof(float) * (size_t)(tokens > 0 ? tokens : 1));
-  p.x8 = at;         at += align256((size_t)tokens * (hidden / 128) * CHUNK);
+  p.row_token = at;  at += align256(sizeof(int32_t) * (size_t)(rows > 0 ? rows : 1));
+  p.x8 = at;         at += align256((size_t)tokens * (hidden / 128) * rowb + XSLACK);
   p.xs = at;         at += align256((size_t)tokens * (hidden / 128) * 8);
-  p.a8 = at;         at += align256((size_t)rows * (inter / 128) * CHUNK);
+  p.a8 = at;         at += align256((size_t)rows * (inter / 128) * rowb + XSLACK);
   p.as8 = at;        at += align256((size_t)rows * (inter / 128) * 8);
   p.rows = at;       at += align256(sizeof(uint16_t) * (size_t)rows * hidden);
   p.total = at;
@@ -846,7 +1471,9 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
   const int H = routed.hidden, I = routed.inter;
   if (H % 128 || I % 128) fail("prefill: hidden and intermediate must be multiples of 128");
   const bool has_shared = combine && shared != nullptr;
-  const Layout p = layout(tokens, k, routed.experts, H, I, has_shared);
+  constexpr bool fp6_terms = W::FMT == FMT_FP4;  // MXFP4 weights take E2M3 activation terms
+  constexpr int rowb = fp6_terms ? XSTEP : CHUNK;
+  const Layout p = layout(tokens, k, routed.experts, H, I, has_shared, rowb);
   if (ws_bytes < p.total) fail("prefill: workspace too small");
   const int64_t pairs = (int64_t)tokens * k;
   const int64_t rows = pairs + (has_shared ? tokens : 0);
@@ -857,7 +1484,7 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
                 !dword_rows(t->down_scales, t->down_scales_stride)))
         fail("prefill: MXFP4 scale regions and strides must be 4-byte aligned");
   }
-  if ((int64_t)rows * (I / 128) * CHUNK >= ((int64_t)1 << 32) || (int64_t)tokens * (H / 128) * CHUNK >= ((int64_t)1 << 32))
+  if ((int64_t)rows * (I / 128) * rowb >= ((int64_t)1 << 32) || (int64_t)tokens * (H / 128) * rowb >= ((int64_t)1 << 32))
     fail("prefill: split operands of 4 GiB or more (split the call into smaller token batches)");
   uint8_t* base = (uint8_t*)ws;
   Lists L;
@@ -882,8 +1509,21 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
   }
   uint8_t* x8 = base + p.x8;
   uint8_t* xs = base + p.xs;
-  const int64_t split_jobs = (int64_t)tokens * (H / 128);
-  hipLaunchKernelGGL(split_rows_kernel, dim3((unsigned)((split_jobs + 3) / 4)), dim3(256), 0, s, x, tokens, H, x8, xs);
+  int32_t* row_token = (int32_t*)(base + p.row_token);
+  if constexpr (fp6_terms) {
+    if (rows > 0) {
+      hipLaunchKernelGGL(row_tokens_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, L.order, (int)pairs,
+                         k, (int)rows, row_token);
+      check_launch("row_tokens");
+    }
+    const int64_t split_jobs = (int64_t)tokens * (H / 32);
+    hipLaunchKernelGGL(split6_rows_kernel, dim3((unsigned)((split_jobs + 255) / 256)), dim3(256), 0, s, x, tokens, H,
+                       x8);
+  } else {
+    const int64_t split_jobs = (int64_t)tokens * (H / 128);
+    hipLaunchKernelGGL(split_rows_kernel, dim3((unsigned)((split_jobs + 3) / 4)), dim3(256), 0, s, x, tokens, H, x8,
+                       xs);
+  }
   check_launch("split_rows");
   const Table sh = shared ? *shared : routed;
   const int64_t max_row_tiles = (pairs + BM - 1) / BM + routed.experts + (has_shared ? (tokens + BM - 1) / BM : 0);
@@ -900,28 +1540,35 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
   uint16_t* out_rows = (uint16_t*)(base + p.rows);
   TimingEvents* te = g_timing.load() ? timing_events() : nullptr;
   if (te) check_hip(hipEventRecord(te->ev[0], s), "hipEventRecord");
-  hipLaunchKernelGGL((gate_up_kernel<W, Table>), grid_for((I + W::TW / 2 - 1) / (W::TW / 2)), dim3(64 * W::WAVES), 0,
-                     s, x8, xs, L, routed, sh, a8, as8);
+  if constexpr (fp6_terms)
+    hipLaunchKernelGGL((gate_up4_kernel<Table>), grid_for((I + TW4 / 2 - 1) / (TW4 / 2)), dim3(64 * WAVES4), 0, s, x8,
+                       row_token, L, routed, sh, a8);
+  else
+    hipLaunchKernelGGL((gate_up_kernel<W, Table>), grid_for((I + W::TW / 2 - 1) / (W::TW / 2)), dim3(64 * W::WAVES),
+                       0, s, x8, xs, L, routed, sh, a8, as8);
   check_launch("gate_up");
   if (te) check_hip(hipEventRecord(te->ev[1], s), "hipEventRecord");
-  hipLaunchKernelGGL((down_kernel<W, Table>), grid_for((H + W::TW - 1) / W::TW), dim3(64 * W::WAVES), 0, s, a8, as8, L,
-                     weights,
-                     combine ? 1 : 0, routed, sh, out_rows);
+  if constexpr (fp6_terms)
+    hipLaunchKernelGGL((down4_kernel<Table>), grid_for((H + TW4 - 1) / TW4), dim3(64 * WAVES4), 0, s, a8, L, routed,
+                       sh, out_rows);
+  else  // unweighted rows: the combine applies the routing weights and the shared gate
+    hipLaunchKernelGGL((down_kernel<W, Table>), grid_for((H + W::TW - 1) / W::TW), dim3(64 * W::WAVES), 0, s, a8, as8,
+                       L, weights, 0, routed, sh, out_rows);
   check_launch("down");
   if (te) check_hip(hipEventRecord(te->ev[2], s), "hipEventRecord");
   if (combine)
     hipLaunchKernelGGL(combine_rows_kernel, dim3(tokens, (H / 8 + 255) / 256), dim3(256), 0, s, out_rows, inverse,
-                       tokens, k, H, has_shared ? 1 : 0, 1, y);
+                       weights, L.shared_gate, tokens, k, H, has_shared ? 1 : 0, 1, y);
   else
     hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)pairs, (H / 8 + 255) / 256), dim3(256), 0, s, out_rows,
-                       inverse, tokens, k, H, 0, 0, y);
+                       inverse, weights, L.shared_gate, tokens, k, H, 0, 0, y);
   check_launch("combine_rows");
 }
 
 }  // namespace mf
 
 size_t prefill_workspace_size(int tokens, int k, const wm_mxfp4_experts& e, bool has_shared) {
-  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared).total;
+  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared, mf::XSTEP).total;
 }
 
 void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
@@ -931,7 +1578,7 @@ void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const 
 }
 
 size_t prefill_fp8_workspace_size(int tokens, int k, const wm_fp8_experts& e, bool has_shared) {
-  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared).total;
+  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared, mf::CHUNK).total;
 }
 
 void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
@@ -943,6 +1590,36 @@ void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const fl
 }  // namespace wm
 
 extern "C" {
+
+WM_EXPORT int wm_repack_prefill_mxfp4(const wm_mxfp4_experts* src, void* gate_up, void* gate_up_scales, void* down,
+                                      void* down_scales, void* stream) {
+  return wm::guarded([&] {
+    wm::validate_experts(src, "wm_repack_prefill_mxfp4 source", false);
+    if (src->tiled) wm::fail("wm_repack_prefill_mxfp4: the source is already in the prefill tile layout");
+    if (src->hidden % 128 || src->inter % 128)
+      wm::fail("wm_repack_prefill_mxfp4: hidden and intermediate must be multiples of 128");
+    if (!gate_up || !gate_up_scales || !down || !down_scales) wm::fail("wm_repack_prefill_mxfp4: null destination");
+    auto aligned = [](const void* p, uintptr_t a) { return (uintptr_t)p % a == 0; };
+    if (!aligned(gate_up, 16) || !aligned(down, 16) || !aligned(gate_up_scales, 4) || !aligned(down_scales, 4))
+      wm::fail("wm_repack_prefill_mxfp4: destination weights must be 16-byte and scales 4-byte aligned");
+    if (!aligned(src->gate_up_scales, 4) || !aligned(src->down_scales, 4) || src->gate_up_scales_stride % 4 ||
+        src->down_scales_stride % 4)
+      wm::fail("wm_repack_prefill_mxfp4: source scale regions and strides must be 4-byte aligned");
+    const int E = src->experts, H = src->hidden, I = src->inter;
+    hipStream_t s = wm::as_stream(stream);
+    auto launch = [&](const void* w, const void* ws, int64_t stride, int64_t stride_s, int rows, int k, void* dst,
+                      void* dst_s) {
+      const int64_t n = (int64_t)E * ((int64_t)rows * (k / 32) + (int64_t)rows * (k / 128));
+      hipLaunchKernelGGL(wm::mf::repack_prefill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                         (const uint8_t*)w, (const uint8_t*)ws, stride, stride_s, src->slots, E, rows, k,
+                         (uint8_t*)dst, (uint8_t*)dst_s);
+      wm::check_launch("repack_prefill");
+    };
+    launch(src->gate_up, src->gate_up_scales, src->gate_up_stride, src->gate_up_scales_stride, 2 * I, H, gate_up,
+           gate_up_scales);
+    launch(src->down, src->down_scales, src->down_stride, src->down_scales_stride, H, I, down, down_scales);
+  });
+}
 
 WM_EXPORT int wm_set_kernel_timing(int enable) {
   wm::mf::g_timing.store(enable ? 1 : 0);

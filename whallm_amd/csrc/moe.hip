@@ -25,15 +25,21 @@ void validate_experts(const wm_mxfp4_experts* e, const char* what, bool shared) 
 
 static void validate_pair(const wm_mxfp4_experts* routed, const wm_mxfp4_experts* shared) {
   validate_experts(routed, "routed experts", false);
+  if (routed->tiled && (routed->hidden % 128 || routed->inter % 128))
+    fail("routed experts: the prefill tile layout needs hidden and intermediate multiples of 128");
   if (shared) {
     validate_experts(shared, "shared expert", true);
     if (shared->hidden != routed->hidden) fail("shared expert: hidden differs from the routed experts");
     if (shared->inter != routed->inter)
       fail("shared expert: intermediate must equal the routed experts' (one act buffer layout)");
+    if ((shared->tiled != 0) != (routed->tiled != 0))
+      fail("shared expert: the routed and shared tables must both be in the row layout or both tiled");
   }
 }
 
 static bool use_decode(int tokens, int k) { return (int64_t)tokens * k <= DECODE_MAX_PAIRS; }
+// Tables in the prefill tile layout always take the grouped GEMM.
+static bool use_decode(int tokens, int k, const wm_mxfp4_experts& e) { return !e.tiled && use_decode(tokens, k); }
 
 static void validate_fp8(const wm_fp8_experts* e, const char* what, bool shared) {
   std::string w(what);
@@ -79,7 +85,7 @@ extern "C" {
 
 WM_EXPORT size_t wm_moe_mxfp4_workspace_size(int32_t tokens, int32_t k, const wm_mxfp4_experts* experts) {
   if (!experts || tokens < 0 || k < 1) return 0;
-  if (use_decode(tokens, k)) return decode_workspace(tokens, k, *experts) + 256;
+  if (use_decode(tokens, k, *experts)) return decode_workspace(tokens, k, *experts) + 256;
   return prefill_workspace_size(tokens, k, *experts, true) + 256;
 }
 
@@ -95,7 +101,7 @@ WM_EXPORT int wm_moe_mxfp4(const void* x, int32_t tokens, const int32_t* indices
     if (workspace_bytes < wm_moe_mxfp4_workspace_size(tokens, k, experts) - 256 || !workspace)
       fail("wm_moe_mxfp4: workspace too small");
     hipStream_t s = as_stream(stream);
-    if (use_decode(tokens, k))
+    if (use_decode(tokens, k, *experts))
       decode_mxfp4((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
                     (uint16_t*)y, true, (float*)workspace, s);
     else
@@ -116,7 +122,7 @@ WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* ind
     if (workspace_bytes < wm_moe_mxfp4_workspace_size(tokens, k, experts) - 256 || !workspace)
       fail("wm_experts_mxfp4: workspace too small");
     hipStream_t s = as_stream(stream);
-    if (use_decode(tokens, k))
+    if (use_decode(tokens, k, *experts))
       decode_mxfp4((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out, false,
                    (float*)workspace, s);
     else

@@ -4,7 +4,7 @@
 // qwen4_exp.py:865-868).
 //
 //   count   : one wave per chunk of 1024 pairs counts its experts in LDS
-//   scan    : one workgroup turns the per-chunk counts into per-chunk bases,
+//   scan    : one workgroup turns the per-chunk counts into per-chunk prefixes,
 //             per-expert offsets, and the (expert, first row) tile list
 //   scatter : one wave per chunk walks its pairs in order, 64 at a time; lanes
 //             with the same expert find each other with ballots, so every pair's
@@ -34,70 +34,116 @@ __global__ void __launch_bounds__(64) permute_count_kernel(const int32_t* __rest
   for (int e = lane; e < experts; e += 64) chunk_counts[chunk * experts + e] = counts[e];
 }
 
-// One workgroup of 1024 threads. chunk_counts[c][e] becomes the first row of
-// chunk c's pairs of expert e.
+// Inclusive prefix sum over the 1024 threads of the block (wave shuffles, then the 16
+// wave totals). Every thread of the block must call it.
+__device__ __forceinline__ int32_t block_inclusive_scan(int32_t v, int32_t* wave_total) {
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  if (lane == 63) wave_total[wave] = v;
+  __syncthreads();
+  int32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += wave_total[w];
+  __syncthreads();  // wave_total is reused by the next call
+  return v + before;
+}
+
+// One workgroup of 1024 threads. Thread t = s * pad + e (pad = E rounded up to a power of
+// two) owns chunk segment s of expert e, so each expert's chunk counts are read by
+// 1024 / pad threads, 16 independent loads at a time. chunk_counts[c][e] becomes the
+// number of expert-e pairs in chunks before c (the scatter adds offsets[e]); offsets,
+// tile_count and the (expert, first row) tile list come from block scans over experts.
 __global__ void __launch_bounds__(1024) permute_scan_kernel(int32_t* __restrict__ chunk_counts, int64_t chunks,
                                                            int experts, int tile_rows, int32_t* __restrict__ offsets,
                                                            int32_t* __restrict__ tiles,
                                                            int32_t* __restrict__ tile_count) {
-  __shared__ int32_t total[PERMUTE_MAX_EXPERTS];
-  __shared__ int32_t ntiles[PERMUTE_MAX_EXPERTS];
-  __shared__ int32_t scan_a[PERMUTE_MAX_EXPERTS];
-  __shared__ int32_t scan_b[PERMUTE_MAX_EXPERTS];
-  int e = threadIdx.x;
-  int32_t running = 0;
-  if (e < experts) {
-    for (int64_t c = 0; c < chunks; ++c) {
-      int32_t n = chunk_counts[c * experts + e];
-      chunk_counts[c * experts + e] = running;
-      running += n;
+  __shared__ int32_t part[1024];
+  __shared__ int32_t row_end[PERMUTE_MAX_EXPERTS];   // inclusive scan of the expert totals
+  __shared__ int32_t tile_end[PERMUTE_MAX_EXPERTS];  // inclusive scan of the expert tile counts
+  __shared__ int32_t wave_total[16];
+  const int t = threadIdx.x;
+  const int pad = experts > 1 ? 1 << (32 - __clz(experts - 1)) : 1;
+  const int segs = 1024 / pad;
+  const int e = t % pad, s = t / pad;
+  const bool live = e < experts;
+  const int64_t c0 = chunks * s / segs, c1 = chunks * (s + 1) / segs;
+  constexpr int BATCH = 16;
+  int32_t sum = 0;
+  if (live) {
+    for (int64_t c = c0; c < c1; c += BATCH) {
+      int32_t v[BATCH];
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) v[q] = c + q < c1 ? chunk_counts[(c + q) * experts + e] : 0;
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) sum += v[q];
     }
   }
-  total[e] = e < experts ? running : 0;
-  ntiles[e] = e < experts ? (running + tile_rows - 1) / tile_rows : 0;
+  part[t] = sum;
   __syncthreads();
-  // Inclusive Hillis-Steele scans of total and ntiles over 1024 entries.
-  int32_t* a = scan_a;
-  int32_t* b = scan_b;
-  a[e] = total[e];
-  __syncthreads();
-  for (int offset = 1; offset < PERMUTE_MAX_EXPERTS; offset <<= 1) {
-    b[e] = a[e] + (e >= offset ? a[e - offset] : 0);
-    __syncthreads();
-    int32_t* t = a; a = b; b = t;
+  int32_t before = 0, total = 0;
+  for (int q = 0; q < segs; ++q) {
+    const int32_t v = part[q * pad + e];
+    before += q < s ? v : 0;
+    total += v;
   }
-  int32_t row_base = a[e] - total[e];
-  __syncthreads();
-  a[e] = ntiles[e];
-  __syncthreads();
-  for (int offset = 1; offset < PERMUTE_MAX_EXPERTS; offset <<= 1) {
-    b[e] = a[e] + (e >= offset ? a[e - offset] : 0);
-    __syncthreads();
-    int32_t* t = a; a = b; b = t;
+  if (live) {
+    int32_t running = before;
+    for (int64_t c = c0; c < c1; c += BATCH) {
+      int32_t v[BATCH];
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) v[q] = c + q < c1 ? chunk_counts[(c + q) * experts + e] : 0;
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q)
+        if (c + q < c1) {
+          chunk_counts[(c + q) * experts + e] = running;
+          running += v[q];
+        }
+    }
   }
-  int32_t tile_base = a[e] - ntiles[e];
-  if (e < experts) {
-    offsets[e] = row_base;
-    if (e == experts - 1) {
-      offsets[experts] = row_base + total[e];
-      tile_count[0] = tile_base + ntiles[e];
+  __syncthreads();
+  if (s == 0) part[e] = live ? total : 0;  // expert totals (every thread has read part above)
+  __syncthreads();
+  const int32_t mine = t < experts ? part[t] : 0;
+  const int32_t my_tiles = (mine + tile_rows - 1) / tile_rows;
+  const int32_t rows_incl = block_inclusive_scan(mine, wave_total);
+  const int32_t tiles_incl = block_inclusive_scan(my_tiles, wave_total);
+  if (t < experts) {
+    row_end[t] = rows_incl;
+    tile_end[t] = tiles_incl;
+    offsets[t] = rows_incl - mine;
+    if (t == experts - 1) {
+      offsets[experts] = rows_incl;
+      tile_count[0] = tiles_incl;
     }
-    for (int j = 0; j < ntiles[e]; ++j) {
-      tiles[2 * (tile_base + j)] = e;
-      tiles[2 * (tile_base + j) + 1] = row_base + j * tile_rows;
+  }
+  __syncthreads();
+  // tile i belongs to the first expert whose inclusive tile count exceeds i
+  const int32_t n_tiles = tile_end[experts - 1];
+  for (int32_t i = t; i < n_tiles; i += 1024) {
+    int lo = 0, hi = experts - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) / 2;
+      if (tile_end[mid] > i) hi = mid; else lo = mid + 1;
     }
-    for (int64_t c = 0; c < chunks; ++c) chunk_counts[c * experts + e] += row_base;
+    const int32_t first_tile = tile_end[lo] - (row_end[lo] - (lo ? row_end[lo - 1] : 0) + tile_rows - 1) / tile_rows;
+    const int32_t row_base = lo ? row_end[lo - 1] : 0;
+    tiles[2 * i] = lo;
+    tiles[2 * i + 1] = row_base + (i - first_tile) * tile_rows;
   }
 }
 
 __global__ void __launch_bounds__(64) permute_scatter_kernel(const int32_t* __restrict__ idx, int64_t pairs,
                                                             int experts, const int32_t* __restrict__ chunk_base,
+                                                            const int32_t* __restrict__ offsets,
                                                             int32_t* __restrict__ order,
                                                             int32_t* __restrict__ inverse) {
   __shared__ int32_t base[PERMUTE_MAX_EXPERTS];
   int lane = threadIdx.x;
   int64_t chunk = blockIdx.x;
-  for (int e = lane; e < experts; e += 64) base[e] = chunk_base[chunk * experts + e];
+  for (int e = lane; e < experts; e += 64) base[e] = chunk_base[chunk * experts + e] + offsets[e];
   __syncthreads();
   int bits = 32 - __clz(experts);  // enough bits to tell experts (and the sentinel `experts`) apart
   int64_t begin = chunk * PERMUTE_CHUNK, end = min<int64_t>(pairs, begin + PERMUTE_CHUNK);
@@ -158,7 +204,7 @@ WM_EXPORT int wm_permute(const int32_t* indices, int64_t pairs, int32_t experts,
     check_launch("permute_scan");
     if (chunks > 0) {
       hipLaunchKernelGGL(permute_scatter_kernel, dim3((unsigned)chunks), dim3(64), 0, s, indices, pairs, experts,
-                         counts, order, inverse);
+                         counts, offsets, order, inverse);
       check_launch("permute_scatter");
     }
   });

@@ -73,6 +73,8 @@ WM_EXPORT int wm_moe_stack_mxfp4(const float* logits, int32_t layers, int32_t to
     if (!experts || !residual || !logits) fail("wm_moe_stack_mxfp4: null pointer");
     for (int l = 0; l < layers; ++l) {
       validate_experts(&experts[l], "stack routed experts", false);
+      if (experts[l].tiled || (shared && shared[l].tiled))
+        fail("wm_moe_stack_mxfp4: the decode stack takes tables in the row layout, not the prefill tile layout");
       if (experts[l].hidden != experts[0].hidden || experts[l].inter != experts[0].inter ||
           experts[l].experts != experts[0].experts)
         fail("wm_moe_stack_mxfp4: layers differ in shape");

@@ -59,7 +59,9 @@ class MXFP4Experts:
     [.., H, I/8], down_scales u8 [.., H, I/32], with a leading expert/slot axis
     (QwenBatchedExperts, expert_cache.py:70-75) or none for a single expert
     (QwenExpertWeights, :62-67). ``slots`` (int32 [E]) maps expert -> slot when
-    the regions are a slot pool rather than a whole layer.
+    the regions are a slot pool rather than a whole layer. ``tiled`` marks regions in the
+    prefill tile layout (``prefill_layout``): same shapes and bytes, reordered for the
+    grouped GEMM, and accepted by the grouped-GEMM path only.
     """
     gate_up: torch.Tensor
     gate_up_scales: torch.Tensor
@@ -69,6 +71,7 @@ class MXFP4Experts:
     experts: int | None = None
     up_first: bool = False
     swiglu_limit: float = 0.0
+    tiled: bool = False
 
     @property
     def hidden(self) -> int:
@@ -106,10 +109,29 @@ class MXFP4Experts:
             self.gate_up.data_ptr(), self.gate_up_scales.data_ptr(), self.down.data_ptr(), self.down_scales.data_ptr(),
             stride(self.gate_up), stride(self.gate_up_scales), stride(self.down), stride(self.down_scales),
             0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
-            float(self.swiglu_limit))
+            float(self.swiglu_limit), int(self.tiled))
 
     def tensors(self):
         return (self.gate_up, self.gate_up_scales, self.down, self.down_scales, self.slots)
+
+
+def prefill_layout(experts: MXFP4Experts) -> MXFP4Experts:
+    """A copy of ``experts`` in the prefill tile layout (wm_repack_prefill_mxfp4): one
+    expert after another (``slots`` resolved), each 16-row group's 128-wide K step one
+    contiguous KB, each step's scale bytes one run. Same shapes and bytes as the row layout;
+    only the grouped-GEMM path (any batch size) takes it. A one-time repack, like the
+    reference's install-time blob repack (Sources/DeepSeekRepack/Repacker.swift:17-124)."""
+    if experts.tiled:
+        return experts
+    device = _require_device(*experts.tensors())
+    E, H, I = experts.count, experts.hidden, experts.inter
+    lead = (E,) if experts.gate_up.dim() == 3 or E > 1 else ()
+    out = [torch.empty(*lead, *t.shape[-2:], dtype=t.dtype, device=device)
+           for t in (experts.gate_up, experts.gate_up_scales, experts.down, experts.down_scales)]
+    table = experts.c_struct()
+    _lib.call("wm_repack_prefill_mxfp4", ctypes.byref(table), *(_ptr(t) for t in out), _stream(device))
+    return MXFP4Experts(*out, experts=E if lead else None, up_first=experts.up_first,
+                        swiglu_limit=experts.swiglu_limit, tiled=True)
 
 
 # ----------------------------------------------------------------------------- formats
