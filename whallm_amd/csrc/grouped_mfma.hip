@@ -755,48 +755,53 @@ __device__ __forceinline__ int fp6_exponent(float amax) {
   return e - 2 > 1 ? e - 2 : 1;
 }
 
-// Round |q| to an E2M3 magnitude code (nearest even, saturating at 7.5) and return the code
-// with its sign; `value` gets the signed E2M3 value. Each binade's offset is subtracted
-// exactly (Sterbenz), so the only rounding is the rint.
-__device__ __forceinline__ uint32_t e2m3_encode(float q, float& value) {
-  const float a = fabsf(q);
-  const float t0 = rintf(a * 8.0f);                               // [0, 2): step 1/8
-  const float t1 = 16.0f + rintf((a - 2.0f) * 4.0f);              // [2, 4): step 1/4
-  const float t2 = 24.0f + rintf((fminf(a, 8.0f) - 4.0f) * 2.0f);  // [4, 8): step 1/2
-  const bool b0 = a < 2.0f, b1 = a < 4.0f;
-  const float t = fminf(b0 ? t0 : (b1 ? t1 : t2), 31.0f);
-  // value of code t in the binade the rounding started from (a carry into the next binade
-  // gives the same value: 16 / 8 = (16 - 8) / 4 = 2, (24 - 8) / 4 = (24 - 16) / 2 = 4)
-  const float step = b0 ? 0.125f : (b1 ? 0.25f : 0.5f);
-  const float base = b0 ? 0.0f : (b1 ? 8.0f : 16.0f);
-  const float mag = (t - base) * step;
-  const uint32_t neg = __float_as_uint(q) >> 31;
-  value = neg ? -mag : mag;
-  return (uint32_t)t | (neg << 5);
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef unsigned v6u_t __attribute__((ext_vector_type(6)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){a, b}, bf16x2_t));
 }
 
-// Codes of 32 values (v[i], block maximum amax) into 6 words of contiguous 6-bit fields,
-// and the block exponent; `resid` gets v - hi (exact).
-__device__ __forceinline__ void fp6_term32(const float (&v)[32], float amax, uint32_t (&w)[6], int& s,
-                                           float (&resid)[32]) {
-  s = fp6_exponent(amax);
-  const float down = pow2_biased(254 - s), up = pow2_biased(s);
+// The hi and lo E2M3 terms of one 32-value block (v in K order) with the hardware
+// conversions: v_cvt_scalef32_2xpk16_fp6_f32 packs e2m3(x / scale) of its two 16-value
+// operands interleaved (field 2i from the first, 2i + 1 from the second), rounding to
+// nearest even and saturating at 7.5; v_cvt_scalef32_pk32_f32_fp6 gives field * scale back,
+// so the residual v - hi is exact.
+__device__ __forceinline__ void fp6_terms32(const float (&v)[32], v6u_t& hi, v6u_t& lo, int& s_hi, int& s_lo) {
+  float amax = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 6; ++k) w[k] = 0;
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  s_hi = fp6_exponent(amax);
+  const float sc_hi = pow2_biased(s_hi);
+  v16f_t ev, od;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    float hv;
-    const uint32_t code = e2m3_encode(v[i] * down, hv);
-    resid[i] = v[i] - hv * up;
-    const int bit = 6 * i;
-    w[bit / 32] |= code << (bit % 32);
-    if (bit % 32 > 26) w[bit / 32 + 1] |= code >> (32 - bit % 32);
+  for (int m = 0; m < 16; ++m) {
+    ev[m] = v[2 * m];
+    od[m] = v[2 * m + 1];
   }
+  hi = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, sc_hi);
+  const auto back = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(hi, sc_hi);
+  float rmax = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    ev[m] = v[2 * m] - back[2 * m];
+    od[m] = v[2 * m + 1] - back[2 * m + 1];
+    rmax = fmaxf(rmax, fmaxf(fabsf(ev[m]), fabsf(od[m])));
+  }
+  s_lo = fp6_exponent(rmax);
+  lo = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, pow2_biased(s_lo));
 }
 
 // x [rows, H] bf16 -> split rows [rows][H/128][208 bytes]. One lane per 32-value block.
+// With g (bf16 [H]) the kernel also writes gate[row] = sigmoid(x[row] . g), the shared
+// expert's gate: a row's H/32 lanes are contiguous and aligned (H/32 a power of two <= 64),
+// so their partial dots meet in a butterfly inside the group.
 __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __restrict__ x, int rows, int hidden,
-                                                          uint8_t* __restrict__ x6) {
+                                                          uint8_t* __restrict__ x6, const uint16_t* __restrict__ g,
+                                                          float* __restrict__ gate) {
   const int blocks = hidden / 32;
   const int64_t job = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, block)
   if (job >= (int64_t)rows * blocks) return;
@@ -804,7 +809,6 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
   const int blk = (int)(job % blocks);
   const uint4* src = reinterpret_cast<const uint4*>(x + row * hidden + blk * 32);
   float v[32];
-  float amax = 0.0f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const uint4 u = src[q];
@@ -815,16 +819,9 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
       v[8 * q + 2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
     }
   }
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  uint32_t hi[6], lo[6];
-  float r[32], r2[32];
+  v6u_t hi, lo;
   int s_hi, s_lo;
-  fp6_term32(v, amax, hi, s_hi, r);
-  float rmax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) rmax = fmaxf(rmax, fabsf(r[i]));
-  fp6_term32(r, rmax, lo, s_lo, r2);
+  fp6_terms32(v, hi, lo, s_hi, s_lo);
   uint8_t* step = x6 + (row * (hidden / 128) + blk / 4) * XSTEP;
   uint4* dst = reinterpret_cast<uint4*>(step + (blk % 4) * 48);
   dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -832,6 +829,22 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
   dst[2] = make_uint4(lo[2], lo[3], lo[4], lo[5]);
   step[192 + blk % 4] = (uint8_t)s_hi;
   step[196 + blk % 4] = (uint8_t)s_lo;
+  if (g) {
+    const uint4* gs = reinterpret_cast<const uint4*>(g + blk * 32);
+    float dot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 u = gs[q];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dot = fmaf(v[8 * q + 2 * j], bf16_bits_to_f32(w[j] & 0xffffu), dot);
+        dot = fmaf(v[8 * q + 2 * j + 1], bf16_bits_to_f32(w[j] >> 16), dot);
+      }
+    }
+    for (int off = 1; off < blocks; off <<= 1) dot += __shfl_xor(dot, off, 64);
+    if (blk == 0) gate[row] = 1.0f / (1.0f + __expf(-dot));
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -1083,20 +1096,6 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcn
 // This wave's LDS writes are done before its next LDS reads (and its reads before its writes).
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// 16 codes of a lane (its rows 8j + 4 half + 0..3 of a block, j = 0..3) as four 24-bit groups.
-__device__ __forceinline__ void fp6_groups16(const float (&v)[16], float scale_down, uint32_t (&grp)[4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t gword = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float unused;
-      gword |= e2m3_encode(v[4 * j + q] * scale_down, unused) << (6 * q);
-    }
-    grp[j] = gword;
-  }
-}
-
 // gate_up: act rows of a tile's 256 intermediate columns; weight tile rows [0, 256) are the
 // gate rows nt * 256 + j, [256, 512) the matching up rows; wave wn owns gate rows
 // 64 wn + [0, 64) (mi 0, 1) and the same up rows (mi 2, 3).
@@ -1156,9 +1155,9 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
 
   // Epilogue: lane (r, half) holds act rows 8 j + 4 half + q (j, q = 0..3; register 4 j + q)
   // of 32-column block kb = 2 wn + b of the tile (b = 0, 1: gate mi b, up mi b + 2) for row
-  // 64 wm + 32 ni + r. The two lanes of a block exchange 24-bit field groups so that lane
-  // half 0 writes the block's hi fields and half 1 its lo fields, into the consumed stage as
-  // the tile's act rows (416 bytes: 2 steps), which all threads then copy out row by row.
+  // 64 wm + 32 ni + r. Both lanes of a block form its terms; lane half 0 writes the hi
+  // fields and half 1 the lo fields, into the consumed stage as the tile's act rows (416
+  // bytes: 2 steps), which all threads then copy out row by row.
   auto epilogue = [&](const Tile4& t, Stage4& st) {
     stage_barrier();
     uint8_t* stg = reinterpret_cast<uint8_t*>(&st);
@@ -1170,7 +1169,6 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
           float v[16];
-          float amax = 0.0f;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             float gv = acc[b][ni][i], uv = acc[b + 2][ni][i];
@@ -1179,45 +1177,23 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
               uv = fminf(fmaxf(uv, -t.limit), t.limit);
             }
             v[i] = silu(gv) * uv;
-            amax = fmaxf(amax, fabsf(v[i]));
           }
-          amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-          const int s_hi = fp6_exponent(amax);
-          const float down_hi = pow2_biased(254 - s_hi), up_hi = pow2_biased(s_hi);
-          float res[16];
-          float rmax = 0.0f;
-          uint32_t ghi[4];
+          // both lanes of the pair take the block's 32 values in K order: rows 8 j + q from
+          // half 0, rows 8 j + 4 + q from half 1 (v_permlane32_swap of a register with itself)
+          float full[32];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            uint32_t gword = 0;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float hv;
-              gword |= e2m3_encode(v[4 * j + q] * down_hi, hv) << (6 * q);
-              res[4 * j + q] = v[4 * j + q] - hv * up_hi;
-              rmax = fmaxf(rmax, fabsf(res[4 * j + q]));
-            }
-            ghi[j] = gword;
+          for (int i = 0; i < 16; ++i) {
+            const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false,
+                                                             false);
+            full[8 * (i / 4) + i % 4] = __uint_as_float(pr[0]);
+            full[8 * (i / 4) + 4 + i % 4] = __uint_as_float(pr[1]);
           }
-          rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
-          const int s_lo = fp6_exponent(rmax);
-          uint32_t glo[4];
-          fp6_groups16(res, pow2_biased(254 - s_lo), glo);
-          uint32_t g0[4], g1[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t recv = __shfl_xor(half ? ghi[j] : glo[j], 32, 64);
-            g0[j] = half ? recv : ghi[j];   // rows 8 j + 0..3 of the term this lane writes
-            g1[j] = half ? glo[j] : recv;   // rows 8 j + 4..7
-          }
-          // group pair j = 48 bits at bit 48 j of the 24-byte term
+          v6u_t hi, lo;
+          int s_hi, s_lo;
+          fp6_terms32(full, hi, lo, s_hi, s_lo);
           uint32_t d[6];
-          d[0] = g0[0] | (g1[0] << 24);
-          d[1] = (g1[0] >> 8) | (g0[1] << 16);
-          d[2] = (g0[1] >> 16) | (g1[1] << 8);
-          d[3] = g0[2] | (g1[2] << 24);
-          d[4] = (g1[2] >> 8) | (g0[3] << 16);
-          d[5] = (g0[3] >> 16) | (g1[3] << 8);
+#pragma unroll
+          for (int w6 = 0; w6 < 6; ++w6) d[w6] = half ? lo[w6] : hi[w6];
           const int kb = 2 * wn + b;  // block of the tile: step kb / 4, block kb % 4 of the step
           uint8_t* step = stg + lr * 416 + (kb / 4) * XSTEP;
           uint2* dst = reinterpret_cast<uint2*>(step + (kb % 4) * 48 + half * 24);
@@ -1298,8 +1274,8 @@ __global__ void __launch_bounds__(64 * WAVES4) down4_kernel(const uint8_t* __res
             for (int j = 0; j < 4; ++j) {
               const v16f& a = acc[2 * mp + m][ni];
               uint2 o;
-              o.x = f32_to_bf16_bits(a[4 * j]) | ((uint32_t)f32_to_bf16_bits(a[4 * j + 1]) << 16);
-              o.y = f32_to_bf16_bits(a[4 * j + 2]) | ((uint32_t)f32_to_bf16_bits(a[4 * j + 3]) << 16);
+              o.x = pack_bf16x2(a[4 * j], a[4 * j + 1]);
+              o.y = pack_bf16x2(a[4 * j + 2], a[4 * j + 3]);
               *reinterpret_cast<uint2*>(slice + r * 144 + 64 * m + 16 * j + 8 * half) = o;
             }
           wave_lds_fence();
@@ -1502,7 +1478,10 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
                  (int32_t*)L.tiles, (int32_t*)L.tile_count, base + p.permute_ws,
                  wm_permute_workspace_size(pairs, routed.experts), s) != 0)
     fail(std::string("prefill permute: ") + wm_last_error());
-  if (has_shared) {
+  // MXFP4: the split kernel computes the shared gate when a row's blocks fit one wave in a
+  // power-of-two group; otherwise (and for FP8) a kernel of its own does
+  const bool fused_gate = fp6_terms && has_shared && shared_gate && (H / 32) <= 64 && ((H / 32) & (H / 32 - 1)) == 0;
+  if (has_shared && !fused_gate) {
     hipLaunchKernelGGL(shared_gate_kernel, dim3(tokens), dim3(64), 0, s, x, shared_gate, tokens, H,
                        (float*)L.shared_gate);
     check_launch("shared_gate");
@@ -1518,7 +1497,7 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
     }
     const int64_t split_jobs = (int64_t)tokens * (H / 32);
     hipLaunchKernelGGL(split6_rows_kernel, dim3((unsigned)((split_jobs + 255) / 256)), dim3(256), 0, s, x, tokens, H,
-                       x8);
+                       x8, fused_gate ? shared_gate : nullptr, (float*)L.shared_gate);
   } else {
     const int64_t split_jobs = (int64_t)tokens * (H / 128);
     hipLaunchKernelGGL(split_rows_kernel, dim3((unsigned)((split_jobs + 3) / 4)), dim3(256), 0, s, x, tokens, H, x8,
