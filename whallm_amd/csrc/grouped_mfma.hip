@@ -1155,9 +1155,10 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
 
   // Epilogue: lane (r, half) holds act rows 8 j + 4 half + q (j, q = 0..3; register 4 j + q)
   // of 32-column block kb = 2 wn + b of the tile (b = 0, 1: gate mi b, up mi b + 2) for row
-  // 64 wm + 32 ni + r. Both lanes of a block form its terms; lane half 0 writes the hi
-  // fields and half 1 the lo fields, into the consumed stage as the tile's act rows (416
-  // bytes: 2 steps), which all threads then copy out row by row.
+  // 64 wm + 32 ni + r. After one swap between the lane halves each lane holds a whole block
+  // (half 0 block b = 0, half 1 block b = 1), forms its two terms and writes them with the
+  // scales into the consumed stage as the tile's act rows (416 bytes: 2 steps), which all
+  // threads then copy out row by row.
   auto epilogue = [&](const Tile4& t, Stage4& st) {
     stage_barrier();
     uint8_t* stg = reinterpret_cast<uint8_t*>(&st);
@@ -1166,9 +1167,9 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
 #pragma unroll
       for (int ni = 0; ni < NI4; ++ni) {
         const int lr = 64 * wm + 32 * ni + r;
+        float v[2][16];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          float v[16];
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             float gv = acc[b][ni][i], uv = acc[b + 2][ni][i];
@@ -1176,32 +1177,30 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
               gv = fminf(gv, t.limit);
               uv = fminf(fmaxf(uv, -t.limit), t.limit);
             }
-            v[i] = silu(gv) * uv;
+            v[b][i] = silu(gv) * uv;
           }
-          // both lanes of the pair take the block's 32 values in K order: rows 8 j + q from
-          // half 0, rows 8 j + 4 + q from half 1 (v_permlane32_swap of a register with itself)
-          float full[32];
+        // v_permlane32_swap(block 0, block 1): lanes of half 0 then hold all of block 0 and
+        // lanes of half 1 all of block 1, in K order (rows 8 j + q from the first result, rows
+        // 8 j + 4 + q from the second)
+        float full[32];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false,
-                                                             false);
-            full[8 * (i / 4) + i % 4] = __uint_as_float(pr[0]);
-            full[8 * (i / 4) + 4 + i % 4] = __uint_as_float(pr[1]);
-          }
-          v6u_t hi, lo;
-          int s_hi, s_lo;
-          fp6_terms32(full, hi, lo, s_hi, s_lo);
-          uint32_t d[6];
-#pragma unroll
-          for (int w6 = 0; w6 < 6; ++w6) d[w6] = half ? lo[w6] : hi[w6];
-          const int kb = 2 * wn + b;  // block of the tile: step kb / 4, block kb % 4 of the step
-          uint8_t* step = stg + lr * 416 + (kb / 4) * XSTEP;
-          uint2* dst = reinterpret_cast<uint2*>(step + (kb % 4) * 48 + half * 24);
-          dst[0] = make_uint2(d[0], d[1]);
-          dst[1] = make_uint2(d[2], d[3]);
-          dst[2] = make_uint2(d[4], d[5]);
-          step[192 + 4 * half + kb % 4] = (uint8_t)(half ? s_lo : s_hi);
+        for (int i = 0; i < 16; ++i) {
+          const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0][i]), __float_as_uint(v[1][i]), false,
+                                                           false);
+          full[8 * (i / 4) + i % 4] = __uint_as_float(pr[0]);
+          full[8 * (i / 4) + 4 + i % 4] = __uint_as_float(pr[1]);
         }
+        v6u_t hi, lo;
+        int s_hi, s_lo;
+        fp6_terms32(full, hi, lo, s_hi, s_lo);
+        const int kb = 2 * wn + half;  // this lane's block of the tile: step kb / 4, block kb % 4
+        uint8_t* step = stg + lr * 416 + (kb / 4) * XSTEP;
+        uint4* dst = reinterpret_cast<uint4*>(step + (kb % 4) * 48);
+        dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        dst[1] = make_uint4(hi[4], hi[5], lo[0], lo[1]);
+        dst[2] = make_uint4(lo[2], lo[3], lo[4], lo[5]);
+        step[192 + kb % 4] = (uint8_t)s_hi;
+        step[196 + kb % 4] = (uint8_t)s_lo;
       }
     }
     stage_barrier();
