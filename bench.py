@@ -323,6 +323,13 @@ class FP8Layer:
         log(f"[bench] generating {experts} + 1 FP8 experts (H {hidden}, I {inter}) on device")
         self.experts = S.fp8_experts_device(experts, hidden, inter, device, g)
         self.shared = S.fp8_experts_device(1, hidden, inter, device, g)
+        # prefill runs on the weights repacked once into the prefill tile layout (the grouped
+        # GEMM's loads); decode reads the row layout (the fused GEMV's)
+        if tokens > 1:
+            import whallm_amd as wa
+            self.run_experts, self.run_shared = wa.prefill_layout(self.experts), wa.prefill_layout(self.shared)
+        else:
+            self.run_experts, self.run_shared = self.experts, self.shared
         self.bias = torch.randn(experts, device=device, generator=g) * 0.1
         self.gen = g
         self.graph = None
@@ -352,7 +359,7 @@ class FP8Layer:
         import whallm_amd as wa
         idx, w = wa.route_scored(self.logits, self.bias, self.K, func="sigmoid", route_scale=2.5, n_groups=8,
                                  topk_groups=4)
-        self.y = wa.moe_fp8(self.x, idx, w, self.experts, self.shared, None)
+        self.y = wa.moe_fp8(self.x, idx, w, self.run_experts, self.run_shared, None)
 
     def capture(self):
         self.logits.copy_(self.step_logits[0])
@@ -634,7 +641,7 @@ def main():
                     "frac": round(achieved / FP4_PEAK_TFLOPS, 4), "traffic": profiled_traffic("prefill_c3_gate_up"),
                     "mfma_instruction_frac": round(2 * achieved / FP4_PEAK_TFLOPS, 4),
                     "frac_of_fp8_peak": round(achieved / FP8_PEAK_TFLOPS, 4),
-                    "kernel": "gate_up4_kernel (grouped gate/up GEMM + SwiGLU, one launch per layer)",
+                    "kernel": "gate_up_mx_kernel<Mx4> (grouped gate/up GEMM + SwiGLU, one launch per layer)",
                     "kernel_ms": round(gu_ms, 5), "down_kernel_ms": round(dn_ms, 5),
                     "algorithmic_flops_per_launch": wl.gate_up_flops(),
                     "layer_tflops": round(layer_tflops, 1)}

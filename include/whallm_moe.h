@@ -68,6 +68,8 @@ typedef struct wm_fp8_experts {
   int32_t inter;
   int32_t up_first;
   float swiglu_limit;
+  int32_t tiled;                 /* 0: the reference's row layout; 1: prefill tile layout of the
+                                    weight bytes (wm_repack_prefill_fp8), grouped-GEMM path only */
 } wm_fp8_experts;
 
 /* Message of the last failed call on this thread ("" when none). */
@@ -169,6 +171,18 @@ WM_EXPORT int wm_moe_fp8(const void* x, int32_t tokens, const int32_t* indices, 
 WM_EXPORT int wm_experts_fp8(const void* x, int32_t tokens, const int32_t* indices, int32_t k,
                              const wm_fp8_experts* experts, void* out, void* workspace, size_t workspace_bytes,
                              void* stream);
+/* Prefill tile layout of FP8 weights: writes every expert of src (resolved through
+ * src->slots) into the caller's four device regions, one expert after another with the
+ * region sizes of the row layout (2I*H, 4*(2I/128)*(H/128), H*I, 4*(H/128)*(I/128) bytes):
+ * the weight bytes reordered so that the grouped GEMM reads each 16-row group's 128-wide
+ * K step as two contiguous KB, the block scales copied unchanged:
+ *   weights [K/128 steps][rows/16 groups][8 x 16 bytes of the step][16 rows][16 bytes]
+ * (w13: rows 2I, K = H; w2: rows H, K = I; H and I multiples of 128). Describe the result
+ * with slots = NULL, the region sizes as strides and tiled = 1; such a table always takes
+ * the grouped-GEMM path. The counterpart of the reference's install-time FP8 expert
+ * repack (Sources/DeepSeekRepack/Repacker.swift:601-715), for this GPU's loads. */
+WM_EXPORT int wm_repack_prefill_fp8(const wm_fp8_experts* src, void* w13, void* w13_scales, void* w2,
+                                    void* w2_scales, void* stream);
 
 /* ---- measurement ----------------------------------------------------------
  * When enabled, every later wm_moe_mxfp4 / wm_experts_mxfp4 / wm_moe_fp8 / wm_experts_fp8

@@ -78,3 +78,29 @@ def test_prefill_tile_layout_argument_checks():
     lib = _lib.load()
     assert lib.wm_moe_mxfp4_workspace_size(1, 2, ctypes.byref(routed)) > \
         lib.wm_moe_mxfp4_workspace_size(1, 2, ctypes.byref(_fake_table(0)))
+
+
+def _fake_fp8_table(tiled: int, hidden=1024, inter=1024):
+    """An FP8 table with aligned non-null (never dereferenced) addresses: argument checks only."""
+    t = _lib.FP8ExpertsC()
+    t.w13 = t.w13_scales = t.w2 = t.w2_scales = 0x10000
+    t.experts, t.hidden, t.inter, t.tiled = 8, hidden, inter, tiled
+    return t
+
+
+def test_fp8_prefill_tile_layout_argument_checks():
+    routed, shared = _fake_fp8_table(1), _fake_fp8_table(0)
+    with pytest.raises(_lib.WhallmError, match="both tiled"):
+        _lib.call("wm_moe_fp8", 1, 1, 1, 1, 2, ctypes.byref(routed), ctypes.byref(shared), None, 1, 1, 1 << 40, None)
+    with pytest.raises(_lib.WhallmError, match="already in the prefill tile layout"):
+        _lib.call("wm_repack_prefill_fp8", ctypes.byref(routed), 16, 16, 16, 16, None)
+    with pytest.raises(_lib.WhallmError, match="null destination"):
+        _lib.call("wm_repack_prefill_fp8", ctypes.byref(shared), 16, None, 16, 16, None)
+    with pytest.raises(_lib.WhallmError, match="16-byte aligned"):
+        _lib.call("wm_repack_prefill_fp8", ctypes.byref(shared), 8, 16, 16, 16, None)
+    with pytest.raises(_lib.WhallmError, match="multiples of 128"):
+        _lib.call("wm_repack_prefill_fp8", ctypes.byref(_fake_fp8_table(0, hidden=96)), 16, 16, 16, 16, None)
+    # a tiled table always takes the grouped GEMM, whose workspace exceeds the decode buffer
+    lib = _lib.load()
+    assert lib.wm_moe_fp8_workspace_size(1, 2, ctypes.byref(routed)) > \
+        lib.wm_moe_fp8_workspace_size(1, 2, ctypes.byref(shared))

@@ -79,3 +79,51 @@ def test_router_order_clamp_and_up_first(device, T):
     ex = oracle_experts(a, E, up_first=True)
     want = M.routed_outputs(S.bf16_bits_to_f32(x), idx, ex, ffn=M.fp8_expert_ffn, limit=10.0)
     close(out.float().cpu().numpy(), want, f"router order T={T}")
+
+
+def _fp8_tile_layout_np(w):
+    """[R, K] FP8 rows -> the prefill tile layout [K/128][R/16][8][16 rows][16 bytes], flattened
+    back to [R, K] (the row layout's region size)."""
+    R, K = w.shape
+    return np.ascontiguousarray(w.reshape(R // 16, 16, K // 128, 8, 16).transpose(2, 0, 3, 1, 4)).reshape(R, K)
+
+
+def test_fp8_prefill_layout_bytes(device):
+    H, I, E, pool = 384, 256, 3, 5
+    rng = np.random.default_rng(11)
+    a = S.fp8_experts_np(rng, pool, H, I)
+    slots = np.array([4, 0, 2], np.int32)
+    table = S.fp8_experts_to_device(a, device, slots=torch.from_numpy(slots).to(device), experts=E)
+    tiled = wa.prefill_layout(table)
+    torch.cuda.synchronize()
+    assert tiled.tiled and tiled.slots is None and tiled.count == E
+    for e, s in enumerate(slots):
+        np.testing.assert_array_equal(tiled.w13[e].cpu().numpy(), _fp8_tile_layout_np(a["w13"][s]))
+        np.testing.assert_array_equal(tiled.w2[e].cpu().numpy(), _fp8_tile_layout_np(a["w2"][s]))
+        np.testing.assert_array_equal(tiled.w13_scales[e].cpu().numpy(), a["w13_scales"][s])
+        np.testing.assert_array_equal(tiled.w2_scales[e].cpu().numpy(), a["w2_scales"][s])
+
+
+@pytest.mark.parametrize("case", ["decode-small", "prefill-small", "prefill-odd"])
+def test_fp8_prefill_layout_matches_oracle_and_row_layout(device, case):
+    """Tables in the prefill tile layout take the grouped GEMM at every batch size; the GEMM
+    reads the same bytes in the same order, so its output equals the row layout's bit for bit
+    (where the row layout also takes the GEMM) and the oracle within the FP8 tolerance."""
+    H, I, E, K, T = CASES[case]
+    rng = np.random.default_rng(H + 7 * T)
+    a = S.fp8_experts_np(rng, E, H, I)
+    sh = S.fp8_experts_np(rng, 1, H, I)
+    x = S.bf16_normal_np(rng, (T, H))
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.1, 1.0, size=(T, K)).astype(np.float32)
+    rows, rows_sh = S.fp8_experts_to_device(a, device), S.fp8_experts_to_device(sh, device)
+    tiled, tiled_sh = wa.prefill_layout(rows), wa.prefill_layout(rows_sh)
+    xt = S.bf16_bits_to_tensor(x, device)
+    it, wt = torch.from_numpy(idx).to(device), torch.from_numpy(w).to(device)
+    y = wa.moe_fp8(xt, it, wt, tiled, tiled_sh, None)
+    xf = S.bf16_bits_to_f32(x)
+    want = M.combine(M.routed_outputs(xf, idx, oracle_experts(a, E), ffn=M.fp8_expert_ffn), w,
+                     M.fp8_expert_ffn(xf, oracle_experts(sh, 1)[0]), None)
+    close(y.float().cpu().numpy(), want, f"tiled {case}")
+    if T * K > 256 or H % 1024 or I % 1024:  # the row layout takes the grouped GEMM as well
+        assert torch.equal(y, wa.moe_fp8(xt, it, wt, rows, rows_sh, None)), case

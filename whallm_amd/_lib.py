@@ -29,7 +29,7 @@ class FP8ExpertsC(ctypes.Structure):
         ("w13", c_void_p), ("w13_scales", c_void_p), ("w2", c_void_p), ("w2_scales", c_void_p),
         ("w13_stride", c_int64), ("w13_scales_stride", c_int64), ("w2_stride", c_int64), ("w2_scales_stride", c_int64),
         ("slots", c_void_p), ("experts", c_int32), ("hidden", c_int32), ("inter", c_int32),
-        ("up_first", c_int32), ("swiglu_limit", c_float),
+        ("up_first", c_int32), ("swiglu_limit", c_float), ("tiled", c_int32),
     ]
 
 
@@ -62,6 +62,7 @@ _SIGNATURES = {
                              _P, _P, c_size_t, _P]),
     "wm_experts_mxfp4": (c_int, [_P, c_int32, _P, c_int32, POINTER(MXFP4ExpertsC), _P, _P, c_size_t, _P]),
     "wm_repack_prefill_mxfp4": (c_int, [POINTER(MXFP4ExpertsC), _P, _P, _P, _P, _P]),
+    "wm_repack_prefill_fp8": (c_int, [POINTER(FP8ExpertsC), _P, _P, _P, _P, _P]),
     "wm_residual_rmsnorm": (c_int, [_P, _P, c_int32, c_int32, c_float, _P, _P]),
     "wm_moe_stack_mxfp4_workspace_size": (c_size_t, [c_int32, c_int32, POINTER(MXFP4ExpertsC)]),
     "wm_moe_stack_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, POINTER(MXFP4ExpertsC),

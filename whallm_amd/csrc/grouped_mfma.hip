@@ -1,4 +1,4 @@
-// Prefill-time expert FFN on gfx950 scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4):
+// Prefill-time expert FFN on gfx950 scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4):
 // grouped GEMMs over the row tiles of the permute kernel, for MXFP4 weights (E2M1 codes
 // with an E8M0 scale per 32, fed to the MFMA as stored) and for FP8-E4M3 weights with
 // fp32 128 x 128 block scales.
@@ -7,31 +7,17 @@
 // moe_combine_rows (Native/QwenNative/kernels.metal:691-765, engine.mm:2104-2162) and
 // mx.gather_qmm (qwen4_exp.py:857-897, model.py:435-501):
 //
-//   split   : every token row of x (bf16) becomes two E4M3 terms, hi and lo, each with
-//             an E8M0 scale per 32 values: x = hi * 2^(s-127) + lo * 2^(s-131), which keeps
-//             the 8 significant bits of a bf16 for values within 2^8 of their block's
-//             maximum. The bytes are stored in MFMA B-operand order (below), so the GEMMs
-//             copy them to LDS unchanged.
-//   gate_up : tile = 128 permuted rows x (64 gate + the 64 matching up weight rows); per
-//             128-wide K step each wave runs 4 x 4 (weight tile x row tile) MFMA pairs
-//             (hi term, lo term). SwiGLU is the epilogue, which writes act straight back
-//             as E4M3 hi/lo terms with per-32 scales (the down GEMM's B operand).
-//   down    : tile = 128 permuted rows x 128 output columns over K = intermediate; the
-//             row's routing weight (or the shared expert's sigmoid gate) is applied in the
-//             epilogue; bf16 rows in permuted order.
-//   combine : y[t] = sum of the token's K rows in k order, plus the shared row.
-//
-// MFMA operand layout (16 x 16 x 128; lane l, c = l % 16, g = l / 16):
-//   fp4 operand: lane holds row c's K values [32g, 32g+32) as nibbles (low first), 16 bytes;
-//   fp8 operand: lane holds row c's K values [16g, 16g+16) in bytes 0-15 and
-//                [64+16g, 64+16g+16) in bytes 16-31;
-//   scale     : lane (c, g) gives the E8M0 scale of row c, K block [32g, 32g+32);
-//   result    : lane holds D[4g + r][c], r = 0..3 (A rows = weight rows, B columns = rows).
-// "B-operand order" of a 128-value chunk is therefore position 32g + 16h + e for K value
-// 64h + 16g + e, so lane group g reads its 32 bytes contiguously.
-//
-// Precision: per element the two terms carry 8 significant bits (bf16 has 8); the MFMA's
-// own summation keeps about 2^-13 of the sum of |products|.
+//   split   : every token row of x (bf16) becomes two E2M3 (fp6) terms, hi and lo, each
+//             with an E8M0 scale per 32 values, stored as the MFMA's B operand reads them
+//             (the GEMMs copy them to LDS unchanged).
+//   gate_up : tile = 128 permuted rows x (TW / 2 gate + the matching up weight rows); per
+//             128-wide K step each wave runs its weight tiles x 2 row tiles x 2 halves of
+//             the step x 2 terms MFMAs. SwiGLU is the epilogue, which writes act straight
+//             back as E2M3 terms (the down GEMM's B operand).
+//   down    : tile = 128 permuted rows x TW output columns over K = intermediate; bf16
+//             rows in permuted order, unweighted.
+//   combine : y[t] = sum of the token's K rows times their routing weights in k order,
+//             plus the shared row times its gate.
 //
 // The shared expert is one more row group after the routed ones (rows P .. P+T-1). Work
 // tiles are mapped XCD-major so the column tiles of one row tile share an L2.
@@ -48,13 +34,10 @@ namespace mf {
 
 constexpr int BM = 128;     // permuted rows per tile
 constexpr int XCDS = 8;
-constexpr int CHUNK = 256;  // bytes per (row, 128-wide K step) of a split operand: hi | lo
-constexpr int XSTR = 272;   // LDS bytes per row of the split operand: 256 + 16 pad
 constexpr int FMT_FP8 = 0;
 constexpr int FMT_FP4 = 4;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 struct Lists {
@@ -69,133 +52,14 @@ struct Lists {
   int has_shared;
 };
 
-// Row range and expert of logical row tile m; expert -1 is the shared expert.
-__device__ __forceinline__ bool resolve_tile(const Lists& L, int m, int& expert, int& begin, int& end) {
-  const int routed_tiles = L.tile_count[0];
-  if (m < routed_tiles) {
-    expert = L.tiles[2 * m];
-    begin = L.tiles[2 * m + 1];
-    end = min(begin + BM, L.offsets[expert + 1]);
-    return true;
-  }
-  const int j = m - routed_tiles;
-  if (!L.has_shared || j * BM >= L.tokens) return false;
-  expert = -1;
-  begin = L.pairs + j * BM;
-  end = min(begin + BM, L.pairs + L.tokens);
-  return true;
-}
-
 __device__ __forceinline__ int active_row_tiles(const Lists& L) {
   return L.tile_count[0] + (L.has_shared ? (L.tokens + BM - 1) / BM : 0);
 }
 
-// XCD-major work mapping (block b runs on XCD b % 8): each XCD takes a contiguous range
-// of the (row tile, column tile) list. False for workgroups past the active work.
-__device__ __forceinline__ bool map_work(int active, int& logical) {
-  const int l = blockIdx.x;
-  const int xcd = l % XCDS, local = l / XCDS;
-  const int share = (active + XCDS - 1) / XCDS;
-  if (local >= share) return false;
-  logical = xcd * share + local;
-  return logical < active;
-}
-
-// ---------------------------------------------------------------------------------
-// split: one wave per 128-wide chunk of a row; lane l holds values 2l, 2l+1.
-
-__device__ __forceinline__ int term_exponent(float amax) {
-  const int be = (int)((__float_as_uint(amax) >> 23) & 0xff);
-  return be - 7 > 1 ? be - 7 : 1;  // maps the block maximum into [2^7, 2^8): E4M3 max is 448
-}
 __device__ __forceinline__ float pow2_biased(int e) { return __uint_as_float((uint32_t)e << 23); }
-__device__ __forceinline__ float e4m3_byte0(uint32_t w) { return __builtin_amdgcn_cvt_f32_fp8((int)w, 0); }
-__device__ __forceinline__ float e4m3_byte1(uint32_t w) { return __builtin_amdgcn_cvt_f32_fp8((int)w, 1); }
-
-// Maximum over the 16 lanes of each row of the wave (DPP within rows of 16).
-__device__ __forceinline__ float max16(float v) {
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
-  return v;
-}
-
-// x [rows, H] bf16 -> x8 [rows][H/128][hi 128 | lo 128] (B-operand order), xs [rows][H/128][hi 4 | lo 4].
-__global__ void __launch_bounds__(256) split_rows_kernel(const uint16_t* __restrict__ x, int rows, int hidden,
-                                                         uint8_t* __restrict__ x8, uint8_t* __restrict__ xs) {
-  const int chunks = hidden / 128;
-  const int64_t job = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;  // (row, chunk)
-  if (job >= (int64_t)rows * chunks) return;
-  const int lane = threadIdx.x % 64;
-  const int64_t row = job / chunks;
-  const int c = (int)(job % chunks);
-  const uint32_t pair = reinterpret_cast<const uint32_t*>(x + row * hidden + c * 128)[lane];
-  const float v0 = bf16_bits_to_f32(pair & 0xffffu), v1 = bf16_bits_to_f32(pair >> 16);
-  const float amax = max16(fmaxf(fabsf(v0), fabsf(v1)));  // lanes 16b..16b+15 hold block b
-  const int s = term_exponent(amax);
-  const float f = pow2_biased(254 - s);
-  const float h0 = v0 * f, h1 = v1 * f;
-  const uint32_t hw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(h0, h1, 0, false);
-  const float l0 = (h0 - e4m3_byte0(hw)) * 16.0f, l1 = (h1 - e4m3_byte1(hw)) * 16.0f;
-  const uint32_t lw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(l0, l1, 0, false);
-  const int kk = 2 * lane;  // K value within the chunk
-  const int pos = 32 * ((kk >> 4) & 3) + 16 * (kk >> 6) + (kk & 15);
-  uint8_t* dst = x8 + (row * chunks + c) * CHUNK;
-  *reinterpret_cast<uint16_t*>(dst + pos) = (uint16_t)hw;
-  *reinterpret_cast<uint16_t*>(dst + 128 + pos) = (uint16_t)lw;
-  if ((lane & 15) == 0) {
-    uint8_t* sd = xs + (row * chunks + c) * 8;
-    sd[lane >> 4] = (uint8_t)s;
-    sd[4 + (lane >> 4)] = (uint8_t)(s > 4 ? s - 4 : 0);
-  }
-}
 
 // ---------------------------------------------------------------------------------
-// Tiles and formats.
-//
-// A workgroup computes a 128-row x TW-weight-row tile with WAVES waves: wave (wm, wn) =
-// (w & 1, w >> 1) owns rows 64 wm + [0, 64) and weight rows wrow(wn, mi) + [0, 16) for
-// mi = 0..7, i.e. 8 x 4 MFMA tiles per term (each B fragment of the split rows, 64 bytes
-// per lane, feeds 8 weight tiles). MXFP4: 8 waves (two per SIMD, which overlap one wave's
-// LDS reads with the other's MFMAs), TW = 512. FP8: 4 waves, TW = 256 (its weight rows
-// are twice as large). Each K step's operands go straight from global memory into LDS
-// (global_load_lds: lane i of a wave writes LDS base + size * i) in a ring of 2 stages;
-// the loads of step k + 1 are issued when step k starts.
-//
-// LDS placement (16-byte pieces, swizzled so the 16 rows served by one ds_read_b128 cycle
-// fall on distinct banks): split row r piece p at r * 256 + 16 (p ^ (r & 15)); weight row j
-// piece p at j * STEP_BYTES + 16 (p ^ swz(j)).
-
-constexpr int MI = 8;        // weight tiles per wave
-constexpr int NI = 4;        // row tiles per wave
-
-struct Fp4Weights {
-  static constexpr int FMT = FMT_FP4;
-  static constexpr int STEP_BYTES = 64;   // bytes of one weight row per 128-wide K step
-  static constexpr int PIECES = 4;
-  static constexpr int WAVES = 8;
-  static constexpr int TW = 512;          // weight rows per tile
-  static constexpr int SCALE_BYTES = TW * 4;  // E8M0 scales of the step: 4 per weight row
-  __device__ static int swz(int row) { return (row >> 2) & 3; }
-};
-struct Fp8Weights {
-  static constexpr int FMT = FMT_FP8;
-  static constexpr int STEP_BYTES = 128;
-  static constexpr int PIECES = 8;
-  static constexpr int WAVES = 4;
-  static constexpr int TW = 256;
-  static constexpr int SCALE_BYTES = 16;      // unused: block scales are read from global memory
-  __device__ static int swz(int row) { return (row >> 1) & 7; }
-};
-
-template <typename W>
-struct Stage {
-  __attribute__((aligned(16))) uint8_t b[BM * CHUNK];              // split rows: hi 128 | lo 128
-  __attribute__((aligned(16))) uint8_t bs[BM * 8];                 // their scales: hi 4 | lo 4
-  __attribute__((aligned(16))) uint8_t a[W::TW * W::STEP_BYTES];   // weight rows
-  __attribute__((aligned(16))) uint8_t as[W::SCALE_BYTES];         // MXFP4: 4 E8M0 bytes per row
-};
+// Loads and the persistent K loop.
 
 // Direct global -> LDS loads, lane i writing LDS address lds + size * i. Written as inline
 // assembly so the compiler does not treat them as LDS stores it must wait for before every
@@ -235,151 +99,6 @@ __device__ __forceinline__ const uint8_t* uniform_u8(const uint8_t* p) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return reinterpret_cast<const uint8_t*>((uintptr_t)(((uint64_t)hi << 32) | lo));
 }
-
-// Per-lane LDS read offsets of a wave's operands within a stage. Weight tile mi of wave
-// (wm, wn) is rows wave_row0 + mrow(mi) + c, where mrow is a compile-time constant; its
-// swizzle depends on the lane only (rows are 16-aligned). Row tile ni is rows
-// 64 wm + 16 ni + c, whose swizzle r & 15 = c & 15 is also per lane. So every read is a
-// per-lane base plus an immediate offset.
-struct LaneOffsets {
-  uint32_t a, a2;        // weight piece g (and, FP8, piece g + 4) of row wave_row0 + c
-  uint32_t as;           // its MXFP4 scale byte: (wave_row0 + c) * 4 + g
-  uint32_t b[4];         // split-row pieces 2g, 2g+1, 8+2g, 9+2g of row 64 wm + c
-  uint32_t bs;           // its scale byte: (64 wm + c) * 8 + g
-};
-
-template <typename W>
-__device__ __forceinline__ LaneOffsets lane_offsets(int wave_row0, int wm) {
-  const int lane = threadIdx.x % 64, c = lane % 16, g = lane / 16;
-  LaneOffsets o;
-  const int arow = wave_row0 + c, z = W::swz(arow);
-  o.a = arow * W::STEP_BYTES + 16 * (g ^ z);
-  o.a2 = arow * W::STEP_BYTES + 16 * ((g + 4) ^ z);
-  o.as = arow * 4 + g;
-  const int brow = 64 * wm + c, zb = brow & 15;
-  o.b[0] = brow * CHUNK + 16 * ((2 * g) ^ zb);
-  o.b[1] = brow * CHUNK + 16 * ((2 * g + 1) ^ zb);
-  o.b[2] = brow * CHUNK + 16 * ((8 + 2 * g) ^ zb);
-  o.b[3] = brow * CHUNK + 16 * ((9 + 2 * g) ^ zb);
-  o.bs = brow * 8 + g;
-  return o;
-}
-
-// One 128-wide K step of the wave's 64 x 128 sub-tile from LDS (rows 64 wm + 16 ni + c,
-// weight rows wave_row0 + MROW(mi) + c). The 8 A fragments are read first; then each row
-// tile's B fragment feeds the 8 weight tiles (16 MFMAs). For FP8 weights each (mi, ni)
-// accumulates the step on its own and adds it times the block scale bscale(mi).
-template <typename W, typename MRow, typename BScale>
-__device__ __forceinline__ void step_mfma(const Stage<W>& st, const LaneOffsets& lo, v4f (&acc)[MI][NI], MRow mrow,
-                                          BScale bscale) {
-  v8i a[MI];
-  int sa[MI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-    const int dr = mrow(mi);  // compile-time after unrolling
-    if constexpr (W::FMT == FMT_FP4) {
-      const uint4 v = *reinterpret_cast<const uint4*>(st.a + lo.a + dr * W::STEP_BYTES);
-      a[mi] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
-      sa[mi] = st.as[lo.as + dr * 4];
-    } else {
-      const uint4 v0 = *reinterpret_cast<const uint4*>(st.a + lo.a + dr * W::STEP_BYTES);
-      const uint4 v1 = *reinterpret_cast<const uint4*>(st.a + lo.a2 + dr * W::STEP_BYTES);
-      a[mi] = v8i{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
-      sa[mi] = 127;
-    }
-  }
-#pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    const int db = 16 * ni * CHUNK;
-    const uint4 h0 = *reinterpret_cast<const uint4*>(st.b + lo.b[0] + db);
-    const uint4 h1 = *reinterpret_cast<const uint4*>(st.b + lo.b[1] + db);
-    const uint4 l0 = *reinterpret_cast<const uint4*>(st.b + lo.b[2] + db);
-    const uint4 l1 = *reinterpret_cast<const uint4*>(st.b + lo.b[3] + db);
-    const v8i bh = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-    const v8i bl = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
-    const int sbh = st.bs[lo.bs + 16 * ni * 8], sbl = st.bs[lo.bs + 16 * ni * 8 + 4];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      if constexpr (W::FMT == FMT_FP4) {
-        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bh, acc[mi][ni], FMT_FP4, FMT_FP8, 0,
-                                                                       sa[mi], 0, sbh);
-        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bl, acc[mi][ni], FMT_FP4, FMT_FP8, 0,
-                                                                       sa[mi], 0, sbl);
-      } else {
-        v4f blk = {0.0f, 0.0f, 0.0f, 0.0f};
-        blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bh, blk, FMT_FP8, FMT_FP8, 0, 127, 0, sbh);
-        blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bl, blk, FMT_FP8, FMT_FP8, 0, 127, 0, sbl);
-        const float s = bscale(mi);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][ni][r] = fmaf(s, blk[r], acc[mi][ni][r]);
-      }
-    }
-    // one row tile's fragment live at a time (the scheduler would otherwise hoist all four
-    // reads and run out of registers)
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// Per-lane sources of the direct-to-LDS loads of one K step. Split rows: 32 x 1 KB
-// (4 rows each; slot q of wave w is slot w + WAVES q: rows 4 slot + lane / 16, piece
-// (lane % 16) ^ (row & 15)); their scales: 4 x 256 B (slot s = rows 32 s + lane / 2, hi or
-// lo word lane % 2), issued by waves 0-3. Weight rows: TW * STEP_BYTES / 1024 x 1 KB
-// (slot q of wave w is slot w + WAVES q: rows slot * (1024 / STEP_BYTES) + lane / PIECES).
-// MXFP4 scales: TW / 64 x 256 B (slot w + WAVES q: weight rows 64 slot + lane). Only 4-
-// and 16-byte loads (their lane layout is the documented base + size * lane). Offsets
-// are taken at K step 0; step ks adds ks * CHUNK, ks * 8, ks * STEP_BYTES and ks * 4.
-template <typename W>
-struct Loader {
-  static constexpr int BQ = 32 / W::WAVES;                                   // split-row loads per wave
-  static constexpr int AQ = W::TW * W::STEP_BYTES / 1024 / W::WAVES;         // weight loads per wave
-  static constexpr int SQ = W::FMT == FMT_FP4 ? W::TW / 64 / W::WAVES : 0;   // MXFP4 scale loads per wave
-  const uint8_t* b;              // split operand [rows][chunks][CHUNK]
-  const uint8_t* bsc;            // its scales [rows][chunks][8]
-  const uint8_t* wbase;          // the tile's weight region (wave-uniform)
-  const uint8_t* sbase;          // its MXFP4 scale region (wave-uniform)
-  uint32_t boff[BQ];
-  uint32_t bsoff;
-  uint32_t aoff[AQ];             // byte offsets from wbase
-  uint32_t soff[SQ > 0 ? SQ : 1];
-
-  // row_b(r): split-operand row of tile row r; row_w(j): byte offset from wbase of tile
-  // weight row j; row_s(j): byte offset from sbase of its MXFP4 scale row.
-  template <typename RowB, typename RowW, typename RowS>
-  __device__ __forceinline__ void init(const uint8_t* b_, const uint8_t* bsc_, int chunks, const uint8_t* wbase_,
-                                       const uint8_t* sbase_, RowB row_b, RowW row_w, RowS row_s) {
-    const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
-    b = uniform_u8(b_);
-    bsc = uniform_u8(bsc_);
-    wbase = uniform_u8(wbase_);
-    sbase = uniform_u8(sbase_);
-#pragma unroll
-    for (int q = 0; q < BQ; ++q) {
-      const int r = 4 * (w + W::WAVES * q) + lane / 16;
-      boff[q] = (uint32_t)row_b(r) * (uint32_t)(chunks * CHUNK) + 16u * (uint32_t)((lane % 16) ^ (r & 15));
-    }
-    bsoff = (uint32_t)row_b((32 * w + lane / 2) & (BM - 1)) * (uint32_t)(chunks * 8) + 4u * (uint32_t)(lane % 2);
-    constexpr int RPI = 1024 / W::STEP_BYTES;  // weight rows per 1 KB load
-#pragma unroll
-    for (int q = 0; q < AQ; ++q) {
-      const int j = (w + W::WAVES * q) * RPI + lane / W::PIECES;
-      aoff[q] = row_w(j) + 16u * (uint32_t)((lane % W::PIECES) ^ W::swz(j));
-    }
-#pragma unroll
-    for (int q = 0; q < SQ; ++q) soff[q] = row_s(64 * (w + W::WAVES * q) + lane);
-  }
-
-  __device__ __forceinline__ void issue(Stage<W>& st, int ks) {
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-#pragma unroll
-    for (int q = 0; q < BQ; ++q) dma16(b, boff[q] + (uint32_t)ks * CHUNK, lds_addr(st.b + (w + W::WAVES * q) * 1024));
-#pragma unroll
-    for (int q = 0; q < AQ; ++q)
-      dma16(wbase, aoff[q] + (uint32_t)(ks * W::STEP_BYTES), lds_addr(st.a + (w + W::WAVES * q) * 1024));
-    if (w < 4) dma4(bsc, bsoff + (uint32_t)ks * 8, lds_addr(st.bs + 256 * w));
-#pragma unroll
-    for (int q = 0; q < SQ; ++q) dma4(sbase, soff[q] + (uint32_t)ks * 4, lds_addr(st.as + 256 * (w + W::WAVES * q)));
-  }
-};
 
 // Wait until this wave's loads have landed and its LDS reads have returned, then let every
 // wave see every wave's loads. One asm statement, so no LDS access is scheduled across
@@ -461,277 +180,11 @@ struct TileWeights {
   float limit;
 };
 
-__device__ __forceinline__ TileWeights tile_weights(const wm_mxfp4_experts& routed, const wm_mxfp4_experts& shared,
-                                                    int expert) {
-  const wm_mxfp4_experts& t = expert < 0 ? shared : routed;
-  const ExpertRegions r = expert_regions(t, expert < 0 ? 0 : expert);
-  return {r.gate_up, r.gate_up_scales, r.down, r.down_scales, t.up_first, t.swiglu_limit};
-}
-__device__ __forceinline__ TileWeights tile_weights(const wm_fp8_experts& routed, const wm_fp8_experts& shared,
-                                                    int expert) {
-  const wm_fp8_experts& t = expert < 0 ? shared : routed;
-  const Fp8Regions r = fp8_regions(t, expert < 0 ? 0 : expert);
-  return {r.w13, reinterpret_cast<const uint8_t*>(r.w13_scales), r.w2, reinterpret_cast<const uint8_t*>(r.w2_scales),
-          t.up_first, t.swiglu_limit};
-}
-
-// E4M3 hi/lo terms of 4 act values (already times 2^(127 - s)) into bytes 0..3 of hi, lo.
-__device__ __forceinline__ void act_terms(float v0, float v1, float v2, float v3, uint32_t& hi, uint32_t& lo) {
-  const uint32_t w01 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
-  const uint32_t w23 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, 0, false);
-  const float l0 = (v0 - e4m3_byte0(w01)) * 16.0f, l1 = (v1 - e4m3_byte1(w01)) * 16.0f;
-  const float l2 = (v2 - e4m3_byte0(w23)) * 16.0f, l3 = (v3 - e4m3_byte1(w23)) * 16.0f;
-  hi = (w01 & 0xffffu) | (w23 << 16);
-  lo = ((uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(l0, l1, 0, false) & 0xffffu) |
-       ((uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(l2, l3, 0, false) << 16);
-}
-
 // ---------------------------------------------------------------------------------
-// gate_up: act rows of a tile's TW / 2 intermediate columns. Weight tile rows [0, TW/2)
-// are the gate rows nt * TW/2 + j, [TW/2, TW) the matching up rows; wave wn owns gate rows
-// 64 wn + [0, 64) (mi 0..3) and the same up rows (mi 4..7). When I is not a multiple of
-// TW / 2, the last tile's columns past I are computed on repeated rows and not written.
-
-template <typename W>
-struct GateUpTile {
-  Loader<W> ld;
-  int begin, end, nt, valid;
-  float limit;
-  const_f32_ptr sg, su;   // FP8 block scales of the wave's gate and up rows (per K step)
-};
-
-template <typename W, typename Table>
-__global__ void __launch_bounds__(64 * W::WAVES) gate_up_kernel(const uint8_t* __restrict__ x8,
-                                                                const uint8_t* __restrict__ xs, Lists L,
-                                                                Table routed, Table shared, uint8_t* __restrict__ a8,
-                                                                uint8_t* __restrict__ as8) {
-  constexpr int TG = W::TW / 2;  // gate (and up) rows per tile
-  const int H = routed.hidden, I = routed.inter;
-  const int n_tiles = (I + TG - 1) / TG;
-  const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int wm = wave & 1, wn = wave >> 1;
-  const LaneOffsets lo = lane_offsets<W>(64 * wn, wm);
-  const int64_t wrow_bytes = (int64_t)H * W::STEP_BYTES / 128;
-  using Tile = GateUpTile<W>;
-
-  auto setup = [&](int j, Tile& t) {
-    const int logical = tr.first + tr.stride * j;
-    const int mt = logical / n_tiles;
-    t.nt = logical - mt * n_tiles;
-    int expert, begin_, end_;
-    if (!resolve_tile(L, mt, expert, begin_, end_)) return false;
-    t.begin = uniform_i(begin_);
-    t.end = uniform_i(end_);
-    const TileWeights tw = tile_weights(routed, shared, uniform_i(expert));
-    t.limit = uniform_f(tw.limit);
-    t.valid = min(TG, I - t.nt * TG);  // a multiple of 128
-    const int gate0 = (tw.up_first ? I : 0) + t.nt * TG;
-    const int up0 = (tw.up_first ? 0 : I) + t.nt * TG;
-    const int valid = t.valid;
-    auto weight_row = [gate0, up0, valid](int r) {
-      const int rr = r % TG;
-      return (r < TG ? gate0 : up0) + (rr < valid ? rr : rr % valid);
-    };
-    const int begin = t.begin, end = t.end;
-    auto token_of = [&](int pr) { return pr < L.pairs ? L.order[pr] / L.k : pr - L.pairs; };
-    t.ld.init(
-        x8, xs, H / 128, tw.w13, tw.w13s,
-        // pad rows repeat the tile's first row; their results are never written
-        [&](int r) { return token_of(begin + r < end ? begin + r : begin); },
-        [&](int r) { return (uint32_t)(weight_row(r) * wrow_bytes); },
-        [&](int r) { return (uint32_t)(weight_row(r) * (H / 32)); });
-    // FP8: the wave's 64 gate (up) rows lie in one 128-row scale block
-    t.sg = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(weight_row(64 * wn) / 128) * (H / 128));
-    t.su = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(weight_row(TG + 64 * wn) / 128) * (H / 128));
-    return true;
-  };
-
-  v4f acc[MI][NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-  auto mfma = [&](const Tile& t, const Stage<W>& st, int k) {
-    step_mfma<W>(st, lo, acc, [](int mi) { return (mi < 4 ? 0 : TG) + 16 * (mi & 3); },
-                 [&](int mi) { return W::FMT == FMT_FP8 ? (mi < 4 ? t.sg[k] : t.su[k]) : 1.0f; });
-  };
-
-  // Epilogue: lane holds act columns col0 + 16 mi + 4 g + r (mi 0..3) of row
-  // 64 wm + 16 ni + c, col0 = nt * TG + 64 wn: 128-wide act chunk col0 / 128, K offset
-  // kin0 = col0 % 128 (0 or 64). E8M0 block (kin0 + 32 half) / 32 holds mi 2 half, 2 half + 1.
-  auto epilogue = [&](const Tile& t, Stage<W>&) {
-    if (64 * wn < t.valid) {
-      const int c = lane % 16, g = lane / 16;
-      const int chunks = I / 128;
-      const int col0 = t.nt * TG + 64 * wn;
-      const int chunk = col0 / 128, kin0 = col0 % 128;
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        const int row = t.begin + 64 * wm + 16 * ni + c;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          float h[2][4];
-          float amax = 0.0f;
-#pragma unroll
-          for (int m = 0; m < 2; ++m)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int mi = 2 * half + m;
-              float gv = acc[mi][ni][r], uv = acc[mi + 4][ni][r];
-              if (t.limit > 0.0f) {
-                gv = fminf(gv, t.limit);
-                uv = fminf(fmaxf(uv, -t.limit), t.limit);
-              }
-              h[m][r] = silu(gv) * uv;
-              amax = fmaxf(amax, fabsf(h[m][r]));
-            }
-          amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-          amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-          if (row >= t.end) continue;
-          const int s = term_exponent(amax);
-          const float f = pow2_biased(254 - s);
-          uint8_t* dst = a8 + ((int64_t)row * chunks + chunk) * CHUNK;
-#pragma unroll
-          for (int m = 0; m < 2; ++m) {
-            uint32_t hi, lo_;
-            act_terms(h[m][0] * f, h[m][1] * f, h[m][2] * f, h[m][3] * f, hi, lo_);
-            // K = kin0 + 32 half + 16 m + 4 g + r -> B-operand position 32 (K/16 % 4) + 16 (K/64) + K % 16
-            const int K = kin0 + 32 * half + 16 * m + 4 * g;
-            const int pos = 32 * ((K >> 4) & 3) + 16 * (K >> 6) + (K & 15);
-            *reinterpret_cast<uint32_t*>(dst + pos) = hi;
-            *reinterpret_cast<uint32_t*>(dst + 128 + pos) = lo_;
-          }
-          if (g == 0) {
-            const int blk = (kin0 >> 5) + half;
-            uint8_t* sd = as8 + ((int64_t)row * chunks + chunk) * 8;
-            sd[blk] = (uint8_t)s;
-            sd[4 + blk] = (uint8_t)(s > 4 ? s - 4 : 0);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  };
-
-  __shared__ Stage<W> s0, s1;
-  persistent_tiles<Tile>(tr, H / 128, s0, s1, setup, mfma, epilogue);
-}
-
-// ---------------------------------------------------------------------------------
-// down: out[row, n] = w(row) * act[row] . W2[n], bf16, permuted rows; tile = 128 rows x
-// TW output columns, wave wn owns columns 128 wn + [0, 128). When H is not a multiple of
-// TW, the last tile's columns past H are computed on repeated rows and not written.
-
-template <typename W>
-struct DownTile {
-  Loader<W> ld;
-  int begin, end, nt, valid;
-  int slot;               // LDS slot of the tile's row weights (tiles alternate)
-  const_f32_ptr sd;       // FP8 block scales of the wave's 128 columns (per K step)
-};
-
-template <typename W, typename Table>
-__global__ void __launch_bounds__(64 * W::WAVES) down_kernel(const uint8_t* __restrict__ a8,
-                                                             const uint8_t* __restrict__ as8, Lists L,
-                                                             const float* __restrict__ weights, int weighted,
-                                                             Table routed, Table shared, uint16_t* __restrict__ out) {
-  const int H = routed.hidden, I = routed.inter;
-  const int n_tiles = (H + W::TW - 1) / W::TW;
-  const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int wm = wave & 1, wn = wave >> 1;
-  const LaneOffsets lo = lane_offsets<W>(128 * wn, wm);
-  const int64_t wrow_bytes = (int64_t)I * W::STEP_BYTES / 128;
-  using Tile = DownTile<W>;
-  __shared__ float row_weight[2][BM];
-
-  auto setup = [&](int j, Tile& t) {
-    const int logical = tr.first + tr.stride * j;
-    const int mt = logical / n_tiles;
-    t.nt = logical - mt * n_tiles;
-    int expert, begin_, end_;
-    if (!resolve_tile(L, mt, expert, begin_, end_)) return false;
-    t.begin = uniform_i(begin_);
-    t.end = uniform_i(end_);
-    const TileWeights tw = tile_weights(routed, shared, uniform_i(expert));
-    t.valid = min(W::TW, H - t.nt * W::TW);  // a multiple of 128
-    const int nt = t.nt, valid = t.valid, begin = t.begin, end = t.end;
-    auto col_row = [nt, valid](int r) { return nt * W::TW + (r < valid ? r : r % valid); };  // never past H
-    t.ld.init(
-        a8, as8, I / 128, tw.w2, tw.w2s, [&](int r) { return begin + r < end ? begin + r : begin; },
-        [&](int r) { return (uint32_t)(col_row(r) * wrow_bytes); },
-        [&](int r) { return (uint32_t)(col_row(r) * (I / 32)); });
-    // routing weight (or shared gate) of the tile's rows, kept in LDS until the epilogue (at
-    // least one barrier later; the two slots alternate between consecutive tiles)
-    t.slot = j & 1;
-    if (threadIdx.x < BM) {
-      const int row = begin + (int)threadIdx.x;
-      float w = 1.0f;
-      if (weighted && row < end) w = row < L.pairs ? weights[L.order[row]] : L.shared_gate[row - L.pairs];
-      row_weight[t.slot][threadIdx.x] = w;
-    }
-    // FP8: the wave's 128 columns are one 128-row scale block
-    t.sd = uniform_ptr(reinterpret_cast<const float*>(tw.w2s) + (int64_t)(col_row(128 * wn) / 128) * (I / 128));
-    return true;
-  };
-
-  v4f acc[MI][NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-  auto mfma = [&](const Tile& t, const Stage<W>& st, int k) {
-    step_mfma<W>(st, lo, acc, [](int mi) { return 16 * mi; },
-                 [&](int) { return W::FMT == FMT_FP8 ? t.sd[k] : 1.0f; });
-  };
-
-  // lane holds output columns nt*TW + 128 wn + 16 mi + 4 g + r of row 64 wm + 16 ni + c
-  auto epilogue = [&](const Tile& t, Stage<W>&) {
-    if (128 * wn < t.valid) {
-      const int c = lane % 16, g = lane / 16;
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        const int row = t.begin + 64 * wm + 16 * ni + c;
-        if (row >= t.end) continue;
-        const float w = row_weight[t.slot][64 * wm + 16 * ni + c];
-#pragma unroll
-        for (int mi = 0; mi < MI; ++mi) {
-          const int col = t.nt * W::TW + 128 * wn + 16 * mi + 4 * g;
-          uint2 o;
-          o.x = f32_to_bf16_bits(w * acc[mi][ni][0]) | ((uint32_t)f32_to_bf16_bits(w * acc[mi][ni][1]) << 16);
-          o.y = f32_to_bf16_bits(w * acc[mi][ni][2]) | ((uint32_t)f32_to_bf16_bits(w * acc[mi][ni][3]) << 16);
-          *reinterpret_cast<uint2*>(out + (int64_t)row * H + col) = o;
-        }
-      }
-    }
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  };
-
-  __shared__ Stage<W> s0, s1;
-  persistent_tiles<Tile>(tr, I / 128, s0, s1, setup, mfma, epilogue);
-}
-
-// ---------------------------------------------------------------------------------
-// MXFP4 weights on v_mfma_scale_f32_32x32x64_f8f6f4 with the activations as two E2M3
-// (fp6) terms. This MFMA shape runs fp4 x fp6 at twice the rate of any fp8 operand
-// (measured on MI355X: 33 against 64 cycles per instruction; the 16x16x128 shape runs
-// every format at the fp8 rate).
-//
-// Operand layout (32 x 32 x 64; lane l, r = l % 32, g = l / 32):
-//   fp4 operand: lane holds row r's K values [32g, 32g+32) as nibbles (low first), 16 bytes;
-//   fp6 operand: lane holds row r's K values [32g, 32g+32) as 32 contiguous 6-bit fields
-//                (bit 6f of the lane's 24 bytes is K value 32g + f), 24 bytes;
-//   scale     : lane (r, g) gives the E8M0 scale of row r, K block g;
-//   result    : lane holds D[8 (i / 4) + 4 g + i % 4][r] in its register i (16 registers).
+// Activations as two E2M3 (fp6) terms. On v_mfma_scale_f32_32x32x64_f8f6f4 fp4 x fp6 runs
+// at twice the rate of any fp8 operand (measured on MI355X: 32 against 64 cycles per
+// instruction), and fp8 x fp6 at the fp8 rate (the 16x16x128 shape runs every format at
+// the fp8 rate).
 //
 // Terms: a 32-value block gets hi = e2m3(x / 2^(s - 127)) with s = e(max |x|) - 2, so the
 // block maximum lands in [4, 8); the residual x - hi (exact in fp32) gets its own block
@@ -848,18 +301,23 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
 }
 
 // ---------------------------------------------------------------------------------
-// Prefill tile layout of MXFP4 weights (one expert region; rows R, K values per row):
-//   weights [K/128 steps][R/16 groups][4 pieces][16 rows][16 bytes]: piece p of a row's step
-//           is its bytes [16p, 16p + 16) of the 64 the step takes in the row layout;
-//   scales  [K/128 steps][R rows][4 bytes]: the row's 4 E8M0 bytes of the step.
+// Prefill tile layout of expert weights (one expert region; rows R, K values per row, P
+// 16-byte pieces per row and 128-wide K step: MXFP4 4, FP8 8):
+//   weights [K/128 steps][R/16 groups][P pieces][16 rows][16 bytes]: piece p of a row's step
+//           is its bytes [16p, 16p + 16) of the 16 P the step takes in the row layout;
+//   MXFP4 scales [K/128 steps][R rows][4 bytes]: the row's 4 E8M0 bytes of the step;
+//   FP8 block scales [R/128][K/128] fp32, copied unchanged.
 // One 16-byte piece (or one 4-byte scale word) per thread.
+template <int P>
 __global__ void __launch_bounds__(256) repack_prefill_kernel(const uint8_t* __restrict__ src,
                                                              const uint8_t* __restrict__ src_s, int64_t stride,
                                                              int64_t stride_s, const int32_t* __restrict__ slots,
                                                              int experts, int rows, int k, uint8_t* __restrict__ dst,
                                                              uint8_t* __restrict__ dst_s) {
-  const int64_t pieces = (int64_t)rows * (k / 32);  // 16-byte pieces per expert
-  const int64_t words = (int64_t)rows * (k / 128);  // scale words per expert
+  const int64_t row_pieces = (int64_t)(k / 128) * P;   // 16-byte pieces per row
+  const int64_t row_bytes = 16 * row_pieces;
+  const int64_t pieces = (int64_t)rows * row_pieces;   // per expert
+  const int64_t words = (int64_t)(P == 4 ? rows : rows / 128) * (k / 128);  // scale words per expert
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)experts * (pieces + words)) return;
   const int e = (int)(i / (pieces + words));
@@ -867,34 +325,25 @@ __global__ void __launch_bounds__(256) repack_prefill_kernel(const uint8_t* __re
   int64_t slot = slots ? slots[e] : e;
   if (slot < 0) slot = 0;
   if (j < pieces) {
-    const int64_t row = j / (k / 32);
-    const int pr = (int)(j % (k / 32)), step = pr / 4, p = pr % 4;
-    const uint4 v = *reinterpret_cast<const uint4*>(src + slot * stride + row * (k / 2) + 16 * pr);
-    *reinterpret_cast<uint4*>(dst + (int64_t)e * rows * (k / 2) + (int64_t)step * rows * 64 + (row / 16) * 1024 +
+    const int64_t row = j / row_pieces;
+    const int64_t pr = j % row_pieces;
+    const int64_t step = pr / P, p = pr % P;
+    const uint4 v = *reinterpret_cast<const uint4*>(src + slot * stride + row * row_bytes + 16 * pr);
+    *reinterpret_cast<uint4*>(dst + (int64_t)e * rows * row_bytes + step * rows * (16 * P) + (row / 16) * (256 * P) +
                               p * 256 + (row % 16) * 16) = v;
-  } else {
+  } else if (P == 4) {
     const int64_t w = j - pieces;
     const int64_t row = w / (k / 128);
     const int step = (int)(w % (k / 128));
     const uint32_t v = *reinterpret_cast<const uint32_t*>(src_s + slot * stride_s + row * (k / 32) + 4 * step);
     *reinterpret_cast<uint32_t*>(dst_s + (int64_t)e * rows * (k / 32) + (int64_t)step * rows * 4 + row * 4) = v;
+  } else {
+    const int64_t w = j - pieces;
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(src_s + slot * stride_s + 4 * w);
+    *reinterpret_cast<uint32_t*>(dst_s + 4 * ((int64_t)e * words + w)) = v;
   }
 }
 
-// ---------------------------------------------------------------------------------
-// Grouped GEMMs for MXFP4 weights. A workgroup computes a 128-row x 512-weight-row tile
-// with 8 waves: wave w = (wm, wn) = (w & 1, w >> 1) owns 64 rows (2 tiles of 32) and
-// 4 weight tiles of 32 rows. Each 128-wide K step's operands go straight from global memory
-// into LDS (global_load_lds: lane i of a wave writes LDS base + 16 i) in a ring of two
-// stages; step k + 1's loads are issued when step k starts.
-//
-// LDS stage:
-//   split rows: 256 bytes per row, piece p of the row's 208-byte step in slot p ^ (row & 15)
-//     (the 16 rows a ds_read_b128 phase serves fall on distinct banks); one load takes 4
-//     rows (lane: row 4q + lane / 16, slot lane % 16), so each row's step arrives as one run;
-//   weight rows: 16-row groups [4 pieces][16 rows][16 bytes], one load per group: in the
-//     tile layout one contiguous KB, in the row layout 64 contiguous bytes of each row;
-//   weight scales: one dword per row (its 4 E8M0 bytes of the step).
 // A uniform int32 read through the scalar cache (data written by an earlier launch).
 __device__ __forceinline__ int32_t scalar_i32(const int32_t* p, int idx) {
   typedef const __attribute__((address_space(4))) int32_t* cptr;
@@ -934,37 +383,65 @@ __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& ro
           t.up_first, t.swiglu_limit};
 }
 
-struct TileWeightsRegion {
-  const uint8_t* w;  // weight region of the expert
-  const uint8_t* s;  // its scale region
+// ---------------------------------------------------------------------------------
+// Grouped GEMMs on v_mfma_scale_f32_32x32x64_f8f6f4 against the E2M3 split rows, for
+// MXFP4 weights (Mx4: fp4 x fp6 at twice the FP8 rate) and FP8-E4M3 weights with fp32
+// 128 x 128 block scales (Mx8: fp8 x fp6 at the FP8 rate). A workgroup computes a 128-row
+// x TW-weight-row tile with 8 waves: wave w = (wm, wn) = (w & 1, w >> 1) owns 64 rows
+// (2 tiles of 32) and MI weight tiles of 32 rows. Each 128-wide K step's operands go
+// straight from global memory into LDS (global_load_lds: lane i of a wave writes LDS
+// base + 16 i) in a ring of two stages; step k + 1's loads are issued when step k starts.
+//
+// LDS stage:
+//   split rows: 256 bytes per row, piece p of the row's 208-byte step in slot p ^ (row & 15)
+//     (the 16 rows a ds_read_b128 phase serves fall on distinct banks); one load takes 4
+//     rows (lane: row 4q + lane / 16, slot lane % 16), so each row's step arrives as one run;
+//   weight rows: 16-row groups [PIECES][16 rows][16 bytes], a row's step being PIECES
+//     16-byte pieces (fp4: 4, fp8: 8); one load fills 4 pieces of a group: in the prefill
+//     tile layout one contiguous KB, in the row layout 64 contiguous bytes of each row;
+//   MXFP4 weight scales: one dword per row (its 4 E8M0 bytes of the step). FP8 block scales
+//     are one float per wave and step, read through the scalar cache.
+//
+// Operand layouts (32 x 32 x 64; lane l, r = l % 32, g = l / 32):
+//   fp4 A: row r's K [32g, 32g + 32) as nibbles, 16 bytes;
+//   fp8 A: row r's K [16g, 16g + 16) in bytes 0-15 and [32 + 16g, 32 + 16g + 16) in 16-31;
+//   fp6 B: row r's K [32g, 32g + 32) as contiguous 6-bit fields, 24 bytes;
+//   scale lane (r, g): K block g; result register i: D[8 (i / 4) + 4 g + i % 4][r].
+struct Mx4 {
+  static constexpr bool FP8 = false;
+  static constexpr int TW = 512, MI = 4, PIECES = 4, A_FMT = FMT_FP4;
 };
-
-constexpr int TW4 = 512;
+struct Mx8 {
+  static constexpr bool FP8 = true;
+  static constexpr int TW = 256, MI = 2, PIECES = 8, A_FMT = FMT_FP8;
+};
 constexpr int WAVES4 = 8;
-constexpr int MI4 = 4;      // 32-row weight tiles per wave
 constexpr int NI4 = 2;      // 32-row row tiles per wave
 
-struct Stage4 {
+template <typename F>
+struct StageMx {
   __attribute__((aligned(16))) uint8_t b[BM * 256];
-  __attribute__((aligned(16))) uint8_t a[TW4 * 64];
-  __attribute__((aligned(16))) uint8_t as[TW4 * 4];
+  __attribute__((aligned(16))) uint8_t a[F::TW * F::PIECES * 16];
+  __attribute__((aligned(16))) uint8_t as[F::FP8 ? 16 : F::TW * 4];
 };
 
 // Per-lane LDS read offsets. Weight tile mi of the wave is rows wave_row0 + mrow(mi) + r
 // (multiples of 32 plus the lane's row); row tile ni is rows 64 wm + 32 ni + r. Half h of
 // the step is K [64h, 64h + 64); the lane's K block in it is 2h + g.
-struct Lane4 {
-  uint32_t a;        // + 64 mrow(mi) + 512 h
+template <typename F>
+struct LaneMx {
+  uint32_t a;        // + 16 PIECES mrow(mi) + (fp4: 512, fp8: 1024) h; fp8 second piece + 512
   uint32_t as;       // + 4 mrow(mi)
   uint32_t b[2][3];  // [h][piece of the lane's 48 bytes] + 8192 ni
   uint32_t bs;       // the row's scale piece (bytes 192..207 of the step) + 8192 ni
   uint32_t shift;    // 8 g
 };
 
-__device__ __forceinline__ Lane4 lane4(int wave_row0, int wm) {
+template <typename F>
+__device__ __forceinline__ LaneMx<F> lane_mx(int wave_row0, int wm) {
   const int lane = threadIdx.x % 64, r = lane % 32, g = lane / 32;
-  Lane4 o;
-  o.a = (uint32_t)((wave_row0 / 16 + r / 16) * 1024 + 256 * g + 16 * (r % 16));
+  LaneMx<F> o;
+  o.a = (uint32_t)((wave_row0 / 16 + r / 16) * (F::PIECES * 256) + 256 * g + 16 * (r % 16));
   o.as = (uint32_t)(4 * (wave_row0 + r));
   const int row = 64 * wm + r, z = r & 15;
 #pragma unroll
@@ -976,25 +453,46 @@ __device__ __forceinline__ Lane4 lane4(int wave_row0, int wm) {
   return o;
 }
 
-// One 128-wide K step of the wave's sub-tile. Per half: the 4 A fragments, then per row
-// tile its hi B fragment feeds 4 MFMAs and its lo fragment 4 more, so no MFMA waits on the
-// one before it.
-template <typename MRow>
-__device__ __forceinline__ void step4(const Stage4& st, const Lane4& lo, v16f (&acc)[MI4][NI4], MRow mrow) {
-  uint32_t sa[MI4];
+// One 128-wide K step of the wave's sub-tile. Per half: the MI A fragments, then per row
+// tile its hi B fragment feeds MI MFMAs and its lo fragment MI more, so no MFMA waits on
+// the one before it. FP8 accumulates the step in blk and adds it times its block scale
+// bscale(mi) (the fp32 scale cannot ride on the MFMA's E8M0 scales).
+template <typename F, typename MRow, typename BScale>
+__device__ __forceinline__ void step_mx(const StageMx<F>& st, const LaneMx<F>& lo, v16f (&acc)[F::MI][NI4], MRow mrow,
+                                        BScale bscale) {
+  constexpr int MI = F::MI;
+  uint32_t sa[MI];
   uint2 sb[NI4];
+  if constexpr (!F::FP8) {
 #pragma unroll
-  for (int mi = 0; mi < MI4; ++mi) sa[mi] = *reinterpret_cast<const uint32_t*>(st.as + lo.as + 4 * mrow(mi));
+    for (int mi = 0; mi < MI; ++mi) sa[mi] = *reinterpret_cast<const uint32_t*>(st.as + lo.as + 4 * mrow(mi));
+  }
 #pragma unroll
   for (int ni = 0; ni < NI4; ++ni) sb[ni] = *reinterpret_cast<const uint2*>(st.b + lo.bs + 8192 * ni);
+  v16f blk[F::FP8 ? MI : 1][NI4];
+  if constexpr (F::FP8) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI4; ++ni)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) blk[mi][ni][i] = 0.0f;
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const uint32_t sh = lo.shift + 16u * (uint32_t)h;
-    v8i a[MI4];
+    v8i a[MI];
 #pragma unroll
-    for (int mi = 0; mi < MI4; ++mi) {
-      const uint4 v = *reinterpret_cast<const uint4*>(st.a + lo.a + 64 * mrow(mi) + 512 * h);
-      a[mi] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+    for (int mi = 0; mi < MI; ++mi) {
+      if constexpr (F::FP8) {
+        const uint8_t* p = st.a + lo.a + 128 * mrow(mi) + 1024 * h;
+        const uint4 v0 = *reinterpret_cast<const uint4*>(p);
+        const uint4 v1 = *reinterpret_cast<const uint4*>(p + 512);
+        a[mi] = v8i{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(st.a + lo.a + 64 * mrow(mi) + 512 * h);
+        a[mi] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+      }
     }
 #pragma unroll
     for (int ni = 0; ni < NI4; ++ni) {
@@ -1004,23 +502,46 @@ __device__ __forceinline__ void step4(const Stage4& st, const Lane4& lo, v16f (&
       const v8i bh = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, 0, 0};
       const v8i bl = {(int)b1.z, (int)b1.w, (int)b2.x, (int)b2.y, (int)b2.z, (int)b2.w, 0, 0};
       const int sbh = (int)(sb[ni].x >> sh), sbl = (int)(sb[ni].y >> sh);
+      if constexpr (F::FP8) {
 #pragma unroll
-      for (int mi = 0; mi < MI4; ++mi)
-        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
-                                                                      (int)(sa[mi] >> sh), 0, sbh);
+        for (int mi = 0; mi < MI; ++mi)
+          blk[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, blk[mi][ni], FMT_FP8, FMT_FP6, 0,
+                                                                        127, 0, sbh);
 #pragma unroll
-      for (int mi = 0; mi < MI4; ++mi)
-        acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
-                                                                      (int)(sa[mi] >> sh), 0, sbl);
+        for (int mi = 0; mi < MI; ++mi)
+          blk[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, blk[mi][ni], FMT_FP8, FMT_FP6, 0,
+                                                                        127, 0, sbl);
+      } else {
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
+                                                                        (int)(sa[mi] >> sh), 0, sbh);
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
+                                                                        (int)(sa[mi] >> sh), 0, sbl);
+      }
       __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if constexpr (F::FP8) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const float s = bscale(mi);
+#pragma unroll
+      for (int ni = 0; ni < NI4; ++ni)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mi][ni][i] = fmaf(s, blk[mi][ni][i], acc[mi][ni][i]);
     }
   }
 }
 
-// Per-lane sources of one K step's loads (9 per wave): split rows, loads q = w + 8i
-// (i = 0..3), rows 4q + lane / 16; weight groups q = w + 8i; weight scales rows 64 w + lane.
-// Offsets are taken at step 0; step ks adds ks * XSTEP, ks * a_step and ks * s_step.
-struct Loader4 {
+// Per-lane sources of one K step's loads: split rows, loads q = w + 8i (i = 0..3), rows
+// 4q + lane / 16; weights, loads q = w + 8i (fp4: group q; fp8: group q / 2, pieces
+// 4 (q % 2)..); MXFP4 scales, rows 64 w + lane. Offsets are taken at step 0; step ks adds
+// ks * XSTEP, ks * a_step and ks * s_step.
+template <typename F>
+struct LoaderMx {
   const uint8_t* b;
   const uint8_t* wbase;
   const uint8_t* sbase;
@@ -1029,7 +550,7 @@ struct Loader4 {
   uint32_t soff;
   uint32_t a_step, s_step;
 
-  __device__ __forceinline__ void issue(Stage4& st, int ks) {
+  __device__ __forceinline__ void issue(StageMx<F>& st, int ks) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -1037,13 +558,13 @@ struct Loader4 {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(st.a + (w + WAVES4 * i) * 1024));
-    dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(st.as + 256 * w));
+    if constexpr (!F::FP8) dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(st.as + 256 * w));
   }
 };
 
-// The split-row part of a loader: row_off(r) is the byte offset of tile row r's split row.
-template <typename RowOff>
-__device__ __forceinline__ void split_row_offsets(Loader4& ld, RowOff row_off) {
+// The split-row part of a loader: row_off(i, r) is the byte offset of tile row r's split row.
+template <typename F, typename RowOff>
+__device__ __forceinline__ void split_row_offsets(LoaderMx<F>& ld, RowOff row_off) {
   const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -1052,15 +573,33 @@ __device__ __forceinline__ void split_row_offsets(Loader4& ld, RowOff row_off) {
   }
 }
 
-// The weight part: tile rows [0, TW4) are expert rows row_of(j) (multiples of 16 in runs of
+// The weight part: tile rows [0, TW) are expert rows row_of(j) (multiples of 16 in runs of
 // 16, so a tile group is an expert group); rows is the expert region's row count, k its K.
-template <typename RowOf>
-__device__ __forceinline__ void weight_offsets(Loader4& ld, const TileWeightsRegion& tr_, int rows, int k, int tiled,
-                                               RowOf row_of) {
+template <typename F, typename RowOf>
+__device__ __forceinline__ void weight_offsets(LoaderMx<F>& ld, const uint8_t* w_region, const uint8_t* s_region,
+                                               int rows, int k, int tiled, RowOf row_of) {
   const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
-  ld.wbase = uniform_u8(tr_.w);
-  ld.sbase = uniform_u8(tr_.s);
-  if (tiled) {
+  ld.wbase = uniform_u8(w_region);
+  ld.sbase = uniform_u8(s_region);
+  if constexpr (F::FP8) {
+    if (tiled) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = w + WAVES4 * i;
+        ld.aoff[i] = (uint32_t)(row_of(16 * (q / 2)) / 16 * 2048 + 1024 * (q % 2) + 16 * lane);
+      }
+      ld.a_step = (uint32_t)(rows * 128);
+    } else {  // row layout: [rows][k] bytes, 128 per step
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = w + WAVES4 * i;
+        ld.aoff[i] = (uint32_t)(row_of(16 * (q / 2) + lane % 16) * k + 16 * (4 * (q % 2) + lane / 16));
+      }
+      ld.a_step = 128;
+    }
+    ld.soff = 0;
+    ld.s_step = 0;
+  } else if (tiled) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + WAVES4 * i)) / 16 * 1024 + 16 * lane);
     ld.soff = (uint32_t)(row_of(64 * w + lane) * 4);
@@ -1076,15 +615,18 @@ __device__ __forceinline__ void weight_offsets(Loader4& ld, const TileWeightsReg
   }
 }
 
-struct Tile4 {
-  Loader4 ld;
+template <typename F>
+struct TileMx {
+  LoaderMx<F> ld;
   int begin, end, nt, valid;
   float limit;
+  const_f32_ptr s0, s1;  // FP8: block scale rows of the wave's weight tiles (gate / up, or down)
 };
 
-__device__ __forceinline__ void zero_acc4(v16f (&acc)[MI4][NI4]) {
+template <typename F>
+__device__ __forceinline__ void zero_acc(v16f (&acc)[F::MI][NI4]) {
 #pragma unroll
-  for (int mi = 0; mi < MI4; ++mi)
+  for (int mi = 0; mi < F::MI; ++mi)
 #pragma unroll
     for (int ni = 0; ni < NI4; ++ni)
 #pragma unroll
@@ -1096,24 +638,39 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcn
 // This wave's LDS writes are done before its next LDS reads (and its reads before its writes).
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// gate_up: act rows of a tile's 256 intermediate columns; weight tile rows [0, 256) are the
-// gate rows nt * 256 + j, [256, 512) the matching up rows; wave wn owns gate rows
-// 64 wn + [0, 64) (mi 0, 1) and the same up rows (mi 2, 3).
-template <typename Table>
-__global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __restrict__ x6,
-                                                               const int32_t* __restrict__ row_token, Lists L,
-                                                               Table routed, Table shared, uint8_t* __restrict__ a6) {
-  constexpr int TG = TW4 / 2;
+// The expert regions of a tile (scalar loads only).
+__device__ __forceinline__ TileWeights tile_weights_s(const wm_fp8_experts& routed, const wm_fp8_experts& shared,
+                                                      int expert) {
+  const wm_fp8_experts& t = expert < 0 ? shared : routed;
+  const int e = expert < 0 ? 0 : expert;
+  int64_t slot = t.slots ? scalar_i32(t.slots, e) : e;
+  if (slot < 0) slot = 0;
+  return {(const uint8_t*)t.w13 + slot * t.w13_stride, (const uint8_t*)t.w13_scales + slot * t.w13_scales_stride,
+          (const uint8_t*)t.w2 + slot * t.w2_stride, (const uint8_t*)t.w2_scales + slot * t.w2_scales_stride,
+          t.up_first, t.swiglu_limit};
+}
+__device__ __forceinline__ int table_tiled(const wm_mxfp4_experts& t) { return t.tiled; }
+__device__ __forceinline__ int table_tiled(const wm_fp8_experts& t) { return t.tiled; }
+
+// gate_up: act rows of a tile's TG = TW / 2 intermediate columns; weight tile rows [0, TG)
+// are the gate rows nt * TG + j, [TG, TW) the matching up rows; wave wn owns gate rows
+// 32 (MI / 2) wn + [0, 32 MI / 2) (mi < MI / 2) and the same up rows (mi >= MI / 2).
+template <typename F, typename Table>
+__global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* __restrict__ x6,
+                                                                 const int32_t* __restrict__ row_token, Lists L,
+                                                                 Table routed, Table shared, uint8_t* __restrict__ a6) {
+  constexpr int TG = F::TW / 2, MI = F::MI, HM = MI / 2;
   const int H = routed.hidden, I = routed.inter;
   const int n_tiles = (I + TG - 1) / TG;
   const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int wm = wave & 1, wn = wave >> 1;
-  const Lane4 lo = lane4(64 * wn, wm);
+  const LaneMx<F> lo = lane_mx<F>(32 * HM * wn, wm);
   const uint32_t x_row = (uint32_t)(H / 128 * XSTEP);
   const int64_t a_row = (int64_t)(I / 128) * XSTEP;
+  using Tile = TileMx<F>;
 
-  auto setup = [&](int j, Tile4& t) {
+  auto setup = [&](int j, Tile& t) {
     const int logical = tr.first + tr.stride * j;
     const int mt = logical / n_tiles;
     t.nt = logical - mt * n_tiles;
@@ -1122,19 +679,23 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
     t.begin = begin;
     t.end = end;
     const TileWeights tw = tile_weights_s(routed, shared, expert);
-    const Table& tab = expert < 0 ? shared : routed;
     t.limit = tw.limit;
     t.valid = min(TG, I - t.nt * TG);  // a multiple of 128
     const int gate0 = (tw.up_first ? I : 0) + t.nt * TG;
     const int up0 = (tw.up_first ? 0 : I) + t.nt * TG;
     const int valid = t.valid;
-    weight_offsets(t.ld, TileWeightsRegion{tw.w13, tw.w13s}, 2 * I, H, tab.tiled, [gate0, up0, valid](int r) {
-      const int rr = r % TG;
-      return (r < TG ? gate0 : up0) + (rr < valid ? rr : rr % valid);
-    });
+    weight_offsets<F>(t.ld, tw.w13, tw.w13s, 2 * I, H, table_tiled(expert < 0 ? shared : routed),
+                      [gate0, up0, valid](int r) {
+                        const int rr = r % TG;
+                        return (r < TG ? gate0 : up0) + (rr < valid ? rr : rr % valid);
+                      });
+    if constexpr (F::FP8) {  // a wave's gate (up) rows lie in one 128-row scale block
+      t.s0 = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(gate0 / 128) * (H / 128));
+      t.s1 = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(up0 / 128) * (H / 128));
+    }
     t.ld.b = uniform_u8(x6);
     // tokens of this lane's split rows 4q + 0..3 (q = w + 8i), through scalar loads
-    split_row_offsets(t.ld, [&](int i, int r) {
+    split_row_offsets<F>(t.ld, [&](int i, int r) {
       const int q0 = 4 * (__builtin_amdgcn_readfirstlane(threadIdx.x / 64) + WAVES4 * i);
       int tok = 0;
 #pragma unroll
@@ -1148,57 +709,55 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
     return true;
   };
 
-  v16f acc[MI4][NI4];
-  zero_acc4(acc);
-  auto mrow = [](int mi) { return (mi < 2 ? 0 : TG) + 32 * (mi & 1); };
-  auto mfma = [&](const Tile4&, const Stage4& st, int) { step4(st, lo, acc, mrow); };
+  v16f acc[MI][NI4];
+  zero_acc<F>(acc);
+  auto mrow = [](int mi) { return (mi < HM ? 0 : TG) + 32 * (mi % HM); };
+  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k) {
+    step_mx<F>(st, lo, acc, mrow, [&](int mi) { return mi < HM ? t.s0[k] : t.s1[k]; });
+  };
 
   // Epilogue: lane (r, half) holds act rows 8 j + 4 half + q (j, q = 0..3; register 4 j + q)
-  // of 32-column block kb = 2 wn + b of the tile (b = 0, 1: gate mi b, up mi b + 2) for row
-  // 64 wm + 32 ni + r. After one swap between the lane halves each lane holds a whole block
-  // (half 0 block b = 0, half 1 block b = 1), forms its two terms and writes them with the
-  // scales into the consumed stage as the tile's act rows (416 bytes: 2 steps), which all
-  // threads then copy out row by row.
-  auto epilogue = [&](const Tile4& t, Stage4& st) {
+  // of a 32-column block for row 64 wm + 32 ni + r. One swap between the lane halves gives
+  // each lane a whole block: for MXFP4 (two gate tiles per wave) blocks 2 wn + half of row
+  // tile ni, for FP8 (one gate tile) block wn of row tile half. The lane forms the block's
+  // two terms and writes them with the scales into the consumed stage as the tile's act
+  // rows (TG / 128 steps of 208 bytes), which all threads then copy out row by row.
+  auto epilogue = [&](const Tile& t, StageMx<F>& st) {
+    constexpr int STG = TG / 128 * XSTEP;  // staged bytes per row
     stage_barrier();
     uint8_t* stg = reinterpret_cast<uint8_t*>(&st);
-    if (64 * wn < t.valid) {
+    if (32 * HM * wn < t.valid) {
       const int r = lane % 32, half = lane / 32;
+      auto act = [&](int b, int ni, int i) {
+        float gv = acc[b][ni][i], uv = acc[b + HM][ni][i];
+        if (t.limit > 0.0f) {
+          gv = fminf(gv, t.limit);
+          uv = fminf(fmaxf(uv, -t.limit), t.limit);
+        }
+        return silu(gv) * uv;
+      };
+      constexpr int PAIRS = HM == 2 ? NI4 : 1;  // MXFP4: one swap per row tile; FP8: one in all
 #pragma unroll
-      for (int ni = 0; ni < NI4; ++ni) {
-        const int lr = 64 * wm + 32 * ni + r;
-        float v[2][16];
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            float gv = acc[b][ni][i], uv = acc[b + 2][ni][i];
-            if (t.limit > 0.0f) {
-              gv = fminf(gv, t.limit);
-              uv = fminf(fmaxf(uv, -t.limit), t.limit);
-            }
-            v[b][i] = silu(gv) * uv;
-          }
-        // v_permlane32_swap(block 0, block 1): lanes of half 0 then hold all of block 0 and
-        // lanes of half 1 all of block 1, in K order (rows 8 j + q from the first result, rows
-        // 8 j + 4 + q from the second)
+      for (int pi = 0; pi < PAIRS; ++pi) {
         float full[32];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0][i]), __float_as_uint(v[1][i]), false,
-                                                           false);
+          const float x0 = HM == 2 ? act(0, pi, i) : act(0, 0, i);
+          const float x1 = HM == 2 ? act(1 % HM, pi, i) : act(0, 1, i);
+          const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
           full[8 * (i / 4) + i % 4] = __uint_as_float(pr[0]);
           full[8 * (i / 4) + 4 + i % 4] = __uint_as_float(pr[1]);
         }
-        v6u_t hi, lo;
+        v6u_t hi, lo6;
         int s_hi, s_lo;
-        fp6_terms32(full, hi, lo, s_hi, s_lo);
-        const int kb = 2 * wn + half;  // this lane's block of the tile: step kb / 4, block kb % 4
-        uint8_t* step = stg + lr * 416 + (kb / 4) * XSTEP;
+        fp6_terms32(full, hi, lo6, s_hi, s_lo);
+        const int lr = HM == 2 ? 64 * wm + 32 * pi + r : 64 * wm + 32 * half + r;
+        const int kb = HM == 2 ? 2 * wn + half : wn;  // block of the tile: step kb / 4, block kb % 4
+        uint8_t* step = stg + lr * STG + (kb / 4) * XSTEP;
         uint4* dst = reinterpret_cast<uint4*>(step + (kb % 4) * 48);
         dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        dst[1] = make_uint4(hi[4], hi[5], lo[0], lo[1]);
-        dst[2] = make_uint4(lo[2], lo[3], lo[4], lo[5]);
+        dst[1] = make_uint4(hi[4], hi[5], lo6[0], lo6[1]);
+        dst[2] = make_uint4(lo6[2], lo6[3], lo6[4], lo6[5]);
         step[192 + kb % 4] = (uint8_t)s_hi;
         step[196 + kb % 4] = (uint8_t)s_lo;
       }
@@ -1208,30 +767,33 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up4_kernel(const uint8_t* __
     const int n = (t.end - t.begin) * chunks;
     for (int idx = threadIdx.x; idx < n; idx += 64 * WAVES4) {
       const int lr = idx / chunks, c = idx - lr * chunks;
-      const uint4 v = *reinterpret_cast<const uint4*>(stg + lr * 416 + 16 * c);
-      *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(2 * t.nt) * XSTEP + 16 * c) = v;
+      const uint4 v4 = *reinterpret_cast<const uint4*>(stg + lr * STG + 16 * c);
+      *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(t.nt * TG / 128) * XSTEP + 16 * c) =
+          v4;
     }
-    zero_acc4(acc);
+    zero_acc<F>(acc);
   };
 
-  __shared__ Stage4 s0, s1;
-  persistent_tiles<Tile4>(tr, H / 128, s0, s1, setup, mfma, epilogue);
+  __shared__ StageMx<F> s0, s1;
+  persistent_tiles<Tile>(tr, H / 128, s0, s1, setup, mfma, epilogue);
 }
 
 // down: out[row, n] = act[row] . W2[n], bf16, permuted rows (the combine applies the routing
-// weights); tile = 128 rows x 512 output columns, wave wn owns columns 128 wn + [0, 128).
-template <typename Table>
-__global__ void __launch_bounds__(64 * WAVES4) down4_kernel(const uint8_t* __restrict__ a6, Lists L, Table routed,
-                                                            Table shared, uint16_t* __restrict__ out) {
+// weights); tile = 128 rows x TW output columns, wave wn owns columns 32 MI wn + [0, 32 MI).
+template <typename F, typename Table>
+__global__ void __launch_bounds__(64 * WAVES4) down_mx_kernel(const uint8_t* __restrict__ a6, Lists L, Table routed,
+                                                              Table shared, uint16_t* __restrict__ out) {
+  constexpr int MI = F::MI;
   const int H = routed.hidden, I = routed.inter;
-  const int n_tiles = (H + TW4 - 1) / TW4;
+  const int n_tiles = (H + F::TW - 1) / F::TW;
   const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int wm = wave & 1, wn = wave >> 1;
-  const Lane4 lo = lane4(128 * wn, wm);
+  const LaneMx<F> lo = lane_mx<F>(32 * MI * wn, wm);
   const uint32_t a_row = (uint32_t)(I / 128 * XSTEP);
+  using Tile = TileMx<F>;
 
-  auto setup = [&](int j, Tile4& t) {
+  auto setup = [&](int j, Tile& t) {
     const int logical = tr.first + tr.stride * j;
     const int mt = logical / n_tiles;
     t.nt = logical - mt * n_tiles;
@@ -1240,33 +802,37 @@ __global__ void __launch_bounds__(64 * WAVES4) down4_kernel(const uint8_t* __res
     t.begin = begin;
     t.end = end;
     const TileWeights tw = tile_weights_s(routed, shared, expert);
-    const Table& tab = expert < 0 ? shared : routed;
-    t.valid = min(TW4, H - t.nt * TW4);  // a multiple of 128
+    t.valid = min(F::TW, H - t.nt * F::TW);  // a multiple of 128
     const int nt = t.nt, valid = t.valid;
-    weight_offsets(t.ld, TileWeightsRegion{tw.w2, tw.w2s}, H, I, tab.tiled,
-                   [nt, valid](int r) { return nt * TW4 + (r < valid ? r : r % valid); });  // never past H
+    auto col_row = [nt, valid](int r) { return nt * F::TW + (r < valid ? r : r % valid); };  // never past H
+    weight_offsets<F>(t.ld, tw.w2, tw.w2s, H, I, table_tiled(expert < 0 ? shared : routed), col_row);
+    if constexpr (F::FP8)  // the wave's columns lie in one 128-row scale block
+      t.s0 = t.s1 = uniform_ptr(reinterpret_cast<const float*>(tw.w2s) +
+                                (int64_t)(col_row(32 * MI * wn) / 128) * (I / 128));
     t.ld.b = uniform_u8(a6);
-    split_row_offsets(t.ld, [&](int, int r) { return (uint32_t)(begin + r < end ? begin + r : begin) * a_row; });
+    split_row_offsets<F>(t.ld, [&](int, int r) { return (uint32_t)(begin + r < end ? begin + r : begin) * a_row; });
     return true;
   };
 
-  v16f acc[MI4][NI4];
-  zero_acc4(acc);
-  auto mfma = [&](const Tile4&, const Stage4& st, int) { step4(st, lo, acc, [](int mi) { return 32 * mi; }); };
+  v16f acc[MI][NI4];
+  zero_acc<F>(acc);
+  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k) {
+    step_mx<F>(st, lo, acc, [](int mi) { return 32 * mi; }, [&](int) { return t.s0[k]; });
+  };
 
-  // Epilogue: lane (r, half) holds output columns nt * 512 + 128 wn + 32 mi + 8 j + 4 half + q
+  // Epilogue: lane (r, half) holds output columns nt * TW + 32 MI wn + 32 mi + 8 j + 4 half + q
   // (register 4 j + q) of row 64 wm + 32 ni + r. Each wave turns 32 rows x 64 columns at a
   // time around in its own slice of the consumed stage (rows of 144 bytes) and stores each
   // row's 128 bytes as 8 lanes x 16.
-  auto epilogue = [&](const Tile4& t, Stage4& st) {
+  auto epilogue = [&](const Tile& t, StageMx<F>& st) {
     stage_barrier();
-    if (128 * wn < t.valid) {
+    if (32 * MI * wn < t.valid) {
       uint8_t* slice = reinterpret_cast<uint8_t*>(&st) + wave * 4608;
       const int r = lane % 32, half = lane / 32;
 #pragma unroll
       for (int ni = 0; ni < NI4; ++ni)
 #pragma unroll
-        for (int mp = 0; mp < 2; ++mp) {
+        for (int mp = 0; mp < MI / 2; ++mp) {
 #pragma unroll
           for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -1281,19 +847,19 @@ __global__ void __launch_bounds__(64 * WAVES4) down4_kernel(const uint8_t* __res
 #pragma unroll
           for (int it = 0; it < 4; ++it) {
             const int rr = lane / 8 + 8 * it, c = lane % 8;
-            const uint4 v = *reinterpret_cast<const uint4*>(slice + rr * 144 + 16 * c);
+            const uint4 v4 = *reinterpret_cast<const uint4*>(slice + rr * 144 + 16 * c);
             const int row = t.begin + 64 * wm + 32 * ni + rr;
             if (row < t.end)
-              *reinterpret_cast<uint4*>(out + (int64_t)row * H + t.nt * TW4 + 128 * wn + 64 * mp + 8 * c) = v;
+              *reinterpret_cast<uint4*>(out + (int64_t)row * H + t.nt * F::TW + 32 * MI * wn + 64 * mp + 8 * c) = v4;
           }
           wave_lds_fence();
         }
     }
-    zero_acc4(acc);
+    zero_acc<F>(acc);
   };
 
-  __shared__ Stage4 s0, s1;
-  persistent_tiles<Tile4>(tr, I / 128, s0, s1, setup, mfma, epilogue);
+  __shared__ StageMx<F> s0, s1;
+  persistent_tiles<Tile>(tr, I / 128, s0, s1, setup, mfma, epilogue);
 }
 
 // Token of every permuted row: order[p] / K for routed rows, p - P for the shared rows.
@@ -1411,12 +977,12 @@ static int compute_units() {
 }
 
 struct Layout {
-  size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, row_token, x8, xs, a8, as8, rows, total;
+  size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, row_token, x6, a6, rows, total;
 };
 
-// rowb: bytes of one row's 128-wide K step in the split format (E4M3 terms 256 with separate
-// scales, E2M3 terms XSTEP with the scales inside); split buffers end with XSLACK spare bytes.
-static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool has_shared, int rowb) {
+// Split rows take XSTEP bytes per 128-wide K step (E2M3 terms with their scales inside);
+// each split buffer ends with XSLACK spare bytes.
+static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool has_shared) {
   const int64_t pairs = (int64_t)tokens * k;
   const int64_t rows = pairs + (has_shared ? tokens : 0);
   const int64_t max_tiles = (pairs + BM - 1) / BM + experts;
@@ -1430,36 +996,39 @@ static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool
   p.tile_count = at; at += align256(sizeof(int32_t));
   p.gate = at;       at += align256(sizeof(float) * (size_t)(tokens > 0 ? tokens : 1));
   p.row_token = at;  at += align256(sizeof(int32_t) * (size_t)(rows > 0 ? rows : 1));
-  p.x8 = at;         at += align256((size_t)tokens * (hidden / 128) * rowb + XSLACK);
-  p.xs = at;         at += align256((size_t)tokens * (hidden / 128) * 8);
-  p.a8 = at;         at += align256((size_t)rows * (inter / 128) * rowb + XSLACK);
-  p.as8 = at;        at += align256((size_t)rows * (inter / 128) * 8);
+  p.x6 = at;         at += align256((size_t)tokens * (hidden / 128) * XSTEP + XSLACK);
+  p.a6 = at;         at += align256((size_t)rows * (inter / 128) * XSTEP + XSLACK);
   p.rows = at;       at += align256(sizeof(uint16_t) * (size_t)rows * hidden);
   p.total = at;
   return p;
 }
 
-template <typename W, typename Table>
+template <typename F, typename Table>
 static void run(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                 const Table& routed, const Table* shared, const uint16_t* shared_gate, uint16_t* y, bool combine,
                 void* ws, size_t ws_bytes, hipStream_t s) {
   const int H = routed.hidden, I = routed.inter;
   if (H % 128 || I % 128) fail("prefill: hidden and intermediate must be multiples of 128");
   const bool has_shared = combine && shared != nullptr;
-  constexpr bool fp6_terms = W::FMT == FMT_FP4;  // MXFP4 weights take E2M3 activation terms
-  constexpr int rowb = fp6_terms ? XSTEP : CHUNK;
-  const Layout p = layout(tokens, k, routed.experts, H, I, has_shared, rowb);
+  const Layout p = layout(tokens, k, routed.experts, H, I, has_shared);
   if (ws_bytes < p.total) fail("prefill: workspace too small");
   const int64_t pairs = (int64_t)tokens * k;
   const int64_t rows = pairs + (has_shared ? tokens : 0);
-  if constexpr (W::FMT == FMT_FP4) {  // the K loop reads 4 scale bytes of a row as one dword
+  if constexpr (!F::FP8) {  // the K loop reads 4 scale bytes of a row as one dword
     auto dword_rows = [](const void* p, int64_t stride) { return (uintptr_t)p % 4 == 0 && stride % 4 == 0; };
     for (const Table* t : {&routed, shared})
       if (t && (!dword_rows(t->gate_up_scales, t->gate_up_scales_stride) ||
                 !dword_rows(t->down_scales, t->down_scales_stride)))
         fail("prefill: MXFP4 scale regions and strides must be 4-byte aligned");
+  } else {  // 16-byte loads of weight rows; the fp32 block scales go through scalar loads
+    auto rows16 = [](const void* p, int64_t stride) { return (uintptr_t)p % 16 == 0 && stride % 16 == 0; };
+    auto f32 = [](const void* p, int64_t stride) { return (uintptr_t)p % 4 == 0 && stride % 4 == 0; };
+    for (const Table* t : {&routed, shared})
+      if (t && (!rows16(t->w13, t->w13_stride) || !rows16(t->w2, t->w2_stride) ||
+                !f32(t->w13_scales, t->w13_scales_stride) || !f32(t->w2_scales, t->w2_scales_stride)))
+        fail("prefill: FP8 weight regions and strides must be 16-byte aligned, scales 4-byte");
   }
-  if ((int64_t)rows * (I / 128) * rowb >= ((int64_t)1 << 32) || (int64_t)tokens * (H / 128) * rowb >= ((int64_t)1 << 32))
+  if ((int64_t)rows * (I / 128) * XSTEP >= ((int64_t)1 << 32) || (int64_t)tokens * (H / 128) * XSTEP >= ((int64_t)1 << 32))
     fail("prefill: split operands of 4 GiB or more (split the call into smaller token batches)");
   uint8_t* base = (uint8_t*)ws;
   Lists L;
@@ -1477,31 +1046,24 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
                  (int32_t*)L.tiles, (int32_t*)L.tile_count, base + p.permute_ws,
                  wm_permute_workspace_size(pairs, routed.experts), s) != 0)
     fail(std::string("prefill permute: ") + wm_last_error());
-  // MXFP4: the split kernel computes the shared gate when a row's blocks fit one wave in a
-  // power-of-two group; otherwise (and for FP8) a kernel of its own does
-  const bool fused_gate = fp6_terms && has_shared && shared_gate && (H / 32) <= 64 && ((H / 32) & (H / 32 - 1)) == 0;
+  // the split kernel computes the shared gate when a row's blocks fit one wave in a
+  // power-of-two group; otherwise a kernel of its own does
+  const bool fused_gate = has_shared && shared_gate && (H / 32) <= 64 && ((H / 32) & (H / 32 - 1)) == 0;
   if (has_shared && !fused_gate) {
     hipLaunchKernelGGL(shared_gate_kernel, dim3(tokens), dim3(64), 0, s, x, shared_gate, tokens, H,
                        (float*)L.shared_gate);
     check_launch("shared_gate");
   }
-  uint8_t* x8 = base + p.x8;
-  uint8_t* xs = base + p.xs;
+  uint8_t* x6 = base + p.x6;
   int32_t* row_token = (int32_t*)(base + p.row_token);
-  if constexpr (fp6_terms) {
-    if (rows > 0) {
-      hipLaunchKernelGGL(row_tokens_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, L.order, (int)pairs,
-                         k, (int)rows, row_token);
-      check_launch("row_tokens");
-    }
-    const int64_t split_jobs = (int64_t)tokens * (H / 32);
-    hipLaunchKernelGGL(split6_rows_kernel, dim3((unsigned)((split_jobs + 255) / 256)), dim3(256), 0, s, x, tokens, H,
-                       x8, fused_gate ? shared_gate : nullptr, (float*)L.shared_gate);
-  } else {
-    const int64_t split_jobs = (int64_t)tokens * (H / 128);
-    hipLaunchKernelGGL(split_rows_kernel, dim3((unsigned)((split_jobs + 3) / 4)), dim3(256), 0, s, x, tokens, H, x8,
-                       xs);
+  if (rows > 0) {
+    hipLaunchKernelGGL(row_tokens_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, L.order, (int)pairs,
+                       k, (int)rows, row_token);
+    check_launch("row_tokens");
   }
+  const int64_t split_jobs = (int64_t)tokens * (H / 32);
+  hipLaunchKernelGGL(split6_rows_kernel, dim3((unsigned)((split_jobs + 255) / 256)), dim3(256), 0, s, x, tokens, H,
+                     x6, fused_gate ? shared_gate : nullptr, (float*)L.shared_gate);
   check_launch("split_rows");
   const Table sh = shared ? *shared : routed;
   const int64_t max_row_tiles = (pairs + BM - 1) / BM + routed.experts + (has_shared ? (tokens + BM - 1) / BM : 0);
@@ -1513,25 +1075,17 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
     const int64_t per_xcd = std::min<int64_t>((work + XCDS - 1) / XCDS, std::max(cus / XCDS, 1));
     return dim3((unsigned)(per_xcd * XCDS));
   };
-  uint8_t* a8 = base + p.a8;
-  uint8_t* as8 = base + p.as8;
+  uint8_t* a6 = base + p.a6;
   uint16_t* out_rows = (uint16_t*)(base + p.rows);
   TimingEvents* te = g_timing.load() ? timing_events() : nullptr;
   if (te) check_hip(hipEventRecord(te->ev[0], s), "hipEventRecord");
-  if constexpr (fp6_terms)
-    hipLaunchKernelGGL((gate_up4_kernel<Table>), grid_for((I + TW4 / 2 - 1) / (TW4 / 2)), dim3(64 * WAVES4), 0, s, x8,
-                       row_token, L, routed, sh, a8);
-  else
-    hipLaunchKernelGGL((gate_up_kernel<W, Table>), grid_for((I + W::TW / 2 - 1) / (W::TW / 2)), dim3(64 * W::WAVES),
-                       0, s, x8, xs, L, routed, sh, a8, as8);
+  hipLaunchKernelGGL((gate_up_mx_kernel<F, Table>), grid_for((I + F::TW / 2 - 1) / (F::TW / 2)), dim3(64 * WAVES4), 0,
+                     s, x6, row_token, L, routed, sh, a6);
   check_launch("gate_up");
   if (te) check_hip(hipEventRecord(te->ev[1], s), "hipEventRecord");
-  if constexpr (fp6_terms)
-    hipLaunchKernelGGL((down4_kernel<Table>), grid_for((H + TW4 - 1) / TW4), dim3(64 * WAVES4), 0, s, a8, L, routed,
-                       sh, out_rows);
-  else  // unweighted rows: the combine applies the routing weights and the shared gate
-    hipLaunchKernelGGL((down_kernel<W, Table>), grid_for((H + W::TW - 1) / W::TW), dim3(64 * W::WAVES), 0, s, a8, as8,
-                       L, weights, 0, routed, sh, out_rows);
+  // unweighted rows: the combine applies the routing weights and the shared gate
+  hipLaunchKernelGGL((down_mx_kernel<F, Table>), grid_for((H + F::TW - 1) / F::TW), dim3(64 * WAVES4), 0, s, a6, L,
+                     routed, sh, out_rows);
   check_launch("down");
   if (te) check_hip(hipEventRecord(te->ev[2], s), "hipEventRecord");
   if (combine)
@@ -1546,23 +1100,23 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
 }  // namespace mf
 
 size_t prefill_workspace_size(int tokens, int k, const wm_mxfp4_experts& e, bool has_shared) {
-  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared, mf::XSTEP).total;
+  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared).total;
 }
 
 void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                    const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared, const uint16_t* shared_gate,
                    uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s) {
-  mf::run<mf::Fp4Weights>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  mf::run<mf::Mx4>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
 }
 
 size_t prefill_fp8_workspace_size(int tokens, int k, const wm_fp8_experts& e, bool has_shared) {
-  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared, mf::CHUNK).total;
+  return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared).total;
 }
 
 void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                  const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
                  uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s) {
-  mf::run<mf::Fp8Weights>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  mf::run<mf::Mx8>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
 }
 
 }  // namespace wm
@@ -1588,7 +1142,7 @@ WM_EXPORT int wm_repack_prefill_mxfp4(const wm_mxfp4_experts* src, void* gate_up
     auto launch = [&](const void* w, const void* ws, int64_t stride, int64_t stride_s, int rows, int k, void* dst,
                       void* dst_s) {
       const int64_t n = (int64_t)E * ((int64_t)rows * (k / 32) + (int64_t)rows * (k / 128));
-      hipLaunchKernelGGL(wm::mf::repack_prefill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+      hipLaunchKernelGGL(wm::mf::repack_prefill_kernel<4>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                          (const uint8_t*)w, (const uint8_t*)ws, stride, stride_s, src->slots, E, rows, k,
                          (uint8_t*)dst, (uint8_t*)dst_s);
       wm::check_launch("repack_prefill");
@@ -1596,6 +1150,40 @@ WM_EXPORT int wm_repack_prefill_mxfp4(const wm_mxfp4_experts* src, void* gate_up
     launch(src->gate_up, src->gate_up_scales, src->gate_up_stride, src->gate_up_scales_stride, 2 * I, H, gate_up,
            gate_up_scales);
     launch(src->down, src->down_scales, src->down_stride, src->down_scales_stride, H, I, down, down_scales);
+  });
+}
+
+WM_EXPORT int wm_repack_prefill_fp8(const wm_fp8_experts* src, void* w13, void* w13_scales, void* w2,
+                                    void* w2_scales, void* stream) {
+  return wm::guarded([&] {
+    if (!src) wm::fail("wm_repack_prefill_fp8: source table is null");
+    if (!src->w13 || !src->w2 || !src->w13_scales || !src->w2_scales)
+      wm::fail("wm_repack_prefill_fp8: source region pointer is null");
+    if (src->tiled) wm::fail("wm_repack_prefill_fp8: the source is already in the prefill tile layout");
+    if (src->experts < 1 || src->experts > 1024) wm::fail("wm_repack_prefill_fp8: expert count must be in 1..1024");
+    if (src->hidden < 128 || src->hidden % 128 || src->inter < 128 || src->inter % 128)
+      wm::fail("wm_repack_prefill_fp8: hidden and intermediate must be positive multiples of 128");
+    if (!w13 || !w2 || !w13_scales || !w2_scales) wm::fail("wm_repack_prefill_fp8: null destination");
+    auto aligned = [](const void* p, uintptr_t a) { return (uintptr_t)p % a == 0; };
+    if (!aligned(w13, 16) || !aligned(w2, 16) || !aligned(src->w13, 16) || !aligned(src->w2, 16) ||
+        src->w13_stride % 16 || src->w2_stride % 16 || src->w13_stride < 0 || src->w2_stride < 0)
+      wm::fail("wm_repack_prefill_fp8: weight regions and strides must be 16-byte aligned");
+    if (!aligned(w13_scales, 4) || !aligned(w2_scales, 4) || !aligned(src->w13_scales, 4) ||
+        !aligned(src->w2_scales, 4) || src->w13_scales_stride % 4 || src->w2_scales_stride % 4 ||
+        src->w13_scales_stride < 0 || src->w2_scales_stride < 0)
+      wm::fail("wm_repack_prefill_fp8: scale regions and strides must be 4-byte aligned");
+    const int E = src->experts, H = src->hidden, I = src->inter;
+    hipStream_t s = wm::as_stream(stream);
+    auto launch = [&](const void* w, const void* ws, int64_t stride, int64_t stride_s, int rows, int k, void* dst,
+                      void* dst_s) {
+      const int64_t n = (int64_t)E * ((int64_t)rows * (k / 16) + (int64_t)(rows / 128) * (k / 128));
+      hipLaunchKernelGGL(wm::mf::repack_prefill_kernel<8>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                         (const uint8_t*)w, (const uint8_t*)ws, stride, stride_s, src->slots, E, rows, k,
+                         (uint8_t*)dst, (uint8_t*)dst_s);
+      wm::check_launch("repack_prefill_fp8");
+    };
+    launch(src->w13, src->w13_scales, src->w13_stride, src->w13_scales_stride, 2 * I, H, w13, w13_scales);
+    launch(src->w2, src->w2_scales, src->w2_stride, src->w2_scales_stride, H, I, w2, w2_scales);
   });
 }
 

@@ -64,13 +64,15 @@ static void validate_fp8_pair(const wm_fp8_experts* routed, const wm_fp8_experts
     validate_fp8(shared, "shared expert", true);
     if (shared->hidden != routed->hidden || shared->inter != routed->inter)
       fail("shared expert: hidden and intermediate must equal the routed experts'");
+    if ((shared->tiled != 0) != (routed->tiled != 0))
+      fail("shared expert: the routed and shared tables must both be in the row layout or both tiled");
   }
 }
 
-// The fused GEMV handles hidden / intermediate multiples of 1024; other shapes and
-// larger batches take the grouped GEMM.
+// The fused GEMV handles hidden / intermediate multiples of 1024 in the row layout; other
+// shapes, tables in the prefill tile layout and larger batches take the grouped GEMM.
 static bool use_decode_fp8(int tokens, int k, const wm_fp8_experts& e) {
-  return use_decode(tokens, k) && e.hidden % 1024 == 0 && e.inter % 1024 == 0 && e.hidden <= 8192 && e.inter <= 8192;
+  return !e.tiled && use_decode(tokens, k) && e.hidden % 1024 == 0 && e.inter % 1024 == 0 && e.hidden <= 8192 && e.inter <= 8192;
 }
 
 static size_t decode_workspace(int tokens, int k, const wm_mxfp4_experts& e) {

@@ -115,23 +115,28 @@ class MXFP4Experts:
         return (self.gate_up, self.gate_up_scales, self.down, self.down_scales, self.slots)
 
 
-def prefill_layout(experts: MXFP4Experts) -> MXFP4Experts:
-    """A copy of ``experts`` in the prefill tile layout (wm_repack_prefill_mxfp4): one
-    expert after another (``slots`` resolved), each 16-row group's 128-wide K step one
-    contiguous KB, each step's scale bytes one run. Same shapes and bytes as the row layout;
+def prefill_layout(experts):
+    """A copy of ``experts`` (MXFP4Experts or FP8Experts) in the prefill tile layout
+    (wm_repack_prefill_mxfp4 / wm_repack_prefill_fp8): one expert after another (``slots``
+    resolved), each 16-row group's 128-wide K step contiguous (MXFP4: each step's scale
+    bytes one run; FP8: block scales unchanged). Same shapes and bytes as the row layout;
     only the grouped-GEMM path (any batch size) takes it. A one-time repack, like the
     reference's install-time blob repack (Sources/DeepSeekRepack/Repacker.swift:17-124)."""
     if experts.tiled:
         return experts
     device = _require_device(*experts.tensors())
-    E, H, I = experts.count, experts.hidden, experts.inter
-    lead = (E,) if experts.gate_up.dim() == 3 or E > 1 else ()
-    out = [torch.empty(*lead, *t.shape[-2:], dtype=t.dtype, device=device)
-           for t in (experts.gate_up, experts.gate_up_scales, experts.down, experts.down_scales)]
+    E = experts.count
+    fp8 = isinstance(experts, FP8Experts)
+    regions = ((experts.w13, experts.w13_scales, experts.w2, experts.w2_scales) if fp8 else
+               (experts.gate_up, experts.gate_up_scales, experts.down, experts.down_scales))
+    lead = (E,) if regions[0].dim() == 3 or E > 1 else ()
+    out = [torch.empty(*lead, *t.shape[-2:], dtype=t.dtype, device=device) for t in regions]
     table = experts.c_struct()
-    _lib.call("wm_repack_prefill_mxfp4", ctypes.byref(table), *(_ptr(t) for t in out), _stream(device))
-    return MXFP4Experts(*out, experts=E if lead else None, up_first=experts.up_first,
-                        swiglu_limit=experts.swiglu_limit, tiled=True)
+    _lib.call("wm_repack_prefill_fp8" if fp8 else "wm_repack_prefill_mxfp4", ctypes.byref(table),
+              *(_ptr(t) for t in out), _stream(device))
+    cls = FP8Experts if fp8 else MXFP4Experts
+    return cls(*out, experts=E if lead else None, up_first=experts.up_first, swiglu_limit=experts.swiglu_limit,
+               tiled=True)
 
 
 # ----------------------------------------------------------------------------- formats
@@ -313,6 +318,7 @@ class FP8Experts:
     experts: int | None = None
     up_first: bool = False
     swiglu_limit: float = 0.0
+    tiled: bool = False
 
     @property
     def hidden(self) -> int:
@@ -348,7 +354,7 @@ class FP8Experts:
             self.w13.data_ptr(), self.w13_scales.data_ptr(), self.w2.data_ptr(), self.w2_scales.data_ptr(),
             stride(self.w13), stride(self.w13_scales), stride(self.w2), stride(self.w2_scales),
             0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
-            float(self.swiglu_limit))
+            float(self.swiglu_limit), int(self.tiled))
 
     def tensors(self):
         return (self.w13, self.w13_scales, self.w2, self.w2_scales, self.slots)
