@@ -129,7 +129,8 @@ __device__ __forceinline__ TileRange tile_range(int active) {
 // next tile is set up (index loads, load offsets) after the MFMAs of the tile's
 // second-to-last step, and its first loads fly during this tile's epilogue.
 //   setup(j, tile) -> bool: fills tile j's state; false for a tile with no rows
-//   mfma(tile, stage, k): step k of a tile
+//   mfma(tile, stage, k, load_part): step k of a tile, calling load_part(p) for p = 0..3
+//     between its MFMAs (the next step's loads)
 //   epilogue(tile, stage): after a tile's last step (stage: the one just consumed, free
 //     until the next step's loads are issued once every wave has passed its top barrier)
 template <typename Tile, typename S, typename Setup, typename Mfma, typename Epilogue>
@@ -144,12 +145,20 @@ __device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps,
     if (g >= total) return;
     const int j = g / steps, k = g - j * steps;
     ring_wait_all();
-    if (k + 1 < steps) {
-      if (cur_ok) cur.ld.issue(other, k + 1);
-    } else if (j + 1 < tr.count && steps > 1 && nxt_ok) {
-      nxt.ld.issue(other, 0);
+    // loads into the other stage: the tile's next step, or the next tile's first step
+    const int target = k + 1 < steps ? (cur_ok ? 1 : 0) : (j + 1 < tr.count && steps > 1 && nxt_ok ? 2 : 0);
+    auto load_part = [&](int p) {
+      if (target == 1)
+        cur.ld.issue_part(other, k + 1, p);
+      else if (target == 2)
+        nxt.ld.issue_part(other, 0, p);
+    };
+    if (cur_ok) {
+      mfma(cur, stage, k, load_part);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) load_part(p);
     }
-    if (cur_ok) mfma(cur, stage, k);
     if (k == steps - 2 && j + 1 < tr.count) nxt_ok = setup(j + 1, nxt);
     if (k == steps - 1) {
       if (cur_ok) epilogue(cur, stage);
@@ -371,6 +380,31 @@ __device__ __forceinline__ bool resolve_tile_s(const Lists& L, int m, int& exper
   return true;
 }
 
+// (row tile, column tile) of logical work tile `logical`. The list is blocked by expert
+// (the shared expert's row tiles are one more block): a block of c row tiles takes
+// c * n_tiles consecutive logical tiles, column-major, so the row tiles that read the same
+// weight columns are adjacent and run together on one XCD (one L2 fetch of the weights),
+// while a row tile's column tiles stay within c * n_tiles of each other (its split rows
+// stay in L2). Scalar loads only.
+__device__ __forceinline__ void order_tile(const Lists& L, int logical, int n_tiles, int& mt, int& nt) {
+  const int m0 = logical / n_tiles;
+  const int routed = scalar_i32(L.tile_count, 0);
+  int t0, c;
+  if (m0 < routed) {
+    const int e = scalar_i32(L.tiles, 2 * m0);
+    const int begin = scalar_i32(L.tiles, 2 * m0 + 1);
+    const int lo = scalar_i32(L.offsets, e), hi = scalar_i32(L.offsets, e + 1);
+    t0 = m0 - (begin - lo) / BM;
+    c = (hi - lo + BM - 1) / BM;
+  } else {
+    t0 = routed;
+    c = (L.tokens + BM - 1) / BM;
+  }
+  const int local = logical - t0 * n_tiles;
+  nt = local / c;
+  mt = t0 + (local - nt * c);
+}
+
 __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& routed, const wm_mxfp4_experts& shared,
                                                       int expert) {
   const wm_mxfp4_experts& t = expert < 0 ? shared : routed;
@@ -455,11 +489,12 @@ __device__ __forceinline__ LaneMx<F> lane_mx(int wave_row0, int wm) {
 
 // One 128-wide K step of the wave's sub-tile. Per half: the MI A fragments, then per row
 // tile its hi B fragment feeds MI MFMAs and its lo fragment MI more, so no MFMA waits on
-// the one before it. FP8 accumulates the step in blk and adds it times its block scale
+// the one before it; between(g) follows group g = 2 h + ni (the next step's loads). FP8
+// accumulates the step in blk and adds it times its block scale
 // bscale(mi) (the fp32 scale cannot ride on the MFMA's E8M0 scales).
-template <typename F, typename MRow, typename BScale>
+template <typename F, typename MRow, typename BScale, typename Between>
 __device__ __forceinline__ void step_mx(const StageMx<F>& st, const LaneMx<F>& lo, v16f (&acc)[F::MI][NI4], MRow mrow,
-                                        BScale bscale) {
+                                        BScale bscale, Between between) {
   constexpr int MI = F::MI;
   uint32_t sa[MI];
   uint2 sb[NI4];
@@ -522,6 +557,7 @@ __device__ __forceinline__ void step_mx(const StageMx<F>& st, const LaneMx<F>& l
                                                                         (int)(sa[mi] >> sh), 0, sbl);
       }
       __builtin_amdgcn_sched_barrier(0);
+      between(2 * h + ni);
     }
   }
   if constexpr (F::FP8) {
@@ -550,15 +586,25 @@ struct LoaderMx {
   uint32_t soff;
   uint32_t a_step, s_step;
 
-  __device__ __forceinline__ void issue(StageMx<F>& st, int ks) {
+  // Part p (0..3) of step ks's loads into st: the weight loads (the longer way, from HBM)
+  // first, then the split rows. The K loop issues one part after each group of MFMAs, so
+  // no wave stalls for long on a full load queue with its MFMAs waiting behind.
+  __device__ __forceinline__ void issue_part(StageMx<F>& st, int ks, int p) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    if (p < 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(st.b + (w + WAVES4 * i) * 1024));
+      for (int i = 2 * p; i < 2 * p + 2; ++i)
+        dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(st.a + (w + WAVES4 * i) * 1024));
+      if (!F::FP8 && p == 1) dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(st.as + 256 * w));
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(st.a + (w + WAVES4 * i) * 1024));
-    if constexpr (!F::FP8) dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(st.as + 256 * w));
+      for (int i = 2 * (p - 2); i < 2 * (p - 2) + 2; ++i)
+        dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(st.b + (w + WAVES4 * i) * 1024));
+    }
+  }
+  __device__ __forceinline__ void issue(StageMx<F>& st, int ks) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) issue_part(st, ks, p);
   }
 };
 
@@ -671,9 +717,8 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
   using Tile = TileMx<F>;
 
   auto setup = [&](int j, Tile& t) {
-    const int logical = tr.first + tr.stride * j;
-    const int mt = logical / n_tiles;
-    t.nt = logical - mt * n_tiles;
+    int mt = 0;
+    order_tile(L, tr.first + tr.stride * j, n_tiles, mt, t.nt);
     int expert = 0, begin = 0, end = 0;
     if (!resolve_tile_s(L, mt, expert, begin, end)) return false;
     t.begin = begin;
@@ -712,8 +757,8 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
   v16f acc[MI][NI4];
   zero_acc<F>(acc);
   auto mrow = [](int mi) { return (mi < HM ? 0 : TG) + 32 * (mi % HM); };
-  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k) {
-    step_mx<F>(st, lo, acc, mrow, [&](int mi) { return mi < HM ? t.s0[k] : t.s1[k]; });
+  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k, auto load_part) {
+    step_mx<F>(st, lo, acc, mrow, [&](int mi) { return mi < HM ? t.s0[k] : t.s1[k]; }, load_part);
   };
 
   // Epilogue: lane (r, half) holds act rows 8 j + 4 half + q (j, q = 0..3; register 4 j + q)
@@ -794,9 +839,8 @@ __global__ void __launch_bounds__(64 * WAVES4) down_mx_kernel(const uint8_t* __r
   using Tile = TileMx<F>;
 
   auto setup = [&](int j, Tile& t) {
-    const int logical = tr.first + tr.stride * j;
-    const int mt = logical / n_tiles;
-    t.nt = logical - mt * n_tiles;
+    int mt = 0;
+    order_tile(L, tr.first + tr.stride * j, n_tiles, mt, t.nt);
     int expert = 0, begin = 0, end = 0;
     if (!resolve_tile_s(L, mt, expert, begin, end)) return false;
     t.begin = begin;
@@ -816,8 +860,8 @@ __global__ void __launch_bounds__(64 * WAVES4) down_mx_kernel(const uint8_t* __r
 
   v16f acc[MI][NI4];
   zero_acc<F>(acc);
-  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k) {
-    step_mx<F>(st, lo, acc, [](int mi) { return 32 * mi; }, [&](int) { return t.s0[k]; });
+  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k, auto load_part) {
+    step_mx<F>(st, lo, acc, [](int mi) { return 32 * mi; }, [&](int) { return t.s0[k]; }, load_part);
   };
 
   // Epilogue: lane (r, half) holds output columns nt * TW + 32 MI wn + 32 mi + 8 j + 4 half + q
