@@ -121,62 +121,6 @@ __device__ __forceinline__ TileRange tile_range(int active) {
   return t;
 }
 
-// Persistent K loop over this workgroup's tiles, as one flat sequence of 128-wide steps
-// through two LDS stages (global step g uses stage g % 2; the loop is unrolled over the
-// two stages so their addresses are static). At the top of each step every wave has the
-// step's loads landed and is done with the other stage, which then takes the next step's
-// loads: the tile's next K step, or at a tile's last step the next tile's first step. The
-// next tile is set up (index loads, load offsets) after the MFMAs of the tile's
-// second-to-last step, and its first loads fly during this tile's epilogue.
-//   setup(j, tile) -> bool: fills tile j's state; false for a tile with no rows
-//   mfma(tile, stage, k, load_part): step k of a tile, calling load_part(p) for p = 0..3
-//     between its MFMAs (the next step's loads)
-//   epilogue(tile, stage): after a tile's last step (stage: the one just consumed, free
-//     until the next step's loads are issued once every wave has passed its top barrier)
-template <typename Tile, typename S, typename Setup, typename Mfma, typename Epilogue>
-__device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps, S& s0, S& s1, Setup setup, Mfma mfma,
-                                                 Epilogue epilogue) {
-  if (tr.count == 0) return;
-  Tile cur, nxt;
-  bool cur_ok = setup(0, cur), nxt_ok = false;
-  if (cur_ok) cur.ld.issue(s0, 0);
-  const int total = tr.count * steps;
-  auto body = [&](int g, S& stage, S& other) {
-    if (g >= total) return;
-    const int j = g / steps, k = g - j * steps;
-    ring_wait_all();
-    // loads into the other stage: the tile's next step, or the next tile's first step
-    const int target = k + 1 < steps ? (cur_ok ? 1 : 0) : (j + 1 < tr.count && steps > 1 && nxt_ok ? 2 : 0);
-    auto load_part = [&](int p) {
-      if (target == 1)
-        cur.ld.issue_part(other, k + 1, p);
-      else if (target == 2)
-        nxt.ld.issue_part(other, 0, p);
-    };
-    if (cur_ok) {
-      mfma(cur, stage, k, load_part);
-    } else {
-#pragma unroll
-      for (int p = 0; p < 4; ++p) load_part(p);
-    }
-    if (k == steps - 2 && j + 1 < tr.count) nxt_ok = setup(j + 1, nxt);
-    if (k == steps - 1) {
-      if (cur_ok) epilogue(cur, stage);
-      if (steps == 1 && j + 1 < tr.count) {
-        nxt_ok = setup(j + 1, nxt);
-        if (nxt_ok) nxt.ld.issue(other, 0);
-      }
-      cur = nxt;
-      cur_ok = nxt_ok;
-      nxt_ok = false;
-    }
-  };
-  for (int g = 0; g < total; g += 2) {
-    body(g, s0, s1);
-    body(g + 1, s1, s0);
-  }
-}
-
 // ---------------------------------------------------------------------------------
 // Expert regions of a tile.
 
@@ -424,12 +368,12 @@ __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& ro
 // x TW-weight-row tile with 8 waves: wave w = (wm, wn) = (w & 1, w >> 1) owns 64 rows
 // (2 tiles of 32) and MI weight tiles of 32 rows. Each 128-wide K step's operands go
 // straight from global memory into LDS (global_load_lds: lane i of a wave writes LDS
-// base + 16 i) in a ring of two stages; step k + 1's loads are issued when step k starts.
+// base + 16 i).
 //
-// LDS stage:
-//   split rows: 256 bytes per row, piece p of the row's 208-byte step in slot p ^ (row & 15)
-//     (the 16 rows a ds_read_b128 phase serves fall on distinct banks); one load takes 4
-//     rows (lane: row 4q + lane / 16, slot lane % 16), so each row's step arrives as one run;
+// LDS (see RingMx): a ring of weight slots and a ring of split-row slots, one deeper than
+// the other so the operand with the longer way from memory is loaded further ahead:
+//   split rows: 128 rows x 208 bytes (one row's step), unswizzled; one load takes 4 rows
+//     (52 lanes: row 4q + lane / 13, piece lane % 13), so each row's step arrives as one run;
 //   weight rows: 16-row groups [PIECES][16 rows][16 bytes], a row's step being PIECES
 //     16-byte pieces (fp4: 4, fp8: 8); one load fills 4 pieces of a group: in the prefill
 //     tile layout one contiguous KB, in the row layout 64 contiguous bytes of each row;
@@ -441,22 +385,30 @@ __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& ro
 //   fp8 A: row r's K [16g, 16g + 16) in bytes 0-15 and [32 + 16g, 32 + 16g + 16) in 16-31;
 //   fp6 B: row r's K [32g, 32g + 32) as contiguous 6-bit fields, 24 bytes;
 //   scale lane (r, g): K block g; result register i: D[8 (i / 4) + 4 g + i % 4][r].
+// DA, DB: depths of the weight and split-row rings
 struct Mx4 {
   static constexpr bool FP8 = false;
-  static constexpr int TW = 512, MI = 4, PIECES = 4, A_FMT = FMT_FP4;
+  static constexpr int TW = 512, MI = 4, PIECES = 4, A_FMT = FMT_FP4, DA = 2, DB = 3;
 };
 struct Mx8 {
   static constexpr bool FP8 = true;
-  static constexpr int TW = 256, MI = 2, PIECES = 8, A_FMT = FMT_FP8;
+  static constexpr int TW = 256, MI = 2, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2;
 };
 constexpr int WAVES4 = 8;
 constexpr int NI4 = 2;      // 32-row row tiles per wave
 
-template <typename F>
-struct StageMx {
-  __attribute__((aligned(16))) uint8_t b[BM * 256];
-  __attribute__((aligned(16))) uint8_t a[F::TW * F::PIECES * 16];
-  __attribute__((aligned(16))) uint8_t as[F::FP8 ? 16 : F::TW * 4];
+// LDS of a workgroup: a ring of DA weight slots (a step's weight rows, then MXFP4 their
+// scales) and a ring of DB split-row slots (128 rows x XSTEP bytes, unswizzled: XSTEP / 16 =
+// 13 is odd, so the 8 rows one ds_read_b128 cycle serves fall on distinct banks). Step g
+// uses weight slot g % DA and split-row slot g % DB; the deeper ring runs its loads further
+// ahead (the operand with the longer way from memory).
+template <typename F, int DA, int DB>
+struct RingMx {
+  static constexpr int A_BYTES = F::TW * F::PIECES * 16;
+  static constexpr int A_SLOT = A_BYTES + (F::FP8 ? 0 : F::TW * 4);
+  static constexpr int B_SLOT = BM * XSTEP;
+  static constexpr int BYTES = DA * A_SLOT + DB * B_SLOT;
+  static_assert(BYTES <= 160 * 1024, "LDS");
 };
 
 // Per-lane LDS read offsets. Weight tile mi of the wave is rows wave_row0 + mrow(mi) + r
@@ -466,8 +418,8 @@ template <typename F>
 struct LaneMx {
   uint32_t a;        // + 16 PIECES mrow(mi) + (fp4: 512, fp8: 1024) h; fp8 second piece + 512
   uint32_t as;       // + 4 mrow(mi)
-  uint32_t b[2][3];  // [h][piece of the lane's 48 bytes] + 8192 ni
-  uint32_t bs;       // the row's scale piece (bytes 192..207 of the step) + 8192 ni
+  uint32_t b[2][3];  // [h][piece of the lane's 48 bytes] + 32 XSTEP ni
+  uint32_t bs;       // the row's scale bytes (192..199 of the step) + 32 XSTEP ni
   uint32_t shift;    // 8 g
 };
 
@@ -477,12 +429,12 @@ __device__ __forceinline__ LaneMx<F> lane_mx(int wave_row0, int wm) {
   LaneMx<F> o;
   o.a = (uint32_t)((wave_row0 / 16 + r / 16) * (F::PIECES * 256) + 256 * g + 16 * (r % 16));
   o.as = (uint32_t)(4 * (wave_row0 + r));
-  const int row = 64 * wm + r, z = r & 15;
+  const int row = 64 * wm + r;
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int e = 0; e < 3; ++e) o.b[h][e] = (uint32_t)(row * 256 + 16 * ((6 * h + 3 * g + e) ^ z));
-  o.bs = (uint32_t)(row * 256 + 16 * (12 ^ z));
+    for (int e = 0; e < 3; ++e) o.b[h][e] = (uint32_t)(row * XSTEP + 16 * (6 * h + 3 * g + e));
+  o.bs = (uint32_t)(row * XSTEP + 192);
   o.shift = (uint32_t)(8 * g);
   return o;
 }
@@ -493,17 +445,18 @@ __device__ __forceinline__ LaneMx<F> lane_mx(int wave_row0, int wm) {
 // accumulates the step in blk and adds it times its block scale
 // bscale(mi) (the fp32 scale cannot ride on the MFMA's E8M0 scales).
 template <typename F, typename MRow, typename BScale, typename Between>
-__device__ __forceinline__ void step_mx(const StageMx<F>& st, const LaneMx<F>& lo, v16f (&acc)[F::MI][NI4], MRow mrow,
-                                        BScale bscale, Between between) {
+__device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, const LaneMx<F>& lo,
+                                        v16f (&acc)[F::MI][NI4], MRow mrow, BScale bscale, Between between) {
+  constexpr int A_BYTES = F::TW * F::PIECES * 16;
   constexpr int MI = F::MI;
   uint32_t sa[MI];
   uint2 sb[NI4];
   if constexpr (!F::FP8) {
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) sa[mi] = *reinterpret_cast<const uint32_t*>(st.as + lo.as + 4 * mrow(mi));
+    for (int mi = 0; mi < MI; ++mi) sa[mi] = *reinterpret_cast<const uint32_t*>(sta + A_BYTES + lo.as + 4 * mrow(mi));
   }
 #pragma unroll
-  for (int ni = 0; ni < NI4; ++ni) sb[ni] = *reinterpret_cast<const uint2*>(st.b + lo.bs + 8192 * ni);
+  for (int ni = 0; ni < NI4; ++ni) sb[ni] = *reinterpret_cast<const uint2*>(stb + lo.bs + 32 * XSTEP * ni);
   v16f blk[F::FP8 ? MI : 1][NI4];
   if constexpr (F::FP8) {
 #pragma unroll
@@ -520,20 +473,20 @@ __device__ __forceinline__ void step_mx(const StageMx<F>& st, const LaneMx<F>& l
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       if constexpr (F::FP8) {
-        const uint8_t* p = st.a + lo.a + 128 * mrow(mi) + 1024 * h;
+        const uint8_t* p = sta + lo.a + 128 * mrow(mi) + 1024 * h;
         const uint4 v0 = *reinterpret_cast<const uint4*>(p);
         const uint4 v1 = *reinterpret_cast<const uint4*>(p + 512);
         a[mi] = v8i{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
       } else {
-        const uint4 v = *reinterpret_cast<const uint4*>(st.a + lo.a + 64 * mrow(mi) + 512 * h);
+        const uint4 v = *reinterpret_cast<const uint4*>(sta + lo.a + 64 * mrow(mi) + 512 * h);
         a[mi] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
       }
     }
 #pragma unroll
     for (int ni = 0; ni < NI4; ++ni) {
-      const uint4 b0 = *reinterpret_cast<const uint4*>(st.b + lo.b[h][0] + 8192 * ni);
-      const uint4 b1 = *reinterpret_cast<const uint4*>(st.b + lo.b[h][1] + 8192 * ni);
-      const uint4 b2 = *reinterpret_cast<const uint4*>(st.b + lo.b[h][2] + 8192 * ni);
+      const uint4 b0 = *reinterpret_cast<const uint4*>(stb + lo.b[h][0] + 32 * XSTEP * ni);
+      const uint4 b1 = *reinterpret_cast<const uint4*>(stb + lo.b[h][1] + 32 * XSTEP * ni);
+      const uint4 b2 = *reinterpret_cast<const uint4*>(stb + lo.b[h][2] + 32 * XSTEP * ni);
       const v8i bh = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, 0, 0};
       const v8i bl = {(int)b1.z, (int)b1.w, (int)b2.x, (int)b2.y, (int)b2.z, (int)b2.w, 0, 0};
       const int sbh = (int)(sb[ni].x >> sh), sbl = (int)(sb[ni].y >> sh);
@@ -572,10 +525,11 @@ __device__ __forceinline__ void step_mx(const StageMx<F>& st, const LaneMx<F>& l
   }
 }
 
-// Per-lane sources of one K step's loads: split rows, loads q = w + 8i (i = 0..3), rows
-// 4q + lane / 16; weights, loads q = w + 8i (fp4: group q; fp8: group q / 2, pieces
-// 4 (q % 2)..); MXFP4 scales, rows 64 w + lane. Offsets are taken at step 0; step ks adds
-// ks * XSTEP, ks * a_step and ks * s_step.
+// Per-lane sources of one K step's loads: split rows, loads q = w + 8i (i = 0..3) of 52
+// lanes, rows 4q + lane / 13, piece lane % 13 (LDS: slot + 832 q + 16 lane); weights, loads
+// q = w + 8i (fp4: group q; fp8: group q / 2, pieces 4 (q % 2)..); MXFP4 scales, rows
+// 64 w + lane. Offsets are taken at step 0; step ks adds ks * XSTEP, ks * a_step and
+// ks * s_step.
 template <typename F>
 struct LoaderMx {
   const uint8_t* b;
@@ -586,25 +540,21 @@ struct LoaderMx {
   uint32_t soff;
   uint32_t a_step, s_step;
 
-  // Part p (0..3) of step ks's loads into st: the weight loads (the longer way, from HBM)
-  // first, then the split rows. The K loop issues one part after each group of MFMAs, so
-  // no wave stalls for long on a full load queue with its MFMAs waiting behind.
-  __device__ __forceinline__ void issue_part(StageMx<F>& st, int ks, int p) {
+  // Half h (0, 1) of step ks's weight loads into weight slot `slot`: 2 loads, and for
+  // MXFP4 with h = 1 the scale load (5 instructions per step).
+  __device__ __forceinline__ void issue_a(uint8_t* slot, int ks, int h) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    if (p < 2) {
 #pragma unroll
-      for (int i = 2 * p; i < 2 * p + 2; ++i)
-        dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(st.a + (w + WAVES4 * i) * 1024));
-      if (!F::FP8 && p == 1) dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(st.as + 256 * w));
-    } else {
-#pragma unroll
-      for (int i = 2 * (p - 2); i < 2 * (p - 2) + 2; ++i)
-        dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(st.b + (w + WAVES4 * i) * 1024));
-    }
+    for (int i = 2 * h; i < 2 * h + 2; ++i)
+      dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(slot + (w + WAVES4 * i) * 1024));
+    if (!F::FP8 && h == 1) dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * w));
   }
-  __device__ __forceinline__ void issue(StageMx<F>& st, int ks) {
+  // Half h of step ks's split-row loads into split-row slot `slot` (4 instructions per step).
+  __device__ __forceinline__ void issue_b(uint8_t* slot, int ks, int h) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) issue_part(st, ks, p);
+    for (int i = 2 * h; i < 2 * h + 2; ++i)
+      if (threadIdx.x % 64 < 52) dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(slot + (w + WAVES4 * i) * 832));
   }
 };
 
@@ -612,10 +562,11 @@ struct LoaderMx {
 template <typename F, typename RowOff>
 __device__ __forceinline__ void split_row_offsets(LoaderMx<F>& ld, RowOff row_off) {
   const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int d = lane < 52 ? lane / 13 : 3, piece = lane < 52 ? lane % 13 : 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = 4 * (w + WAVES4 * i) + lane / 16;
-    ld.boff[i] = row_off(i, r) + 16u * (uint32_t)((lane % 16) ^ (r & 15));
+    const int r = 4 * (w + WAVES4 * i) + d;
+    ld.boff[i] = row_off(i, r) + 16u * (uint32_t)piece;
   }
 }
 
@@ -684,6 +635,115 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcn
 // This wave's LDS writes are done before its next LDS reads (and its reads before its writes).
 __device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// The ring wait leaving this wave's last N vector memory instructions (the deeper ring's
+// loads of the previous step) in flight: loads complete in issue order, and no store may
+// be outstanding.
+template <int N>
+__device__ __forceinline__ void ring_wait_keep();
+template <>
+__device__ __forceinline__ void ring_wait_keep<4>() {
+  asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+template <>
+__device__ __forceinline__ void ring_wait_keep<5>() {
+  asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Persistent K loop over this workgroup's tiles, as one flat sequence of 128-wide steps.
+// Step g reads weight slot g % DA and split-row slot g % DB. At the top of step g every
+// wave has step g's loads landed and is done with step g - 1's slots; the shallower ring
+// then loads step g + 1 into its freed slot and the deeper ring (depth D) step g + D - 1
+// (a tile's later step, or the next tile's first steps), each in two halves issued
+// between the step's MFMA groups, the deeper ring's last. With K steps fewer than D the
+// deeper ring also loads one step ahead. The next tile is set up (index loads, load
+// offsets) after the MFMAs of the step before its first loads; after an epilogue (whose
+// stores may complete out of order with loads) the top waits for everything.
+//   setup(j, tile) -> bool: fills tile j's state; false for a tile with no rows
+//   mfma(tile, wslot, rslot, k, load_part): step k of a tile, calling load_part(p) for
+//     p = 0..3 between its MFMAs
+//   epilogue(tile, wslot, rslot): after a tile's last step (its two slots are free)
+template <typename F, int DA, int DB, typename Tile, typename Setup, typename Mfma, typename Epilogue>
+__device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps, uint8_t* lds, Setup setup, Mfma mfma,
+                                                 Epilogue epilogue) {
+  using R = RingMx<F, DA, DB>;
+  constexpr bool A_DEEP = DA > DB;
+  constexpr int D = A_DEEP ? DA : DB, DS = A_DEEP ? DB : DA;
+  constexpr int N_DEEP = A_DEEP && !F::FP8 ? 5 : 4;  // deeper ring's load instructions per wave and step
+  if (tr.count == 0) return;
+  const int la = steps >= D ? D - 1 : 1;  // deeper ring's lookahead
+  auto wslot = [&](int i) { return lds + i * R::A_SLOT; };
+  auto rslot = [&](int i) { return lds + DA * R::A_SLOT + i * R::B_SLOT; };
+  // half h of tile t's step ks into slot i of the deeper (deep) or shallower ring
+  auto issue = [&](Tile& t, bool deep, int i, int ks, int h) {
+    if (deep == A_DEEP)
+      t.ld.issue_a(wslot(i), ks, h);
+    else
+      t.ld.issue_b(rslot(i), ks, h);
+  };
+  Tile cur, nxt;
+  bool cur_ok = setup(0, cur), nxt_ok = false;
+  if (cur_ok) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) issue(cur, false, 0, 0, h);
+    for (int d = 0; d < la; ++d)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) issue(cur, true, d, d, h);
+  }
+  const int total = tr.count * steps;
+  bool deep_last = false;  // the previous step's last loads were the deeper ring's
+  for (int g = 0; g < total; ++g) {
+    const int j = g / steps, k = g - j * steps;
+    if (k != 0 && la >= 2 && deep_last)
+      ring_wait_keep<N_DEEP>();
+    else
+      ring_wait_all();
+    // targets: 0 none, 1 this tile, 2 the next tile
+    const bool more = j + 1 < tr.count && nxt_ok;
+    const int ts = k + 1 < steps ? (cur_ok ? 1 : 0) : (more ? 2 : 0);
+    const int kd = k + la;
+    const int td = kd < steps ? (cur_ok ? 1 : 0) : (more ? 2 : 0);
+    const int ks_s = k + 1 < steps ? k + 1 : 0, ks_d = kd < steps ? kd : kd - steps;
+    const int sl_s = (g + 1) % DS, sl_d = (g + la) % D;
+    auto load_part = [&](int p) {
+      if (p < 2) {
+        if (ts == 1)
+          issue(cur, false, sl_s, ks_s, p);
+        else if (ts == 2)
+          issue(nxt, false, sl_s, ks_s, p);
+      } else {
+        if (td == 1)
+          issue(cur, true, sl_d, ks_d, p - 2);
+        else if (td == 2)
+          issue(nxt, true, sl_d, ks_d, p - 2);
+      }
+    };
+    if (cur_ok) {
+      mfma(cur, wslot(g % DA), rslot(g % DB), k, load_part);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) load_part(p);
+    }
+    deep_last = td != 0;
+    if (k == steps - la - 1 && j + 1 < tr.count) nxt_ok = setup(j + 1, nxt);
+    if (k == steps - 1) {
+      if (cur_ok) epilogue(cur, wslot(g % DA), rslot(g % DB));
+      if (steps == 1 && j + 1 < tr.count) {
+        nxt_ok = setup(j + 1, nxt);
+        if (nxt_ok) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            issue(nxt, false, (g + 1) % DS, 0, h);
+            issue(nxt, true, (g + 1) % D, 0, h);
+          }
+        }
+      }
+      cur = nxt;
+      cur_ok = nxt_ok;
+      nxt_ok = false;
+    }
+  }
+}
+
 // The expert regions of a tile (scalar loads only).
 __device__ __forceinline__ TileWeights tile_weights_s(const wm_fp8_experts& routed, const wm_fp8_experts& shared,
                                                       int expert) {
@@ -701,7 +761,7 @@ __device__ __forceinline__ int table_tiled(const wm_fp8_experts& t) { return t.t
 // gate_up: act rows of a tile's TG = TW / 2 intermediate columns; weight tile rows [0, TG)
 // are the gate rows nt * TG + j, [TG, TW) the matching up rows; wave wn owns gate rows
 // 32 (MI / 2) wn + [0, 32 MI / 2) (mi < MI / 2) and the same up rows (mi >= MI / 2).
-template <typename F, typename Table>
+template <typename F, int DA, int DB, typename Table>
 __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* __restrict__ x6,
                                                                  const int32_t* __restrict__ row_token, Lists L,
                                                                  Table routed, Table shared, uint8_t* __restrict__ a6) {
@@ -757,8 +817,8 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
   v16f acc[MI][NI4];
   zero_acc<F>(acc);
   auto mrow = [](int mi) { return (mi < HM ? 0 : TG) + 32 * (mi % HM); };
-  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k, auto load_part) {
-    step_mx<F>(st, lo, acc, mrow, [&](int mi) { return mi < HM ? t.s0[k] : t.s1[k]; }, load_part);
+  auto mfma = [&](const Tile& t, const uint8_t* wa, const uint8_t* rb, int k, auto load_part) {
+    step_mx<F>(wa, rb, lo, acc, mrow, [&](int mi) { return mi < HM ? t.s0[k] : t.s1[k]; }, load_part);
   };
 
   // Epilogue: lane (r, half) holds act rows 8 j + 4 half + q (j, q = 0..3; register 4 j + q)
@@ -767,10 +827,10 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
   // tile ni, for FP8 (one gate tile) block wn of row tile half. The lane forms the block's
   // two terms and writes them with the scales into the consumed stage as the tile's act
   // rows (TG / 128 steps of 208 bytes), which all threads then copy out row by row.
-  auto epilogue = [&](const Tile& t, StageMx<F>& st) {
-    constexpr int STG = TG / 128 * XSTEP;  // staged bytes per row
-    stage_barrier();
-    uint8_t* stg = reinterpret_cast<uint8_t*>(&st);
+  auto epilogue = [&](const Tile& t, uint8_t* wa, uint8_t* rb) {
+    constexpr int STG = TG / 128 * XSTEP;  // staged bytes per row: rows 0..63 in the split-row
+    stage_barrier();                       // slot (64 STG = its size for MXFP4), 64..127 in the weight slot
+    auto srow = [&](int lr) { return lr < 64 ? rb + lr * STG : wa + (lr - 64) * STG; };
     if (32 * HM * wn < t.valid) {
       const int r = lane % 32, half = lane / 32;
       auto act = [&](int b, int ni, int i) {
@@ -798,7 +858,7 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
         fp6_terms32(full, hi, lo6, s_hi, s_lo);
         const int lr = HM == 2 ? 64 * wm + 32 * pi + r : 64 * wm + 32 * half + r;
         const int kb = HM == 2 ? 2 * wn + half : wn;  // block of the tile: step kb / 4, block kb % 4
-        uint8_t* step = stg + lr * STG + (kb / 4) * XSTEP;
+        uint8_t* step = srow(lr) + (kb / 4) * XSTEP;
         uint4* dst = reinterpret_cast<uint4*>(step + (kb % 4) * 48);
         dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         dst[1] = make_uint4(hi[4], hi[5], lo6[0], lo6[1]);
@@ -812,20 +872,20 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
     const int n = (t.end - t.begin) * chunks;
     for (int idx = threadIdx.x; idx < n; idx += 64 * WAVES4) {
       const int lr = idx / chunks, c = idx - lr * chunks;
-      const uint4 v4 = *reinterpret_cast<const uint4*>(stg + lr * STG + 16 * c);
+      const uint4 v4 = *reinterpret_cast<const uint4*>(srow(lr) + 16 * c);
       *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(t.nt * TG / 128) * XSTEP + 16 * c) =
           v4;
     }
     zero_acc<F>(acc);
   };
 
-  __shared__ StageMx<F> s0, s1;
-  persistent_tiles<Tile>(tr, H / 128, s0, s1, setup, mfma, epilogue);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[RingMx<F, DA, DB>::BYTES];
+  persistent_tiles<F, DA, DB, Tile>(tr, H / 128, lds, setup, mfma, epilogue);
 }
 
 // down: out[row, n] = act[row] . W2[n], bf16, permuted rows (the combine applies the routing
 // weights); tile = 128 rows x TW output columns, wave wn owns columns 32 MI wn + [0, 32 MI).
-template <typename F, typename Table>
+template <typename F, int DA, int DB, typename Table>
 __global__ void __launch_bounds__(64 * WAVES4) down_mx_kernel(const uint8_t* __restrict__ a6, Lists L, Table routed,
                                                               Table shared, uint16_t* __restrict__ out) {
   constexpr int MI = F::MI;
@@ -860,18 +920,19 @@ __global__ void __launch_bounds__(64 * WAVES4) down_mx_kernel(const uint8_t* __r
 
   v16f acc[MI][NI4];
   zero_acc<F>(acc);
-  auto mfma = [&](const Tile& t, const StageMx<F>& st, int k, auto load_part) {
-    step_mx<F>(st, lo, acc, [](int mi) { return 32 * mi; }, [&](int) { return t.s0[k]; }, load_part);
+  auto mfma = [&](const Tile& t, const uint8_t* wa, const uint8_t* rb, int k, auto load_part) {
+    step_mx<F>(wa, rb, lo, acc, [](int mi) { return 32 * mi; }, [&](int) { return t.s0[k]; }, load_part);
   };
 
   // Epilogue: lane (r, half) holds output columns nt * TW + 32 MI wn + 32 mi + 8 j + 4 half + q
   // (register 4 j + q) of row 64 wm + 32 ni + r. Each wave turns 32 rows x 64 columns at a
   // time around in its own slice of the consumed stage (rows of 144 bytes) and stores each
   // row's 128 bytes as 8 lanes x 16.
-  auto epilogue = [&](const Tile& t, StageMx<F>& st) {
+  auto epilogue = [&](const Tile& t, uint8_t* wa, uint8_t* rb) {
     stage_barrier();
     if (32 * MI * wn < t.valid) {
-      uint8_t* slice = reinterpret_cast<uint8_t*>(&st) + wave * 4608;
+      // waves 0..5 in the weight slot, 6 and 7 in the split-row slot
+      uint8_t* slice = wave < 6 ? wa + wave * 4608 : rb + (wave - 6) * 4608;
       const int r = lane % 32, half = lane / 32;
 #pragma unroll
       for (int ni = 0; ni < NI4; ++ni)
@@ -902,8 +963,8 @@ __global__ void __launch_bounds__(64 * WAVES4) down_mx_kernel(const uint8_t* __r
     zero_acc<F>(acc);
   };
 
-  __shared__ StageMx<F> s0, s1;
-  persistent_tiles<Tile>(tr, I / 128, s0, s1, setup, mfma, epilogue);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[RingMx<F, DA, DB>::BYTES];
+  persistent_tiles<F, DA, DB, Tile>(tr, I / 128, lds, setup, mfma, epilogue);
 }
 
 // Token of every permuted row: order[p] / K for routed rows, p - P for the shared rows.
@@ -1123,13 +1184,13 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
   uint16_t* out_rows = (uint16_t*)(base + p.rows);
   TimingEvents* te = g_timing.load() ? timing_events() : nullptr;
   if (te) check_hip(hipEventRecord(te->ev[0], s), "hipEventRecord");
-  hipLaunchKernelGGL((gate_up_mx_kernel<F, Table>), grid_for((I + F::TW / 2 - 1) / (F::TW / 2)), dim3(64 * WAVES4), 0,
-                     s, x6, row_token, L, routed, sh, a6);
+  hipLaunchKernelGGL((gate_up_mx_kernel<F, F::DA, F::DB, Table>), grid_for((I + F::TW / 2 - 1) / (F::TW / 2)),
+                     dim3(64 * WAVES4), 0, s, x6, row_token, L, routed, sh, a6);
   check_launch("gate_up");
   if (te) check_hip(hipEventRecord(te->ev[1], s), "hipEventRecord");
   // unweighted rows: the combine applies the routing weights and the shared gate
-  hipLaunchKernelGGL((down_mx_kernel<F, Table>), grid_for((H + F::TW - 1) / F::TW), dim3(64 * WAVES4), 0, s, a6, L,
-                     routed, sh, out_rows);
+  hipLaunchKernelGGL((down_mx_kernel<F, F::DA, F::DB, Table>), grid_for((H + F::TW - 1) / F::TW), dim3(64 * WAVES4), 0,
+                     s, a6, L, routed, sh, out_rows);
   check_launch("down");
   if (te) check_hip(hipEventRecord(te->ev[2], s), "hipEventRecord");
   if (combine)
