@@ -38,6 +38,7 @@ CASES = {  # name: (H, I, E, K, T)
     "decode-small": (1024, 1024, 16, 4, 2),
     "prefill-small": (1024, 1024, 16, 4, 300),
     "prefill-odd": (640, 384, 8, 2, 70),   # multiples of 128 only: GEMM path even at small T
+    "prefill-tiny-k": (256, 128, 8, 2, 150),  # 2 and 1 K steps per tile: the rings' short paths
     "c4-decode": (7168, 2048, 8, 4, 1),
 }
 
@@ -104,7 +105,7 @@ def test_fp8_prefill_layout_bytes(device):
         np.testing.assert_array_equal(tiled.w2_scales[e].cpu().numpy(), a["w2_scales"][s])
 
 
-@pytest.mark.parametrize("case", ["decode-small", "prefill-small", "prefill-odd"])
+@pytest.mark.parametrize("case", ["decode-small", "prefill-small", "prefill-odd", "prefill-tiny-k"])
 def test_fp8_prefill_layout_matches_oracle_and_row_layout(device, case):
     """Tables in the prefill tile layout take the grouped GEMM at every batch size; the GEMM
     reads the same bytes in the same order, so its output equals the row layout's bit for bit

@@ -89,10 +89,6 @@ __device__ __forceinline__ const_f32_ptr uniform_ptr(const float* p) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return (const_f32_ptr)(((uint64_t)hi << 32) | lo);
 }
-__device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ float uniform_f(float v) {
-  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
-}
 __device__ __forceinline__ const uint8_t* uniform_u8(const uint8_t* p) {
   const uint64_t v = (uint64_t)(uintptr_t)p;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
@@ -147,12 +143,11 @@ struct TileWeights {
 //
 // Split rows (x, and act for the down GEMM): per row, per 128-wide K step, 208 bytes: the
 // 4 blocks' terms (hi fields 24 bytes, lo fields 24 bytes, each), then the 4 blocks' hi
-// E8M0 bytes, their lo bytes, and 8 bytes of padding. The GEMMs load whole 256-byte row
-// steps, so a buffer of split rows ends with XSLACK spare bytes.
+// E8M0 bytes, their lo bytes, and 8 bytes of padding. The GEMMs load a row's step as 13
+// pieces of 16 bytes.
 
 constexpr int FMT_FP6 = 2;
 constexpr int XSTEP = 208;
-constexpr int XSLACK = 256;
 
 // E8M0 exponent that maps a block maximum into [4, 8) (never below 1, so 2^(127 - s) stays
 // a normal float).
@@ -385,16 +380,18 @@ __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& ro
 //   fp8 A: row r's K [16g, 16g + 16) in bytes 0-15 and [32 + 16g, 32 + 16g + 16) in 16-31;
 //   fp6 B: row r's K [32g, 32g + 32) as contiguous 6-bit fields, 24 bytes;
 //   scale lane (r, g): K block g; result register i: D[8 (i / 4) + 4 g + i % 4][r].
-// DA, DB: depths of the weight and split-row rings
+// WAVES: waves per workgroup (4: one per SIMD, 8: two); MI = TW / (16 WAVES) weight tiles
+// of 32 rows per wave; DA, DB: depths of the weight and split-row rings.
 struct Mx4 {
   static constexpr bool FP8 = false;
-  static constexpr int TW = 512, MI = 4, PIECES = 4, A_FMT = FMT_FP4, DA = 2, DB = 3;
+  static constexpr int TW = 512, PIECES = 4, A_FMT = FMT_FP4, DA = 2, DB = 3, WAVES = 8;
+  static constexpr int MI = TW / (16 * WAVES);
 };
 struct Mx8 {
   static constexpr bool FP8 = true;
-  static constexpr int TW = 256, MI = 2, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2;
+  static constexpr int TW = 256, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2, WAVES = 8;
+  static constexpr int MI = TW / (16 * WAVES);
 };
-constexpr int WAVES4 = 8;
 constexpr int NI4 = 2;      // 32-row row tiles per wave
 
 // LDS of a workgroup: a ring of DA weight slots (a step's weight rows, then MXFP4 their
@@ -535,26 +532,31 @@ struct LoaderMx {
   const uint8_t* b;
   const uint8_t* wbase;
   const uint8_t* sbase;
-  uint32_t boff[4];
-  uint32_t aoff[4];
-  uint32_t soff;
+  static constexpr int NQ = 32 / F::WAVES;                // 1 KB loads per wave and operand
+  static constexpr int SQ = F::FP8 ? 0 : 8 / F::WAVES;     // MXFP4 scale loads per wave
+  uint32_t boff[NQ];
+  uint32_t aoff[NQ];
+  uint32_t soff[SQ > 0 ? SQ : 1];
   uint32_t a_step, s_step;
 
-  // Half h (0, 1) of step ks's weight loads into weight slot `slot`: 2 loads, and for
-  // MXFP4 with h = 1 the scale load (5 instructions per step).
+  // Half h (0, 1) of step ks's weight loads into weight slot `slot`: NQ / 2 loads, and for
+  // MXFP4 with h = 1 the scale loads (NQ + SQ instructions per step).
   __device__ __forceinline__ void issue_a(uint8_t* slot, int ks, int h) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
 #pragma unroll
-    for (int i = 2 * h; i < 2 * h + 2; ++i)
-      dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(slot + (w + WAVES4 * i) * 1024));
-    if (!F::FP8 && h == 1) dma4(sbase, soff + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * w));
+    for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
+      dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(slot + (w + F::WAVES * i) * 1024));
+    if (h == 1)
+#pragma unroll
+      for (int q = 0; q < SQ; ++q)
+        dma4(sbase, soff[q] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * (w + F::WAVES * q)));
   }
-  // Half h of step ks's split-row loads into split-row slot `slot` (4 instructions per step).
+  // Half h of step ks's split-row loads into split-row slot `slot` (NQ instructions per step).
   __device__ __forceinline__ void issue_b(uint8_t* slot, int ks, int h) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
 #pragma unroll
-    for (int i = 2 * h; i < 2 * h + 2; ++i)
-      if (threadIdx.x % 64 < 52) dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(slot + (w + WAVES4 * i) * 832));
+    for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
+      if (threadIdx.x % 64 < 52) dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(slot + (w + F::WAVES * i) * 832));
   }
 };
 
@@ -564,8 +566,8 @@ __device__ __forceinline__ void split_row_offsets(LoaderMx<F>& ld, RowOff row_of
   const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int d = lane < 52 ? lane / 13 : 3, piece = lane < 52 ? lane % 13 : 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * (w + WAVES4 * i) + d;
+  for (int i = 0; i < LoaderMx<F>::NQ; ++i) {
+    const int r = 4 * (w + F::WAVES * i) + d;
     ld.boff[i] = row_off(i, r) + 16u * (uint32_t)piece;
   }
 }
@@ -578,35 +580,38 @@ __device__ __forceinline__ void weight_offsets(LoaderMx<F>& ld, const uint8_t* w
   const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
   ld.wbase = uniform_u8(w_region);
   ld.sbase = uniform_u8(s_region);
+  constexpr int NQ = LoaderMx<F>::NQ, SQ = LoaderMx<F>::SQ;
   if constexpr (F::FP8) {
     if (tiled) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = w + WAVES4 * i;
+      for (int i = 0; i < NQ; ++i) {
+        const int q = w + F::WAVES * i;
         ld.aoff[i] = (uint32_t)(row_of(16 * (q / 2)) / 16 * 2048 + 1024 * (q % 2) + 16 * lane);
       }
       ld.a_step = (uint32_t)(rows * 128);
     } else {  // row layout: [rows][k] bytes, 128 per step
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = w + WAVES4 * i;
+      for (int i = 0; i < NQ; ++i) {
+        const int q = w + F::WAVES * i;
         ld.aoff[i] = (uint32_t)(row_of(16 * (q / 2) + lane % 16) * k + 16 * (4 * (q % 2) + lane / 16));
       }
       ld.a_step = 128;
     }
-    ld.soff = 0;
+    ld.soff[0] = 0;
     ld.s_step = 0;
   } else if (tiled) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + WAVES4 * i)) / 16 * 1024 + 16 * lane);
-    ld.soff = (uint32_t)(row_of(64 * w + lane) * 4);
+    for (int i = 0; i < NQ; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::WAVES * i)) / 16 * 1024 + 16 * lane);
+#pragma unroll
+    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::WAVES * q) + lane) * 4);
     ld.a_step = (uint32_t)(rows * 64);
     ld.s_step = (uint32_t)(rows * 4);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      ld.aoff[i] = (uint32_t)(row_of(16 * (w + WAVES4 * i) + lane % 16) * (k / 2) + 16 * (lane / 16));
-    ld.soff = (uint32_t)(row_of(64 * w + lane) * (k / 32));
+    for (int i = 0; i < NQ; ++i)
+      ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::WAVES * i) + lane % 16) * (k / 2) + 16 * (lane / 16));
+#pragma unroll
+    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::WAVES * q) + lane) * (k / 32));
     ld.a_step = 64;
     ld.s_step = 4;
   }
@@ -648,6 +653,14 @@ template <>
 __device__ __forceinline__ void ring_wait_keep<5>() {
   asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+template <>
+__device__ __forceinline__ void ring_wait_keep<8>() {
+  asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+template <>
+__device__ __forceinline__ void ring_wait_keep<10>() {
+  asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // Persistent K loop over this workgroup's tiles, as one flat sequence of 128-wide steps.
 // Step g reads weight slot g % DA and split-row slot g % DB. At the top of step g every
@@ -668,7 +681,8 @@ __device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps,
   using R = RingMx<F, DA, DB>;
   constexpr bool A_DEEP = DA > DB;
   constexpr int D = A_DEEP ? DA : DB, DS = A_DEEP ? DB : DA;
-  constexpr int N_DEEP = A_DEEP && !F::FP8 ? 5 : 4;  // deeper ring's load instructions per wave and step
+  // deeper ring's load instructions per wave and step
+  constexpr int N_DEEP = LoaderMx<F>::NQ + (A_DEEP ? LoaderMx<F>::SQ : 0);
   if (tr.count == 0) return;
   const int la = steps >= D ? D - 1 : 1;  // deeper ring's lookahead
   auto wslot = [&](int i) { return lds + i * R::A_SLOT; };
@@ -762,7 +776,7 @@ __device__ __forceinline__ int table_tiled(const wm_fp8_experts& t) { return t.t
 // are the gate rows nt * TG + j, [TG, TW) the matching up rows; wave wn owns gate rows
 // 32 (MI / 2) wn + [0, 32 MI / 2) (mi < MI / 2) and the same up rows (mi >= MI / 2).
 template <typename F, int DA, int DB, typename Table>
-__global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* __restrict__ x6,
+__global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel(const uint8_t* __restrict__ x6,
                                                                  const int32_t* __restrict__ row_token, Lists L,
                                                                  Table routed, Table shared, uint8_t* __restrict__ a6) {
   constexpr int TG = F::TW / 2, MI = F::MI, HM = MI / 2;
@@ -801,7 +815,7 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
     t.ld.b = uniform_u8(x6);
     // tokens of this lane's split rows 4q + 0..3 (q = w + 8i), through scalar loads
     split_row_offsets<F>(t.ld, [&](int i, int r) {
-      const int q0 = 4 * (__builtin_amdgcn_readfirstlane(threadIdx.x / 64) + WAVES4 * i);
+      const int q0 = 4 * (__builtin_amdgcn_readfirstlane(threadIdx.x / 64) + F::WAVES * i);
       int tok = 0;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
@@ -841,14 +855,17 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
         }
         return silu(gv) * uv;
       };
-      constexpr int PAIRS = HM == 2 ? NI4 : 1;  // MXFP4: one swap per row tile; FP8: one in all
+      // HM >= 2: the swap pairs gate tiles (2p, 2p + 1) of row tile ni, lane half h taking
+      // tile 2p + h; HM = 1: it pairs row tiles 0 and 1 of the one gate tile
+      constexpr int PAIRS = HM >= 2 ? NI4 * HM / 2 : 1;
 #pragma unroll
       for (int pi = 0; pi < PAIRS; ++pi) {
+        const int ni = HM >= 2 ? pi / (HM / 2) : 0, p = HM >= 2 ? pi % (HM / 2) : 0;
         float full[32];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float x0 = HM == 2 ? act(0, pi, i) : act(0, 0, i);
-          const float x1 = HM == 2 ? act(1 % HM, pi, i) : act(0, 1, i);
+          const float x0 = HM >= 2 ? act(2 * p, ni, i) : act(0, 0, i);
+          const float x1 = HM >= 2 ? act((2 * p + 1) % HM, ni, i) : act(0, 1, i);
           const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
           full[8 * (i / 4) + i % 4] = __uint_as_float(pr[0]);
           full[8 * (i / 4) + 4 + i % 4] = __uint_as_float(pr[1]);
@@ -856,8 +873,8 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
         v6u_t hi, lo6;
         int s_hi, s_lo;
         fp6_terms32(full, hi, lo6, s_hi, s_lo);
-        const int lr = HM == 2 ? 64 * wm + 32 * pi + r : 64 * wm + 32 * half + r;
-        const int kb = HM == 2 ? 2 * wn + half : wn;  // block of the tile: step kb / 4, block kb % 4
+        const int lr = HM >= 2 ? 64 * wm + 32 * ni + r : 64 * wm + 32 * half + r;
+        const int kb = HM >= 2 ? HM * wn + 2 * p + half : wn;  // block of the tile: step kb / 4, block kb % 4
         uint8_t* step = srow(lr) + (kb / 4) * XSTEP;
         uint4* dst = reinterpret_cast<uint4*>(step + (kb % 4) * 48);
         dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -870,7 +887,7 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
     stage_barrier();
     const int chunks = t.valid / 128 * (XSTEP / 16);  // 16-byte pieces of a row's act steps
     const int n = (t.end - t.begin) * chunks;
-    for (int idx = threadIdx.x; idx < n; idx += 64 * WAVES4) {
+    for (int idx = threadIdx.x; idx < n; idx += 64 * F::WAVES) {
       const int lr = idx / chunks, c = idx - lr * chunks;
       const uint4 v4 = *reinterpret_cast<const uint4*>(srow(lr) + 16 * c);
       *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(t.nt * TG / 128) * XSTEP + 16 * c) =
@@ -886,7 +903,7 @@ __global__ void __launch_bounds__(64 * WAVES4) gate_up_mx_kernel(const uint8_t* 
 // down: out[row, n] = act[row] . W2[n], bf16, permuted rows (the combine applies the routing
 // weights); tile = 128 rows x TW output columns, wave wn owns columns 32 MI wn + [0, 32 MI).
 template <typename F, int DA, int DB, typename Table>
-__global__ void __launch_bounds__(64 * WAVES4) down_mx_kernel(const uint8_t* __restrict__ a6, Lists L, Table routed,
+__global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) down_mx_kernel(const uint8_t* __restrict__ a6, Lists L, Table routed,
                                                               Table shared, uint16_t* __restrict__ out) {
   constexpr int MI = F::MI;
   const int H = routed.hidden, I = routed.inter;
@@ -1085,8 +1102,7 @@ struct Layout {
   size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, row_token, x6, a6, rows, total;
 };
 
-// Split rows take XSTEP bytes per 128-wide K step (E2M3 terms with their scales inside);
-// each split buffer ends with XSLACK spare bytes.
+// Split rows take XSTEP bytes per 128-wide K step (E2M3 terms with their scales inside).
 static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool has_shared) {
   const int64_t pairs = (int64_t)tokens * k;
   const int64_t rows = pairs + (has_shared ? tokens : 0);
@@ -1101,8 +1117,8 @@ static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool
   p.tile_count = at; at += align256(sizeof(int32_t));
   p.gate = at;       at += align256(sizeof(float) * (size_t)(tokens > 0 ? tokens : 1));
   p.row_token = at;  at += align256(sizeof(int32_t) * (size_t)(rows > 0 ? rows : 1));
-  p.x6 = at;         at += align256((size_t)tokens * (hidden / 128) * XSTEP + XSLACK);
-  p.a6 = at;         at += align256((size_t)rows * (inter / 128) * XSTEP + XSLACK);
+  p.x6 = at;         at += align256((size_t)tokens * (hidden / 128) * XSTEP);
+  p.a6 = at;         at += align256((size_t)rows * (inter / 128) * XSTEP);
   p.rows = at;       at += align256(sizeof(uint16_t) * (size_t)rows * hidden);
   p.total = at;
   return p;
@@ -1185,11 +1201,11 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
   TimingEvents* te = g_timing.load() ? timing_events() : nullptr;
   if (te) check_hip(hipEventRecord(te->ev[0], s), "hipEventRecord");
   hipLaunchKernelGGL((gate_up_mx_kernel<F, F::DA, F::DB, Table>), grid_for((I + F::TW / 2 - 1) / (F::TW / 2)),
-                     dim3(64 * WAVES4), 0, s, x6, row_token, L, routed, sh, a6);
+                     dim3(64 * F::WAVES), 0, s, x6, row_token, L, routed, sh, a6);
   check_launch("gate_up");
   if (te) check_hip(hipEventRecord(te->ev[1], s), "hipEventRecord");
   // unweighted rows: the combine applies the routing weights and the shared gate
-  hipLaunchKernelGGL((down_mx_kernel<F, F::DA, F::DB, Table>), grid_for((H + F::TW - 1) / F::TW), dim3(64 * WAVES4), 0,
+  hipLaunchKernelGGL((down_mx_kernel<F, F::DA, F::DB, Table>), grid_for((H + F::TW - 1) / F::TW), dim3(64 * F::WAVES), 0,
                      s, a6, L, routed, sh, out_rows);
   check_launch("down");
   if (te) check_hip(hipEventRecord(te->ev[2], s), "hipEventRecord");
