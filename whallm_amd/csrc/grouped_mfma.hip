@@ -319,14 +319,20 @@ __device__ __forceinline__ bool resolve_tile_s(const Lists& L, int m, int& exper
   return true;
 }
 
-// (row tile, column tile) of logical work tile `logical`. The list is blocked by expert
-// (the shared expert's row tiles are one more block): a block of c row tiles takes
-// c * n_tiles consecutive logical tiles, column-major, so the row tiles that read the same
-// weight columns are adjacent and run together on one XCD (one L2 fetch of the weights),
-// while a row tile's column tiles stay within c * n_tiles of each other (its split rows
-// stay in L2). Scalar loads only.
+// (row tile, column tile) of logical work tile `logical`. With more than 4 column tiles
+// the list is blocked by expert (the shared expert's row tiles are one more block) and
+// column-major inside a block, so the row tiles that read the same weight columns run
+// together on one XCD (one L2 fetch of the weights; C4: 11.8 -> 9.6 GB of gate_up HBM
+// reads). With 4 or fewer it is row-major: a row tile's column tiles run together (its
+// split rows stay in L2) while the W workgroups of an XCD still cover W / n_tiles row tiles
+// of an expert at a time (measured faster for C3's down GEMM). Scalar loads only.
 __device__ __forceinline__ void order_tile(const Lists& L, int logical, int n_tiles, int& mt, int& nt) {
   const int m0 = logical / n_tiles;
+  if (n_tiles <= 4) {
+    mt = m0;
+    nt = logical - m0 * n_tiles;
+    return;
+  }
   const int routed = scalar_i32(L.tile_count, 0);
   int t0, c;
   if (m0 < routed) {
@@ -1037,21 +1043,27 @@ __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __res
       acc[2 * q + 1] = fmaf(s, bf16_bits_to_f32(w[q] >> 16), acc[2 * q + 1]);
     }
   };
-  // the rows of up to 8 pairs are loaded before any is summed (sums stay in k order)
-  constexpr int BATCH = 8;
-  for (int j0 = 0; j0 < k; j0 += BATCH) {
+  // the rows of up to 16 pairs (and the shared row, when it fits in the batch) are loaded
+  // before any is summed (sums stay in k order, the shared row last)
+  constexpr int BATCH = 16;
+  const int n = k + (has_shared ? 1 : 0);
+  for (int j0 = 0; j0 < n; j0 += BATCH) {
     int row[BATCH];
     uint4 v[BATCH];
 #pragma unroll
-    for (int q = 0; q < BATCH; ++q) row[q] = j0 + q < k ? inverse[t * k + j0 + q] : -1;
+    for (int q = 0; q < BATCH; ++q) {
+      const int j = j0 + q;
+      row[q] = j < k ? inverse[t * k + j] : (j < n ? pairs + t : -1);
+    }
 #pragma unroll
     for (int q = 0; q < BATCH; ++q)
       if (row[q] >= 0) v[q] = reinterpret_cast<const uint4*>(rows + (int64_t)row[q] * hidden)[c8];
 #pragma unroll
-    for (int q = 0; q < BATCH; ++q)
-      if (row[q] >= 0) add(v[q], weights[t * k + j0 + q]);
+    for (int q = 0; q < BATCH; ++q) {
+      const int j = j0 + q;
+      if (row[q] >= 0) add(v[q], j < k ? weights[t * k + j] : gate[t]);
+    }
   }
-  if (has_shared) add(reinterpret_cast<const uint4*>(rows + (int64_t)(pairs + t) * hidden)[c8], gate[t]);
   uint4 o;
   o.x = f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16);
   o.y = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
