@@ -390,12 +390,12 @@ __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& ro
 // of 32 rows per wave; DA, DB: depths of the weight and split-row rings.
 struct Mx4 {
   static constexpr bool FP8 = false;
-  static constexpr int TW = 512, PIECES = 4, A_FMT = FMT_FP4, DA = 2, DB = 3, WAVES = 8;
+  static constexpr int TW = 512, PIECES = 4, A_FMT = FMT_FP4, DA = 2, DB = 3, WAVES = 8, LW = 8;
   static constexpr int MI = TW / (16 * WAVES);
 };
 struct Mx8 {
   static constexpr bool FP8 = true;
-  static constexpr int TW = 256, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2, WAVES = 8;
+  static constexpr int TW = 256, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2, WAVES = 8, LW = 8;
   static constexpr int MI = TW / (16 * WAVES);
 };
 constexpr int NI4 = 2;      // 32-row row tiles per wave
@@ -538,8 +538,8 @@ struct LoaderMx {
   const uint8_t* b;
   const uint8_t* wbase;
   const uint8_t* sbase;
-  static constexpr int NQ = 32 / F::WAVES;                // 1 KB loads per wave and operand
-  static constexpr int SQ = F::FP8 ? 0 : 8 / F::WAVES;     // MXFP4 scale loads per wave
+  static constexpr int NQ = 32 / F::LW;                // 1 KB loads per wave and operand
+  static constexpr int SQ = F::FP8 ? 0 : 8 / F::LW;     // MXFP4 scale loads per wave
   uint32_t boff[NQ];
   uint32_t aoff[NQ];
   uint32_t soff[SQ > 0 ? SQ : 1];
@@ -549,20 +549,22 @@ struct LoaderMx {
   // MXFP4 with h = 1 the scale loads (NQ + SQ instructions per step).
   __device__ __forceinline__ void issue_a(uint8_t* slot, int ks, int h) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    if (F::LW < F::WAVES && w >= F::LW) return;
 #pragma unroll
     for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
-      dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(slot + (w + F::WAVES * i) * 1024));
+      dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(slot + (w + F::LW * i) * 1024));
     if (h == 1)
 #pragma unroll
       for (int q = 0; q < SQ; ++q)
-        dma4(sbase, soff[q] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * (w + F::WAVES * q)));
+        dma4(sbase, soff[q] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * (w + F::LW * q)));
   }
   // Half h of step ks's split-row loads into split-row slot `slot` (NQ instructions per step).
   __device__ __forceinline__ void issue_b(uint8_t* slot, int ks, int h) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    if (F::LW < F::WAVES && w >= F::LW) return;
 #pragma unroll
     for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
-      if (threadIdx.x % 64 < 52) dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(slot + (w + F::WAVES * i) * 832));
+      if (threadIdx.x % 64 < 52) dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(slot + (w + F::LW * i) * 832));
   }
 };
 
@@ -573,7 +575,7 @@ __device__ __forceinline__ void split_row_offsets(LoaderMx<F>& ld, RowOff row_of
   const int d = lane < 52 ? lane / 13 : 3, piece = lane < 52 ? lane % 13 : 0;
 #pragma unroll
   for (int i = 0; i < LoaderMx<F>::NQ; ++i) {
-    const int r = 4 * (w + F::WAVES * i) + d;
+    const int r = 4 * (w + F::LW * i) + d;
     ld.boff[i] = row_off(i, r) + 16u * (uint32_t)piece;
   }
 }
@@ -591,14 +593,14 @@ __device__ __forceinline__ void weight_offsets(LoaderMx<F>& ld, const uint8_t* w
     if (tiled) {
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
-        const int q = w + F::WAVES * i;
+        const int q = w + F::LW * i;
         ld.aoff[i] = (uint32_t)(row_of(16 * (q / 2)) / 16 * 2048 + 1024 * (q % 2) + 16 * lane);
       }
       ld.a_step = (uint32_t)(rows * 128);
     } else {  // row layout: [rows][k] bytes, 128 per step
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
-        const int q = w + F::WAVES * i;
+        const int q = w + F::LW * i;
         ld.aoff[i] = (uint32_t)(row_of(16 * (q / 2) + lane % 16) * k + 16 * (4 * (q % 2) + lane / 16));
       }
       ld.a_step = 128;
@@ -607,17 +609,17 @@ __device__ __forceinline__ void weight_offsets(LoaderMx<F>& ld, const uint8_t* w
     ld.s_step = 0;
   } else if (tiled) {
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::WAVES * i)) / 16 * 1024 + 16 * lane);
+    for (int i = 0; i < NQ; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::LW * i)) / 16 * 1024 + 16 * lane);
 #pragma unroll
-    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::WAVES * q) + lane) * 4);
+    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::LW * q) + lane) * 4);
     ld.a_step = (uint32_t)(rows * 64);
     ld.s_step = (uint32_t)(rows * 4);
   } else {
 #pragma unroll
     for (int i = 0; i < NQ; ++i)
-      ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::WAVES * i) + lane % 16) * (k / 2) + 16 * (lane / 16));
+      ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::LW * i) + lane % 16) * (k / 2) + 16 * (lane / 16));
 #pragma unroll
-    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::WAVES * q) + lane) * (k / 32));
+    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::LW * q) + lane) * (k / 32));
     ld.a_step = 64;
     ld.s_step = 4;
   }
@@ -821,7 +823,7 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
     t.ld.b = uniform_u8(x6);
     // tokens of this lane's split rows 4q + 0..3 (q = w + 8i), through scalar loads
     split_row_offsets<F>(t.ld, [&](int i, int r) {
-      const int q0 = 4 * (__builtin_amdgcn_readfirstlane(threadIdx.x / 64) + F::WAVES * i);
+      const int q0 = 4 * (__builtin_amdgcn_readfirstlane(threadIdx.x / 64) + F::LW * i);
       int tok = 0;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
