@@ -128,3 +128,43 @@ def test_fp8_prefill_layout_matches_oracle_and_row_layout(device, case):
     close(y.float().cpu().numpy(), want, f"tiled {case}")
     if T * K > 256 or H % 1024 or I % 1024:  # the row layout takes the grouped GEMM as well
         assert torch.equal(y, wa.moe_fp8(xt, it, wt, rows, rows_sh, None)), case
+
+
+def test_fp8_edges_empty_k1_slots_and_invalid_ids(device):
+    """Grouped-GEMM path edges (H = 256 is not a decode shape): empty batches in both
+    layouts, K = 1, experts resolved through a slot pool, and an out-of-range expert id."""
+    H, I, E, pool = 256, 128, 6, 9
+    rng = np.random.default_rng(41)
+    a = S.fp8_experts_np(rng, pool, H, I)
+    slots = np.array([7, 2, 0, 5, 8, 3], np.int32)
+    table = S.fp8_experts_to_device(a, device, slots=torch.from_numpy(slots).to(device), experts=E)
+    tiled = wa.prefill_layout(table)
+    # empty batches
+    x0 = torch.empty(0, H, dtype=torch.bfloat16, device=device)
+    i0 = torch.empty(0, 2, dtype=torch.int32, device=device)
+    w0 = torch.empty(0, 2, dtype=torch.float32, device=device)
+    for tab in (table, tiled):
+        assert wa.moe_fp8(x0, i0, w0, tab).shape == (0, H)
+        assert wa.experts_fp8(x0, i0, tab).shape == (0, 2, H)
+    # K = 1 and the slot map (pool entry slots[e] holds expert e)
+    T = 200
+    x = S.bf16_normal_np(rng, (T, H))
+    idx = rng.integers(0, E, size=(T, 1)).astype(np.int32)
+    w = rng.uniform(0.2, 1.0, size=(T, 1)).astype(np.float32)
+    xt, it, wt = S.bf16_bits_to_tensor(x, device), torch.from_numpy(idx).to(device), torch.from_numpy(w).to(device)
+    pool_ex = oracle_experts(a, pool)
+    ex = {e: pool_ex[int(slots[e])] for e in range(E)}
+    xf = S.bf16_bits_to_f32(x)
+    want = M.combine(M.routed_outputs(xf, idx, ex, ffn=M.fp8_expert_ffn), w, None, None)
+    for tab, what in ((table, "slots"), (tiled, "slots tiled")):
+        y = wa.moe_fp8(xt, it, wt, tab)
+        close(y.float().cpu().numpy(), want, what)
+    # an out-of-range id: rejected when validated; otherwise its pair contributes nothing
+    bad = it.clone()
+    bad[0, 0] = E
+    with pytest.raises(ValueError):
+        wa.moe_fp8(xt, bad, wt, table, validate=True)
+    out = wa.experts_fp8(xt, bad, table)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[0, 0]).item() == 0
+    close(out[1:, 0].float().cpu().numpy(), M.routed_outputs(xf, idx, ex, ffn=M.fp8_expert_ffn)[1:, 0], "valid pairs")
