@@ -294,6 +294,27 @@ WM_EXPORT int wm_slot_cache_plan(wm_slot_cache* cache, int32_t file, const int32
  * for the fills, so work enqueued after this call sees the experts resident. */
 WM_EXPORT int wm_slot_cache_acquire(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
                                     int32_t* out_slots, void* compute_stream);
+/* Route mode (ExpertCache with eviction_policy "route", expert_cache.py:1131-1181): scores
+ * [files * experts] (host, the route policy's retention scores) and quotas [files] (its
+ * per-file slot targets) are copied; later victims are the resident expert with the lowest
+ * (tier, score, last access), tier 0 = files over quota (or the incoming file at quota),
+ * never one handed out by the same plan. scores NULL returns to LFU. Call again after each
+ * rebalance of the policy (RouteCachePolicy.rebalance, route_cache.py:68-95). */
+WM_EXPORT int wm_slot_cache_set_route(wm_slot_cache* cache, const double* scores, const int32_t* quotas);
+/* The whole file (experts * blob_bytes) from the host pool into device buffer dst with one
+ * hipMemcpyAsync on the copy stream, after the work already on compute_stream (which may
+ * still read dst): the reference's background whole-layer read into one of two layer
+ * buffers (wait_layer / read_layer, engine.mm:1647-1661). */
+WM_EXPORT int wm_slot_cache_read_layer(wm_slot_cache* cache, int32_t file, void* dst, void* compute_stream);
+/* compute_stream waits for the last read_layer of `file`. */
+WM_EXPORT int wm_slot_cache_wait_layer(wm_slot_cache* cache, int32_t file, void* compute_stream);
+/* Prompt-tail seeding (seed_layer, engine.mm:1664-1678; hot_tail_experts,
+ * qwen_streaming_policy.py:23-45): plan experts[n] of `file` in the given order (least
+ * valuable first), set their use counts to uses[n] (nullable), and fill the misses from
+ * `layer` (a device copy of the whole file, as read_layer writes it) device to device on the
+ * copy stream; compute_stream then waits for them. out_slots[n] receives the slots. */
+WM_EXPORT int wm_slot_cache_seed(wm_slot_cache* cache, int32_t file, const int32_t* experts, const int32_t* uses,
+                                 int32_t n, const void* layer, int32_t* out_slots, void* compute_stream);
 /* out4 = (hits, misses, bytes copied, fills) since open. */
 WM_EXPORT int wm_slot_cache_stats(const wm_slot_cache* cache, int64_t* out4);
 

@@ -96,3 +96,52 @@ def test_fill_waits_for_work_that_reads_the_evicted_slots(device):
     want = M.combine(M.routed_outputs(S.bf16_bits_to_f32(x[:64]), idx[:64], ex), w[:64])
     rel = np.linalg.norm(got[:64] - want) / np.linalg.norm(want)
     assert rel <= 1e-2, rel
+
+
+def test_layer_reads_seeding_and_route_mode(device):
+    """A whole file read into one of two layer buffers lands bit-exact, the layer computed
+    from it matches the oracle, the prompt tail's hottest experts are seeded into slots from
+    that buffer (bytes and map), and route mode keeps serving fills."""
+    from whallm_amd.streaming_policy import hot_tail_experts
+    files, experts, slots, K, T = 2, 16, 6, 4, 96
+    arrays, pool = make_pool(files, experts, 7)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    bufs = [cache.layer_buffer(), cache.layer_buffer()]
+    blob = cache.blob
+    rng = np.random.default_rng(8)
+    cache.read_layer(0, bufs[0])
+    for f in range(files):
+        cache.wait_layer(f)
+        if f + 1 < files:
+            cache.read_layer(f + 1, bufs[(f + 1) % 2])      # the next file streams in meanwhile
+        buf = bufs[f % 2]
+        logits = rng.standard_normal((T, experts)).astype(np.float32)
+        idx, w = M.route_softmax_topk(logits, K)
+        x = S.bf16_normal_np(rng, (T, H))
+        y = wa.moe_mxfp4(S.bf16_bits_to_tensor(x, device), torch.from_numpy(idx.astype(np.int32)).to(device),
+                         torch.from_numpy(w.astype(np.float32)).to(device), cache.layer_table(buf))
+        ex = {e: M.MXFP4Expert(arrays[f]["gate_up"][e], arrays[f]["gate_up_scales"][e], arrays[f]["down"][e],
+                               arrays[f]["down_scales"][e]) for e in range(experts)}
+        want = M.moe_layer(S.bf16_bits_to_f32(x), logits, ex, K)[0]
+        got = y.float().cpu().numpy()
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-2, f
+        host = buf.cpu().numpy().reshape(experts, blob)
+        for e in range(experts):
+            assert np.array_equal(host[e], blob_of(arrays[f], e)), (f, e)
+        # keep this prompt's hottest experts resident (least valuable first)
+        keep = hot_tail_experts(idx, experts, slots // files)
+        uses = [int((idx == e).sum()) for e in keep]
+        got_slots = cache.seed(f, keep, uses, buf)
+        torch.cuda.current_stream(device).synchronize()
+        mem = cache.slot_memory.view(slots, blob).cpu().numpy()
+        row = cache.map[f].cpu().numpy()
+        for e, s in zip(keep, got_slots):
+            assert np.array_equal(mem[s], blob_of(arrays[f], e)) and row[e] == s, (f, e, s)
+    # route mode: a decode request for file 1 through the cache, its experts resident and exact
+    cache.enable_route_policy(K)
+    ids = [1, 5, 9, 13]
+    got = cache.acquire(1, ids)
+    torch.cuda.current_stream(device).synchronize()
+    mem = cache.slot_memory.view(slots, blob).cpu().numpy()
+    for e, s in zip(ids, got):
+        assert np.array_equal(mem[s], blob_of(arrays[1], e))

@@ -77,6 +77,10 @@ _SIGNATURES = {
     "wm_slot_cache_plan": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
     "wm_slot_cache_acquire": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
     "wm_slot_cache_stats": (c_int, [_P, _P]),
+    "wm_slot_cache_set_route": (c_int, [_P, _P, _P]),
+    "wm_slot_cache_read_layer": (c_int, [_P, c_int32, _P, _P]),
+    "wm_slot_cache_wait_layer": (c_int, [_P, c_int32, _P]),
+    "wm_slot_cache_seed": (c_int, [_P, c_int32, _P, _P, c_int32, _P, _P, _P]),
     "wm_moe_fp8_workspace_size": (c_size_t, [c_int32, c_int32, POINTER(FP8ExpertsC)]),
     "wm_moe_fp8": (c_int, [_P, c_int32, _P, _P, c_int32, POINTER(FP8ExpertsC), POINTER(FP8ExpertsC), _P, _P, _P,
                            c_size_t, _P]),

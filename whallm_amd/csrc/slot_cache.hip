@@ -6,6 +6,17 @@
 // in order, else the least-used slot, oldest stamp among equals, never one handed out
 // by the same plan; use counts halve (floor 1) every max(8 * slots, 64) touches.
 //
+// Route mode (ExpertCache with eviction_policy "route", expert_cache.py:1131-1181): the
+// caller supplies a retention score per (file, expert) and a slot quota per file (the
+// route-history policy's output). The victim is the resident expert with the lowest
+// (tier, score, last access), never one handed out by the same plan, where tier 0 holds
+// the files over their quota (or the incoming file at its quota) and tier 1 the rest.
+//
+// Whole-file reads and seeding (engine.mm:1647-1678): a file's blobs are copied in one
+// hipMemcpyAsync into a caller buffer (a prefill layer reads its experts from there while
+// the next file is read into the other buffer), and a file's most used experts can then
+// be seeded into slots from that buffer with device-to-device copies.
+//
 // Fills: the blobs of a plan's misses are copied from the caller's pinned host pool
 // (the stand-in for the reference's SSD expert files: [files][experts][blob]) into
 // their HBM slots with hipMemcpyAsync on the cache's own copy stream. The copy
@@ -33,6 +44,8 @@ class SlotCache {
     owner_.assign(slots, -1);
     stamp_.assign(slots, 0);
     uses_.assign(slots, 0);
+    access_.assign(slots, 0);
+    count_.assign(files, 0);
     host_map_.assign((size_t)files * experts, -1);
     if (dev_) {
       check(hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking), "hipStreamCreateWithFlags");
@@ -49,6 +62,7 @@ class SlotCache {
   ~SlotCache() {
     if (!dev_) return;
     (void)hipStreamSynchronize(copy_);
+    for (auto& kv : layer_done_) (void)hipEventDestroy(kv.second);
     for (auto& st : staging_) {
       (void)hipEventDestroy(st.done);
       (void)hipHostFree(st.row);
@@ -73,20 +87,24 @@ class SlotCache {
         const int s = found->second;
         out_slots[i] = s;
         stamp_[s] = clock_;
+        access_[s] = ++seq_;
         ++uses_[s];
         ++hits_;
         if (filled) filled[i] = 0;
         continue;
       }
-      const int s = victim();
+      const int s = victim(file);
       if (owner_[s] >= 0) {
         where_.erase(owner_[s]);
         host_map_[owner_[s]] = -1;
+        --count_[owner_[s] / experts_];
       }
       owner_[s] = key;
       where_[key] = s;
       host_map_[key] = s;
+      ++count_[file];
       stamp_[s] = clock_;
+      access_[s] = ++seq_;
       uses_[s] = 1;
       out_slots[i] = s;
       if (filled) filled[i] = 1;
@@ -95,6 +113,12 @@ class SlotCache {
   }
 
   void acquire(int file, const int32_t* experts, int n, int32_t* out_slots, hipStream_t compute) {
+    fill(file, experts, n, out_slots, compute, nullptr);
+  }
+
+  // plan + copies of the misses: from the host pool, or with `layer` (a device copy of the
+  // whole file) device to device.
+  void fill(int file, const int32_t* experts, int n, int32_t* out_slots, hipStream_t compute, const uint8_t* layer) {
     if (!dev_) throw std::runtime_error("slot cache: opened without device memory (policy only)");
     std::vector<int32_t> filled(n);
     plan(file, experts, n, out_slots, filled.data());
@@ -106,9 +130,15 @@ class SlotCache {
     check(hipStreamWaitEvent(copy_, compute_done_, 0), "hipStreamWaitEvent");
     for (int i = 0; i < n; ++i) {
       if (!filled[i]) continue;
-      const uint8_t* src = pool_ + ((size_t)file * experts_ + experts[i]) * blob_;
-      check(hipMemcpyAsync(dev_ + (size_t)out_slots[i] * blob_, src, blob_, hipMemcpyHostToDevice, copy_),
-            "hipMemcpyAsync");
+      if (layer) {
+        check(hipMemcpyAsync(dev_ + (size_t)out_slots[i] * blob_, layer + (size_t)experts[i] * blob_, blob_,
+                             hipMemcpyDeviceToDevice, copy_),
+              "hipMemcpyAsync");
+      } else {
+        const uint8_t* src = pool_ + ((size_t)file * experts_ + experts[i]) * blob_;
+        check(hipMemcpyAsync(dev_ + (size_t)out_slots[i] * blob_, src, blob_, hipMemcpyHostToDevice, copy_),
+              "hipMemcpyAsync");
+      }
       copied_ += blob_;
       ++fills_;
     }
@@ -123,6 +153,49 @@ class SlotCache {
     }
     check(hipEventRecord(fills_done_, copy_), "hipEventRecord");
     check(hipStreamWaitEvent(compute, fills_done_, 0), "hipStreamWaitEvent");
+  }
+
+  // ExpertArena::seed (engine.mm:1664-1678): plan `experts` of `file` (least valuable
+  // first) with their use counts, filling the misses from `layer`, a device copy of the
+  // whole file.
+  void seed(int file, const int32_t* experts, const int32_t* uses, int n, const uint8_t* layer, int32_t* out_slots,
+            hipStream_t compute) {
+    fill(file, experts, n, out_slots, compute, layer);
+    for (int i = 0; i < n; ++i)
+      if (uses) uses_[out_slots[i]] = std::max<long>(1, uses[i]);
+  }
+
+  // The whole file's blobs into dst, on the copy stream after the compute stream's
+  // earlier work (which may still read dst); wait_layer makes a stream wait for it.
+  void read_layer(int file, uint8_t* dst, hipStream_t compute) {
+    if (!dev_) throw std::runtime_error("slot cache: opened without device memory (policy only)");
+    if (file < 0 || file >= files_) throw std::runtime_error("slot cache: file out of range");
+    if (!dst) throw std::runtime_error("slot cache: null layer buffer");
+    check(hipEventRecord(compute_done_, compute), "hipEventRecord");
+    check(hipStreamWaitEvent(copy_, compute_done_, 0), "hipStreamWaitEvent");
+    const size_t bytes = (size_t)experts_ * blob_;
+    check(hipMemcpyAsync(dst, pool_ + (size_t)file * bytes, bytes, hipMemcpyHostToDevice, copy_), "hipMemcpyAsync");
+    copied_ += (int64_t)bytes;
+    hipEvent_t& ev = layer_done_[file];
+    if (!ev) check(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate");
+    check(hipEventRecord(ev, copy_), "hipEventRecord");
+  }
+  void wait_layer(int file, hipStream_t compute) {
+    auto it = layer_done_.find(file);
+    if (it == layer_done_.end()) throw std::runtime_error("slot cache: wait for a file that was never read");
+    check(hipStreamWaitEvent(compute, it->second, 0), "hipStreamWaitEvent");
+  }
+
+  // Route mode on (scores [files][experts], quotas [files]) or off (scores NULL).
+  void set_route(const double* scores, const int32_t* quotas) {
+    if (!scores) {
+      route_ = false;
+      return;
+    }
+    if (!quotas) throw std::runtime_error("slot cache: route scores need quotas");
+    score_.assign(scores, scores + (size_t)files_ * experts_);
+    quota_.assign(quotas, quotas + files_);
+    route_ = true;
   }
 
   void stats(int64_t* out) const {
@@ -144,9 +217,33 @@ class SlotCache {
   static void check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string("slot cache: ") + what + ": " + hipGetErrorString(e));
   }
-  // ExpertArena::victim (engine.mm:749-757)
-  int victim() {
+  int victim(int incoming) {
     if (used_ < slots_) return used_++;
+    if (route_) return route_victim(incoming);
+    return lfu_victim();
+  }
+  // ExpertCache._evict_route_locked (expert_cache.py:1143-1181): lowest (tier, score, last
+  // access); the reference's per-layer heaps pick the same entry
+  int route_victim(int incoming) {
+    int best = -1, best_tier = 0;
+    double best_score = 0.0;
+    for (int s = 0; s < slots_; ++s) {
+      if (stamp_[s] == clock_ || owner_[s] < 0) continue;
+      const int f = (int)(owner_[s] / experts_);
+      const int tier = count_[f] > quota_[f] || (f == incoming && count_[f] >= quota_[f]) ? 0 : 1;
+      const double sc = score_[owner_[s]];
+      if (best < 0 || tier < best_tier || (tier == best_tier && (sc < best_score ||
+                                                                  (sc == best_score && access_[s] < access_[best])))) {
+        best = s;
+        best_tier = tier;
+        best_score = sc;
+      }
+    }
+    if (best < 0) throw std::runtime_error("the expert cache is too small for one step");
+    return best;
+  }
+  // ExpertArena::victim (engine.mm:749-757)
+  int lfu_victim() {
     int best = -1;
     for (int s = 0; s < slots_; ++s) {
       if (stamp_[s] == clock_) continue;
@@ -169,8 +266,13 @@ class SlotCache {
   int32_t* map_;
   const uint8_t* pool_;
   int used_ = 0;
-  long clock_ = 0, touches_ = 0;
-  std::vector<long> owner_, stamp_, uses_;
+  long clock_ = 0, touches_ = 0, seq_ = 0;
+  std::vector<long> owner_, stamp_, uses_, access_;
+  std::vector<int> count_;
+  bool route_ = false;
+  std::vector<double> score_;
+  std::vector<int32_t> quota_;
+  std::unordered_map<int, hipEvent_t> layer_done_;
   std::vector<int32_t> host_map_;
   std::unordered_map<long, int> where_;
   int64_t hits_ = 0, misses_ = 0, copied_ = 0, fills_ = 0;
@@ -249,6 +351,30 @@ WM_EXPORT int wm_slot_cache_acquire(wm_slot_cache* cache, int32_t file, const in
   return with_cache(c, [&] {
     if (n < 0 || (n > 0 && (!experts || !out_slots))) throw std::runtime_error("wm_slot_cache_acquire: bad arguments");
     c->acquire(file, experts, n, out_slots, as_stream(compute_stream));
+  });
+}
+
+WM_EXPORT int wm_slot_cache_set_route(wm_slot_cache* cache, const double* scores, const int32_t* quotas) {
+  SlotCache* c = reinterpret_cast<SlotCache*>(cache);
+  return with_cache(c, [&] { c->set_route(scores, quotas); });
+}
+
+WM_EXPORT int wm_slot_cache_read_layer(wm_slot_cache* cache, int32_t file, void* dst, void* compute_stream) {
+  SlotCache* c = reinterpret_cast<SlotCache*>(cache);
+  return with_cache(c, [&] { c->read_layer(file, static_cast<uint8_t*>(dst), as_stream(compute_stream)); });
+}
+
+WM_EXPORT int wm_slot_cache_wait_layer(wm_slot_cache* cache, int32_t file, void* compute_stream) {
+  SlotCache* c = reinterpret_cast<SlotCache*>(cache);
+  return with_cache(c, [&] { c->wait_layer(file, as_stream(compute_stream)); });
+}
+
+WM_EXPORT int wm_slot_cache_seed(wm_slot_cache* cache, int32_t file, const int32_t* experts, const int32_t* uses,
+                                 int32_t n, const void* layer, int32_t* out_slots, void* compute_stream) {
+  SlotCache* c = reinterpret_cast<SlotCache*>(cache);
+  return with_cache(c, [&] {
+    if (n < 0 || (n > 0 && (!experts || !out_slots || !layer))) throw std::runtime_error("wm_slot_cache_seed: bad arguments");
+    c->seed(file, experts, uses, n, static_cast<const uint8_t*>(layer), out_slots, as_stream(compute_stream));
   });
 }
 

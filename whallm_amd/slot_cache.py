@@ -16,6 +16,7 @@ import torch
 
 from . import _lib
 from .ops import MXFP4Experts
+from .route_cache import RouteCachePolicy
 
 
 def qwen_blob_bytes(hidden: int, inter: int) -> int:
@@ -61,6 +62,8 @@ class SlotCache:
         if not handle:
             raise SlotCacheError(err.value.decode(errors="replace"))
         self._handle = ctypes.c_void_p(handle)
+        self.route_policy: RouteCachePolicy | None = None
+        self.route_phase = "decode"
 
     def _check(self, status: int, what: str) -> None:
         if status != 0:
@@ -76,29 +79,117 @@ class SlotCache:
         return out.tolist(), filled.tolist()
 
     def acquire(self, file: int, experts) -> list[int]:
-        """Make ``experts`` of ``file`` resident; the current torch stream waits for the fills."""
+        """Make ``experts`` of ``file`` resident; the current torch stream waits for the fills.
+        In route mode the request counts as routes of ``file`` (expert_cache.py:1483)."""
         if self.device is None:
             raise SlotCacheError("policy-only cache")
         ids = np.ascontiguousarray(np.asarray(experts, np.int32).reshape(-1))
+        if self.route_policy is not None:
+            self.observe(file, ids)
         out = np.empty(ids.size, np.int32)
         stream = torch.cuda.current_stream(self.device).cuda_stream
         self._check(_lib.load().wm_slot_cache_acquire(self._handle, file, ids.ctypes.data, ids.size, out.ctypes.data,
                                                       ctypes.c_void_p(stream)), "acquire")
         return out.tolist()
 
-    def table(self, file: int) -> MXFP4Experts:
-        """The resident experts of ``file`` as an expert table (views of the slot memory)."""
-        H, I, b = self.hidden, self.inter, self.blob
-        mem = self.slot_memory.view(self.slots, b)
+    # ---- route mode (ExpertCache with eviction_policy "route", expert_cache.py:806-815, 1088-1181)
+
+    def enable_route_policy(self, top_k: int) -> RouteCachePolicy:
+        """Evict by the route-history policy (files = layers) instead of LFU."""
+        self.route_policy = RouteCachePolicy(self.files, self.experts, self.slots, top_k)
+        self._push_route()
+        return self.route_policy
+
+    def _push_route(self) -> None:
+        pol = self.route_policy
+        scores = np.ascontiguousarray(pol.scores, np.float64)
+        quotas = np.ascontiguousarray(pol.quotas, np.int32)
+        self._check(_lib.load().wm_slot_cache_set_route(self._handle, scores.ctypes.data, quotas.ctypes.data),
+                    "set_route")
+
+    def observe(self, file: int, selected, phase: str | None = None) -> None:
+        """Routes of ``file`` (expert ids, top_k per token) for the route policy; a batched
+        prefill that bypasses the slots reports its routes here (observe_batched_routes)."""
+        if self.route_policy is not None and self.route_policy.observe(file, selected, phase or self.route_phase):
+            self._push_route()
+
+    def begin_route_request(self) -> None:
+        """A new prompt (begin_route_request, expert_cache.py:1105-1109)."""
+        if self.route_policy is not None:
+            self.route_policy.begin_prefill()
+
+    def set_route_phase(self, phase: str) -> None:
+        """"prefill" or "decode"; leaving a prefill rebalances (trace_routes, :1088-1103)."""
+        previous, self.route_phase = self.route_phase, phase
+        if self.route_policy is not None and previous == "prefill" and phase != "prefill":
+            self.route_policy.rebalance()
+            self._push_route()
+
+    def record_read(self, file: int, seconds: float) -> None:
+        if self.route_policy is not None:
+            self.route_policy.record_read(file, seconds)
+
+    def disable_route_policy(self) -> None:
+        self.route_policy = None
+        self._check(_lib.load().wm_slot_cache_set_route(self._handle, None, None), "set_route")
+
+    # ---- whole-file reads and prompt-tail seeding (engine.mm:1647-1678)
+
+    def layer_buffer(self) -> torch.Tensor:
+        """A device buffer for one whole file (experts x blob bytes)."""
+        return torch.empty(self.experts * self.blob, dtype=torch.uint8, device=self.device)
+
+    def read_layer(self, file: int, buffer: torch.Tensor) -> None:
+        """Start reading the whole of ``file`` into ``buffer`` on the copy stream (after the
+        current stream's earlier work, which may still read the buffer)."""
+        if self.device is None:
+            raise SlotCacheError("policy-only cache")
+        if buffer.device != self.device or buffer.dtype != torch.uint8 or buffer.numel() < self.experts * self.blob \
+                or not buffer.is_contiguous():
+            raise ValueError("the layer buffer must be a contiguous uint8 device tensor of experts * blob bytes")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_read_layer(self._handle, file, ctypes.c_void_p(buffer.data_ptr()),
+                                                         ctypes.c_void_p(stream)), "read_layer")
+
+    def wait_layer(self, file: int) -> None:
+        """The current stream waits for the last read_layer of ``file``."""
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_wait_layer(self._handle, file, ctypes.c_void_p(stream)), "wait_layer")
+
+    def layer_table(self, buffer: torch.Tensor) -> MXFP4Experts:
+        """The experts of a whole-file buffer as an expert table (expert e = blob e)."""
+        return self._blob_table(buffer.view(self.experts, self.blob), self.experts, None)
+
+    def seed(self, file: int, experts, uses, buffer: torch.Tensor) -> list[int]:
+        """Keep ``experts`` of ``file`` (least valuable first, e.g. hot_tail_experts) resident
+        with use counts ``uses`` (or None), copied from the whole-file ``buffer``."""
+        ids = np.ascontiguousarray(np.asarray(experts, np.int32).reshape(-1))
+        cnt = None if uses is None else np.ascontiguousarray(np.asarray(uses, np.int32).reshape(-1))
+        if cnt is not None and cnt.size != ids.size:
+            raise ValueError("uses must match experts")
+        out = np.empty(ids.size, np.int32)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_seed(self._handle, file, ids.ctypes.data,
+                                                   None if cnt is None else cnt.ctypes.data, ids.size,
+                                                   ctypes.c_void_p(buffer.data_ptr()), out.ctypes.data,
+                                                   ctypes.c_void_p(stream)), "seed")
+        return out.tolist()
+
+    def _blob_table(self, mem: torch.Tensor, count: int, slots) -> MXFP4Experts:
+        H, I = self.hidden, self.inter
         o1 = 2 * I * H // 2
         o2 = o1 + 2 * I * H // 32
         o3 = o2 + H * I // 2
         return MXFP4Experts(
-            gate_up=mem[:, :o1].view(torch.int32).view(self.slots, 2 * I, H // 8),
-            gate_up_scales=mem[:, o1:o2].view(self.slots, 2 * I, H // 32),
-            down=mem[:, o2:o3].view(torch.int32).view(self.slots, H, I // 8),
-            down_scales=mem[:, o3:].view(self.slots, H, I // 32),
-            slots=self.map[file], experts=self.experts)
+            gate_up=mem[:, :o1].view(torch.int32).view(count, 2 * I, H // 8),
+            gate_up_scales=mem[:, o1:o2].view(count, 2 * I, H // 32),
+            down=mem[:, o2:o3].view(torch.int32).view(count, H, I // 8),
+            down_scales=mem[:, o3:].view(count, H, I // 32),
+            slots=slots, experts=self.experts)
+
+    def table(self, file: int) -> MXFP4Experts:
+        """The resident experts of ``file`` as an expert table (views of the slot memory)."""
+        return self._blob_table(self.slot_memory.view(self.slots, self.blob), self.slots, self.map[file])
 
     def stats(self) -> dict:
         out = (ctypes.c_int64 * 4)()
