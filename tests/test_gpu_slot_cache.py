@@ -145,3 +145,40 @@ def test_layer_reads_seeding_and_route_mode(device):
     mem = cache.slot_memory.view(slots, blob).cpu().numpy()
     for e, s in zip(ids, got):
         assert np.array_equal(mem[s], blob_of(arrays[1], e))
+
+
+@pytest.mark.parametrize("kind,limit", [("qwen", 0.0), ("deepseek", 1.5)])
+def test_installed_files_feed_the_cache(device, tmp_path, kind, limit):
+    """Expert files in the reference's on-disk format read into the pinned pool (DeepSeek
+    rewritten to the fused slot order) and served through the slot cache: the layer matches
+    the oracle built gate-first from the files' source regions."""
+    from install_files import write_install
+    from whallm_amd.blob_loader import ExpertFiles
+    layers, experts, slots, K, T = 2, 16, 16, 4, 24
+    src = write_install(tmp_path, kind, layers, experts, H, I, seed=9)
+    files = ExpertFiles(tmp_path)
+    pool = files.read()
+    cache = files.slot_cache(slots, pool, device, swiglu_limit=limit)
+    assert cache.up_first == (kind == "deepseek")
+    rng = np.random.default_rng(10)
+    for f in range(layers):
+        s = src[f]
+        if kind == "qwen":
+            gu = lambda e: (s["gate_up.weight"][e], s["gate_up.scale"][e])
+        else:   # gate = w1 then up = w3: the oracle's gate-first expert
+            gu = lambda e: (np.concatenate([s["w1.weight"][e], s["w3.weight"][e]]),
+                            np.concatenate([s["w1.scale"][e], s["w3.scale"][e]]))
+        dn = "down" if kind == "qwen" else "w2"
+        ex = {e: M.MXFP4Expert(gu(e)[0].view(np.uint32).reshape(2 * I, H // 8), gu(e)[1].reshape(2 * I, H // 32),
+                               s[f"{dn}.weight"][e].view(np.uint32).reshape(H, I // 8),
+                               s[f"{dn}.scale"][e].reshape(H, I // 32)) for e in range(experts)}
+        logits = rng.standard_normal((T, experts)).astype(np.float32)
+        idx, w = M.route_softmax_topk(logits, K)
+        cache.acquire(f, sorted(set(int(v) for v in idx.reshape(-1))))   # every routed expert resident
+        x = S.bf16_normal_np(rng, (T, H))
+        y = wa.moe_mxfp4(S.bf16_bits_to_tensor(x, device), torch.from_numpy(idx.astype(np.int32)).to(device),
+                         torch.from_numpy(w.astype(np.float32)).to(device), cache.table(f))
+        want = M.combine(M.routed_outputs(S.bf16_bits_to_f32(x), idx, ex, limit=limit), w)
+        got = y.float().cpu().numpy()
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel <= 1e-2 and np.abs(got - want).max() <= 2e-2 * np.abs(want).max(), (f, rel)

@@ -24,6 +24,24 @@ def qwen_blob_bytes(hidden: int, inter: int) -> int:
     return 2 * inter * hidden // 2 + 2 * inter * hidden // 32 + hidden * inter // 2 + hidden * inter // 32
 
 
+def blob_table(mem: torch.Tensor, hidden: int, inter: int, *, slots=None, experts=None,
+               up_first: bool = False, swiglu_limit: float = 0.0) -> MXFP4Experts:
+    """The expert table over blobs in slot order (uint8 [count, blob]: gate_up | gate_up scales |
+    down | down scales, the Qwen blob of manifest.py:37-42); ``up_first`` when the gate_up
+    rows are up then gate (DeepSeek's w13 = w3 | w1)."""
+    H, I = hidden, inter
+    count = mem.shape[0]
+    o1 = 2 * I * H // 2
+    o2 = o1 + 2 * I * H // 32
+    o3 = o2 + H * I // 2
+    return MXFP4Experts(
+        gate_up=mem[:, :o1].view(torch.int32).view(count, 2 * I, H // 8),
+        gate_up_scales=mem[:, o1:o2].view(count, 2 * I, H // 32),
+        down=mem[:, o2:o3].view(torch.int32).view(count, H, I // 8),
+        down_scales=mem[:, o3:].view(count, H, I // 32),
+        slots=slots, experts=experts, up_first=up_first, swiglu_limit=swiglu_limit)
+
+
 class SlotCacheError(RuntimeError):
     pass
 
@@ -33,12 +51,15 @@ class SlotCache:
     (pinned uint8 [files * experts * blob]) on demand.
 
     With ``device=None`` the handle runs the policy only (plan(); no device memory),
-    which is what host-side tests use.
+    which is what host-side tests use. ``up_first`` / ``swiglu_limit`` are carried into the
+    tables (DeepSeek blobs: w13 = up rows then gate rows, clamped SwiGLU).
     """
 
     def __init__(self, slots: int, hidden: int, inter: int, files: int, experts: int,
-                 host_pool: torch.Tensor | None = None, device: torch.device | str | None = None):
+                 host_pool: torch.Tensor | None = None, device: torch.device | str | None = None,
+                 up_first: bool = False, swiglu_limit: float = 0.0):
         self.slots, self.hidden, self.inter, self.files, self.experts = slots, hidden, inter, files, experts
+        self.up_first, self.swiglu_limit = bool(up_first), float(swiglu_limit)
         self.blob = qwen_blob_bytes(hidden, inter)
         lib = _lib.load()
         self.device = None if device is None else torch.device(device)
@@ -176,16 +197,8 @@ class SlotCache:
         return out.tolist()
 
     def _blob_table(self, mem: torch.Tensor, count: int, slots) -> MXFP4Experts:
-        H, I = self.hidden, self.inter
-        o1 = 2 * I * H // 2
-        o2 = o1 + 2 * I * H // 32
-        o3 = o2 + H * I // 2
-        return MXFP4Experts(
-            gate_up=mem[:, :o1].view(torch.int32).view(count, 2 * I, H // 8),
-            gate_up_scales=mem[:, o1:o2].view(count, 2 * I, H // 32),
-            down=mem[:, o2:o3].view(torch.int32).view(count, H, I // 8),
-            down_scales=mem[:, o3:].view(count, H, I // 32),
-            slots=slots, experts=self.experts)
+        return blob_table(mem.view(count, self.blob), self.hidden, self.inter, slots=slots, experts=self.experts,
+                          up_first=self.up_first, swiglu_limit=self.swiglu_limit)
 
     def table(self, file: int) -> MXFP4Experts:
         """The resident experts of ``file`` as an expert table (views of the slot memory)."""
