@@ -532,8 +532,77 @@ class MtpVerify:
                           f"(numpy oracle, {reps} repeats); the MoE layers are not part of this sample"}
 
 
+class NormRouter:
+    """The fused pre-MoE step (wm_norm_router): residual add, RMSNorm, router GEMV and shared
+    gate in one launch, at the C2 decode (1 token), C3 prefill (16,384 tokens, H 2048,
+    512 experts + shared gate) and C4 prefill (4,096 tokens, H 7168, 256 experts) shapes."""
+    dtype = "bf16"
+    data = "synthetic (N(0,1) fp32 residual, bf16 N(0,1) layer output, bf16 N(0,0.05) router and gate)"
+    SHAPES = {"router-c2": (1, 2048, 512, True), "router-c3": (16384, 2048, 512, True),
+              "router-c4": (4096, 7168, 256, False)}
+
+    def __init__(self, device, name, seed=0):
+        self.name = name
+        self.T, self.H, self.E, gate = self.SHAPES[name]
+        self.device = device
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        self.r = torch.randn(self.T, self.H, device=device, generator=g)
+        self.y = torch.randn(self.T, self.H, device=device, generator=g).to(torch.bfloat16)
+        self.router = (torch.randn(self.E, self.H, device=device, generator=g) * 0.05).to(torch.bfloat16)
+        self.gate = (torch.randn(self.H, device=device, generator=g) * 0.05).to(torch.bfloat16) if gate else None
+        self.r_out = torch.empty_like(self.r)
+        self.graph = None
+
+    def algorithmic_bytes(self):
+        rows = self.E + (self.gate is not None)
+        return rows * self.H * 2 + self.T * self.H * (4 + 2 + 2 + 4) + self.T * rows * 4
+
+    def flops(self):
+        return 2 * self.T * self.H * (self.E + (self.gate is not None))
+
+    def tokens_per_step(self):
+        return self.T
+
+    def prepare_inputs(self, steps):
+        pass
+
+    def _body(self):
+        import whallm_amd as wa
+        self.out = wa.norm_router(self.r, self.y, self.router, self.gate, residual_out=self.r_out)
+
+    def capture(self):
+        self._body()
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body()
+        torch.cuda.synchronize(self.device)
+
+    def step(self, i):
+        self.graph.replay()
+
+    def config(self):
+        return {"workload": f"{self.name}: fused residual add + RMSNorm + router GEMV (+ shared gate) before the MoE",
+                "hidden": self.H, "experts": self.E, "tokens": self.T, "shared_gate": self.gate is not None}
+
+    def cpu_baseline(self, budget_s: float):
+        from oracle import moe as M
+        f = lambda t: None if t is None else t.float().cpu().numpy()
+        n = min(self.T, 256)
+        r, y, w, g = f(self.r[:n]), f(self.y[:n]), f(self.router), f(self.gate)
+        started = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - started < min(budget_s, 10.0):
+            M.norm_router(r, y, w, g)
+            reps += 1
+        elapsed = (time.perf_counter() - started) / reps
+        return {"value": round(n / elapsed, 3), "unit": "tokens/s", "cores": len(os.sched_getaffinity(0)),
+                "kind": "port", "sample": f"oracle.norm_router (numpy, float64 matmul) on {n} tokens, {reps} repeats"}
+
+
 WORKLOADS = {"c2-decode": DecodeStack, "c3-prefill": Prefill, "c4-decode": FP8Layer, "c4-prefill": FP8Layer,
-             "c5-verify": MtpVerify}
+             "c5-verify": MtpVerify, "router-c2": NormRouter, "router-c3": NormRouter, "router-c4": NormRouter}
 
 
 # ----------------------------------------------------------------------------- main
@@ -576,6 +645,8 @@ def main():
         wl = DecodeStack(device, impl=args.decode_impl)
     elif args.config == "c4-prefill":
         wl = FP8Layer(device, tokens=4096)
+    elif args.config.startswith("router-"):
+        wl = NormRouter(device, args.config)
     else:
         wl = WORKLOADS[args.config](device)
     total = args.warmup + args.steps
@@ -620,6 +691,14 @@ def main():
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                     "tflops": round(tflops, 2), "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
                     "kernel": "FP8 MoE layer step (route_scored, FP8 expert kernels, combine) from one graph",
+                    "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
+    elif isinstance(wl, NormRouter):
+        achieved = wl.algorithmic_bytes() / (ms_per_step / 1e3) / 1e9
+        tflops = wl.flops() / (ms_per_step / 1e3) / 1e12
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "tflops": round(tflops, 2),
+                    "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+                    "kernel": "norm_router (one launch per step, graph replay)",
                     "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
     elif isinstance(wl, MtpVerify):
         achieved = wl.algorithmic_bytes() / (ms_per_step / 1e3) / 1e9

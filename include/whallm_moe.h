@@ -199,6 +199,18 @@ WM_EXPORT int wm_kernel_timing_ms(float* out2);
  * without attention). residual fp32 [T, H], y and x bf16 [T, H]. */
 WM_EXPORT int wm_residual_rmsnorm(float* residual, const void* y, int32_t tokens, int32_t hidden, float eps,
                                   void* x, void* stream);
+/* The step before the MoE fused into one launch: v = residual + y (y nullable),
+ * x = bf16(v * rsqrt(mean(v^2) + eps) * norm_weight) (norm_weight nullable: unit),
+ * logits[t, e] = x[t] . router[e] (fp32 [T, E]) and shared_logit[t] = x[t] . shared_gate
+ * (both nullable together). residual_out (nullable, must not overlap residual) receives v.
+ * bf16 y [T, H], norm_weight [H], router [E, H], shared_gate [H]; every pointer 16-byte
+ * aligned, hidden a multiple of 8. Replaces the norm dispatch and the router / shared-gate
+ * linears before the expert step (Native/QwenNative/engine.mm:2074-2079; SparseMoE.gate and
+ * shared_expert_gate, qwen4_exp.py:1000-1003); routing follows with wm_route_softmax_topk or
+ * wm_route_scored on the device. */
+WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* norm_weight, int32_t tokens,
+                             int32_t hidden, float eps, const void* router, int32_t experts, const void* shared_gate,
+                             void* x, float* residual_out, float* logits, float* shared_logit, void* stream);
 /* `layers` MoE layers chained as x_l = rmsnorm(r_l), r_{l+1} = r_l + MoE_l(x_l), routing
  * from logits [layers, T, E] on the device (no host synchronisation; graph-capturable).
  * experts / shared / shared_gates are host arrays of `layers` entries (shared and

@@ -275,6 +275,32 @@ def rms_norm(r: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     return bf16_round_f32((r * inv).astype(np.float32))
 
 
+def norm_router(r: np.ndarray, y: np.ndarray | None, router: np.ndarray, shared_gate: np.ndarray | None = None,
+                norm_weight: np.ndarray | None = None, eps: float = 1e-6):
+    """The step before the MoE: v = r + y (fp32 add), x = bf16(v / rms(v) * w_norm), router
+    logits x @ router^T and the shared gate logit x @ g (float64 sums, returned float32).
+
+    The norm is GroupRMSNorm's fp32 path (qwen4_exp.py:93-117, normalized * weight then
+    cast) / kernels.metal rms_norm (Native/QwenNative/kernels.metal:73-91); the linears are
+    SparseMoE.gate and shared_expert_gate (qwen4_exp.py:1000-1003), run by the native engine
+    right before the expert step (Native/QwenNative/engine.mm:2074-2079). ``y``, ``router``,
+    ``shared_gate`` and ``norm_weight`` are bf16 values as float32. Returns (v, x, logits,
+    shared_logit or None)."""
+    v = np.asarray(r, np.float32)
+    if y is not None:
+        v = (v + np.asarray(y, np.float32)).astype(np.float32)
+    v64 = v.astype(np.float64)
+    inv = 1.0 / np.sqrt((v64 * v64).mean(axis=-1, keepdims=True) + eps)
+    z = v64 * inv
+    if norm_weight is not None:
+        z = z * np.asarray(norm_weight, np.float64)
+    x = bf16_round_f32(z.astype(np.float32))
+    x64 = x.astype(np.float64)
+    logits = (x64 @ np.asarray(router, np.float64).T).astype(np.float32)
+    shared = None if shared_gate is None else (x64 @ np.asarray(shared_gate, np.float64).reshape(-1)).astype(np.float32)
+    return v, x, logits, shared
+
+
 # ----------------------------------------------------------------------------- MTP acceptance
 
 def verify_greedy(drafts: np.ndarray, target_logits: np.ndarray) -> tuple[int, int]:

@@ -104,3 +104,19 @@ def test_fp8_prefill_tile_layout_argument_checks():
     lib = _lib.load()
     assert lib.wm_moe_fp8_workspace_size(1, 2, ctypes.byref(routed)) > \
         lib.wm_moe_fp8_workspace_size(1, 2, ctypes.byref(shared))
+
+
+def test_norm_router_argument_checks():
+    """wm_norm_router refuses bad shapes, unpaired gate pointers, an output residual that
+    overlaps the input and misaligned tensors before any launch."""
+    a = 0x10000
+    def call(*, tokens=1, hidden=256, experts=8, residual=a, router=a, gate=None, shared=None, x=a, r_out=None, logits=a):
+        _lib.call("wm_norm_router", residual, None, None, tokens, hidden, 1e-6, router, experts, gate, x, r_out,
+                  logits, shared, None)
+    for kw, msg in (({"hidden": 260}, "multiple of 8"), ({"hidden": 40000}, "multiple of 8"), ({"experts": 0}, "at least 1"),
+                    ({"gate": a}, "go together"), ({"shared": a}, "go together"), ({"x": None}, "null pointer"),
+                    ({"r_out": a + 512}, "must not overlap"), ({"residual": a + 4}, "16-byte aligned"),
+                    ({"tokens": -1}, "negative")):
+        with pytest.raises(_lib.WhallmError, match=msg):
+            call(**kw)
+    call(tokens=0)   # nothing to do

@@ -247,3 +247,30 @@ def test_arena_lfu_protection_and_decay():
     for _ in range(70):
         b.plan(0, [1])
     assert b.uses[0] < 70                        # halved after max(8, 64) touches
+
+
+def test_norm_router_oracle_against_closed_forms():
+    """Pins oracle.norm_router: a constant row normalises to +-1 (times the norm weight),
+    sum-instead-of-mean or a dropped sqrt would not; the norm weight scales exactly by
+    powers of two; a zero row stays zero (eps); logits and the shared gate logit equal a
+    brute-force dot product."""
+    H = 8
+    r = np.array([[2.0] * H, [-3.0] * H, [0.0] * H], np.float32)
+    w = np.array([0.5, 2, 1, 1, -1, 4, 1, 0.25], np.float32)
+    router = np.arange(3 * H, dtype=np.float32).reshape(3, H) / 8 - 1
+    gate = np.linspace(-1, 1, H).astype(np.float32)
+    v, x, logits, shared = M.norm_router(r, None, router, gate, w)
+    np.testing.assert_array_equal(x, np.stack([w, -w, np.zeros(H, np.float32)]))
+    for t in range(3):
+        for e in range(3):
+            assert logits[t, e] == pytest.approx(sum(float(x[t, h]) * float(router[e, h]) for h in range(H)))
+        assert shared[t] == pytest.approx(sum(float(x[t, h]) * float(gate[h]) for h in range(H)))
+    rng = np.random.default_rng(3)
+    r2 = rng.standard_normal((5, 64)).astype(np.float32)
+    y2 = rng.standard_normal((5, 64)).astype(np.float32)
+    v2, x_unit, _, none = M.norm_router(r2, y2, np.zeros((1, 64), np.float32))
+    assert none is None
+    np.testing.assert_array_equal(v2, r2 + y2)
+    np.testing.assert_array_equal(x_unit, M.rms_norm(v2))
+    _, x_two, _, _ = M.norm_router(r2, y2, np.zeros((1, 64), np.float32), norm_weight=np.full(64, 2.0, np.float32))
+    np.testing.assert_array_equal(x_two, 2 * x_unit)

@@ -418,6 +418,45 @@ def residual_rmsnorm(residual: torch.Tensor, y: torch.Tensor | None, eps: float 
     return x
 
 
+def norm_router(residual: torch.Tensor, y: torch.Tensor | None, router: torch.Tensor,
+                shared_gate: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                residual_out: torch.Tensor | None = None):
+    """One launch (wm_norm_router): v = residual + y, x = bf16(rmsnorm(v) * norm_weight),
+    router logits = x @ router^T (fp32) and the shared gate logit x @ shared_gate (fp32, or
+    None). Returns (x, logits, shared_logit); ``residual_out`` (a separate fp32 buffer)
+    receives v. The residual itself is not written (other blocks still read it)."""
+    device = _require_device(residual, y, router, shared_gate, norm_weight, residual_out)
+    if residual.dtype != torch.float32 or not residual.is_contiguous():
+        raise ValueError("residual must be a contiguous float32 tensor")
+    H = residual.shape[-1]
+    T = residual.numel() // H if H else 0
+    y = None if y is None else _contig(y, torch.bfloat16, "y")
+    router = _contig(router, torch.bfloat16, "router")
+    if y is not None and y.shape != residual.shape:
+        raise ValueError("y must match residual")
+    if router.dim() != 2 or router.shape[1] != H:
+        raise ValueError("router must be [experts, hidden]")
+    if shared_gate is not None:
+        shared_gate = _contig(shared_gate, torch.bfloat16, "shared_gate").reshape(-1)
+        if shared_gate.numel() != H:
+            raise ValueError("shared_gate must hold hidden values")
+    if norm_weight is not None:
+        norm_weight = _contig(norm_weight, torch.bfloat16, "norm_weight").reshape(-1)
+        if norm_weight.numel() != H:
+            raise ValueError("norm_weight must hold hidden values")
+    if residual_out is not None and (residual_out.dtype != torch.float32 or residual_out.shape != residual.shape
+                                     or not residual_out.is_contiguous()):
+        raise ValueError("residual_out must be a contiguous float32 tensor shaped like residual")
+    E = router.shape[0]
+    x = torch.empty(residual.shape, dtype=torch.bfloat16, device=device)
+    logits = torch.empty(*residual.shape[:-1], E, dtype=torch.float32, device=device)
+    shared_logit = (torch.empty(residual.shape[:-1], dtype=torch.float32, device=device)
+                    if shared_gate is not None else None)
+    _lib.call("wm_norm_router", _ptr(residual), _ptr(y), _ptr(norm_weight), T, H, float(eps), _ptr(router), E,
+              _ptr(shared_gate), _ptr(x), _ptr(residual_out), _ptr(logits), _ptr(shared_logit), _stream(device))
+    return x, logits, shared_logit
+
+
 class MoEStack:
     """L chained MXFP4 MoE layers run by one wm_moe_stack_mxfp4 call (device routing,
     no host synchronisation, graph-capturable). Holds the C tables of every layer."""
