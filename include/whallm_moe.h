@@ -204,13 +204,23 @@ WM_EXPORT int wm_residual_rmsnorm(float* residual, const void* y, int32_t tokens
  * logits[t, e] = x[t] . router[e] (fp32 [T, E]) and shared_logit[t] = x[t] . shared_gate
  * (both nullable together). residual_out (nullable, must not overlap residual) receives v.
  * bf16 y [T, H], norm_weight [H], router [E, H], shared_gate [H]; every pointer 16-byte
- * aligned, hidden a multiple of 8. Replaces the norm dispatch and the router / shared-gate
- * linears before the expert step (Native/QwenNative/engine.mm:2074-2079; SparseMoE.gate and
+ * aligned, hidden a multiple of 8. router_packed (nullable) is the same rows from
+ * wm_repack_router, router_packed_bytes its size; the prefill path (16+ tokens) then reads
+ * it instead of router. Replaces the norm dispatch and the router / shared-gate linears
+ * before the expert step (Native/QwenNative/engine.mm:2074-2079; SparseMoE.gate and
  * shared_expert_gate, qwen4_exp.py:1000-1003); routing follows with wm_route_softmax_topk or
  * wm_route_scored on the device. */
 WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* norm_weight, int32_t tokens,
                              int32_t hidden, float eps, const void* router, int32_t experts, const void* shared_gate,
-                             void* x, float* residual_out, float* logits, float* shared_logit, void* stream);
+                             const void* router_packed, size_t router_packed_bytes, void* x,
+                             float* residual_out, float* logits, float* shared_logit, void* stream);
+/* The router rows (and the shared gate row when shared_gate is set) in the fragment order of
+ * wm_norm_router's prefill GEMM: [ceil((E + gate) / 16) + gate][H / 32][64] x 16 bytes,
+ * zero-padded rows (the spare group with a gate makes the size tell whether it is packed). A one-time repack, like the prefill tile layout of the experts (no reference
+ * counterpart: the reference's router weight stays [E, H]). hidden a multiple of 32. */
+WM_EXPORT size_t wm_router_packed_bytes(int32_t experts, int32_t hidden, int32_t has_gate);
+WM_EXPORT int wm_repack_router(const void* router, const void* shared_gate, int32_t experts, int32_t hidden,
+                               void* packed, void* stream);
 /* `layers` MoE layers chained as x_l = rmsnorm(r_l), r_{l+1} = r_l + MoE_l(x_l), routing
  * from logits [layers, T, E] on the device (no host synchronisation; graph-capturable).
  * experts / shared / shared_gates are host arrays of `layers` entries (shared and

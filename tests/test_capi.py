@@ -110,13 +110,22 @@ def test_norm_router_argument_checks():
     """wm_norm_router refuses bad shapes, unpaired gate pointers, an output residual that
     overlaps the input and misaligned tensors before any launch."""
     a = 0x10000
-    def call(*, tokens=1, hidden=256, experts=8, residual=a, router=a, gate=None, shared=None, x=a, r_out=None, logits=a):
-        _lib.call("wm_norm_router", residual, None, None, tokens, hidden, 1e-6, router, experts, gate, x, r_out,
-                  logits, shared, None)
+    def call(*, tokens=1, hidden=256, experts=8, residual=a, router=a, gate=None, shared=None, x=a, r_out=None, logits=a,
+             packed=None, packed_bytes=0):
+        _lib.call("wm_norm_router", residual, None, None, tokens, hidden, 1e-6, router, experts, gate, packed,
+                  packed_bytes, x, r_out, logits, shared, None)
     for kw, msg in (({"hidden": 260}, "multiple of 8"), ({"hidden": 40000}, "multiple of 8"), ({"experts": 0}, "at least 1"),
                     ({"gate": a}, "go together"), ({"shared": a}, "go together"), ({"x": None}, "null pointer"),
                     ({"r_out": a + 512}, "must not overlap"), ({"residual": a + 4}, "16-byte aligned"),
-                    ({"tokens": -1}, "negative")):
+                    ({"tokens": -1}, "negative"), ({"packed": a, "packed_bytes": 4096}, "packed router does not match"),
+                    ({"packed": a, "packed_bytes": 8192, "gate": a, "shared": a}, "packed router does not match")):
         with pytest.raises(_lib.WhallmError, match=msg):
             call(**kw)
     call(tokens=0)   # nothing to do
+    lib = _lib.load()
+    assert lib.wm_router_packed_bytes(8, 256, 0) == 16 * 256 * 2
+    assert lib.wm_router_packed_bytes(16, 256, 1) == 48 * 256 * 2 and lib.wm_router_packed_bytes(8, 40, 0) == 0
+    for e in range(1, 70):   # with and without the gate row the sizes always differ
+        assert lib.wm_router_packed_bytes(e, 256, 1) != lib.wm_router_packed_bytes(e, 256, 0)
+    with pytest.raises(_lib.WhallmError, match="multiple of 32"):
+        _lib.call("wm_repack_router", a, None, 8, 40, a, None)

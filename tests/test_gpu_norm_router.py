@@ -106,3 +106,31 @@ def test_empty_and_error_paths(device):
         wa.norm_router(r, None, router, residual_out=r)
     with pytest.raises(ValueError, match="router"):
         wa.norm_router(r, None, router[:, :128])
+
+
+@pytest.mark.parametrize("T,H,E,with_gate", [(300, 2560, 512, True), (20, 7168, 256, True), (64, 2048, 40, False),
+                                             (1, 2048, 512, True)])
+def test_packed_router_is_bit_identical(device, T, H, E, with_gate):
+    """repack_router's fragment order (checked against a torch permute of the zero-padded
+    rows) feeds the prefill GEMM the same operands, so logits are bit-identical to the row
+    path; at one token (dot-product path) the packed copy is not read."""
+    rng = np.random.default_rng(T * 7 + E)
+    r = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(device)
+    y = bf16_tensor(rng, (T, H), device)
+    router = bf16_tensor(rng, (E, H), device, 0.05)
+    gate = bf16_tensor(rng, (H,), device, 0.05) if with_gate else None
+    packed = wa.repack_router(router, gate)
+    rows = torch.cat([router, gate[None]]) if with_gate else router
+    G = (rows.shape[0] + 15) // 16 + int(with_gate)   # a spare zero group marks a packed gate
+    padded = torch.zeros(G * 16, H, dtype=torch.bfloat16, device=device)
+    padded[:rows.shape[0]] = rows
+    want = padded.view(G, 16, H // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous()
+    assert torch.equal(packed.view(torch.bfloat16).view(want.shape), want)
+    a = wa.norm_router(r, y, router, gate)
+    b = wa.norm_router(r, y, router, gate, router_packed=packed)
+    torch.cuda.synchronize()
+    for u, v in zip(a, b):
+        assert (u is None and v is None) or torch.equal(u, v)
+    if T >= 16:
+        with pytest.raises(Exception, match="does not match"):
+            wa.norm_router(r, y, router, None if with_gate else bf16_tensor(rng, (H,), device), router_packed=packed)

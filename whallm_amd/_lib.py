@@ -64,7 +64,10 @@ _SIGNATURES = {
     "wm_repack_prefill_mxfp4": (c_int, [POINTER(MXFP4ExpertsC), _P, _P, _P, _P, _P]),
     "wm_repack_prefill_fp8": (c_int, [POINTER(FP8ExpertsC), _P, _P, _P, _P, _P]),
     "wm_residual_rmsnorm": (c_int, [_P, _P, c_int32, c_int32, c_float, _P, _P]),
-    "wm_norm_router": (c_int, [_P, _P, _P, c_int32, c_int32, c_float, _P, c_int32, _P, _P, _P, _P, _P, _P]),
+    "wm_norm_router": (c_int, [_P, _P, _P, c_int32, c_int32, c_float, _P, c_int32, _P, _P, c_size_t, _P, _P, _P, _P,
+                               _P]),
+    "wm_router_packed_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
+    "wm_repack_router": (c_int, [_P, _P, c_int32, c_int32, _P, _P]),
     "wm_moe_stack_mxfp4_workspace_size": (c_size_t, [c_int32, c_int32, POINTER(MXFP4ExpertsC)]),
     "wm_moe_stack_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, POINTER(MXFP4ExpertsC),
                                    POINTER(MXFP4ExpertsC), _P, _P, c_float, _P, _P, c_size_t, _P]),

@@ -17,6 +17,7 @@
 // of the weight row once and
 // applies each to the TB tokens' x chunks (V_DOT2_F32_BF16), then one wave reduction
 // per token.
+#include <algorithm>
 #include <cmath>
 
 #include "moe_internal.h"
@@ -208,13 +209,33 @@ __global__ void __launch_bounds__(256) norm_router_kernel(
 // fragments (16 bytes per lane, loaded four steps ahead) against one x fragment.
 // Operands: lane l holds row / token l % 16 and K chunk (l / 16) of each 32-wide step (the
 // same lane-to-K map for both, so the K order inside a step cancels); the result holds
-// token l % 16 for rows 4 (l / 16) .. +3 of the group.
+// token l % 16 for rows 4 (l / 16) .. +3 of the group. With `packed` (wm_repack_router)
+// each fragment is one contiguous 1 KB read instead of 16 rows x 64 bytes.
+
+// The packed router: [groups][hidden / 32][64 lanes] uint4, lane l of group g and step s
+// holding row 16 g + l % 16 (router rows, then the gate row, then zeros; one spare zero
+// group follows when the gate is packed), 8 values from column 32 s + 8 (l / 16).
+__global__ void __launch_bounds__(256) repack_router_kernel(const uint4* __restrict__ router,
+                                                            const uint4* __restrict__ gate, int experts, int hidden,
+                                                            int64_t total, uint4* __restrict__ packed) {
+  const int steps = hidden / 32, chunks = hidden / 8;
+  for (int64_t o = blockIdx.x * 256 + threadIdx.x; o < total; o += (int64_t)gridDim.x * 256) {
+    const int lane = (int)(o % 64);
+    const int64_t gs = o / 64;
+    const int st = (int)(gs % steps), g = (int)(gs / steps);
+    const int row = 16 * g + lane % 16, chunk = 4 * st + lane / 16;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < experts) v = router[(int64_t)row * chunks + chunk];
+    else if (row == experts && gate) v = gate[chunk];
+    packed[o] = v;
+  }
+}
 template <int TB>
 __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
     const float* __restrict__ r, const uint16_t* __restrict__ y, const uint16_t* __restrict__ nw, int tokens,
     int hidden, float eps, const uint16_t* __restrict__ router, int experts, const uint16_t* __restrict__ gate,
-    uint16_t* __restrict__ x_out, float* __restrict__ r_out, float* __restrict__ logits,
-    float* __restrict__ shared_logit) {
+    const uint4* __restrict__ packed, uint16_t* __restrict__ x_out, float* __restrict__ r_out,
+    float* __restrict__ logits, float* __restrict__ shared_logit) {
   extern __shared__ uint4 x_tile[];  // [TB][hidden / 8 + 1]
   __shared__ float inv_s[TB];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -230,10 +251,14 @@ __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
   const uint4* xb = x_tile + (has_col ? n : 0) * stride + kq;
   for (int g0 = wave; g0 < groups; g0 += 16) {
     const uint4* wp[4];
+    const int wstep = packed ? 64 : 4;  // uint4s from one K step's fragment to the next
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = (g0 + 4 * j) * 16 + n;
-      wp[j] = weight_row(router, gate, experts, hidden, e < rows ? e : 0) + kq;
+      if (packed)  // fragment-major: group g's step-s fragment is 64 consecutive uint4, one per lane
+        wp[j] = packed + (int64_t)min(g0 + 4 * j, groups - 1) * steps * 64 + lane;
+      else
+        wp[j] = weight_row(router, gate, experts, hidden, e < rows ? e : 0) + kq;
     }
     // four K steps of fragments in flight: set u holds step s + u
     constexpr int PD = 4;
@@ -245,7 +270,7 @@ __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
     for (int u = 0; u < PD; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (g0 + 4 * j < groups) a[u][j] = wp[j][4 * (u < steps ? u : 0)];
+        if (g0 + 4 * j < groups) a[u][j] = wp[j][wstep * (u < steps ? u : 0)];
     for (int s = 0; s < steps; s += PD) {
 #pragma unroll
       for (int u = 0; u < PD; ++u) {
@@ -256,7 +281,7 @@ __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
             if (g0 + 4 * j >= groups) break;  // wave-uniform: a last batch with fewer groups
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(nr_bf16x8, a[u][j]),
                                                              __builtin_bit_cast(nr_bf16x8, b), acc[j], 0, 0, 0);
-            if (s + u + PD < steps) a[u][j] = wp[j][4 * (s + u + PD)];
+            if (s + u + PD < steps) a[u][j] = wp[j][wstep * (s + u + PD)];
           }
         }
       }
@@ -296,9 +321,32 @@ using namespace wm;
 
 extern "C" {
 
+WM_EXPORT size_t wm_router_packed_bytes(int32_t experts, int32_t hidden, int32_t has_gate) {
+  if (experts < 1 || hidden < 32 || hidden % 32) return 0;
+  // one spare zero group when the gate row is packed, so the size alone tells whether it is
+  const int g = has_gate ? 1 : 0;
+  return (size_t)((experts + g + 15) / 16 + g) * 16 * hidden * 2;
+}
+
+WM_EXPORT int wm_repack_router(const void* router, const void* shared_gate, int32_t experts, int32_t hidden,
+                               void* packed, void* stream) {
+  return guarded([&] {
+    if (experts < 1 || hidden < 32 || hidden % 32) fail("wm_repack_router: hidden must be a multiple of 32");
+    if (!router || !packed) fail("wm_repack_router: null pointer");
+    for (const void* p : {router, shared_gate, (const void*)packed})
+      if (p && ((uintptr_t)p % 16)) fail("wm_repack_router: tensors must be 16-byte aligned");
+    const int64_t total = (int64_t)wm_router_packed_bytes(experts, hidden, shared_gate != nullptr) / 16;
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(repack_router_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), (const uint4*)router,
+                       (const uint4*)shared_gate, experts, hidden, total, (uint4*)packed);
+    check_launch("repack_router");
+  });
+}
+
 WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* norm_weight, int32_t tokens,
                              int32_t hidden, float eps, const void* router, int32_t experts, const void* shared_gate,
-                             void* x, float* residual_out, float* logits, float* shared_logit, void* stream) {
+                             const void* router_packed, size_t router_packed_bytes, void* x,
+                             float* residual_out, float* logits, float* shared_logit, void* stream) {
   return guarded([&] {
     if (tokens < 0) fail("wm_norm_router: negative token count");
     if (hidden < 8 || hidden % 8 || hidden * 2 > 64 * 1024) fail("wm_norm_router: hidden must be a multiple of 8 up to 32768");
@@ -312,7 +360,9 @@ WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* n
       size_t n = (size_t)tokens * hidden * sizeof(float);
       if (a < b + n && b < a + n) fail("wm_norm_router: residual_out must not overlap residual (other blocks still read it)");
     }
-    for (const void* p : {(const void*)residual, y, norm_weight, router, shared_gate, (const void*)x,
+    if (router_packed && (hidden % 32 || router_packed_bytes != wm_router_packed_bytes(experts, hidden, shared_gate != nullptr)))
+      fail("wm_norm_router: the packed router does not match experts, hidden and the shared gate (wm_router_packed_bytes)");
+    for (const void* p : {(const void*)residual, y, norm_weight, router, shared_gate, router_packed, (const void*)x,
                           (const void*)residual_out})
       if (p && ((uintptr_t)p % 16)) fail("wm_norm_router: tensors must be 16-byte aligned");
     hipStream_t s = as_stream(stream);
@@ -323,8 +373,8 @@ WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* n
       const size_t lds = (size_t)mfma_tb * (hidden / 8 + 1) * 16;
 #define WM_NRM(TB) hipLaunchKernelGGL(norm_router_mfma_kernel<TB>, dim3(blocks), dim3(256), lds, s, residual, \
                                       (const uint16_t*)y, (const uint16_t*)norm_weight, tokens, hidden, eps, \
-                                      (const uint16_t*)router, experts, (const uint16_t*)shared_gate, (uint16_t*)x, \
-                                      residual_out, logits, shared_logit)
+                                      (const uint16_t*)router, experts, (const uint16_t*)shared_gate, \
+                                      (const uint4*)router_packed, (uint16_t*)x, residual_out, logits, shared_logit)
       if (mfma_tb == 16) WM_NRM(16);
       else WM_NRM(8);
 #undef WM_NRM

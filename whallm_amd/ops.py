@@ -418,14 +418,34 @@ def residual_rmsnorm(residual: torch.Tensor, y: torch.Tensor | None, eps: float 
     return x
 
 
+def repack_router(router: torch.Tensor, shared_gate: torch.Tensor | None = None) -> torch.Tensor:
+    """The router rows (+ the shared gate row) in the prefill GEMM's fragment order
+    (wm_repack_router): a one-time copy that norm_router(..., router_packed=) reads at 16+
+    tokens as contiguous 1 KB fragments."""
+    device = _require_device(router, shared_gate)
+    router = _contig(router, torch.bfloat16, "router")
+    E, H = router.shape
+    if shared_gate is not None:
+        shared_gate = _contig(shared_gate, torch.bfloat16, "shared_gate").reshape(-1)
+        if shared_gate.numel() != H:
+            raise ValueError("shared_gate must hold hidden values")
+    nbytes = _lib.load().wm_router_packed_bytes(E, H, int(shared_gate is not None))
+    if nbytes == 0:
+        raise ValueError("the packed router needs hidden a multiple of 32")
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    _lib.call("wm_repack_router", _ptr(router), _ptr(shared_gate), E, H, _ptr(packed), _stream(device))
+    return packed
+
+
 def norm_router(residual: torch.Tensor, y: torch.Tensor | None, router: torch.Tensor,
                 shared_gate: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
-                residual_out: torch.Tensor | None = None):
+                residual_out: torch.Tensor | None = None, router_packed: torch.Tensor | None = None):
     """One launch (wm_norm_router): v = residual + y, x = bf16(rmsnorm(v) * norm_weight),
     router logits = x @ router^T (fp32) and the shared gate logit x @ shared_gate (fp32, or
     None). Returns (x, logits, shared_logit); ``residual_out`` (a separate fp32 buffer)
-    receives v. The residual itself is not written (other blocks still read it)."""
-    device = _require_device(residual, y, router, shared_gate, norm_weight, residual_out)
+    receives v. The residual itself is not written (other blocks still read it).
+    ``router_packed`` (repack_router of the same router and gate) speeds up 16+ tokens."""
+    device = _require_device(residual, y, router, shared_gate, norm_weight, residual_out, router_packed)
     if residual.dtype != torch.float32 or not residual.is_contiguous():
         raise ValueError("residual must be a contiguous float32 tensor")
     H = residual.shape[-1]
@@ -452,8 +472,10 @@ def norm_router(residual: torch.Tensor, y: torch.Tensor | None, router: torch.Te
     logits = torch.empty(*residual.shape[:-1], E, dtype=torch.float32, device=device)
     shared_logit = (torch.empty(residual.shape[:-1], dtype=torch.float32, device=device)
                     if shared_gate is not None else None)
+    packed_bytes = 0 if router_packed is None else router_packed.numel() * router_packed.element_size()
     _lib.call("wm_norm_router", _ptr(residual), _ptr(y), _ptr(norm_weight), T, H, float(eps), _ptr(router), E,
-              _ptr(shared_gate), _ptr(x), _ptr(residual_out), _ptr(logits), _ptr(shared_logit), _stream(device))
+              _ptr(shared_gate), _ptr(router_packed), packed_bytes, _ptr(x), _ptr(residual_out), _ptr(logits),
+              _ptr(shared_logit), _stream(device))
     return x, logits, shared_logit
 
 
