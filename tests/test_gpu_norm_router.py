@@ -42,6 +42,7 @@ def check_dot(got, x, w):
     (40, 4096, 256, False, True, False),     # DeepSeek width, no y, no gate
     (300, 2560, 512, True, True, True),      # MFMA path, 16-token blocks, ragged last block
     (20, 7168, 256, True, False, True),      # MFMA path, 8-token blocks (C4 width)
+    (70, 2048, 512, True, True, True),       # MFMA path, 32-token blocks (two column blocks), ragged tail
     (17, 1000, 64, True, True, True),        # hidden not a multiple of 32: dot-product path, 16 tokens
 ])
 def test_norm_router_matches_oracle(device, T, H, E, with_y, with_w, with_gate):

@@ -247,8 +247,14 @@ __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
   const int rows = experts + (gate ? 1 : 0);
   const int groups = (rows + 15) / 16;
   const int n = lane % 16, kq = lane / 16;
-  const bool has_col = n < TB;
-  const uint4* xb = x_tile + (has_col ? n : 0) * stride + kq;
+  constexpr int NCOL = TB > 16 ? TB / 16 : 1;  // 16-token column blocks
+  const uint4* xb[NCOL];
+  bool has_col[NCOL];
+#pragma unroll
+  for (int cb = 0; cb < NCOL; ++cb) {
+    has_col[cb] = 16 * cb + n < TB;
+    xb[cb] = x_tile + (has_col[cb] ? 16 * cb + n : 0) * stride + kq;
+  }
   for (int g0 = wave; g0 < groups; g0 += 16) {
     const uint4* wp[4];
     const int wstep = packed ? 64 : 4;  // uint4s from one K step's fragment to the next
@@ -262,10 +268,12 @@ __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
     }
     // four K steps of fragments in flight: set u holds step s + u
     constexpr int PD = 4;
-    nr_f32x4 acc[4];
+    nr_f32x4 acc[4][NCOL];
     uint4 a[PD][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = nr_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int cb = 0; cb < NCOL; ++cb) acc[j][cb] = nr_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < PD; ++u)
 #pragma unroll
@@ -275,33 +283,43 @@ __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
 #pragma unroll
       for (int u = 0; u < PD; ++u) {
         if (s + u < steps) {
-          const uint4 b = has_col ? xb[4 * (s + u)] : make_uint4(0, 0, 0, 0);
+          uint4 bv[NCOL];
+#pragma unroll
+          for (int cb = 0; cb < NCOL; ++cb) bv[cb] = has_col[cb] ? xb[cb][4 * (s + u)] : make_uint4(0, 0, 0, 0);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             if (g0 + 4 * j >= groups) break;  // wave-uniform: a last batch with fewer groups
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(nr_bf16x8, a[u][j]),
-                                                             __builtin_bit_cast(nr_bf16x8, b), acc[j], 0, 0, 0);
+#pragma unroll
+            for (int cb = 0; cb < NCOL; ++cb)
+              acc[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(nr_bf16x8, a[u][j]),
+                                                                   __builtin_bit_cast(nr_bf16x8, bv[cb]), acc[j][cb],
+                                                                   0, 0, 0);
             if (s + u + PD < steps) a[u][j] = wp[j][wstep * (s + u + PD)];
           }
         }
       }
     }
-    if (n < nt) {
+#pragma unroll
+    for (int cb = 0; cb < NCOL; ++cb) {
+      const int t = 16 * cb + n;
+      if (t >= nt) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = (g0 + 4 * j) * 16 + 4 * kq + i;
-          if (e < rows) store_row(logits, shared_logit, experts, t0 + n, e, acc[j][i]);
+          if (e < rows) store_row(logits, shared_logit, experts, t0 + t, e, acc[j][cb][i]);
         }
     }
   }
 }
 
-// The MFMA path's token block: 16 tokens when the padded x tile fits 150 KB of LDS, else
-// 8; 0 (the dot-product path) below 16 tokens or when hidden is not a multiple of 32.
+// The MFMA path's token block: 32 tokens (two column blocks per weight fragment) or 16 when
+// the padded x tile fits 150 KB of LDS, else 8; 0 (the dot-product path) below 16 tokens or
+// when hidden is not a multiple of 32.
 static int mfma_token_block(int tokens, int hidden) {
   if (tokens < 16 || hidden % 32) return 0;
+  if (tokens >= 32 && (size_t)32 * (hidden / 8 + 1) * 16 + 128 <= 150 * 1024) return 32;
   for (int tb : {16, 8})
     if ((size_t)tb * (hidden / 8 + 1) * 16 + 64 <= 150 * 1024) return tb;
   return 0;
@@ -375,7 +393,8 @@ WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* n
                                       (const uint16_t*)y, (const uint16_t*)norm_weight, tokens, hidden, eps, \
                                       (const uint16_t*)router, experts, (const uint16_t*)shared_gate, \
                                       (const uint4*)router_packed, (uint16_t*)x, residual_out, logits, shared_logit)
-      if (mfma_tb == 16) WM_NRM(16);
+      if (mfma_tb == 32) WM_NRM(32);
+      else if (mfma_tb == 16) WM_NRM(16);
       else WM_NRM(8);
 #undef WM_NRM
       check_launch("norm_router_mfma");
