@@ -109,14 +109,15 @@ def test_fp8_prefill_tile_layout_argument_checks():
 def test_norm_router_argument_checks():
     """wm_norm_router refuses bad shapes, unpaired gate pointers, an output residual that
     overlaps the input and misaligned tensors before any launch."""
-    a = 0x10000
-    def call(*, tokens=1, hidden=256, experts=8, residual=a, router=a, gate=None, shared=None, x=a, r_out=None, logits=a,
-             packed=None, packed_bytes=0):
+    a, b = 0x10000, 0x20000   # residual at a, everything else elsewhere
+    def call(*, tokens=1, hidden=256, experts=8, residual=a, router=b, gate=None, shared=None, x=b + 0x10000, r_out=None,
+             logits=b + 0x20000, packed=None, packed_bytes=0):
         _lib.call("wm_norm_router", residual, None, None, tokens, hidden, 1e-6, router, experts, gate, packed,
                   packed_bytes, x, r_out, logits, shared, None)
     for kw, msg in (({"hidden": 260}, "multiple of 8"), ({"hidden": 40000}, "multiple of 8"), ({"experts": 0}, "at least 1"),
                     ({"gate": a}, "go together"), ({"shared": a}, "go together"), ({"x": None}, "null pointer"),
-                    ({"r_out": a + 512}, "must not overlap"), ({"residual": a + 4}, "16-byte aligned"),
+                    ({"r_out": a + 512}, "must not overlap"), ({"x": a + 512}, "x must not overlap"),
+                    ({"residual": a + 4}, "16-byte aligned"),
                     ({"tokens": -1}, "negative"), ({"packed": a, "packed_bytes": 4096}, "packed router does not match"),
                     ({"packed": a, "packed_bytes": 8192, "gate": a, "shared": a}, "packed router does not match")):
         with pytest.raises(_lib.WhallmError, match=msg):

@@ -373,11 +373,16 @@ WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* n
       fail("wm_norm_router: shared_gate and shared_logit go together");
     if (tokens == 0) return;
     if (!residual || !router || !x || !logits) fail("wm_norm_router: null pointer");
-    if (residual_out) {
-      const char *a = (const char*)residual, *b = (const char*)residual_out;
-      size_t n = (size_t)tokens * hidden * sizeof(float);
-      if (a < b + n && b < a + n) fail("wm_norm_router: residual_out must not overlap residual (other blocks still read it)");
-    }
+    // Row block 0 writes x and v while other blocks still read residual and y.
+    auto overlap = [](const void* p, size_t pn, const void* q, size_t qn) {
+      const char *a = (const char*)p, *b = (const char*)q;
+      return p && q && a < b + qn && b < a + pn;
+    };
+    const size_t n4 = (size_t)tokens * hidden * sizeof(float), n2 = (size_t)tokens * hidden * 2;
+    if (overlap(residual_out, n4, residual, n4) || overlap(residual_out, n4, y, n2))
+      fail("wm_norm_router: residual_out must not overlap residual or y (other blocks still read them)");
+    if (overlap(x, n2, residual, n4) || overlap(x, n2, y, n2))
+      fail("wm_norm_router: x must not overlap residual or y (other blocks still read them)");
     if (router_packed && (hidden % 32 || router_packed_bytes != wm_router_packed_bytes(experts, hidden, shared_gate != nullptr)))
       fail("wm_norm_router: the packed router does not match experts, hidden and the shared gate (wm_router_packed_bytes)");
     for (const void* p : {(const void*)residual, y, norm_weight, router, shared_gate, router_packed, (const void*)x,
