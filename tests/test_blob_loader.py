@@ -168,3 +168,45 @@ def test_scatter_reads_resume_after_short_reads(tmp_path, monkeypatch):
 
     monkeypatch.setattr(blob_loader.os, "preadv", trickle)
     assert np.array_equal(ExpertFiles(tmp_path).read(pinned=False).numpy(), want)
+
+
+# The reference's expert region tables (runtime/deepseek_v4_ssd/manifest.py:21-42): name,
+# dtype, shape, offset, length, with the blob size, hidden and intermediate they imply.
+REFERENCE_LAYOUTS = {
+    "deepseek-v4": (13_369_344, 4096, 2048, [
+        ("w1.weight", "I8", [2048, 2048], 0, 4_194_304), ("w1.scale", "F8_E8M0", [2048, 128], 4_194_304, 262_144),
+        ("w2.weight", "I8", [4096, 1024], 4_456_448, 4_194_304), ("w2.scale", "F8_E8M0", [4096, 64], 8_650_752, 262_144),
+        ("w3.weight", "I8", [2048, 2048], 8_912_896, 4_194_304), ("w3.scale", "F8_E8M0", [2048, 128], 13_107_200, 262_144)]),
+    "deepseek-v4.1": (18_800_640, 5120, 2304, [
+        ("w1.weight", "I8", [2304, 2560], 0, 5_898_240), ("w1.scale", "F8_E8M0", [2304, 160], 5_898_240, 368_640),
+        ("w2.weight", "I8", [5120, 1152], 6_266_880, 5_898_240), ("w2.scale", "F8_E8M0", [5120, 72], 12_165_120, 368_640),
+        ("w3.weight", "I8", [2304, 2560], 12_533_760, 5_898_240), ("w3.scale", "F8_E8M0", [2304, 160], 18_432_000, 368_640)]),
+    "qwen": (2_611_200, 2560, 640, [
+        ("gate_up.weight", "U32", [1280, 320], 0, 1_638_400), ("gate_up.scale", "U8", [1280, 80], 1_638_400, 102_400),
+        ("down.weight", "U32", [2560, 80], 1_740_800, 819_200), ("down.scale", "U8", [2560, 20], 2_560_000, 51_200)]),
+}
+
+
+@pytest.mark.parametrize("model", sorted(REFERENCE_LAYOUTS))
+def test_reference_region_tables_are_accepted(tmp_path, model):
+    """The loader accepts the reference's own region tables, derives their shapes, and lands
+    one expert's bytes in slot order (DeepSeek: w3 | w1 | w3.scale | w1.scale | w2 | w2.scale)."""
+    blob, hidden, inter, regions = REFERENCE_LAYOUTS[model]
+    (tmp_path / "experts").mkdir()
+    rng = np.random.default_rng(len(model))
+    data = rng.integers(0, 256, size=blob, dtype=np.uint8)
+    (tmp_path / "experts" / "layer_00.bin").write_bytes(data.tobytes())
+    manifest = {"files": [{"path": "experts/layer_00.bin", "size": blob}],
+                "expertRegions": [{"name": n, "dtype": d, "shape": sh, "offset": o, "length": ln}
+                                  for n, d, sh, o, ln in regions]}
+    (tmp_path / "manifest.json").write_text(json.dumps(manifest))
+    files = ExpertFiles(tmp_path)
+    assert (files.blob, files.hidden, files.inter, files.experts, files.layers) == (blob, hidden, inter, 1, 1)
+    assert files.blob == qwen_blob_bytes(hidden, inter)
+    got = files.read(pinned=False).numpy()
+    span = {n: data[o:o + ln] for n, _, _, o, ln in regions}
+    order = (("gate_up.weight", "gate_up.scale", "down.weight", "down.scale") if model == "qwen" else
+             ("w3.weight", "w1.weight", "w3.scale", "w1.scale", "w2.weight", "w2.scale"))
+    assert np.array_equal(got, np.concatenate([span[n] for n in order]))
+    t = files.table(files.read(pinned=False), 0)
+    assert t.up_first == (model != "qwen") and (t.hidden, t.inter) == (hidden, inter)
