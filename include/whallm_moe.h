@@ -107,7 +107,8 @@ WM_EXPORT int wm_route_scored(const float* logits, const float* bias, int32_t to
                               void* stream);
 /* logits[t, e] = x[t] . w[e] for bf16 x [T, H] and bf16 w [E, H], fp32 out: the
  * router linear (SparseMoE.gate, qwen4_exp.py:1000; linear_bf16,
- * Native/QwenNative/kernels.metal:18-67). */
+ * Native/QwenNative/kernels.metal:18-67). 64+ tokens with hidden a multiple of 32 run on
+ * bf16 MFMA (the GEMM of wm_norm_router); fewer run one wave per output. */
 WM_EXPORT int wm_linear_bf16(const void* x, const void* w, int32_t tokens, int32_t hidden, int32_t outputs,
                              float* out, void* stream);
 

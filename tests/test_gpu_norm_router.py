@@ -135,3 +135,16 @@ def test_packed_router_is_bit_identical(device, T, H, E, with_gate):
     if T >= 16:
         with pytest.raises(Exception, match="does not match"):
             wa.norm_router(r, y, router, None if with_gate else bf16_tensor(rng, (H,), device), router_packed=packed)
+
+
+@pytest.mark.parametrize("T,H,E", [(300, 2048, 512), (70, 7168, 256), (64, 1024, 64), (63, 2048, 128)])
+def test_linear_bf16_prefill_path(device, T, H, E):
+    """wm_linear_bf16 at 64+ tokens runs on the router GEMM's MFMA path (a tile of x as
+    given): within the dot-product bound of the float64 product; 63 tokens stay on the
+    one-wave-per-output kernel."""
+    rng = np.random.default_rng(T + E)
+    x = bf16_tensor(rng, (T, H), device)
+    w = bf16_tensor(rng, (E, H), device, 0.05)
+    got = wa.linear_bf16(x, w)
+    torch.cuda.synchronize()
+    check_dot(got.cpu().numpy(), x.float().cpu().numpy(), w.float().cpu().numpy())

@@ -34,9 +34,17 @@ template <int TB>
 __device__ __forceinline__ void build_x_tile(const float* __restrict__ r, const uint16_t* __restrict__ y,
                                              const uint16_t* __restrict__ nw, int t0, int nt, int hidden, float eps,
                                              bool writer, uint16_t* __restrict__ x_out, float* __restrict__ r_out,
-                                             uint4* tile, int stride, float* inv_s) {
+                                             uint4* tile, int stride, float* inv_s,
+                                             const uint16_t* __restrict__ xin = nullptr) {
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int chunks = hidden / 8;
+  if (xin) {  // a plain linear: the tile is the given bf16 rows
+    for (int t = 0; t < TB; ++t)
+      for (int c = threadIdx.x; c < chunks; c += 256)
+        tile[t * stride + c] = t < nt ? ((const uint4*)(xin + (int64_t)(t0 + t) * hidden))[c] : make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    return;
+  }
   constexpr int QU = 8;  // float4 loads in flight per lane
   const int quads = hidden / 4;
   for (int t = wave; t < nt; t += 4) {
@@ -235,14 +243,14 @@ __global__ void __launch_bounds__(256) norm_router_mfma_kernel(
     const float* __restrict__ r, const uint16_t* __restrict__ y, const uint16_t* __restrict__ nw, int tokens,
     int hidden, float eps, const uint16_t* __restrict__ router, int experts, const uint16_t* __restrict__ gate,
     const uint4* __restrict__ packed, uint16_t* __restrict__ x_out, float* __restrict__ r_out,
-    float* __restrict__ logits, float* __restrict__ shared_logit) {
+    float* __restrict__ logits, float* __restrict__ shared_logit, const uint16_t* __restrict__ xin) {
   extern __shared__ uint4 x_tile[];  // [TB][hidden / 8 + 1]
   __shared__ float inv_s[TB];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int t0 = blockIdx.x * TB;
   const int nt = min(TB, tokens - t0);
   const int chunks = hidden / 8, stride = chunks + 1, steps = hidden / 32;
-  build_x_tile<TB>(r, y, nw, t0, nt, hidden, eps, true, x_out, r_out, x_tile, stride, inv_s);
+  build_x_tile<TB>(r, y, nw, t0, nt, hidden, eps, xin == nullptr, x_out, r_out, x_tile, stride, inv_s, xin);
 
   const int rows = experts + (gate ? 1 : 0);
   const int groups = (rows + 15) / 16;
@@ -333,6 +341,25 @@ static int pick_token_block(int tokens, int hidden) {
   return 1;
 }
 
+// logits = x . w^T on the router GEMM's MFMA path (a tile of x as given, no norm), for
+// wm_linear_bf16 at 64+ tokens. False when the shape does not suit it (the caller then uses
+// the one-wave-per-output kernel).
+bool linear_bf16_mfma(const void* x, const void* w, int tokens, int hidden, int outputs, float* out, hipStream_t s) {
+  const int tb = tokens >= 64 ? mfma_token_block(tokens, hidden) : 0;
+  if (!tb || ((uintptr_t)x % 16) || ((uintptr_t)w % 16)) return false;
+  const int blocks = (tokens + tb - 1) / tb;
+  const size_t lds = (size_t)tb * (hidden / 8 + 1) * 16;
+#define WM_LIN(TB) hipLaunchKernelGGL(norm_router_mfma_kernel<TB>, dim3(blocks), dim3(256), lds, s, nullptr, nullptr, \
+                                      nullptr, tokens, hidden, 0.0f, (const uint16_t*)w, outputs, nullptr, nullptr, \
+                                      nullptr, nullptr, out, nullptr, (const uint16_t*)x)
+  if (tb == 32) WM_LIN(32);
+  else if (tb == 16) WM_LIN(16);
+  else WM_LIN(8);
+#undef WM_LIN
+  check_launch("linear_bf16 (MFMA)");
+  return true;
+}
+
 }  // namespace wm
 
 using namespace wm;
@@ -397,7 +424,8 @@ WM_EXPORT int wm_norm_router(const float* residual, const void* y, const void* n
 #define WM_NRM(TB) hipLaunchKernelGGL(norm_router_mfma_kernel<TB>, dim3(blocks), dim3(256), lds, s, residual, \
                                       (const uint16_t*)y, (const uint16_t*)norm_weight, tokens, hidden, eps, \
                                       (const uint16_t*)router, experts, (const uint16_t*)shared_gate, \
-                                      (const uint4*)router_packed, (uint16_t*)x, residual_out, logits, shared_logit)
+                                      (const uint4*)router_packed, (uint16_t*)x, residual_out, logits, shared_logit, \
+                                      nullptr)
       if (mfma_tb == 32) WM_NRM(32);
       else if (mfma_tb == 16) WM_NRM(16);
       else WM_NRM(8);

@@ -7,6 +7,8 @@
 
 namespace wm {
 
+bool linear_bf16_mfma(const void* x, const void* w, int tokens, int hidden, int outputs, float* out, hipStream_t s);
+
 constexpr int ROUTE_MAX_K = 32;
 
 template <int PER_LANE>
@@ -201,6 +203,8 @@ WM_EXPORT int wm_linear_bf16(const void* x, const void* w, int32_t tokens, int32
     if (tokens < 0 || outputs < 0 || hidden < 2 || hidden % 2) fail("wm_linear_bf16: bad shape");
     if (tokens == 0 || outputs == 0) return;
     if (!x || !w || !out) fail("wm_linear_bf16: null pointer");
+    // 64+ tokens: the router GEMM on MFMA (norm_router.hip); else one wave per output
+    if (linear_bf16_mfma(x, w, tokens, hidden, outputs, out, as_stream(stream))) return;
     hipLaunchKernelGGL(linear_bf16_kernel, dim3((outputs + 3) / 4, tokens), dim3(256), 0, as_stream(stream),
                        (const uint32_t*)x, (const uint32_t*)w, tokens, hidden, outputs, out);
     check_launch("linear_bf16");
