@@ -91,13 +91,13 @@ class DecodeStack:
 
     def _body(self):
         if self.impl == "persistent":
-            self.stack(self.logits, self.residual.view(-1), self.x_out.view(-1))
+            self.stack(self.logits, self.residual.view(-1), self.x_out.view(-1), check=False)
         else:
             self.stack(self.logits, self.residual, self.x_out)
 
     def check(self):
-        if self.impl == "persistent" and self.stack.status() != 0:
-            raise RuntimeError("persistent decode: a message exchange stalled (status word set)")
+        if self.impl == "persistent":
+            self.stack.raise_for_status()
 
     def kernel_ms(self, launches: int) -> float:
         """Average duration of the persistent kernel itself: HIP events recorded on the

@@ -2,8 +2,10 @@
  *
  * Conventions (mirroring Native/QwenNative/capi.h:1-5 and capi.mm:20-37):
  *  - every entry point returns int: 0 on success, 1 on an error whose message
- *    wm_last_error() returns (per calling thread); nothing is launched when an
- *    argument check fails;
+ *    wm_last_error() returns (per calling thread), 2 when the caller's cancel hook
+ *    stopped the call; nothing is launched when an argument check fails; after a
+ *    nonzero status of a call that carries state (a decode stack, a residual), that
+ *    state must be reset before it is used again;
  *  - pointers are device pointers unless named host_*; sizes are element counts;
  *  - `stream` is a hipStream_t (NULL = the default stream); work is enqueued,
  *    not waited for. Outputs are caller-owned and valid once the stream reaches
@@ -18,6 +20,12 @@
  * An expert table locates expert e's regions at base + slot(e) * stride, which
  * covers both per-slot blobs (stride = blob size) and the region-major layer
  * buffers of expert_layout.py:83-119 (stride = region size).
+ *
+ * Expert ids and residency: a pair whose id is outside [0, experts) or whose slot map
+ * entry is negative (an expert that is not resident) contributes nothing to a layer
+ * output and gives a zero row in the per-pair (router order) outputs; a pair with a
+ * negative id leaves its per-pair output row unwritten, so a layer can be run in two
+ * calls over complementary pair masks (ready experts first, the rest after their fills).
  */
 #ifndef WHALLM_MOE_H
 #define WHALLM_MOE_H
@@ -156,6 +164,26 @@ WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* ind
 WM_EXPORT int wm_repack_prefill_mxfp4(const wm_mxfp4_experts* src, void* gate_up, void* gate_up_scales,
                                       void* down, void* down_scales, void* stream);
 
+/* Combine of per-pair rows [T, K, H] bf16 in router order (the output of
+ * wm_experts_mxfp4 / wm_experts_fp8): y[t] = sum_k weights[t, k] * rows[t, k] (+ add[t]),
+ * fp32 in k order, bf16 out; add (nullable) bf16 [T, H], e.g. the gated shared expert.
+ * SparseMoE._combine (qwen4_exp.py:1048-1051) and _route_reduce + shared (model.py:540-546).
+ * rows, add and y 16-byte aligned, hidden a multiple of 8, k <= 64. */
+WM_EXPORT int wm_combine_pairs(const void* rows, const float* weights, int32_t tokens, int32_t k, int32_t hidden,
+                               const void* add, void* y, void* stream);
+
+/* The reference's bf16 shared expert: y[t] = add[t] + g(t) * down(silu(x[t] gate_w^T) * (x[t] up_w^T)),
+ * g(t) = sigmoid(x[t] . gate_vec) (1 when gate_vec is NULL), the act rounded to bf16 once.
+ * MLP (qwen4_exp.py:763-771) with shared_expert_gate (:1002-1003, :1045); native
+ * engine.mm:2075-2079. x [T, H], gate_w / up_w [I, H], down_w [H, I], gate_vec [H], add and y
+ * [T, H], all bf16 and 16-byte aligned; add (nullable) may alias y. H and I multiples of
+ * 32. Fewer than 64 tokens run two GEMV kernels, more the bf16 MFMA GEMM of wm_linear_bf16.
+ * workspace: wm_mlp_bf16_workspace_size bytes. */
+WM_EXPORT size_t wm_mlp_bf16_workspace_size(int32_t tokens, int32_t hidden, int32_t inter);
+WM_EXPORT int wm_mlp_bf16(const void* x, int32_t tokens, int32_t hidden, int32_t inter, const void* gate_w,
+                          const void* up_w, const void* down_w, const void* gate_vec, const void* add, void* y,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- FP8-E4M3 expert FFN (fp32 128x128 block scales) ----------------------
  * The DeepSeek-V3 expert format (runtime/deepseek_v4_ssd/mimo/weights.py:17-43):
  * SharedExpert / routed experts of deepseek_v41/moe.py:77-93, y = W2(swiglu(W1 x, W3 x)),
@@ -227,13 +255,18 @@ WM_EXPORT int wm_repack_router(const void* router, const void* shared_gate, int3
  * experts / shared / shared_gates are host arrays of `layers` entries (shared and
  * shared_gates nullable). The per-layer loop of the native engine
  * (Native/QwenNative/engine.mm:1567-1588, experts() at :2073-2236). x_out (nullable)
- * receives the last rmsnorm(r_L). */
+ * receives the last rmsnorm(r_L). cancel (nullable) is the reference's cancel callback
+ * (wq_cancel_fn, Native/QwenNative/capi.h:36-37; Engine::set_cancel, engine.h:112-113):
+ * it is called with cancel_context before each layer is enqueued, and a nonzero return
+ * stops the call with status 2; the layers already enqueued still run, so the residual
+ * must then be restored by the caller. */
 WM_EXPORT size_t wm_moe_stack_mxfp4_workspace_size(int32_t tokens, int32_t k, const wm_mxfp4_experts* experts);
 WM_EXPORT int wm_moe_stack_mxfp4(const float* logits, int32_t layers, int32_t tokens, int32_t k,
                                  int32_t norm_topk_prob, const wm_mxfp4_experts* experts,
                                  const wm_mxfp4_experts* shared, const void* const* shared_gates,
                                  float* residual, float eps, void* x_out, void* workspace,
-                                 size_t workspace_bytes, void* stream);
+                                 size_t workspace_bytes, int (*cancel)(void*), void* cancel_context,
+                                 void* stream);
 
 /* ---- persistent decode (one kernel per token through every layer) ----------
  * Per-layer descriptor of the persistent decode kernel. Routed experts keep the
@@ -270,20 +303,36 @@ WM_EXPORT size_t wm_decode_state_size(int32_t layers, int32_t experts);
  * (8 XCDs x 32): x_l = rmsnorm(r_l); r_{l+1} = r_l + bf16(MoE_l(x_l)) with top-k
  * softmax routing from logits [layers, E] (fp32). layers_dev: device array of
  * wm_decode_layer. residual fp32 [H] in/out; x_out (nullable) bf16 rmsnorm(r_L).
- * Supports hidden 2048, inter 512, k <= 11, one token. A stalled
- * exchange ends the kernel after a bounded wait and makes wm_decode_status report it.
- * Calls that share a state buffer must be stream-ordered. */
+ * Supports hidden 2048, inter 512, k <= 11, one token.
+ * down_row_layout: 0 when every descriptor's down regions are slice-major
+ * (wm_repack_down_slices), 1 when they are in the reference row layout (e.g. the blobs
+ * of a slot cache, read in place).
+ * cancel (nullable): an int32 the host may set while the launch runs (pinned host
+ * memory, or device memory written from another stream); it is read once per layer,
+ * and a nonzero value ends the launch after that layer with status 2 (the device
+ * counterpart of the reference's per-layer cancel poll, Native/QwenNative/capi.h:36-37).
+ * The launch runs asynchronously, so the outcome is in the state's status word
+ * (wm_decode_status_offset): 0 done, 1 a message wait ran out, 2 cancelled, 3 a selected
+ * expert is not resident (negative slot map entry; checked before any layer runs).
+ * A launch that ends with a nonzero status leaves residual and x_out unchanged; the
+ * state must then be zero-filled again. Calls that share a state buffer must be
+ * stream-ordered.
+ * residual_trace (nullable): fp32 [layers, H] receives the residual after every layer
+ * (row l = r_{l+1}), for per-layer verification; no counterpart in the reference. */
 WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers, int32_t experts, int32_t k,
                                              int32_t hidden, int32_t inter, const wm_decode_layer* layers_dev,
                                              float* residual, float eps, void* x_out, void* state,
-                                             size_t state_bytes, void* stream);
-/* Device word of the state buffer that a stalled exchange sets (0 = healthy). */
+                                             size_t state_bytes, int32_t down_row_layout, const int32_t* cancel,
+                                             float* residual_trace, void* stream);
+/* Byte offset of the state buffer's int32 status word (0 = healthy; see above). */
 WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts);
 /* 1 when the current device runs block b of the persistent launch on XCC b % 8, so
  * messages read only within one XCD use XCD-local stores; 0 when it does not (the
  * persistent launch then uses device-scope stores throughout); -1 on error. Checked
- * once per device with a probe launch on `stream`. No counterpart in the reference
- * (an MI355X placement detail of the persistent decode). */
+ * once per device with a probe launch on `stream` (it allocates and synchronises; a
+ * persistent launch into a stream being captured skips the probe and uses device-scope
+ * stores unless this was called before). No counterpart in the reference (an MI355X
+ * placement detail of the persistent decode). */
 WM_EXPORT int wm_decode_xcd_local(void* stream);
 
 /* ---- HBM expert slot cache ----------------------------------------------------
@@ -317,6 +366,17 @@ WM_EXPORT int wm_slot_cache_plan(wm_slot_cache* cache, int32_t file, const int32
  * for the fills, so work enqueued after this call sees the experts resident. */
 WM_EXPORT int wm_slot_cache_acquire(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
                                     int32_t* out_slots, void* compute_stream);
+/* Cached-first acquire (the native engine's ready-then-late pair order,
+ * Native/QwenNative/engine.mm:2204-2234; ExpertCache.iter_ready, expert_cache.py:1541-1645):
+ * plan as wm_slot_cache_acquire and enqueue the misses' fills on the copy stream (after the
+ * work already on compute_stream), but do not make compute_stream wait for them.
+ * out_ready[i] = 1 where the expert was already resident: work enqueued on compute_stream
+ * right away may read those experts (no fill of the plan touches their slots), e.g. a layer
+ * call whose other pairs are masked with id -1. wm_slot_cache_wait_fills then makes
+ * compute_stream wait for the fills, after which the remaining pairs may run. */
+WM_EXPORT int wm_slot_cache_acquire_ready(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
+                                          int32_t* out_slots, int32_t* out_ready, void* compute_stream);
+WM_EXPORT int wm_slot_cache_wait_fills(wm_slot_cache* cache, void* compute_stream);
 /* Route mode (ExpertCache with eviction_policy "route", expert_cache.py:1131-1181): scores
  * [files * experts] (host, the route policy's retention scores) and quotas [files] (its
  * per-file slot targets) are copied; later victims are the resident expert with the lowest
@@ -338,8 +398,65 @@ WM_EXPORT int wm_slot_cache_wait_layer(wm_slot_cache* cache, int32_t file, void*
  * copy stream; compute_stream then waits for them. out_slots[n] receives the slots. */
 WM_EXPORT int wm_slot_cache_seed(wm_slot_cache* cache, int32_t file, const int32_t* experts, const int32_t* uses,
                                  int32_t n, const void* layer, int32_t* out_slots, void* compute_stream);
-/* out4 = (hits, misses, bytes copied, fills) since open. */
-WM_EXPORT int wm_slot_cache_stats(const wm_slot_cache* cache, int64_t* out4);
+/* One plan over several files (layers): n_files requests, request r = counts[r] experts of
+ * files[r], the experts (host ids) and out_slots concatenated in request order. Every slot
+ * the plan hands out is protected from its own evictions, so all requested experts are
+ * resident together afterwards, as one launch over several layers (the persistent decode
+ * stack) needs. Fills and map refreshes as wm_slot_cache_acquire. */
+WM_EXPORT int wm_slot_cache_acquire_files(wm_slot_cache* cache, int32_t n_files, const int32_t* files,
+                                          const int32_t* counts, const int32_t* experts, int32_t* out_slots,
+                                          void* compute_stream);
+/* The listed experts (host ids, sorted and unique) of `file` from the host pool into dst at
+ * their offsets in the file (blob e at e * blob_bytes), one copy per run of consecutive ids
+ * of at most 32 blobs, on the copy stream after the work already on compute_stream; the
+ * reference's prefill reads of the routed experts (expert_cache.py:2062-2085, batched by
+ * contiguous_batches, qwen_streaming_policy.py:7-20). wm_slot_cache_wait_layer waits for it. */
+WM_EXPORT int wm_slot_cache_read_experts(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
+                                         void* dst, void* compute_stream);
+/* Prompt-tail seeding (ExpertCache._seed_from_batched_layer, expert_cache.py:1399-1430, with
+ * hot_tail_experts, qwen_streaming_policy.py:23-45): routes [rows, k] int32 on the device
+ * (written on compute_stream) are ranked on the device: over the last 128 rows, experts by
+ * count, then latest position, then id; the first `limit` that are not resident are copied
+ * from `layer` (the file's device copy) into free slots only, the most valuable first when
+ * free slots run short (a prediction never evicts a demand-loaded expert). Synchronises
+ * compute_stream to read the ranking. out_experts / out_slots (host, limit entries) receive
+ * the seeded experts, least valuable first, and *out_count their number. E <= 1024. */
+WM_EXPORT int wm_slot_cache_seed_tail(wm_slot_cache* cache, int32_t file, const int32_t* routes, int64_t rows,
+                                      int32_t k, int32_t limit, const void* layer, int32_t* out_experts,
+                                      int32_t* out_slots, int32_t* out_count, void* compute_stream);
+/* out5 = (hits, misses, bytes copied, blobs filled, copies issued) since open. */
+WM_EXPORT int wm_slot_cache_stats(const wm_slot_cache* cache, int64_t* out5);
+
+/* ---- the slot cache's route-history policy (route mode with its own scores) --------
+ * The reference's RouteCachePolicy (runtime/deepseek_v4_ssd/route_cache.py:12-120) as used
+ * by ExpertCache (expert_cache.py:1088-1181), files = layers: two decayed decode routing
+ * rates per (layer, expert) (half-lives 16 and 256 tokens of the layer), the prompt's
+ * routes as a prior of weight 0.1 fading as 2^(-t/32) with the request's decode tokens,
+ * a per-layer read cost relative to the median layer (clipped to [0.5, 2]), retention
+ * score = (0.75 short + 0.25 long + prior) * cost, slot quotas per layer by marginal
+ * value; rebalanced every 16 * layers decode tokens, when a prefill phase ends and on
+ * request. In route mode the cache evicts by these scores and quotas (see set_route);
+ * wm_slot_cache_acquire / acquire_ready / acquire_files observe the requested ids as
+ * routes of the current phase. top_k 0 turns route mode off. */
+WM_EXPORT int wm_slot_cache_route_policy(wm_slot_cache* cache, int32_t top_k);
+/* Routes of `file` (token-major, top_k ids a token) that did not go through an acquire,
+ * e.g. a batched prefill that reads whole files (observe_batched_routes). */
+WM_EXPORT int wm_slot_cache_route_observe(wm_slot_cache* cache, int32_t file, const int32_t* experts, int64_t n,
+                                          int32_t prefill);
+/* The phase of the routes observed next: prefill (1) or decode (0); leaving a prefill
+ * rebalances (ExpertCache.trace_routes). */
+WM_EXPORT int wm_slot_cache_route_phase(wm_slot_cache* cache, int32_t prefill);
+/* A new prompt: its routes become the prior (ExpertCache.begin_route_request). */
+WM_EXPORT int wm_slot_cache_route_begin_request(wm_slot_cache* cache);
+/* One expert read's duration for `file`, in seconds (nonpositive or non-finite ignored). */
+WM_EXPORT int wm_slot_cache_route_record_read(wm_slot_cache* cache, int32_t file, double seconds);
+WM_EXPORT int wm_slot_cache_route_rebalance(wm_slot_cache* cache);
+/* The policy's state, every pointer nullable: scores [files * experts], quotas [files],
+ * the short and long decayed rates [files * experts] at each file's current token count,
+ * tokens [2 * files] (decode tokens, then prompt tokens, per file), read_cost [files],
+ * counters [2] = (rebalances, slot capacity). */
+WM_EXPORT int wm_slot_cache_route_state(wm_slot_cache* cache, double* scores, int32_t* quotas, double* short_rates,
+                                        double* long_rates, int64_t* tokens, double* read_cost, int64_t* counters);
 
 /* ---- MTP acceptance ----------------------------------------------------------
  * Verify n draft tokens (n <= 15) against n + 1 target rows [n + 1, vocab] fp32.

@@ -7,7 +7,12 @@ Pinning (tests/test_oracle_moe.py):
   renormalised full softmax (the two forms in qwen4_exp.py:1038-1042 and
   Native/QwenNative/engine.mm:2091-2096).
 * ``route_scored`` (DeepSeek sqrt-softplus / sigmoid / softmax with bias-select)
-  — closed form on hand-built rows; bias selects but does not weight.
+  — closed form on hand-built rows; bias selects but does not weight. Its scores
+  are the build's stated fp32 arithmetic (``exp_f32``, ``log1p_f32``,
+  ``score_f32``, the device's reduction order for softmax sums), so device and
+  oracle select identical experts; that arithmetic is pinned against float64
+  math to a few ulp over the whole input range and at special values (exp 0 = 1,
+  exp ln 2 = 2, sigmoid 0 = 1/2, softplus 0 = ln 2, under/overflow edges).
   Group-limited selection (n_groups > 1) has no reference implementation:
   PARITY UNPINNED against the reference; pinned only by brute force over all
   group subsets on tiny E.
@@ -69,6 +74,90 @@ def route_softmax_topk(logits: np.ndarray, k: int, norm_topk_prob: bool = True):
     return idx, w.astype(np.float32)
 
 
+# The router's score arithmetic, stated in fp32 operations (each rounded to nearest even,
+# no fused multiply-add) so that the device kernel (route_device.h) computes the same bits:
+#   exp_f32(x):   n = rint(x log2e); r = (x - n ln2_hi) - n ln2_lo; p = degree-7 Taylor
+#                 polynomial of e^r by Horner; e^x = p 2^n (0 when n < -125, +inf when n > 128);
+#   log1p_f32(u): u in [0, 1]: m = 1 + u, halved when above sqrt 2 (k = 1); s = (m - 1)/(m + 1);
+#                 ln m = k ln2 + 2 s (1 + z/3 + ... + z^5/11), z = s^2, plus the rounding
+#                 correction (u - (m - 1)) / m;
+#   sigmoid:      1 / (1 + exp_f32(-l));
+#   sqrt-softplus: sqrt(max(l, 0) + log1p_f32(exp_f32(-|l|))), and exp_f32(l / 2) below l = -64;
+#   softmax:      exp_f32(l - max) / sum, the sum in the device's wave order (softmax_sums_f32).
+F32 = np.float32
+LOG2E = F32(1.4426950408889634)
+LN2_HI = F32(0.693145751953125)       # 0x3F317200: n * LN2_HI is exact for |n| <= 256
+LN2_LO = F32(0.6931471805599453 - 0.693145751953125)
+SQRT2 = F32(1.4142135623730951)
+EXP_POLY = [F32(1.0 / f) for f in (1, 1, 2, 6, 24, 120, 720, 5040)]   # 1/j! for j = 0..7
+ATANH_POLY = [F32(1.0 / j) for j in (1, 3, 5, 7, 9, 11)]
+
+
+def exp_f32(x) -> np.ndarray:
+    x = np.asarray(x, F32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        n = np.rint(x * LOG2E)
+        r = (x - n * LN2_HI) - n * LN2_LO
+        p = EXP_POLY[7]
+        for c in reversed(EXP_POLY[:7]):
+            p = p * r + c
+        ni = np.where(np.isfinite(n), n, 0).astype(np.int32)
+        out = np.ldexp(p, ni).astype(F32)
+    out = np.where(n > 128, F32(np.inf), out)
+    out = np.where(n < -125, F32(0.0), out)
+    return np.where(np.isnan(x), F32(np.nan), out).astype(F32)
+
+
+def log1p_f32(u) -> np.ndarray:
+    u = np.asarray(u, F32)
+    m = F32(1.0) + u
+    k = m > SQRT2
+    m2 = np.where(k, m * F32(0.5), m)
+    s = (m2 - F32(1.0)) / (m2 + F32(1.0))
+    z = s * s
+    p = ATANH_POLY[5]
+    for c in reversed(ATANH_POLY[:5]):
+        p = p * z + c
+    lg = (s + s) * p
+    corr = (u - (m - F32(1.0))) / m
+    kf = k.astype(F32)
+    return (kf * LN2_HI + (kf * LN2_LO + (lg + corr))).astype(F32)
+
+
+def score_f32(logits: np.ndarray, func: str) -> np.ndarray:
+    """The router's scores in the stated fp32 arithmetic (sigmoid, sqrt-softplus, softmax)."""
+    l = np.asarray(logits, F32)
+    if func == "sigmoid":
+        return (F32(1.0) / (F32(1.0) + exp_f32(-l))).astype(F32)
+    if func == "sqrtsoftplus":
+        sp = np.maximum(l, F32(0.0)) + log1p_f32(exp_f32(-np.abs(l)))
+        return np.where(l < F32(-64.0), exp_f32(F32(0.5) * l), np.sqrt(sp)).astype(F32)
+    if func == "softmax":
+        top = l.max(axis=-1, keepdims=True)
+        e = exp_f32(l - top)
+        return (e / softmax_sums_f32(e)[..., None]).astype(F32)
+    raise ValueError(f"unknown score function {func!r}")
+
+
+def softmax_sums_f32(e: np.ndarray) -> np.ndarray:
+    """Row sums of e [.., E] in the router wave's order: lane j < 64 adds e[j], e[64 + j],
+    ... in turn; then pairs of lanes (j, j ^ 1), quads (j ^ 2), eights (mirrored in each
+    half row), sixteens (mirrored in each row), and the four rows as (r0 + r1) + (r2 + r3)."""
+    e = np.asarray(e, F32)
+    E = e.shape[-1]
+    per = (E + 63) // 64
+    pad = np.zeros(e.shape[:-1] + (per * 64,), F32)
+    pad[..., :E] = e
+    lanes = pad.reshape(e.shape[:-1] + (per, 64))
+    v = lanes[..., 0, :].copy()
+    for r in range(1, per):
+        v = v + lanes[..., r, :]
+    j = np.arange(64)
+    for partner in (j ^ 1, j ^ 2, (j & ~7) | (7 - (j & 7)), (j & ~15) | (15 - (j & 15))):
+        v = v + v[..., partner]
+    return ((v[..., 0] + v[..., 16]) + (v[..., 32] + v[..., 48])).astype(F32)
+
+
 def score_function(logits: np.ndarray, func: str) -> np.ndarray:
     """DeepSeek gate scores (deepseek_v41/moe.py:61-67; native sqrt-softplus at
     Native/DeepSeekNative/engine.mm:1875-1876), float64."""
@@ -88,15 +177,15 @@ def route_scored(logits: np.ndarray, bias: np.ndarray | None, k: int, func: str 
                  n_groups: int = 1, topk_groups: int = 1):
     """DeepSeek-style routing: the bias picks the experts but does not weight them.
 
-    Gate.__call__ (deepseek_v41/moe.py:58-74): s = f(l); selection on s + bias;
-    w = s[idx] / (sum + 1e-20) * route_scale. With n_groups > 1, the DeepSeek-V3
+    Gate.__call__ (deepseek_v41/moe.py:58-74): s = f(l) in the stated fp32 arithmetic
+    (score_f32); selection on the fp32 s + bias; w = s[idx] / (sum + 1e-20) * route_scale
+    (float64 sum). With n_groups > 1, the DeepSeek-V3
     group-limited rule (not in the reference): a group's score is the sum of
     its two largest biased scores, the topk_groups best groups are kept, and
     top-k runs over their experts. Ties go to the lower index (group or expert).
     """
-    s = score_function(logits, func)
-    biased = s + (0.0 if bias is None else np.asarray(bias, np.float64))
-    biased32 = biased.astype(np.float32)
+    s = score_f32(logits, func)
+    biased32 = (s + (F32(0.0) if bias is None else np.asarray(bias, F32))).astype(F32)
     T, E = biased32.shape
     if n_groups > 1:
         if E % n_groups:
@@ -109,7 +198,7 @@ def route_scored(logits: np.ndarray, bias: np.ndarray | None, k: int, func: str 
         np.put_along_axis(mask, keep, False, axis=-1)
         biased32 = np.where(np.repeat(mask, E // n_groups, axis=-1), np.float32(-np.inf), biased32)
     idx = topk_desc(biased32, k)
-    w = np.take_along_axis(s, idx, axis=-1)
+    w = np.take_along_axis(s, idx, axis=-1).astype(np.float64)
     if norm_topk_prob and k > 1:
         w = w / (w.sum(axis=-1, keepdims=True) + 1e-20)
     return idx, (w * route_scale).astype(np.float32)

@@ -70,7 +70,7 @@ def test_prefill_tile_layout_argument_checks():
                   None)
     with pytest.raises(_lib.WhallmError, match="prefill tile layout"):
         _lib.call("wm_moe_stack_mxfp4", 1, 1, 1, 2, 1, ctypes.byref(routed), None, None, 1, 1e-6, None, 1, 1 << 40,
-                  None)
+                  None, None, None)
     with pytest.raises(_lib.WhallmError, match="already in the prefill tile layout"):
         _lib.call("wm_repack_prefill_mxfp4", ctypes.byref(routed), 16, 16, 16, 16, None)
     # a tiled table always takes the grouped GEMM: its workspace is the prefill one, not the

@@ -3,7 +3,19 @@
 Chain (both sides): x_l = bf16(rmsnorm(r_l)); top-10 softmax routing from the
 layer's logits; y = sum_k w_k FFN_k(x_l) + sigmoid(x_l . g) FFN_shared(x_l);
 r_{l+1} = r_l + bf16(y). Tolerance: relative L2 <= 1e-2 and max |err| <=
-2e-2 * max |ref| on the final residual and on the rmsnorm output.
+2e-2 * max |ref|.
+
+Every layer is checked on its own: the kernel's residual trace gives r_l, the oracle
+computes layer l's y from it (the kernel's glue: the norm of layer l > 0 reads the bf16
+copy of r_l that the kernel broadcasts), and r_{l+1} - r_l must match bf16(y). This
+holds the timed configuration (48 layers x 512 experts) to the per-layer bar. The
+free-running chain is compared end to end only up to 6 layers: at these synthetic
+scales |y| is ~3e4 per layer against |r_0| ~ 45, and a 1e-4 relative perturbation of
+every layer's y moves the oracle's own 48-layer result by 1.6e-2 (bf16 roundings of y
+flip and the next norms carry the change), so no bound of 1e-2 is meaningful there.
+Also: the reference row layout of the down regions read in place (bit-identical to the
+slice-major copy), slot-cache tables, a non-resident expert (status 3), and
+cancellation (status 2) with recovery.
 """
 import numpy as np
 import pytest
@@ -13,7 +25,8 @@ import whallm_amd as wa
 from oracle import formats as F
 from oracle import moe as M
 from whallm_amd import synthetic as S
-from whallm_amd.ops import PersistentDecodeStack, repack_down_slices
+from whallm_amd._lib import Cancelled
+from whallm_amd.ops import DecodeStackError, PersistentDecodeStack, repack_down_slices
 
 pytestmark = pytest.mark.gpu
 
@@ -42,7 +55,7 @@ def test_repack_down_slices_bytes(device):
 
 
 class Chain:
-    def __init__(self, device, layers, experts, seed):
+    def __init__(self, device, layers, experts, seed, down_layout="slices"):
         rng = np.random.default_rng(seed)
         self.L, self.E = layers, experts
         self.arrays = [S.mxfp4_experts_np(rng, experts, H, I) for _ in range(layers)]
@@ -51,7 +64,7 @@ class Chain:
         self.dev = [S.experts_to_device(a, device) for a in self.arrays]
         self.dev_shared = [S.experts_to_device(a, device) for a in self.shared]
         self.dev_gates = [S.bf16_bits_to_tensor(g, device) for g in self.gates]
-        self.stack = PersistentDecodeStack(self.dev, self.dev_shared, self.dev_gates, k=K)
+        self.stack = PersistentDecodeStack(self.dev, self.dev_shared, self.dev_gates, k=K, down_layout=down_layout)
         self.rng = rng
 
     def inputs(self):
@@ -59,38 +72,54 @@ class Chain:
         r0 = self.rng.standard_normal(H).astype(np.float32)
         return logits, r0
 
+    def layer_y(self, l, logits, x):
+        """The oracle's MoE output of layer l for the bf16 input x [1, H]."""
+        idx, w = M.route_softmax_topk(logits[l][None], K)
+        a = self.arrays[l]
+        routed = np.stack([M.expert_ffn(x, M.MXFP4Expert(a["gate_up"][e], a["gate_up_scales"][e], a["down"][e],
+                                                          a["down_scales"][e]))[0] for e in idx[0]])[None]
+        s = self.shared[l]
+        sh = M.expert_ffn(x, M.MXFP4Expert(s["gate_up"][0], s["gate_up_scales"][0], s["down"][0],
+                                            s["down_scales"][0]))
+        g = x.astype(np.float64) @ S.bf16_bits_to_f32(self.gates[l]).astype(np.float64)
+        return M.combine(routed, w, sh, g)[0]
+
     def oracle(self, logits, r0):
         r = r0.astype(np.float64)
         for l in range(self.L):
-            x = M.rms_norm(r[None])
-            idx, w = M.route_softmax_topk(logits[l][None], K)
-            a = self.arrays[l]
-            experts = {int(e): M.MXFP4Expert(a["gate_up"][e], a["gate_up_scales"][e], a["down"][e],
-                                             a["down_scales"][e]) for e in idx[0]}
-            routed = np.stack([M.expert_ffn(x, experts[int(e)])[0] for e in idx[0]])[None]
-            s = self.shared[l]
-            sh = M.expert_ffn(x, M.MXFP4Expert(s["gate_up"][0], s["gate_up_scales"][0], s["down"][0],
-                                                s["down_scales"][0]))
-            g = x.astype(np.float64) @ S.bf16_bits_to_f32(self.gates[l]).astype(np.float64)
-            y = M.combine(routed, w, sh, g)[0]
-            r = r + F.bf16_round_f32(y)
+            r = r + F.bf16_round_f32(self.layer_y(l, logits, M.rms_norm(r[None])))
         return r.astype(np.float32), M.rms_norm(r[None])[0]
 
+    def check_layers(self, logits, r0, trace):
+        """Teacher-forced check of every layer from the kernel's residual trace [L, H]."""
+        prev = r0.astype(np.float32)
+        for l in range(self.L):
+            seen = prev if l == 0 else F.bf16_round_f32(prev)   # the bf16 broadcast feeds later norms
+            y = self.layer_y(l, logits, M.rms_norm(seen[None]))
+            close(trace[l].astype(np.float64) - prev.astype(np.float64), F.bf16_round_f32(y), f"layer {l}")
+            prev = trace[l]
 
-@pytest.mark.parametrize("layers,experts", [(1, 16), (6, 64), (3, 512)])
-def test_persistent_decode_matches_oracle_chain(device, layers, experts):
+
+@pytest.mark.parametrize("layers,experts,calls", [(1, 16, 3), (6, 64, 3), (3, 512, 3), (48, 512, 2)])
+def test_persistent_decode_matches_oracle_chain(device, layers, experts, calls):
     chain = Chain(device, layers, experts, seed=layers * 7 + experts)
     print(f"xcd_local={chain.stack.xcd_local()}", flush=True)
-    for call in range(3):  # successive launches advance the message epochs
+    for call in range(calls):  # successive launches advance the message epochs
         logits, r0 = chain.inputs()
         residual = torch.from_numpy(r0.copy()).to(device)
         x_out = torch.empty(H, dtype=torch.bfloat16, device=device)
-        chain.stack(torch.from_numpy(logits).to(device), residual, x_out)
+        trace = torch.empty(layers, H, dtype=torch.float32, device=device)
+        chain.stack(torch.from_numpy(logits).to(device), residual, x_out, trace=trace)
         torch.cuda.synchronize()
         assert chain.stack.status() == 0
-        want_r, want_x = chain.oracle(logits, r0)
-        close(residual.cpu().numpy(), want_r, f"residual call {call}")
-        close(x_out.float().cpu().numpy(), want_x, f"x_out call {call}")
+        tr = trace.cpu().numpy()
+        assert np.array_equal(tr[-1], residual.cpu().numpy())
+        chain.check_layers(logits, r0, tr)
+        close(x_out.float().cpu().numpy(), M.rms_norm(tr[-1][None].astype(np.float64))[0], f"x_out call {call}")
+        if layers <= 6:
+            want_r, want_x = chain.oracle(logits, r0)
+            close(residual.cpu().numpy(), want_r, f"residual call {call}")
+            close(x_out.float().cpu().numpy(), want_x, f"x_out call {call}")
 
 
 def test_persistent_decode_agrees_with_per_layer_path(device):
@@ -104,3 +133,119 @@ def test_persistent_decode_agrees_with_per_layer_path(device):
     stack(torch.from_numpy(logits[:, None, :].copy()).to(device), r_b.view(1, H))
     torch.cuda.synchronize()
     close(r_a.cpu().numpy(), r_b.cpu().numpy(), "persistent vs per-layer")
+
+
+def test_row_layout_equals_slice_layout(device):
+    """The down regions read in place (reference row layout) give the slice-major result bit
+    for bit: the same operands reach the same MFMAs."""
+    chain = Chain(device, 4, 64, seed=21)
+    rows = PersistentDecodeStack(chain.dev, chain.dev_shared, chain.dev_gates, k=K, down_layout="rows")
+    for _ in range(2):
+        logits, r0 = chain.inputs()
+        lt = torch.from_numpy(logits).to(device)
+        a, b = torch.from_numpy(r0.copy()).to(device), torch.from_numpy(r0.copy()).to(device)
+        chain.stack(lt, a)
+        rows(lt, b)
+        assert torch.equal(a, b)
+
+
+def _slot_cache_chain(device, layers, experts, seed):
+    from whallm_amd.slot_cache import SlotCache, qwen_blob_bytes
+    chain = Chain(device, layers, experts, seed=seed)
+    blob = qwen_blob_bytes(H, I)
+    pool = torch.empty(layers * experts * blob, dtype=torch.uint8).pin_memory()
+    host = pool.numpy().reshape(layers, experts, blob)
+    for l, a in enumerate(chain.arrays):
+        host[l] = np.concatenate([a["gate_up"].view(np.uint8).reshape(experts, -1), a["gate_up_scales"].reshape(experts, -1),
+                                  a["down"].view(np.uint8).reshape(experts, -1), a["down_scales"].reshape(experts, -1)],
+                                 axis=1)
+    cache = SlotCache(layers * (K + 4), H, I, layers, experts, pool, device)
+    stack = PersistentDecodeStack([cache.table(l) for l in range(layers)], chain.dev_shared, chain.dev_gates, k=K)
+    return chain, cache, stack
+
+
+def test_decode_served_from_the_slot_cache(device):
+    """Tables of a slot cache (refilled between tokens) are read in place: each token's routed
+    experts are acquired per layer, then one launch runs the stack; the result equals the
+    fully resident stack's bit for bit, and an expert that was not acquired ends the launch
+    with status 3 before any layer runs (residual unchanged, state reset)."""
+    layers, experts = 3, 64
+    chain, cache, stack = _slot_cache_chain(device, layers, experts, seed=22)
+    rows = PersistentDecodeStack(chain.dev, chain.dev_shared, chain.dev_gates, k=K, down_layout="rows")
+    assert stack.down_layout == "rows"
+    for token in range(3):
+        logits, r0 = chain.inputs()
+        # one plan over every layer: all of the token's experts resident together
+        cache.acquire_files({l: sorted(int(e) for e in M.route_softmax_topk(logits[l][None], K)[0][0])
+                             for l in range(layers)})
+        lt = torch.from_numpy(logits).to(device)
+        a, b = torch.from_numpy(r0.copy()).to(device), torch.from_numpy(r0.copy()).to(device)
+        stack(lt, a)
+        rows(lt, b)
+        assert torch.equal(a, b), token
+    # a token whose experts were never acquired for layer 1
+    logits, r0 = chain.inputs()
+    idx, _ = M.route_softmax_topk(logits[1][None], K)
+    cache.acquire_files({l: sorted(int(e) for e in M.route_softmax_topk(logits[l][None], K)[0][0]) for l in (0, 2)})
+    missing = [int(e) for e in idx[0] if int(cache.map[1][int(e)]) < 0]
+    assert missing, "the test expects some of layer 1's experts to be missing"
+    r = torch.from_numpy(r0.copy()).to(device)
+    with pytest.raises(DecodeStackError, match="not resident"):
+        stack(torch.from_numpy(logits).to(device), r)
+    assert torch.equal(r.cpu(), torch.from_numpy(r0))
+    cache.acquire_files({l: sorted(int(e) for e in M.route_softmax_topk(logits[l][None], K)[0][0])
+                         for l in range(layers)})
+    stack(torch.from_numpy(logits).to(device), r)      # the state was reset: the next launch runs
+    want_r, _ = chain.oracle(logits, r0)
+    close(r.cpu().numpy(), want_r, "after a non-resident launch")
+
+
+def test_persistent_cancel_and_recovery(device):
+    chain = Chain(device, 48, 128, seed=23)
+    cancel = torch.zeros(1, dtype=torch.int32).pin_memory()
+    trace = torch.empty(48, H, dtype=torch.float32, device=device)
+    logits, r0 = chain.inputs()
+    lt = torch.from_numpy(logits).to(device)
+    cancel[0] = 1                                       # set before the launch: stops at layer 0
+    r = torch.from_numpy(r0.copy()).to(device)
+    with pytest.raises(Cancelled):
+        chain.stack(lt, r, cancel=cancel)
+    assert torch.equal(r.cpu(), torch.from_numpy(r0))
+    cancel[0] = 0
+    chain.stack(lt, r, cancel=cancel, trace=trace)      # reset by the raise; runs to the end
+    done = r.cpu().numpy()
+    chain.check_layers(logits, r0, trace.cpu().numpy())
+    # set while the launch runs: it ends cancelled (residual unchanged) or, if it got there
+    # first, complete (the same residual as the run above: the launch is deterministic)
+    r = torch.from_numpy(r0.copy()).to(device)
+    chain.stack(lt, r, check=False, cancel=cancel)
+    cancel[0] = 1
+    torch.cuda.synchronize()
+    status = chain.stack.status()
+    print(f"mid-run cancel: status {status}", flush=True)
+    assert status in (0, 2)
+    if status == 2:
+        assert torch.equal(r.cpu(), torch.from_numpy(r0))
+        chain.stack.reset()
+    else:
+        assert np.array_equal(r.cpu().numpy(), done)
+
+
+def test_per_layer_stack_cancel_callback(device):
+    """The host-looped stack polls the reference-style callback before each layer: a
+    cancel after two layers returns status 2 (Cancelled); rerun from the saved residual the
+    stack matches the persistent kernel."""
+    chain = Chain(device, 5, 128, seed=24)
+    stack = wa.ops.MoEStack(chain.dev, chain.dev_shared, chain.dev_gates, k=K)
+    logits, r0 = chain.inputs()
+    lt = torch.from_numpy(logits[:, None, :].copy()).to(device)
+    polls = []
+    r = torch.from_numpy(r0.copy()).to(device).view(1, H)
+    with pytest.raises(Cancelled, match="layer 2"):
+        stack(lt, r, cancel=lambda: polls.append(1) or len(polls) > 2)
+    assert len(polls) == 3
+    r.copy_(torch.from_numpy(r0).view(1, H))
+    stack(lt, r)
+    p = torch.from_numpy(r0.copy()).to(device)
+    chain.stack(torch.from_numpy(logits).to(device), p)
+    close(r.view(-1).cpu().numpy(), p.cpu().numpy(), "per-layer stack vs persistent")

@@ -1,0 +1,189 @@
+"""GPU tests of expert residency, masked pairs and the cached-first order.
+
+- The slot cache's device map always equals the oracle arena's placement: an expert that
+  lost its slot to another file reads -1 in its own file's row.
+- A pair whose expert is not resident contributes nothing (zero per-pair row, no share of
+  the combine), on the decode GEMV and the grouped-GEMM paths, MXFP4 and FP8.
+- A pair with a negative id leaves its per-pair row as it was, so two calls over
+  complementary masks give the one-call result bit for bit.
+- The cached-first acquire (ready experts computed while the missing ones are copied in)
+  gives the all-resident result bit for bit.
+- The per-pair combine and the bf16 shared-expert MLP match the oracle's float64 closed
+  forms (relative L2 <= 1e-2, max |err| <= 2e-2 max |ref|).
+"""
+import numpy as np
+import pytest
+import torch
+
+import whallm_amd as wa
+from oracle import moe as M
+from whallm_amd import synthetic as S
+from whallm_amd.slot_cache import SlotCache, qwen_blob_bytes
+
+pytestmark = pytest.mark.gpu
+
+H, I = 256, 128
+
+
+def close(got, want, what):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert np.all(np.isfinite(got)), what
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    mx = np.abs(got - want).max() / max(np.abs(want).max(), 1e-30)
+    assert rel <= 1e-2 and mx <= 2e-2, f"{what}: rel L2 {rel:.3e} max {mx:.3e}"
+
+
+def blob_of(a, e):
+    return np.concatenate([a["gate_up"][e].view(np.uint8).reshape(-1), a["gate_up_scales"][e].reshape(-1),
+                           a["down"][e].view(np.uint8).reshape(-1), a["down_scales"][e].reshape(-1)])
+
+
+def make_pool(files, experts, seed, hidden=H, inter=I):
+    rng = np.random.default_rng(seed)
+    arrays = [S.mxfp4_experts_np(rng, experts, hidden, inter) for _ in range(files)]
+    blob = qwen_blob_bytes(hidden, inter)
+    pool = torch.empty(files * experts * blob, dtype=torch.uint8).pin_memory()
+    host = pool.numpy().reshape(files, experts, blob)
+    for f in range(files):
+        for e in range(experts):
+            host[f, e] = blob_of(arrays[f], e)
+    return arrays, pool
+
+
+def test_device_map_tracks_evictions(device):
+    files, experts, slots = 3, 24, 12
+    _, pool = make_pool(files, experts, 11)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    oracle = M.SlotArena(slots=slots, experts_per_layer=experts)
+    rng = np.random.default_rng(12)
+    for step in range(30):
+        f = int(rng.integers(files))
+        ids = [int(v) for v in rng.choice(experts, size=5, replace=False)]
+        cache.acquire(f, ids)
+        oracle.plan(f, ids)
+        torch.cuda.current_stream(device).synchronize()
+        want = np.full((files, experts), -1, np.int32)
+        for key, s in oracle.where.items():
+            want[key // experts, key % experts] = s
+        np.testing.assert_array_equal(cache.map.cpu().numpy(), want, err_msg=f"step {step}")
+
+
+@pytest.mark.parametrize("tokens", [4, 200])   # decode GEMV (T*K <= 256) and grouped GEMM
+def test_evicted_experts_contribute_nothing(device, tokens):
+    files, experts, slots, K = 2, 8, 8, 4
+    arrays, pool = make_pool(files, experts, 13)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    cache.acquire(0, list(range(8)))
+    cache.acquire(1, [0, 1, 2])          # takes three of file 0's slots (LFU: the oldest)
+    torch.cuda.current_stream(device).synchronize()
+    row = cache.map[0].cpu().numpy()
+    gone = [e for e in range(experts) if row[e] < 0]
+    assert len(gone) == 3, row
+    rng = np.random.default_rng(14)
+    idx = np.stack([rng.choice(experts, K, replace=False) for _ in range(tokens)]).astype(np.int32)
+    w = rng.random((tokens, K)).astype(np.float32)
+    x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, H)), device)
+    it, wt = torch.from_numpy(idx).to(device), torch.from_numpy(w).to(device)
+    dense = S.experts_to_device(arrays[0], device)
+    got = wa.experts_mxfp4(x, it, cache.table(0)).cpu()
+    want = wa.experts_mxfp4(x, it, dense).cpu()
+    dead = torch.from_numpy(np.isin(idx, gone))
+    assert bool((got[dead] == 0).all())
+    assert torch.equal(got[~dead], want[~dead])
+    # the layer: evicted pairs drop out of the combine (their weight counts as 0)
+    y = wa.moe_mxfp4(x, it, wt, cache.table(0)).float().cpu().numpy()
+    w0 = np.where(np.isin(idx, gone), 0.0, w).astype(np.float32)
+    y0 = wa.moe_mxfp4(x, it, torch.from_numpy(w0).to(device), dense).float().cpu().numpy()
+    np.testing.assert_allclose(y, y0, rtol=1e-2, atol=1e-6 * np.abs(y0).max())
+
+
+@pytest.mark.parametrize("tokens", [4, 200])
+def test_fp8_non_resident_slots_contribute_nothing(device, tokens):
+    E, Hf, If, K = 6, 256, 256, 2
+    rng = np.random.default_rng(15)
+    arrays = S.fp8_experts_np(rng, E, Hf, If)
+    dense = S.fp8_experts_to_device(arrays, device)
+    slots = torch.tensor([0, -1, 2, 3, -1, 5], dtype=torch.int32, device=device)
+    table = S.fp8_experts_to_device(arrays, device, slots=slots, experts=E)
+    idx = np.stack([rng.choice(E, K, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, Hf)), device)
+    it = torch.from_numpy(idx).to(device)
+    got = wa.experts_fp8(x, it, table).cpu()
+    want = wa.experts_fp8(x, it, dense).cpu()
+    dead = torch.from_numpy(np.isin(idx, [1, 4]))
+    assert bool((got[dead] == 0).all())
+    assert torch.equal(got[~dead], want[~dead])
+
+
+@pytest.mark.parametrize("kind,tokens", [("mxfp4", 6), ("mxfp4", 300), ("fp8", 6), ("fp8", 300)])
+def test_complementary_masks_equal_one_call(device, kind, tokens):
+    E, K = 16, 4
+    rng = np.random.default_rng(16 + tokens)
+    if kind == "mxfp4":
+        table = S.experts_to_device(S.mxfp4_experts_np(rng, E, H, I), device)
+        run, hid = wa.experts_mxfp4, H
+    else:
+        table = S.fp8_experts_to_device(S.fp8_experts_np(rng, E, 256, 256), device)
+        run, hid = wa.experts_fp8, 256
+    idx = np.stack([rng.choice(E, K, replace=False) for _ in range(tokens)]).astype(np.int32)
+    mask = rng.random(idx.shape) < 0.5
+    x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, hid)), device)
+    full = run(x, torch.from_numpy(idx).to(device), table)
+    out = torch.full((tokens, K, hid), 7.0, dtype=torch.bfloat16, device=device)
+    run(x, torch.from_numpy(np.where(mask, idx, -1)).to(device), table, out=out)
+    held = out.cpu()
+    m = torch.from_numpy(mask)
+    assert bool((held[~m] == 7.0).all()), "a masked pair's row was written"
+    run(x, torch.from_numpy(np.where(mask, -1, idx)).to(device), table, out=out)
+    assert torch.equal(out.cpu(), full.cpu())
+
+
+@pytest.mark.parametrize("tokens", [1, 40])
+def test_cached_first_acquire_equals_all_resident(device, tokens):
+    files, experts, slots, K = 2, 32, 28, 6
+    arrays, pool = make_pool(files, experts, 17)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    rng = np.random.default_rng(18)
+    cache.acquire(0, list(range(0, 12)))                     # half of what the step routes to
+    idx = np.stack([rng.choice(24, K, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, H)), device)
+    it = torch.from_numpy(idx).to(device)
+    unique = sorted(set(idx.reshape(-1).tolist()))
+    got = cache.experts_ready_first(0, x, it)
+    want = wa.experts_mxfp4(x, it, S.experts_to_device(arrays[0], device))
+    assert torch.equal(got.cpu(), want.cpu())
+    _, ready = cache.acquire_ready(0, unique)                # now every one is resident
+    assert all(ready)
+    cache.wait_fills()
+
+
+def test_combine_pairs_matches_oracle(device):
+    rng = np.random.default_rng(19)
+    T, K, Hc = 37, 10, 2048
+    rows = S.bf16_normal_np(rng, (T, K, Hc))
+    w = rng.random((T, K)).astype(np.float32)
+    add = S.bf16_normal_np(rng, (T, Hc))
+    y = wa.combine_pairs(S.bf16_bits_to_tensor(rows, device), torch.from_numpy(w).to(device),
+                         S.bf16_bits_to_tensor(add, device))
+    want = M.combine(S.bf16_bits_to_f32(rows), w) + S.bf16_bits_to_f32(add)
+    close(y.float().cpu().numpy(), want, "combine_pairs")
+
+
+@pytest.mark.parametrize("tokens,gated,added", [(1, True, True), (16, False, False), (130, True, True)])
+def test_mlp_bf16_matches_oracle(device, tokens, gated, added):
+    rng = np.random.default_rng(20 + tokens)
+    Hm, Im = 2048, 512
+    x = S.bf16_normal_np(rng, (tokens, Hm))
+    g, u = S.bf16_normal_np(rng, (Im, Hm), 0.02), S.bf16_normal_np(rng, (Im, Hm), 0.02)
+    d = S.bf16_normal_np(rng, (Hm, Im), 0.02)
+    gv = S.bf16_normal_np(rng, (Hm,), 0.02) if gated else None
+    add = S.bf16_normal_np(rng, (tokens, Hm), 0.1) if added else None
+    t = lambda a: None if a is None else S.bf16_bits_to_tensor(a, device)  # noqa: E731
+    y = wa.mlp_bf16(t(x), t(g), t(u), t(d), t(gv), t(add))
+    xf, gf, uf, df = (S.bf16_bits_to_f32(a).astype(np.float64) for a in (x, g, u, d))
+    want = (M.silu(xf @ gf.T) * (xf @ uf.T)) @ df.T
+    if gated:
+        want = want / (1.0 + np.exp(-(xf @ S.bf16_bits_to_f32(gv).astype(np.float64))))[:, None]
+    if added:
+        want = want + S.bf16_bits_to_f32(add)
+    close(y.float().cpu().numpy(), want, f"mlp_bf16 T={tokens}")

@@ -9,7 +9,7 @@ import torch
 import whallm_amd as wa
 from oracle import moe as M
 from whallm_amd import synthetic as S
-from whallm_amd.slot_cache import SlotCache, qwen_blob_bytes
+from whallm_amd.slot_cache import SlotCache, SlotCacheError, qwen_blob_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -100,9 +100,8 @@ def test_fill_waits_for_work_that_reads_the_evicted_slots(device):
 
 def test_layer_reads_seeding_and_route_mode(device):
     """A whole file read into one of two layer buffers lands bit-exact, the layer computed
-    from it matches the oracle, the prompt tail's hottest experts are seeded into slots from
-    that buffer (bytes and map), and route mode keeps serving fills."""
-    from whallm_amd.streaming_policy import hot_tail_experts
+    from it matches the oracle, the prompt tail's hottest experts are seeded into free slots
+    from that buffer (bytes and map), and route mode keeps serving fills."""
     files, experts, slots, K, T = 2, 16, 6, 4, 96
     arrays, pool = make_pool(files, experts, 7)
     cache = SlotCache(slots, H, I, files, experts, pool, device)
@@ -118,8 +117,9 @@ def test_layer_reads_seeding_and_route_mode(device):
         logits = rng.standard_normal((T, experts)).astype(np.float32)
         idx, w = M.route_softmax_topk(logits, K)
         x = S.bf16_normal_np(rng, (T, H))
-        y = wa.moe_mxfp4(S.bf16_bits_to_tensor(x, device), torch.from_numpy(idx.astype(np.int32)).to(device),
-                         torch.from_numpy(w.astype(np.float32)).to(device), cache.layer_table(buf))
+        it = torch.from_numpy(idx.astype(np.int32)).to(device)
+        y = wa.moe_mxfp4(S.bf16_bits_to_tensor(x, device), it, torch.from_numpy(w.astype(np.float32)).to(device),
+                         cache.layer_table(buf))
         ex = {e: M.MXFP4Expert(arrays[f]["gate_up"][e], arrays[f]["gate_up_scales"][e], arrays[f]["down"][e],
                                arrays[f]["down_scales"][e]) for e in range(experts)}
         want = M.moe_layer(S.bf16_bits_to_f32(x), logits, ex, K)[0]
@@ -128,10 +128,9 @@ def test_layer_reads_seeding_and_route_mode(device):
         host = buf.cpu().numpy().reshape(experts, blob)
         for e in range(experts):
             assert np.array_equal(host[e], blob_of(arrays[f], e)), (f, e)
-        # keep this prompt's hottest experts resident (least valuable first)
-        keep = hot_tail_experts(idx, experts, slots // files)
-        uses = [int((idx == e).sum()) for e in keep]
-        got_slots = cache.seed(f, keep, uses, buf)
+        # keep this prompt's hottest experts resident (free slots only)
+        keep, got_slots = cache.seed_tail(f, it, slots // files, buf)
+        assert keep == tail_ranking(idx, experts, slots // files)
         torch.cuda.current_stream(device).synchronize()
         mem = cache.slot_memory.view(slots, blob).cpu().numpy()
         row = cache.map[f].cpu().numpy()
@@ -145,6 +144,79 @@ def test_layer_reads_seeding_and_route_mode(device):
     mem = cache.slot_memory.view(slots, blob).cpu().numpy()
     for e, s in zip(ids, got):
         assert np.array_equal(mem[s], blob_of(arrays[1], e))
+    assert cache.route_state()["decode_tokens"][1] == 1     # the request counted as routes
+
+
+def tail_ranking(routes, experts, limit):
+    """Brute force of the prompt-tail ranking: the last 128 token rows, experts by count,
+    then latest position, then id; the first `limit`, least valuable first."""
+    flat = np.asarray(routes).reshape(-1, np.asarray(routes).shape[-1])[-128:].reshape(-1).tolist()
+    stats = {e: (flat.count(e), max(i for i, v in enumerate(flat) if v == e)) for e in set(flat) if 0 <= e < experts}
+    return sorted(stats, key=lambda e: (-stats[e][0], -stats[e][1], e))[:limit][::-1]
+
+
+def test_tail_seeding_ranks_like_brute_force_and_uses_free_slots_only(device):
+    experts, slots = 40, 30
+    _, pool = make_pool(1, experts, 30)
+    rng = np.random.default_rng(31)
+    for trial in range(12):
+        cache = SlotCache(slots, H, I, 1, experts, pool, device)
+        buf = cache.layer_buffer()
+        cache.read_layer(0, buf)
+        cache.wait_layer(0)
+        pre = sorted(set(int(v) for v in rng.choice(experts, size=int(rng.integers(0, 20)), replace=False)))
+        if pre:
+            cache.acquire(0, pre)
+        T, k = int(rng.integers(1, 300)), int(rng.integers(1, 5))
+        routes = rng.integers(0, experts, size=(T, k)).astype(np.int32)
+        limit = int(rng.integers(0, experts + 3))
+        got, got_slots = cache.seed_tail(0, torch.from_numpy(routes).to(device), limit, buf)
+        ranked = [e for e in tail_ranking(routes, experts, limit) if e not in pre]
+        free = slots - len(pre)
+        want = ranked[-free:] if free and len(ranked) > free else (ranked if free else [])
+        assert got == want, trial
+        assert sorted(got_slots) == list(range(len(pre), len(pre) + len(got)))  # free slots, in order
+
+
+def test_partial_layer_reads_batch_consecutive_experts(device):
+    experts = 64
+    arrays, pool = make_pool(1, experts, 32)
+    cache = SlotCache(4, H, I, 1, experts, pool, device)
+    buf = cache.layer_buffer()
+    buf.fill_(0xAB)
+    ids = [0, 1, 2, 3, 7, 9, 10] + list(range(20, 60))       # runs: 4, 1, 2, 32, 8
+    before = cache.stats()
+    cache.read_layer(0, buf, ids)
+    cache.wait_layer(0)
+    after = cache.stats()
+    assert after["copies"] - before["copies"] == 5
+    assert after["bytes"] - before["bytes"] == len(ids) * cache.blob
+    host = buf.cpu().numpy().reshape(experts, cache.blob)
+    for e in range(experts):
+        if e in ids:
+            assert np.array_equal(host[e], blob_of(arrays[0], e)), e
+        else:
+            assert (host[e] == 0xAB).all(), e
+    with pytest.raises(SlotCacheError, match="sorted"):
+        cache.read_layer(0, buf, [3, 2])
+
+
+def test_acquire_files_keeps_every_layer_resident(device):
+    files, experts, slots = 4, 16, 12
+    arrays, pool = make_pool(files, experts, 33)
+    cache = SlotCache(slots, H, I, files, experts, pool, device)
+    rng = np.random.default_rng(34)
+    for step in range(20):
+        req = {f: sorted(int(v) for v in rng.choice(experts, 3, replace=False)) for f in range(files)}
+        got = cache.acquire_files(req)
+        torch.cuda.current_stream(device).synchronize()
+        mem = cache.slot_memory.view(slots, cache.blob).cpu().numpy()
+        m = cache.map.cpu().numpy()
+        for f, ids in req.items():
+            for e, s in zip(ids, got[f]):
+                assert m[f, e] == s and np.array_equal(mem[s], blob_of(arrays[f], e)), (step, f, e)
+    with pytest.raises(SlotCacheError, match="too small"):
+        cache.acquire_files({f: list(range(4)) for f in range(files)})   # 16 experts, 12 slots
 
 
 @pytest.mark.parametrize("kind,limit", [("qwen", 0.0), ("deepseek", 1.5)])

@@ -70,7 +70,7 @@ def test_group_limited_matches_brute_force_over_group_subsets():
         logits = rng.standard_normal((1, E)).astype(np.float32)
         bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
         idx, _ = M.route_scored(logits, bias, K, "sigmoid", n_groups=G, topk_groups=TG)
-        s = (1 / (1 + np.exp(-logits[0].astype(np.float64))) + bias).astype(np.float32)
+        s = (M.score_f32(logits[0], "sigmoid") + bias).astype(np.float32)
         gscore = [np.float32(sum(sorted(s[g * 4:(g + 1) * 4])[-2:])) for g in range(G)]
         best = sorted(range(G), key=lambda g: (-gscore[g], g))[:TG]
         allowed = [e for e in range(E) if e // 4 in best]
@@ -274,3 +274,64 @@ def test_norm_router_oracle_against_closed_forms():
     np.testing.assert_array_equal(x_unit, M.rms_norm(v2))
     _, x_two, _, _ = M.norm_router(r2, y2, np.zeros((1, 64), np.float32), norm_weight=np.full(64, 2.0, np.float32))
     np.testing.assert_array_equal(x_two, 2 * x_unit)
+
+
+# ----------------------------------------------------------------------------- router score arithmetic
+
+def _ulps(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return np.abs(got - want) / np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+
+
+def test_exp_f32_is_exp_to_about_one_ulp():
+    # the stated fp32 exp against float64 exp over its whole normal range; a dropped
+    # polynomial term, a wrong ln2 split or a wrong rounding of n breaks the bound
+    x = np.linspace(-86.9, 88.7, 300001).astype(np.float32)   # below: flushed to 0 by definition
+    assert _ulps(M.exp_f32(x), np.exp(x.astype(np.float64))).max() <= 1.5
+    assert M.exp_f32(np.float32(0.0)) == 1.0
+    assert M.exp_f32(np.float32(np.log(2.0))) == 2.0
+    assert M.exp_f32(np.float32(-88.0)) == 0.0 and M.exp_f32(np.float32(89.0)) == np.inf
+    assert np.isnan(M.exp_f32(np.float32(np.nan))) and M.exp_f32(np.float32(-np.inf)) == 0.0
+
+
+def test_log1p_and_scores_are_the_functions_to_a_few_ulp():
+    u = np.linspace(0.0, 1.0, 100001).astype(np.float32)[1:]
+    assert _ulps(M.log1p_f32(u), np.log1p(u.astype(np.float64))).max() <= 4
+    assert M.log1p_f32(np.float32(0.0)) == 0.0
+    assert _ulps(M.log1p_f32(np.float32(1.0)), np.log(2.0)) <= 1
+    z = np.linspace(-100.0, 100.0, 200001).astype(np.float32)
+    zd = z.astype(np.float64)
+    sig = 1.0 / (1.0 + np.exp(-zd))
+    keep = sig > 1e-37
+    assert _ulps(M.score_f32(z, "sigmoid")[keep], sig[keep]).max() <= 2.5
+    ssp = np.sqrt(np.logaddexp(zd, 0.0))
+    assert _ulps(M.score_f32(z, "sqrtsoftplus"), ssp).max() <= 2.5
+    assert M.score_f32(np.float32(0.0), "sigmoid") == 0.5
+    assert _ulps(M.score_f32(np.float32(0.0), "sqrtsoftplus"), np.sqrt(np.log(2.0))) <= 1
+    # symmetric sigmoid, and the e^(l/2) branch joins the softplus branch at l = -64
+    np.testing.assert_allclose(M.score_f32(z, "sigmoid") + M.score_f32(-z, "sigmoid"), 1.0, atol=1.2e-7)
+    edge = np.float32([-64.0001, -63.9999])
+    np.testing.assert_allclose(M.score_f32(edge, "sqrtsoftplus"), np.sqrt(np.logaddexp(edge.astype(np.float64), 0)),
+                               rtol=3e-7)
+
+
+def test_softmax_sums_follow_the_wave_tree():
+    rng = np.random.default_rng(5)
+    for E in (1, 7, 64, 200, 512, 1000):
+        e = rng.random((9, E)).astype(np.float32)
+        got = M.softmax_sums_f32(e)
+        np.testing.assert_allclose(got, e.astype(np.float64).sum(-1), rtol=1e-6)
+        # the tree itself: lane j sums e[j], e[64 + j], ... then the lanes combine pairwise
+        lanes = np.zeros((9, 64), np.float32)
+        for j in range(64):
+            for col in range(j, E, 64):
+                lanes[:, j] = lanes[:, j] + e[:, col]
+        v = lanes
+        for step in (1, 2):
+            v = v + v[:, np.arange(64) ^ step]
+        v = v + v[:, [(j & ~7) | (7 - (j & 7)) for j in range(64)]]
+        v = v + v[:, [(j & ~15) | (15 - (j & 15)) for j in range(64)]]
+        np.testing.assert_array_equal(got, (v[:, 0] + v[:, 16]) + (v[:, 32] + v[:, 48]))
+    s = M.score_f32(rng.standard_normal((4, 300)).astype(np.float32), "softmax")
+    np.testing.assert_allclose(s.astype(np.float64).sum(-1), 1.0, rtol=1e-6)

@@ -62,6 +62,9 @@ _SIGNATURES = {
                              _P, _P, c_size_t, _P]),
     "wm_experts_mxfp4": (c_int, [_P, c_int32, _P, c_int32, POINTER(MXFP4ExpertsC), _P, _P, c_size_t, _P]),
     "wm_repack_prefill_mxfp4": (c_int, [POINTER(MXFP4ExpertsC), _P, _P, _P, _P, _P]),
+    "wm_combine_pairs": (c_int, [_P, _P, c_int32, c_int32, c_int32, _P, _P, _P]),
+    "wm_mlp_bf16_workspace_size": (c_size_t, [c_int32, c_int32, c_int32]),
+    "wm_mlp_bf16": (c_int, [_P, c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]),
     "wm_repack_prefill_fp8": (c_int, [POINTER(FP8ExpertsC), _P, _P, _P, _P, _P]),
     "wm_residual_rmsnorm": (c_int, [_P, _P, c_int32, c_int32, c_float, _P, _P]),
     "wm_norm_router": (c_int, [_P, _P, _P, c_int32, c_int32, c_float, _P, c_int32, _P, _P, c_size_t, _P, _P, _P, _P,
@@ -70,7 +73,7 @@ _SIGNATURES = {
     "wm_repack_router": (c_int, [_P, _P, c_int32, c_int32, _P, _P]),
     "wm_moe_stack_mxfp4_workspace_size": (c_size_t, [c_int32, c_int32, POINTER(MXFP4ExpertsC)]),
     "wm_moe_stack_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, POINTER(MXFP4ExpertsC),
-                                   POINTER(MXFP4ExpertsC), _P, _P, c_float, _P, _P, c_size_t, _P]),
+                                   POINTER(MXFP4ExpertsC), _P, _P, c_float, _P, _P, c_size_t, _P, _P, _P]),
     "wm_repack_down_slices": (c_int, [_P, _P, c_int64, c_int64, c_int32, c_int32, c_int32, _P, _P, _P]),
     "wm_decode_state_size": (c_size_t, [c_int32, c_int32]),
     "wm_decode_status_offset": (c_size_t, [c_int32, c_int32]),
@@ -81,6 +84,18 @@ _SIGNATURES = {
     "wm_slot_cache_plan": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
     "wm_slot_cache_acquire": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
     "wm_slot_cache_stats": (c_int, [_P, _P]),
+    "wm_slot_cache_acquire_ready": (c_int, [_P, c_int32, _P, c_int32, _P, _P, _P]),
+    "wm_slot_cache_acquire_files": (c_int, [_P, c_int32, _P, _P, _P, _P, _P]),
+    "wm_slot_cache_read_experts": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
+    "wm_slot_cache_seed_tail": (c_int, [_P, c_int32, _P, c_int64, c_int32, c_int32, _P, _P, _P, _P, _P]),
+    "wm_slot_cache_route_policy": (c_int, [_P, c_int32]),
+    "wm_slot_cache_route_observe": (c_int, [_P, c_int32, _P, c_int64, c_int32]),
+    "wm_slot_cache_route_phase": (c_int, [_P, c_int32]),
+    "wm_slot_cache_route_begin_request": (c_int, [_P]),
+    "wm_slot_cache_route_record_read": (c_int, [_P, c_int32, ctypes.c_double]),
+    "wm_slot_cache_route_rebalance": (c_int, [_P]),
+    "wm_slot_cache_route_state": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "wm_slot_cache_wait_fills": (c_int, [_P, _P]),
     "wm_slot_cache_set_route": (c_int, [_P, _P, _P]),
     "wm_slot_cache_read_layer": (c_int, [_P, c_int32, _P, _P]),
     "wm_slot_cache_wait_layer": (c_int, [_P, c_int32, _P]),
@@ -95,7 +110,7 @@ _SIGNATURES = {
     "wm_set_kernel_timing": (c_int, [c_int]),
     "wm_kernel_timing_ms": (c_int, [_P]),
     "wm_moe_decode_persistent_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, c_float,
-                                               _P, _P, c_size_t, _P]),
+                                               _P, _P, c_size_t, c_int32, _P, _P, _P]),
 }
 
 _lib = None
@@ -103,6 +118,15 @@ _lib = None
 
 class WhallmError(RuntimeError):
     """A libwhallm_moe call returned a nonzero status."""
+
+
+class Cancelled(WhallmError):
+    """A call stopped by its cancel hook (status 2, Native/QwenNative/capi.h:1-5); the
+    state it carried (a residual, a decode state) must be reset before reuse."""
+
+
+# The reference's cancel callback type (wq_cancel_fn, Native/QwenNative/capi.h:36-37).
+CANCEL_FN = ctypes.CFUNCTYPE(c_int, c_void_p)
 
 
 def load() -> ctypes.CDLL:
@@ -128,7 +152,8 @@ def call(name: str, *args) -> None:
     lib = load()
     status = getattr(lib, name)(*args)
     if status != 0:
-        raise WhallmError(f"{name}: {lib.wm_last_error().decode(errors='replace')}")
+        kind = Cancelled if status == 2 else WhallmError
+        raise kind(f"{name}: {lib.wm_last_error().decode(errors='replace')}")
 
 
 def exported_symbols() -> list[str]:

@@ -57,21 +57,23 @@ __device__ __forceinline__ float group_dot_bf16(uint4 w, float scale, const uint
   return acc;
 }
 
-// One pair of the decode list: its token row and expert (or the shared expert).
+// One pair of the decode list: its token row and expert (or the shared expert); false
+// for an id outside the table or an expert that is not resident (slot map entry < 0).
 __device__ __forceinline__ bool decode_pair(int p, int tokens, int k, const int32_t* __restrict__ indices,
                                             const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared_opt,
                                             const wm_mxfp4_experts& shared, int& t, ExpertRegions& r) {
+  bool resident;
   if (p < tokens * k) {
     t = p / k;
     int e = indices[p];
     if (e < 0 || e >= routed.experts) return false;
-    r = expert_regions(routed, e);
-    return true;
+    r = expert_regions(routed, e, resident);
+    return resident;
   }
   t = p - tokens * k;
   if (!shared_opt) return false;
-  r = expert_regions(shared, 0);
-  return true;
+  r = expert_regions(shared, 0, resident);
+  return resident;
 }
 
 // grid: (ceil(I / (4 * RPW)), pairs). act[p, i] fp32.
@@ -91,7 +93,7 @@ __global__ void __launch_bounds__(256) gate_up_act_kernel(const uint16_t* __rest
   int t;
   ExpertRegions r;
   if (!decode_pair(p, tokens, k, indices, routed, has_shared ? &shared : nullptr, shared, t, r)) {
-    // Unknown expert id: its act row is zero (the index check of the host layer reports it).
+    // Unknown or non-resident expert: its act row is zero and the down kernels skip the pair.
     for (int i = blockIdx.x * 4 * RPW + threadIdx.x; i < min(I, (int)(blockIdx.x + 1) * 4 * RPW); i += 256)
       act[(int64_t)p * I + i] = 0.0f;
     return;
@@ -205,27 +207,31 @@ __global__ void __launch_bounds__(256) down_kernel(const float* __restrict__ act
     int p;          // act row
     float w;        // weight of this expert's output
     ExpertRegions r;
+    bool resident;
     if (COMBINE) {
       if (entry < k) {
         p = t * k + entry;
         int e = indices[p];
         if (e < 0 || e >= routed.experts) continue;
-        r = expert_regions(routed, e);
+        r = expert_regions(routed, e, resident);
         w = weights[p];
       } else {
         p = tokens * k + t;
-        r = expert_regions(shared, 0);
+        r = expert_regions(shared, 0, resident);
         w = gate_value;
       }
+      if (!resident) continue;  // a non-resident expert contributes nothing
     } else {
       p = t;
       if (p < tokens * k) {
         int e = indices[p];
-        if (e < 0 || e >= routed.experts) break;  // zero row
-        r = expert_regions(routed, e);
+        if (e < 0) return;  // a masked pair: its output row is left as it is (uniform per block)
+        if (e >= routed.experts) break;  // zero row
+        r = expert_regions(routed, e, resident);
       } else {
-        r = expert_regions(shared, 0);
+        r = expert_regions(shared, 0, resident);
       }
+      if (!resident) break;  // zero row
       w = 1.0f;
     }
     // act values of this lane's groups: 32 floats per group.

@@ -50,6 +50,9 @@ constexpr int DS_NE_MAX = 12;         // routed + shared experts per layer
 constexpr int DS_KB = DS_H / 128;     // K-steps of a phase-A tile (128 per MFMA)
 constexpr int DS_KB_B = DS_NE_MAX / 2;  // K-steps of phase B (two 64-wide expert slices each)
 constexpr uint32_t DS_SPIN_LIMIT = 1u << 20;
+// Status word values (0 = healthy): a message wait ran out, the caller's cancel word was
+// set, a selected expert is not resident (its slot map entry is negative).
+constexpr uint32_t DS_STALLED = 1, DS_CANCELLED = 2, DS_NOT_RESIDENT = 3;
 constexpr int DS_MAX_LAYERS = 128;    // layer descriptors kept in LDS
 constexpr int DS_CW = 3;                      // compute waves (prefetch weights and compute)
 constexpr int DS_THREADS = (DS_CW + 1) * 64;  // + one message wave (polls and publishes)
@@ -114,7 +117,7 @@ __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int s
     for (int m = 0; m < N; ++m) ready &= tag(v[m]) == want;
     if (ready) break;
     if (++spins > DS_SPIN_LIMIT) {
-      __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(status, DS_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ok = false;
       break;
     }
@@ -187,6 +190,8 @@ struct DSCtx {
   uint32_t base;
   uint64_t *route_ll, *act_ll, *part_ll, *r_ll;
   uint32_t* status;
+  const int32_t* cancel;  // nullable: a word the host sets to stop the launch
+  float* trace;           // nullable: [L][H] fp32 residual after each layer
 };
 
 // Workgroup barrier over LDS only: this wave's LDS operations complete (lgkmcnt 0),
@@ -241,7 +246,7 @@ __device__ __forceinline__ void ds_build_x(DSShared& sh, int tid) {
 //                     message wave: publish the row block's partial, gather the 8
 //                     XCDs' partials, r += bf16(sum), publish r, gather the XCD's r
 // Compute waves never wait on a message. One wave per SIMD.
-template <bool LOCAL>
+template <bool LOCAL, bool DOWN_ROWS>
 __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
   const int lane = c.lane, wave = c.wave, x = c.x, j = c.j, K = c.K, NE = c.NE;
   const int tiles = 8 * NE;                     // phase-A tiles of the XCD
@@ -289,9 +294,13 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
   // Phase-B K-steps 2 wave + i (i = 0, 1): experts 2 kb and 2 kb + 1 of the slice.
   // Lane (row r, group a) reads half a % 2 of expert 2 kb + a / 2's row-slice for each
   // of the four 16-row tiles; missing experts re-read the step's first expert.
+  // Slice-major down (DOWN_ROWS false): row o's slice x is 32 bytes at (x H + o) 32 and its
+  // two scale bytes at (x H + o) 2, so a dword holds rows o and o ^ 1. The reference row
+  // layout (DOWN_ROWS true, e.g. blobs of the slot cache): the slice is 32 bytes at
+  // o I/2 + 32 x and its scale bytes at o I/32 + 2 x, so a dword holds slices x and x ^ 1.
   uint4 bw[2][4];
   uint32_t bs[2][4];
-  const int bshift = 8 * (2 * (col & 1) + (grp & 1));  // byte of the scale word
+  const int bshift = 8 * (2 * (DOWN_ROWS ? (x & 1) : (col & 1)) + (grp & 1));  // byte of the scale word
   auto issue_b = [&](int l) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -302,9 +311,15 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
       expert_base(l, e, gu, gus, dn, dns);
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
-        const size_t row = (size_t)x * DS_H + j * DS_ROWS + 16 * rt + col;
-        bw[i][rt] = gload16(dn + row * (DS_SLICE / 2) + 16 * (grp & 1));
-        bs[i][rt] = gload<uint32_t>(dns + ((row * (DS_SLICE / 32)) & ~(size_t)3));
+        const size_t o = (size_t)j * DS_ROWS + 16 * rt + col;
+        if constexpr (DOWN_ROWS) {
+          bw[i][rt] = gload16(dn + o * (DS_I / 2) + x * (DS_SLICE / 2) + 16 * (grp & 1));
+          bs[i][rt] = gload<uint32_t>(dns + o * (DS_I / 32) + ((x * (DS_SLICE / 32)) & ~3));
+        } else {
+          const size_t row = (size_t)x * DS_H + o;
+          bw[i][rt] = gload16(dn + row * (DS_SLICE / 2) + 16 * (grp & 1));
+          bs[i][rt] = gload<uint32_t>(dns + ((row * (DS_SLICE / 32)) & ~(size_t)3));
+        }
       }
     }
   };
@@ -456,6 +471,10 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     uint64_t* act_buf = c.act_ll + ((size_t)par * DS_X + x) * DS_NE_MAX * DS_SLICE;
     uint64_t* part_buf = c.part_ll + (size_t)par * DS_X * DS_H;
     uint64_t* r_buf = c.r_ll + ((size_t)par * DS_X + x) * DS_J * DS_RW;
+    // the cancel word is read at the top of the layer and looked at once the act gather
+    // below has waited (loads complete in order), so the read adds no wait of its own
+    int32_t cancel_word = 0;
+    if (c.cancel && lane == 0) cancel_word = __hip_atomic_load(c.cancel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const uint8_t* sg = (const uint8_t*)sh.desc[l].shared_gate;
     uint4 gw[4] = {};
     if (sg) {
@@ -494,6 +513,11 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     ll_gather<DS_NE_MAX * DS_SLICE / 64>(act_buf, lane, 64, c.NE * DS_SLICE, e_act, c.status, ok,
                                          [&](int w, uint64_t v) { sh.act[w / DS_SLICE][w % DS_SLICE] = __uint_as_float((uint32_t)v); });
     WM_DS_TRACE(l, 9);
+    if (__builtin_amdgcn_readfirstlane(cancel_word) != 0) {
+      // leave after this layer's phase B; the others see the status word in their next wait
+      if (lane == 0) __hip_atomic_store(c.status, DS_CANCELLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = false;
+    }
     if (!ok) sh.failures = 1;
     ds_barrier();  // S1
     WM_DS_TRACE(l, 10);
@@ -511,6 +535,7 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
                     [&](int i, uint64_t v) { y += __uint_as_float((uint32_t)v); });
     WM_DS_TRACE(l, 12);
     r_own += bf16_bits_to_f32(f32_to_bf16_bits(y));
+    if (c.trace && x == 0) c.trace[(size_t)l * DS_H + j * DS_ROWS + lane] = r_own;
     // publish the row block as bf16 triples under a 16-bit epoch (the hidden state that
     // feeds the next rmsnorm is bf16, as in the reference's bf16 residual stream; the
     // owner keeps accumulating r in fp32)
@@ -540,10 +565,11 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
   }
 }
 
-template <int PER_LANE, bool LOCAL>
+template <int PER_LANE, bool LOCAL, bool DOWN_ROWS>
 __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
     const float* __restrict__ logits, int L, int E, int K, int norm_topk, const wm_decode_layer* layers,
-    float* __restrict__ residual, float eps, uint16_t* __restrict__ x_out, uint8_t* state) {
+    float* __restrict__ residual, float eps, uint16_t* __restrict__ x_out, uint8_t* state,
+    const int32_t* cancel, float* trace) {
   __shared__ DSShared sh;
   const int b = blockIdx.x, tid = threadIdx.x;
   const DSLayout lay = ds_layout(L);
@@ -560,6 +586,8 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   c.part_ll = (uint64_t*)(state + lay.part);
   c.r_ll = (uint64_t*)(state + lay.r);
   c.status = (uint32_t*)(state + lay.status);
+  c.cancel = cancel;
+  c.trace = trace;
   uint32_t* wg_epoch = (uint32_t*)(state + lay.epoch);
   c.base = wg_epoch[b];
   const uint32_t e_route = c.base + 1;
@@ -567,7 +595,10 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   bool ok = true;
   if (tid == 0) sh.failures = 0;
   if (tid == 0) sh.eps = eps;
-  ds_barrier();  // failures is cleared before any wave can raise it
+  __syncthreads();  // failures is cleared before any wave can raise it; every wave holds its epoch
+  // Every launch advances the epochs by the same amount, whether it completes or not, so
+  // words left by a launch that ended early never match a later launch's epochs.
+  if (tid == 0) wg_epoch[b] = c.base + 3 * (uint32_t)L + 5;
 
   // ---- prologue: routes of layers b, b + 256, ... (message wave), descriptors, r_0
   if (msg) {
@@ -597,11 +628,22 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   if (!ok) sh.failures = 1;
   ds_barrier();
   if (sh.failures != 0) return;
-  // Expert ids -> slots once, so the prefetch loops read only LDS.
+  // Expert ids -> slots once, so the prefetch loops read only LDS. A negative map entry
+  // (an expert that is not resident) ends the launch before any layer runs: every
+  // workgroup reads the same map and leaves here, the status word tells the caller.
   for (int i = tid; i < L * 16; i += DS_THREADS) {
     int l = i / 16, k = i % 16;
     const int32_t* slots = sh.desc[l].slots;
-    if (k < K && slots) sh.slot[l][k] = max(0, gload<int32_t>(slots + sh.slot[l][k]));  // -1: not resident
+    if (k < K && slots) {
+      const int32_t v = gload<int32_t>(slots + sh.slot[l][k]);
+      if (v < 0) sh.failures = 1;
+      sh.slot[l][k] = max(0, v);
+    }
+  }
+  ds_barrier();
+  if (sh.failures != 0) {
+    if (tid == 0) __hip_atomic_store(c.status, DS_NOT_RESIDENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
   }
   if (msg) {  // rmsnorm statistics of r_0
     float ss = 0.0f, mx = 0.0f;
@@ -614,7 +656,7 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   ds_barrier();
 
   if (msg) ds_message_role<LOCAL>(sh, c, r_own);
-  else ds_compute_role<LOCAL>(sh, c);
+  else ds_compute_role<LOCAL, DOWN_ROWS>(sh, c);
   if (sh.failures != 0) return;
 
   // ---- outputs (XCD 0's message waves): r_L and rmsnorm(r_L); sh.inv is r_L's
@@ -622,7 +664,6 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
     residual[c.j * DS_ROWS + c.lane] = r_own;
     if (x_out) x_out[c.j * DS_ROWS + c.lane] = f32_to_bf16_bits(r_own * sh.inv);
   }
-  if (tid == 0) wg_epoch[b] = c.base + 3 * (uint32_t)L + 5;
 }
 
 // Repack of down regions into the slice-major layout: one thread per (expert, slice, row).
@@ -657,7 +698,10 @@ __global__ void __launch_bounds__(64) xcc_map_kernel(uint32_t* out) {
 
 // Whether block b of a DS_WGS-block launch runs on XCC b % DS_X on the current
 // device, checked once per device with a probe launch on `s`. Only then are the
-// messages that stay within one XCD written with XCD-local stores.
+// messages that stay within one XCD written with XCD-local stores. The probe
+// allocates and synchronises, so it is not run while `s` is being captured into a
+// graph: such a launch uses device-scope stores (call wm_decode_xcd_local before
+// capturing to decide once).
 static bool xcd_local_ok(hipStream_t s) {
   static std::mutex mu;
   static int known[64];  // 0 unknown, 1 yes, 2 no
@@ -665,6 +709,8 @@ static bool xcd_local_ok(hipStream_t s) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
   std::lock_guard<std::mutex> lock(mu);
   if (known[dev] == 0) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) return false;
     bool ok = false;
     uint32_t* d = nullptr;
     if (hipMalloc(&d, DS_WGS * sizeof(uint32_t)) == hipSuccess) {
@@ -725,6 +771,7 @@ WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts) {
 WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers, int32_t experts, int32_t k,
                                              int32_t hidden, int32_t inter, const wm_decode_layer* layers_dev,
                                              float* residual, float eps, void* x_out, void* state, size_t state_bytes,
+                                             int32_t down_row_layout, const int32_t* cancel, float* residual_trace,
                                              void* stream) {
   return guarded([&] {
     if (hidden != DS_H || inter != DS_I)
@@ -738,13 +785,16 @@ WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers
     hipStream_t s = as_stream(stream);
     const int per_lane = (experts + 63) / 64;
     const bool local = xcd_local_ok(s);
-#define WM_DP(P, LOC) hipLaunchKernelGGL((decode_persistent_kernel<P, LOC>), dim3(DS_WGS), dim3(DS_THREADS), 0, s, logits, \
-                                         layers, experts, k, 1, layers_dev, residual, eps, (uint16_t*)x_out, (uint8_t*)state)
+#define WM_DP(P, LOC, ROWS) hipLaunchKernelGGL((decode_persistent_kernel<P, LOC, ROWS>), dim3(DS_WGS), dim3(DS_THREADS), 0, \
+                                               s, logits, layers, experts, k, 1, layers_dev, residual, eps, \
+                                               (uint16_t*)x_out, (uint8_t*)state, cancel, residual_trace)
+#define WM_DP_ROWS(P, LOC) if (down_row_layout) WM_DP(P, LOC, true); else WM_DP(P, LOC, false)
     if (per_lane <= 8) {
-      if (local) WM_DP(8, true); else WM_DP(8, false);
+      if (local) { WM_DP_ROWS(8, true); } else { WM_DP_ROWS(8, false); }
     } else {
-      if (local) WM_DP(16, true); else WM_DP(16, false);
+      if (local) { WM_DP_ROWS(16, true); } else { WM_DP_ROWS(16, false); }
     }
+#undef WM_DP_ROWS
 #undef WM_DP
     check_launch("decode_persistent");
   });

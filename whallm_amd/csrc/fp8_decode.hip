@@ -52,22 +52,24 @@ __device__ __forceinline__ float e4m3x16_dot_f32(uint4 w, const float* a, float 
   return acc;
 }
 
-// The pair's token and expert (or the shared expert); false for an unknown expert id.
+// The pair's token and expert (or the shared expert); false for an unknown expert id or
+// an expert that is not resident (slot map entry < 0).
 __device__ __forceinline__ bool fp8_pair(int p, int tokens, int k, const int32_t* __restrict__ indices,
                                          const wm_fp8_experts& routed, bool has_shared, const wm_fp8_experts& shared,
                                          int& t, Fp8Regions& r, bool& is_shared) {
+  bool resident;
   is_shared = p >= tokens * k;
   if (!is_shared) {
     t = p / k;
     const int e = indices[p];
     if (e < 0 || e >= routed.experts) return false;
-    r = fp8_regions(routed, e);
-    return true;
+    r = fp8_regions(routed, e, resident);
+    return resident;
   }
   t = p - tokens * k;
   if (!has_shared) return false;
-  r = fp8_regions(shared, 0);
-  return true;
+  r = fp8_regions(shared, 0, resident);
+  return resident;
 }
 
 constexpr int FP8_RPW = 2;  // intermediate rows per wave (4 weight rows: gate and up of each)
@@ -87,7 +89,7 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
   Fp8Regions r;
   bool is_shared;
   if (!fp8_pair(p, tokens, k, indices, routed, has_shared != 0, shared, t, r, is_shared)) {
-    // unknown expert id: its act rows are zero (the host layer's index check reports it)
+    // unknown or non-resident expert: its act rows are zero and the down kernels skip the pair
     for (int i = blockIdx.x * 4 * FP8_RPW + threadIdx.x; i < (int)(blockIdx.x + 1) * 4 * FP8_RPW; i += 256)
       act[(int64_t)p * I + i] = 0.0f;
     return;
@@ -188,23 +190,27 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
     int p;
     float w;
     Fp8Regions r;
+    bool resident;
     if (COMBINE) {
       if (entry < k) {
         p = t * k + entry;
         const int e = indices[p];
         if (e < 0 || e >= routed.experts) continue;
-        r = fp8_regions(routed, e);
+        r = fp8_regions(routed, e, resident);
         w = weights[p];
       } else {
         p = tokens * k + t;
-        r = fp8_regions(shared, 0);
+        r = fp8_regions(shared, 0, resident);
         w = gate_value;
       }
+      if (!resident) continue;  // a non-resident expert contributes nothing
     } else {
       p = t;
       const int e = indices[p];
-      if (e < 0 || e >= routed.experts) break;  // zero row
-      r = fp8_regions(routed, e);
+      if (e < 0) return;  // a masked pair: its output row is left as it is (uniform per block)
+      if (e >= routed.experts) break;  // zero row
+      r = fp8_regions(routed, e, resident);
+      if (!resident) break;  // zero row
       w = 1.0f;
     }
     float av[CPL][16];

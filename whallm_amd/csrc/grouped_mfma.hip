@@ -1017,25 +1017,41 @@ __global__ void __launch_bounds__(64) shared_gate_kernel(const uint16_t* __restr
   if (lane == 0) gate[t] = v;
 }
 
+// Whether pair p's expert is resident: its slot map entry (when the table has one) is
+// not negative. The GEMMs read slot 0 for a non-resident expert; its rows are dropped here.
+__device__ __forceinline__ bool pair_resident(const int32_t* __restrict__ indices, const int32_t* __restrict__ slots,
+                                              int p) {
+  return !slots || slots[indices[p]] >= 0;
+}
+
 // combine: y[t, c] = sum_k w[t, k] rows[inverse[t*K + k], c] (+ gate[t] rows[P + t, c]), fp32
-// sum in k order, bf16 out (the expert rows are unweighted).
-// per-pair (combine = 0): out[p, c] = rows[inverse[p], c]. 8 columns per thread.
+// sum in k order, bf16 out (the expert rows are unweighted). Pairs with an unknown or
+// non-resident expert contribute nothing; so does a non-resident shared expert.
+// per-pair (combine = 0): out[p, c] = rows[inverse[p], c], a zero row for an unknown or
+// non-resident expert, and no write at all for a masked pair (negative index).
+// 8 columns per thread.
 __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __restrict__ rows,
                                                            const int32_t* __restrict__ inverse,
                                                            const float* __restrict__ weights,
                                                            const float* __restrict__ gate, int tokens, int k,
                                                            int hidden, int has_shared, int combine,
+                                                           const int32_t* __restrict__ indices,
+                                                           const int32_t* __restrict__ slots,
+                                                           const int32_t* __restrict__ shared_slots,
                                                            uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
   const int c8 = blockIdx.y * blockDim.x + threadIdx.x;
   if (c8 * 8 >= hidden) return;
   const int pairs = tokens * k;
   if (!combine) {
+    if (indices[t] < 0) return;
     const int row = inverse[t];
-    const uint4 v = row >= 0 ? reinterpret_cast<const uint4*>(rows + (int64_t)row * hidden)[c8] : make_uint4(0, 0, 0, 0);
+    const bool live = row >= 0 && pair_resident(indices, slots, t);
+    const uint4 v = live ? reinterpret_cast<const uint4*>(rows + (int64_t)row * hidden)[c8] : make_uint4(0, 0, 0, 0);
     reinterpret_cast<uint4*>(out + (int64_t)t * hidden)[c8] = v;
     return;
   }
+  const bool shared_live = has_shared && (!shared_slots || shared_slots[0] >= 0);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   auto add = [&](const uint4 v, float s) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -1055,7 +1071,8 @@ __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __res
 #pragma unroll
     for (int q = 0; q < BATCH; ++q) {
       const int j = j0 + q;
-      row[q] = j < k ? inverse[t * k + j] : (j < n ? pairs + t : -1);
+      row[q] = j < k ? inverse[t * k + j] : (j < n && shared_live ? pairs + t : -1);
+      if (j < k && row[q] >= 0 && !pair_resident(indices, slots, t * k + j)) row[q] = -1;
     }
 #pragma unroll
     for (int q = 0; q < BATCH; ++q)
@@ -1223,12 +1240,14 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
                      s, a6, L, routed, sh, out_rows);
   check_launch("down");
   if (te) check_hip(hipEventRecord(te->ev[2], s), "hipEventRecord");
+  const int32_t* shared_slots = has_shared ? shared->slots : nullptr;
   if (combine)
     hipLaunchKernelGGL(combine_rows_kernel, dim3(tokens, (H / 8 + 255) / 256), dim3(256), 0, s, out_rows, inverse,
-                       weights, L.shared_gate, tokens, k, H, has_shared ? 1 : 0, 1, y);
+                       weights, L.shared_gate, tokens, k, H, has_shared ? 1 : 0, 1, indices, routed.slots,
+                       shared_slots, y);
   else
     hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)pairs, (H / 8 + 255) / 256), dim3(256), 0, s, out_rows,
-                       inverse, weights, L.shared_gate, tokens, k, H, 0, 0, y);
+                       inverse, weights, L.shared_gate, tokens, k, H, 0, 0, indices, routed.slots, nullptr, y);
   check_launch("combine_rows");
 }
 

@@ -13,9 +13,13 @@ struct ExpertRegions {
   const uint8_t* down_scales;
 };
 
-__device__ __forceinline__ ExpertRegions expert_regions(const wm_mxfp4_experts& t, int e) {
+// Regions of expert e. A slot map entry below 0 means the expert is not resident: the
+// regions then point at slot 0 (so no access leaves the pool) and `resident` is false;
+// every kernel makes such a pair contribute nothing.
+__device__ __forceinline__ ExpertRegions expert_regions(const wm_mxfp4_experts& t, int e, bool& resident) {
   int64_t slot = t.slots ? t.slots[e] : e;
-  if (slot < 0) slot = 0;  // an expert that is not resident (map entry -1): never address outside the pool
+  resident = slot >= 0;
+  if (slot < 0) slot = 0;
   ExpertRegions r;
   r.gate_up = (const uint8_t*)t.gate_up + slot * t.gate_up_stride;
   r.gate_up_scales = (const uint8_t*)t.gate_up_scales + slot * t.gate_up_scales_stride;
@@ -32,9 +36,10 @@ struct Fp8Regions {
   const float* w2_scales;
 };
 
-__device__ __forceinline__ Fp8Regions fp8_regions(const wm_fp8_experts& t, int e) {
+__device__ __forceinline__ Fp8Regions fp8_regions(const wm_fp8_experts& t, int e, bool& resident) {
   int64_t slot = t.slots ? t.slots[e] : e;
-  if (slot < 0) slot = 0;  // not resident: never address outside the pool
+  resident = slot >= 0;
+  if (slot < 0) slot = 0;  // not resident: slot 0's address, and the pair contributes nothing
   Fp8Regions r;
   r.w13 = (const uint8_t*)t.w13 + slot * t.w13_stride;
   r.w13_scales = (const float*)((const uint8_t*)t.w13_scales + slot * t.w13_scales_stride);

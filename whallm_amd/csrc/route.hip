@@ -37,10 +37,10 @@ __global__ void __launch_bounds__(64) route_softmax_topk_kernel(const float* __r
   }
 }
 
+// Scores of the DeepSeek gate in the stated arithmetic of route_device.h: sigmoid, or
+// sqrt(softplus(l)) = sqrt(max(l, 0) + log1p(exp(-|l|))) (Native/DeepSeekNative/engine.mm:1875-1876).
 __device__ __forceinline__ float score_fn(float l, int func) {
-  if (func == 1) return 1.0f / (1.0f + __expf(-l));
-  // sqrt(softplus(l)) = sqrt(max(l, 0) + log1p(exp(-|l|))) (Native/DeepSeekNative/engine.mm:1875-1876)
-  return sqrtf(fmaxf(l, 0.0f) + log1pf(__expf(-fabsf(l))));
+  return func == 1 ? sigmoid_defined(l) : sqrt_softplus_defined(l);
 }
 
 template <int PER_LANE>
@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restric
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
-      if (e < experts) part += __expf(row[e] - top);
+      if (e < experts) part += exp_defined(row[e] - top);
     }
     denom = segment_sum<64>(part);
   }
@@ -78,7 +78,7 @@ __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restric
   for (int r = 0; r < PER_LANE; ++r) {
     int e = r * 64 + lane;
     if (e < experts) {
-      float s = func == 0 ? __expf(row[e] - top) / denom : score_fn(row[e], func);
+      float s = func == 0 ? exp_defined(row[e] - top) / denom : score_fn(row[e], func);
       float b = s + (bias ? bias[e] : 0.0f);
       score_lds[e] = s;
       biased_lds[e] = b;

@@ -13,6 +13,69 @@
 
 namespace wm {
 
+// ---- the router's score arithmetic, stated in fp32 operations --------------------------
+// Each operation is rounded to nearest even and none is fused (contraction off), so the
+// test oracle restates it op for op in numpy float32 (oracle/moe.py exp_f32, log1p_f32,
+// score_f32) and both select the same experts:
+//   exp:   n = rint(x log2e); r = (x - n ln2_hi) - n ln2_lo; p = degree-7 Taylor polynomial
+//          of e^r by Horner; e^x = p 2^n, 0 when n < -125, +inf when n > 128;
+//   log1p: u in [0, 1]: m = 1 + u, halved when above sqrt 2 (k = 1); s = (m - 1)/(m + 1);
+//          ln m = k ln2 + 2 s (1 + z/3 + ... + z^5/11), z = s^2; plus (u - (m - 1)) / m.
+// Division and square root are the correctly rounded IEEE operations.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2Hi = 0.693145751953125f;  // 0x3F317200: n * kLn2Hi is exact for |n| <= 256
+constexpr float kLn2Lo = (float)(0.6931471805599453 - 0.693145751953125);
+constexpr float kSqrt2 = 1.4142135623730951f;
+
+__device__ __forceinline__ float exp_defined(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  const float n = __builtin_rintf(x * kLog2e);
+  const float r = (x - n * kLn2Hi) - n * kLn2Lo;
+  float p = (float)(1.0 / 5040.0);
+  p = p * r + (float)(1.0 / 720.0);
+  p = p * r + (float)(1.0 / 120.0);
+  p = p * r + (float)(1.0 / 24.0);
+  p = p * r + (float)(1.0 / 6.0);
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  if (n > 128.0f) return __builtin_inff();
+  if (n < -125.0f) return 0.0f;
+  return __builtin_ldexpf(p, (int)n);
+}
+
+__device__ __forceinline__ float log1p_defined(float u) {
+#pragma clang fp contract(off)
+  const float m = 1.0f + u;
+  const bool k = m > kSqrt2;
+  const float m2 = k ? m * 0.5f : m;
+  const float s = (m2 - 1.0f) / (m2 + 1.0f);
+  const float z = s * s;
+  float p = (float)(1.0 / 11.0);
+  p = p * z + (float)(1.0 / 9.0);
+  p = p * z + (float)(1.0 / 7.0);
+  p = p * z + (float)(1.0 / 5.0);
+  p = p * z + (float)(1.0 / 3.0);
+  p = p * z + 1.0f;
+  const float lg = (s + s) * p;
+  const float corr = (u - (m - 1.0f)) / m;
+  const float kf = k ? 1.0f : 0.0f;
+  return kf * kLn2Hi + (kf * kLn2Lo + (lg + corr));
+}
+
+__device__ __forceinline__ float sigmoid_defined(float l) {
+#pragma clang fp contract(off)
+  return 1.0f / (1.0f + exp_defined(-l));
+}
+
+// sqrt(softplus(l)); below l = -64, where softplus(l) = e^l to fp32 precision, e^(l/2).
+__device__ __forceinline__ float sqrt_softplus_defined(float l) {
+#pragma clang fp contract(off)
+  if (l < -64.0f) return exp_defined(0.5f * l);
+  return __builtin_sqrtf(fmaxf(l, 0.0f) + log1p_defined(exp_defined(-fabsf(l))));
+}
+
 __device__ __forceinline__ bool topk_better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }

@@ -67,7 +67,8 @@ WM_EXPORT size_t wm_moe_stack_mxfp4_workspace_size(int32_t tokens, int32_t k, co
 WM_EXPORT int wm_moe_stack_mxfp4(const float* logits, int32_t layers, int32_t tokens, int32_t k,
                                  int32_t norm_topk_prob, const wm_mxfp4_experts* experts,
                                  const wm_mxfp4_experts* shared, const void* const* shared_gates, float* residual,
-                                 float eps, void* x_out, void* workspace, size_t workspace_bytes, void* stream) {
+                                 float eps, void* x_out, void* workspace, size_t workspace_bytes,
+                                 int (*cancel)(void*), void* cancel_context, void* stream) {
   return guarded([&] {
     if (layers < 1 || tokens < 0 || k < 1) fail("wm_moe_stack_mxfp4: bad shape");
     if (!experts || !residual || !logits) fail("wm_moe_stack_mxfp4: null pointer");
@@ -97,6 +98,10 @@ WM_EXPORT int wm_moe_stack_mxfp4(const float* logits, int32_t layers, int32_t to
     size_t rest = workspace_bytes - (size_t)(base - (uint8_t*)workspace);
     residual_rmsnorm(residual, nullptr, tokens, H, eps, x, s);
     for (int l = 0; l < layers; ++l) {
+      // polled before each layer is enqueued, as the reference engine polls between layers
+      // (Native/QwenNative/engine.h:112-113); earlier layers stay enqueued
+      if (cancel && cancel(cancel_context))
+        throw Cancelled("wm_moe_stack_mxfp4: cancelled before layer " + std::to_string(l));
       if (wm_route_softmax_topk(logits + (size_t)l * tokens * E, tokens, E, k, norm_topk_prob, idx, w, nullptr,
                                 stream) != 0)
         fail(wm_last_error());

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <stdexcept>
 #include <string>
 
 #include "../../include/whallm_moe.h"
@@ -19,14 +20,23 @@ namespace wm {
 void set_error(const std::string& message);
 void clear_error();
 
-// Runs `body`; a thrown std::exception becomes status 1 with its message
-// (Native/QwenNative/capi.mm:20-37 turns exceptions into a status the same way).
+// Thrown when a caller's cancel callback asks to stop; the entry point returns 2
+// (Native/QwenNative/capi.h:1-5: 0 ok, 1 error, 2 cancelled).
+struct Cancelled : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+// Runs `body`; a thrown std::exception becomes status 1 with its message, Cancelled
+// status 2 (Native/QwenNative/capi.mm:20-37 turns exceptions into a status the same way).
 template <typename Body>
 int guarded(Body body) {
   try {
     clear_error();
     body();
     return 0;
+  } catch (const Cancelled& e) {
+    set_error(e.what());
+    return 2;
   } catch (const std::exception& e) {
     set_error(e.what());
     return 1;

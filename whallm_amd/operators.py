@@ -12,9 +12,12 @@ with torch device tensors in place of mlx arrays. The cache is duck-typed as in 
 reference: ``current_batched(layer)`` (a whole-layer table: no host sync, the fused
 kernels index experts on the device), ``get_many(layer, ids)`` / ``iter_ready(layer, ids)``
 (individual resident experts: their regions are gathered into one table), plus the
-optional recording hooks. Routed experts always run on the library's kernels; a
-bf16 shared ``MLP`` and an activation other than (clamped) SwiGLU run as library GEMMs
-(hipBLASLt through torch) over weights that the library dequantizes.
+optional recording hooks. Routed experts, the bf16 shared ``MLP`` (with its sigmoid gate
+and the add) and the combines run on the library's kernels. Only an activation other than
+(clamped) SwiGLU takes a generic path: library GEMMs (hipBLASLt through torch) over
+weights the library dequantizes, one expert at a time with a host loop over the touched
+experts; it exists for the reference tests' arbitrary activations and is never on the
+SwiGLU hot path.
 """
 from __future__ import annotations
 
@@ -23,8 +26,8 @@ from dataclasses import dataclass, replace
 
 import torch
 
-from .ops import (FP8Experts, MXFP4Experts, dequant_fp8_blocks, dequant_mxfp4, experts_fp8, experts_mxfp4,
-                  linear_bf16, moe_fp8, moe_mxfp4, route_scored, route_softmax_topk)
+from .ops import (FP8Experts, MXFP4Experts, combine_pairs, dequant_fp8_blocks, dequant_mxfp4, experts_fp8,
+                  experts_mxfp4, linear_bf16, mlp_bf16, moe_fp8, moe_mxfp4, route_scored, route_softmax_topk)
 
 # Whole-layer prefill groups rows by expert from this many rows (qwen4_exp.py:789).
 GROUPED_PREFILL_ROWS = 64
@@ -242,15 +245,19 @@ class Linear:
 
 
 class MLP:
-    """The bf16 shared expert: down(silu(gate(x)) * up(x)) (qwen4_exp.py:763-771)."""
+    """The bf16 shared expert: down(silu(gate(x)) * up(x)) (qwen4_exp.py:763-771), on the
+    library's fused kernels (wm_mlp_bf16)."""
 
     def __init__(self, dimensions: int, intermediate: int, device="cuda"):
         self.gate_proj = Linear(dimensions, intermediate, device)
         self.up_proj = Linear(dimensions, intermediate, device)
         self.down_proj = Linear(intermediate, dimensions, device)
 
-    def __call__(self, value: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(torch.nn.functional.silu(self.gate_proj(value)) * self.up_proj(value))
+    def __call__(self, value: torch.Tensor, gate: torch.Tensor | None = None,
+                 add: torch.Tensor | None = None) -> torch.Tensor:
+        """down(silu(gate_proj(x)) * up_proj(x)), scaled by sigmoid(x . gate) and added to
+        ``add`` when those are given (the shared-expert term of SparseMoE, qwen4_exp.py:1045)."""
+        return mlp_bf16(value, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight, gate, add)
 
 
 class StreamingExperts:
@@ -337,10 +344,9 @@ class SparseMoE:
                 scores = scores / scores.sum(dim=-1, keepdim=True)
         if getattr(self.cache, "route_trace_enabled", False):
             self.cache.record_routes(self.layer, indices.to("cpu", torch.int32).numpy())
-        shared = None
-        if self.shared_expert is not None and not isinstance(self.shared_expert, MXFP4Experts):
-            gate = torch.sigmoid(self.shared_expert_gate(value).float())
-            shared = (gate * self.shared_expert(value).float()).to(torch.bfloat16)
+        # The shared term is added to the routed combine by the library (_layer); True marks a
+        # layer that has a bf16 shared MLP.
+        shared = self.shared_expert is not None and not isinstance(self.shared_expert, MXFP4Experts)
         return indices, scores, shared
 
     def _layer(self, value: torch.Tensor, indices, scores, shared) -> torch.Tensor:
@@ -349,7 +355,10 @@ class SparseMoE:
             return moe_mxfp4(value, idx, scores.contiguous(), table, self.shared_expert,
                              self.shared_expert_gate.weight.reshape(-1))
         y = moe_mxfp4(value, idx, scores.contiguous(), table)
-        return y if shared is None else (y.float() + shared.float()).to(torch.bfloat16)
+        if not shared:
+            return y
+        # y + sigmoid(x . g) * MLP(x) on the MLP kernels (wm_mlp_bf16)
+        return self.shared_expert(value, self.shared_expert_gate.weight.reshape(-1), y)
 
     def __call__(self, value: torch.Tensor, routes=None) -> torch.Tensor:
         indices, scores, shared = self._gates(value, routes)
@@ -363,14 +372,14 @@ class SparseMoE:
         joined = torch.cat(values, dim=axis)
         indices = torch.cat([g[0] for g in gates], dim=axis)
         scores = torch.cat([g[1] for g in gates], dim=axis)
-        shared = None if gates[0][2] is None else torch.cat([g[2] for g in gates], dim=axis)
-        y = self._layer(joined, indices, scores, shared)
+        y = self._layer(joined, indices, scores, gates[0][2])
         return list(torch.split(y, [v.shape[axis] for v in values], dim=axis))
 
     @staticmethod
     def _combine(routed: torch.Tensor, scores: torch.Tensor, shared: torch.Tensor) -> torch.Tensor:
-        """sum_k scores_k * routed_k + shared (qwen4_exp.py:1048-1051), fp32 accumulation."""
-        return ((routed.float() * scores[..., None].float()).sum(dim=-2) + shared.float()).to(routed.dtype)
+        """sum_k scores_k * routed_k + shared (qwen4_exp.py:1048-1051), fp32 accumulation in k
+        order (wm_combine_pairs)."""
+        return combine_pairs(routed, scores.float(), shared)
 
 
 # ----------------------------------------------------------------------------- DeepSeek operators
@@ -444,9 +453,10 @@ class Gate:
         return weights, indices
 
 
-def route_reduce(routed: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
-    """sum_k routed_k * scores_k (model.py:544-546), fp32 accumulation, routed dtype out."""
-    return (routed.float() * scores[..., None].float()).sum(dim=-2).to(routed.dtype)
+def route_reduce(routed: torch.Tensor, scores: torch.Tensor, add: torch.Tensor | None = None) -> torch.Tensor:
+    """sum_k routed_k * scores_k (+ add) (model.py:544-546, :540-541), fp32 accumulation in k
+    order, bf16 out (wm_combine_pairs)."""
+    return combine_pairs(routed, scores.float(), add)
 
 
 def streaming_moe(gate: Gate, switch_mlp: _StreamingSwitchGLU, shared, x: torch.Tensor) -> torch.Tensor:
@@ -461,5 +471,4 @@ def streaming_moe(gate: Gate, switch_mlp: _StreamingSwitchGLU, shared, x: torch.
         if isinstance(table, FP8Experts):
             return moe_fp8(x, idx, weights, table, shared, None)
         return moe_mxfp4(x, idx, weights, table, shared, None)
-    routed = route_reduce(switch_mlp(x, indices), weights)
-    return (routed.float() + shared(x).float()).to(x.dtype)
+    return route_reduce(switch_mlp(x, indices), weights, shared(x).to(torch.bfloat16))

@@ -283,10 +283,21 @@ def moe_mxfp4(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, exp
     return y
 
 
+def _pair_out(out: torch.Tensor | None, x: torch.Tensor, k: int, device) -> torch.Tensor:
+    H = x.shape[-1]
+    if out is None:
+        return torch.empty(*x.shape[:-1], k, H, dtype=torch.bfloat16, device=device)
+    if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != x.numel() * k or out.device != device:
+        raise ValueError("out must be a contiguous bf16 tensor of [.., K, H] on the device")
+    return out
+
+
 def experts_mxfp4(x: torch.Tensor, indices: torch.Tensor, experts: MXFP4Experts,
-                  validate: bool = False) -> torch.Tensor:
-    """Per-pair expert outputs in router order: [.., K, H] bf16 (StreamingExperts contract)."""
-    device = _require_device(x, indices, *experts.tensors())
+                  validate: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-pair expert outputs in router order: [.., K, H] bf16 (StreamingExperts contract).
+    A pair with a negative id leaves its row of ``out`` as it is (a masked pair); an unknown
+    or non-resident expert gives a zero row."""
+    device = _require_device(x, indices, *experts.tensors(), out)
     x = _contig(x, torch.bfloat16, "x")
     H = x.shape[-1]
     T = x.numel() // H if H else 0
@@ -296,10 +307,58 @@ def experts_mxfp4(x: torch.Tensor, indices: torch.Tensor, experts: MXFP4Experts,
     table = experts.c_struct()
     ws_bytes = _lib.load().wm_moe_mxfp4_workspace_size(T, k, ctypes.byref(table))
     ws = _workspace(ws_bytes, device)
-    out = torch.empty(*x.shape[:-1], k, H, dtype=torch.bfloat16, device=device)
+    out = _pair_out(out, x, k, device)
     _lib.call("wm_experts_mxfp4", _ptr(x), T, _ptr(idx), k, ctypes.byref(table), _ptr(out), _ptr(ws), ws_bytes,
               _stream(device))
     return out
+
+
+def combine_pairs(rows: torch.Tensor, weights: torch.Tensor, add: torch.Tensor | None = None) -> torch.Tensor:
+    """y = sum_k weights[.., k] * rows[.., k, :] (+ add), fp32 in k order, bf16 [.., H]
+    (SparseMoE._combine, qwen4_exp.py:1048-1051; _route_reduce, model.py:544-546)."""
+    device = _require_device(rows, weights, add)
+    rows = _contig(rows, torch.bfloat16, "rows")
+    H, k = rows.shape[-1], rows.shape[-2]
+    T = rows.numel() // (H * k) if H and k else 0
+    w = _contig(weights, torch.float32, "weights")
+    if w.numel() != T * k:
+        raise ValueError("weights must be [.., K] matching rows")
+    a = None if add is None else _contig(add, torch.bfloat16, "add")
+    if a is not None and a.numel() != T * H:
+        raise ValueError("add must be [.., H] matching rows")
+    y = torch.empty(*rows.shape[:-2], H, dtype=torch.bfloat16, device=device)
+    _lib.call("wm_combine_pairs", _ptr(rows), _ptr(w), T, k, H, _ptr(a), _ptr(y), _stream(device))
+    return y
+
+
+def mlp_bf16(x: torch.Tensor, gate_w: torch.Tensor, up_w: torch.Tensor, down_w: torch.Tensor,
+             gate_vec: torch.Tensor | None = None, add: torch.Tensor | None = None,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """add + sigmoid(x . gate_vec) * down(silu(x gate_w^T) * (x up_w^T)), bf16 [.., H]: the
+    reference's bf16 shared expert (qwen4_exp.py:763-771, :1045) on the library's kernels.
+    ``out`` may be ``add`` (in place)."""
+    device = _require_device(x, gate_w, up_w, down_w, gate_vec, add, out)
+    x = _contig(x, torch.bfloat16, "x")
+    H = x.shape[-1]
+    T = x.numel() // H if H else 0
+    I = gate_w.shape[0]
+    gw, uw, dw = (_contig(t, torch.bfloat16, n) for t, n in ((gate_w, "gate_w"), (up_w, "up_w"), (down_w, "down_w")))
+    if gw.shape != (I, H) or uw.shape != (I, H) or dw.shape != (H, I):
+        raise ValueError("weights must be gate/up [I, H] and down [H, I]")
+    gv = None if gate_vec is None else _contig(gate_vec, torch.bfloat16, "gate_vec").reshape(-1)
+    if gv is not None and gv.numel() != H:
+        raise ValueError("gate_vec must have H elements")
+    a = None if add is None else _contig(add, torch.bfloat16, "add")
+    if a is not None and a.numel() != T * H:
+        raise ValueError("add must match x")
+    y = torch.empty_like(x) if out is None else out
+    if y.dtype != torch.bfloat16 or not y.is_contiguous() or y.numel() != T * H:
+        raise ValueError("out must be a contiguous bf16 tensor shaped like x")
+    ws_bytes = _lib.load().wm_mlp_bf16_workspace_size(T, H, I)
+    ws = _workspace(ws_bytes, device)
+    _lib.call("wm_mlp_bf16", _ptr(x), T, H, I, _ptr(gw), _ptr(uw), _ptr(dw), _ptr(gv), _ptr(a), _ptr(y), _ptr(ws),
+              ws_bytes, _stream(device))
+    return y
 
 
 @dataclass(frozen=True)
@@ -384,9 +443,11 @@ def moe_fp8(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, exper
     return y
 
 
-def experts_fp8(x: torch.Tensor, indices: torch.Tensor, experts: FP8Experts, validate: bool = False) -> torch.Tensor:
-    """Per-pair FP8 expert outputs in router order: [.., K, H] bf16 (_StreamingSwitchGLU contract)."""
-    device = _require_device(x, indices, *experts.tensors())
+def experts_fp8(x: torch.Tensor, indices: torch.Tensor, experts: FP8Experts, validate: bool = False,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-pair FP8 expert outputs in router order: [.., K, H] bf16 (_StreamingSwitchGLU
+    contract); masked pairs (negative ids) leave their rows of ``out`` as they are."""
+    device = _require_device(x, indices, *experts.tensors(), out)
     x = _contig(x, torch.bfloat16, "x")
     H = x.shape[-1]
     T = x.numel() // H if H else 0
@@ -396,7 +457,7 @@ def experts_fp8(x: torch.Tensor, indices: torch.Tensor, experts: FP8Experts, val
     table = experts.c_struct()
     ws_bytes = _lib.load().wm_moe_fp8_workspace_size(T, k, ctypes.byref(table))
     ws = _workspace(ws_bytes, device)
-    out = torch.empty(*x.shape[:-1], k, H, dtype=torch.bfloat16, device=device)
+    out = _pair_out(out, x, k, device)
     _lib.call("wm_experts_fp8", _ptr(x), T, _ptr(idx), k, ctypes.byref(table), _ptr(out), _ptr(ws), ws_bytes,
               _stream(device))
     return out
@@ -498,8 +559,14 @@ class MoEStack:
     def workspace_bytes(self, tokens: int) -> int:
         return _lib.load().wm_moe_stack_mxfp4_workspace_size(tokens, self.k, ctypes.byref(self._tables[0]))
 
-    def __call__(self, logits: torch.Tensor, residual: torch.Tensor, x_out: torch.Tensor | None = None):
-        """logits fp32 [L, T, E]; residual fp32 [T, H] updated in place; x_out bf16 [T, H] (optional)."""
+    def __call__(self, logits: torch.Tensor, residual: torch.Tensor, x_out: torch.Tensor | None = None,
+                 cancel=None):
+        """logits fp32 [L, T, E]; residual fp32 [T, H] updated in place; x_out bf16 [T, H] (optional).
+
+        ``cancel`` (optional) is a callable polled before each layer is enqueued, like the
+        reference's cancel callback (Native/QwenNative/capi.h:36-37): when it returns true the
+        call raises ``Cancelled`` (status 2); the layers enqueued before it still run, so the
+        caller restores the residual."""
         _require_device(logits, residual, x_out)
         L = len(self.layers)
         T = residual.shape[0]
@@ -508,9 +575,10 @@ class MoEStack:
         need = self.workspace_bytes(T)
         if self._ws is None or self._ws.numel() < need:
             self._ws = _workspace(need, self.device)
+        hook = None if cancel is None else _lib.CANCEL_FN(lambda _ctx: 1 if cancel() else 0)
         _lib.call("wm_moe_stack_mxfp4", _ptr(logits), L, T, self.k, int(self.norm), self._tables, self._shared,
                   self._gates, _ptr(residual), float(self.eps), _ptr(x_out), _ptr(self._ws), self._ws.numel(),
-                  _stream(self.device))
+                  hook, None, _stream(self.device))
         return residual
 
 
@@ -530,15 +598,34 @@ def repack_down_slices(experts: MXFP4Experts) -> tuple[torch.Tensor, torch.Tenso
     return dst, dst_s
 
 
+class DecodeStackError(_lib.WhallmError):
+    """A persistent decode launch ended early (its status word was nonzero)."""
+
+
 class PersistentDecodeStack:
     """One-token decode through L MXFP4 MoE layers in one persistent kernel launch
-    (wm_moe_decode_persistent_mxfp4). Repacks the down regions slice-major once,
-    keeps the per-layer descriptor table and the message state on the device."""
+    (wm_moe_decode_persistent_mxfp4); keeps the per-layer descriptor table and the message
+    state on the device.
+
+    ``down_layout``: "slices" repacks every layer's down regions slice-major once (the
+    fastest reads; the tables must not change afterwards), "rows" reads them in place in
+    the reference row layout. Tables with a slot map (a slot cache's ``table(file)``,
+    whose slots are refilled over time) are always read in place.
+    """
+
+    # status word values (wm_moe_decode_persistent_mxfp4)
+    STATUS_TEXT = {1: "a message wait ran out", 2: "cancelled", 3: "a selected expert is not resident"}
 
     def __init__(self, layers: list[MXFP4Experts], shared: list[MXFP4Experts],
-                 shared_gates: list[torch.Tensor] | None = None, k: int = 10, eps: float = 1e-6):
+                 shared_gates: list[torch.Tensor] | None = None, k: int = 10, eps: float = 1e-6,
+                 down_layout: str = "slices"):
         if not layers or len(shared) != len(layers):
             raise ValueError("one shared expert per layer is required")
+        if down_layout not in ("slices", "rows"):
+            raise ValueError("down_layout must be 'slices' or 'rows'")
+        if any(e.slots is not None for e in layers):
+            down_layout = "rows"  # a private copy would go stale when the slots are refilled
+        self.down_layout = down_layout
         self.device = layers[0].gate_up.device
         self.k, self.eps = k, eps
         self.L, self.E = len(layers), layers[0].count
@@ -551,17 +638,25 @@ class PersistentDecodeStack:
                 raise ValueError("layers differ in shape")
             if e.gate_up.dim() != 3:
                 raise ValueError("routed experts need a leading expert axis")
-            d, ds = repack_down_slices(e)
-            sd, sds = repack_down_slices(s)
+            if s.slots is not None:
+                raise ValueError("the shared expert must be resident (no slot map)")
+            if down_layout == "slices":
+                d, ds = repack_down_slices(e)
+                sd, sds = repack_down_slices(s)
+                self._keep += [d, ds, sd, sds]
+                down = (d.data_ptr(), ds.data_ptr(), d.stride(0) * 4, ds.stride(0))
+                sdown = (sd.data_ptr(), sds.data_ptr())
+            else:
+                down = (e.down.data_ptr(), e.down_scales.data_ptr(), e.down.stride(0) * 4, e.down_scales.stride(0))
+                sdown = (s.down.data_ptr(), s.down_scales.data_ptr())
             g = shared_gates[l] if shared_gates is not None else None
             if g is not None and (g.dtype != torch.bfloat16 or g.numel() != self.H):
                 raise ValueError("shared gate must be bf16 [H]")
-            self._keep += [d, ds, sd, sds]
             descs.append(_lib.DecodeLayerC(
-                e.gate_up.data_ptr(), e.gate_up_scales.data_ptr(), d.data_ptr(), ds.data_ptr(),
-                e.gate_up.stride(0) * 4, e.gate_up_scales.stride(0), d.stride(0) * 4, ds.stride(0),
+                e.gate_up.data_ptr(), e.gate_up_scales.data_ptr(), down[0], down[1],
+                e.gate_up.stride(0) * 4, e.gate_up_scales.stride(0), down[2], down[3],
                 0 if e.slots is None else e.slots.data_ptr(),
-                s.gate_up.data_ptr(), s.gate_up_scales.data_ptr(), sd.data_ptr(), sds.data_ptr(),
+                s.gate_up.data_ptr(), s.gate_up_scales.data_ptr(), sdown[0], sdown[1],
                 0 if g is None else g.data_ptr()))
         table = (_lib.DecodeLayerC * self.L)(*descs)
         raw = bytes(table)
@@ -570,22 +665,47 @@ class PersistentDecodeStack:
         self.state = torch.zeros(lib.wm_decode_state_size(self.L, self.E), dtype=torch.uint8, device=self.device)
         self.status_offset = lib.wm_decode_status_offset(self.L, self.E)
 
-    def __call__(self, logits: torch.Tensor, residual: torch.Tensor, x_out: torch.Tensor | None = None):
-        """logits fp32 [L, E] (or [L, 1, E]); residual fp32 [H] (or [1, H]) updated in place."""
+    def __call__(self, logits: torch.Tensor, residual: torch.Tensor, x_out: torch.Tensor | None = None,
+                 check: bool = True, cancel: torch.Tensor | None = None, trace: torch.Tensor | None = None):
+        """logits fp32 [L, E] (or [L, 1, E]); residual fp32 [H] (or [1, H]) updated in place.
+
+        With ``check`` the call waits for the launch and raises ``DecodeStackError`` (or
+        ``Cancelled``) when it ended early, after resetting the state; residual and x_out are
+        then unchanged. ``check=False`` leaves the launch running: read ``status()`` later.
+        ``cancel``: an int32 tensor (pinned host memory or on the device) the caller may set
+        nonzero while the launch runs; the launch stops after the layer that reads it.
+        ``trace``: fp32 [L, H] on the device, receives the residual after every layer."""
         _require_device(logits, residual, x_out)
         if logits.dtype != torch.float32 or not logits.is_contiguous() or logits.numel() != self.L * self.E:
             raise ValueError("logits must be contiguous float32 [layers, experts]")
         if residual.dtype != torch.float32 or not residual.is_contiguous() or residual.numel() != self.H:
             raise ValueError("residual must be contiguous float32 [hidden] (one token)")
+        if cancel is not None and (cancel.dtype != torch.int32 or cancel.numel() < 1
+                                   or not (cancel.is_cuda or cancel.is_pinned())):
+            raise ValueError("cancel must be an int32 tensor on the device or in pinned host memory")
+        if trace is not None and (trace.dtype != torch.float32 or not trace.is_contiguous()
+                                  or trace.numel() != self.L * self.H or trace.device != self.device):
+            raise ValueError("trace must be a contiguous float32 [layers, hidden] device tensor")
         _lib.call("wm_moe_decode_persistent_mxfp4", _ptr(logits), self.L, self.E, self.k, self.H, self.I,
                   _ptr(self.table), _ptr(residual), float(self.eps), _ptr(x_out), _ptr(self.state),
-                  self.state.numel(), _stream(self.device))
+                  self.state.numel(), 1 if self.down_layout == "rows" else 0, _ptr(cancel), _ptr(trace),
+                  _stream(self.device))
+        if check:
+            self.raise_for_status()
         return residual
 
     def status(self) -> int:
-        """0 when every exchange completed; nonzero after a stalled exchange ended a
-        launch (then call reset() before the next one). Synchronises the device."""
+        """The launch's outcome: 0 done, 1 a message wait ran out, 2 cancelled, 3 a selected
+        expert is not resident. Nonzero needs reset() before the next launch. Synchronises."""
         return int(self.state[self.status_offset:self.status_offset + 4].view(torch.int32).item())
+
+    def raise_for_status(self) -> None:
+        """Raises (after reset()) when the last launch ended early."""
+        st = self.status()
+        if st != 0:
+            self.reset()
+            kind = _lib.Cancelled if st == 2 else DecodeStackError
+            raise kind(f"persistent decode: {self.STATUS_TEXT.get(st, f'status {st}')}")
 
     def reset(self):
         self.state.zero_()

@@ -15,8 +15,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .ops import MXFP4Experts
-from .route_cache import RouteCachePolicy
+from .ops import MXFP4Experts, experts_mxfp4
 
 
 def qwen_blob_bytes(hidden: int, inter: int) -> int:
@@ -83,7 +82,7 @@ class SlotCache:
         if not handle:
             raise SlotCacheError(err.value.decode(errors="replace"))
         self._handle = ctypes.c_void_p(handle)
-        self.route_policy: RouteCachePolicy | None = None
+        self.route_policy = False
         self.route_phase = "decode"
 
     def _check(self, status: int, what: str) -> None:
@@ -105,54 +104,128 @@ class SlotCache:
         if self.device is None:
             raise SlotCacheError("policy-only cache")
         ids = np.ascontiguousarray(np.asarray(experts, np.int32).reshape(-1))
-        if self.route_policy is not None:
-            self.observe(file, ids)
         out = np.empty(ids.size, np.int32)
         stream = torch.cuda.current_stream(self.device).cuda_stream
         self._check(_lib.load().wm_slot_cache_acquire(self._handle, file, ids.ctypes.data, ids.size, out.ctypes.data,
                                                       ctypes.c_void_p(stream)), "acquire")
         return out.tolist()
 
-    # ---- route mode (ExpertCache with eviction_policy "route", expert_cache.py:806-815, 1088-1181)
+    def acquire_ready(self, file: int, experts) -> tuple[list[int], list[bool]]:
+        """The cached-first acquire (engine.mm:2204-2234): (slots, ready flags). Ready experts
+        were resident already and may be used by work enqueued now; the others are being
+        filled on the copy stream until ``wait_fills()``."""
+        if self.device is None:
+            raise SlotCacheError("policy-only cache")
+        ids = np.ascontiguousarray(np.asarray(experts, np.int32).reshape(-1))
+        out = np.empty(ids.size, np.int32)
+        ready = np.empty(ids.size, np.int32)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_acquire_ready(self._handle, file, ids.ctypes.data, ids.size,
+                                                            out.ctypes.data, ready.ctypes.data,
+                                                            ctypes.c_void_p(stream)), "acquire_ready")
+        return out.tolist(), [bool(r) for r in ready]
 
-    def enable_route_policy(self, top_k: int) -> RouteCachePolicy:
-        """Evict by the route-history policy (files = layers) instead of LFU."""
-        self.route_policy = RouteCachePolicy(self.files, self.experts, self.slots, top_k)
-        self._push_route()
-        return self.route_policy
+    def wait_fills(self) -> None:
+        """The current stream waits for the fills of earlier ``acquire_ready`` calls."""
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_wait_fills(self._handle, ctypes.c_void_p(stream)), "wait_fills")
 
-    def _push_route(self) -> None:
-        pol = self.route_policy
-        scores = np.ascontiguousarray(pol.scores, np.float64)
-        quotas = np.ascontiguousarray(pol.quotas, np.int32)
-        self._check(_lib.load().wm_slot_cache_set_route(self._handle, scores.ctypes.data, quotas.ctypes.data),
-                    "set_route")
+    def experts_ready_first(self, file: int, x: torch.Tensor, indices: torch.Tensor,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+        """Per-pair outputs [.., K, H] of ``file``'s experts in router order, the pairs whose
+        experts are resident computed while the missing ones are copied in, the rest after
+        (the native engine's ready-then-late order, engine.mm:2204-2234). The result equals
+        one call with every expert resident, bit for bit. ``indices`` is read on the host,
+        as the reference's acquire is."""
+        ids = indices.to("cpu", torch.int64)
+        unique = sorted(set(ids.reshape(-1).tolist()))
+        _, ready = self.acquire_ready(file, unique)
+        ready_ids = torch.tensor([e for e, r in zip(unique, ready) if r], dtype=torch.int64)
+        is_ready = torch.isin(ids, ready_ids).to(indices.device)
+        idx = indices.to(torch.int32)
+        none = torch.full_like(idx, -1)
+        table = self.table(file)
+        out = experts_mxfp4(x, torch.where(is_ready, idx, none), table, out=out)
+        self.wait_fills()
+        if not all(ready):
+            experts_mxfp4(x, torch.where(is_ready, none, idx), table, out=out)
+        return out
+
+    def acquire_files(self, requests: dict) -> dict:
+        """One plan over several files ({file: expert ids}): every requested expert is resident
+        together afterwards (the persistent decode stack reads all layers in one launch)."""
+        if self.device is None:
+            raise SlotCacheError("policy-only cache")
+        files = np.ascontiguousarray(list(requests), np.int32)
+        lists = [np.asarray(requests[int(f)], np.int32).reshape(-1) for f in files]
+        counts = np.ascontiguousarray([a.size for a in lists], np.int32)
+        ids = np.ascontiguousarray(np.concatenate(lists) if lists else np.zeros(0, np.int32), np.int32)
+        out = np.empty(ids.size, np.int32)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_acquire_files(self._handle, files.size, files.ctypes.data,
+                                                            counts.ctypes.data, ids.ctypes.data, out.ctypes.data,
+                                                            ctypes.c_void_p(stream)), "acquire_files")
+        got, at = {}, 0
+        for f, n in zip(files.tolist(), counts.tolist()):
+            got[f] = out[at:at + n].tolist()
+            at += n
+        return got
+
+    # ---- route mode: the native route-history policy (expert_cache.py:806-815, 1088-1181)
+
+    def enable_route_policy(self, top_k: int) -> None:
+        """Evict by the cache's route-history policy (files = layers) instead of LFU; acquires
+        then count as routes of the current phase."""
+        self._check(_lib.load().wm_slot_cache_route_policy(self._handle, int(top_k)), "route_policy")
+        self.route_policy = True
+
+    def disable_route_policy(self) -> None:
+        self._check(_lib.load().wm_slot_cache_route_policy(self._handle, 0), "route_policy")
+        self.route_policy = False
 
     def observe(self, file: int, selected, phase: str | None = None) -> None:
-        """Routes of ``file`` (expert ids, top_k per token) for the route policy; a batched
-        prefill that bypasses the slots reports its routes here (observe_batched_routes)."""
-        if self.route_policy is not None and self.route_policy.observe(file, selected, phase or self.route_phase):
-            self._push_route()
+        """Routes of ``file`` that bypassed the slots (observe_batched_routes, :1115-1118):
+        token-major expert ids, top_k per token."""
+        ids = np.ascontiguousarray(np.asarray(selected, np.int32).reshape(-1))
+        prefill = (phase or self.route_phase) == "prefill"
+        self._check(_lib.load().wm_slot_cache_route_observe(self._handle, file, ids.ctypes.data, ids.size,
+                                                            int(prefill)), "route_observe")
 
     def begin_route_request(self) -> None:
-        """A new prompt (begin_route_request, expert_cache.py:1105-1109)."""
-        if self.route_policy is not None:
-            self.route_policy.begin_prefill()
+        """A new prompt: its routes become the prior (begin_route_request, :1105-1109)."""
+        if self.route_policy:
+            self._check(_lib.load().wm_slot_cache_route_begin_request(self._handle), "route_begin_request")
 
     def set_route_phase(self, phase: str) -> None:
         """"prefill" or "decode"; leaving a prefill rebalances (trace_routes, :1088-1103)."""
-        previous, self.route_phase = self.route_phase, phase
-        if self.route_policy is not None and previous == "prefill" and phase != "prefill":
-            self.route_policy.rebalance()
-            self._push_route()
+        if phase not in ("prefill", "decode"):
+            raise ValueError("phase must be 'prefill' or 'decode'")
+        self.route_phase = phase
+        self._check(_lib.load().wm_slot_cache_route_phase(self._handle, int(phase == "prefill")), "route_phase")
 
     def record_read(self, file: int, seconds: float) -> None:
-        if self.route_policy is not None:
-            self.route_policy.record_read(file, seconds)
+        if self.route_policy:
+            self._check(_lib.load().wm_slot_cache_route_record_read(self._handle, file, float(seconds)),
+                        "route_record_read")
 
-    def disable_route_policy(self) -> None:
-        self.route_policy = None
-        self._check(_lib.load().wm_slot_cache_set_route(self._handle, None, None), "set_route")
+    def rebalance(self) -> None:
+        self._check(_lib.load().wm_slot_cache_route_rebalance(self._handle), "route_rebalance")
+
+    def route_state(self) -> dict:
+        """The policy's arrays: scores and short / long rates [files, experts], quotas,
+        decode / prompt tokens and read cost per file, rebalances and slot capacity."""
+        F, E = self.files, self.experts
+        scores, short, long_ = (np.empty((F, E), np.float64) for _ in range(3))
+        quotas = np.empty(F, np.int32)
+        tokens = np.empty(2 * F, np.int64)
+        cost = np.empty(F, np.float64)
+        counters = np.empty(2, np.int64)
+        self._check(_lib.load().wm_slot_cache_route_state(
+            self._handle, scores.ctypes.data, quotas.ctypes.data, short.ctypes.data, long_.ctypes.data,
+            tokens.ctypes.data, cost.ctypes.data, counters.ctypes.data), "route_state")
+        return {"scores": scores, "quotas": quotas, "short": short, "long": long_, "decode_tokens": tokens[:F],
+                "prompt_tokens": tokens[F:], "read_cost": cost, "rebalances": int(counters[0]),
+                "capacity": int(counters[1])}
 
     # ---- whole-file reads and prompt-tail seeding (engine.mm:1647-1678)
 
@@ -160,17 +233,23 @@ class SlotCache:
         """A device buffer for one whole file (experts x blob bytes)."""
         return torch.empty(self.experts * self.blob, dtype=torch.uint8, device=self.device)
 
-    def read_layer(self, file: int, buffer: torch.Tensor) -> None:
-        """Start reading the whole of ``file`` into ``buffer`` on the copy stream (after the
-        current stream's earlier work, which may still read the buffer)."""
+    def read_layer(self, file: int, buffer: torch.Tensor, experts=None) -> None:
+        """Start reading ``file`` into ``buffer`` on the copy stream (after the current stream's
+        earlier work, which may still read the buffer): the whole file, or only ``experts``
+        (sorted unique ids; consecutive ids are read together, up to 32 blobs a copy)."""
         if self.device is None:
             raise SlotCacheError("policy-only cache")
         if buffer.device != self.device or buffer.dtype != torch.uint8 or buffer.numel() < self.experts * self.blob \
                 or not buffer.is_contiguous():
             raise ValueError("the layer buffer must be a contiguous uint8 device tensor of experts * blob bytes")
-        stream = torch.cuda.current_stream(self.device).cuda_stream
-        self._check(_lib.load().wm_slot_cache_read_layer(self._handle, file, ctypes.c_void_p(buffer.data_ptr()),
-                                                         ctypes.c_void_p(stream)), "read_layer")
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        if experts is None:
+            self._check(_lib.load().wm_slot_cache_read_layer(self._handle, file, ctypes.c_void_p(buffer.data_ptr()),
+                                                             stream), "read_layer")
+            return
+        ids = np.ascontiguousarray(np.asarray(experts, np.int32).reshape(-1))
+        self._check(_lib.load().wm_slot_cache_read_experts(self._handle, file, ids.ctypes.data, ids.size,
+                                                           ctypes.c_void_p(buffer.data_ptr()), stream), "read_experts")
 
     def wait_layer(self, file: int) -> None:
         """The current stream waits for the last read_layer of ``file``."""
@@ -181,9 +260,29 @@ class SlotCache:
         """The experts of a whole-file buffer as an expert table (expert e = blob e)."""
         return self._blob_table(buffer.view(self.experts, self.blob), self.experts, None)
 
+    def seed_tail(self, file: int, routes: torch.Tensor, limit: int, buffer: torch.Tensor) -> tuple[list, list]:
+        """Prompt-tail seeding (expert_cache.py:1399-1430): the experts of the last 128 token
+        rows of ``routes`` (int32 [T, K] on the device) ranked by count, latest use and id on
+        the device; the first ``limit`` that are not resident go into free slots from the
+        whole-file ``buffer``. Returns (experts, slots), least valuable first."""
+        if routes.dtype != torch.int32 or not routes.is_contiguous() or routes.device != self.device:
+            raise ValueError("routes must be a contiguous int32 device tensor [tokens, k]")
+        k = routes.shape[-1]
+        rows = routes.numel() // k if k else 0
+        experts = np.empty(max(limit, 1), np.int32)
+        slots = np.empty(max(limit, 1), np.int32)
+        count = np.zeros(1, np.int32)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_seed_tail(self._handle, file, ctypes.c_void_p(routes.data_ptr()), rows, k,
+                                                        limit, ctypes.c_void_p(buffer.data_ptr()), experts.ctypes.data,
+                                                        slots.ctypes.data, count.ctypes.data,
+                                                        ctypes.c_void_p(stream)), "seed_tail")
+        n = int(count[0])
+        return experts[:n].tolist(), slots[:n].tolist()
+
     def seed(self, file: int, experts, uses, buffer: torch.Tensor) -> list[int]:
-        """Keep ``experts`` of ``file`` (least valuable first, e.g. hot_tail_experts) resident
-        with use counts ``uses`` (or None), copied from the whole-file ``buffer``."""
+        """Keep ``experts`` of ``file`` (least valuable first) resident with use counts ``uses``
+        (or None), copied from the whole-file ``buffer`` (the native engine's seed_layer)."""
         ids = np.ascontiguousarray(np.asarray(experts, np.int32).reshape(-1))
         cnt = None if uses is None else np.ascontiguousarray(np.asarray(uses, np.int32).reshape(-1))
         if cnt is not None and cnt.size != ids.size:
@@ -205,9 +304,9 @@ class SlotCache:
         return self._blob_table(self.slot_memory.view(self.slots, self.blob), self.slots, self.map[file])
 
     def stats(self) -> dict:
-        out = (ctypes.c_int64 * 4)()
+        out = (ctypes.c_int64 * 5)()
         _lib.load().wm_slot_cache_stats(self._handle, out)
-        return {"hits": out[0], "misses": out[1], "bytes": out[2], "fills": out[3]}
+        return {"hits": out[0], "misses": out[1], "bytes": out[2], "fills": out[3], "copies": out[4]}
 
     def close(self) -> None:
         if getattr(self, "_handle", None):
