@@ -143,6 +143,19 @@ WM_EXPORT int wm_moe_mxfp4(const void* x, int32_t tokens, const int32_t* indices
                            int32_t k, const wm_mxfp4_experts* experts, const wm_mxfp4_experts* shared,
                            const void* shared_gate, void* y, void* workspace, size_t workspace_bytes,
                            void* stream);
+/* wm_moe_mxfp4 without a workspace and without any allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Its scratch (the decode path's act rows) is
+ * a file-scope device array of wm_moe_mxfp4_noalloc_max_bytes() = 4 MiB per GPU, held until
+ * the process ends; its address is looked up on a device's first call. Only calls that take
+ * the decode path (tokens * k <= 256, row layout) and need at most that much scratch
+ * (4 * (tokens * (k + 1)) * inter bytes) are accepted; others fail with a message. Every
+ * call on one GPU shares its array, so calls that may overlap on one GPU (other streams,
+ * other threads) race; calls ordered on one stream do not. Same results as wm_moe_mxfp4. */
+WM_EXPORT size_t wm_moe_mxfp4_noalloc_max_bytes(void);
+WM_EXPORT int wm_moe_mxfp4_noalloc(const void* x, int32_t tokens, const int32_t* indices, const float* weights,
+                                   int32_t k, const wm_mxfp4_experts* experts, const wm_mxfp4_experts* shared,
+                                   const void* shared_gate, void* y, void* stream);
 /* Per-pair expert outputs in router order, out bf16 [T, K, H]: the
  * StreamingExperts.__call__ contract (qwen4_exp.py:853-904) and
  * _StreamingSwitchGLU.__call__ (model.py:325-385). Same workspace size. */

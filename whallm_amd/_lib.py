@@ -61,6 +61,9 @@ _SIGNATURES = {
     "wm_moe_mxfp4": (c_int, [_P, c_int32, _P, _P, c_int32, POINTER(MXFP4ExpertsC), POINTER(MXFP4ExpertsC), _P,
                              _P, _P, c_size_t, _P]),
     "wm_experts_mxfp4": (c_int, [_P, c_int32, _P, c_int32, POINTER(MXFP4ExpertsC), _P, _P, c_size_t, _P]),
+    "wm_moe_mxfp4_noalloc_max_bytes": (c_size_t, []),
+    "wm_moe_mxfp4_noalloc": (c_int, [_P, c_int32, _P, _P, c_int32, POINTER(MXFP4ExpertsC), POINTER(MXFP4ExpertsC), _P,
+                                     _P, _P]),
     "wm_repack_prefill_mxfp4": (c_int, [POINTER(MXFP4ExpertsC), _P, _P, _P, _P, _P]),
     "wm_combine_pairs": (c_int, [_P, _P, c_int32, c_int32, c_int32, _P, _P, _P]),
     "wm_mlp_bf16_workspace_size": (c_size_t, [c_int32, c_int32, c_int32]),

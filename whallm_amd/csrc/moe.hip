@@ -1,5 +1,8 @@
 // C-ABI entry points of the MXFP4 MoE layer: argument checks, path choice
 // (fused dequant-GEMV for decode, MFMA grouped GEMM for prefill) and workspace sizing.
+#include <mutex>
+#include <string>
+
 #include "moe_internal.h"
 
 namespace wm {
@@ -79,6 +82,30 @@ static size_t decode_workspace(int tokens, int k, const wm_mxfp4_experts& e) {
   return sizeof(float) * (size_t)(tokens * k + tokens) * e.inter;
 }
 
+// Scratch of the allocation-free entry point: the decode path's act rows live in this
+// file-scope device array instead of a caller workspace. Each GPU holds its own copy for
+// the life of the process. Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in for the symbol): the device address is looked up once per
+// device with hipGetSymbolAddress, with that device current, and kept here.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static void* g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+static void* scratch_for_current_device() {
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) fail("wm_moe_mxfp4_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!ptr) fail("wm_moe_mxfp4_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace wm
 
 using namespace wm;
@@ -109,6 +136,29 @@ WM_EXPORT int wm_moe_mxfp4(const void* x, int32_t tokens, const int32_t* indices
     else
       prefill_mxfp4((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
                     (uint16_t*)y, true, workspace, workspace_bytes, s);
+  });
+}
+
+WM_EXPORT size_t wm_moe_mxfp4_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+WM_EXPORT int wm_moe_mxfp4_noalloc(const void* x, int32_t tokens, const int32_t* indices, const float* weights,
+                                   int32_t k, const wm_mxfp4_experts* experts, const wm_mxfp4_experts* shared,
+                                   const void* shared_gate, void* y, void* stream) {
+  return guarded([&] {
+    if (tokens < 0) fail("wm_moe_mxfp4_noalloc: negative token count");
+    if (k < 1 || k > 32) fail("wm_moe_mxfp4_noalloc: k must be in 1..32");
+    validate_pair(experts, shared);
+    if (tokens == 0) return;
+    if (!x || !indices || !weights || !y) fail("wm_moe_mxfp4_noalloc: null pointer");
+    if (!use_decode(tokens, k, *experts))
+      fail("wm_moe_mxfp4_noalloc: only calls that take the decode path (tokens * k <= 256, row layout)");
+    const size_t need = decode_workspace(tokens, k, *experts);
+    if (need > kNoAllocScratchBytes)
+      fail("wm_moe_mxfp4_noalloc: the call needs " + std::to_string(need) + " bytes of scratch, more than the " +
+           std::to_string(kNoAllocScratchBytes) + " it has");
+    void* ws = scratch_for_current_device();
+    decode_mxfp4((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
+                 (uint16_t*)y, true, (float*)ws, as_stream(stream));
   });
 }
 
