@@ -437,6 +437,8 @@ class MtpVerify:
         self.shared = [S.fp8_experts_device(1, hidden, inter, device, g) for _ in range(layers)]
         self.bias = [torch.randn(experts, device=device, generator=g) * 0.1 for _ in range(layers)]
         self.head = (torch.randn(vocab, hidden, device=device, generator=g) * hidden ** -0.5).to(torch.bfloat16)
+        from whallm_amd.verify import VerifyStep
+        self.verify = VerifyStep(self.layers, self.shared, self.bias, self.head, k=k)
         self.gen = g
         self.graph = None
 
@@ -458,24 +460,9 @@ class MtpVerify:
         self.r = torch.empty(self.T, self.H, device=self.device)
         self.drafts = torch.zeros(self.T - 1, dtype=torch.int32, device=self.device)
 
-    def _layers(self):
-        import whallm_amd as wa
-        x = wa.ops.residual_rmsnorm(self.r, None)
-        for l in range(self.L):
-            idx, w = wa.route_scored(self.logits[l], self.bias[l], self.K, func="sigmoid", route_scale=2.5,
-                                     n_groups=8, topk_groups=4)
-            y = wa.moe_fp8(x, idx, w, self.layers[l], self.shared[l], None)
-            x = wa.ops.residual_rmsnorm(self.r, y)
-        self.x_last = x
-
-    def _head_and_accept(self):
-        import whallm_amd as wa
-        self.vocab_logits = torch.matmul(self.x_last, self.head.t()).float()
-        self.accept = wa.mtp_verify_greedy(self.vocab_logits, self.drafts)
-
     def _body(self):
-        self._layers()
-        self._head_and_accept()
+        # the package's verify step: MoE layers, the LM head in fp32 (wm_linear_bf16), acceptance
+        self.accept, self.vocab_logits = self.verify(self.logits, self.r, self.drafts)
 
     def capture(self):
         self.logits.copy_(self.step_logits[0])
@@ -511,8 +498,9 @@ class MtpVerify:
         return total / launches
 
     def config(self):
-        return {"workload": "c5-verify: MTP verify, 4 tokens (1 accepted + 3 drafts) through a 4-layer FP8 MoE "
-                            "stack, bf16 LM head to 129280 fp32 logits, greedy acceptance on the device",
+        return {"workload": "c5-verify: MTP verify (whallm_amd.verify.VerifyStep), 4 tokens (1 accepted + 3 drafts) "
+                            "through a 4-layer FP8 MoE stack, bf16 LM head to 129280 fp32 logits, greedy acceptance "
+                            "on the device",
                 "hidden": self.H, "experts": self.E, "moe_intermediate": self.I, "top_k": self.K, "layers": self.L,
                 "tokens": self.T, "vocab": self.V}
 

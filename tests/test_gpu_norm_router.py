@@ -137,11 +137,13 @@ def test_packed_router_is_bit_identical(device, T, H, E, with_gate):
             wa.norm_router(r, y, router, None if with_gate else bf16_tensor(rng, (H,), device), router_packed=packed)
 
 
-@pytest.mark.parametrize("T,H,E", [(300, 2048, 512), (70, 7168, 256), (64, 1024, 64), (63, 2048, 128)])
+@pytest.mark.parametrize("T,H,E", [(300, 2048, 512), (70, 7168, 256), (64, 1024, 64), (63, 2048, 128),
+                                   (1, 2048, 512), (3, 7168, 1000), (4, 7168, 129280), (16, 1032, 77), (9, 2048, 64)])
 def test_linear_bf16_prefill_path(device, T, H, E):
     """wm_linear_bf16 at 64+ tokens runs on the router GEMM's MFMA path (a tile of x as
-    given): within the dot-product bound of the float64 product; 63 tokens stay on the
-    one-wave-per-output kernel."""
+    given), up to 16 tokens on the row-streaming kernel (every weight row read once for all
+    tokens; the C5 LM head at 4 x 129,280), in between on the one-wave-per-output kernel:
+    each within the dot-product bound of the float64 product."""
     rng = np.random.default_rng(T + E)
     x = bf16_tensor(rng, (T, H), device)
     w = bf16_tensor(rng, (E, H), device, 0.05)

@@ -140,6 +140,41 @@ __global__ void __launch_bounds__(256) linear_bf16_kernel(const uint32_t* __rest
   if (lane == 0) out[(int64_t)t * outputs + e] = acc;
 }
 
+// dot of 8 bf16 (one 16-byte chunk) against 8 bf16
+__device__ __forceinline__ float dot8_bf16x(uint4 a, uint4 b, float acc) {
+  acc = dot2_bf16(bits_to_bf16x2(a.x), bits_to_bf16x2(b.x), acc);
+  acc = dot2_bf16(bits_to_bf16x2(a.y), bits_to_bf16x2(b.y), acc);
+  acc = dot2_bf16(bits_to_bf16x2(a.z), bits_to_bf16x2(b.z), acc);
+  return dot2_bf16(bits_to_bf16x2(a.w), bits_to_bf16x2(b.w), acc);
+}
+
+// Few tokens (<= TMAX): a wave per output row streams the row once in 16-byte chunks and
+// dots every chunk with all tokens' x (which stay in the caches), so each weight byte is
+// read once however many tokens there are. grid: ceil(outputs / 4), 4 waves a block.
+template <int TMAX>
+__global__ void __launch_bounds__(256) linear_rows_kernel(const uint4* __restrict__ x, const uint4* __restrict__ w,
+                                                         int tokens, int chunks, int outputs, float* __restrict__ out) {
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int o = blockIdx.x * 4 + wave;
+  if (o >= outputs) return;
+  const uint4* wr = w + (int64_t)o * chunks;
+  float acc[TMAX];
+#pragma unroll
+  for (int t = 0; t < TMAX; ++t) acc[t] = 0.0f;
+  for (int c = lane; c < chunks; c += 64) {
+    const uint4 wv = wr[c];
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t)
+      if (t < tokens) acc[t] = dot8_bf16x(wv, x[(int64_t)t * chunks + c], acc[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < TMAX; ++t) {
+    if (t >= tokens) break;
+    const float v = segment_sum<64>(acc[t]);
+    if (lane == 0) out[(int64_t)t * outputs + o] = v;
+  }
+}
+
 }  // namespace wm
 
 using namespace wm;
@@ -203,8 +238,23 @@ WM_EXPORT int wm_linear_bf16(const void* x, const void* w, int32_t tokens, int32
     if (tokens < 0 || outputs < 0 || hidden < 2 || hidden % 2) fail("wm_linear_bf16: bad shape");
     if (tokens == 0 || outputs == 0) return;
     if (!x || !w || !out) fail("wm_linear_bf16: null pointer");
-    // 64+ tokens: the router GEMM on MFMA (norm_router.hip); else one wave per output
+    // 64+ tokens: the router GEMM on MFMA (norm_router.hip); up to 16 tokens with 16-byte
+    // rows: one pass over each weight row; else one wave per output
     if (linear_bf16_mfma(x, w, tokens, hidden, outputs, out, as_stream(stream))) return;
+    if (tokens <= 16 && hidden % 8 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0) {
+      const dim3 grid((outputs + 3) / 4);
+      const int chunks = hidden / 8;
+#define WM_LR(T) hipLaunchKernelGGL(linear_rows_kernel<T>, grid, dim3(256), 0, as_stream(stream), (const uint4*)x, \
+                                    (const uint4*)w, tokens, chunks, outputs, out)
+      if (tokens <= 1) WM_LR(1);
+      else if (tokens <= 2) WM_LR(2);
+      else if (tokens <= 4) WM_LR(4);
+      else if (tokens <= 8) WM_LR(8);
+      else WM_LR(16);
+#undef WM_LR
+      check_launch("linear_rows");
+      return;
+    }
     hipLaunchKernelGGL(linear_bf16_kernel, dim3((outputs + 3) / 4, tokens), dim3(256), 0, as_stream(stream),
                        (const uint32_t*)x, (const uint32_t*)w, tokens, hidden, outputs, out);
     check_launch("linear_bf16");
