@@ -5,8 +5,10 @@ Default workload ("c2-decode"): a Qwen3-Next-style
 48-layer stack of MXFP4 MoE layers (H 2048, 512 experts, I 512, top-10 + one
 always-on MXFP4 shared expert), one token per step, router logits N(0, 1), all
 weights resident in HBM (41 GB). A step = one token through the 48 layers,
-replayed from one HIP graph. ``--config c3-prefill`` runs one layer at a
-16,384-token prefill with Zipf(1.1)-skewed routing.
+replayed from one HIP graph. The same run then times the metric's other half, one
+layer at a 16,384-token prefill with Zipf(1.1)-skewed routing (
+"c3-prefill"), and reports it under "prefill" in the same line (``--no-prefill`` leaves
+it out; ``--config c3-prefill`` runs it alone).
 
 Synthetic data (random-init weights of the configured shapes; no checkpoints).
 """
@@ -613,37 +615,15 @@ def profiled_traffic(name: str):
     return None
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2-decode", choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--decode-impl", default="persistent", choices=["persistent", "layers"],
-                    help="c2-decode: one persistent kernel per token, or the per-layer kernel chain")
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
-    args = ap.parse_args()
-
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
-              "run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
-    device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    if args.config == "c2-decode":
-        wl = DecodeStack(device, impl=args.decode_impl)
-    elif args.config == "c4-prefill":
-        wl = FP8Layer(device, tokens=4096)
-    elif args.config.startswith("router-"):
-        wl = NormRouter(device, args.config)
-    else:
-        wl = WORKLOADS[args.config](device)
-    total = args.warmup + args.steps
+def measure(wl, steps: int, warmup: int):
+    """Times `steps` graph replays of the workload after `warmup` untimed ones (HIP events
+    on the replay stream, synchronised on both sides); returns (ms per step, tokens/s,
+    roofline object, wall seconds of the timed region)."""
+    device = wl.device
+    total = warmup + steps
     wl.prepare_inputs(total)
     wl.capture()
-    for i in range(args.warmup):
+    for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize(device)
 
@@ -652,7 +632,7 @@ def main():
     end_ev = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start_ev.record(stream)
-    for i in range(args.warmup, total):
+    for i in range(warmup, total):
         wl.step(i)
     end_ev.record(stream)
     torch.cuda.synchronize(device)
@@ -660,12 +640,11 @@ def main():
     gpu_ms = start_ev.elapsed_time(end_ev)
     if hasattr(wl, "check"):
         wl.check()
-    ms_per_step = gpu_ms / args.steps
+    ms_per_step = gpu_ms / steps
     value = wl.tokens_per_step() / (ms_per_step / 1e3)
-
     if isinstance(wl, DecodeStack):
         if wl.impl == "persistent":
-            k_ms = wl.kernel_ms(args.steps)
+            k_ms = wl.kernel_ms(steps)
             kernel = "decode_persistent_kernel (one launch = one token through 48 layers)"
         else:
             k_ms = ms_per_step
@@ -701,7 +680,7 @@ def main():
                     "algorithmic_bytes_per_launch": wl.algorithmic_bytes()}
     else:
         # dominant kernel: the grouped gate_up GEMM, timed with the library's HIP events
-        gu_ms, dn_ms = wl.kernel_ms(args.steps)
+        gu_ms, dn_ms = wl.kernel_ms(steps)
         achieved = wl.gate_up_flops() / (gu_ms / 1e3) / 1e12
         layer_tflops = wl.flops() / (ms_per_step / 1e3) / 1e12
         # fp4 x fp6 operands run the 32x32x64 f8f6f4 MFMA at the FP4/FP6 rate; the two
@@ -716,19 +695,72 @@ def main():
                     "algorithmic_flops_per_launch": wl.gate_up_flops(),
                     "layer_tflops": round(layer_tflops, 1)}
 
+    return ms_per_step, value, roofline, wall
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2-decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-impl", default="persistent", choices=["persistent", "layers"],
+                    help="c2-decode: one persistent kernel per token, or the per-layer kernel chain")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="c2-decode: leave out the 16K-token prefill half (the C3 layer) of the line")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    if args.config == "c2-decode":
+        wl = DecodeStack(device, impl=args.decode_impl)
+    elif args.config == "c4-prefill":
+        wl = FP8Layer(device, tokens=4096)
+    elif args.config.startswith("router-"):
+        wl = NormRouter(device, args.config)
+    else:
+        wl = WORKLOADS[args.config](device)
+    ms_per_step, value, roofline, wall = measure(wl, args.steps, args.warmup)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
         cpu = wl.cpu_baseline(args.cpu_budget)
         cpu["host"] = platform.processor() or platform.machine()
 
+    # The metric has two halves (decode and the 16K-token prefill): the default run times the
+    # prefill layer too, after the decode stack's weights are freed, and carries it in the
+    # same line; `value` stays the decode half (BASELINE's headline config).
+    prefill = None
+    if args.config == "c2-decode" and not args.no_prefill:
+        dtype, data, config = wl.dtype, wl.data, wl.config()
+        del wl
+        torch.cuda.empty_cache()
+        log("[bench] c3-prefill half")
+        pf = Prefill(device)
+        p_ms, p_value, p_roof, p_wall = measure(pf, min(args.steps, 20), min(args.warmup, 5))
+        prefill = {"value": round(p_value, 1), "unit": "tokens/s", "ms_per_step": round(p_ms, 5),
+                   "steps": min(args.steps, 20), "warmup": min(args.warmup, 5), "dtype": pf.dtype, "data": pf.data,
+                   "config": pf.config(), "roofline": p_roof, "wall_s_timed_region": round(p_wall, 4)}
+    else:
+        dtype, data, config = wl.dtype, wl.data, wl.config()
+
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": wl.dtype, "data": wl.data,
-        "config": wl.config(), "roofline": roofline, "cpu_baseline": cpu,
+        "vs_baseline": None, "dtype": dtype, "data": data,
+        "config": config, "roofline": roofline, "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }
+    if prefill is not None:
+        line["prefill"] = prefill
     print(json.dumps(line), flush=True)
 
 

@@ -100,7 +100,7 @@ __device__ __forceinline__ void ll_put_xcd(uint64_t* p, uint64_t word) {
 // rounds it raises the status word.
 template <int N, int EBITS = 32, typename Store>
 __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int stride, int limit, uint32_t epoch,
-                                          uint32_t* status, bool& ok, Store store) {
+                                          uint32_t* status, bool& ok, Store store, uint32_t* rounds = nullptr) {
   const uint32_t want = EBITS == 32 ? epoch : (epoch & ((1u << EBITS) - 1));
   auto tag = [](uint64_t v) { return (uint32_t)(v >> (64 - EBITS)); };
   uint64_t v[N];
@@ -138,11 +138,20 @@ __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int s
     int i = first + m * stride;
     if (i < limit) store(i, v[m]);
   }
+  if (rounds) *rounds = spins;
 }
 
-// Phase timestamps for a profiling build (expands to nothing in the library).
+// Phase timestamps and notes for the profiling build of whallm_amd.phase_trace (both expand
+// to nothing in the library). Points of the compute waves: 0 S0, 1 S0b, 3 phase A done
+// (act published), 5 S1, 4 next A tile issued, 6 phase B done; of the message wave: 8 S0,
+// 2 act poll start, 9 act gathered, 10 S1, 11 S2, 4 partial published, 12 partials
+// gathered, 6 r published, 13 r gathered; notes: 14 / 15 / 7 = re-poll rounds of the act,
+// partial and r gathers.
 #ifndef WM_DS_TRACE
 #define WM_DS_TRACE(layer, point)
+#endif
+#ifndef WM_DS_NOTE
+#define WM_DS_NOTE(layer, point, value)
 #endif
 
 __device__ __forceinline__ float bf16_round_f(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
@@ -238,10 +247,10 @@ __device__ __forceinline__ void ds_build_x(DSShared& sh, int tid) {
 // The two roles run separate loops (so their registers do not overlap) and meet at
 // the same four barriers per layer:
 //   S0: r_l and its rmsnorm statistics in LDS -> every wave builds a quarter of x
-//   S0b: x terms in LDS -> compute waves: phase A (one tile each), publish act,
-//                          prefetch the A tile of l+1
+//   S0b: x terms in LDS -> compute waves: phase A (one tile each), publish act
 //                          message wave: shared gate, gather the XCD's act slice
-//   S1: act ready  -> compute waves: phase B partials into LDS, prefetch B(l+1)
+//   S1: act ready  -> compute waves: prefetch the A tile of l+1, phase B partials into
+//                     LDS, prefetch B(l+1)
 //   S2: partials   -> (every wave leaves here if a message wait ran out)
 //                     message wave: publish the row block's partial, gather the 8
 //                     XCDs' partials, r += bf16(sum), publish r, gather the XCD's r
@@ -383,10 +392,13 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
       }
     }
     WM_DS_TRACE(l, 3);
-    issue_a(l + 1 < c.L ? l + 1 : l);
-    WM_DS_TRACE(l, 4);
     ds_barrier();  // S1: act slice and shared gate in LDS
     WM_DS_TRACE(l, 5);
+    // The A tile of l + 1 is issued after S1, not before: issued earlier, its loads sit
+    // in the CU's memory queue ahead of the message wave's act poll and delay it by their
+    // whole transfer (measured: the act gather ends 1.5 us later per layer)
+    issue_a(l + 1 < c.L ? l + 1 : l);
+    WM_DS_TRACE(l, 4);
     // ---- phase B: split-K partials of rows 64 j .. 64 j + 63 over this wave's K-steps
     {
       ds_v4f accb[4];
@@ -510,8 +522,12 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
       if (lane == 0) sh.gate = gv;
     }
     // ---- the XCD's act slice (every expert's 64 columns); tile t wrote words 8t .. 8t+7
+    uint32_t rounds = 0;
+    WM_DS_TRACE(l, 2);
     ll_gather<DS_NE_MAX * DS_SLICE / 64>(act_buf, lane, 64, c.NE * DS_SLICE, e_act, c.status, ok,
-                                         [&](int w, uint64_t v) { sh.act[w / DS_SLICE][w % DS_SLICE] = __uint_as_float((uint32_t)v); });
+                                         [&](int w, uint64_t v) { sh.act[w / DS_SLICE][w % DS_SLICE] = __uint_as_float((uint32_t)v); },
+                                         &rounds);
+    WM_DS_NOTE(l, 14, rounds);
     WM_DS_TRACE(l, 9);
     if (__builtin_amdgcn_readfirstlane(cancel_word) != 0) {
       // leave after this layer's phase B; the others see the status word in their next wait
@@ -529,10 +545,12 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
 #pragma unroll
     for (int w = 0; w < DS_CW; ++w)
       p += (sh.partb[w][0][lane] + sh.partb[w][1][lane]) + sh.partb[w][2][lane];
+    WM_DS_TRACE(l, 4);
     ll_put(&part_buf[(size_t)x * DS_H + j * DS_ROWS + lane], __float_as_uint(p), e_part);
     float y = 0.0f;
     ll_gather<DS_X>(part_buf + j * DS_ROWS, lane, DS_H, DS_X * DS_H, e_part, c.status, ok,
-                    [&](int i, uint64_t v) { y += __uint_as_float((uint32_t)v); });
+                    [&](int i, uint64_t v) { y += __uint_as_float((uint32_t)v); }, &rounds);
+    WM_DS_NOTE(l, 15, rounds);
     WM_DS_TRACE(l, 12);
     r_own += bf16_bits_to_f32(f32_to_bf16_bits(y));
     if (c.trace && x == 0) c.trace[(size_t)l * DS_H + j * DS_ROWS + lane] = r_own;
@@ -546,6 +564,7 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
                             ((uint64_t)sh.rpack[3 * lane + 1] << 16) | sh.rpack[3 * lane];
       ll_put_xcd<LOCAL>(&r_buf[j * DS_RW + lane], word);
     }
+    WM_DS_TRACE(l, 6);
     float ss = 0.0f, mx = 0.0f;
     ll_gather<(DS_J * DS_RW + 63) / 64, 16>(r_buf, lane, 64, DS_J * DS_RW, e_r, c.status, ok, [&](int w, uint64_t v) {
       const int jj = w / DS_RW, t = 3 * (w % DS_RW);
@@ -558,7 +577,8 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
           mx = fmaxf(mx, fabsf(rv));
         }
       }
-    });
+    }, &rounds);
+    WM_DS_NOTE(l, 7, rounds);
     ds_publish_norm(sh, ss, mx, lane);
     if (!ok) sh.failures = 1;
     WM_DS_TRACE(l, 13);
