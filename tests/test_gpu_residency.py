@@ -7,7 +7,7 @@
 - A pair with a negative id leaves its per-pair row as it was, so two calls over
   complementary masks give the one-call result bit for bit.
 - The cached-first acquire (ready experts computed while the missing ones are copied in)
-  gives the all-resident result bit for bit.
+  gives the all-resident result bit for bit, at a small shape and at the C2 expert shape.
 - The per-pair combine and the bf16 shared-expert MLP match the oracle's float64 closed
   forms (relative L2 <= 1e-2, max |err| <= 2e-2 max |ref|).
 """
@@ -155,6 +155,28 @@ def test_cached_first_acquire_equals_all_resident(device, tokens):
     _, ready = cache.acquire_ready(0, unique)                # now every one is resident
     assert all(ready)
     cache.wait_fills()
+
+
+def test_cached_first_at_decode_shape(device):
+    # The C2 expert shape (H 2048, I 512; 1.6 MB blobs). After a warm-up call, 20 of the
+    # step's experts are copied in from pinned host memory while the pairs of the resident
+    # ones run (the rocprofv3 trace of this test shows those kernels inside the copy's span).
+    files, experts, slots, K, tokens = 1, 48, 40, 10, 16
+    arrays, pool = make_pool(files, experts, 21, hidden=2048, inter=512)
+    cache = SlotCache(slots, 2048, 512, files, experts, pool, device)
+    table = S.experts_to_device(arrays[0], device)
+    cache.acquire(0, list(range(12)))
+    rng = np.random.default_rng(22)
+    for lo, hi in ((12, 18), (18, 38)):    # 6 missing experts, then 20
+        idx = np.stack([np.concatenate([rng.choice(12, 4, replace=False), rng.choice(np.arange(lo, hi), K - 4,
+                                                                                    replace=False)])
+                        for _ in range(tokens)]).astype(np.int32)
+        x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, 2048)), device)
+        it = torch.from_numpy(idx).to(device)
+        got = cache.experts_ready_first(0, x, it)
+        want = wa.experts_mxfp4(x, it, table)
+        assert torch.equal(got.cpu(), want.cpu())
+    assert cache.stats()["copies"] > 0
 
 
 def test_combine_pairs_matches_oracle(device):
