@@ -226,6 +226,16 @@ WM_EXPORT int wm_experts_fp8(const void* x, int32_t tokens, const int32_t* indic
 WM_EXPORT int wm_repack_prefill_fp8(const wm_fp8_experts* src, void* w13, void* w13_scales, void* w2,
                                     void* w2_scales, void* stream);
 
+/* ---- the prefill GEMMs' activation terms ------------------------------------
+ * x [rows, hidden] bf16 (hidden a multiple of 128, 16-byte aligned) -> out [rows][hidden/128]
+ * [208 bytes]: per 128-wide K step, for each of its four 32-value blocks the hi and the lo
+ * E2M3 terms (32 six-bit fields each, field k at bits 6k..6k+5), then the four hi and the
+ * four lo E8M0 exponents, then 8 bytes of padding (not written). hi = e2m3(x / 2^(s-127))
+ * with the block maximum in [4, 8) at that scale; lo the same for the exact residual. No
+ * counterpart in the reference: the format in which the grouped GEMMs read activations,
+ * exposed so callers can prepare rows once and so the tests can check it byte for byte. */
+WM_EXPORT int wm_split_rows_e2m3(const void* x, int32_t rows, int32_t hidden, void* out, void* stream);
+
 /* ---- measurement ----------------------------------------------------------
  * When enabled, every later wm_moe_mxfp4 / wm_experts_mxfp4 / wm_moe_fp8 / wm_experts_fp8
  * call that takes the grouped-GEMM path records events on its stream around the gate_up

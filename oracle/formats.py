@@ -200,3 +200,102 @@ def quantize_mxfp4_fp8(fp8: np.ndarray, inverse_scales_bf16: np.ndarray,
     s = np.repeat(np.repeat(s, FP8_BLOCK, axis=0), FP8_BLOCK, axis=1)
     values = bf16_round_f32((w * s).astype(np.float32))
     return _quantize_groups(values, rows, columns)
+
+
+# ---- E2M3 activation terms of the prefill GEMMs (no reference counterpart) ---------------
+# The grouped GEMMs feed bf16 activations to the scaled MFMA as two E2M3 (fp6) terms per
+# 32-value block, each with its own E8M0 exponent. This restates the device's split
+# (whallm_amd/csrc/grouped_mfma.hip split6_rows_kernel / fp6_terms32) byte for byte.
+# Pinned by the OCP MX definition of E2M3 (spacing and range, tests/test_oracle_formats.py),
+# brute-force nearest-value rounding, reconstruction bounds, and the device bytes on MI355X.
+
+SPLIT_STEP = 208   # bytes per row and 128-wide K step
+
+
+def e2m3_value(codes: np.ndarray) -> np.ndarray:
+    """6-bit E2M3 code -> float32: bit 5 sign, bits 3-4 exponent (bias 1), bits 0-2
+    mantissa; exponent 0 is subnormal (m / 8). Max 7.5, no inf or NaN (OCP MX v1.0)."""
+    c = np.asarray(codes, np.int64) & 63
+    e, m = (c >> 3) & 3, c & 7
+    mag = np.where(e == 0, m / 8.0, (1.0 + m / 8.0) * np.exp2(e - 1.0))
+    return np.where(c & 32, -mag, mag).astype(np.float32)
+
+
+E2M3_MAGNITUDES = e2m3_value(np.arange(32))
+
+
+def e2m3_encode(values: np.ndarray) -> np.ndarray:
+    """float -> E2M3 code: nearest magnitude, ties to the even code, saturating at 7.5;
+    the sign bit follows the value's sign, also when the magnitude rounds to 0."""
+    v = np.asarray(values, np.float64)
+    if np.isnan(v).any():
+        raise ValueError("E2M3 has no NaN")
+    mag = np.minimum(np.abs(v), 7.5)
+    d = np.abs(mag[..., None] - E2M3_MAGNITUDES.astype(np.float64))
+    best = d.min(-1, keepdims=True)
+    tie_codes = np.where(d == best, np.arange(32), 99)
+    even = np.where(tie_codes % 2 == 0, tie_codes, 99).min(-1)
+    code = np.where(even != 99, even, tie_codes.min(-1))
+    return (code | np.where(np.signbit(v), 32, 0)).astype(np.uint8)
+
+
+def e8m0_fp6_exponent(amax: np.ndarray) -> np.ndarray:
+    """Biased exponent s putting a block maximum into [4, 8) at scale 2^(s - 127), at least 1."""
+    e = (np.asarray(amax, np.float32).view(np.uint32) >> 23) & 0xFF
+    return np.maximum(e.astype(np.int64) - 2, 1)
+
+
+def e2m3_terms(block: np.ndarray) -> tuple[np.ndarray, np.ndarray, int, int]:
+    """One 32-value fp32 block -> (hi codes, lo codes, s_hi, s_lo): hi = e2m3(x / 2^(s_hi-127));
+    the residual r = x - value(hi) 2^(s_hi-127) (exact in fp32) gets its own exponent."""
+    x = np.asarray(block, np.float32)
+    s_hi = int(e8m0_fp6_exponent(np.abs(x).max()))
+    sc_hi = np.float32(2.0 ** (s_hi - 127))
+    hi = e2m3_encode(x / sc_hi)
+    r = (x - e2m3_value(hi) * sc_hi).astype(np.float32)
+    s_lo = int(e8m0_fp6_exponent(np.abs(r).max()))
+    lo = e2m3_encode(r / np.float32(2.0 ** (s_lo - 127)))
+    return hi, lo, s_hi, s_lo
+
+
+def pack_e2m3_fields(codes: np.ndarray) -> np.ndarray:
+    """32 six-bit codes -> 24 bytes, code k at bits 6k .. 6k + 5 (little-endian)."""
+    bits = 0
+    for k, c in enumerate(np.asarray(codes, np.uint8).reshape(32)):
+        bits |= int(c) << (6 * k)
+    return np.frombuffer(bits.to_bytes(24, "little"), np.uint8)
+
+
+def split_rows_e2m3(x: np.ndarray) -> np.ndarray:
+    """fp32 rows [R, H] (H a multiple of 128) -> [R, H/128, 208] bytes: per 128-wide step, the
+    4 blocks' hi fields (24 B) and lo fields (24 B) in turn, then the 4 hi exponents, the 4 lo
+    exponents; bytes 200-207 are padding (left unwritten by the device, zero here)."""
+    x = np.asarray(x, np.float32)
+    R, H = x.shape
+    if H % 128:
+        raise ValueError("split rows need H a multiple of 128")
+    out = np.zeros((R, H // 128, SPLIT_STEP), np.uint8)
+    for r in range(R):
+        for b in range(H // 32):
+            hi, lo, s_hi, s_lo = e2m3_terms(x[r, 32 * b:32 * b + 32])
+            st, o = out[r, b // 4], (b % 4) * 48
+            st[o:o + 24] = pack_e2m3_fields(hi)
+            st[o + 24:o + 48] = pack_e2m3_fields(lo)
+            st[192 + b % 4] = s_hi
+            st[196 + b % 4] = s_lo
+    return out
+
+
+def split_rows_value(split: np.ndarray, H: int) -> np.ndarray:
+    """Inverse view of split_rows_e2m3: hi 2^(s_hi-127) + lo 2^(s_lo-127) per value, float64."""
+    s = np.asarray(split, np.uint8)
+    R = s.shape[0]
+    out = np.zeros((R, H), np.float64)
+    for r in range(R):
+        for b in range(H // 32):
+            st, o = s[r, b // 4], (b % 4) * 48
+            for part, off, sb in ((0, o, 192), (1, o + 24, 196)):
+                bits = int.from_bytes(bytes(st[off:off + 24]), "little")
+                codes = np.array([(bits >> (6 * k)) & 63 for k in range(32)])
+                out[r, 32 * b:32 * b + 32] += e2m3_value(codes).astype(np.float64) * 2.0 ** (int(st[sb + b % 4]) - 127)
+    return out

@@ -152,3 +152,25 @@ def test_permute_skips_invalid_ids(device):
 def test_permute_empty(device):
     p = wa.permute(torch.empty(0, 10, dtype=torch.int32, device=device), 512)
     assert int(_np(p.tile_count)[0]) == 0 and int(_np(p.offsets)[-1]) == 0
+
+
+@pytest.mark.parametrize("H", [256, 640, 2048])
+def test_split_rows_e2m3_bit_exact(device, H):
+    # the prefill GEMMs' activation terms (wm_split_rows_e2m3) against the restatement, byte
+    # for byte (padding bytes 200-207 of each step excepted), on N(0,1) rows and on rows built
+    # to reach the edges: zero blocks, blocks many binades apart, tiny negatives that round to
+    # -0 beside a large value, exact E2M3 ties, and maxima that saturate (7.9 x 2^k).
+    rng = np.random.default_rng(H)
+    R = 24
+    x = rng.standard_normal((R, H)).astype(np.float32)
+    x[1] = 0.0
+    x[2] *= np.exp2(rng.integers(-40, 40, H // 32)).repeat(32).astype(np.float32)
+    x[3, ::32] = 50.0
+    x[3, 1::32] = -1e-3
+    x[4] = np.float32(2.0 ** -5) * np.tile(F.E2M3_MAGNITUDES[16:] + np.float32(0.125), H // 16)[:H]
+    x[5, ::32] = np.float32(7.9 * 2.0 ** 6)
+    x[6, :] = -x[6, :]
+    bits = F.bf16_round(x)
+    got = wa.split_rows_e2m3(S.bf16_bits_to_tensor(bits, device)).cpu().numpy()
+    want = F.split_rows_e2m3(F.bf16_bits_to_f32(bits))
+    np.testing.assert_array_equal(got[..., :200], want[..., :200])

@@ -163,3 +163,63 @@ def test_fp8_blocks_crop_and_reject():
         F.dequant_fp8_blocks(w, np.ones((1, 2), np.float32))
     with pytest.raises(ValueError):
         F.dequant_fp8_blocks(w, s.astype(np.float64))
+
+
+# ---- E2M3 activation terms of the prefill GEMMs -------------------------------------------
+
+def test_e2m3_is_the_ocp_format():
+    # OCP MX v1.0 E2M3: 1 sign, 2 exponent (bias 1), 3 mantissa bits, no inf / NaN. Checked
+    # through its shape, not its formula: 8 values per binade, the spacing of each binade,
+    # subnormals down to 1/8, maximum 7.5, and the sign bit negating.
+    m = F.E2M3_MAGNITUDES.astype(np.float64)
+    assert m[0] == 0 and np.all(np.diff(m) > 0) and m[-1] == 7.5
+    spacing = np.diff(m)
+    assert np.all(spacing[:16] == 0.125)          # up to 2: subnormals and the first binade
+    assert np.all(spacing[16:24] == 0.25)         # [2, 4]
+    assert np.all(spacing[24:] == 0.5)            # [4, 7.5]
+    assert list(m[[8, 16, 24]]) == [1.0, 2.0, 4.0]
+    np.testing.assert_array_equal(F.e2m3_value(np.arange(32) | 32), -F.E2M3_MAGNITUDES)
+
+
+def test_e2m3_encode_is_nearest_with_ties_to_even_and_saturates():
+    rng = np.random.default_rng(3)
+    v = np.concatenate([rng.uniform(-9, 9, 20000), (F.E2M3_MAGNITUDES[1:] + F.E2M3_MAGNITUDES[:-1]) / 2,
+                        -(F.E2M3_MAGNITUDES[1:] + F.E2M3_MAGNITUDES[:-1]) / 2, [7.74, 7.76, 100.0, -0.0, -0.01]])
+    codes = F.e2m3_encode(v)
+    got = np.abs(F.e2m3_value(codes).astype(np.float64))
+    a = np.minimum(np.abs(v), 7.5)
+    dist = np.abs(a[:, None] - F.E2M3_MAGNITUDES[None, :].astype(np.float64))
+    assert np.all(np.abs(a - got) == dist.min(1))                       # a nearest value
+    mid = np.isin(np.abs(v), (F.E2M3_MAGNITUDES[1:] + F.E2M3_MAGNITUDES[:-1]) / 2)
+    assert np.all((codes[mid] & 1) == 0)                                 # ties to the even code
+    assert F.e2m3_value(F.e2m3_encode(np.array([100.0])))[0] == 7.5        # saturation
+    assert np.all((codes & 32) == np.where(np.signbit(v), 32, 0))        # the sign always kept
+    np.testing.assert_array_equal(F.e2m3_encode(F.e2m3_value(np.arange(64))), np.arange(64))
+
+
+def test_split_rows_reconstruct_within_a_256th_of_the_block_maximum():
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((6, 256)) * np.exp2(rng.integers(-30, 30, (6, 1)))).astype(np.float32)
+    x[1, :32] = 0.0
+    rec = F.split_rows_value(F.split_rows_e2m3(x), 256)
+    for r in range(6):
+        for b in range(8):
+            blk = x[r, 32 * b:32 * b + 32].astype(np.float64)
+            err = np.abs(rec[r, 32 * b:32 * b + 32] - blk).max()
+            assert err <= np.abs(blk).max() / 256.0
+    # a single term would miss by up to 1/16 of the block maximum: the lo term carries weight
+    one = F.split_rows_e2m3(x)
+    one[:, :, 24:48] = one[:, :, 72:96] = one[:, :, 120:144] = one[:, :, 168:192] = 0
+    assert np.abs(F.split_rows_value(one, 256) - x).max() > np.abs(x).max() / 256.0
+
+
+def test_split_rows_exact_and_zero_blocks():
+    # values on the E2M3 grid at the block's scale are the hi term alone (lo fields 0)
+    blk = np.concatenate([F.E2M3_MAGNITUDES[16:], -F.E2M3_MAGNITUDES[16:]]) * np.float32(2.0 ** -3)
+    x = np.zeros((1, 128), np.float32)
+    x[0, :32] = blk
+    s = F.split_rows_e2m3(x)[0, 0]
+    hi, lo, s_hi, s_lo = F.e2m3_terms(blk)
+    assert s_hi == 127 - 3 and s_lo == 1 and not np.any(lo & 31)
+    np.testing.assert_array_equal(F.e2m3_value(hi) * np.float32(2.0 ** -3), blk)
+    assert list(s[192:200]) == [124, 1, 1, 1, 1, 1, 1, 1] and not np.any(s[48:192])   # zero blocks: exponent 1

@@ -110,6 +110,7 @@ _SIGNATURES = {
     "wm_mtp_workspace_size": (c_size_t, [c_int32, c_int32]),
     "wm_mtp_verify_greedy": (c_int, [_P, _P, c_int32, c_int32, _P, _P, c_size_t, _P]),
     "wm_mtp_verify_rejection": (c_int, [_P, _P, _P, c_int32, c_int32, _P, _P, _P, c_size_t, _P]),
+    "wm_split_rows_e2m3": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "wm_set_kernel_timing": (c_int, [c_int]),
     "wm_kernel_timing_ms": (c_int, [_P]),
     "wm_moe_decode_persistent_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, c_float,

@@ -166,11 +166,28 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){a, b}, bf16x2_t));
 }
 
+// The two wide scaled conversions, written as assembly with early-clobber outputs. Both
+// read their source and write their result over several passes, so a result register
+// that overlaps a source register still to be read corrupts that source: the compiler's
+// register allocator (ROCm 7.2) does allocate e.g. v[2:7] over a v[0:15] source, and on
+// MI355X that cleared bits of field 5 in most blocks. "=&v" keeps the result apart.
+__device__ __forceinline__ v6u_t cvt_2xpk16_fp6(const v16f_t& a, const v16f_t& b, float scale) {
+  v6u_t r;
+  asm("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(r) : "v"(a), "v"(b), "v"(scale));
+  return r;
+}
+typedef float v32f_t __attribute__((ext_vector_type(32)));
+__device__ __forceinline__ v32f_t cvt_pk32_f32_fp6(const v6u_t& f, float scale) {
+  v32f_t r;
+  asm("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(r) : "v"(f), "v"(scale));
+  return r;
+}
+
 // The hi and lo E2M3 terms of one 32-value block (v in K order) with the hardware
 // conversions: v_cvt_scalef32_2xpk16_fp6_f32 packs e2m3(x / scale) of its two 16-value
 // operands interleaved (field 2i from the first, 2i + 1 from the second), rounding to
-// nearest even and saturating at 7.5; v_cvt_scalef32_pk32_f32_fp6 gives field * scale back,
-// so the residual v - hi is exact.
+// nearest even and saturating at 7.5 (a negative value that rounds to zero keeps its sign
+// bit); v_cvt_scalef32_pk32_f32_fp6 gives field * scale back, so the residual v - hi is exact.
 __device__ __forceinline__ void fp6_terms32(const float (&v)[32], v6u_t& hi, v6u_t& lo, int& s_hi, int& s_lo) {
   float amax = 0.0f;
 #pragma unroll
@@ -183,8 +200,8 @@ __device__ __forceinline__ void fp6_terms32(const float (&v)[32], v6u_t& hi, v6u
     ev[m] = v[2 * m];
     od[m] = v[2 * m + 1];
   }
-  hi = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, sc_hi);
-  const auto back = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(hi, sc_hi);
+  hi = cvt_2xpk16_fp6(ev, od, sc_hi);
+  const v32f_t back = cvt_pk32_f32_fp6(hi, sc_hi);
   float rmax = 0.0f;
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
@@ -193,7 +210,7 @@ __device__ __forceinline__ void fp6_terms32(const float (&v)[32], v6u_t& hi, v6u
     rmax = fmaxf(rmax, fmaxf(fabsf(ev[m]), fabsf(od[m])));
   }
   s_lo = fp6_exponent(rmax);
-  lo = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, pow2_biased(s_lo));
+  lo = cvt_2xpk16_fp6(ev, od, pow2_biased(s_lo));
 }
 
 // x [rows, H] bf16 -> split rows [rows][H/128][208 bytes]. One lane per 32-value block.
@@ -228,8 +245,17 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
   dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
   dst[1] = make_uint4(hi[4], hi[5], lo[0], lo[1]);
   dst[2] = make_uint4(lo[2], lo[3], lo[4], lo[5]);
-  step[192 + blk % 4] = (uint8_t)s_hi;
-  step[196 + blk % 4] = (uint8_t)s_lo;
+  // the step's four blocks are lanes 4q .. 4q + 3 (blocks is a multiple of 4): the first
+  // lane of the quad gathers their scale bytes and stores them as two words
+  const uint32_t sc = (uint32_t)s_hi | ((uint32_t)s_lo << 8);
+  const uint32_t q1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)sc, 0x55, 0xf, 0xf, false);  // quad_perm [1,1,1,1]
+  const uint32_t q2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)sc, 0xAA, 0xf, 0xf, false);  // [2,2,2,2]
+  const uint32_t q3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)sc, 0xFF, 0xf, 0xf, false);  // [3,3,3,3]
+  if (blk % 4 == 0) {
+    const uint32_t w_hi = (sc & 0xffu) | ((q1 & 0xffu) << 8) | ((q2 & 0xffu) << 16) | ((q3 & 0xffu) << 24);
+    const uint32_t w_lo = (sc >> 8) | ((q1 >> 8) << 8) | ((q2 >> 8) << 16) | ((q3 >> 8) << 24);
+    *reinterpret_cast<uint2*>(step + 192) = make_uint2(w_hi, w_lo);
+  }
   if (g) {
     const uint4* gs = reinterpret_cast<const uint4*>(g + blk * 32);
     float dot = 0.0f;
@@ -243,7 +269,11 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
         dot = fmaf(v[8 * q + 2 * j + 1], bf16_bits_to_f32(w[j] >> 16), dot);
       }
     }
-    for (int off = 1; off < blocks; off <<= 1) dot += __shfl_xor(dot, off, 64);
+    if (blocks == 64) {
+      dot = segment_sum<64>(dot);  // the row is the whole wave: DPP and lane reads, no LDS
+    } else {
+      for (int off = 1; off < blocks; off <<= 1) dot += __shfl_xor(dot, off, 64);
+    }
     if (blk == 0) gate[row] = 1.0f / (1.0f + __expf(-dot));
   }
 }
@@ -1338,6 +1368,20 @@ WM_EXPORT int wm_repack_prefill_fp8(const wm_fp8_experts* src, void* w13, void* 
     };
     launch(src->w13, src->w13_scales, src->w13_stride, src->w13_scales_stride, 2 * I, H, w13, w13_scales);
     launch(src->w2, src->w2_scales, src->w2_stride, src->w2_scales_stride, H, I, w2, w2_scales);
+  });
+}
+
+WM_EXPORT int wm_split_rows_e2m3(const void* x, int32_t rows, int32_t hidden, void* out, void* stream) {
+  return wm::guarded([&] {
+    if (rows < 0 || hidden < 128 || hidden % 128) wm::fail("wm_split_rows_e2m3: hidden must be a positive multiple of 128");
+    if (rows == 0) return;
+    if (!x || !out) wm::fail("wm_split_rows_e2m3: null pointer");
+    if ((uintptr_t)x % 16 || (uintptr_t)out % 16) wm::fail("wm_split_rows_e2m3: x and out must be 16-byte aligned");
+    const int64_t jobs = (int64_t)rows * (hidden / 32);
+    hipLaunchKernelGGL(wm::mf::split6_rows_kernel, dim3((unsigned)((jobs + 255) / 256)), dim3(256), 0,
+                       wm::as_stream(stream), (const uint16_t*)x, (int)rows, (int)hidden, (uint8_t*)out, nullptr,
+                       nullptr);
+    wm::check_launch("split_rows_e2m3");
   });
 }
 

@@ -3,20 +3,25 @@
 // Native/QwenNative/engine.mm:2104-2126, or calls mlx-lm _gather_sort,
 // qwen4_exp.py:865-868).
 //
-//   count   : one wave per chunk of 1024 pairs counts its experts in LDS
-//   scan    : one workgroup turns the per-chunk counts into per-chunk prefixes,
-//             per-expert offsets, and the (expert, first row) tile list
-//   scatter : one wave per chunk walks its pairs in order, 64 at a time; lanes
-//             with the same expert find each other with ballots, so every pair's
-//             row is base + its rank among earlier same-expert pairs: stable.
+//   count   : one wave per chunk of 256 pairs counts its experts in LDS
+//   colscan : a workgroup per 64 experts turns each expert's column of chunk counts into
+//             exclusive prefixes over the chunks (16 segments of chunks per expert, in
+//             parallel), and writes each expert's total
+//   scatter : one wave per chunk computes the experts' offsets (an exclusive scan of the
+//             totals), walks its pairs in order, 64 at a time; lanes with the same expert
+//             find each other with ballots, so every pair's row is base + its rank among
+//             earlier same-expert pairs: stable. Wave 0 also writes the offsets and the
+//             (expert, first row) tile list.
 //
 // Invalid expert ids (< 0 or >= E) are left out of every list; their inverse is -1.
 #include "wm_common.h"
 
 namespace wm {
 
-constexpr int PERMUTE_CHUNK = 1024;
+constexpr int PERMUTE_CHUNK = 256;
 constexpr int PERMUTE_MAX_EXPERTS = 1024;
+constexpr int SCAN_EXPERTS = 64;  // experts per colscan workgroup (one per lane)
+constexpr int SCAN_SEGS = 16;     // chunk segments per expert (one per wave)
 
 __global__ void __launch_bounds__(64) permute_count_kernel(const int32_t* __restrict__ idx, int64_t pairs, int experts,
                                                           int32_t* __restrict__ chunk_counts) {
@@ -34,43 +39,17 @@ __global__ void __launch_bounds__(64) permute_count_kernel(const int32_t* __rest
   for (int e = lane; e < experts; e += 64) chunk_counts[chunk * experts + e] = counts[e];
 }
 
-// Inclusive prefix sum over the 1024 threads of the block (wave shuffles, then the 16
-// wave totals). Every thread of the block must call it.
-__device__ __forceinline__ int32_t block_inclusive_scan(int32_t v, int32_t* wave_total) {
-  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int32_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
-  if (lane == 63) wave_total[wave] = v;
-  __syncthreads();
-  int32_t before = 0;
-  for (int w = 0; w < wave; ++w) before += wave_total[w];
-  __syncthreads();  // wave_total is reused by the next call
-  return v + before;
-}
-
-// One workgroup of 1024 threads. Thread t = s * pad + e (pad = E rounded up to a power of
-// two) owns chunk segment s of expert e, so each expert's chunk counts are read by
-// 1024 / pad threads, 16 independent loads at a time. chunk_counts[c][e] becomes the
-// number of expert-e pairs in chunks before c (the scatter adds offsets[e]); offsets,
-// tile_count and the (expert, first row) tile list come from block scans over experts.
-__global__ void __launch_bounds__(1024) permute_scan_kernel(int32_t* __restrict__ chunk_counts, int64_t chunks,
-                                                           int experts, int tile_rows, int32_t* __restrict__ offsets,
-                                                           int32_t* __restrict__ tiles,
-                                                           int32_t* __restrict__ tile_count) {
-  __shared__ int32_t part[1024];
-  __shared__ int32_t row_end[PERMUTE_MAX_EXPERTS];   // inclusive scan of the expert totals
-  __shared__ int32_t tile_end[PERMUTE_MAX_EXPERTS];  // inclusive scan of the expert tile counts
-  __shared__ int32_t wave_total[16];
-  const int t = threadIdx.x;
-  const int pad = experts > 1 ? 1 << (32 - __clz(experts - 1)) : 1;
-  const int segs = 1024 / pad;
-  const int e = t % pad, s = t / pad;
+// Workgroup b: experts 64 b + lane; wave w: chunks [chunks w / 16, chunks (w + 1) / 16).
+// chunk_counts[c][e] becomes the number of expert-e pairs in chunks before c; totals[e]
+// the expert's pairs.
+__global__ void __launch_bounds__(1024) permute_colscan_kernel(int32_t* __restrict__ chunk_counts, int64_t chunks,
+                                                              int experts, int32_t* __restrict__ totals) {
+  __shared__ int32_t part[SCAN_SEGS][SCAN_EXPERTS];
+  const int lane = threadIdx.x % 64, s = threadIdx.x / 64;
+  const int e = blockIdx.x * SCAN_EXPERTS + lane;
   const bool live = e < experts;
-  const int64_t c0 = chunks * s / segs, c1 = chunks * (s + 1) / segs;
-  constexpr int BATCH = 16;
+  const int64_t c0 = chunks * s / SCAN_SEGS, c1 = chunks * (s + 1) / SCAN_SEGS;
+  constexpr int BATCH = 8;
   int32_t sum = 0;
   if (live) {
     for (int64_t c = c0; c < c1; c += BATCH) {
@@ -81,11 +60,12 @@ __global__ void __launch_bounds__(1024) permute_scan_kernel(int32_t* __restrict_
       for (int q = 0; q < BATCH; ++q) sum += v[q];
     }
   }
-  part[t] = sum;
+  part[s][lane] = sum;
   __syncthreads();
   int32_t before = 0, total = 0;
-  for (int q = 0; q < segs; ++q) {
-    const int32_t v = part[q * pad + e];
+#pragma unroll
+  for (int q = 0; q < SCAN_SEGS; ++q) {
+    const int32_t v = part[q][lane];
     before += q < s ? v : 0;
     total += v;
   }
@@ -102,48 +82,70 @@ __global__ void __launch_bounds__(1024) permute_scan_kernel(int32_t* __restrict_
           running += v[q];
         }
     }
+    if (s == 0) totals[e] = total;
   }
-  __syncthreads();
-  if (s == 0) part[e] = live ? total : 0;  // expert totals (every thread has read part above)
-  __syncthreads();
-  const int32_t mine = t < experts ? part[t] : 0;
-  const int32_t my_tiles = (mine + tile_rows - 1) / tile_rows;
-  const int32_t rows_incl = block_inclusive_scan(mine, wave_total);
-  const int32_t tiles_incl = block_inclusive_scan(my_tiles, wave_total);
-  if (t < experts) {
-    row_end[t] = rows_incl;
-    tile_end[t] = tiles_incl;
-    offsets[t] = rows_incl - mine;
-    if (t == experts - 1) {
-      offsets[experts] = rows_incl;
-      tile_count[0] = tiles_incl;
+}
+
+// Exclusive scan of n values (n <= 64 * 16) held lane-major by one wave: lane l owns
+// entries [l * per, (l + 1) * per). Writes the exclusive prefixes to out[] (LDS) and
+// returns the total in every lane.
+template <typename Value>
+__device__ __forceinline__ int32_t wave_exclusive_scan(int n, int lane, Value value, int32_t* out) {
+  const int per = (n + 63) / 64;
+  int32_t mine = 0;
+  for (int q = 0; q < per; ++q) {
+    const int i = lane * per + q;
+    if (i < n) mine += value(i);
+  }
+  int32_t incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  int32_t run = incl - mine;
+  for (int q = 0; q < per; ++q) {
+    const int i = lane * per + q;
+    if (i < n) {
+      out[i] = run;
+      run += value(i);
     }
   }
-  __syncthreads();
-  // tile i belongs to the first expert whose inclusive tile count exceeds i
-  const int32_t n_tiles = tile_end[experts - 1];
-  for (int32_t i = t; i < n_tiles; i += 1024) {
-    int lo = 0, hi = experts - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi) / 2;
-      if (tile_end[mid] > i) hi = mid; else lo = mid + 1;
-    }
-    const int32_t first_tile = tile_end[lo] - (row_end[lo] - (lo ? row_end[lo - 1] : 0) + tile_rows - 1) / tile_rows;
-    const int32_t row_base = lo ? row_end[lo - 1] : 0;
-    tiles[2 * i] = lo;
-    tiles[2 * i + 1] = row_base + (i - first_tile) * tile_rows;
-  }
+  return __shfl(incl, 63, 64);
 }
 
 __global__ void __launch_bounds__(64) permute_scatter_kernel(const int32_t* __restrict__ idx, int64_t pairs,
                                                             int experts, const int32_t* __restrict__ chunk_base,
-                                                            const int32_t* __restrict__ offsets,
-                                                            int32_t* __restrict__ order,
-                                                            int32_t* __restrict__ inverse) {
+                                                            const int32_t* __restrict__ totals, int tile_rows,
+                                                            int32_t* __restrict__ order, int32_t* __restrict__ inverse,
+                                                            int32_t* __restrict__ offsets,
+                                                            int32_t* __restrict__ tiles,
+                                                            int32_t* __restrict__ tile_count) {
   __shared__ int32_t base[PERMUTE_MAX_EXPERTS];
-  int lane = threadIdx.x;
-  int64_t chunk = blockIdx.x;
-  for (int e = lane; e < experts; e += 64) base[e] = chunk_base[chunk * experts + e] + offsets[e];
+  __shared__ int32_t first_tile[PERMUTE_MAX_EXPERTS];
+  const int lane = threadIdx.x;
+  const int64_t chunk = blockIdx.x;
+  const int32_t rows = wave_exclusive_scan(experts, lane, [&](int e) { return totals[e]; }, base);
+  __syncthreads();
+  if (chunk == 0) {
+    // offsets and the tile list: expert e's tiles are first_tile[e] .. + ceil(total / tile_rows)
+    const int32_t n_tiles = wave_exclusive_scan(
+        experts, lane, [&](int e) { return (totals[e] + tile_rows - 1) / tile_rows; }, first_tile);
+    __syncthreads();
+    for (int e = lane; e < experts; e += 64) {
+      offsets[e] = base[e];
+      const int32_t n = (totals[e] + tile_rows - 1) / tile_rows;
+      for (int32_t q = 0; q < n; ++q) {
+        tiles[2 * (first_tile[e] + q)] = e;
+        tiles[2 * (first_tile[e] + q) + 1] = base[e] + q * tile_rows;
+      }
+    }
+    if (lane == 0) {
+      offsets[experts] = rows;
+      tile_count[0] = n_tiles;
+    }
+  }
+  for (int e = lane; e < experts; e += 64) base[e] += chunk_base[chunk * experts + e];
   __syncthreads();
   int bits = 32 - __clz(experts);  // enough bits to tell experts (and the sentinel `experts`) apart
   int64_t begin = chunk * PERMUTE_CHUNK, end = min<int64_t>(pairs, begin + PERMUTE_CHUNK);
@@ -179,7 +181,8 @@ extern "C" {
 
 WM_EXPORT size_t wm_permute_workspace_size(int64_t pairs, int32_t experts) {
   int64_t chunks = (pairs + PERMUTE_CHUNK - 1) / PERMUTE_CHUNK;
-  return (size_t)(chunks > 0 ? chunks : 1) * (size_t)(experts > 0 ? experts : 1) * sizeof(int32_t);
+  const size_t e = (size_t)(experts > 0 ? experts : 1);
+  return ((size_t)(chunks > 0 ? chunks : 1) * e + e) * sizeof(int32_t);  // chunk counts, then totals
 }
 
 WM_EXPORT int wm_permute(const int32_t* indices, int64_t pairs, int32_t experts, int32_t tile_rows, int32_t* order,
@@ -194,19 +197,19 @@ WM_EXPORT int wm_permute(const int32_t* indices, int64_t pairs, int32_t experts,
       fail("wm_permute: null pointer");
     int64_t chunks = (pairs + PERMUTE_CHUNK - 1) / PERMUTE_CHUNK;
     int32_t* counts = (int32_t*)workspace;
+    int32_t* totals = counts + (size_t)(chunks > 0 ? chunks : 1) * experts;
     hipStream_t s = as_stream(stream);
     if (chunks > 0) {
       hipLaunchKernelGGL(permute_count_kernel, dim3((unsigned)chunks), dim3(64), 0, s, indices, pairs, experts, counts);
       check_launch("permute_count");
     }
-    hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(1024), 0, s, counts, chunks, experts, tile_rows, offsets,
-                       tiles, tile_count);
-    check_launch("permute_scan");
-    if (chunks > 0) {
-      hipLaunchKernelGGL(permute_scatter_kernel, dim3((unsigned)chunks), dim3(64), 0, s, indices, pairs, experts,
-                         counts, offsets, order, inverse);
-      check_launch("permute_scatter");
-    }
+    hipLaunchKernelGGL(permute_colscan_kernel, dim3((unsigned)((experts + SCAN_EXPERTS - 1) / SCAN_EXPERTS)),
+                       dim3(64 * SCAN_SEGS), 0, s, counts, chunks, experts, totals);
+    check_launch("permute_colscan");
+    // with no pairs one scatter wave still writes the (empty) offsets and tile count
+    hipLaunchKernelGGL(permute_scatter_kernel, dim3((unsigned)(chunks > 0 ? chunks : 1)), dim3(64), 0, s, indices,
+                       pairs, experts, counts, totals, tile_rows, order, inverse, offsets, tiles, tile_count);
+    check_launch("permute_scatter");
   });
 }
 

@@ -28,7 +28,7 @@ __global__ void __launch_bounds__(64) route_softmax_topk_kernel(const float* __r
     weights[(int64_t)t * k + lane] = w;
   }
   if (probabilities) {
-    float top = row[__shfl(sel, 0, 64)];
+    float top = row[__builtin_amdgcn_readlane(sel, 0)];
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
@@ -105,7 +105,7 @@ __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restric
     float gval;
     wave_topk<1>(gs, n_groups, topk_groups, lane, gsel, gval);
     uint64_t keep = 0;
-    for (int j = 0; j < topk_groups; ++j) keep |= 1ull << __shfl(gsel, j, 64);
+    for (int j = 0; j < topk_groups; ++j) keep |= 1ull << __builtin_amdgcn_readlane(gsel, j);
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;

@@ -80,14 +80,34 @@ __device__ __forceinline__ bool topk_better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-// Wave-wide arg-max of (v, i); every lane gets the winner.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+
+// Wave-wide arg-max of (v, i); every lane gets the winner. Inside each 16-lane row the
+// candidates meet through DPP moves (pairs, quads, row halves mirrored, rows mirrored: after
+// each step every lane holds the best of its group), then the four rows' winners are read
+// into scalar registers and compared in row order. (value, index) is a strict total order
+// for non-NaN values, so the winner does not depend on the order of the comparisons.
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    float ov = __shfl_xor(v, offset, 64);
-    int oi = __shfl_xor(i, offset, 64);
+  auto take = [&](float ov, int oi) {
     if (topk_better(ov, oi, v, i)) { v = ov; i = oi; }
+  };
+  take(dpp_f<0xB1>(v), dpp_i<0xB1>(i));    // quad_perm [1,0,3,2]
+  take(dpp_f<0x4E>(v), dpp_i<0x4E>(i));    // quad_perm [2,3,0,1]
+  take(dpp_f<0x141>(v), dpp_i<0x141>(i));  // row_half_mirror
+  take(dpp_f<0x140>(v), dpp_i<0x140>(i));  // row_mirror
+  float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+  for (int row = 1; row < 4; ++row) {
+    const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * row));
+    const int ri = __builtin_amdgcn_readlane(i, 16 * row);
+    if (topk_better(rv, ri, bv, bi)) { bv = rv; bi = ri; }
   }
+  v = bv;
+  i = bi;
 }
 
 // k rounds of arg-max over vals (entries with e >= experts are ignored). Lane j < k
@@ -126,7 +146,8 @@ __device__ __forceinline__ void wave_route_softmax(const float* __restrict__ row
   }
   float sel_val;
   wave_topk<PER_LANE>(vals, experts, k, lane, sel, sel_val);
-  float top = __shfl(sel_val, 0, 64);  // the first selection is the row maximum
+  // the first selection (lane 0) is the row maximum
+  float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sel_val), 0));
   float mine = lane < k ? __expf(sel_val - top) : 0.0f;
   float denom;
   float full = 0.0f;

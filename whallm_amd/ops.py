@@ -115,6 +115,19 @@ class MXFP4Experts:
         return (self.gate_up, self.gate_up_scales, self.down, self.down_scales, self.slots)
 
 
+def split_rows_e2m3(x: torch.Tensor) -> torch.Tensor:
+    """bf16 rows [.., H] (H a multiple of 128) -> uint8 [rows, H/128, 208]: the two E2M3 terms
+    per 32 values with their E8M0 exponents, as the prefill GEMMs read activations
+    (wm_split_rows_e2m3; bytes 200-207 of each step are padding and left unwritten)."""
+    device = _require_device(x)
+    x = _contig(x, torch.bfloat16, "x")
+    H = x.shape[-1]
+    rows = x.numel() // H if H else 0
+    out = torch.empty(rows, H // 128, 208, dtype=torch.uint8, device=device)
+    _lib.call("wm_split_rows_e2m3", _ptr(x), rows, H, _ptr(out), _stream(device))
+    return out
+
+
 def prefill_layout(experts):
     """A copy of ``experts`` (MXFP4Experts or FP8Experts) in the prefill tile layout
     (wm_repack_prefill_mxfp4 / wm_repack_prefill_fp8): one expert after another (``slots``
