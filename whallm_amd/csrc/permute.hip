@@ -7,11 +7,11 @@
 //   colscan : a workgroup per 64 experts turns each expert's column of chunk counts into
 //             exclusive prefixes over the chunks (16 segments of chunks per expert, in
 //             parallel), and writes each expert's total
-//   scatter : one wave per chunk computes the experts' offsets (an exclusive scan of the
-//             totals), walks its pairs in order, 64 at a time; lanes with the same expert
-//             find each other with ballots, so every pair's row is base + its rank among
-//             earlier same-expert pairs: stable. Wave 0 also writes the offsets and the
-//             (expert, first row) tile list.
+//   offsets : one workgroup scans the expert totals into offsets[E + 1] and the
+//             (expert, first row) tile list
+//   scatter : one wave per chunk walks its pairs in order, 64 at a time; lanes with the
+//             same expert find each other with ballots, so every pair's row is base + its
+//             rank among earlier same-expert pairs: stable.
 //
 // Invalid expert ids (< 0 or >= E) are left out of every list; their inverse is -1.
 #include "wm_common.h"
@@ -86,66 +86,59 @@ __global__ void __launch_bounds__(1024) permute_colscan_kernel(int32_t* __restri
   }
 }
 
-// Exclusive scan of n values (n <= 64 * 16) held lane-major by one wave: lane l owns
-// entries [l * per, (l + 1) * per). Writes the exclusive prefixes to out[] (LDS) and
-// returns the total in every lane.
-template <typename Value>
-__device__ __forceinline__ int32_t wave_exclusive_scan(int n, int lane, Value value, int32_t* out) {
-  const int per = (n + 63) / 64;
-  int32_t mine = 0;
-  for (int q = 0; q < per; ++q) {
-    const int i = lane * per + q;
-    if (i < n) mine += value(i);
-  }
-  int32_t incl = mine;
+// Inclusive prefix sum over the 1024 threads of the block (wave shuffles, then the 16
+// wave totals). Every thread of the block must call it.
+__device__ __forceinline__ int32_t block_inclusive_scan(int32_t v, int32_t* wave_total) {
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    const int32_t o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
+    const int32_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
   }
-  int32_t run = incl - mine;
-  for (int q = 0; q < per; ++q) {
-    const int i = lane * per + q;
-    if (i < n) {
-      out[i] = run;
-      run += value(i);
+  if (lane == 63) wave_total[wave] = v;
+  __syncthreads();
+  int32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += wave_total[w];
+  __syncthreads();  // wave_total is reused by the next call
+  return v + before;
+}
+
+// One workgroup of 1024 threads, thread e = expert e: offsets[e] (exclusive scan of the
+// totals), offsets[E], the tile count, and expert e's tiles (expert, first row) at its
+// place in the list.
+__global__ void __launch_bounds__(1024) permute_offsets_kernel(const int32_t* __restrict__ totals, int experts,
+                                                              int tile_rows, int32_t* __restrict__ offsets,
+                                                              int32_t* __restrict__ tiles,
+                                                              int32_t* __restrict__ tile_count) {
+  __shared__ int32_t wave_total[16];
+  const int e = threadIdx.x;
+  const int32_t mine = e < experts ? totals[e] : 0;
+  const int32_t my_tiles = (mine + tile_rows - 1) / tile_rows;
+  const int32_t rows_incl = block_inclusive_scan(mine, wave_total);
+  const int32_t tiles_incl = block_inclusive_scan(my_tiles, wave_total);
+  if (e < experts) {
+    const int32_t row0 = rows_incl - mine, tile0 = tiles_incl - my_tiles;
+    offsets[e] = row0;
+    for (int32_t q = 0; q < my_tiles; ++q) {
+      tiles[2 * (tile0 + q)] = e;
+      tiles[2 * (tile0 + q) + 1] = row0 + q * tile_rows;
+    }
+    if (e == experts - 1) {
+      offsets[experts] = rows_incl;
+      tile_count[0] = tiles_incl;
     }
   }
-  return __shfl(incl, 63, 64);
 }
 
 __global__ void __launch_bounds__(64) permute_scatter_kernel(const int32_t* __restrict__ idx, int64_t pairs,
                                                             int experts, const int32_t* __restrict__ chunk_base,
-                                                            const int32_t* __restrict__ totals, int tile_rows,
-                                                            int32_t* __restrict__ order, int32_t* __restrict__ inverse,
-                                                            int32_t* __restrict__ offsets,
-                                                            int32_t* __restrict__ tiles,
-                                                            int32_t* __restrict__ tile_count) {
+                                                            const int32_t* __restrict__ offsets,
+                                                            int32_t* __restrict__ order,
+                                                            int32_t* __restrict__ inverse) {
   __shared__ int32_t base[PERMUTE_MAX_EXPERTS];
-  __shared__ int32_t first_tile[PERMUTE_MAX_EXPERTS];
   const int lane = threadIdx.x;
   const int64_t chunk = blockIdx.x;
-  const int32_t rows = wave_exclusive_scan(experts, lane, [&](int e) { return totals[e]; }, base);
-  __syncthreads();
-  if (chunk == 0) {
-    // offsets and the tile list: expert e's tiles are first_tile[e] .. + ceil(total / tile_rows)
-    const int32_t n_tiles = wave_exclusive_scan(
-        experts, lane, [&](int e) { return (totals[e] + tile_rows - 1) / tile_rows; }, first_tile);
-    __syncthreads();
-    for (int e = lane; e < experts; e += 64) {
-      offsets[e] = base[e];
-      const int32_t n = (totals[e] + tile_rows - 1) / tile_rows;
-      for (int32_t q = 0; q < n; ++q) {
-        tiles[2 * (first_tile[e] + q)] = e;
-        tiles[2 * (first_tile[e] + q) + 1] = base[e] + q * tile_rows;
-      }
-    }
-    if (lane == 0) {
-      offsets[experts] = rows;
-      tile_count[0] = n_tiles;
-    }
-  }
-  for (int e = lane; e < experts; e += 64) base[e] += chunk_base[chunk * experts + e];
+  for (int e = lane; e < experts; e += 64) base[e] = chunk_base[chunk * experts + e] + offsets[e];
   __syncthreads();
   int bits = 32 - __clz(experts);  // enough bits to tell experts (and the sentinel `experts`) apart
   int64_t begin = chunk * PERMUTE_CHUNK, end = min<int64_t>(pairs, begin + PERMUTE_CHUNK);
@@ -206,10 +199,14 @@ WM_EXPORT int wm_permute(const int32_t* indices, int64_t pairs, int32_t experts,
     hipLaunchKernelGGL(permute_colscan_kernel, dim3((unsigned)((experts + SCAN_EXPERTS - 1) / SCAN_EXPERTS)),
                        dim3(64 * SCAN_SEGS), 0, s, counts, chunks, experts, totals);
     check_launch("permute_colscan");
-    // with no pairs one scatter wave still writes the (empty) offsets and tile count
-    hipLaunchKernelGGL(permute_scatter_kernel, dim3((unsigned)(chunks > 0 ? chunks : 1)), dim3(64), 0, s, indices,
-                       pairs, experts, counts, totals, tile_rows, order, inverse, offsets, tiles, tile_count);
-    check_launch("permute_scatter");
+    hipLaunchKernelGGL(permute_offsets_kernel, dim3(1), dim3(1024), 0, s, totals, experts, tile_rows, offsets, tiles,
+                       tile_count);
+    check_launch("permute_offsets");
+    if (chunks > 0) {
+      hipLaunchKernelGGL(permute_scatter_kernel, dim3((unsigned)chunks), dim3(64), 0, s, indices, pairs, experts, counts,
+                         offsets, order, inverse);
+      check_launch("permute_scatter");
+    }
   });
 }
 

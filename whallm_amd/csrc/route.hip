@@ -11,13 +11,16 @@ bool linear_bf16_mfma(const void* x, const void* w, int tokens, int hidden, int 
 
 constexpr int ROUTE_MAX_K = 32;
 
+// The router kernels run a wave per token, four tokens to a 256-thread block. At 16K tokens
+// x 512 experts they are bound by VALU and scalar issue (k rounds of a per-lane scan and a
+// wave arg-max), not by the 33.5 MB of logits.
 template <int PER_LANE>
-__global__ void __launch_bounds__(64) route_softmax_topk_kernel(const float* __restrict__ logits, int tokens,
-                                                               int experts, int k, int norm,
-                                                               int32_t* __restrict__ indices,
-                                                               float* __restrict__ weights,
-                                                               float* __restrict__ probabilities) {
-  int t = blockIdx.x, lane = threadIdx.x;
+__global__ void __launch_bounds__(256) route_softmax_topk_kernel(const float* __restrict__ logits, int tokens,
+                                                                int experts, int k, int norm,
+                                                                int32_t* __restrict__ indices,
+                                                                float* __restrict__ weights,
+                                                                float* __restrict__ probabilities) {
+  const int t = blockIdx.x * 4 + threadIdx.x / 64, lane = threadIdx.x % 64;
   if (t >= tokens) return;
   const float* row = logits + (int64_t)t * experts;
   int sel;
@@ -44,15 +47,17 @@ __device__ __forceinline__ float score_fn(float l, int func) {
 }
 
 template <int PER_LANE>
-__global__ void __launch_bounds__(64) route_scored_kernel(const float* __restrict__ logits,
-                                                         const float* __restrict__ bias, int tokens, int experts,
-                                                         int k, int func, float route_scale, int norm, int n_groups,
-                                                         int topk_groups, int32_t* __restrict__ indices,
-                                                         float* __restrict__ weights) {
-  __shared__ float biased_lds[64 * PER_LANE];
-  __shared__ float score_lds[64 * PER_LANE];
-  int t = blockIdx.x, lane = threadIdx.x;
+__global__ void __launch_bounds__(256) route_scored_kernel(const float* __restrict__ logits,
+                                                          const float* __restrict__ bias, int tokens, int experts,
+                                                          int k, int func, float route_scale, int norm, int n_groups,
+                                                          int topk_groups, int32_t* __restrict__ indices,
+                                                          float* __restrict__ weights) {
+  __shared__ float biased_all[4][64 * PER_LANE];
+  __shared__ float score_all[4][64 * PER_LANE];
+  const int wave = threadIdx.x / 64, t = blockIdx.x * 4 + wave, lane = threadIdx.x % 64;
   if (t >= tokens) return;
+  float* biased_lds = biased_all[wave];  // each wave's own rows: LDS is shared only within the wave
+  float* score_lds = score_all[wave];
   const float* row = logits + (int64_t)t * experts;
   float vals[PER_LANE];
   float top = 0.0f, denom = 1.0f;
@@ -87,7 +92,11 @@ __global__ void __launch_bounds__(64) route_scored_kernel(const float* __restric
       vals[r] = -INFINITY;
     }
   }
-  __syncthreads();
+  // a wave's LDS operations complete in order; the fence keeps the compiler from moving
+  // the reads below above the writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (n_groups > 1) {
     int gsize = experts / n_groups;
     // A group's score is the sum of its two largest biased scores (DeepSeek-V3 rule).
@@ -148,30 +157,47 @@ __device__ __forceinline__ float dot8_bf16x(uint4 a, uint4 b, float acc) {
   return dot2_bf16(bits_to_bf16x2(a.w), bits_to_bf16x2(b.w), acc);
 }
 
-// Few tokens (<= TMAX): a wave per output row streams the row once in 16-byte chunks and
-// dots every chunk with all tokens' x (which stay in the caches), so each weight byte is
-// read once however many tokens there are. grid: ceil(outputs / 4), 4 waves a block.
+// Few tokens (<= TMAX): a wave takes LR_ROWS output rows and streams them once in 16-byte
+// chunks; each chunk of every token's x, loaded once per wave, meets all LR_ROWS rows, so x
+// is read from the caches once per LR_ROWS rows (one x pass per row made x, not the
+// weights, the larger read at 4 tokens). grid: ceil(outputs / (4 LR_ROWS)), 4 waves a block.
+constexpr int LR_ROWS = 4;
 template <int TMAX>
 __global__ void __launch_bounds__(256) linear_rows_kernel(const uint4* __restrict__ x, const uint4* __restrict__ w,
                                                          int tokens, int chunks, int outputs, float* __restrict__ out) {
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int o = blockIdx.x * 4 + wave;
-  if (o >= outputs) return;
-  const uint4* wr = w + (int64_t)o * chunks;
-  float acc[TMAX];
+  const int o0 = (blockIdx.x * 4 + wave) * LR_ROWS;
+  if (o0 >= outputs) return;
+  const uint4* wr[LR_ROWS];
 #pragma unroll
-  for (int t = 0; t < TMAX; ++t) acc[t] = 0.0f;
+  for (int r = 0; r < LR_ROWS; ++r) wr[r] = w + (int64_t)min(o0 + r, outputs - 1) * chunks;  // in bounds
+  float acc[LR_ROWS][TMAX];
+#pragma unroll
+  for (int r = 0; r < LR_ROWS; ++r)
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) acc[r][t] = 0.0f;
+#pragma unroll 2
   for (int c = lane; c < chunks; c += 64) {
-    const uint4 wv = wr[c];
+    uint4 wv[LR_ROWS];
 #pragma unroll
-    for (int t = 0; t < TMAX; ++t)
-      if (t < tokens) acc[t] = dot8_bf16x(wv, x[(int64_t)t * chunks + c], acc[t]);
+    for (int r = 0; r < LR_ROWS; ++r) wv[r] = wr[r][c];
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) {
+      if (t < tokens) {
+        const uint4 xv = x[(int64_t)t * chunks + c];
+#pragma unroll
+        for (int r = 0; r < LR_ROWS; ++r) acc[r][t] = dot8_bf16x(wv[r], xv, acc[r][t]);
+      }
+    }
   }
 #pragma unroll
-  for (int t = 0; t < TMAX; ++t) {
-    if (t >= tokens) break;
-    const float v = segment_sum<64>(acc[t]);
-    if (lane == 0) out[(int64_t)t * outputs + o] = v;
+  for (int r = 0; r < LR_ROWS; ++r) {
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) {
+      if (t >= tokens) break;
+      const float v = segment_sum<64>(acc[r][t]);
+      if (lane == 0 && o0 + r < outputs) out[(int64_t)t * outputs + o0 + r] = v;
+    }
   }
 }
 
@@ -192,7 +218,7 @@ WM_EXPORT int wm_route_softmax_topk(const float* logits, int32_t tokens, int32_t
     if (!logits || !indices || !weights) fail("wm_route_softmax_topk: null pointer");
     hipStream_t s = as_stream(stream);
     int per_lane = (experts + 63) / 64;
-#define WM_RS(P) hipLaunchKernelGGL(route_softmax_topk_kernel<P>, dim3(tokens), dim3(64), 0, s, logits, tokens, experts, \
+#define WM_RS(P) hipLaunchKernelGGL(route_softmax_topk_kernel<P>, dim3((tokens + 3) / 4), dim3(256), 0, s, logits, tokens, experts, \
                                     k, norm_topk_prob, indices, weights, probabilities)
     if (per_lane <= 1) WM_RS(1);
     else if (per_lane <= 2) WM_RS(2);
@@ -220,7 +246,7 @@ WM_EXPORT int wm_route_scored(const float* logits, const float* bias, int32_t to
     if (!logits || !indices || !weights) fail("wm_route_scored: null pointer");
     hipStream_t s = as_stream(stream);
     int per_lane = (experts + 63) / 64;
-#define WM_RS(P) hipLaunchKernelGGL(route_scored_kernel<P>, dim3(tokens), dim3(64), 0, s, logits, bias, tokens, experts, \
+#define WM_RS(P) hipLaunchKernelGGL(route_scored_kernel<P>, dim3((tokens + 3) / 4), dim3(256), 0, s, logits, bias, tokens, experts, \
                                     k, func, route_scale, norm_topk_prob, n_groups, topk_groups, indices, weights)
     if (per_lane <= 1) WM_RS(1);
     else if (per_lane <= 2) WM_RS(2);
@@ -242,7 +268,7 @@ WM_EXPORT int wm_linear_bf16(const void* x, const void* w, int32_t tokens, int32
     // rows: one pass over each weight row; else one wave per output
     if (linear_bf16_mfma(x, w, tokens, hidden, outputs, out, as_stream(stream))) return;
     if (tokens <= 16 && hidden % 8 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0) {
-      const dim3 grid((outputs + 3) / 4);
+      const dim3 grid((outputs + 4 * LR_ROWS - 1) / (4 * LR_ROWS));
       const int chunks = hidden / 8;
 #define WM_LR(T) hipLaunchKernelGGL(linear_rows_kernel<T>, grid, dim3(256), 0, as_stream(stream), (const uint4*)x, \
                                     (const uint4*)w, tokens, chunks, outputs, out)

@@ -92,7 +92,9 @@ __device__ __forceinline__ int dpp_i(int v) {
 // for non-NaN values, so the winner does not depend on the order of the comparisons.
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   auto take = [&](float ov, int oi) {
-    if (topk_better(ov, oi, v, i)) { v = ov; i = oi; }
+    const bool t = (ov > v) | ((ov == v) & (oi < i));
+    v = t ? ov : v;
+    i = t ? oi : i;
   };
   take(dpp_f<0xB1>(v), dpp_i<0xB1>(i));    // quad_perm [1,0,3,2]
   take(dpp_f<0x4E>(v), dpp_i<0x4E>(i));    // quad_perm [2,3,0,1]
@@ -122,10 +124,13 @@ __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int exp
     float bv = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int r = 0; r < PER_LANE; ++r) {
-      int e = r * 64 + lane;
-      bool free_ = e < experts && !((taken >> r) & 1u);
-      if (free_ && topk_better(vals[r], e, bv, bi)) { bv = vals[r]; bi = e; }
+    for (int r = 0; r < PER_LANE; ++r) {  // selects, not branches: every lane scans its column
+      const int e = r * 64 + lane;
+      // bitwise, not short-circuit: no exec-mask branches around each compare
+      const bool take = (e < experts) & (((taken >> r) & 1u) == 0u) &
+                        ((vals[r] > bv) | ((vals[r] == bv) & (e < bi)));
+      bv = take ? vals[r] : bv;
+      bi = take ? e : bi;
     }
     wave_argmax(bv, bi);
     if (lane == j) { sel = bi; sel_val = bv; }
@@ -140,9 +145,10 @@ __device__ __forceinline__ void wave_route_softmax(const float* __restrict__ row
                                                    int lane, int& sel, float& weight, float* full_denominator) {
   float vals[PER_LANE];
 #pragma unroll
-  for (int r = 0; r < PER_LANE; ++r) {
-    int e = r * 64 + lane;
-    vals[r] = e < experts ? row[e] : -INFINITY;
+  for (int r = 0; r < PER_LANE; ++r) {  // every load in bounds, so all are issued together
+    const int e = r * 64 + lane;
+    const float v = row[e < experts ? e : experts - 1];
+    vals[r] = e < experts ? v : -INFINITY;
   }
   float sel_val;
   wave_topk<PER_LANE>(vals, experts, k, lane, sel, sel_val);
