@@ -168,7 +168,9 @@ def _generic_experts(x: torch.Tensor, indices: torch.Tensor, table, activation) 
     """Per-pair outputs [T, K, H] for an activation the kernels do not fuse: the library
     dequantizes each touched expert, the projections run as library GEMMs (the
     _StreamingSwitchGLU arithmetic of model.py:395-426 with mx.quantized_matmul's
-    dequant-then-matmul)."""
+    dequant-then-matmul). It loops over the touched experts on the host (one
+    synchronisation for the id list) and is never taken for SwiGLU or the clamped SwiGLU,
+    which the expert kernels fuse; it exists for arbitrary activation callables only."""
     T, K = indices.shape
     H, I = table.hidden, table.inter
     flat = indices.reshape(-1).long()
@@ -195,7 +197,9 @@ def resolve_table(cache, layer: int, indices: torch.Tensor, limit: float = 0.0):
     """(expert table, indices into it) for one call: the whole-layer table when the cache
     has one (no host synchronisation: the kernels map ids to slots on the device), else the
     resident experts from iter_ready (single-token decode with ready_expert_decode) or
-    get_many, gathered into one table (qwen4_exp.py:857-944, model.py:325-371)."""
+    get_many, gathered into one table (qwen4_exp.py:857-944, model.py:325-371). Those two
+    cache calls take host id lists, as the reference's do, so that path synchronises once
+    to read the ids (timed into record_routing_sync, as expert_cache.py does)."""
     current = getattr(cache, "current_batched", None)
     batched = current(layer) if callable(current) else None
     if batched is not None:
