@@ -1091,19 +1091,33 @@ __global__ void __launch_bounds__(256) combine_rows_kernel(const uint16_t* __res
       acc[2 * q + 1] = fmaf(s, bf16_bits_to_f32(w[q] >> 16), acc[2 * q + 1]);
     }
   };
-  // the rows of up to 16 pairs (and the shared row, when it fits in the batch) are loaded
-  // before any is summed (sums stay in k order, the shared row last)
-  constexpr int BATCH = 16;
+  // the rows of the token's pairs and its shared row are loaded before any is summed (sums
+  // stay in k order, the shared row last); row indices are block-uniform (scalar addressing)
   const int n = k + (has_shared ? 1 : 0);
-  for (int j0 = 0; j0 < n; j0 += BATCH) {
+  auto row_of = [&](int j) {
+    int r = j < k ? inverse[t * k + j] : (j < n && shared_live ? pairs + t : -1);
+    if (j < k && r >= 0 && !pair_resident(indices, slots, t * k + j)) r = -1;
+    return __builtin_amdgcn_readfirstlane(r);
+  };
+  constexpr int ONE_PASS = 17;  // up to 16 pairs + the shared row in one unrolled pass
+  if (n <= ONE_PASS) {
+    int row[ONE_PASS];
+    uint4 v[ONE_PASS];
+#pragma unroll
+    for (int j = 0; j < ONE_PASS; ++j) row[j] = j < n ? row_of(j) : -1;
+#pragma unroll
+    for (int j = 0; j < ONE_PASS; ++j)
+      if (row[j] >= 0) v[j] = reinterpret_cast<const uint4*>(rows + (int64_t)row[j] * hidden)[c8];
+#pragma unroll
+    for (int j = 0; j < ONE_PASS; ++j)
+      if (row[j] >= 0) add(v[j], j < k ? weights[t * k + j] : gate[t]);
+  }
+  constexpr int BATCH = 16;
+  for (int j0 = 0; n > ONE_PASS && j0 < n; j0 += BATCH) {
     int row[BATCH];
     uint4 v[BATCH];
 #pragma unroll
-    for (int q = 0; q < BATCH; ++q) {
-      const int j = j0 + q;
-      row[q] = j < k ? inverse[t * k + j] : (j < n && shared_live ? pairs + t : -1);
-      if (j < k && row[q] >= 0 && !pair_resident(indices, slots, t * k + j)) row[q] = -1;
-    }
+    for (int q = 0; q < BATCH; ++q) row[q] = j0 + q < n ? row_of(j0 + q) : -1;
 #pragma unroll
     for (int q = 0; q < BATCH; ++q)
       if (row[q] >= 0) v[q] = reinterpret_cast<const uint4*>(rows + (int64_t)row[q] * hidden)[c8];
