@@ -154,7 +154,16 @@ __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int s
 #define WM_DS_NOTE(layer, point, value)
 #endif
 
-__device__ __forceinline__ float bf16_round_f(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+// bf16 rounding on the gfx950 conversion v_cvt_pk_bf16_f32 (round to nearest even, as
+// f32_to_bf16_bits; a NaN stays a NaN). Branch-free, where the integer form costs an
+// exec-mask branch per value: these roundings sit on the per-layer critical path.
+typedef __bf16 ds_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float ds_f2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t ds_bf16_pair(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((ds_f2){a, b}, ds_bf16x2));
+}
+__device__ __forceinline__ uint16_t ds_bf16_bits(float v) { return (uint16_t)ds_bf16_pair(v, 0.0f); }
+__device__ __forceinline__ float bf16_round_f(float v) { return __uint_as_float(ds_bf16_pair(v, 0.0f) << 16); }
 
 // ---- E4M3 term splitting -------------------------------------------------------
 // E8M0 exponent s that puts amax / 2^(s-127) in [128, 256) (E4M3's largest finite is
@@ -229,9 +238,10 @@ __device__ __forceinline__ void ds_build_x(DSShared& sh, int tid) {
   uint32_t hw[2], lw[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    float h[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) h[t] = bf16_round_f(rv[4 * p + t] * inv) * f;
+    const uint32_t x01 = ds_bf16_pair(rv[4 * p] * inv, rv[4 * p + 1] * inv);
+    const uint32_t x23 = ds_bf16_pair(rv[4 * p + 2] * inv, rv[4 * p + 3] * inv);
+    const float h[4] = {__uint_as_float(x01 << 16) * f, __uint_as_float(x01 & 0xffff0000u) * f,
+                        __uint_as_float(x23 << 16) * f, __uint_as_float(x23 & 0xffff0000u) * f};
     uint32_t w01 = e4m3_pair(h[0], h[1]), w23 = e4m3_pair(h[2], h[3]);
     float l0 = (h[0] - e4m3_byte<0>(w01)) * 16.0f, l1 = (h[1] - e4m3_byte<1>(w01)) * 16.0f;
     float l2 = (h[2] - e4m3_byte<0>(w23)) * 16.0f, l3 = (h[3] - e4m3_byte<1>(w23)) * 16.0f;
@@ -512,7 +522,7 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
           const uint32_t g4[4] = {gw[m].x, gw[m].y, gw[m].z, gw[m].w};
 #pragma unroll
           for (int h = 0; h < 4; ++h) {
-            uint32_t xv = f32_to_bf16_bits(rv[2 * h] * inv) | ((uint32_t)f32_to_bf16_bits(rv[2 * h + 1] * inv) << 16);
+            const uint32_t xv = ds_bf16_pair(rv[2 * h] * inv, rv[2 * h + 1] * inv);
             a = dot2_bf16(bits_to_bf16x2(xv), bits_to_bf16x2(g4[h]), a);
           }
         }
@@ -552,12 +562,12 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
                     [&](int i, uint64_t v) { y += __uint_as_float((uint32_t)v); }, &rounds);
     WM_DS_NOTE(l, 15, rounds);
     WM_DS_TRACE(l, 12);
-    r_own += bf16_bits_to_f32(f32_to_bf16_bits(y));
+    r_own += bf16_round_f(y);
     if (c.trace && x == 0) c.trace[(size_t)l * DS_H + j * DS_ROWS + lane] = r_own;
     // publish the row block as bf16 triples under a 16-bit epoch (the hidden state that
     // feeds the next rmsnorm is bf16, as in the reference's bf16 residual stream; the
     // owner keeps accumulating r in fp32)
-    sh.rpack[lane] = f32_to_bf16_bits(r_own);
+    sh.rpack[lane] = ds_bf16_bits(r_own);
     if (lane < 3 * DS_RW - DS_ROWS) sh.rpack[DS_ROWS + lane] = 0;
     if (lane < DS_RW) {
       const uint64_t word = ((uint64_t)(e_r & 0xffffu) << 48) | ((uint64_t)sh.rpack[3 * lane + 2] << 32) |
