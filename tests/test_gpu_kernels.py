@@ -104,7 +104,7 @@ def _scored_case(rng, tokens, experts, func, groups, topk_groups, k):
 @pytest.mark.parametrize("func,groups,topk_groups,k,experts",
                          [("sigmoid", 8, 4, 8, 256), ("sigmoid", 1, 1, 8, 256), ("sqrtsoftplus", 1, 1, 6, 384),
                           ("softmax", 1, 1, 6, 64), ("softmax", 1, 1, 10, 512), ("sigmoid", 4, 2, 3, 16),
-                          ("sqrtsoftplus", 8, 4, 8, 256)])
+                          ("sqrtsoftplus", 8, 4, 8, 256), ("sigmoid", 16, 4, 8, 512)])
 def test_route_scored_matches_oracle(device, func, groups, topk_groups, k, experts):
     """Indices bit-exact: the device evaluates the scores in the stated fp32 arithmetic that
     the oracle restates op for op (route_device.h, oracle/moe.py score_f32)."""

@@ -101,7 +101,27 @@ __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restri
     int gsize = experts / n_groups;
     // A group's score is the sum of its two largest biased scores (DeepSeek-V3 rule).
     float gs[1] = {-INFINITY};
-    if (lane < n_groups) {
+    if (gsize == 32 && experts % 64 == 0) {
+      // Group 2 r + h is the lane half h of register r: the half's top two meet in five
+      // xor butterflies (merging two pairs: a = max, b = max(min(a1, a2), max(b1, b2)), the
+      // same multiset rule as the scan below, ties counted twice), then lanes 0 and 32 hold
+      // each register's two group scores.
+#pragma unroll
+      for (int r = 0; r < PER_LANE; ++r) {
+        float a = vals[r], b = -INFINITY;
+#pragma unroll
+        for (int m = 1; m < 32; m <<= 1) {
+          const float oa = __shfl_xor(a, m, 64), ob = __shfl_xor(b, m, 64);
+          b = fmaxf(fminf(a, oa), fmaxf(b, ob));
+          a = fmaxf(a, oa);
+        }
+        const float sum = a + b;
+        const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), 0));
+        const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), 32));
+        gs[0] = lane == 2 * r ? s0 : (lane == 2 * r + 1 ? s1 : gs[0]);
+      }
+      if (lane >= n_groups) gs[0] = -INFINITY;
+    } else if (lane < n_groups) {
       float a = -INFINITY, b = -INFINITY;
       for (int j = 0; j < gsize; ++j) {
         float v = biased_lds[lane * gsize + j];
