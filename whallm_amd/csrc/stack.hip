@@ -34,8 +34,66 @@ __global__ void __launch_bounds__(256) residual_rmsnorm_kernel(float* __restrict
   for (int i = threadIdx.x; i < hidden; i += 256) x[(int64_t)t * hidden + i] = f32_to_bf16_bits(rr[i] * inv);
 }
 
+// The same for hidden = 1024 PER: thread i holds columns 4 (i + 256 c) .. + 3 (c < PER) in
+// registers, every load issued before the first use, so a token costs one memory round
+// trip instead of one per 256 columns; r and y are read once.
+template <int PER>
+__global__ void __launch_bounds__(256) residual_rmsnorm_vec_kernel(float* __restrict__ r, const uint16_t* __restrict__ y,
+                                                                   float eps, uint16_t* __restrict__ x) {
+  __shared__ float partial[4];
+  constexpr int H = 1024 * PER;
+  const int t = blockIdx.x;
+  float4* rr = reinterpret_cast<float4*>(r + (int64_t)t * H);
+  float4 v[PER];
+#pragma unroll
+  for (int c = 0; c < PER; ++c) v[c] = rr[threadIdx.x + 256 * c];
+  if (y) {
+    const uint2* yy = reinterpret_cast<const uint2*>(y + (int64_t)t * H);
+    uint2 yv[PER];
+#pragma unroll
+    for (int c = 0; c < PER; ++c) yv[c] = yy[threadIdx.x + 256 * c];
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      v[c].x += bf16_bits_to_f32(yv[c].x & 0xffffu);
+      v[c].y += bf16_bits_to_f32(yv[c].x >> 16);
+      v[c].z += bf16_bits_to_f32(yv[c].y & 0xffffu);
+      v[c].w += bf16_bits_to_f32(yv[c].y >> 16);
+      rr[threadIdx.x + 256 * c] = v[c];
+    }
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < PER; ++c) {
+    sum += v[c].x * v[c].x;
+    sum += v[c].y * v[c].y;
+    sum += v[c].z * v[c].z;
+    sum += v[c].w * v[c].w;
+  }
+  sum = segment_sum<64>(sum);
+  if (threadIdx.x % 64 == 0) partial[threadIdx.x / 64] = sum;
+  __syncthreads();
+  const float total = partial[0] + partial[1] + partial[2] + partial[3];
+  const float inv = rsqrtf(total / (float)H + eps);
+  uint2* xx = reinterpret_cast<uint2*>(x + (int64_t)t * H);
+#pragma unroll
+  for (int c = 0; c < PER; ++c) {
+    const uint32_t lo = f32_to_bf16_bits(v[c].x * inv) | ((uint32_t)f32_to_bf16_bits(v[c].y * inv) << 16);
+    const uint32_t hi = f32_to_bf16_bits(v[c].z * inv) | ((uint32_t)f32_to_bf16_bits(v[c].w * inv) << 16);
+    xx[threadIdx.x + 256 * c] = make_uint2(lo, hi);
+  }
+}
+
 void residual_rmsnorm(float* r, const uint16_t* y, int tokens, int hidden, float eps, uint16_t* x, hipStream_t s) {
-  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(tokens), dim3(256), 0, s, r, y, hidden, eps, x);
+  const bool aligned = (uintptr_t)r % 16 == 0 && (uintptr_t)y % 8 == 0 && (uintptr_t)x % 8 == 0;
+  if (aligned && hidden % 1024 == 0 && hidden / 1024 >= 1 && hidden / 1024 <= 8) {
+    switch (hidden / 1024) {
+#define WM_RN(P) case P: hipLaunchKernelGGL(residual_rmsnorm_vec_kernel<P>, dim3(tokens), dim3(256), 0, s, r, y, eps, x); break;
+      WM_RN(1) WM_RN(2) WM_RN(3) WM_RN(4) WM_RN(5) WM_RN(6) WM_RN(7) WM_RN(8)
+#undef WM_RN
+    }
+  } else {
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(tokens), dim3(256), 0, s, r, y, hidden, eps, x);
+  }
   check_launch("residual_rmsnorm");
 }
 
