@@ -46,12 +46,15 @@ __device__ __forceinline__ float score_fn(float l, int func) {
   return func == 1 ? sigmoid_defined(l) : sqrt_softplus_defined(l);
 }
 
-template <int PER_LANE>
+// FUNC: 0 softmax, 1 sigmoid, 2 sqrt-softplus (one instance each, so the score code of the
+// others is not carried along). Every logit and bias load of a row is issued before any use.
+template <int PER_LANE, int FUNC>
 __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restrict__ logits,
                                                           const float* __restrict__ bias, int tokens, int experts,
-                                                          int k, int func, float route_scale, int norm, int n_groups,
+                                                          int k, float route_scale, int norm, int n_groups,
                                                           int topk_groups, int32_t* __restrict__ indices,
                                                           float* __restrict__ weights) {
+  constexpr int func = FUNC;
   __shared__ float biased_all[4][64 * PER_LANE];
   __shared__ float score_all[4][64 * PER_LANE];
   const int wave = threadIdx.x / 64, t = blockIdx.x * 4 + wave, lane = threadIdx.x % 64;
@@ -59,14 +62,21 @@ __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restri
   float* biased_lds = biased_all[wave];  // each wave's own rows: LDS is shared only within the wave
   float* score_lds = score_all[wave];
   const float* row = logits + (int64_t)t * experts;
+  float lg[PER_LANE], bs[PER_LANE];
+#pragma unroll
+  for (int r = 0; r < PER_LANE; ++r) {  // in-bounds addresses: every load is unconditional
+    const int e = min(r * 64 + lane, experts - 1);
+    lg[r] = row[e];
+    bs[r] = bias ? bias[e] : 0.0f;
+  }
   float vals[PER_LANE];
   float top = 0.0f, denom = 1.0f;
-  if (func == 0) {  // softmax scores need the row max and sum
+  if constexpr (func == 0) {  // softmax scores need the row max and sum
     float m = -INFINITY;
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
-      if (e < experts) m = fmaxf(m, row[e]);
+      if (e < experts) m = fmaxf(m, lg[r]);
     }
     int dummy = 0;
     wave_argmax(m, dummy);
@@ -75,7 +85,7 @@ __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restri
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
-      if (e < experts) part += exp_defined(row[e] - top);
+      if (e < experts) part += exp_defined(lg[r] - top);
     }
     denom = segment_sum<64>(part);
   }
@@ -83,8 +93,8 @@ __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restri
   for (int r = 0; r < PER_LANE; ++r) {
     int e = r * 64 + lane;
     if (e < experts) {
-      float s = func == 0 ? exp_defined(row[e] - top) / denom : score_fn(row[e], func);
-      float b = s + (bias ? bias[e] : 0.0f);
+      float s = func == 0 ? exp_defined(lg[r] - top) / denom : score_fn(lg[r], func);
+      float b = s + bs[r];
       score_lds[e] = s;
       biased_lds[e] = b;
       vals[r] = b;
@@ -266,14 +276,16 @@ WM_EXPORT int wm_route_scored(const float* logits, const float* bias, int32_t to
     if (!logits || !indices || !weights) fail("wm_route_scored: null pointer");
     hipStream_t s = as_stream(stream);
     int per_lane = (experts + 63) / 64;
-#define WM_RS(P) hipLaunchKernelGGL(route_scored_kernel<P>, dim3((tokens + 3) / 4), dim3(256), 0, s, logits, bias, tokens, experts, \
-                                    k, func, route_scale, norm_topk_prob, n_groups, topk_groups, indices, weights)
+#define WM_RS_F(P, F) hipLaunchKernelGGL((route_scored_kernel<P, F>), dim3((tokens + 3) / 4), dim3(256), 0, s, logits, bias, \
+                                         tokens, experts, k, route_scale, norm_topk_prob, n_groups, topk_groups, indices, weights)
+#define WM_RS(P) do { if (func == 0) WM_RS_F(P, 0); else if (func == 1) WM_RS_F(P, 1); else WM_RS_F(P, 2); } while (0)
     if (per_lane <= 1) WM_RS(1);
     else if (per_lane <= 2) WM_RS(2);
     else if (per_lane <= 4) WM_RS(4);
     else if (per_lane <= 8) WM_RS(8);
     else WM_RS(16);
 #undef WM_RS
+#undef WM_RS_F
     check_launch("route_scored");
   });
 }
