@@ -150,3 +150,20 @@ def test_linear_bf16_prefill_path(device, T, H, E):
     got = wa.linear_bf16(x, w)
     torch.cuda.synchronize()
     check_dot(got.cpu().numpy(), x.float().cpu().numpy(), w.float().cpu().numpy())
+
+
+@pytest.mark.parametrize("T,H,with_y", [(1, 2048, True), (4, 7168, True), (33, 1024, False), (5, 8192, True),
+                                        (3, 2560, True), (2, 640, False)])
+def test_residual_rmsnorm_matches_oracle(device, T, H, with_y):
+    """wm_residual_rmsnorm on both of its kernels (hidden = 1024 n up to 8192 holds a row in
+    registers; other widths walk it 256 columns at a time): r += y exact, x within one bf16
+    step of oracle.rms_norm on the updated r."""
+    rng = np.random.default_rng(T * 131 + H)
+    r0 = rng.standard_normal((T, H)).astype(np.float32) * 3
+    r = torch.from_numpy(r0).to(device)
+    y = bf16_tensor(rng, (T, H), device) if with_y else None
+    x = wa.ops.residual_rmsnorm(r, y)
+    torch.cuda.synchronize()
+    want_r = r0 + (y.float().cpu().numpy() if with_y else 0.0)
+    np.testing.assert_array_equal(r.cpu().numpy(), want_r.astype(np.float32))
+    check_x(x.float().cpu().numpy(), M.rms_norm(want_r, 1e-6))
