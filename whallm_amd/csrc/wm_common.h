@@ -66,6 +66,12 @@ __device__ __forceinline__ uint4 gload16(const void* p) {
   wm_u32x4 v = *(const __attribute__((address_space(1))) wm_u32x4*)(p);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// The same with the non-temporal hint (global_load ... nt), for data read once per call
+// (weights streamed through a decode step).
+__device__ __forceinline__ uint4 gload16_nt(const void* p) {
+  wm_u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) wm_u32x4*)(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
