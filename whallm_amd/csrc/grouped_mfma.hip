@@ -495,6 +495,13 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
 #pragma unroll
   for (int ni = 0; ni < NI4; ++ni) sb[ni] = *reinterpret_cast<const uint2*>(stb + lo.bs + 32 * XSTEP * ni);
   v16f blk[F::FP8 ? MI : 1][NI4];
+  // FP8 block scales (scalar loads) issued before the MFMAs, so their memory round trip
+  // overlaps the step instead of stalling the scale-and-add at its end
+  float bs[F::FP8 ? MI : 1];
+  if constexpr (F::FP8) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) bs[mi] = bscale(mi);
+  }
   if constexpr (F::FP8) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
@@ -568,7 +575,7 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
   if constexpr (F::FP8) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      const float s = bscale(mi);
+      const float s = bs[mi];
 #pragma unroll
       for (int ni = 0; ni < NI4; ++ni)
 #pragma unroll
