@@ -78,6 +78,37 @@ def test_c3_prefill_full_size(device):
     assert torch.equal(out, full)
 
 
+def test_c3_prefill_all_tokens_on_ten_experts(device):
+    """The most skewed routing top-10 allows: 8,192 tokens all on the same 10 experts (64 row
+    tiles each, so one expert's tiles span several XCDs' shares of the tile list), against
+    the oracle on a sample and the row layout bit for bit."""
+    T, H, E, I, K = 8192, 2048, 512, 512, 10
+    g = torch.Generator(device=device)
+    g.manual_seed(13)
+    experts = S.mxfp4_experts_device(E, H, I, device, g)
+    shared = S.mxfp4_experts_device(1, H, I, device, g)
+    gate = (torch.randn(H, device=device, generator=g) * 0.02).to(torch.bfloat16)
+    hot = torch.tensor([3, 17, 64, 100, 200, 256, 300, 400, 450, 511], device=device)
+    logits = torch.randn(T, E, device=device, generator=g)
+    logits[:, hot] += 20.0
+    x = torch.randn(T, H, device=device, generator=g).to(torch.bfloat16)
+    idx, w = wa.route_softmax_topk(logits, K)
+    assert set(np.unique(idx.cpu().numpy()).tolist()) == set(hot.cpu().numpy().tolist())
+    tiled, tiled_shared = wa.prefill_layout(experts), wa.prefill_layout(shared)
+    y = wa.moe_mxfp4(x, idx, w, tiled, tiled_shared, gate)
+    y_rows = wa.moe_mxfp4(x, idx, w, experts, shared, gate)
+    assert torch.equal(y, y_rows), "tile layout differs from the row layout"
+    rng = np.random.default_rng(13)
+    sample = np.sort(rng.choice(T, 64, replace=False))
+    ids, ws = idx.cpu().numpy()[sample], w.cpu().numpy()[sample]
+    xs = x[torch.from_numpy(sample).to(device)].float().cpu().numpy()
+    ex = {int(e): mx_expert(experts, int(e)) for e in np.unique(ids)}
+    routed = M.routed_outputs(xs, ids, ex)
+    sh = M.expert_ffn(xs, mx_expert(shared, 0))
+    want = M.combine(routed, ws, sh, xs.astype(np.float64) @ gate.float().cpu().numpy().astype(np.float64))
+    close(y.float().cpu().numpy()[sample], want, "hot experts, sampled tokens")
+
+
 def test_c4_prefill_full_size(device):
     T, H, E, I, K = 4096, 7168, 256, 2048, 8
     g = torch.Generator(device=device)
