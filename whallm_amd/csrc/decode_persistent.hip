@@ -675,11 +675,16 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
     if (tid == 0) __hip_atomic_store(c.status, DS_NOT_RESIDENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  if (msg) {  // rmsnorm statistics of r_0
+  if (msg) {  // rmsnorm statistics of r_0 (every LDS read issued before the first use)
     float ss = 0.0f, mx = 0.0f;
-    for (int i = c.lane; i < DS_H; i += 64) {
-      ss += sh.r[i] * sh.r[i];
-      mx = fmaxf(mx, fabsf(sh.r[i]));
+    static_assert(DS_H % 256 == 0, "each lane reads whole float4 chunks of r");
+    float4 v[DS_H / 256];
+#pragma unroll
+    for (int q = 0; q < DS_H / 256; ++q) v[q] = *reinterpret_cast<const float4*>(&sh.r[4 * (c.lane + 64 * q)]);
+#pragma unroll
+    for (int q = 0; q < DS_H / 256; ++q) {
+      ss += v[q].x * v[q].x + v[q].y * v[q].y + v[q].z * v[q].z + v[q].w * v[q].w;
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)), fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
     }
     ds_publish_norm(sh, ss, mx, c.lane);
   }
