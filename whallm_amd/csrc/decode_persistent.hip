@@ -69,7 +69,7 @@ struct DSLayout {
 __host__ __device__ inline DSLayout ds_layout(int layers) {
   DSLayout d;
   size_t at = 0;
-  d.route = at;  at += (size_t)layers * 32 * 8;
+  d.route = at;  at += (size_t)DS_X * layers * 32 * 8;  // per XCD: 2 K <= 32 words a layer
   d.act = at;    at += (size_t)2 * DS_X * DS_NE_MAX * DS_SLICE * 8;
   d.part = at;   at += (size_t)2 * DS_X * DS_H * 8;
   d.r = at;      at += (size_t)2 * DS_X * DS_J * DS_RW * 8;
@@ -623,36 +623,43 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   const uint32_t e_route = c.base + 1;
   const bool msg = c.wave == DS_CW;
   bool ok = true;
+
+  // ---- prologue. Its memory round trips overlap: the message wave of workgroup b < L
+  // routes layer b while every wave copies the descriptors and r_0 and the epoch arrives.
+  static_assert(DS_MAX_LAYERS <= DS_WGS, "a workgroup routes one layer at most");
+  int sel = 0;
+  float w = 0.0f;
+  if (msg && b < L)
+    wave_route_softmax<PER_LANE>(logits + (size_t)b * E, E, K, norm_topk != 0, c.lane, sel, w, nullptr);
+  for (int i = tid; i < L * (int)(sizeof(wm_decode_layer) / 8); i += DS_THREADS)
+    reinterpret_cast<uint64_t*>(sh.desc)[i] = reinterpret_cast<const uint64_t*>(layers)[i];
+  for (int i = tid; i < DS_H; i += DS_THREADS) sh.r[i] = residual[i];
+  float r_own = msg ? residual[c.j * DS_ROWS + c.lane] : 0.0f;  // the message wave owns rows 64j + lane
   if (tid == 0) sh.failures = 0;
   if (tid == 0) sh.eps = eps;
   __syncthreads();  // failures is cleared before any wave can raise it; every wave holds its epoch
   // Every launch advances the epochs by the same amount, whether it completes or not, so
   // words left by a launch that ended early never match a later launch's epochs.
   if (tid == 0) wg_epoch[b] = c.base + 3 * (uint32_t)L + 5;
-
-  // ---- prologue: routes of layers b, b + 256, ... (message wave), descriptors, r_0
-  if (msg) {
-    for (int l = b; l < L; l += DS_WGS) {
-      int sel;
-      float w;
-      wave_route_softmax<PER_LANE>(logits + (size_t)l * E, E, K, norm_topk != 0, c.lane, sel, w, nullptr);
-      if (c.lane < 16) {
-        ll_put(&c.route_ll[(size_t)l * 32 + c.lane], c.lane < K ? (uint32_t)sel : 0u, e_route);
-        ll_put(&c.route_ll[(size_t)l * 32 + 16 + c.lane], c.lane < K ? __float_as_uint(w) : 0u, e_route);
-      }
+  // Routes travel as 2 K words per layer (K ids, then K weights), written once per XCD, so
+  // an XCD's 32 workgroups poll lines of their own instead of all 256 polling the same ones.
+  const int rw = 2 * K;
+  if (msg && b < L && c.lane < K) {
+#pragma unroll
+    for (int xc = 0; xc < DS_X; ++xc) {
+      uint64_t* dst = c.route_ll + ((size_t)xc * L + b) * rw;
+      ll_put(&dst[c.lane], (uint32_t)sel, e_route);
+      ll_put(&dst[K + c.lane], __float_as_uint(w), e_route);
     }
   }
-  for (int i = tid; i < L * (int)(sizeof(wm_decode_layer) / 8); i += DS_THREADS)
-    reinterpret_cast<uint64_t*>(sh.desc)[i] = reinterpret_cast<const uint64_t*>(layers)[i];
-  for (int i = tid; i < DS_H; i += DS_THREADS) sh.r[i] = residual[i];
-  float r_own = msg ? residual[c.j * DS_ROWS + c.lane] : 0.0f;  // the message wave owns rows 64j + lane
   if (msg) {
-    for (int s = 0; s < L * 32; s += 64 * 16)
-      ll_gather<16>(c.route_ll, s + c.lane, 64, L * 32, e_route, c.status, ok, [&](int i, uint64_t word) {
+    const uint64_t* src = c.route_ll + (size_t)c.x * L * rw;
+    for (int s = 0; s < L * rw; s += 64 * 16)
+      ll_gather<16>(src, s + c.lane, 64, L * rw, e_route, c.status, ok, [&](int i, uint64_t word) {
         const uint32_t v = (uint32_t)word;
-        int l = i / 32, s_ = i % 32;
-        if (s_ < 16) sh.slot[l][s_] = (int)v;
-        else sh.w[l][s_ - 16] = __uint_as_float(v);
+        const int l = i / rw, k = i - l * rw;
+        if (k < K) sh.slot[l][k] = (int)v;
+        else sh.w[l][k - K] = __uint_as_float(v);
       });
   }
   if (!ok) sh.failures = 1;
