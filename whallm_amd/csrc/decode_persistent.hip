@@ -695,7 +695,8 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
     }
     ds_publish_norm(sh, ss, mx, c.lane);
   }
-  ds_barrier();
+  // No barrier here: the compute waves issue layer 0's weight loads while the message wave
+  // computes the statistics, which the first S0 barrier publishes.
 
   if (msg) ds_message_role<LOCAL>(sh, c, r_own);
   else ds_compute_role<LOCAL, DOWN_ROWS>(sh, c);
