@@ -111,23 +111,28 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
     xw[m][0] = a.x; xw[m][1] = a.y; xw[m][2] = a.z; xw[m][3] = a.w;
     xw[m][4] = b.x; xw[m][5] = b.y; xw[m][6] = b.z; xw[m][7] = b.w;
   }
+  // a wave's FP8_RPW gate rows lie in one 128-row scale block, and so do its up rows
+  static_assert(128 % (4 * FP8_RPW) == 0, "a workgroup's rows lie in one scale block");
   uint4 wq[ROWS][CPL];
-  float sc[ROWS][CPL];
+  float sc[2][CPL];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = (h ^ up_first) ? I + i_base : i_base;  // h 0: gate, 1: up
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) sc[h][m] = gload<float>(r.w13_scales + (int64_t)(row / 128) * HB + 8 * m + lane / 8);
+  }
 #pragma unroll
   for (int q = 0; q < ROWS; ++q) {
     const int i = i_base + q / 2;  // I is a multiple of 8: always in range
     const int row = ((q & 1) ^ up_first) ? I + i : i;  // q even: gate, odd: up
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-      wq[q][m] = gload16_nt(r.w13 + (int64_t)row * H + 1024 * m + 16 * lane);
-      sc[q][m] = gload<float>(r.w13_scales + (int64_t)(row / 128) * HB + 8 * m + lane / 8);
-    }
+    for (int m = 0; m < CPL; ++m) wq[q][m] = gload16_nt(r.w13 + (int64_t)row * H + 1024 * m + 16 * lane);
   }
 #pragma unroll
   for (int q = 0; q < ROWS; ++q) {
     float acc = 0.0f;
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) acc = fmaf(sc[q][m], e4m3x16_dot_bf16(wq[q][m], xw[m], 0.0f), acc);
+    for (int m = 0; m < CPL; ++m) acc = fmaf(sc[q & 1][m], e4m3x16_dot_bf16(wq[q][m], xw[m], 0.0f), acc);
     acc = segment_sum<64>(acc);
     if (lane == 0) sums[wave][q] = acc;
   }
@@ -227,22 +232,24 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
         av[m][4 * q] = v.x; av[m][4 * q + 1] = v.y; av[m][4 * q + 2] = v.z; av[m][4 * q + 3] = v.w;
       }
     }
+    // the step's FP8_OPW rows start at a multiple of FP8_OPW, so they share one 128-row
+    // scale block: one scale load per 1024-wide chunk
+    static_assert(128 % FP8_OPW == 0, "a step's rows lie in one scale block");
     uint4 wq[FP8_OPW][CPL];
-    float sc[FP8_OPW][CPL];
+    float sc[CPL];
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) sc[m] = gload<float>(r.w2_scales + (int64_t)(o_base / 128) * IB + 8 * m + lane / 8);
 #pragma unroll
     for (int q = 0; q < FP8_OPW; ++q) {
       const int o = o_base + q;  // H is a multiple of 32: always in range
 #pragma unroll
-      for (int m = 0; m < CPL; ++m) {
-        wq[q][m] = gload16_nt(r.w2 + (int64_t)o * I + 1024 * m + 16 * lane);
-        sc[q][m] = gload<float>(r.w2_scales + (int64_t)(o / 128) * IB + 8 * m + lane / 8);
-      }
+      for (int m = 0; m < CPL; ++m) wq[q][m] = gload16_nt(r.w2 + (int64_t)o * I + 1024 * m + 16 * lane);
     }
 #pragma unroll
     for (int q = 0; q < FP8_OPW; ++q) {
       float s = 0.0f;
 #pragma unroll
-      for (int m = 0; m < CPL; ++m) s = fmaf(sc[q][m], e4m3x16_dot_f32(wq[q][m], av[m], 0.0f), s);
+      for (int m = 0; m < CPL; ++m) s = fmaf(sc[m], e4m3x16_dot_f32(wq[q][m], av[m], 0.0f), s);
       acc[q] = fmaf(w, s, acc[q]);
     }
   }
