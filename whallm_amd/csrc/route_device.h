@@ -112,29 +112,89 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   i = bi;
 }
 
+// Order-preserving 32-bit key of a score: a larger value has a larger key, +0 and -0 share
+// one (they compare equal), and NaN gets 0, below every number, so it is never selected.
+__device__ __forceinline__ uint32_t topk_key(float v) {
+  const float c = v + 0.0f;  // -0 -> +0
+  const uint32_t u = __float_as_uint(c);
+  const uint32_t key = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return c == c ? key : 0u;
+}
+__device__ __forceinline__ float topk_value(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+// Wave-wide max / min; every lane gets the result (rows through DPP, then the four rows'
+// results through scalar registers).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x141>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x140>((int)v));
+  const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+  const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+  return max(a, b);
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  v = min(v, dpp_i<0xB1>(v));
+  v = min(v, dpp_i<0x4E>(v));
+  v = min(v, dpp_i<0x141>(v));
+  v = min(v, dpp_i<0x140>(v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 // k rounds of arg-max over vals (entries with e >= experts are ignored). Lane j < k
-// receives the j-th selection in (sel, sel_val).
+// receives the j-th selection in (sel, sel_val); a round with nothing left to select
+// gives (0x7fffffff, -inf). Each lane keeps its best remaining entry (the lowest register
+// among equal keys, so the lowest expert id); a round takes the wave max of those keys, and
+// only when several lanes hold it the lowest expert id among them. The winner's lane drops
+// the entry and finds its next best. Values are compared as keys, so -0 and +0 tie and a
+// selected zero is reported as +0.
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int experts, int k, int lane, int& sel,
                                           float& sel_val) {
-  uint32_t taken = 0;
+  uint32_t key[PER_LANE];
+#pragma unroll
+  for (int r = 0; r < PER_LANE; ++r) key[r] = r * 64 + lane < experts ? topk_key(vals[r]) : 0u;
+  uint32_t hk;
+  int hr;
+  auto best = [&]() {
+    hk = key[0];
+    hr = 0;
+#pragma unroll
+    for (int r = 1; r < PER_LANE; ++r) {  // strict: the lowest register wins a tie
+      const bool t = key[r] > hk;
+      hk = t ? key[r] : hk;
+      hr = t ? r : hr;
+    }
+  };
+  best();
   sel = -1;
   sel_val = -INFINITY;
   for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    const uint32_t m = wave_max_u32(hk);
+    int ew = 0x7fffffff;
+    float vw = -INFINITY;
+    if (m != 0u) {
+      const uint64_t tied = __builtin_amdgcn_ballot_w64(hk == m);
+      if (__builtin_popcountll(tied) == 1) {
+        const int wl = (int)__builtin_ctzll(tied);
+        ew = __builtin_amdgcn_readlane(hr, wl) * 64 + wl;
+      } else {
+        ew = wave_min_i32(hk == m ? hr * 64 + lane : 0x7fffffff);
+      }
+      vw = topk_value(m);
+      const bool win = lane == (ew & 63);
+      const int rw = ew >> 6;
 #pragma unroll
-    for (int r = 0; r < PER_LANE; ++r) {  // selects, not branches: every lane scans its column
-      const int e = r * 64 + lane;
-      // bitwise, not short-circuit: no exec-mask branches around each compare
-      const bool take = (e < experts) & (((taken >> r) & 1u) == 0u) &
-                        ((vals[r] > bv) | ((vals[r] == bv) & (e < bi)));
-      bv = take ? vals[r] : bv;
-      bi = take ? e : bi;
+      for (int r = 0; r < PER_LANE; ++r) key[r] = (win & (r == rw)) ? 0u : key[r];
+      best();
     }
-    wave_argmax(bv, bi);
-    if (lane == j) { sel = bi; sel_val = bv; }
-    if (bi < experts && (bi & 63) == lane) taken |= 1u << (bi >> 6);
+    if (lane == j) {
+      sel = ew;
+      sel_val = vw;
+    }
   }
 }
 
