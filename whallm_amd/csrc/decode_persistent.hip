@@ -165,6 +165,15 @@ __device__ __forceinline__ uint32_t ds_bf16_pair(float a, float b) {
 __device__ __forceinline__ uint16_t ds_bf16_bits(float v) { return (uint16_t)ds_bf16_pair(v, 0.0f); }
 __device__ __forceinline__ float bf16_round_f(float v) { return __uint_as_float(ds_bf16_pair(v, 0.0f) << 16); }
 
+// Act values travel two to a message word as 24-bit floats (sign, exponent, 15 mantissa
+// bits, rounded to nearest even) under a 16-bit epoch; phase B uses 12 significant bits
+// of w act (three E4M3 terms), so the shortened mantissa changes nothing it reads.
+__device__ __forceinline__ uint32_t f32_to_f24(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
+}
+__device__ __forceinline__ float f24_to_f32(uint32_t b) { return __uint_as_float(b << 8); }
+
 // ---- E4M3 term splitting -------------------------------------------------------
 // E8M0 exponent s that puts amax / 2^(s-127) in [128, 256) (E4M3's largest finite is
 // 448); at least 1 so the scale stays a normal number. amax 0 gives 1.
@@ -395,10 +404,13 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
         d[i] = v + dpp_f<0xB1>(v);
       }
       if (col == 0) *reinterpret_cast<float4*>(&sh.tile_out[wave][4 * grp]) = make_float4(d[0], d[1], d[2], d[3]);
-      if (tile_valid && lane < 8) {
-        const float g = sh.tile_out[wave][lane], u = sh.tile_out[wave][8 + lane];
-        ll_put_xcd<LOCAL>(&act_buf[tk * DS_SLICE + 8 * tq + lane],
-                          ((uint64_t)e_act << 32) | __float_as_uint(silu(g) * u));
+      {
+        const float g = sh.tile_out[wave][lane & 7], u = sh.tile_out[wave][8 + (lane & 7)];
+        const float a = silu(g) * u;
+        const float a_next = dpp_f<0xB1>(a);  // the odd lane's value
+        if (tile_valid && lane < 8 && !(lane & 1))
+          ll_put_xcd<LOCAL>(&act_buf[tk * (DS_SLICE / 2) + 4 * tq + lane / 2],
+                            ((uint64_t)(e_act & 0xffffu) << 48) | ((uint64_t)f32_to_f24(a_next) << 24) | f32_to_f24(a));
       }
     }
     WM_DS_TRACE(l, 3);
@@ -534,9 +546,13 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     // ---- the XCD's act slice (every expert's 64 columns); tile t wrote words 8t .. 8t+7
     uint32_t rounds = 0;
     WM_DS_TRACE(l, 2);
-    ll_gather<DS_NE_MAX * DS_SLICE / 64>(act_buf, lane, 64, c.NE * DS_SLICE, e_act, c.status, ok,
-                                         [&](int w, uint64_t v) { sh.act[w / DS_SLICE][w % DS_SLICE] = __uint_as_float((uint32_t)v); },
-                                         &rounds);
+    ll_gather<DS_NE_MAX * DS_SLICE / 128, 16>(act_buf, lane, 64, c.NE * DS_SLICE / 2, e_act, c.status, ok,
+                                              [&](int w, uint64_t v) {
+                                                const int e = w / (DS_SLICE / 2), cc = 2 * (w % (DS_SLICE / 2));
+                                                sh.act[e][cc] = f24_to_f32((uint32_t)v & 0xffffffu);
+                                                sh.act[e][cc + 1] = f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
+                                              },
+                                              &rounds);
     WM_DS_NOTE(l, 14, rounds);
     WM_DS_TRACE(l, 9);
     if (__builtin_amdgcn_readfirstlane(cancel_word) != 0) {
