@@ -572,10 +572,30 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     for (int w = 0; w < DS_CW; ++w)
       p += (sh.partb[w][0][lane] + sh.partb[w][1][lane]) + sh.partb[w][2][lane];
     WM_DS_TRACE(l, 4);
-    ll_put(&part_buf[(size_t)x * DS_H + j * DS_ROWS + lane], __float_as_uint(p), e_part);
-    float y = 0.0f;
-    ll_gather<DS_X>(part_buf + j * DS_ROWS, lane, DS_H, DS_X * DS_H, e_part, c.status, ok,
-                    [&](int i, uint64_t v) { y += __uint_as_float((uint32_t)v); }, &rounds);
+    float y;
+    {  // two rows a word as 24-bit floats under a 16-bit epoch
+      const float p_next = dpp_f<0xB1>(p);
+      if (!(lane & 1))
+        __hip_atomic_store(&part_buf[(size_t)x * (DS_H / 2) + j * (DS_ROWS / 2) + lane / 2],
+                           ((uint64_t)(e_part & 0xffffu) << 48) | ((uint64_t)f32_to_f24(p_next) << 24) | f32_to_f24(p),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // lanes 0-31 gather row pair `lane` from XCDs 0-3, lanes 32-63 from XCDs 4-7
+      float s0 = 0.0f, s1 = 0.0f;
+      const uint64_t* src = part_buf + (size_t)(4 * (lane >> 5)) * (DS_H / 2) + j * (DS_ROWS / 2) + (lane & 31);
+      ll_gather<DS_X / 2, 16>(src, 0, DS_H / 2, (DS_X / 2) * (DS_H / 2), e_part, c.status, ok, [&](int i, uint64_t v) {
+        s0 += f24_to_f32((uint32_t)v & 0xffffffu);
+        s1 += f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
+      }, &rounds);
+      // (XCDs 0-3) + (XCDs 4-7) in both halves, then row 64 j + lane from pair lane / 2
+      const auto q0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(s0), __float_as_uint(s0), false, false);
+      const auto q1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(s1), __float_as_uint(s1), false, false);
+      const float o0 = __uint_as_float(lane < 32 ? q0[1] : q0[0]), o1 = __uint_as_float(lane < 32 ? q1[1] : q1[0]);
+      const float y0 = lane < 32 ? s0 + o0 : o0 + s0, y1 = lane < 32 ? s1 + o1 : o1 + s1;
+      const int from = (lane >> 1) * 4;
+      const float a0 = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(y0)));
+      const float a1 = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(y1)));
+      y = (lane & 1) ? a1 : a0;
+    }
     WM_DS_NOTE(l, 15, rounds);
     WM_DS_TRACE(l, 12);
     r_own += bf16_round_f(y);
