@@ -206,8 +206,9 @@ struct DSShared {
   wm_decode_layer desc[DS_MAX_LAYERS];
   float gate;   // sigmoid(x . g) of the current layer
   float eps;
-  float inv;    // 1 / rms(r) of the current layer
-  float xmax;   // max |bf16(r * inv)|
+  float ssw[4];  // each wave's share of sum r^2 of the next layer's r
+  float mxw[4];  // and of max |r|
+  int r_go;      // layers whose r rows this workgroup has published (the compute waves' r polls wait for it)
   int failures;
 };
 
@@ -236,9 +237,8 @@ __device__ __forceinline__ void ds_barrier() {
 // - hi) * 16) under scale 2^(s-131). Thread t handles x[8t .. 8t+7]; x[n] with
 // n = 128 kb + 64 h + 16 g + e sits at byte 16 h + e of xb[term][kb][g], the order in
 // which the MFMA's B lanes of group g pair with the A lanes (block 4 kb + a, a = 0..3).
-__device__ __forceinline__ void ds_build_x(DSShared& sh, int tid) {
-  const float inv = sh.inv;
-  const int s_hi = e4m3_term_exponent(sh.xmax);
+__device__ __forceinline__ void ds_build_x(DSShared& sh, int tid, float inv, float xmax) {
+  const int s_hi = e4m3_term_exponent(xmax);
   const float f = pow2_biased(254 - s_hi);
   const int n0 = tid * 8;
   const float4 ra = *reinterpret_cast<const float4*>(&sh.r[n0]);
@@ -261,6 +261,51 @@ __device__ __forceinline__ void ds_build_x(DSShared& sh, int tid) {
   const int off = (kb * 4 + g) * 32 + 16 * h + e;
   *reinterpret_cast<uint2*>(&sh.xb[0][0][0][0] + off) = make_uint2(hw[0], hw[1]);
   *reinterpret_cast<uint2*>(&sh.xb[1][0][0][0] + off) = make_uint2(lw[0], lw[1]);
+}
+
+// A wave's share of the rmsnorm statistics of r (lane 0 writes; combined after the next barrier).
+__device__ __forceinline__ void ds_norm_part(DSShared& sh, float ss, float mx, int lane, int wave) {
+  ss = segment_sum<64>(ss);
+  mx = segment_max<64>(mx);
+  if (lane == 0) {
+    sh.ssw[wave] = ss;
+    sh.mxw[wave] = mx;
+  }
+}
+
+// 1 / rms(r) and max |bf16(r * inv)| from the four shares, in a fixed order, so every wave
+// of every workgroup gets the same values.
+__device__ __forceinline__ void ds_norm(const DSShared& sh, float& inv, float& xmax) {
+  const float ss = (sh.ssw[0] + sh.ssw[1]) + (sh.ssw[2] + sh.ssw[3]);
+  const float mx = fmaxf(fmaxf(sh.mxw[0], sh.mxw[1]), fmaxf(sh.mxw[2], sh.mxw[3]));
+  inv = rsqrtf(ss / (float)DS_H + sh.eps);
+  xmax = bf16_round_f(mx * inv);
+}
+
+// Wave `wave`'s quarter of the XCD's r words (bf16 triples under a 16-bit epoch) into
+// sh.r, and its share of the statistics. Every wave gathers a quarter, so each polls
+// 3 words a lane instead of one wave polling 11.
+constexpr int DS_R_SHARE = DS_J * DS_RW / 4;
+static_assert(DS_J * DS_RW % 4 == 0, "r words split over four waves");
+__device__ __forceinline__ void ds_gather_r_share(DSShared& sh, const DSCtx& c, const uint64_t* r_buf, uint32_t e_r,
+                                                  int wave, bool& ok, uint32_t* rounds) {
+  float ss = 0.0f, mx = 0.0f;
+  ll_gather<(DS_R_SHARE + 63) / 64, 16>(r_buf + wave * DS_R_SHARE, c.lane, 64, DS_R_SHARE, e_r, c.status, ok,
+                                        [&](int i, uint64_t v) {
+    const int w = wave * DS_R_SHARE + i;
+    const int jj = w / DS_RW, t = 3 * (w % DS_RW);
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      if (t + u < DS_ROWS) {
+        const float rv = bf16_bits_to_f32((uint32_t)(v >> (16 * u)) & 0xffffu);
+        sh.r[jj * DS_ROWS + t + u] = rv;
+        ss += rv * rv;
+        mx = fmaxf(mx, fabsf(rv));
+      }
+    }
+  }, rounds);
+  ds_norm_part(sh, ss, mx, c.lane, wave);
+  if (!ok) sh.failures = 1;
 }
 
 // The two roles run separate loops (so their registers do not overlap) and meet at
@@ -352,19 +397,22 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
     }
   };
 
+  bool ok = true;
   issue_a(0);
   issue_b(0);
   for (int l = 0; l < c.L; ++l) {
     const uint32_t e_act = c.base + 2 + 3 * l;
     uint64_t* act_buf = c.act_ll + ((size_t)(l & 1) * DS_X + x) * DS_NE_MAX * DS_SLICE;
-    ds_barrier();  // S0: r_l, inv, xmax in LDS
+    ds_barrier();  // S0: r_l and its statistics' shares in LDS
     WM_DS_TRACE(l, 0);
-    ds_build_x(sh, c.wave * 64 + lane);
+    float inv, xmax;
+    ds_norm(sh, inv, xmax);
+    ds_build_x(sh, c.wave * 64 + lane, inv, xmax);
     ds_barrier();  // S0b: x terms in LDS
     WM_DS_TRACE(l, 1);
     // ---- phase A: one 16-row tile over the hidden width
     {
-      const int s_hi = e4m3_term_exponent(sh.xmax);
+      const int s_hi = e4m3_term_exponent(xmax);
       // lanes of columns >= 2 feed unused outputs; a scale below 2^-127 only arises for
       // x below 2^-113, so clamping it changes nothing measurable
       const int sb = (col & 1) ? (s_hi > 4 ? s_hi - 4 : 0) : s_hi;
@@ -481,17 +529,21 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
     ds_barrier();  // S2: partials in LDS
     if (sh.failures != 0) break;  // a message wait ran out (every wave leaves here)
     issue_b(l + 1 < c.L ? l + 1 : l);
-  }
-}
-
-// rmsnorm statistics of r in LDS -> sh.inv, sh.xmax (lane 0 writes; read after the next barrier).
-__device__ __forceinline__ void ds_publish_norm(DSShared& sh, float ss, float mx, int lane) {
-  ss = segment_sum<64>(ss);
-  mx = segment_max<64>(mx);
-  const float inv = rsqrtf(ss / (float)DS_H + sh.eps);
-  if (lane == 0) {
-    sh.inv = inv;
-    sh.xmax = bf16_round_f(mx * inv);
+    // ---- this wave's quarter of r_{l+1}, once this workgroup's message wave has published
+    // its rows (so these polls do not queue beside its partial gather)
+    {
+      uint32_t spins = 0;
+      while (__hip_atomic_load(&sh.r_go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <= l) {
+        if (++spins > DS_SPIN_LIMIT) {
+          __hip_atomic_store(c.status, DS_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      const uint64_t* r_buf = c.r_ll + ((size_t)(l & 1) * DS_X + x) * DS_J * DS_RW;
+      ds_gather_r_share(sh, c, r_buf, c.base + 4 + 3 * l, wave, ok, nullptr);
+    }
   }
 }
 
@@ -517,13 +569,14 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     }
     ds_barrier();  // S0
     WM_DS_TRACE(l, 8);
-    ds_build_x(sh, DS_CW * 64 + lane);
+    float inv, xmax;
+    ds_norm(sh, inv, xmax);
+    ds_build_x(sh, DS_CW * 64 + lane, inv, xmax);
     ds_barrier();  // S0b
     // ---- shared-expert gate sigmoid(x . g); lane: x[8 (lane + 64 m) .. + 7]
     {
       float gv = 1.0f;
       if (sg) {
-        const float inv = sh.inv;
         float a = 0.0f;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -611,22 +664,9 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
       ll_put_xcd<LOCAL>(&r_buf[j * DS_RW + lane], word);
     }
     WM_DS_TRACE(l, 6);
-    float ss = 0.0f, mx = 0.0f;
-    ll_gather<(DS_J * DS_RW + 63) / 64, 16>(r_buf, lane, 64, DS_J * DS_RW, e_r, c.status, ok, [&](int w, uint64_t v) {
-      const int jj = w / DS_RW, t = 3 * (w % DS_RW);
-#pragma unroll
-      for (int u = 0; u < 3; ++u) {
-        if (t + u < DS_ROWS) {
-          const float rv = bf16_bits_to_f32((uint32_t)(v >> (16 * u)) & 0xffffu);
-          sh.r[jj * DS_ROWS + t + u] = rv;
-          ss += rv * rv;
-          mx = fmaxf(mx, fabsf(rv));
-        }
-      }
-    }, &rounds);
+    __hip_atomic_store(&sh.r_go, l + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    ds_gather_r_share(sh, c, r_buf, e_r, DS_CW, ok, &rounds);
     WM_DS_NOTE(l, 7, rounds);
-    ds_publish_norm(sh, ss, mx, lane);
-    if (!ok) sh.failures = 1;
     WM_DS_TRACE(l, 13);
   }
 }
@@ -673,6 +713,8 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   float r_own = msg ? residual[c.j * DS_ROWS + c.lane] : 0.0f;  // the message wave owns rows 64j + lane
   if (tid == 0) sh.failures = 0;
   if (tid == 0) sh.eps = eps;
+  if (tid == 0) sh.r_go = 0;
+  if (tid < 4) sh.ssw[tid] = sh.mxw[tid] = 0.0f;  // the prologue's r_0 statistics are the message wave's share
   __syncthreads();  // failures is cleared before any wave can raise it; every wave holds its epoch
   // Every launch advances the epochs by the same amount, whether it completes or not, so
   // words left by a launch that ended early never match a later launch's epochs.
@@ -729,19 +771,22 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
       ss += v[q].x * v[q].x + v[q].y * v[q].y + v[q].z * v[q].z + v[q].w * v[q].w;
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)), fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
     }
-    ds_publish_norm(sh, ss, mx, c.lane);
+    ds_norm_part(sh, ss, mx, c.lane, DS_CW);
   }
   // No barrier here: the compute waves issue layer 0's weight loads while the message wave
   // computes the statistics, which the first S0 barrier publishes.
 
   if (msg) ds_message_role<LOCAL>(sh, c, r_own);
   else ds_compute_role<LOCAL, DOWN_ROWS>(sh, c);
+  ds_barrier();  // every wave's share of r_L's statistics
   if (sh.failures != 0) return;
 
-  // ---- outputs (XCD 0's message waves): r_L and rmsnorm(r_L); sh.inv is r_L's
+  // ---- outputs (XCD 0's message waves): r_L and rmsnorm(r_L)
   if (msg && c.x == 0) {
+    float inv, xmax;
+    ds_norm(sh, inv, xmax);
     residual[c.j * DS_ROWS + c.lane] = r_own;
-    if (x_out) x_out[c.j * DS_ROWS + c.lane] = f32_to_bf16_bits(r_own * sh.inv);
+    if (x_out) x_out[c.j * DS_ROWS + c.lane] = f32_to_bf16_bits(r_own * inv);
   }
 }
 
