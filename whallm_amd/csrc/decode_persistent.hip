@@ -308,6 +308,21 @@ __device__ __forceinline__ void ds_gather_r_share(DSShared& sh, const DSCtx& c, 
   if (!ok) sh.failures = 1;
 }
 
+// Wave `wave`'s quarter of the XCD's act words (c.NE experts x 32 words, two values each)
+// into sh.act.
+__device__ __forceinline__ void ds_gather_act_share(DSShared& sh, const DSCtx& c, const uint64_t* act_buf,
+                                                    uint32_t e_act, int wave, bool& ok, uint32_t* rounds) {
+  const int total = c.NE * (DS_SLICE / 2), share = (total + 3) / 4;
+  const int first = wave * share, n = min(share, total - first);
+  ll_gather<(DS_NE_MAX * DS_SLICE / 2 / 4 + 63) / 64, 16>(act_buf + first, c.lane, 64, n, e_act, c.status, ok,
+                                                          [&](int i, uint64_t v) {
+    const int w = first + i;
+    const int e = w / (DS_SLICE / 2), cc = 2 * (w % (DS_SLICE / 2));
+    sh.act[e][cc] = f24_to_f32((uint32_t)v & 0xffffffu);
+    sh.act[e][cc + 1] = f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
+  }, rounds);
+}
+
 // The two roles run separate loops (so their registers do not overlap) and meet at
 // the same four barriers per layer:
 //   S0: r_l and its rmsnorm statistics in LDS -> every wave builds a quarter of x
@@ -461,6 +476,8 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
                             ((uint64_t)(e_act & 0xffffu) << 48) | ((uint64_t)f32_to_f24(a_next) << 24) | f32_to_f24(a));
       }
     }
+    ds_gather_act_share(sh, c, act_buf, e_act, wave, ok, nullptr);
+    if (!ok) sh.failures = 1;
     WM_DS_TRACE(l, 3);
     ds_barrier();  // S1: act slice and shared gate in LDS
     WM_DS_TRACE(l, 5);
@@ -599,13 +616,7 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
     // ---- the XCD's act slice (every expert's 64 columns); tile t wrote words 8t .. 8t+7
     uint32_t rounds = 0;
     WM_DS_TRACE(l, 2);
-    ll_gather<DS_NE_MAX * DS_SLICE / 128, 16>(act_buf, lane, 64, c.NE * DS_SLICE / 2, e_act, c.status, ok,
-                                              [&](int w, uint64_t v) {
-                                                const int e = w / (DS_SLICE / 2), cc = 2 * (w % (DS_SLICE / 2));
-                                                sh.act[e][cc] = f24_to_f32((uint32_t)v & 0xffffffu);
-                                                sh.act[e][cc + 1] = f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
-                                              },
-                                              &rounds);
+    ds_gather_act_share(sh, c, act_buf, e_act, DS_CW, ok, &rounds);
     WM_DS_NOTE(l, 14, rounds);
     WM_DS_TRACE(l, 9);
     if (__builtin_amdgcn_readfirstlane(cancel_word) != 0) {
