@@ -741,10 +741,11 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
       ll_put(&dst[K + c.lane], __float_as_uint(w), e_route);
     }
   }
-  if (msg) {
+  {  // every wave gathers a quarter of the route words
     const uint64_t* src = c.route_ll + (size_t)c.x * L * rw;
-    for (int s = 0; s < L * rw; s += 64 * 16)
-      ll_gather<16>(src, s + c.lane, 64, L * rw, e_route, c.status, ok, [&](int i, uint64_t word) {
+    const int quarter = (L * rw + 3) / 4, end = min((c.wave + 1) * quarter, L * rw);
+    for (int s = c.wave * quarter; s < end; s += 64 * 4)
+      ll_gather<4>(src, s + c.lane, 64, end, e_route, c.status, ok, [&](int i, uint64_t word) {
         const uint32_t v = (uint32_t)word;
         const int l = i / rw, k = i - l * rw;
         if (k < K) sh.slot[l][k] = (int)v;
