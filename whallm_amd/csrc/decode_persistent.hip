@@ -24,7 +24,9 @@
 // Each exchange has low fan-in (act: within the XCD; partials: the 8 workgroups
 // sharing a row block; r: within the XCD). Messages are 64-bit words carrying the
 // value and an epoch, written and read with agent-scope relaxed atomics, so a
-// reader polls the data itself: no flags, no grid barriers, no L2-wide fences.
+// reader polls the data itself: no flags, no grid barriers, no L2-wide fences. A
+// gather costs about the words each polling wave reads per lane, so act values and
+// partials travel two to a word and the act and r gathers are spread over the waves.
 // Weight loads run a phase ahead: the A tile of layer l+1 is in flight from the end
 // of phase A(l), the down rows of layer l+1 from the end of layer l's phase B.
 //
@@ -143,10 +145,10 @@ __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int s
 
 // Phase timestamps and notes for the profiling build of whallm_amd.phase_trace (both expand
 // to nothing in the library). Points of the compute waves: 0 S0, 1 S0b, 3 phase A done
-// (act published), 5 S1, 4 next A tile issued, 6 phase B done; of the message wave: 8 S0,
-// 2 act poll start, 9 act gathered, 10 S1, 11 S2, 4 partial published, 12 partials
-// gathered, 6 r published, 13 r gathered; notes: 14 / 15 / 7 = re-poll rounds of the act,
-// partial and r gathers.
+// (the wave's act gathered), 5 shared gate ready, 4 next A tile issued, 6 phase B done; of
+// the message wave: 8 S0, 2 gate published, 11 S2, 4 partial published, 12 partials
+// gathered, 6 r published, 13 r gathered; notes: 15 / 7 = re-poll rounds of the partial and
+// r gathers.
 #ifndef WM_DS_TRACE
 #define WM_DS_TRACE(layer, point)
 #endif
@@ -209,6 +211,7 @@ struct DSShared {
   float ssw[4];  // each wave's share of sum r^2 of the next layer's r
   float mxw[4];  // and of max |r|
   int r_go;      // layers whose r rows this workgroup has published (the compute waves' r polls wait for it)
+  int gate_l;    // layers whose shared gate is in sh.gate (the wave with the shared expert waits for it)
   int failures;
 };
 
@@ -308,32 +311,33 @@ __device__ __forceinline__ void ds_gather_r_share(DSShared& sh, const DSCtx& c, 
   if (!ok) sh.failures = 1;
 }
 
-// Wave `wave`'s quarter of the XCD's act words (c.NE experts x 32 words, two values each)
-// into sh.act.
-__device__ __forceinline__ void ds_gather_act_share(DSShared& sh, const DSCtx& c, const uint64_t* act_buf,
-                                                    uint32_t e_act, int wave, bool& ok, uint32_t* rounds) {
-  const int total = c.NE * (DS_SLICE / 2), share = (total + 3) / 4;
-  const int first = wave * share, n = min(share, total - first);
-  ll_gather<(DS_NE_MAX * DS_SLICE / 2 / 4 + 63) / 64, 16>(act_buf + first, c.lane, 64, n, e_act, c.status, ok,
-                                                          [&](int i, uint64_t v) {
+// The act words of the experts compute wave `wave`'s phase B reads (4 wave .. 4 wave + 3,
+// 32 words each) into sh.act; no other wave reads them, so no barrier is needed.
+__device__ __forceinline__ void ds_gather_act_own(DSShared& sh, const DSCtx& c, const uint64_t* act_buf,
+                                                  uint32_t e_act, int wave, bool& ok) {
+  const int first = wave * 4 * (DS_SLICE / 2), n = min(4 * (DS_SLICE / 2), c.NE * (DS_SLICE / 2) - first);
+  ll_gather<2, 16>(act_buf + first, c.lane, 64, n, e_act, c.status, ok, [&](int i, uint64_t v) {
     const int w = first + i;
     const int e = w / (DS_SLICE / 2), cc = 2 * (w % (DS_SLICE / 2));
     sh.act[e][cc] = f24_to_f32((uint32_t)v & 0xffffffu);
     sh.act[e][cc + 1] = f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
-  }, rounds);
+  });
 }
 
 // The two roles run separate loops (so their registers do not overlap) and meet at
-// the same four barriers per layer:
-//   S0: r_l and its rmsnorm statistics in LDS -> every wave builds a quarter of x
-//   S0b: x terms in LDS -> compute waves: phase A (one tile each), publish act
-//                          message wave: shared gate, gather the XCD's act slice
-//   S1: act ready  -> compute waves: prefetch the A tile of l+1, phase B partials into
-//                     LDS, prefetch B(l+1)
+// the same three barriers per layer:
+//   S0: r_l and its statistics' shares in LDS -> every wave builds a quarter of x
+//   S0b: x terms in LDS -> compute waves: phase A (one tile each), publish act, gather
+//                          the act of the four experts their phase B reads, prefetch
+//                          the A tile of l+1, phase B partials into LDS (the wave with
+//                          the shared expert first waits for the gate's LDS flag)
+//                          message wave: shared gate, its flag
 //   S2: partials   -> (every wave leaves here if a message wait ran out)
+//                     compute waves: prefetch B(l+1), wait for the message wave's r
+//                     publish (LDS counter), gather a quarter of the XCD's r
 //                     message wave: publish the row block's partial, gather the 8
-//                     XCDs' partials, r += bf16(sum), publish r, gather the XCD's r
-// Compute waves never wait on a message. One wave per SIMD.
+//                     XCDs' partials, r += bf16(sum), publish r, gather its quarter
+// One wave per SIMD.
 template <bool LOCAL, bool DOWN_ROWS>
 __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
   const int lane = c.lane, wave = c.wave, x = c.x, j = c.j, K = c.K, NE = c.NE;
@@ -476,14 +480,25 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
                             ((uint64_t)(e_act & 0xffffu) << 48) | ((uint64_t)f32_to_f24(a_next) << 24) | f32_to_f24(a));
       }
     }
-    ds_gather_act_share(sh, c, act_buf, e_act, wave, ok, nullptr);
+    ds_gather_act_own(sh, c, act_buf, e_act, wave, ok);
     if (!ok) sh.failures = 1;
     WM_DS_TRACE(l, 3);
-    ds_barrier();  // S1: act slice and shared gate in LDS
+    if (4 * wave <= K && K < 4 * wave + 4) {  // this wave's K-steps include the shared expert
+      uint32_t spins = 0;
+      while (__hip_atomic_load(&sh.gate_l, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= l) {
+        if (++spins > DS_SPIN_LIMIT) {
+          __hip_atomic_store(c.status, DS_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = false;
+          sh.failures = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
     WM_DS_TRACE(l, 5);
-    // The A tile of l + 1 is issued after S1, not before: issued earlier, its loads sit
-    // in the CU's memory queue ahead of the message wave's act poll and delay it by their
-    // whole transfer (measured: the act gather ends 1.5 us later per layer)
+    // The A tile of l + 1 is issued after this wave's act gather, not before: issued
+    // earlier, its loads sit in the CU's memory queue ahead of the act polls and delay them
+    // by their whole transfer (measured: the act gather ended 1.5 us later per layer)
     issue_a(l + 1 < c.L ? l + 1 : l);
     WM_DS_TRACE(l, 4);
     // ---- phase B: split-K partials of rows 64 j .. 64 j + 63 over this wave's K-steps
@@ -611,22 +626,19 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
         a = segment_sum<64>(a);
         gv = 1.0f / (1.0f + __expf(-a));
       }
-      if (lane == 0) sh.gate = gv;
+      if (lane == 0) {
+        sh.gate = gv;
+        __hip_atomic_store(&sh.gate_l, l + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
     }
-    // ---- the XCD's act slice (every expert's 64 columns); tile t wrote words 8t .. 8t+7
     uint32_t rounds = 0;
     WM_DS_TRACE(l, 2);
-    ds_gather_act_share(sh, c, act_buf, e_act, DS_CW, ok, &rounds);
-    WM_DS_NOTE(l, 14, rounds);
-    WM_DS_TRACE(l, 9);
     if (__builtin_amdgcn_readfirstlane(cancel_word) != 0) {
       // leave after this layer's phase B; the others see the status word in their next wait
       if (lane == 0) __hip_atomic_store(c.status, DS_CANCELLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ok = false;
     }
     if (!ok) sh.failures = 1;
-    ds_barrier();  // S1
-    WM_DS_TRACE(l, 10);
     ds_barrier();  // S2
     if (sh.failures != 0) break;
     WM_DS_TRACE(l, 11);
@@ -725,6 +737,7 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   if (tid == 0) sh.failures = 0;
   if (tid == 0) sh.eps = eps;
   if (tid == 0) sh.r_go = 0;
+  if (tid == 0) sh.gate_l = 0;
   if (tid < 4) sh.ssw[tid] = sh.mxw[tid] = 0.0f;  // the prologue's r_0 statistics are the message wave's share
   __syncthreads();  // failures is cleared before any wave can raise it; every wave holds its epoch
   // Every launch advances the epochs by the same amount, whether it completes or not, so

@@ -28,11 +28,11 @@ TRACE_LIB = TRACE_DIR / "libwhallm_moe_trace.so"
 HEADER = hip_build.CSRC / "phase_trace.h"
 
 # point -> (wave role, name); compute waves 0..2, message wave 3
-POINTS = [(0, 0, "compute: S0 (r and its norm in LDS)"), (0, 3, "compute: phase A done (act published)"),
-          (3, 2, "message: act poll start"), (3, 9, "message: act gathered"),
-          (0, 4, "compute: S1 passed, next A tile issued"), (0, 6, "compute: phase B done"), (3, 4, "message: partial published"),
+POINTS = [(0, 0, "compute: S0 (r and its norm in LDS)"), (0, 3, "compute: phase A done, own act gathered"),
+          (3, 2, "message: shared gate published"),
+          (0, 4, "compute: next A tile issued"), (0, 6, "compute: phase B done"), (3, 4, "message: partial published"),
           (3, 12, "message: partials gathered"), (3, 6, "message: r published"), (3, 13, "message: r gathered")]
-NOTES = [(14, "act"), (15, "partial"), (7, "r")]
+NOTES = [(15, "partial"), (7, "r")]
 
 
 def build_traced(source: Path | None = None) -> Path:
