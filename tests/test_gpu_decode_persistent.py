@@ -168,7 +168,8 @@ def test_decode_served_from_the_slot_cache(device):
     """Tables of a slot cache (refilled between tokens) are read in place: each token's routed
     experts are acquired per layer, then one launch runs the stack; the result equals the
     fully resident stack's bit for bit, and an expert that was not acquired ends the launch
-    with status 3 before any layer runs (residual unchanged, state reset)."""
+    with status 3 before any layer runs (residual unchanged, state reset), for a missing
+    expert of layer 1 and of layer 2."""
     layers, experts = 3, 64
     chain, cache, stack = _slot_cache_chain(device, layers, experts, seed=22)
     rows = PersistentDecodeStack(chain.dev, chain.dev_shared, chain.dev_gates, k=K, down_layout="rows")
@@ -183,21 +184,23 @@ def test_decode_served_from_the_slot_cache(device):
         stack(lt, a)
         rows(lt, b)
         assert torch.equal(a, b), token
-    # a token whose experts were never acquired for layer 1
-    logits, r0 = chain.inputs()
-    idx, _ = M.route_softmax_topk(logits[1][None], K)
-    cache.acquire_files({l: sorted(int(e) for e in M.route_softmax_topk(logits[l][None], K)[0][0]) for l in (0, 2)})
-    missing = [int(e) for e in idx[0] if int(cache.map[1][int(e)]) < 0]
-    assert missing, "the test expects some of layer 1's experts to be missing"
-    r = torch.from_numpy(r0.copy()).to(device)
-    with pytest.raises(DecodeStackError, match="not resident"):
-        stack(torch.from_numpy(logits).to(device), r)
-    assert torch.equal(r.cpu(), torch.from_numpy(r0))
-    cache.acquire_files({l: sorted(int(e) for e in M.route_softmax_topk(logits[l][None], K)[0][0])
-                         for l in range(layers)})
-    stack(torch.from_numpy(logits).to(device), r)      # the state was reset: the next launch runs
-    want_r, _ = chain.oracle(logits, r0)
-    close(r.cpu().numpy(), want_r, "after a non-resident launch")
+    # a token whose experts were never acquired for layer 1, then one for layer 2
+    for gap in (1, 2):
+        logits, r0 = chain.inputs()
+        idx, _ = M.route_softmax_topk(logits[gap][None], K)
+        cache.acquire_files({l: sorted(int(e) for e in M.route_softmax_topk(logits[l][None], K)[0][0])
+                             for l in range(layers) if l != gap})
+        missing = [int(e) for e in idx[0] if int(cache.map[gap][int(e)]) < 0]
+        assert missing, f"the test expects some of layer {gap}'s experts to be missing"
+        r = torch.from_numpy(r0.copy()).to(device)
+        with pytest.raises(DecodeStackError, match="not resident"):
+            stack(torch.from_numpy(logits).to(device), r)
+        assert torch.equal(r.cpu(), torch.from_numpy(r0)), gap
+        cache.acquire_files({l: sorted(int(e) for e in M.route_softmax_topk(logits[l][None], K)[0][0])
+                             for l in range(layers)})
+        stack(torch.from_numpy(logits).to(device), r)      # the state was reset: the next launch runs
+        want_r, _ = chain.oracle(logits, r0)
+        close(r.cpu().numpy(), want_r, f"after a launch missing an expert of layer {gap}")
 
 
 def test_persistent_cancel_and_recovery(device):
