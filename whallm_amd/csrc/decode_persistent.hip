@@ -50,7 +50,6 @@ constexpr int DS_SLICE = DS_I / DS_X; // 64 intermediate columns per XCD
 constexpr int DS_ROWS = DS_H / DS_J;  // 64 output rows per workgroup
 constexpr int DS_NE_MAX = 12;         // routed + shared experts per layer
 constexpr int DS_KB = DS_H / 128;     // K-steps of a phase-A tile (128 per MFMA)
-constexpr int DS_KB_B = DS_NE_MAX / 2;  // K-steps of phase B (two 64-wide expert slices each)
 constexpr uint32_t DS_SPIN_LIMIT = 1u << 20;
 // Status word values (0 = healthy): a message wait ran out, the caller's cancel word was
 // set, a selected expert is not resident (its slot map entry is negative).
@@ -585,12 +584,12 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
   bool ok = true;
   for (int l = 0; l < c.L; ++l) {
     const int par = l & 1;
-    const uint32_t e_act = c.base + 2 + 3 * l, e_part = c.base + 3 + 3 * l, e_r = c.base + 4 + 3 * l;
-    uint64_t* act_buf = c.act_ll + ((size_t)par * DS_X + x) * DS_NE_MAX * DS_SLICE;
+    const uint32_t e_part = c.base + 3 + 3 * l, e_r = c.base + 4 + 3 * l;
     uint64_t* part_buf = c.part_ll + (size_t)par * DS_X * DS_H;
     uint64_t* r_buf = c.r_ll + ((size_t)par * DS_X + x) * DS_J * DS_RW;
-    // the cancel word is read at the top of the layer and looked at once the act gather
-    // below has waited (loads complete in order), so the read adds no wait of its own
+    // the cancel word is read at the top of the layer and looked at after the shared gate,
+    // whose loads are issued after it (loads complete in order), so the read adds no wait of
+    // its own
     int32_t cancel_word = 0;
     if (c.cancel && lane == 0) cancel_word = __hip_atomic_load(c.cancel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const uint8_t* sg = (const uint8_t*)sh.desc[l].shared_gate;
@@ -658,7 +657,7 @@ __device__ __forceinline__ void ds_message_role(DSShared& sh, const DSCtx& c, fl
       // lanes 0-31 gather row pair `lane` from XCDs 0-3, lanes 32-63 from XCDs 4-7
       float s0 = 0.0f, s1 = 0.0f;
       const uint64_t* src = part_buf + (size_t)(4 * (lane >> 5)) * (DS_H / 2) + j * (DS_ROWS / 2) + (lane & 31);
-      ll_gather<DS_X / 2, 16>(src, 0, DS_H / 2, (DS_X / 2) * (DS_H / 2), e_part, c.status, ok, [&](int i, uint64_t v) {
+      ll_gather<DS_X / 2, 16>(src, 0, DS_H / 2, (DS_X / 2) * (DS_H / 2), e_part, c.status, ok, [&](int, uint64_t v) {
         s0 += f24_to_f32((uint32_t)v & 0xffffffu);
         s1 += f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
       }, &rounds);
