@@ -28,13 +28,14 @@ __global__ void __launch_bounds__(256) combine_pairs_kernel(const uint16_t* __re
       if (j0 + q < k) v[q] = reinterpret_cast<const uint4*>(rows + ((int64_t)t * k + j0 + q) * hidden)[c8];
 #pragma unroll
     for (int q = 0; q < BATCH; ++q) {
-      if (j0 + q >= k) break;
-      const float w = weights[(int64_t)t * k + j0 + q];
-      const uint32_t u[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+      if (j0 + q < k) {  // pairs in order, as loaded
+        const float w = weights[(int64_t)t * k + j0 + q];
+        const uint32_t u[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        acc[2 * m] = fmaf(w, bf16_bits_to_f32(u[m] & 0xffffu), acc[2 * m]);
-        acc[2 * m + 1] = fmaf(w, bf16_bits_to_f32(u[m] >> 16), acc[2 * m + 1]);
+        for (int m = 0; m < 4; ++m) {
+          acc[2 * m] = fmaf(w, bf16_bits_to_f32(u[m] & 0xffffu), acc[2 * m]);
+          acc[2 * m + 1] = fmaf(w, bf16_bits_to_f32(u[m] >> 16), acc[2 * m + 1]);
+        }
       }
     }
   }

@@ -221,7 +221,7 @@ __global__ void __launch_bounds__(MTP_THREADS) mtp_reject_sample_kernel(const fl
     scan[threadIdx.x] = w;
     __syncthreads();
     for (int off = 1; off < MTP_THREADS; off <<= 1) {  // inclusive scan
-      const float add = threadIdx.x >= off ? scan[threadIdx.x - off] : 0.0f;
+      const float add = (int)threadIdx.x >= off ? scan[threadIdx.x - off] : 0.0f;
       __syncthreads();
       scan[threadIdx.x] += add;
       __syncthreads();

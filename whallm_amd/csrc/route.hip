@@ -224,9 +224,10 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(const uint4* __restric
   for (int r = 0; r < LR_ROWS; ++r) {
 #pragma unroll
     for (int t = 0; t < TMAX; ++t) {
-      if (t >= tokens) break;
-      const float v = segment_sum<64>(acc[r][t]);
-      if (lane == 0 && o0 + r < outputs) out[(int64_t)t * outputs + o0 + r] = v;
+      if (t < tokens) {  // uniform
+        const float v = segment_sum<64>(acc[r][t]);
+        if (lane == 0 && o0 + r < outputs) out[(int64_t)t * outputs + o0 + r] = v;
+      }
     }
   }
 }
