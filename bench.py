@@ -37,6 +37,27 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def capture_steps(device, body, n: int):
+    """One graph per step input: body(j) runs the workload on step j's inputs where they lie
+    in HBM, so a timed step replays graph j and stages nothing. The graphs share one memory
+    pool (replays are stream-ordered); an eager run on a side stream comes first."""
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        body(0)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize(device)
+    graphs, pool = [], None
+    for j in range(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=pool):
+            body(j)
+        pool = g.pool()
+        graphs.append(g)
+    torch.cuda.synchronize(device)
+    return graphs
+
+
 # ----------------------------------------------------------------------------- workloads
 
 class DecodeStack:
@@ -70,7 +91,7 @@ class DecodeStack:
         self.residual = torch.empty(tokens, hidden, dtype=torch.float32, device=device)
         self.x_out = torch.empty(tokens, hidden, dtype=torch.bfloat16, device=device)
         self.gen = g
-        self.graph = None
+        self.graphs = None
 
     # Bytes every step must move: 11 expert blobs per layer-token (10 routed + shared)
     # plus the logits row (fp32) and the token's input and output rows (bf16).
@@ -118,24 +139,17 @@ class DecodeStack:
         self.check()
         return total / launches
 
+    def _body_at(self, j):
+        if self.impl == "persistent":
+            self.stack(self.step_logits[j], self.step_embed[j].view(-1), self.x_out.view(-1), check=False)
+        else:
+            self.stack(self.step_logits[j], self.step_embed[j], self.x_out)
+
     def capture(self):
-        self.logits.copy_(self.step_logits[0])
-        self.residual.copy_(self.step_embed[0])
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            self._body()
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        torch.cuda.synchronize(self.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._body()
-        torch.cuda.synchronize(self.device)
+        self.graphs = capture_steps(self.device, self._body_at, len(self.step_logits))
 
     def step(self, i):
-        self.logits.copy_(self.step_logits[i])
-        self.residual.copy_(self.step_embed[i])
-        self.graph.replay()
+        self.graphs[i].replay()
 
     def config(self):
         return {"workload": "c2-decode: Qwen3-Next-style MXFP4 MoE decode, 48-layer stack, 1 token/step",
@@ -334,7 +348,7 @@ class FP8Layer:
             self.run_experts, self.run_shared = self.experts, self.shared
         self.bias = torch.randn(experts, device=device, generator=g) * 0.1
         self.gen = g
-        self.graph = None
+        self.graphs = None
 
     def expert_bytes(self):
         return 3 * self.H * self.I + 4 * (2 * self.I // 128) * (self.H // 128) + 4 * (self.H // 128) * (self.I // 128)
@@ -354,34 +368,18 @@ class FP8Layer:
         n = min(steps, 4) if self.T > 1 else steps
         self.step_logits = torch.randn(n, self.T, self.E, device=self.device, generator=self.gen)
         self.step_x = torch.randn(n, self.T, self.H, device=self.device, generator=self.gen).to(torch.bfloat16)
-        self.logits = torch.empty(self.T, self.E, device=self.device)
-        self.x = torch.empty(self.T, self.H, dtype=torch.bfloat16, device=self.device)
 
-    def _body(self):
+    def _body_at(self, j):
         import whallm_amd as wa
-        idx, w = wa.route_scored(self.logits, self.bias, self.K, func="sigmoid", route_scale=2.5, n_groups=8,
-                                 topk_groups=4)
-        self.y = wa.moe_fp8(self.x, idx, w, self.run_experts, self.run_shared, None)
+        idx, w = wa.route_scored(self.step_logits[j], self.bias, self.K, func="sigmoid", route_scale=2.5,
+                                 n_groups=8, topk_groups=4)
+        self.y = wa.moe_fp8(self.step_x[j], idx, w, self.run_experts, self.run_shared, None)
 
     def capture(self):
-        self.logits.copy_(self.step_logits[0])
-        self.x.copy_(self.step_x[0])
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            self._body()
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        torch.cuda.synchronize(self.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._body()
-        torch.cuda.synchronize(self.device)
+        self.graphs = capture_steps(self.device, self._body_at, len(self.step_logits))
 
     def step(self, i):
-        j = i % len(self.step_logits)
-        self.logits.copy_(self.step_logits[j])
-        self.x.copy_(self.step_x[j])
-        self.graph.replay()
+        self.graphs[i % len(self.graphs)].replay()
 
     def config(self):
         return {"workload": f"{self.name}: DeepSeek-V3-style FP8 MoE layer, {self.T} token(s)/step",
@@ -442,7 +440,7 @@ class MtpVerify:
         from whallm_amd.verify import VerifyStep
         self.verify = VerifyStep(self.layers, self.shared, self.bias, self.head, k=k)
         self.gen = g
-        self.graph = None
+        self.graphs = None
 
     def expert_bytes(self):
         return 3 * self.H * self.I + 4 * (2 * self.I // 128) * (self.H // 128) + 4 * (self.H // 128) * (self.I // 128)
@@ -458,32 +456,17 @@ class MtpVerify:
     def prepare_inputs(self, steps):
         self.step_logits = torch.randn(steps, self.L, self.T, self.E, device=self.device, generator=self.gen)
         self.step_r = torch.randn(steps, self.T, self.H, device=self.device, generator=self.gen)
-        self.logits = torch.empty(self.L, self.T, self.E, device=self.device)
-        self.r = torch.empty(self.T, self.H, device=self.device)
         self.drafts = torch.zeros(self.T - 1, dtype=torch.int32, device=self.device)
 
-    def _body(self):
+    def _body_at(self, j):
         # the package's verify step: MoE layers, the LM head in fp32 (wm_linear_bf16), acceptance
-        self.accept, self.vocab_logits = self.verify(self.logits, self.r, self.drafts)
+        self.accept, self.vocab_logits = self.verify(self.step_logits[j], self.step_r[j], self.drafts)
 
     def capture(self):
-        self.logits.copy_(self.step_logits[0])
-        self.r.copy_(self.step_r[0])
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            self._body()
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        torch.cuda.synchronize(self.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._body()
-        torch.cuda.synchronize(self.device)
+        self.graphs = capture_steps(self.device, self._body_at, len(self.step_logits))
 
     def step(self, i):
-        self.logits.copy_(self.step_logits[i])
-        self.r.copy_(self.step_r[i])
-        self.graph.replay()
+        self.graphs[i].replay()
 
     def accept_ms(self, launches: int) -> float:
         """Device time of the acceptance kernels alone (HIP events around direct launches)."""
