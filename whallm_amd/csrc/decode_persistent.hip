@@ -126,7 +126,8 @@ __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int s
       ok = false;
       break;
     }
-    __builtin_amdgcn_s_sleep(2);  // leave the CU's memory pipeline to the weight streams
+    // no sleep between rounds: each round already waits for its loads to return (a 64- or
+    // 128-clock pause there measured the same or up to 3% slower)
 #pragma unroll
     for (int m = 0; m < N; ++m) {
       int i = first + m * stride;
