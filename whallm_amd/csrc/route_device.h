@@ -115,10 +115,10 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 // Order-preserving 32-bit key of a score: a larger value has a larger key, +0 and -0 share
 // one (they compare equal), and NaN gets 0, below every number, so it is never selected.
 __device__ __forceinline__ uint32_t topk_key(float v) {
-  const float c = v + 0.0f;  // -0 -> +0
-  const uint32_t u = __float_as_uint(c);
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0u;  // -0 -> +0 on the bits (no reliance on float semantics)
   const uint32_t key = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return c == c ? key : 0u;
+  return (u & 0x7fffffffu) > 0x7f800000u ? 0u : key;  // NaN -> 0
 }
 __device__ __forceinline__ float topk_value(uint32_t key) {
   return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
