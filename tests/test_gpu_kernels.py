@@ -73,6 +73,30 @@ def test_route_softmax_topk_indices_exact(device, tokens, experts, k):
         np.testing.assert_allclose(_np(probs), p / p.sum(-1, keepdims=True), rtol=2e-6, atol=1e-8)
 
 
+@pytest.mark.parametrize("experts,k", [(512, 10), (100, 4), (64, 8)])
+def test_route_softmax_topk_signed_zero_and_masked_logits(device, experts, k):
+    """Ties between +0 and -0 (equal values: the lower index wins), masked experts (-inf
+    logits) and rows whose top k must include masked experts (ties among -inf, again to the
+    lower index): indices equal the oracle's, weights match (masked ones are 0)."""
+    rng = np.random.default_rng(experts + k)
+    logits = rng.standard_normal((6, experts)).astype(np.float32)
+    logits[0] = 0.0
+    logits[0, rng.choice(experts, experts // 2, replace=False)] = -0.0
+    logits[1, rng.choice(experts, experts // 2, replace=False)] = -np.inf
+    logits[2] = -np.inf
+    logits[2, rng.choice(experts, k - 2, replace=False)] = rng.standard_normal(k - 2)
+    logits[3] = np.where(rng.random(experts) < 0.5, np.float32(0.0), np.float32(-0.0))
+    logits[3, ::7] = 0.5
+    logits[4] = np.round(logits[4])
+    logits[4, ::3] = -0.0
+    logits[5, ::2] = -np.inf
+    for norm in (True, False):
+        idx, w = wa.route_softmax_topk(torch.from_numpy(logits).to(device), k, norm)
+        want_idx, want_w = M.route_softmax_topk(logits, k, norm)
+        np.testing.assert_array_equal(_np(idx), want_idx)
+        np.testing.assert_allclose(_np(w), want_w, rtol=2e-6, atol=1e-7)
+
+
 def test_route_softmax_c1_router_linear(device):
     # C1: router weight bf16 N(0, 0.02) [64, 1024], x bf16 N(0, 1) [16, 1024], seed 0.
     rng = np.random.default_rng(0)
