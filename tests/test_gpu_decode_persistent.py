@@ -55,16 +55,16 @@ def test_repack_down_slices_bytes(device):
 
 
 class Chain:
-    def __init__(self, device, layers, experts, seed, down_layout="slices"):
+    def __init__(self, device, layers, experts, seed, down_layout="slices", k=K):
         rng = np.random.default_rng(seed)
-        self.L, self.E = layers, experts
+        self.L, self.E, self.k = layers, experts, k
         self.arrays = [S.mxfp4_experts_np(rng, experts, H, I) for _ in range(layers)]
         self.shared = [S.mxfp4_experts_np(rng, 1, H, I) for _ in range(layers)]
         self.gates = [S.bf16_normal_np(rng, (H,), 0.02) for _ in range(layers)]
         self.dev = [S.experts_to_device(a, device) for a in self.arrays]
         self.dev_shared = [S.experts_to_device(a, device) for a in self.shared]
         self.dev_gates = [S.bf16_bits_to_tensor(g, device) for g in self.gates]
-        self.stack = PersistentDecodeStack(self.dev, self.dev_shared, self.dev_gates, k=K, down_layout=down_layout)
+        self.stack = PersistentDecodeStack(self.dev, self.dev_shared, self.dev_gates, k=k, down_layout=down_layout)
         self.rng = rng
 
     def inputs(self):
@@ -74,7 +74,7 @@ class Chain:
 
     def layer_y(self, l, logits, x):
         """The oracle's MoE output of layer l for the bf16 input x [1, H]."""
-        idx, w = M.route_softmax_topk(logits[l][None], K)
+        idx, w = M.route_softmax_topk(logits[l][None], self.k)
         a = self.arrays[l]
         routed = np.stack([M.expert_ffn(x, M.MXFP4Expert(a["gate_up"][e], a["gate_up_scales"][e], a["down"][e],
                                                           a["down_scales"][e]))[0] for e in idx[0]])[None]
@@ -120,6 +120,23 @@ def test_persistent_decode_matches_oracle_chain(device, layers, experts, calls):
             want_r, want_x = chain.oracle(logits, r0)
             close(residual.cpu().numpy(), want_r, f"residual call {call}")
             close(x_out.float().cpu().numpy(), want_x, f"x_out call {call}")
+
+
+@pytest.mark.parametrize("k,experts", [(1, 64), (2, 64), (3, 64), (4, 64), (7, 64), (8, 512), (11, 64), (11, 512)])
+def test_persistent_decode_top_k(device, k, experts):
+    """Every top-k the kernel takes (1..11 routed experts + the shared one): the experts of a
+    layer are split over the compute waves four at a time (act gather and phase B), so k
+    decides how many waves hold experts and which holds the shared one."""
+    chain = Chain(device, 3, experts, seed=100 + k, k=k)
+    for call in range(2):
+        logits, r0 = chain.inputs()
+        residual = torch.from_numpy(r0.copy()).to(device)
+        x_out = torch.empty(H, dtype=torch.bfloat16, device=device)
+        chain.stack(torch.from_numpy(logits).to(device), residual, x_out)
+        assert chain.stack.status() == 0
+        want_r, want_x = chain.oracle(logits, r0)
+        close(residual.cpu().numpy(), want_r, f"k {k} residual call {call}")
+        close(x_out.float().cpu().numpy(), want_x, f"k {k} x_out call {call}")
 
 
 def test_persistent_decode_agrees_with_per_layer_path(device):
