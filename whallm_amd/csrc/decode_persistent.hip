@@ -506,9 +506,13 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
       ds_v4f accb[4];
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) accb[rt] = ds_v4f{0.f, 0.f, 0.f, 0.f};
+      // both K-steps' B operands are staged first, so one LDS write-read round trip serves
+      // all eight MFMAs
+      int sbs[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int kb = 2 * wave + i;
+        sbs[i] = 0;
         if (2 * kb < NE) {
           // B operand: w_e act_e as three E4M3 terms. A B lane's scale covers the same
           // 32-value K block as the A lanes of its group (block a = expert 2 kb + a / 2,
@@ -535,11 +539,20 @@ __device__ __forceinline__ void ds_compute_role(DSShared& sh, const DSCtx& c) {
           *reinterpret_cast<uint16_t*>(st + 0 * 128 + at) = (uint16_t)c0;
           *reinterpret_cast<uint16_t*>(st + 1 * 128 + at) = (uint16_t)c1;
           *reinterpret_cast<uint16_t*>(st + 2 * 128 + at) = (uint16_t)c2;
+          sbs[i] = s;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int kb = 2 * wave + i;
+        if (2 * kb < NE) {
+          const uint8_t* st = &sh.bstage[wave][i][0][0][0];
           const int term = col < 3 ? col : 0;  // columns >= 3 feed unused outputs
           const uint4 blo = *reinterpret_cast<const uint4*>(st + term * 128 + grp * 32);
           const uint4 bhi = *reinterpret_cast<const uint4*>(st + term * 128 + grp * 32 + 16);
           const ds_v8i bv = {(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w,
                              (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
+          const int s = sbs[i];
           const int sb = s > 4 * term ? s - 4 * term : 0;
 #pragma unroll
           for (int rt = 0; rt < 4; ++rt) {
