@@ -111,6 +111,8 @@ __global__ void __launch_bounds__(1024) permute_offsets_kernel(const int32_t* __
                                                               int32_t* __restrict__ tiles,
                                                               int32_t* __restrict__ tile_count) {
   __shared__ int32_t wave_total[16];
+  __shared__ int32_t tile_start[PERMUTE_MAX_EXPERTS + 1];
+  __shared__ int32_t row_start[PERMUTE_MAX_EXPERTS];
   const int e = threadIdx.x;
   const int32_t mine = e < experts ? totals[e] : 0;
   const int32_t my_tiles = (mine + tile_rows - 1) / tile_rows;
@@ -119,14 +121,27 @@ __global__ void __launch_bounds__(1024) permute_offsets_kernel(const int32_t* __
   if (e < experts) {
     const int32_t row0 = rows_incl - mine, tile0 = tiles_incl - my_tiles;
     offsets[e] = row0;
-    for (int32_t q = 0; q < my_tiles; ++q) {
-      tiles[2 * (tile0 + q)] = e;
-      tiles[2 * (tile0 + q) + 1] = row0 + q * tile_rows;
-    }
+    tile_start[e] = tile0;
+    row_start[e] = row0;
     if (e == experts - 1) {
       offsets[experts] = rows_incl;
       tile_count[0] = tiles_incl;
+      tile_start[experts] = tiles_incl;
     }
+  }
+  __syncthreads();
+  // The whole block writes the tile list (a hot expert owns hundreds of tiles). Tile t belongs
+  // to the last expert whose first tile is <= t: experts without tiles share their start with
+  // the next expert that has some, and come before it.
+  const int32_t n_tiles = tile_start[experts];
+  for (int32_t t = e; t < n_tiles; t += (int32_t)blockDim.x) {
+    int lo = 0, hi = experts - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tile_start[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    tiles[2 * t] = lo;
+    tiles[2 * t + 1] = row_start[lo] + (t - tile_start[lo]) * tile_rows;
   }
 }
 
