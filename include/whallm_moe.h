@@ -336,7 +336,9 @@ WM_EXPORT size_t wm_decode_state_size(int32_t layers, int32_t experts);
  * counterpart of the reference's per-layer cancel poll, Native/QwenNative/capi.h:36-37).
  * The launch runs asynchronously, so the outcome is in the state's status word
  * (wm_decode_status_offset): 0 done, 1 a message wait ran out, 2 cancelled, 3 a selected
- * expert is not resident (negative slot map entry; checked before any layer runs).
+ * expert is not resident (negative slot map entry; checked before any layer runs), 4 no
+ * valid route (a layer's logits row has fewer than k selectable values, e.g. NaN logits;
+ * checked before any layer runs).
  * A launch that ends with a nonzero status leaves residual and x_out unchanged; the
  * state must then be zero-filled again. Calls that share a state buffer must be
  * stream-ordered.
@@ -396,9 +398,24 @@ WM_EXPORT int wm_slot_cache_acquire(wm_slot_cache* cache, int32_t file, const in
  * out_ready[i] = 1 where the expert was already resident: work enqueued on compute_stream
  * right away may read those experts (no fill of the plan touches their slots), e.g. a layer
  * call whose other pairs are masked with id -1. wm_slot_cache_wait_fills then makes
- * compute_stream wait for the fills, after which the remaining pairs may run. */
+ * compute_stream wait for the fills, after which the remaining pairs may run. An expert
+ * whose slot an earlier acquire_ready is still filling (no wait_fills since) is not ready;
+ * wm_slot_cache_acquire waits for such fills as well, even when every expert is a hit. */
 WM_EXPORT int wm_slot_cache_acquire_ready(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
                                           int32_t* out_slots, int32_t* out_ready, void* compute_stream);
+/* wm_slot_cache_acquire_ready for one call's pairs in the reference's order (the ready pairs
+ * are submitted before the reads, Native/QwenNative/engine.mm:2204-2230): plans `experts`
+ * (the call's unique ids, host), then on compute_stream splits the device pair ids
+ * indices [pairs] into ready_indices (the id where its expert is ready, else -1) and
+ * late_indices (the rest; device arrays of `pairs`), with no host -> device copy, and only
+ * then enqueues the fills, which wait for the split but not for later work on
+ * compute_stream. A slot filled by an earlier acquire_ready that no wait_fills has covered
+ * is not ready. Run the ready pairs at once, wm_slot_cache_wait_fills, then the late pairs.
+ * At most 1024 experts. */
+WM_EXPORT int wm_slot_cache_acquire_split(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
+                                          int32_t* out_slots, int32_t* out_ready, const int32_t* indices,
+                                          int64_t pairs, int32_t* ready_indices, int32_t* late_indices,
+                                          void* compute_stream);
 WM_EXPORT int wm_slot_cache_wait_fills(wm_slot_cache* cache, void* compute_stream);
 /* Route mode (ExpertCache with eviction_policy "route", expert_cache.py:1131-1181): scores
  * [files * experts] (host, the route policy's retention scores) and quotas [files] (its

@@ -14,8 +14,8 @@ scales |y| is ~3e4 per layer against |r_0| ~ 45, and a 1e-4 relative perturbatio
 every layer's y moves the oracle's own 48-layer result by 1.6e-2 (bf16 roundings of y
 flip and the next norms carry the change), so no bound of 1e-2 is meaningful there.
 Also: the reference row layout of the down regions read in place (bit-identical to the
-slice-major copy), slot-cache tables, a non-resident expert (status 3), and
-cancellation (status 2) with recovery.
+slice-major copy), slot-cache tables, a non-resident expert (status 3), a layer whose
+logits select fewer than k experts (status 4), and cancellation (status 2) with recovery.
 """
 import numpy as np
 import pytest
@@ -218,6 +218,31 @@ def test_decode_served_from_the_slot_cache(device):
         stack(torch.from_numpy(logits).to(device), r)      # the state was reset: the next launch runs
         want_r, _ = chain.oracle(logits, r0)
         close(r.cpu().numpy(), want_r, f"after a launch missing an expert of layer {gap}")
+
+
+def test_no_valid_route_ends_the_launch(device):
+    """A layer whose logits are all NaN selects no expert (the top-k gives its sentinel id):
+    the launch ends with status 4 before any layer runs and before any expert address is
+    formed (residual unchanged), for tables without and with a slot map; after the reset
+    the next launch runs and matches the oracle."""
+    chain = Chain(device, 3, 64, seed=25)
+    _, cache, slotted = _slot_cache_chain(device, 3, 64, seed=26)
+    for stack in (chain.stack, slotted):
+        logits, r0 = chain.inputs()
+        bad = logits.copy()
+        bad[1] = np.nan
+        r = torch.from_numpy(r0.copy()).to(device)
+        with pytest.raises(DecodeStackError, match="no valid route"):
+            stack(torch.from_numpy(bad).to(device), r)
+        assert torch.equal(r.cpu(), torch.from_numpy(r0))
+        partial = logits.copy()
+        partial[2, 8:] = np.nan                         # 8 selectable experts for k = 10
+        with pytest.raises(DecodeStackError, match="no valid route"):
+            stack(torch.from_numpy(partial).to(device), r)
+        assert torch.equal(r.cpu(), torch.from_numpy(r0))
+    chain.stack(torch.from_numpy(logits).to(device), r)
+    want_r, _ = chain.oracle(logits, r0)
+    close(r.cpu().numpy(), want_r, "after a launch with no valid route")
 
 
 def test_persistent_cancel_and_recovery(device):

@@ -7,7 +7,8 @@
 - A pair with a negative id leaves its per-pair row as it was, so two calls over
   complementary masks give the one-call result bit for bit.
 - The cached-first acquire (ready experts computed while the missing ones are copied in)
-  gives the all-resident result bit for bit, at a small shape and at the C2 expert shape.
+  gives the all-resident result bit for bit, at a small shape and at the C2 expert shape;
+  hits on slots whose fills are still pending are not ready, and acquire waits for them.
 - The per-pair combine and the bf16 shared-expert MLP match the oracle's float64 closed
   forms (relative L2 <= 1e-2, max |err| <= 2e-2 max |ref|).
 """
@@ -177,6 +178,42 @@ def test_cached_first_at_decode_shape(device):
         want = wa.experts_mxfp4(x, it, table)
         assert torch.equal(got.cpu(), want.cpu())
     assert cache.stats()["copies"] > 0
+
+
+def test_hits_on_slots_still_filling_wait_for_their_fills(device):
+    """acquire_ready fills 20 missing experts (33 MB at the C2 expert shape) without making the
+    stream wait. A second request for them before any wait_fills finds hits whose copies may
+    still be in flight: acquire_ready and acquire_split report them not ready, and acquire
+    (every expert a hit) still makes the stream wait for those fills, so the kernel enqueued
+    right after it reads the filled weights (the output equals the all-resident table's bit
+    for bit and matches the oracle)."""
+    files, experts, slots, K, tokens = 1, 48, 40, 10, 4
+    arrays, pool = make_pool(files, experts, 31, hidden=2048, inter=512)
+    cache = SlotCache(slots, 2048, 512, files, experts, pool, device)
+    table = S.experts_to_device(arrays[0], device)
+    missing = list(range(4, 24))
+    _, ready = cache.acquire_ready(0, missing)
+    assert not any(ready)
+    _, ready = cache.acquire_ready(0, missing[:3])          # hits, but their fills are pending
+    assert not any(ready)
+    rng = np.random.default_rng(32)
+    idx = np.stack([rng.choice(missing, K, replace=False) for _ in range(tokens)]).astype(np.int32)
+    it = torch.from_numpy(idx).to(device)
+    ready_idx, late_idx, any_late = cache.acquire_split(0, it)
+    assert any_late and bool((ready_idx == -1).all()) and torch.equal(late_idx, it)
+    cache.acquire(0, missing)                               # every expert a hit
+    x_bits = S.bf16_normal_np(rng, (tokens, 2048))
+    x = S.bf16_bits_to_tensor(x_bits, device)
+    got = wa.experts_mxfp4(x, it, cache.table(0))
+    want = wa.experts_mxfp4(x, it, table)
+    assert torch.equal(got.cpu(), want.cpu())
+    ex = {e: M.MXFP4Expert(arrays[0]["gate_up"][e], arrays[0]["gate_up_scales"][e], arrays[0]["down"][e],
+                           arrays[0]["down_scales"][e]) for e in set(idx.reshape(-1).tolist())}
+    close(got.float().cpu().numpy(), M.routed_outputs(S.bf16_bits_to_f32(x_bits), idx, ex), "after the hits")
+    _, ready = cache.acquire_ready(0, missing)              # acquire waited: resident now
+    assert all(ready)
+    ready_idx, late_idx, any_late = cache.acquire_split(0, it)
+    assert not any_late and torch.equal(ready_idx, it) and bool((late_idx == -1).all())
 
 
 def test_combine_pairs_matches_oracle(device):

@@ -88,6 +88,7 @@ _SIGNATURES = {
     "wm_slot_cache_acquire": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
     "wm_slot_cache_stats": (c_int, [_P, _P]),
     "wm_slot_cache_acquire_ready": (c_int, [_P, c_int32, _P, c_int32, _P, _P, _P]),
+    "wm_slot_cache_acquire_split": (c_int, [_P, c_int32, _P, c_int32, _P, _P, _P, c_int64, _P, _P, _P]),
     "wm_slot_cache_acquire_files": (c_int, [_P, c_int32, _P, _P, _P, _P, _P]),
     "wm_slot_cache_read_experts": (c_int, [_P, c_int32, _P, c_int32, _P, _P]),
     "wm_slot_cache_seed_tail": (c_int, [_P, c_int32, _P, c_int64, c_int32, c_int32, _P, _P, _P, _P, _P]),

@@ -6,11 +6,12 @@
 //
 //   gate_up_act : one workgroup = (pair, block of intermediate rows i). Each wave
 //                 streams the gate row i and the up row I+i of its expert; a row of
-//                 H/2 bytes is read by H/32 lanes, 16 bytes (one 32-value E8M0
-//                 group) per lane per load, so a wave load is 64 x 16 B, fully
-//                 coalesced. Nibbles -> bf16 with the gfx950 scaled convert
+//                 H/2 bytes is read by LPR lanes, 16 bytes (one 32-value E8M0
+//                 group) per lane per load, GPL loads a lane, so a wave load is up to
+//                 64 x 16 B, coalesced. Nibbles -> bf16 with the gfx950 scaled convert
 //                 (scale folded in), dot2 against the bf16 input held in registers,
 //                 segment reduction, then silu(gate) * up in the epilogue -> act (fp32).
+
 //   down_combine: one workgroup = (token, block of output rows o). The four waves
 //                 split the token's experts (routed + shared); each lane keeps its
 //                 partial sums already scaled by the routing weight, so the
@@ -18,6 +19,11 @@
 //                 y[t,o] = sum_k w[t,k] * act_k . Wd_k[o] + gate(t) * act_s . Wd_s[o].
 //                 The same kernel in per-pair mode writes each pair's row unweighted
 //                 (the StreamingExperts [T, K, H] contract, qwen4_exp.py:853-904).
+//
+// Any hidden and intermediate size that is a multiple of 32 up to 16384 runs here (the
+// reference's expert_linear4 takes any multiple of 32): a row of G = size / 32 groups is
+// read by LPR lanes (a power of two) taking GPL groups each, LPR * GPL >= G, and the lanes
+// past the row's last group load nothing and add nothing (lane_split).
 #include <cmath>
 
 #include "wm_common.h"
@@ -27,21 +33,31 @@ namespace wm {
 
 // ---------------------------------------------------------------------------------
 // The input row of a decode token as bf16 pairs: lane group `g` needs values
-// [32 g, 32 g + 32) = 16 words.
+// [32 g, 32 g + 32) = 16 words; groups at or past `groups` (the row's end) read as zero.
 template <int GPL, int LPR>
-__device__ __forceinline__ void load_x_groups(const uint32_t* __restrict__ xrow, int gl, uint32_t (&xw)[GPL][16]) {
+__device__ __forceinline__ void load_x_groups(const uint32_t* __restrict__ xrow, int gl, int groups,
+                                              uint32_t (&xw)[GPL][16]) {
 #pragma unroll
   for (int gp = 0; gp < GPL; ++gp) {
-    const uint4* src = reinterpret_cast<const uint4*>(xrow + (gl + gp * LPR) * 16);
+    const int g = gl + gp * LPR;
+    const uint4* src = reinterpret_cast<const uint4*>(xrow + g * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      uint4 v = src[q];
+      uint4 v = g < groups ? src[q] : make_uint4(0, 0, 0, 0);
       xw[gp][4 * q + 0] = v.x;
       xw[gp][4 * q + 1] = v.y;
       xw[gp][4 * q + 2] = v.z;
       xw[gp][4 * q + 3] = v.w;
     }
   }
+}
+
+// Weight rows a gate_up wave reduces per pass (gate and up rows of RPW = ROWS / 2
+// intermediate indices): one per lane slot when a wave load covers 8 or more rows,
+// otherwise 8, fewer for wide rows so that x (16 GPL registers) and the row loads in
+// flight (5 GPL registers per row step) stay within the register file.
+__host__ __device__ constexpr int gate_up_rows(int lpr, int gpl) {
+  return 64 / lpr >= 8 ? 64 / lpr : (64 / lpr >= 2 ? 8 : (gpl <= 3 ? 8 : gpl == 4 ? 6 : gpl == 5 ? 4 : 2));
 }
 
 // dot of one 32-value group: 16 weight bytes (4 words) against 16 bf16-pair words.
@@ -76,14 +92,15 @@ __device__ __forceinline__ bool decode_pair(int p, int tokens, int k, const int3
   return resident;
 }
 
-// grid: (ceil(I / (4 * RPW)), pairs). act[p, i] fp32.
-template <int LPR, int GPL, int RPW>
+// grid: (ceil(I / (4 * RPW)), pairs), RPW = gate_up_rows(LPR, GPL) / 2. act[p, i] fp32.
+template <int LPR, int GPL>
 __global__ void __launch_bounds__(256) gate_up_act_kernel(const uint16_t* __restrict__ x, int tokens, int k,
                                                           const int32_t* __restrict__ indices, wm_mxfp4_experts routed,
                                                           wm_mxfp4_experts shared, int has_shared,
                                                           float* __restrict__ act) {
   constexpr int NS = 64 / LPR;              // rows a wave reads at once
-  constexpr int ROWS = 2 * RPW;             // gate and up rows of RPW intermediate indices
+  constexpr int ROWS = gate_up_rows(LPR, GPL);  // gate and up rows of RPW intermediate indices
+  constexpr int RPW = ROWS / 2;
   constexpr int STEPS = (ROWS + NS - 1) / NS;
   __shared__ float sums[4][ROWS];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -102,10 +119,10 @@ __global__ void __launch_bounds__(256) gate_up_act_kernel(const uint16_t* __rest
   const float limit = has_shared && p >= tokens * k ? shared.swiglu_limit : routed.swiglu_limit;
   const int i_base = blockIdx.x * 4 * RPW + wave * RPW;
 
-  uint32_t xw[GPL][16];
-  load_x_groups<GPL, LPR>(reinterpret_cast<const uint32_t*>(x) + (int64_t)t * (H / 2), gl, xw);
-
   const int G = H / 32;
+  uint32_t xw[GPL][16];
+  load_x_groups<GPL, LPR>(reinterpret_cast<const uint32_t*>(x) + (int64_t)t * (H / 2), gl, G, xw);
+
   uint4 wq[STEPS][GPL];
   uint32_t sb[STEPS][GPL];
 #pragma unroll
@@ -118,7 +135,7 @@ __global__ void __launch_bounds__(256) gate_up_act_kernel(const uint16_t* __rest
 #pragma unroll
     for (int gp = 0; gp < GPL; ++gp) {
       int g = gl + gp * LPR;
-      if (ok) {
+      if (ok && g < G) {
         wq[st][gp] = reinterpret_cast<const uint4*>(r.gate_up + (int64_t)row * (H / 2))[g];
         sb[st][gp] = r.gate_up_scales[(int64_t)row * G + g];
       } else {
@@ -244,7 +261,7 @@ __global__ void __launch_bounds__(256) down_kernel(const float* __restrict__ act
 #pragma unroll
       for (int gp = 0; gp < GPL; ++gp) {
         int g = gl + gp * LPR;
-        if (o < H) {
+        if (o < H && g < G) {
           wq[st][gp] = reinterpret_cast<const uint4*>(r.down + (int64_t)o * (I / 2))[g];
           sb[st][gp] = r.down_scales[(int64_t)o * G + g];
         } else {
@@ -255,11 +272,12 @@ __global__ void __launch_bounds__(256) down_kernel(const float* __restrict__ act
     }
 #pragma unroll
     for (int gp = 0; gp < GPL; ++gp) {
-      const float4* a4 = reinterpret_cast<const float4*>(arow + (gl + gp * LPR) * 32);
+      const int g = gl + gp * LPR;
+      const float4* a4 = reinterpret_cast<const float4*>(arow + g * 32);
       float av[32];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        float4 v = a4[q];
+        float4 v = g < G ? a4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         av[4 * q] = v.x; av[4 * q + 1] = v.y; av[4 * q + 2] = v.z; av[4 * q + 3] = v.w;
       }
 #pragma unroll
@@ -309,19 +327,42 @@ __global__ void __launch_bounds__(256) down_kernel(const float* __restrict__ act
 }
 
 // ---------------------------------------------------------------------------------
-// Launchers. LPR (lanes per row) = min(64, groups); GPL = groups / LPR.
+// Launchers. A row of G groups is read by LPR lanes x GPL groups (lane_split).
 
-template <int RPW>
-static void launch_gate_up(int lpr, int gpl, dim3 grid, hipStream_t s, const uint16_t* x, int tokens, int k,
+// Every (LPR, GPL) lane_split can choose.
+#define WM_LANE_SPLITS(X)                                                                          \
+  X(4, 1) X(4, 3) X(4, 5) X(8, 1) X(8, 3) X(8, 5) X(16, 1) X(16, 3) X(16, 5) X(32, 1) X(32, 3) X(32, 5) \
+  X(64, 1) X(64, 2) X(64, 3) X(64, 4) X(64, 5) X(64, 6) X(64, 7) X(64, 8)
+
+// Lanes per row and groups per lane for rows of `dim` values (a multiple of 32): the split
+// with the fewest idle lane groups, ties to the wider one (fewer loads per lane). False
+// above 16384 values (512 groups).
+static bool lane_split(int dim, int& lpr, int& gpl) {
+  const int G = dim / 32;
+  int best_waste = 1 << 30;
+  lpr = gpl = 0;
+#define WM_TRY(L, P)                                                  \
+  if (L * P >= G && (L * P - G < best_waste || (L * P - G == best_waste && L > lpr))) { \
+    best_waste = L * P - G;                                           \
+    lpr = L;                                                          \
+    gpl = P;                                                          \
+  }
+  WM_LANE_SPLITS(WM_TRY)
+#undef WM_TRY
+  return lpr > 0;
+}
+
+static void launch_gate_up(int lpr, int gpl, int pairs, int inter, hipStream_t s, const uint16_t* x, int tokens, int k,
                            const int32_t* indices, const wm_mxfp4_experts& routed, const wm_mxfp4_experts& shared,
                            int has_shared, float* act) {
-#define WM_GU(L, G)                                                                                           \
-  if (lpr == L && gpl == G) {                                                                                  \
-    hipLaunchKernelGGL((gate_up_act_kernel<L, G, RPW>), grid, dim3(256), 0, s, x, tokens, k, indices, routed, \
-                       shared, has_shared, act);                                                              \
-    return;                                                                                                    \
+#define WM_GU(L, G)                                                                                            \
+  if (lpr == L && gpl == G) {                                                                                   \
+    constexpr int RPW = gate_up_rows(L, G) / 2;                                                                 \
+    hipLaunchKernelGGL((gate_up_act_kernel<L, G>), dim3((inter + 4 * RPW - 1) / (4 * RPW), pairs), dim3(256), 0, s, \
+                       x, tokens, k, indices, routed, shared, has_shared, act);                                  \
+    return;                                                                                                     \
   }
-  WM_GU(2, 1) WM_GU(4, 1) WM_GU(8, 1) WM_GU(16, 1) WM_GU(32, 1) WM_GU(64, 1) WM_GU(64, 2) WM_GU(64, 3) WM_GU(64, 4)
+  WM_LANE_SPLITS(WM_GU)
 #undef WM_GU
   fail("decode gate_up: unsupported hidden size");
 }
@@ -337,22 +378,14 @@ static void launch_down(int lpr, int gpl, dim3 grid, hipStream_t s, const float*
                        weights, routed, shared, has_shared, x, sg, y);                                          \
     return;                                                                                                     \
   }
-  WM_DN(2, 1) WM_DN(4, 1) WM_DN(8, 1) WM_DN(16, 1) WM_DN(32, 1) WM_DN(64, 1) WM_DN(64, 2) WM_DN(64, 3) WM_DN(64, 4)
+  WM_LANE_SPLITS(WM_DN)
 #undef WM_DN
   fail("decode down: unsupported intermediate size");
 }
 
-static void lanes_for(int dim, int& lpr, int& gpl) {
-  int groups = dim / 32;
-  if (groups >= 64) {
-    lpr = 64;
-    gpl = groups / 64;
-    if (groups % 64 || gpl > 4) fail("decode: size must be a multiple of 2048 up to 8192, or a power of two below");
-  } else {
-    lpr = groups;
-    gpl = 1;
-    if (groups & (groups - 1)) fail("decode: sizes below 2048 must be powers of two");
-  }
+bool decode_mxfp4_supports(int hidden, int inter) {
+  int l, g;
+  return hidden % 32 == 0 && inter % 32 == 0 && lane_split(hidden, l, g) && lane_split(inter, l, g);
 }
 
 void decode_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
@@ -361,22 +394,20 @@ void decode_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const f
   const int H = routed.hidden, I = routed.inter;
   const int pairs = tokens * k + (shared ? tokens : 0);
   wm_mxfp4_experts sh = shared ? *shared : routed;
-  int lpr, gpl;
-  constexpr int RPW = 4;
-  lanes_for(H, lpr, gpl);
-  dim3 g1((I + 4 * RPW - 1) / (4 * RPW), pairs);
-  launch_gate_up<RPW>(lpr, gpl, g1, s, x, tokens, k, indices, routed, sh, shared ? 1 : 0, act);
+  int lpr_h, gpl_h, lpr_i, gpl_i;
+  if (!lane_split(H, lpr_h, gpl_h) || !lane_split(I, lpr_i, gpl_i))
+    fail("decode: hidden and intermediate must be at most 16384");
+  launch_gate_up(lpr_h, gpl_h, pairs, I, s, x, tokens, k, indices, routed, sh, shared ? 1 : 0, act);
   check_launch("gate_up_act");
-  lanes_for(I, lpr, gpl);
   constexpr int STEPS = 2;
-  int opw = (64 / lpr) * STEPS;
+  int opw = (64 / lpr_i) * STEPS;
   if (combine) {
     dim3 g2((H + opw - 1) / opw, tokens);
-    launch_down<STEPS, true>(lpr, gpl, g2, s, act, tokens, k, indices, weights, routed, sh, shared ? 1 : 0, x,
+    launch_down<STEPS, true>(lpr_i, gpl_i, g2, s, act, tokens, k, indices, weights, routed, sh, shared ? 1 : 0, x,
                              shared_gate, y);
   } else {
     dim3 g2((H + 4 * opw - 1) / (4 * opw), tokens * k);
-    launch_down<STEPS, false>(lpr, gpl, g2, s, act, tokens, k, indices, weights, routed, sh, 0, x, nullptr, y);
+    launch_down<STEPS, false>(lpr_i, gpl_i, g2, s, act, tokens, k, indices, weights, routed, sh, 0, x, nullptr, y);
   }
   check_launch("down");
 }

@@ -53,7 +53,7 @@ constexpr int DS_KB = DS_H / 128;     // K-steps of a phase-A tile (128 per MFMA
 constexpr uint32_t DS_SPIN_LIMIT = 1u << 20;
 // Status word values (0 = healthy): a message wait ran out, the caller's cancel word was
 // set, a selected expert is not resident (its slot map entry is negative).
-constexpr uint32_t DS_STALLED = 1, DS_CANCELLED = 2, DS_NOT_RESIDENT = 3;
+constexpr uint32_t DS_STALLED = 1, DS_CANCELLED = 2, DS_NOT_RESIDENT = 3, DS_NO_ROUTE = 4;
 constexpr int DS_MAX_LAYERS = 128;    // layer descriptors kept in LDS
 constexpr int DS_CW = 3;                      // compute waves (prefetch weights and compute)
 constexpr int DS_THREADS = (DS_CW + 1) * 64;  // + one message wave (polls and publishes)
@@ -781,21 +781,32 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   if (!ok) sh.failures = 1;
   ds_barrier();
   if (sh.failures != 0) return;
-  // Expert ids -> slots once, so the prefetch loops read only LDS. A negative map entry
-  // (an expert that is not resident) ends the launch before any layer runs: every
-  // workgroup reads the same map and leaves here, the status word tells the caller.
+  // Expert ids -> slots once, so the prefetch loops read only LDS. Before any address is
+  // formed, a selection outside [0, E) (a logits row with fewer than K selectable values,
+  // e.g. all NaN, gives the top-k's sentinel id) raises failure bit 2, and a negative map
+  // entry (an expert that is not resident) bit 1; either ends the launch before any layer
+  // runs: every workgroup reads the same routes and map and leaves here, and the status
+  // word tells the caller (4 no valid route, 3 not resident).
   for (int i = tid; i < L * 16; i += DS_THREADS) {
     int l = i / 16, k = i % 16;
     const int32_t* slots = sh.desc[l].slots;
-    if (k < K && slots) {
-      const int32_t v = gload<int32_t>(slots + sh.slot[l][k]);
-      if (v < 0) sh.failures = 1;
-      sh.slot[l][k] = max(0, v);
+    if (k < K) {
+      const int e = sh.slot[l][k];
+      if (e < 0 || e >= E) {
+        __hip_atomic_fetch_or(&sh.failures, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        sh.slot[l][k] = 0;
+      } else if (slots) {
+        const int32_t v = gload<int32_t>(slots + e);
+        if (v < 0) __hip_atomic_fetch_or(&sh.failures, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        sh.slot[l][k] = max(0, v);
+      }
     }
   }
   ds_barrier();
   if (sh.failures != 0) {
-    if (tid == 0) __hip_atomic_store(c.status, DS_NOT_RESIDENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0)
+      __hip_atomic_store(c.status, (sh.failures & 2) ? DS_NO_ROUTE : DS_NOT_RESIDENT, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   if (msg) {  // rmsnorm statistics of r_0 (every LDS read issued before the first use)

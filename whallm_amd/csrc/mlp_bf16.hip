@@ -21,6 +21,7 @@
 namespace wm {
 
 bool linear_bf16_mfma(const void* x, const void* w, int tokens, int hidden, int outputs, float* out, hipStream_t s);
+bool linear_bf16_mfma_fits(int tokens, int hidden);
 
 constexpr int MLP_GEMV_MAX_TOKENS = 63;
 
@@ -167,6 +168,10 @@ WM_EXPORT int wm_mlp_bf16(const void* x, int32_t tokens, int32_t hidden, int32_t
       if ((uintptr_t)p % 16) fail("wm_mlp_bf16: every tensor must be 16-byte aligned");
     const MlpLayout p = mlp_layout(tokens, hidden, inter);
     if (workspace_bytes < p.total) fail("wm_mlp_bf16: workspace too small");
+    // every GEMM of the MFMA path is checked before the first launch, so a shape it cannot
+    // hold launches nothing
+    if (tokens > MLP_GEMV_MAX_TOKENS && (!linear_bf16_mfma_fits(tokens, hidden) || !linear_bf16_mfma_fits(tokens, inter)))
+      fail("wm_mlp_bf16: hidden or intermediate too large for the MFMA GEMM's x tile (150 KB of LDS)");
     hipStream_t s = as_stream(stream);
     uint8_t* ws = (uint8_t*)workspace;
     float* gate = (float*)(ws + p.gate);

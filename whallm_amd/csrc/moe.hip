@@ -41,8 +41,11 @@ static void validate_pair(const wm_mxfp4_experts* routed, const wm_mxfp4_experts
 }
 
 static bool use_decode(int tokens, int k) { return (int64_t)tokens * k <= DECODE_MAX_PAIRS; }
-// Tables in the prefill tile layout always take the grouped GEMM.
-static bool use_decode(int tokens, int k, const wm_mxfp4_experts& e) { return !e.tiled && use_decode(tokens, k); }
+// Tables in the prefill tile layout always take the grouped GEMM, and so do shapes the decode
+// kernels do not take (above 16384).
+static bool use_decode(int tokens, int k, const wm_mxfp4_experts& e) {
+  return !e.tiled && use_decode(tokens, k) && decode_mxfp4_supports(e.hidden, e.inter);
+}
 
 static void validate_fp8(const wm_fp8_experts* e, const char* what, bool shared) {
   std::string w(what);

@@ -51,6 +51,9 @@ __device__ __forceinline__ Fp8Regions fp8_regions(const wm_fp8_experts& t, int e
 // Host-side checks of an expert table; raises on a bad shape.
 void validate_experts(const wm_mxfp4_experts* e, const char* what, bool shared);
 
+// Whether the decode kernels take this shape (multiples of 32 up to 16384).
+bool decode_mxfp4_supports(int hidden, int inter);
+
 // Decode path (small T): gate_up_act into `act` [(T*K + T_shared), I] fp32, then
 // down (combined into y [T, H] bf16, or per pair into y [T*K, H] bf16).
 void decode_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,

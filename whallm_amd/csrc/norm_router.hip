@@ -344,6 +344,9 @@ static int pick_token_block(int tokens, int hidden) {
 // logits = x . w^T on the router GEMM's MFMA path (a tile of x as given, no norm), for
 // wm_linear_bf16 at 64+ tokens. False when the shape does not suit it (the caller then uses
 // the one-wave-per-output kernel).
+// Whether linear_bf16_mfma takes x [tokens, hidden] (its x tile must fit the LDS).
+bool linear_bf16_mfma_fits(int tokens, int hidden) { return tokens >= 64 && mfma_token_block(tokens, hidden) > 0; }
+
 bool linear_bf16_mfma(const void* x, const void* w, int tokens, int hidden, int outputs, float* out, hipStream_t s) {
   const int tb = tokens >= 64 ? mfma_token_block(tokens, hidden) : 0;
   if (!tb || ((uintptr_t)x % 16) || ((uintptr_t)w % 16)) return false;

@@ -88,6 +88,26 @@ __global__ void __launch_bounds__(1024) tail_rank_kernel(const int32_t* __restri
   if (t == 0) out[0] = n_sel;
 }
 
+// Ready experts of one plan as a bitmask passed by value (experts <= 1024), so splitting a
+// call's pairs needs no host -> device copy (which would queue behind the fills).
+struct ExpertBits {
+  uint32_t w[32];
+};
+
+// The cached-first split of a call's pairs (indices [n]): ready[i] = the id when its expert is
+// ready, else -1; late[i] = the id otherwise (ids outside [0, experts) and masked ids go to
+// late, where the expert kernels treat them as they always do).
+__global__ void __launch_bounds__(256) split_ready_kernel(const int32_t* __restrict__ indices, int64_t n,
+                                                          ExpertBits bits, int experts, int32_t* __restrict__ ready,
+                                                          int32_t* __restrict__ late) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int e = indices[i];
+  const bool r = e >= 0 && e < experts && ((bits.w[e >> 5] >> (e & 31)) & 1u);
+  ready[i] = r ? e : -1;
+  late[i] = r ? -1 : e;
+}
+
 class SlotCache {
  public:
   SlotCache(int slots, int64_t blob, int files, int experts, void* device_slots, int32_t* device_map,
@@ -98,6 +118,7 @@ class SlotCache {
     stamp_.assign(slots, 0);
     uses_.assign(slots, 0);
     access_.assign(slots, 0);
+    fill_pending_.assign(slots, 0);
     count_.assign(files, 0);
     host_map_.assign((size_t)files * experts, -1);
     if (dev_) {
@@ -178,17 +199,47 @@ class SlotCache {
   // no fill of this plan touches (a plan never evicts a slot it hands out), so work on
   // compute_stream may use them at once; the misses are filled on the copy stream and
   // compute_stream waits for them only at wait_fills.
+  // A hit on a slot whose fill (from an earlier acquire_ready) no compute stream has waited
+  // for yet is not ready either: its copy may still be in flight.
   void acquire_ready(int file, const int32_t* experts, int n, int32_t* out_slots, int32_t* out_ready,
                      hipStream_t compute) {
     observe_request(file, experts, n);
     std::vector<int32_t> filled(n);
     const Request r{file, experts, n, out_slots, filled.data()};
     fill(&r, 1, compute, nullptr, false);
-    for (int i = 0; i < n; ++i) out_ready[i] = filled[i] ? 0 : 1;
+    for (int i = 0; i < n; ++i) out_ready[i] = filled[i] || fill_pending_[out_slots[i]] ? 0 : 1;
   }
   void wait_fills(hipStream_t compute) {
     if (pending_) check(hipStreamWaitEvent(compute, fills_done_, 0), "hipStreamWaitEvent");
     pending_ = false;
+    std::fill(fill_pending_.begin(), fill_pending_.end(), 0);
+  }
+
+  // acquire_ready for one call's pairs, in the reference's order (engine.mm:2204-2230: the
+  // ready pairs are submitted, then the reads): plan, then split the pairs on compute_stream
+  // into ready and late index arrays (split_ready_kernel, the ready set passed by value),
+  // then enqueue the fills, whose copy stream waits for the split but not for work enqueued
+  // after this call, so the caller's ready-pair kernels overlap the fills.
+  void acquire_split(int file, const int32_t* experts, int n, int32_t* out_slots, int32_t* out_ready,
+                     const int32_t* indices, int64_t pairs, int32_t* ready_idx, int32_t* late_idx,
+                     hipStream_t compute) {
+    if (!dev_) throw std::runtime_error("slot cache: opened without device memory (policy only)");
+    if (experts_ > 1024) throw std::runtime_error("slot cache: the pair split takes at most 1024 experts");
+    observe_request(file, experts, n);
+    std::vector<int32_t> filled(n);
+    const Request r{file, experts, n, out_slots, filled.data()};
+    plan_requests(&r, 1);
+    ExpertBits bits{};
+    for (int i = 0; i < n; ++i) {
+      out_ready[i] = filled[i] || fill_pending_[out_slots[i]] ? 0 : 1;
+      if (out_ready[i]) bits.w[experts[i] >> 5] |= 1u << (experts[i] & 31);
+    }
+    if (pairs > 0) {
+      hipLaunchKernelGGL(split_ready_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, compute, indices,
+                         pairs, bits, experts_, ready_idx, late_idx);
+      check(hipGetLastError(), "split_ready_kernel");
+    }
+    enqueue_fills(&r, 1, compute, nullptr, false);
   }
 
   // plan + copies of the misses: from the host pool, or with `layer` (a device copy of the
@@ -197,10 +248,19 @@ class SlotCache {
   void fill(const Request* req, int m, hipStream_t compute, const uint8_t* layer, bool compute_waits) {
     if (!dev_) throw std::runtime_error("slot cache: opened without device memory (policy only)");
     plan_requests(req, m);
+    enqueue_fills(req, m, compute, layer, compute_waits);
+  }
+  // The copies of a planned request's misses (fill after plan_requests).
+  void enqueue_fills(const Request* req, int m, hipStream_t compute, const uint8_t* layer, bool compute_waits) {
     bool any = false;
     for (int r = 0; r < m; ++r)
       for (int i = 0; i < req[r].n; ++i) any |= req[r].filled[i] != 0;
-    if (!any) return;
+    if (!any) {
+      // every expert is a hit, but some may be slots an earlier acquire_ready is still
+      // filling: work enqueued after an acquire must see them resident
+      if (compute_waits) wait_fills(compute);
+      return;
+    }
     // the slots being refilled may still be read by work already on the compute stream
     check(hipEventRecord(compute_done_, compute), "hipEventRecord");
     check(hipStreamWaitEvent(copy_, compute_done_, 0), "hipStreamWaitEvent");
@@ -229,6 +289,7 @@ class SlotCache {
         copied_ += (int64_t)bytes;
         fills_ += run;
         ++copies_;
+        for (int j = 0; j < run; ++j) fill_pending_[q.slots[i + j]] = 1;
         i += run;
       }
     }
@@ -527,6 +588,7 @@ class SlotCache {
   hipStream_t copy_ = nullptr;
   hipEvent_t compute_done_ = nullptr, fills_done_ = nullptr;
   bool pending_ = false;  // fills recorded in fills_done_ that no compute stream waited for yet
+  std::vector<uint8_t> fill_pending_;  // per slot: filled by a copy behind pending_
   std::vector<Staging> staging_;
   unsigned next_staging_ = 0;
 };
@@ -610,6 +672,20 @@ WM_EXPORT int wm_slot_cache_acquire_ready(wm_slot_cache* cache, int32_t file, co
     if (n < 0 || (n > 0 && (!experts || !out_slots || !out_ready)))
       throw std::runtime_error("wm_slot_cache_acquire_ready: bad arguments");
     c->acquire_ready(file, experts, n, out_slots, out_ready, as_stream(compute_stream));
+  });
+}
+
+WM_EXPORT int wm_slot_cache_acquire_split(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
+                                          int32_t* out_slots, int32_t* out_ready, const int32_t* indices,
+                                          int64_t pairs, int32_t* ready_indices, int32_t* late_indices,
+                                          void* compute_stream) {
+  SlotCache* c = reinterpret_cast<SlotCache*>(cache);
+  return with_cache(c, [&] {
+    if (n < 0 || pairs < 0 || (n > 0 && (!experts || !out_slots || !out_ready)) ||
+        (pairs > 0 && (!indices || !ready_indices || !late_indices)))
+      throw std::runtime_error("wm_slot_cache_acquire_split: bad arguments");
+    c->acquire_split(file, experts, n, out_slots, out_ready, indices, pairs, ready_indices, late_indices,
+                     as_stream(compute_stream));
   });
 }
 

@@ -627,7 +627,8 @@ class PersistentDecodeStack:
     """
 
     # status word values (wm_moe_decode_persistent_mxfp4)
-    STATUS_TEXT = {1: "a message wait ran out", 2: "cancelled", 3: "a selected expert is not resident"}
+    STATUS_TEXT = {1: "a message wait ran out", 2: "cancelled", 3: "a selected expert is not resident",
+                   4: "no valid route (a logits row has fewer than k selectable values)"}
 
     def __init__(self, layers: list[MXFP4Experts], shared: list[MXFP4Experts],
                  shared_gates: list[torch.Tensor] | None = None, k: int = 10, eps: float = 1e-6,
@@ -709,7 +710,8 @@ class PersistentDecodeStack:
 
     def status(self) -> int:
         """The launch's outcome: 0 done, 1 a message wait ran out, 2 cancelled, 3 a selected
-        expert is not resident. Nonzero needs reset() before the next launch. Synchronises."""
+        expert is not resident, 4 no valid route. Nonzero needs reset() before the next launch.
+        Synchronises."""
         return int(self.state[self.status_offset:self.status_offset + 4].view(torch.int32).item())
 
     def raise_for_status(self) -> None:

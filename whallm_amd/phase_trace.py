@@ -1,6 +1,6 @@
 """Per-layer phase trace of the persistent decode kernel (a profiling tool, not on the path).
 
-    python -m whallm_amd.phase_trace [--tokens N] [--variant decode_persistent.hip]
+    python -m whallm_amd.phase_trace [--tokens N]
 
 Builds an instrumented copy of libwhallm_moe.so in whallm_amd/_build/trace/: the kernel source
 is compiled with phase_trace.h first, which turns the kernel's WM_DS_TRACE / WM_DS_NOTE
@@ -35,12 +35,12 @@ POINTS = [(0, 0, "compute: S0 (r and its norm in LDS)"), (0, 3, "compute: phase 
 NOTES = [(15, "partial"), (7, "r")]
 
 
-def build_traced(source: Path | None = None) -> Path:
-    """Compile `source` (default: the library's decode_persistent.hip) with the trace hooks and
-    link it with the library's other objects."""
+def build_traced() -> Path:
+    """Compile the library's decode_persistent.hip with the trace hooks and link it with the
+    library's other objects."""
     hip_build.build()
     TRACE_DIR.mkdir(parents=True, exist_ok=True)
-    src = Path(source) if source else hip_build.CSRC / "decode_persistent.hip"
+    src = hip_build.CSRC / "decode_persistent.hip"
     obj = TRACE_DIR / "decode_persistent_trace.o"
     cmd = [hip_build.hipcc(), *hip_build.HIP_FLAGS, f"-I{hip_build.INCLUDE}", f"-I{hip_build.CSRC}", "-include",
            str(HEADER), "-c", str(src), "-o", str(obj)]
@@ -108,10 +108,9 @@ def summary(t: np.ndarray) -> str:
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--tokens", type=int, default=30)
-    ap.add_argument("--variant", default=None, help="a kernel source to trace instead of the library's")
     ap.add_argument("--save", default=None, help="also save the raw trace (.npy)")
     args = ap.parse_args()
-    build_traced(args.variant)
+    build_traced()
     t = run(args.tokens)
     if args.save:
         np.save(args.save, t)

@@ -130,25 +130,39 @@ class SlotCache:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         self._check(_lib.load().wm_slot_cache_wait_fills(self._handle, ctypes.c_void_p(stream)), "wait_fills")
 
+    def acquire_split(self, file: int, indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, bool]:
+        """The cached-first acquire of one call's pairs (engine.mm:2204-2230): plans the call's
+        experts, splits ``indices`` on the current stream into (ready, late) id tensors (-1
+        where a pair is in the other set) with no host -> device copy, then enqueues the fills.
+        Returns (ready, late, whether any pair is late). ``indices`` is read on the host, as the
+        reference's acquire is."""
+        if self.device is None:
+            raise SlotCacheError("policy-only cache")
+        idx = indices.to(torch.int32).contiguous()
+        unique = np.ascontiguousarray(sorted(set(idx.cpu().reshape(-1).tolist())), np.int32)
+        unique = unique[(unique >= 0) & (unique < self.experts)]
+        slots = np.empty(unique.size, np.int32)
+        ready = np.empty(unique.size, np.int32)
+        ready_idx, late_idx = torch.empty_like(idx), torch.empty_like(idx)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        self._check(_lib.load().wm_slot_cache_acquire_split(
+            self._handle, file, unique.ctypes.data, unique.size, slots.ctypes.data, ready.ctypes.data,
+            idx.data_ptr(), idx.numel(), ready_idx.data_ptr(), late_idx.data_ptr(), ctypes.c_void_p(stream)),
+            "acquire_split")
+        return ready_idx, late_idx, not bool(ready.all())
+
     def experts_ready_first(self, file: int, x: torch.Tensor, indices: torch.Tensor,
                             out: torch.Tensor | None = None) -> torch.Tensor:
         """Per-pair outputs [.., K, H] of ``file``'s experts in router order, the pairs whose
         experts are resident computed while the missing ones are copied in, the rest after
         (the native engine's ready-then-late order, engine.mm:2204-2234). The result equals
-        one call with every expert resident, bit for bit. ``indices`` is read on the host,
-        as the reference's acquire is."""
-        ids = indices.to("cpu", torch.int64)
-        unique = sorted(set(ids.reshape(-1).tolist()))
-        _, ready = self.acquire_ready(file, unique)
-        ready_ids = torch.tensor([e for e, r in zip(unique, ready) if r], dtype=torch.int64)
-        is_ready = torch.isin(ids, ready_ids).to(indices.device)
-        idx = indices.to(torch.int32)
-        none = torch.full_like(idx, -1)
+        one call with every expert resident, bit for bit."""
+        ready_idx, late_idx, any_late = self.acquire_split(file, indices)
         table = self.table(file)
-        out = experts_mxfp4(x, torch.where(is_ready, idx, none), table, out=out)
+        out = experts_mxfp4(x, ready_idx, table, out=out)
         self.wait_fills()
-        if not all(ready):
-            experts_mxfp4(x, torch.where(is_ready, none, idx), table, out=out)
+        if any_late:
+            experts_mxfp4(x, late_idx, table, out=out)
         return out
 
     def acquire_files(self, requests: dict) -> dict:
