@@ -18,6 +18,7 @@ The weights are generated on the device (the V4.1 layer is 7 GB). For the oracle
 checked tokens route into a small set of experts (their other logits are pushed to -30) while
 the rest of the 300 tokens route freely; at T <= 4 every token is checked.
 """
+from dataclasses import replace
 from types import SimpleNamespace
 
 import numpy as np
@@ -71,8 +72,8 @@ def layer(device, name):
         experts = S.mxfp4_experts_device(E, H, I, device, g)
         shared = S.mxfp4_experts_device(1, H, I, device, g)
         if ds:
-            experts.up_first = shared.up_first = True
-            experts.swiglu_limit = shared.swiglu_limit = 10.0
+            experts = replace(experts, up_first=True, swiglu_limit=10.0)
+            shared = replace(shared, up_first=True, swiglu_limit=10.0)
         gate = None if ds else (torch.randn(H, device=device, generator=g) * 0.02).to(torch.bfloat16)
         _LAYERS[name] = (experts, shared, gate, g)
     return _LAYERS[name]
