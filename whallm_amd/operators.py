@@ -11,7 +11,8 @@ behaviour as:
 with torch device tensors in place of mlx arrays. The cache is duck-typed as in the
 reference: ``current_batched(layer)`` (a whole-layer table: no host sync, the fused
 kernels index experts on the device), ``get_many(layer, ids)`` / ``iter_ready(layer, ids)``
-(individual resident experts: their regions are gathered into one table), plus the
+(individual resident experts: addressed in place when they are views of one pool, as the
+reference's slot views are, else gathered into one table), plus the
 optional recording hooks. Routed experts, the bf16 shared ``MLP`` (with its sigmoid gate
 and the add) and the combines run on the library's kernels. Only an activation other than
 (clamped) SwiGLU takes a generic path: library GEMMs (hipBLASLt through torch) over
@@ -21,6 +22,7 @@ SwiGLU hot path.
 """
 from __future__ import annotations
 
+import math
 import time
 from dataclasses import dataclass, replace
 
@@ -139,14 +141,50 @@ def _stack_tables(tables: list):
     return type(first)(*fields, up_first=first.up_first, swiglu_limit=first.swiglu_limit)
 
 
+def _pool_table(tables: list):
+    """One table over single-expert tables whose regions are views of shared storages at one
+    stride per region (the slot views of a pool, or [i] of region-major tensors, which is how
+    the reference's get_many hands out resident experts, expert_cache.py:488-497): the
+    library addresses them as base + slot * stride through a slot map, so nothing is copied.
+    None when the regions lie otherwise."""
+    n = len(tables)
+    regions = [[t.tensors()[r] for t in tables] for r in range(4)]
+    slot_of = None
+    fields = []
+    for ts in regions:
+        t0 = ts[0]
+        if any(t.dim() != 2 or t.shape != t0.shape or t.stride() != t0.stride() or t.dtype != t0.dtype
+               or t.untyped_storage().data_ptr() != t0.untyped_storage().data_ptr() for t in ts):
+            return None
+        offs = [t.storage_offset() for t in ts]
+        lo = min(offs)
+        if slot_of is None:       # slot numbers from the first region's offsets
+            unit = 0
+            for o in offs:
+                unit = math.gcd(unit, o - lo)
+            unit = unit or t0.numel()
+            slot_of = [(o - lo) // unit for o in offs]
+            if len(set(slot_of)) != n:
+                return None
+        top = max(range(n), key=lambda i: slot_of[i])
+        step = (offs[top] - lo) // slot_of[top] if slot_of[top] else t0.numel()
+        if step < t0.numel() or any(o - lo != s * step for o, s in zip(offs, slot_of)):
+            return None
+        fields.append(t0.as_strided((slot_of[top] + 1, *t0.shape), (step, *t0.stride()), lo))
+    first = tables[0]
+    slots = torch.tensor(slot_of, dtype=torch.int32).to(fields[0].device, non_blocking=True)
+    return type(first)(*fields, slots=slots, experts=n, up_first=first.up_first, swiglu_limit=first.swiglu_limit)
+
+
 def _resident_table(resident: ResidentExperts, experts: list[int], limit: float):
-    """Gather the individual experts of ``experts`` (unique ids) into one compact table."""
+    """The individual experts of ``experts`` (unique ids) as one compact table: addressed in
+    place when their regions share a pool (_pool_table), else gathered by a copy."""
     singles = []
     for e in experts:
         if e not in resident.slots:
             raise ValueError(f"expert {e} is not resident")
         singles.append(_as_table(resident.individual_weights[resident.slots[e]], limit))
-    return _stack_tables(singles)
+    return _pool_table(singles) or _stack_tables(singles)
 
 
 def _compact(indices: torch.Tensor, experts: list[int]) -> torch.Tensor:
