@@ -61,9 +61,12 @@ typedef struct wm_mxfp4_experts {
                                     (wm_repack_prefill_mxfp4), grouped-GEMM path only */
 } wm_mxfp4_experts;
 
-/* FP8-E4M3 expert set with fp32 128x128 block scales (mimo/weights.py:17-43):
- * w13 [2I, H] bytes (gate rows first unless up_first), scales [ceil(2I/128), ceil(H/128)];
- * w2 [H, I] bytes, scales [ceil(H/128), ceil(I/128)]. I must be a multiple of 128. */
+/* FP8-E4M3 expert set. scale_format 0: fp32 128x128 block scales (the DeepSeek-V3 / MiMo
+ * checkpoints, mimo/weights.py:17-43): w13 [2I, H] bytes (gate rows first unless up_first),
+ * scales fp32 [ceil(2I/128), ceil(H/128)]; w2 [H, I] bytes, scales [ceil(H/128), ceil(I/128)].
+ * scale_format 1: one E8M0 byte (2^(b-127)) per 32x32 block (the V4.1 release,
+ * deepseek_v41/dequant.py:45-50; Native/DeepSeekNative/kernels.metal:17-28): scales u8
+ * [2I/32, H/32] and [H/32, I/32]. H and I must be multiples of 128. */
 typedef struct wm_fp8_experts {
   const void* w13;
   const void* w13_scales;
@@ -78,6 +81,7 @@ typedef struct wm_fp8_experts {
   float swiglu_limit;
   int32_t tiled;                 /* 0: the reference's row layout; 1: prefill tile layout of the
                                     weight bytes (wm_repack_prefill_fp8), grouped-GEMM path only */
+  int32_t scale_format;          /* 0: fp32 128x128 blocks; 1: E8M0 32x32 blocks */
 } wm_fp8_experts;
 
 /* Message of the last failed call on this thread ("" when none). */
@@ -95,6 +99,12 @@ WM_EXPORT int wm_dequant_mxfp4(const void* packed, const void* scales, int64_t r
  * (mimo/weights.py:17-43) without the bf16 rounding. */
 WM_EXPORT int wm_dequant_fp8_blocks(const void* weight, const float* scales, int64_t rows, int64_t cols,
                                     float* out, void* stream);
+/* out[r, c] = e4m3(w[r, c]) * 2^(scales[r/32, c/32] - 127) as fp32 (exact), scales E8M0 u8
+ * [ceil(rows/32), ceil(cols/32)]: dequant_fp8 of the V4.1 release (deepseek_v41/dequant.py:45-50)
+ * before its cast to the output dtype; e8m0_256 x fp8x4 of Native/DeepSeekNative/kernels.metal:17-28.
+ * Scale byte 255 gives NaN (OCP MX). */
+WM_EXPORT int wm_dequant_fp8_e8m0(const void* weight, const void* scales, int64_t rows, int64_t cols, float* out,
+                                  void* stream);
 
 /* ---- routing --------------------------------------------------------------
  * logits [T, E] fp32 -> indices [T, K] int32 (descending, ties -> lower index)

@@ -122,6 +122,32 @@ def dequant_fp8_blocks(weight: np.ndarray, scales: np.ndarray) -> np.ndarray:
     return (e4m3_value(w) * expanded).astype(np.float32)
 
 
+FP8_E8M0_BLOCK = 32  # V4.1 release: one E8M0 byte per 32 x 32 block (deepseek_v41/dequant.py:25)
+
+
+def dequant_fp8_e8m0(weight: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """FP8 E4M3 [rows, cols] bytes + E8M0 u8 [ceil(rows/32), ceil(cols/32)] -> fp32.
+
+    Restates dequant_fp8 of runtime/deepseek_v4_ssd/deepseek_v41/dequant.py:45-50: every
+    value times 2^(b - 127) of its 32 x 32 block (_expand_blocks crops the ceil overhang,
+    :39-42), exact in fp32; the reference then casts to its output dtype (bf16 by default),
+    which the expert path does not (the oracle's dequant-then-matmul is fp32). The native
+    decoders compute the same products (fp8x4 x e8m0_256, Native/DeepSeekNative/kernels.metal:
+    17-28). Byte 255 is NaN (OCP MX), byte 0 is 2^-127.
+    """
+    w = np.asarray(weight)
+    s = np.asarray(scales)
+    if w.ndim != 2 or s.ndim != 2 or w.dtype != np.uint8 or s.dtype != np.uint8:
+        raise ValueError("FP8 weights and E8M0 scales must be 2-D uint8 tensors")
+    rows, cols = w.shape
+    if rows < 1 or cols < 1:
+        raise ValueError("FP8 tensor cannot be empty")
+    if s.shape != (-(-rows // FP8_E8M0_BLOCK), -(-cols // FP8_E8M0_BLOCK)):
+        raise ValueError("E8M0 scale shape does not match 32x32 block padding")
+    expanded = np.repeat(np.repeat(e8m0_value(s), FP8_E8M0_BLOCK, axis=0), FP8_E8M0_BLOCK, axis=1)[:rows, :cols]
+    return (e4m3_value(w) * expanded).astype(np.float32)
+
+
 def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
     return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
 

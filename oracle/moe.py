@@ -32,7 +32,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .formats import dequant_mxfp4, dequant_fp8_blocks, bf16_round_f32
+from .formats import dequant_mxfp4, dequant_fp8_blocks, dequant_fp8_e8m0, bf16_round_f32
 
 
 # ----------------------------------------------------------------------------- routing
@@ -281,21 +281,24 @@ def ffn_dense(x: np.ndarray, wgu: np.ndarray, wd: np.ndarray, limit: float = 0.0
 
 @dataclass
 class FP8Expert:
-    """DeepSeek-style FP8 expert: w1 (gate) / w3 (up) [I, H] and w2 [H, I]
-    E4M3 bytes with fp32 128x128 block scales (mimo/weights.py:17-43)."""
+    """DeepSeek-style FP8 expert: w1 (gate) / w3 (up) [I, H] and w2 [H, I] E4M3 bytes with
+    fp32 128x128 block scales (scale_format 0, mimo/weights.py:17-43) or E8M0 32x32 block
+    scales (scale_format 1, the V4.1 release, deepseek_v41/dequant.py:45-50)."""
     w1: np.ndarray
     w1_scales: np.ndarray
     w3: np.ndarray
     w3_scales: np.ndarray
     w2: np.ndarray
     w2_scales: np.ndarray
+    scale_format: int = 0
 
 
 def fp8_expert_ffn(x: np.ndarray, e: FP8Expert, limit: float = 0.0) -> np.ndarray:
     """SharedExpert / routed expert of deepseek_v41/moe.py:77-93 in fp32."""
-    w1 = dequant_fp8_blocks(e.w1, e.w1_scales)
-    w3 = dequant_fp8_blocks(e.w3, e.w3_scales)
-    w2 = dequant_fp8_blocks(e.w2, e.w2_scales)
+    deq = dequant_fp8_e8m0 if e.scale_format == 1 else dequant_fp8_blocks
+    w1 = deq(e.w1, e.w1_scales)
+    w3 = deq(e.w3, e.w3_scales)
+    w2 = deq(e.w2, e.w2_scales)
     return ffn_dense(x, np.concatenate([w1, w3], axis=0), w2, limit, up_first=False)
 
 

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import whallm_amd as wa
+from oracle import formats as F
 from oracle import moe as M
 from whallm_amd import synthetic as S
 
@@ -17,12 +18,14 @@ pytestmark = pytest.mark.gpu
 
 def oracle_experts(a, n, up_first=False):
     I = a["w13"].shape[1] // 2
+    fmt = 1 if a["w13_scales"].dtype == np.uint8 else 0   # E8M0 32x32 or fp32 128x128 blocks
+    b = I // (32 if fmt else 128)
     out = {}
     for e in range(n):
         w13, s13 = a["w13"][e], a["w13_scales"][e]
-        g, sg = (w13[I:], s13[I // 128:]) if up_first else (w13[:I], s13[:I // 128])
-        u, su = (w13[:I], s13[:I // 128]) if up_first else (w13[I:], s13[I // 128:])
-        out[e] = M.FP8Expert(g, sg, u, su, a["w2"][e], a["w2_scales"][e])
+        g, sg = (w13[I:], s13[b:]) if up_first else (w13[:I], s13[:b])
+        u, su = (w13[:I], s13[:b]) if up_first else (w13[I:], s13[b:])
+        out[e] = M.FP8Expert(g, sg, u, su, a["w2"][e], a["w2_scales"][e], scale_format=fmt)
     return out
 
 
@@ -43,12 +46,13 @@ CASES = {  # name: (H, I, E, K, T)
 }
 
 
+@pytest.mark.parametrize("fmt", [0, 1], ids=["fp32-128", "e8m0-32"])
 @pytest.mark.parametrize("case", sorted(CASES))
-def test_moe_fp8_matches_oracle(device, case):
+def test_moe_fp8_matches_oracle(device, case, fmt):
     H, I, E, K, T = CASES[case]
     rng = np.random.default_rng(H + I + T)
-    a = S.fp8_experts_np(rng, E, H, I)
-    sh = S.fp8_experts_np(rng, 1, H, I)
+    a = S.fp8_experts_np(rng, E, H, I, scale_format=fmt)
+    sh = S.fp8_experts_np(rng, 1, H, I, scale_format=fmt)
     x = S.bf16_normal_np(rng, (T, H))
     logits = rng.standard_normal((T, E)).astype(np.float32)
     bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
@@ -168,3 +172,58 @@ def test_fp8_edges_empty_k1_slots_and_invalid_ids(device):
     torch.cuda.synchronize()
     assert torch.count_nonzero(out[0, 0]).item() == 0
     close(out[1:, 0].float().cpu().numpy(), M.routed_outputs(xf, idx, ex, ffn=M.fp8_expert_ffn)[1:, 0], "valid pairs")
+
+
+# ----------------------------------------------------------------------------- V4.1 FP8 (E8M0 32x32 blocks)
+
+def test_dequant_fp8_e8m0_bit_exact(device):
+    """wm_dequant_fp8_e8m0 against the oracle (dequant_fp8, deepseek_v41/dequant.py:45-50) for
+    every E4M3 code under scale bytes 10..245 (the products stay normal fp32 numbers), on a
+    ragged shape whose last 32 x 32 blocks are cropped; the NaN codes give NaN."""
+    rng = np.random.default_rng(5)
+    rows, cols = 70, 8 * 256 + 24
+    w = np.tile(np.arange(256, dtype=np.uint8), (rows, cols // 256 + 1))[:, :cols].copy()
+    rng.shuffle(w, axis=1)
+    s = rng.integers(10, 246, size=(-(-rows // 32), -(-cols // 32)), dtype=np.uint8)
+    got = wa.dequant_fp8_e8m0(torch.from_numpy(w).to(device), torch.from_numpy(s).to(device)).cpu().numpy()
+    nan = (w & 127) == 127
+    want = F.dequant_fp8_e8m0(np.where(nan, 0, w).astype(np.uint8), s)
+    assert np.all(np.isnan(got[nan]))
+    np.testing.assert_array_equal(got[~nan], want[~nan])
+
+
+V41 = (5120, 2304)   # hidden, moe_inter_dim of the V4.1 release (deepseek_v41/config.py:31-33)
+
+
+@pytest.mark.parametrize("T", [1, 4, 300])
+def test_v41_fp8_shared_expert_and_routed(device, T):
+    """The V4.1 shared expert's format (E4M3 with E8M0 32x32 blocks, deepseek_v41/moe.py:77-93)
+    at its hidden 5120 / intermediate 2304: T = 1 and 4 take the fused GEMV (2304 is not a
+    multiple of 1024, so the last chunk of each down row is partial), T = 300 the grouped GEMM
+    with the E8M0 bytes as MFMA scales; the prefill tile layout gives the row layout's output
+    bit for bit. Routed experts of the same format, clamped SwiGLU (limit 10)."""
+    H, I = V41
+    E, K = 6, 2
+    rng = np.random.default_rng(T + 91)
+    a = S.fp8_experts_np(rng, E, H, I, scale_format=1)
+    sh = S.fp8_experts_np(rng, 1, H, I, scale_format=1)
+    x = S.bf16_normal_np(rng, (T, H))
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.1, 1.0, size=(T, K)).astype(np.float32)
+    rows = S.fp8_experts_to_device(a, device, swiglu_limit=10.0)
+    rows_sh = S.fp8_experts_to_device(sh, device, swiglu_limit=10.0)
+    assert rows.scale_format == 1
+    xt, it, wt = S.bf16_bits_to_tensor(x, device), torch.from_numpy(idx).to(device), torch.from_numpy(w).to(device)
+    y = wa.moe_fp8(xt, it, wt, rows, rows_sh, None)
+    out = wa.experts_fp8(xt, it, rows)
+    torch.cuda.synchronize()
+    xf = S.bf16_bits_to_f32(x)
+    check = np.arange(T) if T <= 4 else np.linspace(0, T - 1, 16).astype(np.int64)
+    ex = oracle_experts(a, E)
+    routed = M.routed_outputs(xf[check], idx[check], ex, ffn=M.fp8_expert_ffn, limit=10.0)
+    shared = M.fp8_expert_ffn(xf[check], oracle_experts(sh, 1)[0], limit=10.0)
+    close(y.float().cpu().numpy()[check], M.combine(routed, w[check], shared, None), f"V4.1 FP8 layer T={T}")
+    close(out.float().cpu().numpy()[check], routed, f"V4.1 FP8 router order T={T}")
+    if T == 300:
+        tiled, tiled_sh = wa.prefill_layout(rows), wa.prefill_layout(rows_sh)
+        assert torch.equal(wa.moe_fp8(xt, it, wt, tiled, tiled_sh, None), y)

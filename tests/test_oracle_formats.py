@@ -223,3 +223,25 @@ def test_split_rows_exact_and_zero_blocks():
     assert s_hi == 127 - 3 and s_lo == 1 and not np.any(lo & 31)
     np.testing.assert_array_equal(F.e2m3_value(hi) * np.float32(2.0 ** -3), blk)
     assert list(s[192:200]) == [124, 1, 1, 1, 1, 1, 1, 1] and not np.any(s[48:192])   # zero blocks: exponent 1
+
+
+def test_fp8_e8m0_dequant_closed_form_and_crop():
+    """dequant_fp8 of the V4.1 release (deepseek_v41/dequant.py:45-50): every E4M3 value (torch's
+    float8_e4m3fn decoder, independent of the oracle's table) times 2^(b - 127) of its 32 x 32
+    block, computed in float64, with the ceil overhang of ragged edges cropped (:39-42); the
+    products are exact, so the comparison is equality."""
+    rng = np.random.default_rng(3)
+    rows, cols = 70, 100
+    w = rng.integers(0, 256, size=(rows, cols), dtype=np.uint8)
+    w[(w & 127) == 127] = 0                       # reserved NaN codes
+    s = rng.integers(100, 155, size=(3, 4), dtype=np.uint8)
+    s[0, 0], s[2, 3] = 1, 254
+    out = F.dequant_fp8_e8m0(w, s)
+    vals = torch.from_numpy(w).view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    r, c = np.meshgrid(np.arange(rows), np.arange(cols), indexing="ij")
+    want = vals * np.exp2(s[r // 32, c // 32].astype(np.float64) - 127)
+    assert out.dtype == np.float32
+    np.testing.assert_array_equal(out.astype(np.float64), want.astype(np.float32).astype(np.float64))
+    assert out[69, 99] == F.e4m3_value(w[69, 99]) * np.float32(2.0 ** (int(s[2, 3]) - 127))
+    with pytest.raises(ValueError):
+        F.dequant_fp8_e8m0(w, s[:2])

@@ -29,7 +29,7 @@ class FP8ExpertsC(ctypes.Structure):
         ("w13", c_void_p), ("w13_scales", c_void_p), ("w2", c_void_p), ("w2_scales", c_void_p),
         ("w13_stride", c_int64), ("w13_scales_stride", c_int64), ("w2_stride", c_int64), ("w2_scales_stride", c_int64),
         ("slots", c_void_p), ("experts", c_int32), ("hidden", c_int32), ("inter", c_int32),
-        ("up_first", c_int32), ("swiglu_limit", c_float), ("tiled", c_int32),
+        ("up_first", c_int32), ("swiglu_limit", c_float), ("tiled", c_int32), ("scale_format", c_int32),
     ]
 
 
@@ -51,6 +51,7 @@ _SIGNATURES = {
     "wm_version": (c_char_p, []),
     "wm_dequant_mxfp4": (c_int, [_P, _P, c_int64, c_int64, _P, c_int, _P]),
     "wm_dequant_fp8_blocks": (c_int, [_P, _P, c_int64, c_int64, _P, _P]),
+    "wm_dequant_fp8_e8m0": (c_int, [_P, _P, c_int64, c_int64, _P, _P]),
     "wm_route_softmax_topk": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, _P, _P, _P, _P]),
     "wm_route_scored": (c_int, [_P, _P, c_int32, c_int32, c_int32, c_int32, c_float, c_int32, c_int32, c_int32,
                                 _P, _P, _P]),

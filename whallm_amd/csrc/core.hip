@@ -55,6 +55,16 @@ __global__ void __launch_bounds__(256) dequant_fp8_kernel(const uint8_t* __restr
   out[i] = e4m3_to_f32(w[i]) * s[(r / 128) * scale_cols + c / 128];
 }
 
+// V4.1 FP8: out[r, c] = e4m3(w[r, c]) * 2^(s[r / 32, c / 32] - 127), the exact product.
+__global__ void __launch_bounds__(256) dequant_fp8_e8m0_kernel(const uint8_t* __restrict__ w,
+                                                              const uint8_t* __restrict__ s, int64_t rows,
+                                                              int64_t cols, float* __restrict__ out) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * cols) return;
+  int64_t r = i / cols, c = i % cols;
+  out[i] = e4m3_to_f32(w[i]) * e8m0_value(s[(r / 32) * ((cols + 31) / 32) + c / 32]);
+}
+
 }  // namespace wm
 
 using namespace wm;
@@ -92,6 +102,19 @@ WM_EXPORT int wm_dequant_fp8_blocks(const void* weight, const float* scales, int
     hipLaunchKernelGGL(dequant_fp8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
                        (const uint8_t*)weight, scales, rows, cols, out);
     check_launch("dequant_fp8_blocks");
+  });
+}
+
+WM_EXPORT int wm_dequant_fp8_e8m0(const void* weight, const void* scales, int64_t rows, int64_t cols, float* out,
+                                  void* stream) {
+  return guarded([&] {
+    if (!weight || !scales || !out) fail("wm_dequant_fp8_e8m0: null pointer");
+    if (rows < 0 || cols < 0) fail("wm_dequant_fp8_e8m0: negative size");
+    int64_t n = rows * cols;
+    if (n == 0) return;
+    hipLaunchKernelGGL(dequant_fp8_e8m0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       (const uint8_t*)weight, (const uint8_t*)scales, rows, cols, out);
+    check_launch("dequant_fp8_e8m0");
   });
 }
 

@@ -1,5 +1,8 @@
 // Decode-time FP8-E4M3 expert FFN with fp32 128x128 block scales (the DeepSeek-V3
-// expert format, mimo/weights.py:17-43): fused dequant + GEMV, HBM-bound.
+// expert format, mimo/weights.py:17-43) or E8M0 32x32 block scales (the V4.1 release,
+// deepseek_v41/dequant.py:45-50): fused dequant + GEMV, HBM-bound. Widths are multiples of
+// 128 up to 8192: a lane reads 16 bytes of each 1024-byte chunk of a row, and the lanes past
+// a row's end (the last chunk of a width that is not a multiple of 1024) load nothing.
 //
 // Replaces the reference's FP8 expert linears (Native/DeepSeekNative/kernels.metal:82-124,
 // linear_fp8 of the shared expert; the routed experts decode FP8 only at install time,
@@ -10,7 +13,8 @@
 //                     1024-byte chunk (fully coalesced), converts them to bf16 exactly
 //                     (v_cvt_scalef32_pk_bf16_fp8 with scale 1), dots them with the bf16
 //                     input (v_dot2_f32_bf16) and multiplies the 16-column partial by the
-//                     fp32 scale of its 128 x 128 block; silu(gate) * up (clamped when the
+//                     scale of its block (fp32, or 2^(b-127) of its E8M0 byte, both exact
+//                     powers or floats applied once per partial); silu(gate) * up (clamped when the
 //                     table sets a SwiGLU limit) -> act (fp32).
 //   fp8_down        : one workgroup = (token, 8 output rows); the four waves split the
 //                     token's experts (routed + shared) and keep routing-weighted partial
@@ -77,8 +81,19 @@ __device__ __forceinline__ bool fp8_pair(int p, int tokens, int k, const int32_t
 
 constexpr int FP8_RPW = 2;  // intermediate rows per wave (4 weight rows: gate and up of each)
 
-// grid: (I / (4 * FP8_RPW), pairs). CPL = H / 1024 chunks of 16 bytes per lane per row.
-template <int CPL>
+// The block scale of the 16 columns [c, c + 16) of row `row` in a matrix of `cols` columns:
+// SF 0, fp32 128 x 128 blocks; SF 1, E8M0 32 x 32 blocks (2^(b - 127)).
+template <int SF>
+__device__ __forceinline__ float fp8_block_scale(const uint8_t* scales, int row, int cols, int c) {
+  if constexpr (SF == 0)
+    return gload<float>(reinterpret_cast<const float*>(scales) + (int64_t)(row / 128) * (cols / 128) + c / 128);
+  else
+    return e8m0_value(gload<uint8_t>(scales + (int64_t)(row / 32) * (cols / 32) + c / 32));
+}
+
+// grid: (I / (4 * FP8_RPW), pairs). CPL = ceil(H / 1024) chunks of 16 bytes per lane per row;
+// SF the scale format.
+template <int CPL, int SF>
 __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __restrict__ x, int tokens, int k,
                                                               const int32_t* __restrict__ indices,
                                                               wm_fp8_experts routed, wm_fp8_experts shared,
@@ -87,7 +102,7 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
   __shared__ float sums[4][ROWS];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int p = blockIdx.y;
-  const int H = routed.hidden, I = routed.inter, HB = H / 128;
+  const int H = routed.hidden, I = routed.inter;
   int t;
   Fp8Regions r;
   bool is_shared;
@@ -102,31 +117,35 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
   const float limit = tab.swiglu_limit;
   const int i_base = blockIdx.x * 4 * FP8_RPW + wave * FP8_RPW;
 
-  uint32_t xw[CPL][8];  // x[1024 m + 16 lane .. +15] as bf16 pairs
+  uint32_t xw[CPL][8];  // x[1024 m + 16 lane .. +15] as bf16 pairs (zero past the row)
   const uint16_t* xr = x + (int64_t)t * H;
 #pragma unroll
   for (int m = 0; m < CPL; ++m) {
+    const bool in = 1024 * m + 16 * lane < H;
     const uint4* src = reinterpret_cast<const uint4*>(xr + 1024 * m + 16 * lane);
-    const uint4 a = src[0], b = src[1];
+    const uint4 a = in ? src[0] : make_uint4(0, 0, 0, 0), b = in ? src[1] : make_uint4(0, 0, 0, 0);
     xw[m][0] = a.x; xw[m][1] = a.y; xw[m][2] = a.z; xw[m][3] = a.w;
     xw[m][4] = b.x; xw[m][5] = b.y; xw[m][6] = b.z; xw[m][7] = b.w;
   }
-  // a wave's FP8_RPW gate rows lie in one 128-row scale block, and so do its up rows
-  static_assert(128 % (4 * FP8_RPW) == 0, "a workgroup's rows lie in one scale block");
+  // a wave's FP8_RPW gate rows lie in one scale block (128 or 32 rows), and so do its up rows
+  static_assert(32 % (4 * FP8_RPW) == 0, "a workgroup's rows lie in one scale block");
   uint4 wq[ROWS][CPL];
   float sc[2][CPL];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int row = (h ^ up_first) ? I + i_base : i_base;  // h 0: gate, 1: up
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) sc[h][m] = gload<float>(r.w13_scales + (int64_t)(row / 128) * HB + 8 * m + lane / 8);
+    for (int m = 0; m < CPL; ++m)
+      sc[h][m] = 1024 * m + 16 * lane < H ? fp8_block_scale<SF>(r.w13_scales, row, H, 1024 * m + 16 * lane) : 0.0f;
   }
 #pragma unroll
   for (int q = 0; q < ROWS; ++q) {
     const int i = i_base + q / 2;  // I is a multiple of 8: always in range
     const int row = ((q & 1) ^ up_first) ? I + i : i;  // q even: gate, odd: up
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) wq[q][m] = gload16_nt(r.w13 + (int64_t)row * H + 1024 * m + 16 * lane);
+    for (int m = 0; m < CPL; ++m)
+      wq[q][m] = 1024 * m + 16 * lane < H ? gload16_nt(r.w13 + (int64_t)row * H + 1024 * m + 16 * lane)
+                                           : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int q = 0; q < ROWS; ++q) {
@@ -149,8 +168,8 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
 
 constexpr int FP8_OPW = 8;  // output rows per wave step
 
-// grid: combine (H / FP8_OPW, tokens); per pair (H / (4 * FP8_OPW), pairs). CPL = I / 1024.
-template <int CPL, bool COMBINE>
+// grid: combine (H / FP8_OPW, tokens); per pair (H / (4 * FP8_OPW), pairs). CPL = ceil(I / 1024).
+template <int CPL, int SF, bool COMBINE>
 __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__ act, int tokens, int k,
                                                        const int32_t* __restrict__ indices,
                                                        const float* __restrict__ weights, wm_fp8_experts routed,
@@ -161,7 +180,7 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
   __shared__ float partial[4][FP8_OPW];
   __shared__ float gate_value;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int H = routed.hidden, I = routed.inter, IB = I / 128;
+  const int H = routed.hidden, I = routed.inter;
   int t, o_base, first, step, n_entries;
   if (COMBINE) {
     t = blockIdx.y;
@@ -225,25 +244,29 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
     const float* arow = act + (int64_t)p * I;
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
+      const bool in = 1024 * m + 16 * lane < I;
       const float4* a4 = reinterpret_cast<const float4*>(arow + 1024 * m + 16 * lane);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float4 v = a4[q];
+        const float4 v = in ? a4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         av[m][4 * q] = v.x; av[m][4 * q + 1] = v.y; av[m][4 * q + 2] = v.z; av[m][4 * q + 3] = v.w;
       }
     }
-    // the step's FP8_OPW rows start at a multiple of FP8_OPW, so they share one 128-row
-    // scale block: one scale load per 1024-wide chunk
-    static_assert(128 % FP8_OPW == 0, "a step's rows lie in one scale block");
+    // the step's FP8_OPW rows start at a multiple of FP8_OPW, so they share one scale block
+    // (128 or 32 rows): one scale load per 1024-wide chunk
+    static_assert(32 % FP8_OPW == 0, "a step's rows lie in one scale block");
     uint4 wq[FP8_OPW][CPL];
     float sc[CPL];
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) sc[m] = gload<float>(r.w2_scales + (int64_t)(o_base / 128) * IB + 8 * m + lane / 8);
+    for (int m = 0; m < CPL; ++m)
+      sc[m] = 1024 * m + 16 * lane < I ? fp8_block_scale<SF>(r.w2_scales, o_base, I, 1024 * m + 16 * lane) : 0.0f;
 #pragma unroll
     for (int q = 0; q < FP8_OPW; ++q) {
       const int o = o_base + q;  // H is a multiple of 32: always in range
 #pragma unroll
-      for (int m = 0; m < CPL; ++m) wq[q][m] = gload16_nt(r.w2 + (int64_t)o * I + 1024 * m + 16 * lane);
+      for (int m = 0; m < CPL; ++m)
+        wq[q][m] = 1024 * m + 16 * lane < I ? gload16_nt(r.w2 + (int64_t)o * I + 1024 * m + 16 * lane)
+                                             : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < FP8_OPW; ++q) {
@@ -270,40 +293,51 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
   }
 }
 
-void decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
-                const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
-                uint16_t* y, bool combine, float* act, hipStream_t s) {
+template <int SF>
+static void launch_decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                              const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
+                              uint16_t* y, bool combine, float* act, hipStream_t s) {
   const int H = routed.hidden, I = routed.inter;
-  if (H % 1024 || I % 1024 || H / 1024 > 8 || I / 1024 > 8)
-    fail("FP8 decode: hidden and intermediate must be multiples of 1024 up to 8192");
   const int pairs = tokens * k + (shared ? tokens : 0);
   const wm_fp8_experts sh = shared ? *shared : routed;
   const dim3 g1(I / (4 * FP8_RPW), pairs);
-  switch (H / 1024) {
-#define WM_F8GU(C) case C: hipLaunchKernelGGL(fp8_gate_up_act_kernel<C>, g1, dim3(256), 0, s, x, tokens, k, indices, \
-                                              routed, sh, shared ? 1 : 0, act); break;
+  switch ((H + 1023) / 1024) {
+#define WM_F8GU(C) case C: hipLaunchKernelGGL((fp8_gate_up_act_kernel<C, SF>), g1, dim3(256), 0, s, x, tokens, k, \
+                                              indices, routed, sh, shared ? 1 : 0, act); break;
     WM_F8GU(1) WM_F8GU(2) WM_F8GU(3) WM_F8GU(4) WM_F8GU(5) WM_F8GU(6) WM_F8GU(7) WM_F8GU(8)
 #undef WM_F8GU
   }
   check_launch("fp8_gate_up_act");
   if (combine) {
     const dim3 g2(H / FP8_OPW, tokens);
-    switch (I / 1024) {
-#define WM_F8DN(C) case C: hipLaunchKernelGGL((fp8_down_kernel<C, true>), g2, dim3(256), 0, s, act, tokens, k, indices, \
-                                              weights, routed, sh, shared ? 1 : 0, x, shared_gate, y); break;
+    switch ((I + 1023) / 1024) {
+#define WM_F8DN(C) case C: hipLaunchKernelGGL((fp8_down_kernel<C, SF, true>), g2, dim3(256), 0, s, act, tokens, k, \
+                                              indices, weights, routed, sh, shared ? 1 : 0, x, shared_gate, y); break;
       WM_F8DN(1) WM_F8DN(2) WM_F8DN(3) WM_F8DN(4) WM_F8DN(5) WM_F8DN(6) WM_F8DN(7) WM_F8DN(8)
 #undef WM_F8DN
     }
   } else {
     const dim3 g2(H / (4 * FP8_OPW), tokens * k);
-    switch (I / 1024) {
-#define WM_F8DP(C) case C: hipLaunchKernelGGL((fp8_down_kernel<C, false>), g2, dim3(256), 0, s, act, tokens, k, indices, \
-                                              weights, routed, sh, 0, x, nullptr, y); break;
+    switch ((I + 1023) / 1024) {
+#define WM_F8DP(C) case C: hipLaunchKernelGGL((fp8_down_kernel<C, SF, false>), g2, dim3(256), 0, s, act, tokens, k, \
+                                              indices, weights, routed, sh, 0, x, nullptr, y); break;
       WM_F8DP(1) WM_F8DP(2) WM_F8DP(3) WM_F8DP(4) WM_F8DP(5) WM_F8DP(6) WM_F8DP(7) WM_F8DP(8)
 #undef WM_F8DP
     }
   }
   check_launch("fp8_down");
+}
+
+void decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
+                const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
+                uint16_t* y, bool combine, float* act, hipStream_t s) {
+  const int H = routed.hidden, I = routed.inter;
+  if (H % 128 || I % 128 || H > 8192 || I > 8192)
+    fail("FP8 decode: hidden and intermediate must be multiples of 128 up to 8192");
+  if (routed.scale_format == 1)
+    launch_decode_fp8<1>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, act, s);
+  else
+    launch_decode_fp8<0>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, act, s);
 }
 
 }  // namespace wm

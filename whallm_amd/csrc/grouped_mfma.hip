@@ -1,7 +1,8 @@
 // Prefill-time expert FFN on gfx950 scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4):
 // grouped GEMMs over the row tiles of the permute kernel, for MXFP4 weights (E2M1 codes
 // with an E8M0 scale per 32, fed to the MFMA as stored) and for FP8-E4M3 weights with
-// fp32 128 x 128 block scales.
+// fp32 128 x 128 block scales or with E8M0 32 x 32 block scales (the V4.1 release; the
+// E8M0 bytes ride on the MFMA's A scales like MXFP4's).
 //
 // Replaces gather_rows16 + expert_gemm_sg (gate_up) + expert_act + expert_gemm_sg (down) +
 // moe_combine_rows (Native/QwenNative/kernels.metal:691-765, engine.mm:2104-2162) and
@@ -284,18 +285,17 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
 //   weights [K/128 steps][R/16 groups][P pieces][16 rows][16 bytes]: piece p of a row's step
 //           is its bytes [16p, 16p + 16) of the 16 P the step takes in the row layout;
 //   MXFP4 scales [K/128 steps][R rows][4 bytes]: the row's 4 E8M0 bytes of the step;
-//   FP8 block scales [R/128][K/128] fp32, copied unchanged.
+//   FP8 block scales copied unchanged: fp32 [R/128][K/128], or E8M0 bytes [R/32][K/32].
 // One 16-byte piece (or one 4-byte scale word) per thread.
 template <int P>
 __global__ void __launch_bounds__(256) repack_prefill_kernel(const uint8_t* __restrict__ src,
                                                              const uint8_t* __restrict__ src_s, int64_t stride,
                                                              int64_t stride_s, const int32_t* __restrict__ slots,
-                                                             int experts, int rows, int k, uint8_t* __restrict__ dst,
-                                                             uint8_t* __restrict__ dst_s) {
+                                                             int experts, int rows, int k, int64_t words,
+                                                             uint8_t* __restrict__ dst, uint8_t* __restrict__ dst_s) {
   const int64_t row_pieces = (int64_t)(k / 128) * P;   // 16-byte pieces per row
   const int64_t row_bytes = 16 * row_pieces;
-  const int64_t pieces = (int64_t)rows * row_pieces;   // per expert
-  const int64_t words = (int64_t)(P == 4 ? rows : rows / 128) * (k / 128);  // scale words per expert
+  const int64_t pieces = (int64_t)rows * row_pieces;   // per expert; `words`: scale words per expert
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)experts * (pieces + words)) return;
   const int e = (int)(i / (pieces + words));
@@ -418,13 +418,22 @@ __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& ro
 //   scale lane (r, g): K block g; result register i: D[8 (i / 4) + 4 g + i % 4][r].
 // WAVES: waves per workgroup (4: one per SIMD, 8: two); MI = TW / (16 WAVES) weight tiles
 // of 32 rows per wave; DA, DB: depths of the weight and split-row rings.
+// FP8: the A operand is E4M3 bytes (else E2M1 nibbles). A_SCALED: E8M0 A scales are staged
+// per weight row and step (4 bytes) and fed to the MFMA (MXFP4, and FP8 with E8M0 32 x 32
+// blocks, whose rows of one 32-row block share their bytes); BLOCK_F32: FP8 with fp32
+// 128 x 128 block scales, which cannot ride on the MFMA's E8M0 scales.
 struct Mx4 {
-  static constexpr bool FP8 = false;
+  static constexpr bool FP8 = false, A_SCALED = true, BLOCK_F32 = false;
   static constexpr int TW = 512, PIECES = 4, A_FMT = FMT_FP4, DA = 2, DB = 3, WAVES = 8, LW = 8;
   static constexpr int MI = TW / (16 * WAVES);
 };
 struct Mx8 {
-  static constexpr bool FP8 = true;
+  static constexpr bool FP8 = true, A_SCALED = false, BLOCK_F32 = true;
+  static constexpr int TW = 256, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2, WAVES = 8, LW = 8;
+  static constexpr int MI = TW / (16 * WAVES);
+};
+struct Mx8e {
+  static constexpr bool FP8 = true, A_SCALED = true, BLOCK_F32 = false;
   static constexpr int TW = 256, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2, WAVES = 8, LW = 8;
   static constexpr int MI = TW / (16 * WAVES);
 };
@@ -438,7 +447,7 @@ constexpr int NI4 = 2;      // 32-row row tiles per wave
 template <typename F, int DA, int DB>
 struct RingMx {
   static constexpr int A_BYTES = F::TW * F::PIECES * 16;
-  static constexpr int A_SLOT = A_BYTES + (F::FP8 ? 0 : F::TW * 4);
+  static constexpr int A_SLOT = A_BYTES + (F::A_SCALED ? F::TW * 4 : 0);
   static constexpr int B_SLOT = BM * XSTEP;
   static constexpr int BYTES = DA * A_SLOT + DB * B_SLOT;
   static_assert(BYTES <= 160 * 1024, "LDS");
@@ -488,21 +497,21 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
   constexpr int MI = F::MI;
   uint32_t sa[MI];
   uint2 sb[NI4];
-  if constexpr (!F::FP8) {
+  if constexpr (F::A_SCALED) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) sa[mi] = *reinterpret_cast<const uint32_t*>(sta + A_BYTES + lo.as + 4 * mrow(mi));
   }
 #pragma unroll
   for (int ni = 0; ni < NI4; ++ni) sb[ni] = *reinterpret_cast<const uint2*>(stb + lo.bs + 32 * XSTEP * ni);
-  v16f blk[F::FP8 ? MI : 1][NI4];
+  v16f blk[F::BLOCK_F32 ? MI : 1][NI4];
   // FP8 block scales (scalar loads) issued before the MFMAs, so their memory round trip
   // overlaps the step instead of stalling the scale-and-add at its end
-  float bs[F::FP8 ? MI : 1];
-  if constexpr (F::FP8) {
+  float bs[F::BLOCK_F32 ? MI : 1];
+  if constexpr (F::BLOCK_F32) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) bs[mi] = bscale(mi);
   }
-  if constexpr (F::FP8) {
+  if constexpr (F::BLOCK_F32) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -549,7 +558,7 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
       const v8i bh = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, 0, 0};
       const v8i bl = {(int)b1.z, (int)b1.w, (int)b2.x, (int)b2.y, (int)b2.z, (int)b2.w, 0, 0};
       const int sbh = (int)(sb[ni].x >> sh), sbl = (int)(sb[ni].y >> sh);
-      if constexpr (F::FP8) {
+      if constexpr (F::BLOCK_F32) {
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
           blk[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, blk[mi][ni], FMT_FP8, FMT_FP6, 0,
@@ -561,18 +570,18 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
       } else {
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
-          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
+          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, acc[mi][ni], F::A_FMT, FMT_FP6, 0,
                                                                         (int)(sa[mi] >> sh), 0, sbh);
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
-          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, acc[mi][ni], FMT_FP4, FMT_FP6, 0,
+          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, acc[mi][ni], F::A_FMT, FMT_FP6, 0,
                                                                         (int)(sa[mi] >> sh), 0, sbl);
       }
       __builtin_amdgcn_sched_barrier(0);
       between(2 * h + ni);
     }
   }
-  if constexpr (F::FP8) {
+  if constexpr (F::BLOCK_F32) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       const float s = bs[mi];
@@ -595,7 +604,8 @@ struct LoaderMx {
   const uint8_t* wbase;
   const uint8_t* sbase;
   static constexpr int NQ = 32 / F::LW;                // 1 KB loads per wave and operand
-  static constexpr int SQ = F::FP8 ? 0 : 8 / F::LW;     // MXFP4 scale loads per wave
+  // A scale loads per wave: a dword (4 E8M0 bytes) per weight row, 64 rows a load
+  static constexpr int SQ = F::A_SCALED ? (F::TW / 64 + F::LW - 1) / F::LW : 0;
   uint32_t boff[NQ];
   uint32_t aoff[NQ];
   uint32_t soff[SQ > 0 ? SQ : 1];
@@ -612,7 +622,8 @@ struct LoaderMx {
     if (h == 1)
 #pragma unroll
       for (int q = 0; q < SQ; ++q)
-        dma4(sbase, soff[q] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * (w + F::LW * q)));
+        if (64 * (w + F::LW * q) < F::TW)  // wave-uniform
+          dma4(sbase, soff[q] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * (w + F::LW * q)));
   }
   // Half h of step ks's split-row loads into split-row slot `slot` (NQ instructions per step).
   __device__ __forceinline__ void issue_b(uint8_t* slot, int ks, int h) {
@@ -661,8 +672,17 @@ __device__ __forceinline__ void weight_offsets(LoaderMx<F>& ld, const uint8_t* w
       }
       ld.a_step = 128;
     }
-    ld.soff[0] = 0;
-    ld.s_step = 0;
+    if constexpr (F::A_SCALED) {  // E8M0 32 x 32 blocks, [rows / 32][k / 32] bytes in either layout
+#pragma unroll
+      for (int q = 0; q < SQ; ++q) {
+        const int r0 = 64 * (w + F::LW * q);
+        ld.soff[q] = r0 < F::TW ? (uint32_t)(row_of(r0 + lane) / 32 * (k / 32)) : 0u;
+      }
+      ld.s_step = 4;
+    } else {
+      ld.soff[0] = 0;
+      ld.s_step = 0;
+    }
   } else if (tiled) {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::LW * i)) / 16 * 1024 + 16 * lane);
@@ -872,7 +892,7 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
                         const int rr = r % TG;
                         return (r < TG ? gate0 : up0) + (rr < valid ? rr : rr % valid);
                       });
-    if constexpr (F::FP8) {  // a wave's gate (up) rows lie in one 128-row scale block
+    if constexpr (F::BLOCK_F32) {  // a wave's gate (up) rows lie in one 128-row scale block
       t.s0 = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(gate0 / 128) * (H / 128));
       t.s1 = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(up0 / 128) * (H / 128));
     }
@@ -991,7 +1011,7 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) down_mx_kernel(co
     const int nt = t.nt, valid = t.valid;
     auto col_row = [nt, valid](int r) { return nt * F::TW + (r < valid ? r : r % valid); };  // never past H
     weight_offsets<F>(t.ld, tw.w2, tw.w2s, H, I, table_tiled(expert < 0 ? shared : routed), col_row);
-    if constexpr (F::FP8)  // the wave's columns lie in one 128-row scale block
+    if constexpr (F::BLOCK_F32)  // the wave's columns lie in one 128-row scale block
       t.s0 = t.s1 = uniform_ptr(reinterpret_cast<const float*>(tw.w2s) +
                                 (int64_t)(col_row(32 * MI * wn) / 128) * (I / 128));
     t.ld.b = uniform_u8(a6);
@@ -1347,7 +1367,10 @@ size_t prefill_fp8_workspace_size(int tokens, int k, const wm_fp8_experts& e, bo
 void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                  const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
                  uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s) {
-  mf::run<mf::Mx8>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  if (routed.scale_format == 1)
+    mf::run<mf::Mx8e>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  else
+    mf::run<mf::Mx8>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
 }
 
 }  // namespace wm
@@ -1372,9 +1395,10 @@ WM_EXPORT int wm_repack_prefill_mxfp4(const wm_mxfp4_experts* src, void* gate_up
     hipStream_t s = wm::as_stream(stream);
     auto launch = [&](const void* w, const void* ws, int64_t stride, int64_t stride_s, int rows, int k, void* dst,
                       void* dst_s) {
-      const int64_t n = (int64_t)E * ((int64_t)rows * (k / 32) + (int64_t)rows * (k / 128));
+      const int64_t words = (int64_t)rows * (k / 128);
+      const int64_t n = (int64_t)E * ((int64_t)rows * (k / 32) + words);
       hipLaunchKernelGGL(wm::mf::repack_prefill_kernel<4>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                         (const uint8_t*)w, (const uint8_t*)ws, stride, stride_s, src->slots, E, rows, k,
+                         (const uint8_t*)w, (const uint8_t*)ws, stride, stride_s, src->slots, E, rows, k, words,
                          (uint8_t*)dst, (uint8_t*)dst_s);
       wm::check_launch("repack_prefill");
     };
@@ -1394,6 +1418,7 @@ WM_EXPORT int wm_repack_prefill_fp8(const wm_fp8_experts* src, void* w13, void* 
     if (src->experts < 1 || src->experts > 1024) wm::fail("wm_repack_prefill_fp8: expert count must be in 1..1024");
     if (src->hidden < 128 || src->hidden % 128 || src->inter < 128 || src->inter % 128)
       wm::fail("wm_repack_prefill_fp8: hidden and intermediate must be positive multiples of 128");
+    if (src->scale_format != 0 && src->scale_format != 1) wm::fail("wm_repack_prefill_fp8: unknown scale format");
     if (!w13 || !w2 || !w13_scales || !w2_scales) wm::fail("wm_repack_prefill_fp8: null destination");
     auto aligned = [](const void* p, uintptr_t a) { return (uintptr_t)p % a == 0; };
     if (!aligned(w13, 16) || !aligned(w2, 16) || !aligned(src->w13, 16) || !aligned(src->w2, 16) ||
@@ -1407,9 +1432,11 @@ WM_EXPORT int wm_repack_prefill_fp8(const wm_fp8_experts* src, void* w13, void* 
     hipStream_t s = wm::as_stream(stream);
     auto launch = [&](const void* w, const void* ws, int64_t stride, int64_t stride_s, int rows, int k, void* dst,
                       void* dst_s) {
-      const int64_t n = (int64_t)E * ((int64_t)rows * (k / 16) + (int64_t)(rows / 128) * (k / 128));
+      // scale words per expert: fp32 [rows/128][k/128], or E8M0 bytes [rows/32][k/32] as dwords
+      const int64_t words = src->scale_format == 1 ? (int64_t)(rows / 32) * (k / 128) : (int64_t)(rows / 128) * (k / 128);
+      const int64_t n = (int64_t)E * ((int64_t)rows * (k / 16) + words);
       hipLaunchKernelGGL(wm::mf::repack_prefill_kernel<8>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                         (const uint8_t*)w, (const uint8_t*)ws, stride, stride_s, src->slots, E, rows, k,
+                         (const uint8_t*)w, (const uint8_t*)ws, stride, stride_s, src->slots, E, rows, k, words,
                          (uint8_t*)dst, (uint8_t*)dst_s);
       wm::check_launch("repack_prefill_fp8");
     };

@@ -57,6 +57,8 @@ static void validate_fp8(const wm_fp8_experts* e, const char* what, bool shared)
   if (e->w13_stride < 0 || e->w13_scales_stride < 0 || e->w2_stride < 0 || e->w2_scales_stride < 0)
     fail(w + ": negative stride");
   if (e->swiglu_limit < 0.0f) fail(w + ": swiglu_limit must be >= 0");
+  if (e->scale_format != 0 && e->scale_format != 1)
+    fail(w + ": scale_format must be 0 (fp32 128x128 blocks) or 1 (E8M0 32x32 blocks)");
   auto aligned = [](const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; };
   if (!aligned(e->w13, 16) || !aligned(e->w2, 16) || e->w13_stride % 16 || e->w2_stride % 16)
     fail(w + ": weight regions and strides must be 16-byte aligned");
@@ -72,13 +74,16 @@ static void validate_fp8_pair(const wm_fp8_experts* routed, const wm_fp8_experts
       fail("shared expert: hidden and intermediate must equal the routed experts'");
     if ((shared->tiled != 0) != (routed->tiled != 0))
       fail("shared expert: the routed and shared tables must both be in the row layout or both tiled");
+    if (shared->scale_format != routed->scale_format)
+      fail("shared expert: the routed and shared tables must share a scale format");
   }
 }
 
-// The fused GEMV handles hidden / intermediate multiples of 1024 in the row layout; other
-// shapes, tables in the prefill tile layout and larger batches take the grouped GEMM.
+// The fused GEMV handles hidden / intermediate (multiples of 128) up to 8192 in the row
+// layout; larger shapes, tables in the prefill tile layout and larger batches take the
+// grouped GEMM.
 static bool use_decode_fp8(int tokens, int k, const wm_fp8_experts& e) {
-  return !e.tiled && use_decode(tokens, k) && e.hidden % 1024 == 0 && e.inter % 1024 == 0 && e.hidden <= 8192 && e.inter <= 8192;
+  return !e.tiled && use_decode(tokens, k) && e.hidden <= 8192 && e.inter <= 8192;
 }
 
 static size_t decode_workspace(int tokens, int k, const wm_mxfp4_experts& e) {

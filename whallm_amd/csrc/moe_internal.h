@@ -28,12 +28,13 @@ __device__ __forceinline__ ExpertRegions expert_regions(const wm_mxfp4_experts& 
   return r;
 }
 
-// Device addresses of one FP8 expert (w13 = gate/up rows, w2 = down; fp32 128x128 block scales).
+// Device addresses of one FP8 expert (w13 = gate/up rows, w2 = down; block scales fp32
+// 128x128 or E8M0 32x32 bytes, by the table's scale_format).
 struct Fp8Regions {
   const uint8_t* w13;
-  const float* w13_scales;
+  const uint8_t* w13_scales;
   const uint8_t* w2;
-  const float* w2_scales;
+  const uint8_t* w2_scales;
 };
 
 __device__ __forceinline__ Fp8Regions fp8_regions(const wm_fp8_experts& t, int e, bool& resident) {
@@ -42,9 +43,9 @@ __device__ __forceinline__ Fp8Regions fp8_regions(const wm_fp8_experts& t, int e
   if (slot < 0) slot = 0;  // not resident: slot 0's address, and the pair contributes nothing
   Fp8Regions r;
   r.w13 = (const uint8_t*)t.w13 + slot * t.w13_stride;
-  r.w13_scales = (const float*)((const uint8_t*)t.w13_scales + slot * t.w13_scales_stride);
+  r.w13_scales = (const uint8_t*)t.w13_scales + slot * t.w13_scales_stride;
   r.w2 = (const uint8_t*)t.w2 + slot * t.w2_stride;
-  r.w2_scales = (const float*)((const uint8_t*)t.w2_scales + slot * t.w2_scales_stride);
+  r.w2_scales = (const uint8_t*)t.w2_scales + slot * t.w2_scales_stride;
   return r;
 }
 
@@ -66,7 +67,7 @@ void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const 
                    const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared, const uint16_t* shared_gate,
                    uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s);
 
-// FP8 expert FFN (hidden and intermediate multiples of 1024 for decode, of 128 for prefill).
+// FP8 expert FFN (hidden and intermediate multiples of 128; up to 8192 for decode).
 void decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                 const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
                 uint16_t* y, bool combine, float* act, hipStream_t s);

@@ -88,6 +88,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 // oracle/formats.py e8m0_value over all 256 bytes.
 __device__ __forceinline__ float e8m0_scale_operand(uint32_t b) { return __uint_as_float(b << 23); }
 
+// E8M0 byte -> its value 2^(b - 127) as a float to multiply by: byte 0 is the denormal
+// 2^-127, 255 NaN (OCP MX), every other byte the normal float with exponent field b.
+__device__ __forceinline__ float e8m0_value(uint32_t b) {
+  return b == 0u ? __uint_as_float(0x00400000u) : (b == 255u ? __uint_as_float(0x7fc00000u) : __uint_as_float(b << 23));
+}
+
 // E2M1 magnitude table as fp32 bit patterns, index = code & 7.
 __device__ __forceinline__ float e2m1_to_f32(uint32_t code) {
   // 0, .5, 1, 1.5, 2, 3, 4, 6: exponent/mantissa built from the 3 magnitude bits.

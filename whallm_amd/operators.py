@@ -28,7 +28,8 @@ from dataclasses import dataclass, replace
 
 import torch
 
-from .ops import (FP8Experts, MXFP4Experts, combine_pairs, dequant_fp8_blocks, dequant_mxfp4, experts_fp8,
+from .ops import (FP8Experts, MXFP4Experts, combine_pairs, dequant_fp8_blocks, dequant_fp8_e8m0, dequant_mxfp4,
+                  experts_fp8,
                   experts_mxfp4, linear_bf16, mlp_bf16, moe_fp8, moe_mxfp4, route_scored, route_softmax_topk)
 
 # Whole-layer prefill groups rows by expert from this many rows (qwen4_exp.py:789).
@@ -220,7 +221,8 @@ def _generic_experts(x: torch.Tensor, indices: torch.Tensor, table, activation) 
         slot = e if slots is None else int(slots[e])
         w13, w13s, w2, w2s = (t[slot] if t.dim() == 3 else t for t in table.tensors()[:4])
         if fp8:
-            wa, wd, src = dequant_fp8_blocks(w13, w13s), dequant_fp8_blocks(w2, w2s), x[rows // K].float()
+            deq = dequant_fp8_e8m0 if table.scale_format == 1 else dequant_fp8_blocks
+            wa, wd, src = deq(w13, w13s), deq(w2, w2s), x[rows // K].float()
         else:
             wa, wd = dequant_mxfp4(w13, w13s, torch.bfloat16), dequant_mxfp4(w2, w2s, torch.bfloat16)
             src = x[rows // K]

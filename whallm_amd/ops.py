@@ -184,6 +184,19 @@ def dequant_fp8_blocks(weight: torch.Tensor, scales: torch.Tensor) -> torch.Tens
     return out
 
 
+def dequant_fp8_e8m0(weight: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """FP8 E4M3 [R, C] + E8M0 u8 [ceil(R/32), ceil(C/32)] -> fp32 (deepseek_v41/dequant.py:45-50)."""
+    device = _require_device(weight, scales)
+    weight = _contig(weight, torch.uint8, "weight")
+    scales = _contig(scales, torch.uint8, "scales")
+    R, C = weight.shape
+    if scales.shape != (-(-R // 32), -(-C // 32)):
+        raise ValueError("E8M0 scale shape does not match 32x32 block padding")
+    out = torch.empty(R, C, dtype=torch.float32, device=device)
+    _lib.call("wm_dequant_fp8_e8m0", _ptr(weight), _ptr(scales), R, C, _ptr(out), _stream(device))
+    return out
+
+
 # ----------------------------------------------------------------------------- routing
 
 def route_softmax_topk(logits: torch.Tensor, k: int, norm_topk_prob: bool = True, probabilities: bool = False):
@@ -376,11 +389,14 @@ def mlp_bf16(x: torch.Tensor, gate_w: torch.Tensor, up_w: torch.Tensor, down_w: 
 
 @dataclass(frozen=True)
 class FP8Experts:
-    """Device regions of a set of FP8-E4M3 experts with fp32 128x128 block scales
-    (the DeepSeek-V3 expert format, mimo/weights.py:17-43), addressed as base + slot * stride.
+    """Device regions of a set of FP8-E4M3 experts, addressed as base + slot * stride.
 
-    w13 uint8 [.., 2I, H] (W1 = gate rows first, then W3 = up; ``up_first`` swaps them),
-    w13_scales fp32 [.., 2I/128, H/128], w2 uint8 [.., H, I], w2_scales fp32 [.., H/128, I/128].
+    w13 uint8 [.., 2I, H] (W1 = gate rows first, then W3 = up; ``up_first`` swaps them) and
+    w2 uint8 [.., H, I], with block scales in one of two formats (``scale_format``):
+    0, fp32 128x128 blocks (the DeepSeek-V3 / MiMo checkpoints, mimo/weights.py:17-43):
+    w13_scales fp32 [.., 2I/128, H/128], w2_scales fp32 [.., H/128, I/128];
+    1, one E8M0 byte per 32x32 block (the V4.1 release, deepseek_v41/dequant.py:45-50):
+    w13_scales uint8 [.., 2I/32, H/32], w2_scales uint8 [.., H/32, I/32].
     """
     w13: torch.Tensor
     w13_scales: torch.Tensor
@@ -391,6 +407,7 @@ class FP8Experts:
     up_first: bool = False
     swiglu_limit: float = 0.0
     tiled: bool = False
+    scale_format: int = 0
 
     @property
     def hidden(self) -> int:
@@ -410,8 +427,11 @@ class FP8Experts:
         def stride(t: torch.Tensor) -> int:
             return t.stride(0) * t.element_size() if t.dim() == 3 else 0
 
+        if self.scale_format not in (0, 1):
+            raise ValueError("scale_format must be 0 (fp32 128x128 blocks) or 1 (E8M0 32x32 blocks)")
+        sdt, blk = (torch.float32, 128) if self.scale_format == 0 else (torch.uint8, 32)
         for name, t, dt in (("w13", self.w13, torch.uint8), ("w2", self.w2, torch.uint8),
-                            ("w13_scales", self.w13_scales, torch.float32), ("w2_scales", self.w2_scales, torch.float32)):
+                            ("w13_scales", self.w13_scales, sdt), ("w2_scales", self.w2_scales, sdt)):
             if t.dtype != dt:
                 raise ValueError(f"{name} must be {dt}, got {t.dtype}")
             if t.stride(-1) != 1 or t.stride(-2) != t.shape[-1]:
@@ -419,14 +439,14 @@ class FP8Experts:
         H, I = self.hidden, self.inter
         if H % 128 or I % 128:
             raise ValueError("FP8 experts need hidden and intermediate multiples of 128")
-        if self.w2.shape[-2:] != (H, I) or self.w13_scales.shape[-2:] != (2 * I // 128, H // 128) \
-                or self.w2_scales.shape[-2:] != (H // 128, I // 128):
+        if self.w2.shape[-2:] != (H, I) or self.w13_scales.shape[-2:] != (2 * I // blk, H // blk) \
+                or self.w2_scales.shape[-2:] != (H // blk, I // blk):
             raise ValueError("FP8 expert region shapes do not agree")
         return _lib.FP8ExpertsC(
             self.w13.data_ptr(), self.w13_scales.data_ptr(), self.w2.data_ptr(), self.w2_scales.data_ptr(),
             stride(self.w13), stride(self.w13_scales), stride(self.w2), stride(self.w2_scales),
             0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
-            float(self.swiglu_limit), int(self.tiled))
+            float(self.swiglu_limit), int(self.tiled), int(self.scale_format))
 
     def tensors(self):
         return (self.w13, self.w13_scales, self.w2, self.w2_scales, self.slots)

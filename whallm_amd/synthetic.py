@@ -78,37 +78,58 @@ def zipf_bias(experts: int, s: float = 1.1, rng: np.random.Generator | None = No
     return bias
 
 
+E8M0_FP8_LOW, E8M0_FP8_HIGH = 120, 122  # E8M0 block scales 2**-7 .. 2**-5
+
+
 def fp8_experts_np(rng: np.random.Generator, experts: int, hidden: int, inter: int,
-                   scale_low: float = 2.0 ** -7, scale_high: float = 2.0 ** -5) -> dict:
+                   scale_low: float = 2.0 ** -7, scale_high: float = 2.0 ** -5, scale_format: int = 0) -> dict:
     """FP8-E4M3 experts as uint8 codes of N(0, 1) clipped to +-448 (round to nearest even,
-    via torch's float8_e4m3fn) with fp32 128x128 block scales uniform in [low, high)."""
+    via torch's float8_e4m3fn) with fp32 128x128 block scales uniform in [low, high)
+    (scale_format 0), or E8M0 32x32 block scale bytes uniform in [120, 122] (scale_format 1,
+    the V4.1 release's format)."""
     def codes(*shape):
         v = np.clip(rng.standard_normal(shape).astype(np.float32), -448, 448)
         return torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
 
-    def scales(*shape):
-        return rng.uniform(scale_low, scale_high, size=shape).astype(np.float32)
+    if scale_format == 1:
+        def scales(*shape):
+            return rng.integers(E8M0_FP8_LOW, E8M0_FP8_HIGH + 1, size=shape, dtype=np.uint8)
+        blk = 32
+    else:
+        def scales(*shape):
+            return rng.uniform(scale_low, scale_high, size=shape).astype(np.float32)
+        blk = 128
 
     return {
-        "w13": codes(experts, 2 * inter, hidden), "w13_scales": scales(experts, 2 * inter // 128, hidden // 128),
-        "w2": codes(experts, hidden, inter), "w2_scales": scales(experts, hidden // 128, inter // 128),
+        "w13": codes(experts, 2 * inter, hidden), "w13_scales": scales(experts, 2 * inter // blk, hidden // blk),
+        "w2": codes(experts, hidden, inter), "w2_scales": scales(experts, hidden // blk, inter // blk),
     }
 
 
 def fp8_experts_to_device(arrays: dict, device, **kw) -> FP8Experts:
+    if arrays["w13_scales"].dtype == np.uint8:
+        kw.setdefault("scale_format", 1)
     return FP8Experts(*(torch.from_numpy(np.ascontiguousarray(arrays[n])).to(device)
                         for n in ("w13", "w13_scales", "w2", "w2_scales")), **kw)
 
 
 def fp8_experts_device(experts: int, hidden: int, inter: int, device, generator: torch.Generator,
-                       scale_low: float = 2.0 ** -7, scale_high: float = 2.0 ** -5) -> FP8Experts:
-    """FP8 experts generated on the device (bench sizes)."""
+                       scale_low: float = 2.0 ** -7, scale_high: float = 2.0 ** -5, scale_format: int = 0) -> FP8Experts:
+    """FP8 experts generated on the device (bench sizes), in either scale format."""
     def codes(*shape):
         v = torch.randn(shape, device=device, generator=generator).clamp_(-448, 448)
         return v.to(torch.float8_e4m3fn).view(torch.uint8)
 
-    def scales(*shape):
-        return torch.rand(shape, device=device, generator=generator) * (scale_high - scale_low) + scale_low
+    if scale_format == 1:
+        def scales(*shape):
+            return torch.randint(E8M0_FP8_LOW, E8M0_FP8_HIGH + 1, shape, dtype=torch.uint8, device=device,
+                                 generator=generator)
+        blk = 32
+    else:
+        def scales(*shape):
+            return torch.rand(shape, device=device, generator=generator) * (scale_high - scale_low) + scale_low
+        blk = 128
 
-    return FP8Experts(codes(experts, 2 * inter, hidden), scales(experts, 2 * inter // 128, hidden // 128),
-                      codes(experts, hidden, inter), scales(experts, hidden // 128, inter // 128))
+    return FP8Experts(codes(experts, 2 * inter, hidden), scales(experts, 2 * inter // blk, hidden // blk),
+                      codes(experts, hidden, inter), scales(experts, hidden // blk, inter // blk),
+                      scale_format=scale_format)
