@@ -604,8 +604,12 @@ struct LoaderMx {
   const uint8_t* wbase;
   const uint8_t* sbase;
   static constexpr int NQ = 32 / F::LW;                // 1 KB loads per wave and operand
-  // A scale loads per wave: a dword (4 E8M0 bytes) per weight row, 64 rows a load
-  static constexpr int SQ = F::A_SCALED ? (F::TW / 64 + F::LW - 1) / F::LW : 0;
+  // A scales: one load per wave and step, a dword (4 E8M0 bytes) per weight row, wave w
+  // taking rows RPWS w + lane for lane < RPWS. Every wave issues it (lanes past RPWS masked),
+  // so every wave has the same loads in flight when the step's ring wait counts them.
+  static constexpr int SQ = F::A_SCALED ? 1 : 0;
+  static constexpr int RPWS = F::TW / F::LW;
+  static_assert(!F::A_SCALED || RPWS <= 64, "one scale load per wave covers the tile's rows");
   uint32_t boff[NQ];
   uint32_t aoff[NQ];
   uint32_t soff[SQ > 0 ? SQ : 1];
@@ -619,11 +623,8 @@ struct LoaderMx {
 #pragma unroll
     for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
       dma16(wbase, aoff[i] + (uint32_t)ks * a_step, lds_addr(slot + (w + F::LW * i) * 1024));
-    if (h == 1)
-#pragma unroll
-      for (int q = 0; q < SQ; ++q)
-        if (64 * (w + F::LW * q) < F::TW)  // wave-uniform
-          dma4(sbase, soff[q] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 256 * (w + F::LW * q)));
+    if (SQ && h == 1 && threadIdx.x % 64 < RPWS)
+      dma4(sbase, soff[0] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 4 * RPWS * w));
   }
   // Half h of step ks's split-row loads into split-row slot `slot` (NQ instructions per step).
   __device__ __forceinline__ void issue_b(uint8_t* slot, int ks, int h) {
@@ -673,11 +674,8 @@ __device__ __forceinline__ void weight_offsets(LoaderMx<F>& ld, const uint8_t* w
       ld.a_step = 128;
     }
     if constexpr (F::A_SCALED) {  // E8M0 32 x 32 blocks, [rows / 32][k / 32] bytes in either layout
-#pragma unroll
-      for (int q = 0; q < SQ; ++q) {
-        const int r0 = 64 * (w + F::LW * q);
-        ld.soff[q] = r0 < F::TW ? (uint32_t)(row_of(r0 + lane) / 32 * (k / 32)) : 0u;
-      }
+      constexpr int RPWS = LoaderMx<F>::RPWS;
+      ld.soff[0] = lane < RPWS ? (uint32_t)(row_of(RPWS * w + lane) / 32 * (k / 32)) : 0u;
       ld.s_step = 4;
     } else {
       ld.soff[0] = 0;
@@ -686,16 +684,16 @@ __device__ __forceinline__ void weight_offsets(LoaderMx<F>& ld, const uint8_t* w
   } else if (tiled) {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::LW * i)) / 16 * 1024 + 16 * lane);
-#pragma unroll
-    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::LW * q) + lane) * 4);
+    constexpr int RPWS = LoaderMx<F>::RPWS;
+    ld.soff[0] = lane < RPWS ? (uint32_t)(row_of(RPWS * w + lane) * 4) : 0u;
     ld.a_step = (uint32_t)(rows * 64);
     ld.s_step = (uint32_t)(rows * 4);
   } else {
 #pragma unroll
     for (int i = 0; i < NQ; ++i)
       ld.aoff[i] = (uint32_t)(row_of(16 * (w + F::LW * i) + lane % 16) * (k / 2) + 16 * (lane / 16));
-#pragma unroll
-    for (int q = 0; q < SQ; ++q) ld.soff[q] = (uint32_t)(row_of(64 * (w + F::LW * q) + lane) * (k / 32));
+    constexpr int RPWS = LoaderMx<F>::RPWS;
+    ld.soff[0] = lane < RPWS ? (uint32_t)(row_of(RPWS * w + lane) * (k / 32)) : 0u;
     ld.a_step = 64;
     ld.s_step = 4;
   }

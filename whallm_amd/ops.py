@@ -147,9 +147,10 @@ def prefill_layout(experts):
     table = experts.c_struct()
     _lib.call("wm_repack_prefill_fp8" if fp8 else "wm_repack_prefill_mxfp4", ctypes.byref(table),
               *(_ptr(t) for t in out), _stream(device))
+    kw = {"scale_format": experts.scale_format} if fp8 else {}
     cls = FP8Experts if fp8 else MXFP4Experts
     return cls(*out, experts=E if lead else None, up_first=experts.up_first, swiglu_limit=experts.swiglu_limit,
-               tiled=True)
+               tiled=True, **kw)
 
 
 # ----------------------------------------------------------------------------- formats
