@@ -59,6 +59,10 @@ typedef struct wm_mxfp4_experts {
   float swiglu_limit;            /* 0: plain SwiGLU; > 0: clamped (deepseek_v41/moe.py:30-43) */
   int32_t tiled;                 /* 0: the reference's row layout; 1: prefill tile layout
                                     (wm_repack_prefill_mxfp4), grouped-GEMM path only */
+  int32_t act_terms;             /* grouped GEMM's activation terms: 0 two E4M3 terms per
+                                    32-value block (bf16-exact above 2^-13 of the block max,
+                                    fp4 x fp8 MFMA rate); 1 two E2M3 terms (~7 significant bits
+                                    of the block max, twice the MFMA rate for MXFP4 weights) */
 } wm_mxfp4_experts;
 
 /* FP8-E4M3 expert set. scale_format 0: fp32 128x128 block scales (the DeepSeek-V3 / MiMo
@@ -82,6 +86,8 @@ typedef struct wm_fp8_experts {
   int32_t tiled;                 /* 0: the reference's row layout; 1: prefill tile layout of the
                                     weight bytes (wm_repack_prefill_fp8), grouped-GEMM path only */
   int32_t scale_format;          /* 0: fp32 128x128 blocks; 1: E8M0 32x32 blocks */
+  int32_t act_terms;             /* as wm_mxfp4_experts.act_terms (fp8 x fp8 and fp8 x fp6 run at
+                                    the same MFMA rate) */
 } wm_fp8_experts;
 
 /* Message of the last failed call on this thread ("" when none). */
@@ -245,6 +251,13 @@ WM_EXPORT int wm_repack_prefill_fp8(const wm_fp8_experts* src, void* w13, void* 
  * counterpart in the reference: the format in which the grouped GEMMs read activations,
  * exposed so callers can prepare rows once and so the tests can check it byte for byte. */
 WM_EXPORT int wm_split_rows_e2m3(const void* x, int32_t rows, int32_t hidden, void* out, void* stream);
+/* x [rows, hidden] bf16 -> the grouped GEMM's bf16-exact split rows: terms [rows][hidden/128]
+ * [256 bytes] (per 128-wide step the hi terms of K 0..127 in K order, then the lo terms) and
+ * scales [rows][hidden/128] u32 (the step's 4 hi E8M0 bytes; the lo scale is hi - 4). Per
+ * 32-value block hi = e4m3(x / 2^(s-127)), s = max(e(max |x|) - 7, 5), lo = e4m3((x /
+ * 2^(s-127) - hi) * 16), round to nearest even. No counterpart in the reference (its
+ * activations stay bf16 / fp32); exposed for the bit-exact test of the split. */
+WM_EXPORT int wm_split_rows_e4m3(const void* x, int32_t rows, int32_t hidden, void* terms, void* scales, void* stream);
 
 /* ---- measurement ----------------------------------------------------------
  * When enabled, every later wm_moe_mxfp4 / wm_experts_mxfp4 / wm_moe_fp8 / wm_experts_fp8

@@ -312,6 +312,80 @@ def split_rows_e2m3(x: np.ndarray) -> np.ndarray:
     return out
 
 
+# ---- bf16-exact activation terms: two E4M3 terms per 32 values --------------------------
+
+_E4M3_MAG = None
+
+
+def e4m3_encode(v: np.ndarray) -> np.ndarray:
+    """fp32 values with |v| <= 448 -> E4M3FN bytes, rounded to nearest, ties to the even code;
+    a negative value that rounds to zero keeps its sign (0x80)."""
+    global _E4M3_MAG
+    if _E4M3_MAG is None:
+        _E4M3_MAG = e4m3_value(np.arange(127, dtype=np.uint8)).astype(np.float64)  # codes 0..126 ascend
+    v = np.asarray(v, np.float64)
+    a = np.abs(v)
+    if np.any(a > 448) or np.any(~np.isfinite(v)):
+        raise ValueError("e4m3_encode takes finite values up to 448")
+    hi = np.clip(np.searchsorted(_E4M3_MAG, a, side="left"), 0, 126)   # first code >= a
+    lo = np.clip(hi - 1, 0, 126)
+    d_lo, d_hi = a - _E4M3_MAG[lo], _E4M3_MAG[hi] - a
+    code = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, hi, np.where(lo % 2 == 0, lo, hi)))
+    code = np.where(a == _E4M3_MAG[hi], hi, code)
+    return (code | np.where(np.signbit(v), 0x80, 0)).astype(np.uint8)
+
+
+def e4m3_term_exponent(amax) -> int:
+    """E8M0 exponent of a block's hi term: e(amax) - 7 (biased), at least 5."""
+    e = int((np.float32(amax).view(np.uint32) >> 23) & 0xFF)
+    return max(e - 7, 5)
+
+
+def e4m3_terms(block: np.ndarray) -> tuple[np.ndarray, np.ndarray, int]:
+    """One 32-value block -> (hi bytes, lo bytes, s): hi = e4m3(x / 2^(s-127)) and lo =
+    e4m3((x / 2^(s-127) - value(hi)) * 16), the lo scale being 2^(s-131)."""
+    x = np.asarray(block, np.float32)
+    s = e4m3_term_exponent(np.abs(x).max())
+    h = (x * np.float32(2.0 ** (127 - s))).astype(np.float32)
+    hi = e4m3_encode(h)
+    lo = e4m3_encode(((h - e4m3_value(hi)) * np.float32(16.0)).astype(np.float32))
+    return hi, lo, s
+
+
+def split_rows_e4m3(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """fp32 rows [R, H] (H a multiple of 128) -> (terms [R, H/128, 256] bytes: per 128-wide step
+    the hi terms of K 0..127, then the lo terms; scales [R, H/128] uint32: the step's 4 hi
+    exponents, byte b for block b)."""
+    x = np.asarray(x, np.float32)
+    R, H = x.shape
+    if H % 128:
+        raise ValueError("split rows need H a multiple of 128")
+    terms = np.zeros((R, H // 128, 256), np.uint8)
+    scales = np.zeros((R, H // 128), np.uint32)
+    for r in range(R):
+        for b in range(H // 32):
+            hi, lo, sc = e4m3_terms(x[r, 32 * b:32 * b + 32])
+            st = terms[r, b // 4]
+            st[32 * (b % 4):32 * (b % 4) + 32] = hi
+            st[128 + 32 * (b % 4):128 + 32 * (b % 4) + 32] = lo
+            scales[r, b // 4] |= np.uint32(sc) << np.uint32(8 * (b % 4))
+    return terms, scales
+
+
+def split_rows_e4m3_value(terms: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """Inverse view of split_rows_e4m3: hi 2^(s-127) + lo 2^(s-131) per value, float64."""
+    t = np.asarray(terms, np.uint8)
+    R, steps = t.shape[:2]
+    sc = np.asarray(scales).astype(np.uint32)
+    out = np.zeros((R, steps * 128), np.float64)
+    for b in range(steps * 4):
+        s = ((sc[:, b // 4] >> np.uint32(8 * (b % 4))) & np.uint32(0xFF)).astype(np.float64)[:, None]
+        hi = e4m3_value(t[:, b // 4, 32 * (b % 4):32 * (b % 4) + 32]).astype(np.float64)
+        lo = e4m3_value(t[:, b // 4, 128 + 32 * (b % 4):160 + 32 * (b % 4)]).astype(np.float64)
+        out[:, 32 * b:32 * b + 32] = hi * np.exp2(s - 127) + lo * np.exp2(s - 131)
+    return out
+
+
 def split_rows_value(split: np.ndarray, H: int) -> np.ndarray:
     """Inverse view of split_rows_e2m3: hi 2^(s_hi-127) + lo 2^(s_lo-127) per value, float64."""
     s = np.asarray(split, np.uint8)

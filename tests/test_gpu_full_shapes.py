@@ -10,6 +10,8 @@ dequantizes 17 experts instead of all 257, while the rest of the 4,096 tokens ro
 (sigmoid, bias select, 8 groups / top 4). C5 checks every layer of the verify step from
 its own inputs (teacher forcing), the LM head, and acceptance.
 """
+from dataclasses import replace
+
 import numpy as np
 import pytest
 import torch
@@ -28,6 +30,7 @@ def close(got, want, what):
     mx = np.abs(got - want).max() / np.abs(want).max()
     assert rel <= 1e-2 and mx <= 2e-2, f"{what}: rel L2 {rel:.3e} max {mx:.3e}"
     print(f"{what}: rel L2 {rel:.2e} max {mx:.2e}", flush=True)
+    return rel
 
 
 def mx_expert(tab, e):
@@ -67,7 +70,11 @@ def test_c3_prefill_full_size(device):
     routed = M.routed_outputs(xs, ids, ex)
     sh = M.expert_ffn(xs, mx_expert(shared, 0))
     want = M.combine(routed, ws, sh, xs.astype(np.float64) @ gate.float().cpu().numpy().astype(np.float64))
-    close(y.float().cpu().numpy()[sample], want, "C3 sampled tokens")
+    rel = close(y.float().cpu().numpy()[sample], want, "C3 sampled tokens, E4M3 activation terms")
+    # the faster E2M3 terms (about 7 significant bits of each block's maximum) on the same call
+    y6 = wa.moe_mxfp4(x, idx, w, replace(tiled, act_terms="e2m3"), replace(tiled_shared, act_terms="e2m3"), gate)
+    rel6 = close(y6.float().cpu().numpy()[sample], want, "C3 sampled tokens, E2M3 activation terms")
+    assert rel < rel6, "the bf16-exact terms should be the closer ones"
     # per-pair outputs: complementary masks give the one-call rows bit for bit
     full = wa.experts_mxfp4(x, idx, tiled)
     mask = torch.from_numpy(rng.random((T, K)) < 0.5).to(device)
@@ -138,7 +145,10 @@ def test_c4_prefill_full_size(device):
     ex = {int(e): fp8_expert(experts, int(e)) for e in np.unique(ids)}
     routed = M.routed_outputs(xs, ids, ex, ffn=M.fp8_expert_ffn)
     want = M.combine(routed, ws, M.fp8_expert_ffn(xs, fp8_expert(shared, 0)), None)
-    close(y.float().cpu().numpy()[sample], want, "C4 sampled tokens")
+    rel = close(y.float().cpu().numpy()[sample], want, "C4 sampled tokens, E4M3 activation terms")
+    y6 = wa.moe_fp8(x, idx, w, replace(tiled, act_terms="e2m3"), replace(tiled_shared, act_terms="e2m3"), None)
+    rel6 = close(y6.float().cpu().numpy()[sample], want, "C4 sampled tokens, E2M3 activation terms")
+    assert rel < rel6, "the bf16-exact terms should be the closer ones"
 
 
 def test_c5_verify_step(device):

@@ -198,3 +198,33 @@ def test_split_rows_e2m3_bit_exact(device, H):
     got = wa.split_rows_e2m3(S.bf16_bits_to_tensor(bits, device)).cpu().numpy()
     want = F.split_rows_e2m3(F.bf16_bits_to_f32(bits))
     np.testing.assert_array_equal(got[..., :200], want[..., :200])
+
+
+@pytest.mark.parametrize("H", [128, 2048, 7168])
+def test_split_rows_e4m3_bit_exact(device, H):
+    # the bf16-exact activation terms (wm_split_rows_e4m3) against the restatement, byte for
+    # byte (terms and scale dwords), on N(0,1) rows and on rows built to reach the edges: zero
+    # blocks, blocks many binades apart, tiny negatives that round to -0 beside a large value,
+    # E4M3 ties in the hi and the lo term, block maxima at a binade's top, and rows of one sign
+    rng = np.random.default_rng(H + 1)
+    R = 24
+    x = rng.standard_normal((R, H)).astype(np.float32)
+    x[1] = 0.0
+    x[2] *= np.exp2(rng.integers(-40, 40, H // 32)).repeat(32).astype(np.float32)
+    x[3, ::32] = 50.0
+    x[3, 1::32] = -1e-5
+    x[4] = np.tile(np.float32(128.0) + np.arange(32, dtype=np.float32) * 8 + 4, H // 32)[:H]   # hi ties
+    x[5] = np.tile(np.float32(200.0) + np.arange(32, dtype=np.float32) * 0.75, H // 32)[:H]   # lo ties
+    x[6, ::32] = np.float32(255.9 * 2.0 ** 9)
+    x[7, :] = -np.abs(x[7, :])
+    bits = F.bf16_round(x)
+    terms, scales = wa.split_rows_e4m3(S.bf16_bits_to_tensor(bits, device))
+    want_t, want_s = F.split_rows_e4m3(F.bf16_bits_to_f32(bits))
+    np.testing.assert_array_equal(terms.cpu().numpy(), want_t)
+    np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), want_s)
+    # and the terms reproduce every bf16 value at or above 2^-13 of its block's maximum
+    xf = F.bf16_bits_to_f32(bits).astype(np.float64)
+    back = F.split_rows_e4m3_value(want_t, want_s)
+    blk = np.abs(xf).reshape(R, -1, 32).max(-1, keepdims=True)
+    keep = (np.abs(xf).reshape(R, -1, 32) >= blk * 2.0 ** -13).reshape(R, H)
+    np.testing.assert_array_equal(back[keep], xf[keep])

@@ -4,6 +4,8 @@ Tolerance (BASELINE correctness bar, written here): relative L2 error <= 1e-2 an
 max |error| <= 2e-2 * max |reference| (outputs are O(100-1000) at the benchmark
 distributions, so the max-abs bar is stated relative to the output scale).
 """
+from dataclasses import replace
+
 import numpy as np
 import pytest
 import torch
@@ -72,8 +74,10 @@ class Layer:
             sg = xf.astype(np.float64) @ S.bf16_bits_to_f32(self.gate_bits).astype(np.float64)
         return M.combine(routed, self.w, sh, sg)
 
-    def run(self):
-        return wa.moe_mxfp4(self.x, self.idx_d, self.w_d, self.dev, self.dev_shared, self.gate)
+    def run(self, act_terms="e4m3"):
+        dev = replace(self.dev, act_terms=act_terms)
+        sh = None if self.dev_shared is None else replace(self.dev_shared, act_terms=act_terms)
+        return wa.moe_mxfp4(self.x, self.idx_d, self.w_d, dev, sh, self.gate)
 
 
 # T*K <= 256 takes the decode (GEMV) path, larger calls the grouped-GEMM path.
@@ -88,12 +92,14 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("act_terms", ["e4m3", "e2m3"])
 @pytest.mark.parametrize("name,tokens,experts,hidden,inter,k", CASES, ids=[c[0] for c in CASES])
-def test_moe_layer_matches_oracle(device, name, tokens, experts, hidden, inter, k):
+def test_moe_layer_matches_oracle(device, name, tokens, experts, hidden, inter, k, act_terms):
+    # act_terms picks the grouped GEMM's activation terms (decode-sized calls take the GEMV)
     layer = Layer(device, 0, tokens, experts, hidden, inter, k)
-    y = layer.run()
+    y = layer.run(act_terms)
     torch.cuda.synchronize()
-    assert_close(y.float().cpu().numpy(), layer.oracle_layer(), name)
+    assert_close(y.float().cpu().numpy(), layer.oracle_layer(), f"{name} {act_terms}")
 
 
 @pytest.mark.parametrize("name,tokens,experts,hidden,inter,k", CASES, ids=[c[0] for c in CASES])

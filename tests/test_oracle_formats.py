@@ -245,3 +245,36 @@ def test_fp8_e8m0_dequant_closed_form_and_crop():
     assert out[69, 99] == F.e4m3_value(w[69, 99]) * np.float32(2.0 ** (int(s[2, 3]) - 127))
     with pytest.raises(ValueError):
         F.dequant_fp8_e8m0(w, s[:2])
+
+
+def test_e4m3_encode_matches_torch_rounding():
+    """The oracle's E4M3 encoder (nearest, ties to the even code, signed zero) against torch's
+    float8_e4m3fn conversion, over a wide sample, every representable value, every midpoint
+    between neighbours (the ties) and tiny negatives."""
+    rng = np.random.default_rng(9)
+    grid = F.e4m3_value(np.arange(127, dtype=np.uint8)).astype(np.float64)
+    mids = (grid[:-1] + grid[1:]) / 2
+    v = np.concatenate([rng.standard_normal(50000) * 60, grid, -grid, mids, -mids, -rng.random(500) * 1e-4,
+                        [0.0, -0.0, 448.0, -448.0]]).astype(np.float32)
+    got = F.e4m3_encode(v)
+    want = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(got, want)
+
+
+def test_split_rows_e4m3_is_bf16_exact():
+    """Two E4M3 terms per 32-value block reproduce every bf16 value at or above 2^-13 of the
+    block's maximum exactly (hi: the top 4 significant bits, lo: the residual times 16), over
+    rows whose blocks span many binades; the hi scale puts the block maximum in [128, 256)."""
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((6, 512)) * np.exp2(rng.integers(-30, 30, (6, 16))).repeat(32, axis=1)).astype(np.float32)
+    x[0, :32] = 0.0
+    xb = F.bf16_round_f32(x).astype(np.float64)
+    terms, scales = F.split_rows_e4m3(xb.astype(np.float32))
+    back = F.split_rows_e4m3_value(terms, scales)
+    blk = np.abs(xb).reshape(6, -1, 32).max(-1, keepdims=True)
+    keep = (np.abs(xb).reshape(6, -1, 32) >= blk * 2.0 ** -13).reshape(6, 512)
+    np.testing.assert_array_equal(back[keep], xb[keep])
+    assert np.all(np.abs(back - xb) <= blk.repeat(32, axis=-1).reshape(6, 512) * 2.0 ** -20)
+    hi = F.e4m3_value(terms[:, :, :128].reshape(6, -1, 32)).astype(np.float64)
+    top = np.abs(hi).max(-1)
+    assert np.all((top == 0) | ((top >= 128) & (top <= 256)))

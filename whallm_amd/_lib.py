@@ -19,7 +19,7 @@ class MXFP4ExpertsC(ctypes.Structure):
         ("gate_up_stride", c_int64), ("gate_up_scales_stride", c_int64),
         ("down_stride", c_int64), ("down_scales_stride", c_int64),
         ("slots", c_void_p), ("experts", c_int32), ("hidden", c_int32), ("inter", c_int32),
-        ("up_first", c_int32), ("swiglu_limit", c_float), ("tiled", c_int32),
+        ("up_first", c_int32), ("swiglu_limit", c_float), ("tiled", c_int32), ("act_terms", c_int32),
     ]
 
 
@@ -30,6 +30,7 @@ class FP8ExpertsC(ctypes.Structure):
         ("w13_stride", c_int64), ("w13_scales_stride", c_int64), ("w2_stride", c_int64), ("w2_scales_stride", c_int64),
         ("slots", c_void_p), ("experts", c_int32), ("hidden", c_int32), ("inter", c_int32),
         ("up_first", c_int32), ("swiglu_limit", c_float), ("tiled", c_int32), ("scale_format", c_int32),
+        ("act_terms", c_int32),
     ]
 
 
@@ -113,6 +114,7 @@ _SIGNATURES = {
     "wm_mtp_verify_greedy": (c_int, [_P, _P, c_int32, c_int32, _P, _P, c_size_t, _P]),
     "wm_mtp_verify_rejection": (c_int, [_P, _P, _P, c_int32, c_int32, _P, _P, _P, c_size_t, _P]),
     "wm_split_rows_e2m3": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
+    "wm_split_rows_e4m3": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "wm_set_kernel_timing": (c_int, [c_int]),
     "wm_kernel_timing_ms": (c_int, [_P]),
     "wm_moe_decode_persistent_mxfp4": (c_int, [_P, c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P, c_float,

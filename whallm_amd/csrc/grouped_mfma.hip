@@ -280,6 +280,116 @@ __global__ void __launch_bounds__(256) split6_rows_kernel(const uint16_t* __rest
 }
 
 // ---------------------------------------------------------------------------------
+// Activations as two E4M3 terms (the bf16-exact form). A 32-value block gets hi =
+// e4m3(x / 2^(s - 127)) with s = max(e(max |x|) - 7, 5), so the block maximum lands in
+// [128, 256) (E4M3's largest finite is 448), and lo = e4m3((x / 2^(s - 127) - hi) * 16)
+// under the scale 2^(s - 131), rounded to nearest even (the hardware conversion; both terms
+// stay below 448, so nothing saturates). hi + lo reproduces every bf16 x with |x| >= 2^-13
+// of its block's maximum exactly (hi keeps x's top 4 significant bits, the residual the
+// other 4, and the residual times 16 stays on E4M3's grid down to 2^-13), the precision of
+// the reference's bf16 activations (Native/QwenNative/kernels.metal:706-751 multiplies
+// fp32 activations, qwen4_exp.py:774-783 feeds bf16 into quantized_matmul). An fp8 operand
+// runs the 32x32x64 MFMA at the FP8 rate: fp4 x fp8 takes 64 cycles against fp4 x fp6's 32.
+//
+// Split rows: per row and 128-wide K step, 256 term bytes (hi for K 0..127, then lo, each in
+// K order) in one array and the step's 4 hi scale bytes as one dword in another ([rows][steps]);
+// the lo scale is the hi scale minus 4.
+constexpr int XSTEP8 = 256;
+
+// E8M0 exponent of a block's hi term: e(max) - 7, at least 5 so that the lo scale (s - 4)
+// stays a normal power of two.
+__device__ __forceinline__ int fp8_term_exponent(float amax) {
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xff);
+  return e - 7 > 5 ? e - 7 : 5;
+}
+
+// The hi and lo E4M3 terms of one 32-value block (v in K order) as 8 words each (byte i of
+// the 32 = value i), and the hi scale byte.
+__device__ __forceinline__ void fp8_terms32(const float (&v)[32], uint32_t (&hi)[8], uint32_t (&lo)[8], int& s_hi) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  s_hi = fp8_term_exponent(amax);
+  const float f = pow2_biased(254 - s_hi);  // 2^(127 - s): exact
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    float h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = v[4 * q + j] * f;
+    const uint32_t w01 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(h[0], h[1], 0, false);
+    const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(h[2], h[3], (int)w01, true);
+    l[0] = (h[0] - __builtin_amdgcn_cvt_f32_fp8((int)w, 0)) * 16.0f;
+    l[1] = (h[1] - __builtin_amdgcn_cvt_f32_fp8((int)w, 1)) * 16.0f;
+    l[2] = (h[2] - __builtin_amdgcn_cvt_f32_fp8((int)w, 2)) * 16.0f;
+    l[3] = (h[3] - __builtin_amdgcn_cvt_f32_fp8((int)w, 3)) * 16.0f;
+    const uint32_t u01 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(l[0], l[1], 0, false);
+    hi[q] = w;
+    lo[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(l[2], l[3], (int)u01, true);
+  }
+}
+
+// x [rows, H] bf16 -> E4M3 split rows: terms [rows][H/128][256 bytes], scales
+// [rows][H/128] dwords. One lane per 32-value block. With g (bf16 [H]) also gate[row] =
+// sigmoid(x[row] . g) as in split6_rows_kernel.
+__global__ void __launch_bounds__(256) split8_rows_kernel(const uint16_t* __restrict__ x, int rows, int hidden,
+                                                          uint8_t* __restrict__ x8, uint32_t* __restrict__ x8s,
+                                                          const uint16_t* __restrict__ g, float* __restrict__ gate) {
+  const int blocks = hidden / 32;
+  const int64_t job = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, block)
+  if (job >= (int64_t)rows * blocks) return;
+  const int64_t row = job / blocks;
+  const int blk = (int)(job % blocks);
+  const uint4* src = reinterpret_cast<const uint4*>(x + row * hidden + blk * 32);
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint4 u = src[q];
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[8 * q + 2 * j] = bf16_bits_to_f32(w[j] & 0xffffu);
+      v[8 * q + 2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
+    }
+  }
+  uint32_t hi[8], lo[8];
+  int s_hi;
+  fp8_terms32(v, hi, lo, s_hi);
+  uint8_t* step = x8 + (row * (hidden / 128) + blk / 4) * XSTEP8;
+  uint4* dh = reinterpret_cast<uint4*>(step + (blk % 4) * 32);
+  uint4* dl = reinterpret_cast<uint4*>(step + 128 + (blk % 4) * 32);
+  dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+  dl[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  dl[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+  // the step's four blocks are lanes 4q .. 4q + 3: the quad's first lane stores their bytes
+  const uint32_t sc = (uint32_t)s_hi;
+  const uint32_t q1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)sc, 0x55, 0xf, 0xf, false);
+  const uint32_t q2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)sc, 0xAA, 0xf, 0xf, false);
+  const uint32_t q3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)sc, 0xFF, 0xf, 0xf, false);
+  if (blk % 4 == 0) x8s[row * (hidden / 128) + blk / 4] = sc | (q1 << 8) | (q2 << 16) | (q3 << 24);
+  if (g) {
+    const uint4* gs = reinterpret_cast<const uint4*>(g + blk * 32);
+    float dot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 u = gs[q];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dot = fmaf(v[8 * q + 2 * j], bf16_bits_to_f32(w[j] & 0xffffu), dot);
+        dot = fmaf(v[8 * q + 2 * j + 1], bf16_bits_to_f32(w[j] >> 16), dot);
+      }
+    }
+    if (blocks == 64) {
+      dot = segment_sum<64>(dot);
+    } else {
+      for (int off = 1; off < blocks; off <<= 1) dot += __shfl_xor(dot, off, 64);
+    }
+    if (blk == 0) gate[row] = 1.0f / (1.0f + __expf(-dot));
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // Prefill tile layout of expert weights (one expert region; rows R, K values per row, P
 // 16-byte pieces per row and 128-wide K step: MXFP4 4, FP8 8):
 //   weights [K/128 steps][R/16 groups][P pieces][16 rows][16 bytes]: piece p of a row's step
@@ -418,24 +528,56 @@ __device__ __forceinline__ TileWeights tile_weights_s(const wm_mxfp4_experts& ro
 //   scale lane (r, g): K block g; result register i: D[8 (i / 4) + 4 g + i % 4][r].
 // WAVES: waves per workgroup (4: one per SIMD, 8: two); MI = TW / (16 WAVES) weight tiles
 // of 32 rows per wave; DA, DB: depths of the weight and split-row rings.
+// Activation term formats of the split rows (the B operand):
+//   E2M3 pairs: XS = 208 bytes per row and step, scales inside (read from LDS unswizzled);
+//   E4M3 pairs (bf16-exact): 256 term bytes per row and step plus a scale dword from its own
+//   array; in LDS the row's 16-byte pieces are XOR-swizzled by (row & 15), so the 8 rows one
+//   ds_read_b128 cycle serves fall on distinct banks at the 256-byte pitch, and the scale
+//   dwords follow the 128 rows.
+struct TermsE2M3 {
+  static constexpr bool E4 = false;
+  static constexpr int XS = XSTEP, FMT = FMT_FP6, SLOT = BM * XSTEP;
+};
+struct TermsE4M3 {
+  static constexpr bool E4 = true;
+  static constexpr int XS = XSTEP8, FMT = FMT_FP8, SLOT = BM * XSTEP8 + BM * 4;
+};
+
 // FP8: the A operand is E4M3 bytes (else E2M1 nibbles). A_SCALED: E8M0 A scales are staged
 // per weight row and step (4 bytes) and fed to the MFMA (MXFP4, and FP8 with E8M0 32 x 32
 // blocks, whose rows of one 32-row block share their bytes); BLOCK_F32: FP8 with fp32
-// 128 x 128 block scales, which cannot ride on the MFMA's E8M0 scales.
+// 128 x 128 block scales, which cannot ride on the MFMA's E8M0 scales. Terms: the
+// activation terms; the E4M3 variants hold two slots per ring (the deeper rings of the E2M3
+// variants do not fit 160 KB beside 256-byte split rows).
 struct Mx4 {
   static constexpr bool FP8 = false, A_SCALED = true, BLOCK_F32 = false;
   static constexpr int TW = 512, PIECES = 4, A_FMT = FMT_FP4, DA = 2, DB = 3, WAVES = 8, LW = 8;
   static constexpr int MI = TW / (16 * WAVES);
+  using Terms = TermsE2M3;
+};
+struct Mx4x : Mx4 {
+  static constexpr int DA = 2, DB = 2;
+  using Terms = TermsE4M3;
 };
 struct Mx8 {
   static constexpr bool FP8 = true, A_SCALED = false, BLOCK_F32 = true;
   static constexpr int TW = 256, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2, WAVES = 8, LW = 8;
   static constexpr int MI = TW / (16 * WAVES);
+  using Terms = TermsE2M3;
+};
+struct Mx8x : Mx8 {
+  static constexpr int DA = 2, DB = 2;
+  using Terms = TermsE4M3;
 };
 struct Mx8e {
   static constexpr bool FP8 = true, A_SCALED = true, BLOCK_F32 = false;
   static constexpr int TW = 256, PIECES = 8, A_FMT = FMT_FP8, DA = 3, DB = 2, WAVES = 8, LW = 8;
   static constexpr int MI = TW / (16 * WAVES);
+  using Terms = TermsE2M3;
+};
+struct Mx8ex : Mx8e {
+  static constexpr int DA = 2, DB = 2;
+  using Terms = TermsE4M3;
 };
 constexpr int NI4 = 2;      // 32-row row tiles per wave
 
@@ -448,7 +590,7 @@ template <typename F, int DA, int DB>
 struct RingMx {
   static constexpr int A_BYTES = F::TW * F::PIECES * 16;
   static constexpr int A_SLOT = A_BYTES + (F::A_SCALED ? F::TW * 4 : 0);
-  static constexpr int B_SLOT = BM * XSTEP;
+  static constexpr int B_SLOT = F::Terms::SLOT;
   static constexpr int BYTES = DA * A_SLOT + DB * B_SLOT;
   static_assert(BYTES <= 160 * 1024, "LDS");
 };
@@ -456,12 +598,22 @@ struct RingMx {
 // Per-lane LDS read offsets. Weight tile mi of the wave is rows wave_row0 + mrow(mi) + r
 // (multiples of 32 plus the lane's row); row tile ni is rows 64 wm + 32 ni + r. Half h of
 // the step is K [64h, 64h + 64); the lane's K block in it is 2h + g.
+// Split-row LDS offsets of tile row `row`: piece p (16 bytes) of an E4M3 row is stored at
+// piece p ^ (row & 15); its scale dword is written by the loader at position
+// 16 w + 4 i + d for row 4 (w + 8 i) + d (the wave that loads the row's terms).
+__device__ __forceinline__ uint32_t e4_piece(int row, int p) { return (uint32_t)(row * XSTEP8 + 16 * (p ^ (row & 15))); }
+__device__ __forceinline__ uint32_t e4_scale(int row) {
+  return (uint32_t)(BM * XSTEP8 + 4 * (16 * ((row / 4) % 8) + 4 * (row / 32) + row % 4));
+}
+
 template <typename F>
 struct LaneMx {
   uint32_t a;        // + 16 PIECES mrow(mi) + (fp4: 512, fp8: 1024) h; fp8 second piece + 512
   uint32_t as;       // + 4 mrow(mi)
-  uint32_t b[2][3];  // [h][piece of the lane's 48 bytes] + 32 XSTEP ni
-  uint32_t bs;       // the row's scale bytes (192..199 of the step) + 32 XSTEP ni
+  uint32_t b[2][4];  // [h][piece]: E2M3 the 3 pieces of the lane's 48 bytes (+ 32 XSTEP ni);
+                     // E4M3 hi K [64h + 16g, +16), hi K [64h + 32 + 16g, +16), then lo (+ 32 XSTEP8 ni)
+  uint32_t bs[2];    // the row's scale bytes: E2M3 192..199 of the step (+ 32 XSTEP ni); E4M3 the
+                     // scale dword of row tile ni
   uint32_t shift;    // 8 g
 };
 
@@ -472,11 +624,26 @@ __device__ __forceinline__ LaneMx<F> lane_mx(int wave_row0, int wm) {
   o.a = (uint32_t)((wave_row0 / 16 + r / 16) * (F::PIECES * 256) + 256 * g + 16 * (r % 16));
   o.as = (uint32_t)(4 * (wave_row0 + r));
   const int row = 64 * wm + r;
+  if constexpr (F::Terms::E4) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h) {
+      o.b[h][0] = e4_piece(row, 4 * h + g);
+      o.b[h][1] = e4_piece(row, 4 * h + 2 + g);
+      o.b[h][2] = e4_piece(row, 8 + 4 * h + g);
+      o.b[h][3] = e4_piece(row, 8 + 4 * h + 2 + g);
+    }
 #pragma unroll
-    for (int e = 0; e < 3; ++e) o.b[h][e] = (uint32_t)(row * XSTEP + 16 * (6 * h + 3 * g + e));
-  o.bs = (uint32_t)(row * XSTEP + 192);
+    for (int ni = 0; ni < 2; ++ni) o.bs[ni] = e4_scale(row + 32 * ni);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int e = 0; e < 3; ++e) o.b[h][e] = (uint32_t)(row * XSTEP + 16 * (6 * h + 3 * g + e));
+      o.b[h][3] = 0;
+    }
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) o.bs[ni] = (uint32_t)((row + 32 * ni) * XSTEP + 192);
+  }
   o.shift = (uint32_t)(8 * g);
   return o;
 }
@@ -502,7 +669,14 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
     for (int mi = 0; mi < MI; ++mi) sa[mi] = *reinterpret_cast<const uint32_t*>(sta + A_BYTES + lo.as + 4 * mrow(mi));
   }
 #pragma unroll
-  for (int ni = 0; ni < NI4; ++ni) sb[ni] = *reinterpret_cast<const uint2*>(stb + lo.bs + 32 * XSTEP * ni);
+  for (int ni = 0; ni < NI4; ++ni) {
+    if constexpr (F::Terms::E4) {
+      sb[ni].x = *reinterpret_cast<const uint32_t*>(stb + lo.bs[ni]);
+      sb[ni].y = sb[ni].x - 0x04040404u;  // lo scales: hi - 4 (every hi scale byte is >= 5)
+    } else {
+      sb[ni] = *reinterpret_cast<const uint2*>(stb + lo.bs[ni]);
+    }
+  }
   v16f blk[F::BLOCK_F32 ? MI : 1][NI4];
   // FP8 block scales (scalar loads) issued before the MFMAs, so their memory round trip
   // overlaps the step instead of stalling the scale-and-add at its end
@@ -535,47 +709,53 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
         a[mi] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
       }
     }
-    uint4 bq[NI4][3];
+    constexpr int NP = F::Terms::E4 ? 4 : 3;               // 16-byte B pieces per row tile and half
+    constexpr uint32_t TSTEP = 32 * F::Terms::XS;           // LDS bytes between the two row tiles
+    uint4 bq[NI4][NP];
     if constexpr (AHEAD) {
 #pragma unroll
       for (int ni = 0; ni < NI4; ++ni)
 #pragma unroll
-        for (int e = 0; e < 3; ++e) bq[ni][e] = *reinterpret_cast<const uint4*>(stb + lo.b[h][e] + 32 * XSTEP * ni);
+        for (int e = 0; e < NP; ++e) bq[ni][e] = *reinterpret_cast<const uint4*>(stb + lo.b[h][e] + TSTEP * ni);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int ni = 0; ni < NI4; ++ni) {
-      uint4 b0, b1, b2;
-      if constexpr (AHEAD) {
-        b0 = bq[ni][0];
-        b1 = bq[ni][1];
-        b2 = bq[ni][2];
-      } else {
-        b0 = *reinterpret_cast<const uint4*>(stb + lo.b[h][0] + 32 * XSTEP * ni);
-        b1 = *reinterpret_cast<const uint4*>(stb + lo.b[h][1] + 32 * XSTEP * ni);
-        b2 = *reinterpret_cast<const uint4*>(stb + lo.b[h][2] + 32 * XSTEP * ni);
+      uint4 b[NP];
+#pragma unroll
+      for (int e = 0; e < NP; ++e) {
+        if constexpr (AHEAD)
+          b[e] = bq[ni][e];
+        else
+          b[e] = *reinterpret_cast<const uint4*>(stb + lo.b[h][e] + TSTEP * ni);
       }
-      const v8i bh = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, 0, 0};
-      const v8i bl = {(int)b1.z, (int)b1.w, (int)b2.x, (int)b2.y, (int)b2.z, (int)b2.w, 0, 0};
+      v8i bh, bl;
+      if constexpr (F::Terms::E4) {
+        bh = v8i{(int)b[0].x, (int)b[0].y, (int)b[0].z, (int)b[0].w, (int)b[1].x, (int)b[1].y, (int)b[1].z, (int)b[1].w};
+        bl = v8i{(int)b[2].x, (int)b[2].y, (int)b[2].z, (int)b[2].w, (int)b[3].x, (int)b[3].y, (int)b[3].z, (int)b[3].w};
+      } else {
+        bh = v8i{(int)b[0].x, (int)b[0].y, (int)b[0].z, (int)b[0].w, (int)b[1].x, (int)b[1].y, 0, 0};
+        bl = v8i{(int)b[1].z, (int)b[1].w, (int)b[2].x, (int)b[2].y, (int)b[2].z, (int)b[2].w, 0, 0};
+      }
       const int sbh = (int)(sb[ni].x >> sh), sbl = (int)(sb[ni].y >> sh);
       if constexpr (F::BLOCK_F32) {
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
-          blk[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, blk[mi][ni], FMT_FP8, FMT_FP6, 0,
-                                                                        127, 0, sbh);
+          blk[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, blk[mi][ni], FMT_FP8, F::Terms::FMT,
+                                                                        0, 127, 0, sbh);
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
-          blk[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, blk[mi][ni], FMT_FP8, FMT_FP6, 0,
-                                                                        127, 0, sbl);
+          blk[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, blk[mi][ni], FMT_FP8, F::Terms::FMT,
+                                                                        0, 127, 0, sbl);
       } else {
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
-          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, acc[mi][ni], F::A_FMT, FMT_FP6, 0,
-                                                                        (int)(sa[mi] >> sh), 0, sbh);
+          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bh, acc[mi][ni], F::A_FMT,
+                                                                        F::Terms::FMT, 0, (int)(sa[mi] >> sh), 0, sbh);
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
-          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, acc[mi][ni], F::A_FMT, FMT_FP6, 0,
-                                                                        (int)(sa[mi] >> sh), 0, sbl);
+          acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[mi], bl, acc[mi][ni], F::A_FMT,
+                                                                        F::Terms::FMT, 0, (int)(sa[mi] >> sh), 0, sbl);
       }
       __builtin_amdgcn_sched_barrier(0);
       between(2 * h + ni);
@@ -601,9 +781,13 @@ __device__ __forceinline__ void step_mx(const uint8_t* sta, const uint8_t* stb, 
 template <typename F>
 struct LoaderMx {
   const uint8_t* b;
+  const uint8_t* bsbase;  // E4M3 terms: the split rows' scale dwords
   const uint8_t* wbase;
   const uint8_t* sbase;
   static constexpr int NQ = 32 / F::LW;                // 1 KB loads per wave and operand
+  // E4M3 terms: one scale load per wave and step (lanes 0..15, the scale dwords of the
+  // wave's 16 term rows), counted like the A scales
+  static constexpr int SQB = F::Terms::E4 ? 1 : 0;
   // A scales: one load per wave and step, a dword (4 E8M0 bytes) per weight row, wave w
   // taking rows RPWS w + lane for lane < RPWS. Every wave issues it (lanes past RPWS masked),
   // so every wave has the same loads in flight when the step's ring wait counts them.
@@ -611,6 +795,7 @@ struct LoaderMx {
   static constexpr int RPWS = F::TW / F::LW;
   static_assert(!F::A_SCALED || RPWS <= 64, "one scale load per wave covers the tile's rows");
   uint32_t boff[NQ];
+  uint32_t bsoff;
   uint32_t aoff[NQ];
   uint32_t soff[SQ > 0 ? SQ : 1];
   uint32_t a_step, s_step;
@@ -626,25 +811,53 @@ struct LoaderMx {
     if (SQ && h == 1 && threadIdx.x % 64 < RPWS)
       dma4(sbase, soff[0] + (uint32_t)ks * s_step, lds_addr(slot + F::TW * F::PIECES * 16 + 4 * RPWS * w));
   }
-  // Half h of step ks's split-row loads into split-row slot `slot` (NQ instructions per step).
+  // Half h of step ks's split-row loads into split-row slot `slot` (NQ + SQB instructions
+  // per step): E2M3 rows 4 to a load (52 lanes x 16 bytes), E4M3 rows 4 to a load (64 lanes)
+  // and with h = 1 the scale dwords of the wave's rows.
   __device__ __forceinline__ void issue_b(uint8_t* slot, int ks, int h) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     if (F::LW < F::WAVES && w >= F::LW) return;
+    if constexpr (F::Terms::E4) {
 #pragma unroll
-    for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
-      if (threadIdx.x % 64 < 52) dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(slot + (w + F::LW * i) * 832));
+      for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
+        dma16(b, boff[i] + (uint32_t)ks * XSTEP8, lds_addr(slot + (w + F::LW * i) * 1024));
+      if (h == 1 && threadIdx.x % 64 < 16) dma4(bsbase, bsoff + (uint32_t)ks * 4, lds_addr(slot + BM * XSTEP8 + 64 * w));
+    } else {
+#pragma unroll
+      for (int i = h * NQ / 2; i < (h + 1) * NQ / 2; ++i)
+        if (threadIdx.x % 64 < 52) dma16(b, boff[i] + (uint32_t)ks * XSTEP, lds_addr(slot + (w + F::LW * i) * 832));
+    }
   }
 };
 
-// The split-row part of a loader: row_off(i, r) is the byte offset of tile row r's split row.
-template <typename F, typename RowOff>
-__device__ __forceinline__ void split_row_offsets(LoaderMx<F>& ld, RowOff row_off) {
-  const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int d = lane < 52 ? lane / 13 : 3, piece = lane < 52 ? lane % 13 : 0;
+// The split-row part of a loader: row_index(r) is the split row (a token, or a permuted
+// row) of tile row r, called with wave-uniform r only (it may use scalar loads); row_bytes
+// and srow_bytes are a split row's bytes in the term and (E4M3) scale arrays. A wave loads
+// tile rows 4 (w + 8 i) + d, d = 0..3: E2M3 lanes 13 d + piece, E4M3 lanes 16 d + piece with
+// the piece swizzled by (row & 15), and E4M3 scale lane 4 i + d.
+template <typename F, typename RowIndex>
+__device__ __forceinline__ void split_row_offsets(LoaderMx<F>& ld, RowIndex row_index, uint32_t row_bytes,
+                                                  uint32_t srow_bytes) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  ld.bsoff = 0;
 #pragma unroll
   for (int i = 0; i < LoaderMx<F>::NQ; ++i) {
-    const int r = 4 * (w + F::LW * i) + d;
-    ld.boff[i] = row_off(i, r) + 16u * (uint32_t)piece;
+    const int q0 = 4 * (w + F::LW * i);
+    int idx[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) idx[d] = row_index(q0 + d);
+    if constexpr (F::Terms::E4) {
+      const int d = lane / 16, piece = (lane % 16) ^ ((q0 + d) & 15);
+      const int mine = d == 0 ? idx[0] : d == 1 ? idx[1] : d == 2 ? idx[2] : idx[3];
+      ld.boff[i] = (uint32_t)mine * row_bytes + 16u * (uint32_t)piece;
+      const int sd = lane % 4;
+      const int srow = sd == 0 ? idx[0] : sd == 1 ? idx[1] : sd == 2 ? idx[2] : idx[3];
+      if (lane / 4 == i) ld.bsoff = (uint32_t)srow * srow_bytes;
+    } else {
+      const int d = lane < 52 ? lane / 13 : 3, piece = lane < 52 ? lane % 13 : 0;
+      const int mine = d == 0 ? idx[0] : d == 1 ? idx[1] : d == 2 ? idx[2] : idx[3];
+      ld.boff[i] = (uint32_t)mine * row_bytes + 16u * (uint32_t)piece;
+    }
   }
 }
 
@@ -764,7 +977,7 @@ __device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps,
   constexpr bool A_DEEP = DA > DB;
   constexpr int D = A_DEEP ? DA : DB, DS = A_DEEP ? DB : DA;
   // deeper ring's load instructions per wave and step
-  constexpr int N_DEEP = LoaderMx<F>::NQ + (A_DEEP ? LoaderMx<F>::SQ : 0);
+  constexpr int N_DEEP = LoaderMx<F>::NQ + (A_DEEP ? LoaderMx<F>::SQ : LoaderMx<F>::SQB);
   if (tr.count == 0) return;
   const int la = steps >= D ? D - 1 : 1;  // deeper ring's lookahead
   auto wslot = [&](int i) { return lds + i * R::A_SLOT; };
@@ -857,19 +1070,23 @@ __device__ __forceinline__ int table_tiled(const wm_fp8_experts& t) { return t.t
 // gate_up: act rows of a tile's TG = TW / 2 intermediate columns; weight tile rows [0, TG)
 // are the gate rows nt * TG + j, [TG, TW) the matching up rows; wave wn owns gate rows
 // 32 (MI / 2) wn + [0, 32 MI / 2) (mi < MI / 2) and the same up rows (mi >= MI / 2).
+// x6 / a6: the split rows' terms (and, E4M3, x6s / a6s their scale dwords).
 template <typename F, int DA, int DB, typename Table>
 __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel(const uint8_t* __restrict__ x6,
+                                                                 const uint8_t* __restrict__ x6s,
                                                                  const int32_t* __restrict__ row_token, Lists L,
-                                                                 Table routed, Table shared, uint8_t* __restrict__ a6) {
+                                                                 Table routed, Table shared, uint8_t* __restrict__ a6,
+                                                                 uint32_t* __restrict__ a6s) {
   constexpr int TG = F::TW / 2, MI = F::MI, HM = MI / 2;
+  constexpr int XS = F::Terms::XS;
   const int H = routed.hidden, I = routed.inter;
   const int n_tiles = (I + TG - 1) / TG;
   const TileRange tr = tile_range(active_row_tiles(L) * n_tiles);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int wm = wave & 1, wn = wave >> 1;
   const LaneMx<F> lo = lane_mx<F>(32 * HM * wn, wm);
-  const uint32_t x_row = (uint32_t)(H / 128 * XSTEP);
-  const int64_t a_row = (int64_t)(I / 128) * XSTEP;
+  const uint32_t x_row = (uint32_t)(H / 128 * XS);
+  const int64_t a_row = (int64_t)(I / 128) * XS;
   using Tile = TileMx<F>;
 
   auto setup = [&](int j, Tile& t) {
@@ -895,18 +1112,11 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
       t.s1 = uniform_ptr(reinterpret_cast<const float*>(tw.w13s) + (int64_t)(up0 / 128) * (H / 128));
     }
     t.ld.b = uniform_u8(x6);
-    // tokens of this lane's split rows 4q + 0..3 (q = w + 8i), through scalar loads
-    split_row_offsets<F>(t.ld, [&](int i, int r) {
-      const int q0 = 4 * (__builtin_amdgcn_readfirstlane(threadIdx.x / 64) + F::LW * i);
-      int tok = 0;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int pr = begin + q0 + d < end ? begin + q0 + d : begin;
-        const int td = scalar_i32(row_token, pr);
-        tok = r == q0 + d ? td : tok;
-      }
-      return (uint32_t)tok * x_row;
-    });
+    if constexpr (F::Terms::E4) t.ld.bsbase = uniform_u8(x6s);
+    // the tokens of the tile's split rows, through scalar loads
+    split_row_offsets<F>(
+        t.ld, [&](int r) { return scalar_i32(row_token, begin + r < end ? begin + r : begin); }, x_row,
+        (uint32_t)(H / 128 * 4));
     return true;
   };
 
@@ -914,7 +1124,7 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
   zero_acc<F>(acc);
   auto mrow = [](int mi) { return (mi < HM ? 0 : TG) + 32 * (mi % HM); };
   auto mfma = [&](const Tile& t, const uint8_t* wa, const uint8_t* rb, int k, auto load_part) {
-    step_mx<F, !F::FP8>(wa, rb, lo, acc, mrow, [&](int mi) { return mi < HM ? t.s0[k] : t.s1[k]; }, load_part);
+    step_mx<F, !F::FP8 && !F::Terms::E4>(wa, rb, lo, acc, mrow, [&](int mi) { return mi < HM ? t.s0[k] : t.s1[k]; }, load_part);
   };
 
   // Epilogue: lane (r, half) holds act rows 8 j + 4 half + q (j, q = 0..3; register 4 j + q)
@@ -924,9 +1134,11 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
   // two terms and writes them with the scales into the consumed stage as the tile's act
   // rows (TG / 128 steps of 208 bytes), which all threads then copy out row by row.
   auto epilogue = [&](const Tile& t, uint8_t* wa, uint8_t* rb) {
-    constexpr int STG = TG / 128 * XSTEP;  // staged bytes per row: rows 0..63 in the split-row
-    stage_barrier();                       // slot (64 STG = its size for MXFP4), 64..127 in the weight slot
+    constexpr int STG = TG / 128 * XS;  // staged bytes per row: rows 0..63 in the split-row slot
+    stage_barrier();                    // (64 STG = its size for MXFP4), 64..127 in the weight slot
     auto srow = [&](int lr) { return lr < 64 ? rb + lr * STG : wa + (lr - 64) * STG; };
+    // E4M3: the row's scale dwords (TG / 128 of them) after the 64 rows' terms of its slot
+    auto sscale = [&](int lr) { return (lr < 64 ? rb : wa) + 64 * STG + (lr % 64) * (TG / 128) * 4; };
     if (32 * HM * wn < t.valid) {
       const int r = lane % 32, half = lane / 32;
       auto act = [&](int b, int ni, int i) {
@@ -952,28 +1164,49 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
           full[8 * (i / 4) + i % 4] = __uint_as_float(pr[0]);
           full[8 * (i / 4) + 4 + i % 4] = __uint_as_float(pr[1]);
         }
-        v6u_t hi, lo6;
-        int s_hi, s_lo;
-        fp6_terms32(full, hi, lo6, s_hi, s_lo);
         const int lr = HM >= 2 ? 64 * wm + 32 * ni + r : 64 * wm + 32 * half + r;
         const int kb = HM >= 2 ? HM * wn + 2 * p + half : wn;  // block of the tile: step kb / 4, block kb % 4
-        uint8_t* step = srow(lr) + (kb / 4) * XSTEP;
-        uint4* dst = reinterpret_cast<uint4*>(step + (kb % 4) * 48);
-        dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        dst[1] = make_uint4(hi[4], hi[5], lo6[0], lo6[1]);
-        dst[2] = make_uint4(lo6[2], lo6[3], lo6[4], lo6[5]);
-        step[192 + kb % 4] = (uint8_t)s_hi;
-        step[196 + kb % 4] = (uint8_t)s_lo;
+        uint8_t* step = srow(lr) + (kb / 4) * XS;
+        if constexpr (F::Terms::E4) {
+          uint32_t hi[8], lo8[8];
+          int s_hi;
+          fp8_terms32(full, hi, lo8, s_hi);
+          uint4* dh = reinterpret_cast<uint4*>(step + (kb % 4) * 32);
+          uint4* dl = reinterpret_cast<uint4*>(step + 128 + (kb % 4) * 32);
+          dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+          dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+          dl[0] = make_uint4(lo8[0], lo8[1], lo8[2], lo8[3]);
+          dl[1] = make_uint4(lo8[4], lo8[5], lo8[6], lo8[7]);
+          sscale(lr)[kb] = (uint8_t)s_hi;  // byte kb % 4 of the row's dword kb / 4
+        } else {
+          v6u_t hi, lo6;
+          int s_hi, s_lo;
+          fp6_terms32(full, hi, lo6, s_hi, s_lo);
+          uint4* dst = reinterpret_cast<uint4*>(step + (kb % 4) * 48);
+          dst[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+          dst[1] = make_uint4(hi[4], hi[5], lo6[0], lo6[1]);
+          dst[2] = make_uint4(lo6[2], lo6[3], lo6[4], lo6[5]);
+          step[192 + kb % 4] = (uint8_t)s_hi;
+          step[196 + kb % 4] = (uint8_t)s_lo;
+        }
       }
     }
     stage_barrier();
-    const int chunks = t.valid / 128 * (XSTEP / 16);  // 16-byte pieces of a row's act steps
+    const int chunks = t.valid / 128 * (XS / 16);  // 16-byte pieces of a row's act steps
     const int n = (t.end - t.begin) * chunks;
     for (int idx = threadIdx.x; idx < n; idx += 64 * F::WAVES) {
       const int lr = idx / chunks, c = idx - lr * chunks;
       const uint4 v4 = *reinterpret_cast<const uint4*>(srow(lr) + 16 * c);
-      *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(t.nt * TG / 128) * XSTEP + 16 * c) =
-          v4;
+      *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(t.nt * TG / 128) * XS + 16 * c) = v4;
+    }
+    if constexpr (F::Terms::E4) {
+      const int steps = t.valid / 128;
+      const int ns = (t.end - t.begin) * steps;
+      for (int idx = threadIdx.x; idx < ns; idx += 64 * F::WAVES) {
+        const int lr = idx / steps, j = idx - lr * steps;
+        a6s[(int64_t)(t.begin + lr) * (I / 128) + t.nt * TG / 128 + j] =
+            *reinterpret_cast<const uint32_t*>(sscale(lr) + 4 * j);
+      }
     }
     zero_acc<F>(acc);
   };
@@ -985,7 +1218,8 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
 // down: out[row, n] = act[row] . W2[n], bf16, permuted rows (the combine applies the routing
 // weights); tile = 128 rows x TW output columns, wave wn owns columns 32 MI wn + [0, 32 MI).
 template <typename F, int DA, int DB, typename Table>
-__global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) down_mx_kernel(const uint8_t* __restrict__ a6, Lists L, Table routed,
+__global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) down_mx_kernel(const uint8_t* __restrict__ a6,
+                                                              const uint8_t* __restrict__ a6s, Lists L, Table routed,
                                                               Table shared, uint16_t* __restrict__ out) {
   constexpr int MI = F::MI;
   const int H = routed.hidden, I = routed.inter;
@@ -994,7 +1228,7 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) down_mx_kernel(co
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int wm = wave & 1, wn = wave >> 1;
   const LaneMx<F> lo = lane_mx<F>(32 * MI * wn, wm);
-  const uint32_t a_row = (uint32_t)(I / 128 * XSTEP);
+  const uint32_t a_row = (uint32_t)(I / 128 * F::Terms::XS);
   using Tile = TileMx<F>;
 
   auto setup = [&](int j, Tile& t) {
@@ -1013,7 +1247,9 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) down_mx_kernel(co
       t.s0 = t.s1 = uniform_ptr(reinterpret_cast<const float*>(tw.w2s) +
                                 (int64_t)(col_row(32 * MI * wn) / 128) * (I / 128));
     t.ld.b = uniform_u8(a6);
-    split_row_offsets<F>(t.ld, [&](int, int r) { return (uint32_t)(begin + r < end ? begin + r : begin) * a_row; });
+    if constexpr (F::Terms::E4) t.ld.bsbase = uniform_u8(a6s);
+    split_row_offsets<F>(t.ld, [&](int r) { return begin + r < end ? begin + r : begin; }, a_row,
+                         (uint32_t)(I / 128 * 4));
     return true;
   };
 
@@ -1225,10 +1461,12 @@ static int compute_units() {
 }
 
 struct Layout {
-  size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, row_token, x6, a6, rows, total;
+  size_t permute_ws, order, inverse, offsets, tiles, tile_count, gate, row_token, x6, x6s, a6, a6s, rows, total;
 };
 
-// Split rows take XSTEP bytes per 128-wide K step (E2M3 terms with their scales inside).
+// Split rows take the larger of the two term formats' bytes per 128-wide K step (E4M3: 256
+// term bytes plus a scale dword; E2M3: 208 bytes, scales inside), so one workspace size
+// serves either.
 static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool has_shared) {
   const int64_t pairs = (int64_t)tokens * k;
   const int64_t rows = pairs + (has_shared ? tokens : 0);
@@ -1243,8 +1481,10 @@ static Layout layout(int tokens, int k, int experts, int hidden, int inter, bool
   p.tile_count = at; at += align256(sizeof(int32_t));
   p.gate = at;       at += align256(sizeof(float) * (size_t)(tokens > 0 ? tokens : 1));
   p.row_token = at;  at += align256(sizeof(int32_t) * (size_t)(rows > 0 ? rows : 1));
-  p.x6 = at;         at += align256((size_t)tokens * (hidden / 128) * XSTEP);
-  p.a6 = at;         at += align256((size_t)rows * (inter / 128) * XSTEP);
+  p.x6 = at;         at += align256((size_t)tokens * (hidden / 128) * XSTEP8);
+  p.x6s = at;        at += align256((size_t)tokens * (hidden / 128) * 4);
+  p.a6 = at;         at += align256((size_t)rows * (inter / 128) * XSTEP8);
+  p.a6s = at;        at += align256((size_t)rows * (inter / 128) * 4);
   p.rows = at;       at += align256(sizeof(uint16_t) * (size_t)rows * hidden);
   p.total = at;
   return p;
@@ -1275,7 +1515,8 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
                 !f32(t->w13_scales, t->w13_scales_stride) || !f32(t->w2_scales, t->w2_scales_stride)))
         fail("prefill: FP8 weight regions and strides must be 16-byte aligned, scales 4-byte");
   }
-  if ((int64_t)rows * (I / 128) * XSTEP >= ((int64_t)1 << 32) || (int64_t)tokens * (H / 128) * XSTEP >= ((int64_t)1 << 32))
+  constexpr int XS = F::Terms::XS;
+  if ((int64_t)rows * (I / 128) * XS >= ((int64_t)1 << 32) || (int64_t)tokens * (H / 128) * XS >= ((int64_t)1 << 32))
     fail("prefill: split operands of 4 GiB or more (split the call into smaller token batches)");
   uint8_t* base = (uint8_t*)ws;
   Lists L;
@@ -1308,9 +1549,14 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
                        k, (int)rows, row_token);
     check_launch("row_tokens");
   }
+  uint8_t* x6s = base + p.x6s;
   const int64_t split_jobs = (int64_t)tokens * (H / 32);
-  hipLaunchKernelGGL(split6_rows_kernel, dim3((unsigned)((split_jobs + 255) / 256)), dim3(256), 0, s, x, tokens, H,
-                     x6, fused_gate ? shared_gate : nullptr, (float*)L.shared_gate);
+  if constexpr (F::Terms::E4)
+    hipLaunchKernelGGL(split8_rows_kernel, dim3((unsigned)((split_jobs + 255) / 256)), dim3(256), 0, s, x, tokens, H,
+                       x6, (uint32_t*)x6s, fused_gate ? shared_gate : nullptr, (float*)L.shared_gate);
+  else
+    hipLaunchKernelGGL(split6_rows_kernel, dim3((unsigned)((split_jobs + 255) / 256)), dim3(256), 0, s, x, tokens, H,
+                       x6, fused_gate ? shared_gate : nullptr, (float*)L.shared_gate);
   check_launch("split_rows");
   const Table sh = shared ? *shared : routed;
   const int64_t max_row_tiles = (pairs + BM - 1) / BM + routed.experts + (has_shared ? (tokens + BM - 1) / BM : 0);
@@ -1323,16 +1569,17 @@ static void run(const uint16_t* x, int tokens, const int32_t* indices, const flo
     return dim3((unsigned)(per_xcd * XCDS));
   };
   uint8_t* a6 = base + p.a6;
+  uint32_t* a6s = (uint32_t*)(base + p.a6s);
   uint16_t* out_rows = (uint16_t*)(base + p.rows);
   TimingEvents* te = g_timing.load() ? timing_events() : nullptr;
   if (te) check_hip(hipEventRecord(te->ev[0], s), "hipEventRecord");
   hipLaunchKernelGGL((gate_up_mx_kernel<F, F::DA, F::DB, Table>), grid_for((I + F::TW / 2 - 1) / (F::TW / 2)),
-                     dim3(64 * F::WAVES), 0, s, x6, row_token, L, routed, sh, a6);
+                     dim3(64 * F::WAVES), 0, s, x6, x6s, row_token, L, routed, sh, a6, a6s);
   check_launch("gate_up");
   if (te) check_hip(hipEventRecord(te->ev[1], s), "hipEventRecord");
   // unweighted rows: the combine applies the routing weights and the shared gate
   hipLaunchKernelGGL((down_mx_kernel<F, F::DA, F::DB, Table>), grid_for((H + F::TW - 1) / F::TW), dim3(64 * F::WAVES), 0,
-                     s, a6, L, routed, sh, out_rows);
+                     s, a6, (const uint8_t*)a6s, L, routed, sh, out_rows);
   check_launch("down");
   if (te) check_hip(hipEventRecord(te->ev[2], s), "hipEventRecord");
   const int32_t* shared_slots = has_shared ? shared->slots : nullptr;
@@ -1352,10 +1599,14 @@ size_t prefill_workspace_size(int tokens, int k, const wm_mxfp4_experts& e, bool
   return mf::layout(tokens, k, e.experts, e.hidden, e.inter, has_shared).total;
 }
 
+// act_terms 0: the bf16-exact E4M3 activation terms; 1: the faster E2M3 terms.
 void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                    const wm_mxfp4_experts& routed, const wm_mxfp4_experts* shared, const uint16_t* shared_gate,
                    uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s) {
-  mf::run<mf::Mx4>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  if (routed.act_terms == 1)
+    mf::run<mf::Mx4>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  else
+    mf::run<mf::Mx4x>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
 }
 
 size_t prefill_fp8_workspace_size(int tokens, int k, const wm_fp8_experts& e, bool has_shared) {
@@ -1365,10 +1616,18 @@ size_t prefill_fp8_workspace_size(int tokens, int k, const wm_fp8_experts& e, bo
 void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                  const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
                  uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s) {
-  if (routed.scale_format == 1)
-    mf::run<mf::Mx8e>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
-  else
-    mf::run<mf::Mx8>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  const bool e2m3 = routed.act_terms == 1;
+  if (routed.scale_format == 1) {
+    if (e2m3)
+      mf::run<mf::Mx8e>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+    else
+      mf::run<mf::Mx8ex>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  } else {
+    if (e2m3)
+      mf::run<mf::Mx8>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+    else
+      mf::run<mf::Mx8x>(x, tokens, indices, weights, k, routed, shared, shared_gate, y, combine, ws, ws_bytes, s);
+  }
 }
 
 }  // namespace wm
@@ -1454,6 +1713,21 @@ WM_EXPORT int wm_split_rows_e2m3(const void* x, int32_t rows, int32_t hidden, vo
                        wm::as_stream(stream), (const uint16_t*)x, (int)rows, (int)hidden, (uint8_t*)out, nullptr,
                        nullptr);
     wm::check_launch("split_rows_e2m3");
+  });
+}
+
+WM_EXPORT int wm_split_rows_e4m3(const void* x, int32_t rows, int32_t hidden, void* terms, void* scales, void* stream) {
+  return wm::guarded([&] {
+    if (rows < 0 || hidden < 128 || hidden % 128) wm::fail("wm_split_rows_e4m3: hidden must be a positive multiple of 128");
+    if (rows == 0) return;
+    if (!x || !terms || !scales) wm::fail("wm_split_rows_e4m3: null pointer");
+    if ((uintptr_t)x % 16 || (uintptr_t)terms % 16 || (uintptr_t)scales % 4)
+      wm::fail("wm_split_rows_e4m3: x and terms must be 16-byte aligned, scales 4-byte");
+    const int64_t jobs = (int64_t)rows * (hidden / 32);
+    hipLaunchKernelGGL(wm::mf::split8_rows_kernel, dim3((unsigned)((jobs + 255) / 256)), dim3(256), 0,
+                       wm::as_stream(stream), (const uint16_t*)x, (int)rows, (int)hidden, (uint8_t*)terms,
+                       (uint32_t*)scales, nullptr, nullptr);
+    wm::check_launch("split_rows_e4m3");
   });
 }
 

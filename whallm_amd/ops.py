@@ -72,6 +72,7 @@ class MXFP4Experts:
     up_first: bool = False
     swiglu_limit: float = 0.0
     tiled: bool = False
+    act_terms: str = "e4m3"
 
     @property
     def hidden(self) -> int:
@@ -109,10 +110,33 @@ class MXFP4Experts:
             self.gate_up.data_ptr(), self.gate_up_scales.data_ptr(), self.down.data_ptr(), self.down_scales.data_ptr(),
             stride(self.gate_up), stride(self.gate_up_scales), stride(self.down), stride(self.down_scales),
             0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
-            float(self.swiglu_limit), int(self.tiled))
+            float(self.swiglu_limit), int(self.tiled), _act_terms(self.act_terms))
 
     def tensors(self):
         return (self.gate_up, self.gate_up_scales, self.down, self.down_scales, self.slots)
+
+
+def _act_terms(name: str) -> int:
+    """The grouped GEMM's activation terms: "e4m3" (two E4M3 terms per 32 values, bf16-exact
+    above 2^-13 of the block maximum, the default) or "e2m3" (two E2M3 terms, ~7 significant
+    bits of the block maximum, twice the MFMA rate against MXFP4 weights)."""
+    if name not in ("e4m3", "e2m3"):
+        raise ValueError('act_terms must be "e4m3" or "e2m3"')
+    return 0 if name == "e4m3" else 1
+
+
+def split_rows_e4m3(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 rows [.., H] (H a multiple of 128) -> (uint8 terms [rows, H/128, 256], int32 scales
+    [rows, H/128]): the bf16-exact E4M3 term pairs as the prefill GEMMs read activations
+    (wm_split_rows_e4m3)."""
+    device = _require_device(x)
+    x = _contig(x, torch.bfloat16, "x")
+    H = x.shape[-1]
+    rows = x.numel() // H if H else 0
+    terms = torch.empty(rows, H // 128, 256, dtype=torch.uint8, device=device)
+    scales = torch.empty(rows, H // 128, dtype=torch.int32, device=device)
+    _lib.call("wm_split_rows_e4m3", _ptr(x), rows, H, _ptr(terms), _ptr(scales), _stream(device))
+    return terms, scales
 
 
 def split_rows_e2m3(x: torch.Tensor) -> torch.Tensor:
@@ -148,6 +172,7 @@ def prefill_layout(experts):
     _lib.call("wm_repack_prefill_fp8" if fp8 else "wm_repack_prefill_mxfp4", ctypes.byref(table),
               *(_ptr(t) for t in out), _stream(device))
     kw = {"scale_format": experts.scale_format} if fp8 else {}
+    kw["act_terms"] = experts.act_terms
     cls = FP8Experts if fp8 else MXFP4Experts
     return cls(*out, experts=E if lead else None, up_first=experts.up_first, swiglu_limit=experts.swiglu_limit,
                tiled=True, **kw)
@@ -409,6 +434,7 @@ class FP8Experts:
     swiglu_limit: float = 0.0
     tiled: bool = False
     scale_format: int = 0
+    act_terms: str = "e4m3"
 
     @property
     def hidden(self) -> int:
@@ -447,7 +473,7 @@ class FP8Experts:
             self.w13.data_ptr(), self.w13_scales.data_ptr(), self.w2.data_ptr(), self.w2_scales.data_ptr(),
             stride(self.w13), stride(self.w13_scales), stride(self.w2), stride(self.w2_scales),
             0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
-            float(self.swiglu_limit), int(self.tiled), int(self.scale_format))
+            float(self.swiglu_limit), int(self.tiled), int(self.scale_format), _act_terms(self.act_terms))
 
     def tensors(self):
         return (self.w13, self.w13_scales, self.w2, self.w2_scales, self.slots)
