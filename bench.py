@@ -215,16 +215,22 @@ class DecodeStack:
 
 
 class Prefill:
-    """C3: one MXFP4 MoE layer at a 16,384-token prefill, Zipf(1.1)-skewed routing."""
+    """C3: one MXFP4 MoE layer at a 16,384-token prefill, Zipf(1.1)-skewed routing.
+
+    act_terms "e4m3": the activations enter the scaled MFMAs as two E4M3 terms per 32 values
+    (bf16-exact above 2^-13 of each block's maximum, the reference's activation precision;
+    fp4 x fp8 at the FP8 rate); "e2m3": two E2M3 terms (~7 significant bits of the block
+    maximum; fp4 x fp6 at the FP4 rate)."""
     name = "c3-prefill"
-    # MXFP4 weights (E2M1 + E8M0 per 32) straight into scaled MFMAs against two E2M3 terms
-    # (hi, lo; E8M0 per 32 each) of the bf16 activations, fp32 accumulation
+    # MXFP4 weights (E2M1 + E8M0 per 32) straight into scaled MFMAs against two terms (hi, lo)
+    # of the bf16 activations, fp32 accumulation
     dtype = "mxfp4"
     data = "synthetic (random-init MXFP4 weights, N(0,1) bf16 tokens, N(0,1) + Zipf(1.1) bias router logits)"
 
-    def __init__(self, device, hidden=2048, experts=512, inter=512, k=10, tokens=16384, seed=0):
+    def __init__(self, device, hidden=2048, experts=512, inter=512, k=10, tokens=16384, seed=0, act_terms="e4m3"):
         from whallm_amd import synthetic as S
         self.H, self.E, self.I, self.K, self.T = hidden, experts, inter, k, tokens
+        self.act_terms = act_terms
         self.device = device
         g = torch.Generator(device=device)
         g.manual_seed(seed)
@@ -232,9 +238,10 @@ class Prefill:
         self.shared = S.mxfp4_experts_device(1, hidden, inter, device, g)
         # the layer's weights are repacked once into the prefill tile layout (set-up, untimed);
         # the row-layout copies stay for the CPU baseline
+        import dataclasses
         import whallm_amd as wa
-        self.tiled = wa.prefill_layout(self.experts)
-        self.tiled_shared = wa.prefill_layout(self.shared)
+        self.tiled = dataclasses.replace(wa.prefill_layout(self.experts), act_terms=act_terms)
+        self.tiled_shared = dataclasses.replace(wa.prefill_layout(self.shared), act_terms=act_terms)
         self.gate = (torch.randn(hidden, device=device, generator=g) * 0.02).to(torch.bfloat16)
         rng = np.random.default_rng(seed)
         bias = torch.from_numpy(S.zipf_bias(experts, 1.1, rng)).to(device)
@@ -299,10 +306,13 @@ class Prefill:
         self.graph.replay()
 
     def config(self):
+        terms = ("two E4M3 terms per 32 values (bf16-exact above 2^-13 of the block maximum), fp4 x fp8"
+                 if self.act_terms == "e4m3" else
+                 "two E2M3 terms per 32 values (~7 significant bits of the block maximum), fp4 x fp6")
         return {"workload": "c3-prefill: Qwen3-Next-style MXFP4 MoE layer, 16384-token prefill, Zipf(1.1) routing",
                 "hidden": self.H, "experts": self.E, "moe_intermediate": self.I, "top_k": self.K,
-                "shared_experts": 1, "tokens": self.T, "activations": "bf16",
-                "compute": "v_mfma_scale_f32_32x32x64_f8f6f4: MXFP4 weights (prefill tile layout) x E2M3 hi/lo "
+                "shared_experts": 1, "tokens": self.T, "activations": "bf16", "activation_terms": terms,
+                "compute": "v_mfma_scale_f32_32x32x64_f8f6f4: MXFP4 weights (prefill tile layout) x the "
                            "activation terms"}
 
     def cpu_baseline(self, budget_s: float):
@@ -799,12 +809,16 @@ def measure(wl, steps: int, warmup: int):
         gu_ms, dn_ms = wl.kernel_ms(steps)
         achieved = wl.gate_up_flops() / (gu_ms / 1e3) / 1e12
         layer_tflops = wl.flops() / (ms_per_step / 1e3) / 1e12
-        # fp4 x fp6 operands run the 32x32x64 f8f6f4 MFMA at the FP4/FP6 rate; the two
-        # activation terms make every product two MFMA products, so useful FLOPs top out at
-        # peak / 2 (mfma_instruction_frac counts the instructions)
+        # fp4 x fp6 operands run the 32x32x64 f8f6f4 MFMA at the FP4/FP6 rate, fp4 x fp8 at the
+        # FP8 rate; the two activation terms make every product two MFMA products, so useful
+        # FLOPs top out at half the instruction's rate (mfma_instruction_frac counts the
+        # instructions against that rate)
+        rate = FP4_PEAK_TFLOPS if getattr(wl, "act_terms", "e2m3") == "e2m3" else FP8_PEAK_TFLOPS
+        traffic = profiled_traffic("prefill_c3_gate_up" + ("" if wl.act_terms == "e4m3" else "_e2m3"))
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": FP4_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(achieved / FP4_PEAK_TFLOPS, 4), "traffic": profiled_traffic("prefill_c3_gate_up"),
-                    "mfma_instruction_frac": round(2 * achieved / FP4_PEAK_TFLOPS, 4),
+                    "frac": round(achieved / FP4_PEAK_TFLOPS, 4), "traffic": traffic,
+                    "mfma_instruction_frac": round(2 * achieved / rate, 4),
+                    "mfma_instruction_rate_tflops": rate,
                     "frac_of_fp8_peak": round(achieved / FP8_PEAK_TFLOPS, 4),
                     "kernel": "gate_up_mx_kernel<Mx4> (grouped gate/up GEMM + SwiGLU, one launch per layer)",
                     "kernel_ms": round(gu_ms, 5), "down_kernel_ms": round(dn_ms, 5),
@@ -812,6 +826,21 @@ def measure(wl, steps: int, warmup: int):
                     "layer_tflops": round(layer_tflops, 1)}
 
     return ms_per_step, value, roofline, wall
+
+
+def prefill_e2m3(pf, args):
+    """The same C3 layer on the faster E2M3 activation terms (the bench's other prefill path),
+    timed the same way, as a secondary record beside the bf16-exact default."""
+    import dataclasses
+    pf2 = Prefill.__new__(Prefill)
+    pf2.__dict__.update(pf.__dict__)
+    pf2.act_terms = "e2m3"
+    pf2.tiled = dataclasses.replace(pf.tiled, act_terms="e2m3")
+    pf2.tiled_shared = dataclasses.replace(pf.tiled_shared, act_terms="e2m3")
+    pf2.graph = None
+    ms, value, roof, _ = measure(pf2, min(args.steps, 20), min(args.warmup, 5))
+    return {"value": round(value, 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "config": pf2.config(),
+            "roofline": roof}
 
 
 def main():
@@ -862,6 +891,7 @@ def main():
         log("[bench] c3-prefill half")
         pf = Prefill(device)
         p_ms, p_value, p_roof, p_wall = measure(pf, min(args.steps, 20), min(args.warmup, 5))
+        e2m3 = prefill_e2m3(pf, args)
         p_cpu = None
         if not args.no_cpu_baseline:
             log("[bench] timing the prefill CPU baseline")
@@ -870,9 +900,11 @@ def main():
         prefill = {"value": round(p_value, 1), "unit": "tokens/s", "ms_per_step": round(p_ms, 5),
                    "steps": min(args.steps, 20), "warmup": min(args.warmup, 5), "dtype": pf.dtype, "data": pf.data,
                    "config": pf.config(), "roofline": p_roof, "cpu_baseline": p_cpu,
-                   "wall_s_timed_region": round(p_wall, 4)}
+                   "wall_s_timed_region": round(p_wall, 4), "e2m3": e2m3}
     else:
         dtype, data, config = wl.dtype, wl.data, wl.config()
+    if args.config == "c3-prefill":
+        config = dict(config, e2m3=prefill_e2m3(wl, args))
 
     # BASELINE.md publishes one number, for the qwen-resident workload (p50 ms per call)
     published = getattr(WORKLOADS[args.config], "PUBLISHED_P50_MS", None)

@@ -374,6 +374,32 @@ WM_EXPORT int wm_moe_decode_persistent_mxfp4(const float* logits, int32_t layers
                                              float* residual_trace, void* stream);
 /* Byte offset of the state buffer's int32 status word (0 = healthy; see above). */
 WM_EXPORT size_t wm_decode_status_offset(int32_t layers, int32_t experts);
+
+/* One MoE decode layer for one token in one launch: x = bf16(rmsnorm(residual) * norm_weight)
+ * (norm_weight nullable: unit), logits = x . router^T (bf16 [experts, hidden]), softmax top-k
+ * (norm_topk_prob), y = sum_k w_k FFN_k(x) + sigmoid(x . shared_gate) FFN_shared(x) (shared and
+ * shared_gate nullable; a null gate leaves the shared expert ungated), residual_out = residual
+ * + bf16(y) (nullable; may alias residual). The decoder layer's MoE half between its attention
+ * blocks, called once per layer (DecoderLayer.feed_forward -> SparseMoE, qwen4_exp.py:1146,
+ * :1036-1051; the native engine's expert step with its router GEMV and shared gate,
+ * Native/QwenNative/engine.mm:2073-2236). Optional outputs: y bf16 [hidden], x_out bf16
+ * [hidden], logits_out fp32 [experts], indices_out int32 [k], weights_out fp32 [k].
+ * Shapes with a fused kernel (hidden / intermediate 2048 / 512 and 1024 / 512, k <= 11) run
+ * as one launch whose outcome is in the state's status word (wm_moe_layer_decode_status_offset:
+ * 0 done, 1 a grid-wide wait ran out, 4 no valid route: fewer than k selectable logits, e.g.
+ * NaN; after a nonzero status residual_out and y are not written and the state must be
+ * zero-filled again); other shapes run norm_router, the router, the decode GEMV kernels and the
+ * residual add (errors returned at once). state: wm_moe_layer_decode_state_size bytes,
+ * zero-filled before the first call, reused by calls in stream order (one call at a time).
+ * Tables in the row layout; experts <= 1024; vectors and router 16-byte aligned. */
+WM_EXPORT size_t wm_moe_layer_decode_state_size(int32_t experts, int32_t hidden, int32_t inter, int32_t k);
+WM_EXPORT size_t wm_moe_layer_decode_status_offset(int32_t experts, int32_t inter);
+WM_EXPORT int wm_moe_layer_decode(const float* residual, float* residual_out, const void* norm_weight, float eps,
+                                  const void* router, const void* shared_gate, int32_t experts, int32_t k,
+                                  int32_t norm_topk_prob, const wm_mxfp4_experts* routed,
+                                  const wm_mxfp4_experts* shared, void* y, void* x_out, float* logits_out,
+                                  int32_t* indices_out, float* weights_out, void* state, size_t state_bytes,
+                                  void* stream);
 /* 1 when the current device runs block b of the persistent launch on XCC b % 8, so
  * messages read only within one XCD use XCD-local stores; 0 when it does not (the
  * persistent launch then uses device-scope stores throughout); -1 on error. Checked

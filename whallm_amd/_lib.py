@@ -82,6 +82,10 @@ _SIGNATURES = {
     "wm_repack_down_slices": (c_int, [_P, _P, c_int64, c_int64, c_int32, c_int32, c_int32, _P, _P, _P]),
     "wm_decode_state_size": (c_size_t, [c_int32, c_int32]),
     "wm_decode_status_offset": (c_size_t, [c_int32, c_int32]),
+    "wm_moe_layer_decode_state_size": (c_size_t, [c_int32, c_int32, c_int32, c_int32]),
+    "wm_moe_layer_decode_status_offset": (c_size_t, [c_int32, c_int32]),
+    "wm_moe_layer_decode": (c_int, [_P, _P, _P, c_float, _P, _P, c_int32, c_int32, c_int32, POINTER(MXFP4ExpertsC),
+                                    POINTER(MXFP4ExpertsC), _P, _P, _P, _P, _P, _P, c_size_t, _P]),
     "wm_decode_xcd_local": (c_int, [_P]),
     "wm_slot_cache_open": (c_void_p, [c_int32, c_int64, c_int32, c_int32, _P, _P, _P, c_char_p, c_size_t]),
     "wm_slot_cache_close": (None, [_P]),

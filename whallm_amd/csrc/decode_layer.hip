@@ -1,0 +1,648 @@
+// One decode layer of the MXFP4 MoE in one launch: the step a decoder layer takes between
+// its attention blocks (DecoderLayer.feed_forward -> SparseMoE, qwen4_exp.py:1146 and
+// :1036-1051; the native engine's expert step with its pre-norm, router GEMV and shared
+// gate, Native/QwenNative/engine.mm:2073-2236), for one token:
+//
+//   x = bf16(rmsnorm(r) * w_norm);  logits = x . Wr^T;  (idx, w) = softmax top-k;
+//   y = sum_k w_k FFN_k(x) + sigmoid(x . g) FFN_shared(x);  r' = r + bf16(y).
+//
+// The per-layer path launches norm_router, route, gate_up and down (four dependent kernels,
+// ~31 us a layer at C2); here 256 workgroups of 4 waves, all resident, run the whole layer
+// with two grid-wide exchanges:
+//   1. every workgroup normalises r into LDS (x, bf16) and computes its share of the router
+//      logits (one wave per expert row, rows loaded before the norm) and publishes them as
+//      64-bit message words (value | epoch); every workgroup gathers all E logits and routes
+//      redundantly (the wave top-k of route_device.h: same selections as wm_route_softmax_topk
+//      on the same logits);
+//   2. gate_up: the (entry, intermediate index) pairs of the K routed experts and the shared one
+//      are spread evenly over the 1024 waves; each wave streams its gate and up rows (64 lanes
+//      x 16 bytes a row chunk), dots them with x held in registers and writes act; then each
+//      workgroup raises a completion counter (release, agent scope);
+//   3. down: workgroup b owns output rows [H/256 b, H/256 (b + 1)); its waves split the layer's
+//      entries and load their down rows into registers right after routing, before waiting for
+//      the counter; once every workgroup has published act they read it from L2 and reduce
+//      y = sum_k w_k act_k . Wd_k[o] + gate act_s . Wd_s[o] in fp32 (lanes, then waves).
+//
+// Exchanges use per-call epochs kept in the state buffer (each workgroup's own word), so the
+// same launch can be replayed from a graph; every wait is bounded and raises the status word.
+#include <cmath>
+#include <string>
+
+#include "moe_internal.h"
+#include "route_device.h"
+#include "wm_common.h"
+
+namespace wm {
+namespace dl {
+
+constexpr int WGS = 256;                 // workgroups (all resident: 256 threads, ~170 VGPRs)
+constexpr int WAVES = 4;
+constexpr int THREADS = 64 * WAVES;
+constexpr int MAX_ENTRIES = 12;          // routed (k <= 11) + shared
+constexpr int MAX_EXPERTS = 1024;        // router rows: 4 per workgroup
+constexpr uint32_t SPIN_LIMIT = 1u << 20;
+constexpr uint32_t ST_STALLED = 1, ST_NO_ROUTE = 4;
+
+// State buffer (zero-filled once by the caller): logit words, act rows, the completion
+// counter, per-workgroup epochs and the status word.
+struct Layout {
+  size_t logits, act, counter, epoch, status, total;
+};
+__host__ __device__ inline Layout layout(int experts, int inter) {
+  Layout d;
+  size_t at = 0;
+  d.logits = at;  at += (size_t)MAX_EXPERTS * 8;
+  d.act = at;     at += (size_t)MAX_ENTRIES * inter * 4;
+  d.counter = at; at += 256;
+  d.epoch = at;   at += (size_t)WGS * 4;
+  d.status = at;  at += 256;
+  d.total = at;
+  (void)experts;
+  return d;
+}
+
+struct Params {
+  const float* r;            // [H] fp32 residual
+  float* r_out;              // [H] r + bf16(y) (may alias r), nullable
+  const uint16_t* norm_w;    // [H] bf16 RMSNorm weight, nullable (no weight)
+  float eps;
+  const uint16_t* router;    // [E, H] bf16
+  const uint16_t* gate_vec;  // [H] bf16 shared-expert gate, nullable (ungated shared expert)
+  wm_mxfp4_experts routed;
+  wm_mxfp4_experts shared;
+  int has_shared;
+  int experts, k, norm_topk;
+  uint16_t* y;               // [H] bf16 MoE output, nullable
+  uint16_t* x_out;           // [H] bf16 normalised input, nullable
+  float* logits_out;         // [E] fp32, nullable
+  int32_t* idx_out;          // [k] int32, nullable
+  float* w_out;              // [k] fp32, nullable
+  uint8_t* state;
+};
+
+__device__ __forceinline__ void put_word(uint64_t* p, uint32_t bits, uint32_t epoch) {
+  __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Row chunks of 1 KB (64 lanes x 16 bytes): a gate_up row of H / 2 bytes spans CH chunks; the
+// lanes past the row's end in the last chunk load nothing.
+template <int H>
+struct GateUpShape {
+  static constexpr int CH = (H / 2 + 1023) / 1024;
+};
+
+// The down rows' lane split (as the per-layer decode kernel's): LPR lanes per row, GPL groups
+// of 32 values per lane, lanes past the row's last group idle.
+template <int I>
+struct DownShape {
+  static constexpr int G = I / 32;
+  static constexpr int LPR = G >= 64 ? 64 : (G > 16 ? (G % 16 == 0 ? 16 : 4) : (G > 8 ? 16 : (G > 4 ? 8 : 4)));
+  static constexpr int GPL = (G + LPR - 1) / LPR;
+  static constexpr int NS = 64 / LPR;  // rows a wave reads at once
+};
+
+template <int H, int I, int PMAX>
+__global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
+  static_assert(H % WGS == 0 && I % 32 == 0, "fused decode layer shape");
+  constexpr int CH = GateUpShape<H>::CH;
+  using DS = DownShape<I>;
+  constexpr int RPB = H / WGS;                          // output rows of a workgroup
+  constexpr int STEPS = (RPB + DS::NS - 1) / DS::NS;    // down row loads per entry
+  constexpr int EPW = (MAX_ENTRIES + WAVES - 1) / WAVES;  // down entries per wave
+
+  __shared__ __attribute__((aligned(16))) uint32_t xs[H / 2];  // x as bf16 pairs
+  __shared__ float lg[MAX_EXPERTS];
+  __shared__ float red[2 * WAVES];
+  __shared__ int rid[MAX_ENTRIES];
+  __shared__ float rw[MAX_ENTRIES];
+  __shared__ int rres[MAX_ENTRIES];  // entry resident (its slot map entry, if any, >= 0)
+  __shared__ float part[WAVES][RPB];
+  __shared__ uint32_t epoch_s;
+  __shared__ int fail_s;
+
+  const int b = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const Layout L = layout(p.experts, I);
+  uint64_t* logit_words = reinterpret_cast<uint64_t*>(p.state + L.logits);
+  float* act = reinterpret_cast<float*>(p.state + L.act);
+  uint32_t* counter = reinterpret_cast<uint32_t*>(p.state + L.counter);
+  uint32_t* epochs = reinterpret_cast<uint32_t*>(p.state + L.epoch);
+  uint32_t* status = reinterpret_cast<uint32_t*>(p.state + L.status);
+  const int E = p.experts, K = p.k;
+  const int NE = K + (p.has_shared ? 1 : 0);
+
+  // ---- router rows (before the norm: they do not depend on x) and the epoch
+  const int e_row = b + WGS * wave;  // this wave's router row, if any
+  uint4 rrow[H / 512];                // H bf16 = H / 512 chunks of 1 KB (64 lanes x 16 bytes)
+  const bool has_row = e_row < E;
+  if (has_row) {
+#pragma unroll
+    for (int c = 0; c < H / 512; ++c)
+      rrow[c] = gload16(p.router + (int64_t)e_row * H + 512 * c + 8 * lane);
+  }
+  uint4 grow[H / 512];  // the shared gate vector, on the last wave
+  const bool gate_wave = wave == WAVES - 1 && p.gate_vec != nullptr;
+  if (gate_wave) {
+#pragma unroll
+    for (int c = 0; c < H / 512; ++c) grow[c] = gload16(p.gate_vec + 512 * c + 8 * lane);
+  }
+  if (tid == 0) {
+    epoch_s = epochs[b] + 1;
+    fail_s = 0;
+  }
+
+  // ---- x = bf16(rmsnorm(r) * w) (wm_norm_router's arithmetic): each thread H / 256 values
+  static_assert(H % 512 == 0, "router rows of whole 1 KB chunks, an even share of r per thread");
+  constexpr int VPT = H / THREADS;
+  float rv[VPT];
+#pragma unroll
+  for (int q = 0; q < VPT; q += 2) {
+    const float2 v = *reinterpret_cast<const float2*>(p.r + VPT * tid + q);
+    rv[q] = v.x;
+    rv[q + 1] = v.y;
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) ss += rv[q] * rv[q];
+  ss = segment_sum<64>(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + p.eps);
+  const uint32_t epoch = epoch_s;
+#pragma unroll
+  for (int q = 0; q < VPT; q += 2) {
+    float a = rv[q] * inv, c = rv[q + 1] * inv;
+    if (p.norm_w) {
+      const uint32_t wpair = *reinterpret_cast<const uint32_t*>(p.norm_w + VPT * tid + q);
+      a *= bf16_bits_to_f32(wpair & 0xffffu);
+      c *= bf16_bits_to_f32(wpair >> 16);
+    }
+    xs[(VPT * tid + q) / 2] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(c) << 16);
+  }
+  __syncthreads();
+  if (b == 0 && p.x_out)
+    for (int i = tid; i < H / 2; i += THREADS) reinterpret_cast<uint32_t*>(p.x_out)[i] = xs[i];
+
+  // ---- router logits of this workgroup's rows, published; the shared gate
+  if (has_row) {
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < H / 512; ++c) {
+      const uint4 wq = rrow[c];
+      const uint4 xq = *reinterpret_cast<const uint4*>(&xs[(512 * c + 8 * lane) / 2]);
+      a = dot2_bf16(bits_to_bf16x2(wq.x), bits_to_bf16x2(xq.x), a);
+      a = dot2_bf16(bits_to_bf16x2(wq.y), bits_to_bf16x2(xq.y), a);
+      a = dot2_bf16(bits_to_bf16x2(wq.z), bits_to_bf16x2(xq.z), a);
+      a = dot2_bf16(bits_to_bf16x2(wq.w), bits_to_bf16x2(xq.w), a);
+    }
+    a = segment_sum<64>(a);
+    if (lane == 0) {
+      put_word(&logit_words[e_row], __float_as_uint(a), epoch);
+      if (p.logits_out) p.logits_out[e_row] = a;
+    }
+  }
+  float gate = 1.0f;
+  if (gate_wave) {
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < H / 512; ++c) {
+      const uint4 wq = grow[c];
+      const uint4 xq = *reinterpret_cast<const uint4*>(&xs[(512 * c + 8 * lane) / 2]);
+      a = dot2_bf16(bits_to_bf16x2(wq.x), bits_to_bf16x2(xq.x), a);
+      a = dot2_bf16(bits_to_bf16x2(wq.y), bits_to_bf16x2(xq.y), a);
+      a = dot2_bf16(bits_to_bf16x2(wq.z), bits_to_bf16x2(xq.z), a);
+      a = dot2_bf16(bits_to_bf16x2(wq.w), bits_to_bf16x2(xq.w), a);
+    }
+    a = segment_sum<64>(a);
+    gate = 1.0f / (1.0f + __expf(-a));
+  }
+  if (gate_wave && lane == 0) red[4] = gate;
+
+  // ---- wave 0 gathers every logit (bounded polls) and routes
+  if (wave == 0) {
+    bool ok = true;
+    constexpr int PER = MAX_EXPERTS / 64;
+    uint64_t v[PER];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+      const int e = lane + 64 * m;
+      v[m] = e < E ? __hip_atomic_load(&logit_words[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : (uint64_t)epoch << 32;
+    }
+    uint32_t spins = 0;
+    while (true) {
+      bool ready = true;
+#pragma unroll
+      for (int m = 0; m < PER; ++m) ready &= (uint32_t)(v[m] >> 32) == epoch;
+      if (__all(ready)) break;
+      if (++spins > SPIN_LIMIT) {
+        __hip_atomic_store(status, ST_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = false;
+        break;
+      }
+      if ((spins & 255) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        ok = false;
+        break;
+      }
+#pragma unroll
+      for (int m = 0; m < PER; ++m) {
+        const int e = lane + 64 * m;
+        if (e < E && (uint32_t)(v[m] >> 32) != epoch)
+          v[m] = __hip_atomic_load(&logit_words[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+      const int e = lane + 64 * m;
+      if (e < E) lg[e] = __uint_as_float((uint32_t)v[m]);
+    }
+    if (!ok && lane == 0) fail_s = 1;
+    if (ok) {
+      int sel = 0;
+      float w = 0.0f;
+      if (E <= 512)
+        wave_route_softmax<8>(lg, E, K, p.norm_topk != 0, lane, sel, w, nullptr);
+      else
+        wave_route_softmax<16>(lg, E, K, p.norm_topk != 0, lane, sel, w, nullptr);
+      // a selection outside [0, E) (fewer than k selectable logits, e.g. NaN) ends the call
+      const bool bad = lane < K && (sel < 0 || sel >= E);
+      if (__any(bad)) {
+        if (lane == 0) {
+          fail_s = 1;
+          __hip_atomic_store(status, ST_NO_ROUTE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else if (lane < K) {
+        rid[lane] = sel;
+        rw[lane] = w;
+        if (b == 0 && p.idx_out) p.idx_out[lane] = sel;
+        if (b == 0 && p.w_out) p.w_out[lane] = w;
+      }
+    }
+  }
+  __syncthreads();
+  if (p.has_shared && tid == 0) {
+    rid[K] = -1;
+    rw[K] = p.gate_vec ? red[4] : 1.0f;
+  }
+  if (fail_s) {  // every workgroup routes the same logits, so all leave here
+    if (tid == 0) epochs[b] = epoch;
+    return;
+  }
+  __syncthreads();
+  if (tid < NE) {  // residency of the entries (a non-resident expert contributes nothing)
+    const int e = rid[tid];
+    const wm_mxfp4_experts& t = e < 0 ? p.shared : p.routed;
+    rres[tid] = !t.slots || gload<int32_t>(t.slots + (e < 0 ? 0 : e)) >= 0;
+  }
+  __syncthreads();
+
+  // regions of an entry (the routed expert rid[entry], or the shared one for rid < 0), each
+  // field selected on its own so no table is copied to scratch memory
+  auto regions = [&](int entry) {
+    const int e = rid[entry];
+    const bool sh = e < 0;
+    int64_t slot = sh ? 0 : (p.routed.slots ? (int64_t)gload<int32_t>(p.routed.slots + e) : e);
+    slot = slot < 0 ? 0 : slot;  // not resident: the entry is skipped, slot 0 keeps addresses valid
+    ExpertRegions r;
+    r.gate_up = (const uint8_t*)(sh ? p.shared.gate_up : p.routed.gate_up) +
+                slot * (sh ? p.shared.gate_up_stride : p.routed.gate_up_stride);
+    r.gate_up_scales = (const uint8_t*)(sh ? p.shared.gate_up_scales : p.routed.gate_up_scales) +
+                       slot * (sh ? p.shared.gate_up_scales_stride : p.routed.gate_up_scales_stride);
+    r.down = (const uint8_t*)(sh ? p.shared.down : p.routed.down) + slot * (sh ? p.shared.down_stride : p.routed.down_stride);
+    r.down_scales = (const uint8_t*)(sh ? p.shared.down_scales : p.routed.down_scales) +
+                    slot * (sh ? p.shared.down_scales_stride : p.routed.down_scales_stride);
+    return r;
+  };
+
+  // ---- down prefetch: this wave's entries (wave, wave + 4, ...) for the workgroup's rows
+  const int o0 = RPB * b;
+  const int slot = lane / DS::LPR, gl = lane % DS::LPR;
+  uint4 dq[EPW][STEPS][DS::GPL];
+  uint32_t ds_[EPW][STEPS][DS::GPL];
+#pragma unroll
+  for (int j = 0; j < EPW; ++j) {
+    const int entry = wave + WAVES * j;
+    const bool live = entry < NE && rres[entry < NE ? entry : 0];
+    ExpertRegions r = regions(live ? entry : 0);
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+      const int row = st * DS::NS + slot;
+      const int o = o0 + row;
+#pragma unroll
+      for (int gp = 0; gp < DS::GPL; ++gp) {
+        const int g = gl + gp * DS::LPR;
+        if (live && row < RPB && g < DS::G) {
+          dq[j][st][gp] = reinterpret_cast<const uint4*>(r.down + (int64_t)o * (I / 2))[g];
+          ds_[j][st][gp] = r.down_scales[(int64_t)o * DS::G + g];
+        } else {
+          dq[j][st][gp] = make_uint4(0, 0, 0, 0);
+          ds_[j][st][gp] = 127;
+        }
+      }
+    }
+  }
+
+  // ---- gate_up: this wave's (entry, intermediate index) pairs
+  {
+    const int gw = b * WAVES + wave, nwaves = WGS * WAVES;
+    const int total = NE * I;
+    const int per = (total + nwaves - 1) / nwaves;
+    const int n0 = gw * per;
+    uint32_t xr[CH][16];  // x values [1024 c + 32 lane, +32) of a row chunk (H / 2 bytes a row)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const bool in = 1024 * c + 16 * lane < H / 2;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = in ? *reinterpret_cast<const uint4*>(&xs[(2048 * c + 32 * lane) / 2 + 4 * q])
+                           : make_uint4(0, 0, 0, 0);
+        xr[c][4 * q] = v.x; xr[c][4 * q + 1] = v.y; xr[c][4 * q + 2] = v.z; xr[c][4 * q + 3] = v.w;
+      }
+    }
+    uint4 wq[PMAX][2][CH];
+    uint32_t sq[PMAX][2][CH];
+#pragma unroll
+    for (int u = 0; u < PMAX; ++u) {
+      const int n = n0 + u;
+      const bool live = u < per && n < total;
+      const int entry = live ? n / I : 0, i = live ? n % I : 0;
+      const ExpertRegions r = regions(entry);
+      const int up_first = rid[entry] < 0 ? p.shared.up_first : p.routed.up_first;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // h 0: gate row, 1: up row
+        const int row = (h ^ up_first) ? I + i : i;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const int off = 1024 * c + 16 * lane;
+          if (live && off < H / 2) {
+            wq[u][h][c] = gload16(r.gate_up + (int64_t)row * (H / 2) + off);
+            sq[u][h][c] = r.gate_up_scales[(int64_t)row * (H / 32) + off / 16];
+          } else {
+            wq[u][h][c] = make_uint4(0, 0, 0, 0);
+            sq[u][h][c] = 127;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < PMAX; ++u) {
+      const int n = n0 + u;
+      const bool live = u < per && n < total;  // wave-uniform
+      const int entry = live ? n / I : 0, i = live ? n % I : 0;
+      float g2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float a = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const uint32_t words[4] = {wq[u][h][c].x, wq[u][h][c].y, wq[u][h][c].z, wq[u][h][c].w};
+          const float sc = e8m0_scale_operand(sq[u][h][c]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            wm_bf16x2 wv[4];
+            fp4x8_to_bf16(words[j], sc, wv);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) a = dot2_bf16(wv[m], bits_to_bf16x2(xr[c][4 * j + m]), a);
+          }
+        }
+        g2[h] = segment_sum<64>(a);
+      }
+      if (live && lane == 0) {
+        const float limit = rid[entry] < 0 ? p.shared.swiglu_limit : p.routed.swiglu_limit;
+        float g = g2[0], u2 = g2[1];
+        if (limit > 0.0f) {
+          g = fminf(g, limit);
+          u2 = fminf(fmaxf(u2, -limit), limit);
+        }
+        act[entry * I + i] = rres[entry] ? silu(g) * u2 : 0.0f;
+      }
+    }
+  }
+  // every wave releases its act stores at agent scope, then one increment of the counter
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (tid == 0) {
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // wait until every workgroup of this call has published (bounded)
+    const uint32_t target = epoch * (uint32_t)WGS;
+    uint32_t spins = 0;
+    while ((int32_t)(__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+      if (++spins > SPIN_LIMIT) {
+        __hip_atomic_store(status, ST_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fail_s = 1;
+        break;
+      }
+      if ((spins & 255) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        fail_s = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+  if (fail_s) {
+    if (tid == 0) epochs[b] = epoch;
+    return;
+  }
+  // the other workgroups' act rows: read after an acquire at agent scope (every wave)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+
+  // ---- down: y[o] = sum over the wave's entries of w act . Wd[o]
+  float acc[STEPS];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) acc[st] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < EPW; ++j) {
+    const int entry = wave + WAVES * j;
+    const bool live = entry < NE && rres[entry < NE ? entry : 0];  // wave-uniform
+    const float w = live ? rw[entry] : 0.0f;
+    const float* arow = act + (live ? entry : 0) * I;
+#pragma unroll
+    for (int gp = 0; gp < DS::GPL; ++gp) {
+      const int g = gl + gp * DS::LPR;
+      float av[32];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float4 v = live && g < DS::G ? *reinterpret_cast<const float4*>(arow + 32 * g + 4 * q)
+                                            : make_float4(0, 0, 0, 0);
+        av[4 * q] = v.x; av[4 * q + 1] = v.y; av[4 * q + 2] = v.z; av[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        const float scale = e8m0_scale_operand(ds_[j][st][gp]);
+        const uint32_t words[4] = {dq[j][st][gp].x, dq[j][st][gp].y, dq[j][st][gp].z, dq[j][st][gp].w};
+        float s = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) {
+            wm_f32x2 wf;
+            switch (bb) {
+              case 0: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[jj], scale, 0); break;
+              case 1: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[jj], scale, 1); break;
+              case 2: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[jj], scale, 2); break;
+              default: wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(words[jj], scale, 3); break;
+            }
+            s = fmaf(wf[0], av[8 * jj + 2 * bb], s);
+            s = fmaf(wf[1], av[8 * jj + 2 * bb + 1], s);
+          }
+        }
+        acc[st] = fmaf(w, s, acc[st]);
+      }
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const float v = segment_sum<DS::LPR>(acc[st]);
+    const int row = st * DS::NS + slot;
+    if (gl == 0 && row < RPB) part[wave][row] = v;
+  }
+  __syncthreads();
+  if (tid < RPB) {
+    const int o = o0 + tid;
+    const float v = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
+    const uint16_t yb = f32_to_bf16_bits(v);
+    if (p.y) p.y[o] = yb;
+    if (p.r_out) p.r_out[o] = p.r[o] + bf16_bits_to_f32(yb);
+  }
+  if (tid == 0) epochs[b] = epoch;
+}
+
+}  // namespace dl
+
+// Shapes with a fused instantiation (hidden, intermediate).
+#define WM_DL_SHAPES(X) X(1024, 512) X(2048, 512)
+
+bool moe_layer_fused_supports(int hidden, int inter, int k) {
+  if (k < 1 || k > dl::MAX_ENTRIES - 1) return false;
+#define WM_DL_TRY(HH, II) if (hidden == HH && inter == II) return true;
+  WM_DL_SHAPES(WM_DL_TRY)
+#undef WM_DL_TRY
+  return false;
+}
+
+size_t moe_layer_state_size(int experts, int inter) { return dl::layout(experts, inter).total; }
+
+void moe_layer_fused(const dl::Params& p, int hidden, int inter, hipStream_t s) {
+#define WM_DL_RUN(HH, II)                                                                                     \
+  if (hidden == HH && inter == II) {                                                                           \
+    constexpr int PMAX = (dl::MAX_ENTRIES * II + dl::WGS * dl::WAVES - 1) / (dl::WGS * dl::WAVES);            \
+    hipLaunchKernelGGL((dl::moe_layer_kernel<HH, II, PMAX>), dim3(dl::WGS), dim3(dl::THREADS), 0, s, p);       \
+    check_launch("moe_layer_kernel");                                                                          \
+    return;                                                                                                    \
+  }
+  WM_DL_SHAPES(WM_DL_RUN)
+#undef WM_DL_RUN
+  fail("moe layer: no fused instantiation for this shape");
+}
+
+// r_out = r + bf16(y) for the unfused path.
+__global__ void __launch_bounds__(256) residual_add_kernel(const float* __restrict__ r, const uint16_t* __restrict__ y,
+                                                           int n, float* __restrict__ r_out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) r_out[i] = r[i] + bf16_bits_to_f32(y[i]);
+}
+
+// The unfused path's buffers, after the fused path's state in the same caller buffer.
+struct Scratch {
+  size_t x, logits, idx, w, y, act, total;
+};
+static Scratch scratch_layout(int experts, int hidden, int inter, int k, size_t base) {
+  auto al = [](size_t n) { return (n + 255) & ~(size_t)255; };
+  Scratch sc;
+  size_t at = al(base);
+  sc.x = at;      at += al((size_t)hidden * 2);
+  sc.logits = at; at += al((size_t)experts * 4);
+  sc.idx = at;    at += al((size_t)k * 4);
+  sc.w = at;      at += al((size_t)k * 4);
+  sc.y = at;      at += al((size_t)hidden * 2);
+  sc.act = at;    at += al((size_t)(k + 1) * inter * 4);
+  sc.total = at;
+  return sc;
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+WM_EXPORT size_t wm_moe_layer_decode_state_size(int32_t experts, int32_t hidden, int32_t inter, int32_t k) {
+  if (experts < 1 || hidden < 1 || inter < 1 || k < 1) return 0;
+  return scratch_layout(experts, hidden, inter, k, dl::layout(experts, inter).total).total;
+}
+
+WM_EXPORT size_t wm_moe_layer_decode_status_offset(int32_t experts, int32_t inter) {
+  return dl::layout(experts, inter).status;
+}
+
+WM_EXPORT int wm_moe_layer_decode(const float* residual, float* residual_out, const void* norm_weight, float eps,
+                                  const void* router, const void* shared_gate, int32_t experts, int32_t k,
+                                  int32_t norm_topk_prob, const wm_mxfp4_experts* routed,
+                                  const wm_mxfp4_experts* shared, void* y, void* x_out, float* logits_out,
+                                  int32_t* indices_out, float* weights_out, void* state, size_t state_bytes,
+                                  void* stream) {
+  return guarded([&] {
+    if (!residual || !router || !routed || !state) fail("wm_moe_layer_decode: null pointer");
+    validate_experts(routed, "routed experts", false);
+    if (shared) {
+      validate_experts(shared, "shared expert", true);
+      if (shared->hidden != routed->hidden || shared->inter != routed->inter)
+        fail("wm_moe_layer_decode: the shared expert's shape differs from the routed experts'");
+    }
+    if (routed->tiled || (shared && shared->tiled))
+      fail("wm_moe_layer_decode: the decode layer reads tables in the row layout");
+    const int H = routed->hidden, I = routed->inter;
+    if (experts != routed->experts) fail("wm_moe_layer_decode: experts differs from the table's");
+    if (experts < 1 || experts > dl::MAX_EXPERTS) fail("wm_moe_layer_decode: experts must be in 1..1024");
+    if (k < 1 || k > 32 || k > experts) fail("wm_moe_layer_decode: k must be in 1..min(32, experts)");
+    if (state_bytes < wm_moe_layer_decode_state_size(experts, H, I, k)) fail("wm_moe_layer_decode: state too small");
+    for (const void* q : {(const void*)residual, (const void*)residual_out, norm_weight, router, shared_gate,
+                          (const void*)y, (const void*)x_out})
+      if ((uintptr_t)q % 16) fail("wm_moe_layer_decode: vectors and the router must be 16-byte aligned");
+    if (!decode_mxfp4_supports(H, I)) fail("wm_moe_layer_decode: hidden and intermediate above 16384");
+    hipStream_t s = as_stream(stream);
+    if (moe_layer_fused_supports(H, I, k)) {
+      dl::Params p;
+      p.r = residual;
+      p.r_out = residual_out;
+      p.norm_w = (const uint16_t*)norm_weight;
+      p.eps = eps;
+      p.router = (const uint16_t*)router;
+      p.gate_vec = (const uint16_t*)shared_gate;
+      p.routed = *routed;
+      p.shared = shared ? *shared : *routed;
+      p.has_shared = shared ? 1 : 0;
+      p.experts = experts;
+      p.k = k;
+      p.norm_topk = norm_topk_prob;
+      p.y = (uint16_t*)y;
+      p.x_out = (uint16_t*)x_out;
+      p.logits_out = logits_out;
+      p.idx_out = indices_out;
+      p.w_out = weights_out;
+      p.state = (uint8_t*)state;
+      moe_layer_fused(p, H, I, s);
+      return;
+    }
+    // unfused: norm + router, routing, the decode GEMV kernels, the residual add
+    const Scratch sc = scratch_layout(experts, H, I, k, dl::layout(experts, I).total);
+    uint8_t* base = (uint8_t*)state;
+    uint16_t* xb = x_out ? (uint16_t*)x_out : (uint16_t*)(base + sc.x);
+    float* lg = logits_out ? logits_out : (float*)(base + sc.logits);
+    int32_t* ib = indices_out ? indices_out : (int32_t*)(base + sc.idx);
+    float* wb = weights_out ? weights_out : (float*)(base + sc.w);
+    uint16_t* yb = y ? (uint16_t*)y : (uint16_t*)(base + sc.y);
+    if (wm_norm_router(residual, nullptr, norm_weight, 1, H, eps, router, experts, nullptr, nullptr, 0, xb, nullptr, lg,
+                       nullptr, stream) != 0)
+      fail(std::string("wm_moe_layer_decode: ") + wm_last_error());
+    if (wm_route_softmax_topk(lg, 1, experts, k, norm_topk_prob, ib, wb, nullptr, stream) != 0)
+      fail(std::string("wm_moe_layer_decode: ") + wm_last_error());
+    decode_mxfp4(xb, 1, ib, wb, k, *routed, shared, (const uint16_t*)shared_gate, yb, true, (float*)(base + sc.act), s);
+    if (residual_out) {
+      hipLaunchKernelGGL(residual_add_kernel, dim3((H + 255) / 256), dim3(256), 0, s, residual, yb, H, residual_out);
+      check_launch("residual_add");
+    }
+  });
+}
+
+}  // extern "C"

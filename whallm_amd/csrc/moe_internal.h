@@ -76,6 +76,9 @@ void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const fl
                  const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
                  uint16_t* y, bool combine, void* ws, size_t ws_bytes, hipStream_t s);
 
+// The one-launch decode layer (decode_layer.hip): shapes with a fused instantiation.
+bool moe_layer_fused_supports(int hidden, int inter, int k);
+
 // Pairs at or below this count take the decode path.
 constexpr int DECODE_MAX_PAIRS = 256;
 

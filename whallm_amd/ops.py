@@ -662,6 +662,63 @@ class DecodeStackError(_lib.WhallmError):
     """A persistent decode launch ended early (its status word was nonzero)."""
 
 
+class DecodeLayer:
+    """One MoE decode layer for one token in one call (wm_moe_layer_decode): the pre-norm,
+    the router GEMV and softmax top-k, the routed and shared experts and the residual add,
+    as a decoder layer calls its MoE half between attention blocks (qwen4_exp.py:1146).
+    Holds the call's state buffer on the device (zero-filled; reused by calls in stream
+    order). Shapes with a fused kernel run as one launch; others as the per-layer kernels."""
+
+    STATUS_TEXT = {1: "a grid-wide wait ran out", 4: "no valid route (fewer than k selectable logits)"}
+
+    def __init__(self, experts: MXFP4Experts, router: torch.Tensor, shared: MXFP4Experts | None = None,
+                 shared_gate: torch.Tensor | None = None, k: int = 10, norm_weight: torch.Tensor | None = None,
+                 eps: float = 1e-6, norm_topk_prob: bool = True):
+        self.device = experts.gate_up.device
+        self.experts, self.shared, self.k, self.eps, self.norm_topk = experts, shared, k, eps, norm_topk_prob
+        self.E, self.H, self.I = experts.count, experts.hidden, experts.inter
+        self.router = _contig(router, torch.bfloat16, "router")
+        if self.router.shape != (self.E, self.H):
+            raise ValueError("router must be [experts, hidden]")
+        self.shared_gate = None if shared_gate is None else _contig(shared_gate, torch.bfloat16, "shared_gate")
+        self.norm_weight = None if norm_weight is None else _contig(norm_weight, torch.bfloat16, "norm_weight")
+        self._table = experts.c_struct()
+        self._shared = shared.c_struct() if shared is not None else None
+        lib = _lib.load()
+        self.state = torch.zeros(lib.wm_moe_layer_decode_state_size(self.E, self.H, self.I, k), dtype=torch.uint8,
+                                 device=self.device)
+        self.status_offset = lib.wm_moe_layer_decode_status_offset(self.E, self.I)
+
+    def __call__(self, residual: torch.Tensor, residual_out: torch.Tensor | None = None, y: torch.Tensor | None = None,
+                 x_out: torch.Tensor | None = None, logits_out: torch.Tensor | None = None,
+                 indices_out: torch.Tensor | None = None, weights_out: torch.Tensor | None = None):
+        """residual fp32 [H] -> residual_out (default: residual, updated in place) = residual +
+        bf16(y); the optional outputs receive y, x, the logits and the routes."""
+        if residual.dtype != torch.float32 or not residual.is_contiguous() or residual.numel() != self.H:
+            raise ValueError("residual must be a contiguous float32 [hidden] tensor")
+        if residual_out is None:
+            residual_out = residual
+        _lib.call("wm_moe_layer_decode", _ptr(residual), _ptr(residual_out), _ptr(self.norm_weight), float(self.eps),
+                  _ptr(self.router), _ptr(self.shared_gate), self.E, self.k, int(self.norm_topk),
+                  ctypes.byref(self._table), ctypes.byref(self._shared) if self._shared is not None else None,
+                  _ptr(y), _ptr(x_out), _ptr(logits_out), _ptr(indices_out), _ptr(weights_out), _ptr(self.state),
+                  self.state.numel(), _stream(self.device))
+        return residual_out
+
+    def status(self) -> int:
+        """0 done, 1 a grid-wide wait ran out, 4 no valid route; nonzero needs reset(). Synchronises."""
+        return int(self.state[self.status_offset:self.status_offset + 4].view(torch.int32).item())
+
+    def raise_for_status(self) -> None:
+        st = self.status()
+        if st != 0:
+            self.reset()
+            raise DecodeStackError(f"decode layer: {self.STATUS_TEXT.get(st, f'status {st}')}")
+
+    def reset(self):
+        self.state.zero_()
+
+
 class PersistentDecodeStack:
     """One-token decode through L MXFP4 MoE layers in one persistent kernel launch
     (wm_moe_decode_persistent_mxfp4); keeps the per-layer descriptor table and the message
