@@ -214,6 +214,99 @@ class DecodeStack:
                           f"{threads} threads over experts), scaled to the 48-layer stack"}
 
 
+class LayerCalls(DecodeStack):
+    """The C2 stack driven one layer call at a time (wm_moe_layer_decode, whallm_amd.ops.DecodeLayer):
+    each layer's call takes the residual and that layer's router weights (bf16 [512, 2048]) and
+    runs the pre-norm, the router GEMV and top-k, the 10 routed + 1 shared experts and the
+    residual add in one launch, as a runtime calls the MoE between attention blocks
+    (qwen4_exp.py:1146). A step = one token through the 48 layers = 48 calls, replayed from one
+    graph; the line reports the time per layer call."""
+    name = "layer-c2"
+    data = "synthetic (random-init MXFP4 weights, bf16 N(0, 0.05) router rows, N(0,1) residual inputs)"
+
+    def __init__(self, device, layers=48, hidden=2048, experts=512, inter=512, k=10, seed=0):
+        from whallm_amd.ops import DecodeLayer
+        super().__init__(device, layers, hidden, experts, inter, k, 1, seed, impl="layers")
+        g = self.gen
+        self.routers = [(torch.randn(experts, hidden, device=device, generator=g) * 0.05).to(torch.bfloat16)
+                        for _ in range(layers)]
+        self.calls = [DecodeLayer(self.layers[l], self.routers[l], self.shared[l], self.gates[l], k=k)
+                      for l in range(layers)]
+
+    def algorithmic_bytes(self):
+        # per layer: the router rows, 11 expert blobs, r in and out (fp32) and y (bf16)
+        per_layer = self.E * self.H * 2 + (self.K + 1) * self.expert_bytes() + 2 * self.H * 4 + self.H * 2
+        return per_layer * self.L
+
+    def prepare_inputs(self, steps):
+        self.step_embed = torch.randn(steps, self.H, device=self.device, generator=self.gen)
+
+    def _body_at(self, j):
+        r = self.step_embed[j]
+        for call in self.calls:
+            call(r)
+
+    def capture(self):
+        self.graphs = capture_steps(self.device, self._body_at, len(self.step_embed))
+
+    def cpu_baseline(self, budget_s: float):
+        """The numpy oracle on a bounded sample: one token through as many of the layers as the
+        budget allows (pre-norm, router GEMV, top-k, 11 expert FFNs, combine, residual add)."""
+        from oracle import moe as M
+        from oracle import formats as F
+        from whallm_amd import synthetic as S
+        threads = len(os.sched_getaffinity(0))
+        r = self.step_embed[0].cpu().numpy().astype(np.float64)
+
+        def fetch(t: torch.Tensor, e):
+            a = t[e].cpu().numpy()
+            return a.view(np.uint32) if a.dtype == np.int32 else a
+
+        done, elapsed = 0, 0.0
+        with ThreadPoolExecutor(threads) as pool:
+            for l in range(self.L):
+                router = self.routers[l].float().cpu().numpy()
+                g = S.bf16_bits_to_f32(self.gates[l].view(torch.int16).cpu().numpy().view(np.uint16))
+                sh = M.MXFP4Expert(fetch(self.shared[l].gate_up, 0), fetch(self.shared[l].gate_up_scales, 0),
+                                   fetch(self.shared[l].down, 0), fetch(self.shared[l].down_scales, 0))
+                t0 = time.perf_counter()
+                x = F.bf16_round_f32(M.rms_norm(r[None]).astype(np.float32))
+                logits = (router @ x[0])[None].astype(np.float32)
+                idx, w = M.route_softmax_topk(logits, self.K)
+                elapsed += time.perf_counter() - t0
+                ex = {int(e): M.MXFP4Expert(fetch(self.layers[l].gate_up, e), fetch(self.layers[l].gate_up_scales, e),
+                                            fetch(self.layers[l].down, e), fetch(self.layers[l].down_scales, e))
+                      for e in idx[0]}
+                t0 = time.perf_counter()   # compute only: the experts' bytes were fetched above
+                outs = list(pool.map(lambda e: M.expert_ffn(x, ex[e]), [int(e) for e in idx[0]]))
+                shared_out = M.expert_ffn(x, sh)
+                gate = x.astype(np.float64) @ g.astype(np.float64)
+                y = M.combine(np.stack(outs, axis=1), w, shared_out, gate)
+                r = r + F.bf16_round_f32(y[0])
+                elapsed += time.perf_counter() - t0
+                done += 1
+                if elapsed > budget_s:
+                    break
+        per_call_s = elapsed / done
+        return {"value": round(1.0 / (per_call_s * self.L), 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"1 token through {done} of {self.L} layer calls (numpy oracle: norm, router GEMV, top-k, "
+                          f"fp32 dequant-then-matmul experts, {threads} threads over experts), "
+                          f"{per_call_s * 1e3:.2f} ms per layer call, scaled to the 48-layer stack"}
+
+    def check(self):
+        for call in self.calls:
+            call.raise_for_status()
+
+    def kernel_ms(self, launches: int) -> float:
+        return None
+
+    def config(self):
+        c = super().config()
+        c.update(workload="layer-c2: the C2 stack as 48 one-launch layer calls (pre-norm, router GEMV, top-k, "
+                          "experts, residual add), 1 token/step", router="bf16 [512, 2048] per layer")
+        return c
+
+
 class Prefill:
     """C3: one MXFP4 MoE layer at a 16,384-token prefill, Zipf(1.1)-skewed routing.
 
@@ -717,7 +810,7 @@ class ResidentSingleton:
                           f"10 experts), 15 samples x 3 calls, p50 {p50 * 1e3:.2f} ms"}
 
 
-WORKLOADS = {"c2-decode": DecodeStack, "c3-prefill": Prefill, "c4-decode": FP8Layer, "c4-prefill": FP8Layer,
+WORKLOADS = {"c2-decode": DecodeStack, "layer-c2": LayerCalls, "c3-prefill": Prefill, "c4-decode": FP8Layer, "c4-prefill": FP8Layer,
              "c5-verify": MtpVerify, "router-c2": NormRouter, "router-c3": NormRouter, "router-c4": NormRouter,
              "qwen-resident": ResidentSingleton}
 
@@ -768,7 +861,15 @@ def measure(wl, steps: int, warmup: int):
         wl.check()
     ms_per_step = gpu_ms / steps
     value = wl.tokens_per_step() / (ms_per_step / 1e3)
-    if isinstance(wl, DecodeStack):
+    if isinstance(wl, LayerCalls):
+        per_layer_ms = ms_per_step / wl.L
+        achieved = wl.algorithmic_bytes() / (ms_per_step / 1e3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": "moe_layer_kernel<2048, 512> (one launch per layer call), 48 calls per step",
+                    "layer_call_us": round(per_layer_ms * 1e3, 3),
+                    "algorithmic_bytes_per_launch": wl.algorithmic_bytes() // wl.L}
+    elif isinstance(wl, DecodeStack):
         if wl.impl == "persistent":
             k_ms = wl.kernel_ms(steps)
             kernel = "decode_persistent_kernel (one launch = one token through 48 layers)"

@@ -279,6 +279,61 @@ def ffn_dense(x: np.ndarray, wgu: np.ndarray, wd: np.ndarray, limit: float = 0.0
     return (silu(gate) * up).astype(np.float32) @ wd.T
 
 
+def ffn_dense_bf16_steps(x: np.ndarray, wgu: np.ndarray, wd: np.ndarray, up_first: bool = False,
+                         limit: float = 0.0, fp32_swiglu: bool = False, round_act: bool = True,
+                         round_out: bool = True, rnd=bf16_round_f32) -> np.ndarray:
+    """The reference's own arithmetic for one expert on bf16 activations, where every array op
+    returns its inputs' dtype (MLX), so the fp32-accumulated projections come back as bf16:
+    - Qwen (StreamingExperts._one, qwen4_exp.py:815-818, _qmm :774-783): the gate/up
+      projection, sigmoid(gate), gate * sigmoid(gate) (nn.silu), its product with up and the
+      down projection are each rounded to bf16;
+    - DeepSeek V4.1 (``fp32_swiglu``, deepseek_v41/moe.py:36-44, :80-88): the bf16 gate/up
+      projections are cast to fp32 and the clamped SwiGLU runs in fp32; the routed experts'
+      down projection takes that fp32 input (``round_act``/``round_out`` False), the shared
+      expert casts it back to bf16 first and returns bf16.
+    Used to measure how far the reference itself sits from exact arithmetic; ``rnd`` is the
+    rounding (identity gives ffn_dense)."""
+    I = wgu.shape[0] // 2
+    proj = rnd((x.astype(np.float32) @ wgu.T).astype(np.float32))
+    gate, up = (proj[..., I:], proj[..., :I]) if up_first else (proj[..., :I], proj[..., I:])
+    if limit > 0:
+        up = np.clip(up, -limit, limit)
+        gate = np.minimum(gate, limit)
+    if fp32_swiglu:
+        act = (silu(gate.astype(np.float64)) * up).astype(np.float32)
+    else:
+        sig = rnd((1.0 / (1.0 + np.exp(-gate.astype(np.float64)))).astype(np.float32))
+        act = rnd(rnd((gate * sig).astype(np.float32)) * up)
+    if round_act:
+        act = rnd(act)
+    out = (act.astype(np.float32) @ wd.T).astype(np.float32)
+    return rnd(out) if round_out else out
+
+
+def expert_ffn_bf16_steps(x: np.ndarray, e: MXFP4Expert, rnd=bf16_round_f32) -> np.ndarray:
+    """expert_ffn with the reference's bf16 rounding points (ffn_dense_bf16_steps)."""
+    return ffn_dense_bf16_steps(np.asarray(x, np.float32), dequant_mxfp4(e.gate_up, e.gate_up_scales),
+                                dequant_mxfp4(e.down, e.down_scales), rnd=rnd)
+
+
+def combine_bf16_steps(routed: np.ndarray, weights: np.ndarray, shared: np.ndarray | None = None,
+                       shared_gate: np.ndarray | None = None, rnd=bf16_round_f32) -> np.ndarray:
+    """combine with the reference's bf16 rounding points: the scores cast to the rows' dtype,
+    each weighted row rounded, the sum over k accumulated in fp32 and rounded
+    (SparseMoE._combine, qwen4_exp.py:1048-1051); sigmoid(gate logit) and its product with
+    the shared row rounded, then the final add (_gates, :1045). ``routed``/``shared`` are the
+    bf16 rows; ``rnd`` identity gives combine up to float32 rounding."""
+    w = rnd(np.asarray(weights, np.float32))
+    y = rnd((rnd(np.asarray(routed, np.float32) * w[..., None])).astype(np.float32).sum(axis=-2, dtype=np.float32))
+    if shared is not None:
+        s = np.asarray(shared, np.float32)
+        if shared_gate is not None:
+            g = rnd(np.asarray(shared_gate, np.float32).reshape(-1, 1))
+            s = rnd(rnd((1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)) * s)
+        y = rnd(y + s)
+    return y.astype(np.float32)
+
+
 @dataclass
 class FP8Expert:
     """DeepSeek-style FP8 expert: w1 (gate) / w3 (up) [I, H] and w2 [H, I] E4M3 bytes with
@@ -300,6 +355,17 @@ def fp8_expert_ffn(x: np.ndarray, e: FP8Expert, limit: float = 0.0) -> np.ndarra
     w3 = deq(e.w3, e.w3_scales)
     w2 = deq(e.w2, e.w2_scales)
     return ffn_dense(x, np.concatenate([w1, w3], axis=0), w2, limit, up_first=False)
+
+
+def fp8_expert_ffn_bf16_steps(x: np.ndarray, e: FP8Expert, limit: float = 0.0, shared: bool = False,
+                              rnd=bf16_round_f32) -> np.ndarray:
+    """fp8_expert_ffn with the reference's rounding points (ffn_dense_bf16_steps, DeepSeek
+    form): a routed expert returns fp32 rows, the shared expert bf16 (deepseek_v41/moe.py:80-88,
+    :101-104)."""
+    deq = dequant_fp8_e8m0 if e.scale_format == 1 else dequant_fp8_blocks
+    wgu = np.concatenate([deq(e.w1, e.w1_scales), deq(e.w3, e.w3_scales)], axis=0)
+    return ffn_dense_bf16_steps(np.asarray(x, np.float32), wgu, deq(e.w2, e.w2_scales), limit=limit,
+                                fp32_swiglu=True, round_act=shared, round_out=shared, rnd=rnd)
 
 
 def routed_outputs(x: np.ndarray, indices: np.ndarray, experts, ffn=expert_ffn, **kw) -> np.ndarray:

@@ -22,7 +22,6 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import formats as F
 from oracle import moe as M
 from whallm_amd import synthetic as S
 from whallm_amd.ops import DecodeLayer, DecodeStackError
@@ -78,8 +77,11 @@ class Case:
     def check(self, r, r_out, out, what, skip=()):
         r = r.cpu().numpy().astype(np.float64)
         x = out["x_out"].float().cpu().numpy()
-        nw = 1.0 if self.norm_w is None else self.norm_w.float().cpu().numpy().astype(np.float64)
-        want_x = F.bf16_round_f32((M.rms_norm(r[None])[0] * nw).astype(np.float32))
+        nw = None if self.norm_w is None else self.norm_w.float().cpu().numpy()
+        # GroupRMSNorm's fp32 path: normalized * weight, then one rounding to bf16
+        _, want_x, _, _ = M.norm_router(r.astype(np.float32)[None], None, self.router.float().cpu().numpy(),
+                                        None, nw)
+        want_x = want_x[0]
         step = np.abs(want_x).astype(np.float64) * 2.0 ** -7
         diff = np.abs(x.astype(np.float64) - want_x)
         assert np.all(diff <= step + 1e-30) and np.count_nonzero(diff) <= max(2, x.size // 1000), f"{what}: x"

@@ -76,15 +76,22 @@ def test_c3_prefill_full_size(device):
     y6 = wa.moe_mxfp4(x, idx, w, replace(tiled, act_terms="e2m3"), replace(tiled_shared, act_terms="e2m3"), gate)
     rel6 = close(y6.float().cpu().numpy()[sample], want, "C3 sampled tokens, E2M3 activation terms")
     assert rel < rel6, "the bf16-exact terms should be the closer ones"
-    # most of what is left is the bf16 rounding of the per-pair rows, which the reference's
-    # StreamingExperts contract returns as bf16 too (qwen4_exp.py:853-904): against the oracle
-    # with its routed and shared rows rounded to bf16, the bf16-exact path holds 1.5e-3
-    want_rows = M.combine(F.bf16_round_f32(routed), ws, F.bf16_round_f32(sh),
-                          xs.astype(np.float64) @ gate.float().cpu().numpy().astype(np.float64))
+    # reference precision: the reference's own bf16 arithmetic (projections, SwiGLU steps, rows,
+    # weighted rows, sum and shared term each rounded to bf16) sits this far from the same fp32
+    # oracle; the bf16-exact path (rows and output rounded to bf16 once each) sits no farther
+    gl = xs.astype(np.float64) @ gate.float().cpu().numpy().astype(np.float64)
+    ref = M.combine_bf16_steps(M.routed_outputs(xs, ids, ex, ffn=M.expert_ffn_bf16_steps), ws,
+                               M.expert_ffn_bf16_steps(xs, mx_expert(shared, 0)), gl)
+    rel_ref = float(np.linalg.norm(ref - want) / np.linalg.norm(want))
+    print(f"C3 the reference's bf16 arithmetic against the fp32 oracle: rel L2 {rel_ref:.2e}", flush=True)
+    assert rel <= rel_ref
+    # what is left is mostly the bf16 rounding of the per-pair rows (the StreamingExperts
+    # contract returns them as bf16, qwen4_exp.py:853-904) and of the output
+    want_rows = M.combine(F.bf16_round_f32(routed), ws, F.bf16_round_f32(sh), gl)
     got = y.float().cpu().numpy()[sample].astype(np.float64)
     rel_rows = float(np.linalg.norm(got - want_rows) / np.linalg.norm(want_rows))
     print(f"C3 E4M3 against the oracle with bf16 rows: rel L2 {rel_rows:.2e}", flush=True)
-    assert rel_rows <= 1.5e-3
+    assert rel_rows <= 2.5e-3
     # per-pair outputs: complementary masks give the one-call rows bit for bit
     full = wa.experts_mxfp4(x, idx, tiled)
     mask = torch.from_numpy(rng.random((T, K)) < 0.5).to(device)
@@ -159,12 +166,19 @@ def test_c4_prefill_full_size(device):
     y6 = wa.moe_fp8(x, idx, w, replace(tiled, act_terms="e2m3"), replace(tiled_shared, act_terms="e2m3"), None)
     rel6 = close(y6.float().cpu().numpy()[sample], want, "C4 sampled tokens, E2M3 activation terms")
     assert rel < rel6, "the bf16-exact terms should be the closer ones"
+    # reference precision: the V4.1 reference's arithmetic (bf16 projections, fp32 SwiGLU, fp32
+    # routed rows, bf16 shared row and output) against the same fp32 oracle
+    ref = F.bf16_round_f32(M.combine(M.routed_outputs(xs, ids, ex, ffn=M.fp8_expert_ffn_bf16_steps), ws,
+                                     M.fp8_expert_ffn_bf16_steps(xs, fp8_expert(shared, 0), shared=True), None))
+    rel_ref = float(np.linalg.norm(ref - want) / np.linalg.norm(want))
+    print(f"C4 the reference's arithmetic against the fp32 oracle: rel L2 {rel_ref:.2e}", flush=True)
+    assert rel <= rel_ref
     want_rows = M.combine(F.bf16_round_f32(routed), ws, F.bf16_round_f32(M.fp8_expert_ffn(xs, fp8_expert(shared, 0))),
                           None)
     got = y.float().cpu().numpy()[sample].astype(np.float64)
     rel_rows = float(np.linalg.norm(got - want_rows) / np.linalg.norm(want_rows))
     print(f"C4 E4M3 against the oracle with bf16 rows: rel L2 {rel_rows:.2e}", flush=True)
-    assert rel_rows <= 1.5e-3
+    assert rel_rows <= 2.5e-3
 
 
 def test_c5_verify_step(device):

@@ -204,6 +204,41 @@ def test_routed_outputs_keep_router_order_and_combine():
     np.testing.assert_allclose(y[1], 0.5 * e0 + 0.5 * e1 + 2.0, rtol=1e-6)
 
 
+def test_bf16_steps_models_reduce_to_the_fp32_forms_and_round_at_each_step():
+    """The models of the reference's own bf16 arithmetic: with the rounding taken out they are
+    the fp32 forms; a one-value case worked by hand lands on the value each rounding forces."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 64)).astype(np.float32)
+    wgu = (rng.standard_normal((32, 64)) * 0.1).astype(np.float32)
+    wd = (rng.standard_normal((64, 16)) * 0.1).astype(np.float32)
+    ident = lambda v: np.asarray(v, np.float32)  # noqa: E731
+    np.testing.assert_allclose(M.ffn_dense_bf16_steps(x, wgu, wd, rnd=ident), M.ffn_dense(x, wgu, wd), rtol=1e-5,
+                               atol=1e-6)
+    np.testing.assert_allclose(M.ffn_dense_bf16_steps(x, wgu, wd, limit=0.5, fp32_swiglu=True, rnd=ident),
+                               M.ffn_dense(x, wgu, wd, limit=0.5), rtol=1e-5, atol=1e-6)
+    rows = rng.standard_normal((4, 3, 64)).astype(np.float32)
+    w = rng.random((4, 3)).astype(np.float32)
+    sh = rng.standard_normal((4, 64)).astype(np.float32)
+    g = rng.standard_normal(4)
+    np.testing.assert_allclose(M.combine_bf16_steps(rows, w, sh, g, rnd=ident), M.combine(rows, w, sh, g),
+                               rtol=1e-5, atol=1e-6)
+    # Qwen rows and the shared V4.1 row come back in bf16, the routed V4.1 rows in fp32
+    q = M.ffn_dense_bf16_steps(x, wgu, wd)
+    np.testing.assert_array_equal(q, F.bf16_round_f32(q))
+    ds = M.ffn_dense_bf16_steps(x, wgu, wd, fp32_swiglu=True, round_act=False, round_out=False)
+    assert not np.array_equal(ds, F.bf16_round_f32(ds))
+    # by hand: gate 1 + 2^-10 -> bf16 1; sigmoid(1) = 0.731059 -> bf16 187/256; 1 * 187/256 exact;
+    # times up 3 = 2.19140625 -> bf16 (step 2^-6 in [2, 4)) 2.1875; times 1 exact
+    one = M.ffn_dense_bf16_steps(np.ones((1, 1), np.float32), np.array([[1 + 2.0 ** -10], [3.0]], np.float32),
+                                 np.ones((1, 1), np.float32))
+    assert one[0, 0] == 2.1875
+    # combine: w 0.3 -> bf16 0.30078125; times 1 exact; sum exact; sigmoid(0) = 0.5; 0.5 * 3 exact;
+    # 0.30078125 + 1.5 = 1.80078125 -> bf16 (step 2^-7 in [1, 2)) 1.796875 (ties to even: 230.5 -> 230)
+    y = M.combine_bf16_steps(np.ones((1, 1, 1), np.float32), np.array([[0.3]], np.float32),
+                             np.array([[3.0]], np.float32), np.zeros(1))
+    assert y[0, 0] == 1.796875
+
+
 # ----------------------------------------------------------------------------- acceptance
 
 def test_greedy_acceptance_cases():

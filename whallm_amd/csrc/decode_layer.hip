@@ -8,29 +8,39 @@
 //
 // The per-layer path launches norm_router, route, gate_up and down (four dependent kernels,
 // ~31 us a layer at C2); here 256 workgroups of 4 waves, all resident, run the whole layer
-// with two grid-wide exchanges:
+// with two grid-wide exchanges, both in message words (messages.h: value and epoch in one
+// 64-bit word, agent-scope relaxed atomics, no fences or counters):
 //   1. every workgroup normalises r into LDS (x, bf16) and computes its share of the router
-//      logits (one wave per expert row, rows loaded before the norm) and publishes them as
-//      64-bit message words (value | epoch); every workgroup gathers all E logits and routes
-//      redundantly (the wave top-k of route_device.h: same selections as wm_route_softmax_topk
-//      on the same logits);
+//      logits (one wave per expert row, rows loaded before the norm) and publishes them
+//      (fp32 | 32-bit epoch); every workgroup gathers all E logits and routes redundantly (the
+//      wave top-k of route_device.h: same selections as wm_route_softmax_topk on the same
+//      logits);
 //   2. gate_up: the (entry, intermediate index) pairs of the K routed experts and the shared one
-//      are spread evenly over the 1024 waves; each wave streams its gate and up rows (64 lanes
-//      x 16 bytes a row chunk), dots them with x held in registers and writes act; then each
-//      workgroup raises a completion counter (release, agent scope);
+//      are spread evenly over the 1024 waves, an even number to a wave; each wave streams its
+//      gate and up rows (64 lanes x 16 bytes a row chunk), dots them with x held in registers
+//      and publishes act two values to a word (24-bit floats | 16-bit epoch);
 //   3. down: workgroup b owns output rows [H/256 b, H/256 (b + 1)); its waves split the layer's
-//      entries and load their down rows into registers right after routing, before waiting for
-//      the counter; once every workgroup has published act they read it from L2 and reduce
-//      y = sum_k w_k act_k . Wd_k[o] + gate act_s . Wd_s[o] in fp32 (lanes, then waves).
+//      entries and load their down rows into registers right after routing, then gather those
+//      entries' act words into LDS and reduce y = sum_k w_k act_k . Wd_k[o] + gate act_s .
+//      Wd_s[o] in fp32 (lanes, then waves).
 //
 // Exchanges use per-call epochs kept in the state buffer (each workgroup's own word), so the
 // same launch can be replayed from a graph; every wait is bounded and raises the status word.
 #include <cmath>
 #include <string>
 
+#include "messages.h"
 #include "moe_internal.h"
 #include "route_device.h"
 #include "wm_common.h"
+
+// Phase timestamps of the profiling build (phase_trace.h; nothing in the library): slot
+// epoch % 128, points 0 start, 1 x in LDS, 2 logits published, 3 logits gathered (wave 0),
+// 4 routed, 5 gate_up computed and published, 6 act gathered, 7 done; 8 top-k done (wave 0),
+// 9 routes in LDS.
+#ifndef WM_DS_TRACE
+#define WM_DS_TRACE(layer, point)
+#endif
 
 namespace wm {
 namespace dl {
@@ -40,20 +50,18 @@ constexpr int WAVES = 4;
 constexpr int THREADS = 64 * WAVES;
 constexpr int MAX_ENTRIES = 12;          // routed (k <= 11) + shared
 constexpr int MAX_EXPERTS = 1024;        // router rows: 4 per workgroup
-constexpr uint32_t SPIN_LIMIT = 1u << 20;
-constexpr uint32_t ST_STALLED = 1, ST_NO_ROUTE = 4;
+constexpr uint32_t ST_STALLED = MSG_STALLED, ST_NO_ROUTE = 4;
 
-// State buffer (zero-filled once by the caller): logit words, act rows, the completion
-// counter, per-workgroup epochs and the status word.
+// State buffer (zero-filled once by the caller): logit words, act words, per-workgroup
+// epochs and the status word.
 struct Layout {
-  size_t logits, act, counter, epoch, status, total;
+  size_t logits, act, epoch, status, total;
 };
 __host__ __device__ inline Layout layout(int experts, int inter) {
   Layout d;
   size_t at = 0;
   d.logits = at;  at += (size_t)MAX_EXPERTS * 8;
-  d.act = at;     at += (size_t)MAX_ENTRIES * inter * 4;
-  d.counter = at; at += 256;
+  d.act = at;     at += (size_t)MAX_ENTRIES * (inter / 2) * 8;
   d.epoch = at;   at += (size_t)WGS * 4;
   d.status = at;  at += 256;
   d.total = at;
@@ -80,10 +88,6 @@ struct Params {
   uint8_t* state;
 };
 
-__device__ __forceinline__ void put_word(uint64_t* p, uint32_t bits, uint32_t epoch) {
-  __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Row chunks of 1 KB (64 lanes x 16 bytes): a gate_up row of H / 2 bytes spans CH chunks; the
 // lanes past the row's end in the last chunk load nothing.
 template <int H>
@@ -104,6 +108,7 @@ struct DownShape {
 template <int H, int I, int PMAX>
 __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   static_assert(H % WGS == 0 && I % 32 == 0, "fused decode layer shape");
+  static_assert(PMAX % 2 == 0, "act pairs: an even number of (entry, index) pairs a wave");
   constexpr int CH = GateUpShape<H>::CH;
   using DS = DownShape<I>;
   constexpr int RPB = H / WGS;                          // output rows of a workgroup
@@ -117,14 +122,15 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   __shared__ float rw[MAX_ENTRIES];
   __shared__ int rres[MAX_ENTRIES];  // entry resident (its slot map entry, if any, >= 0)
   __shared__ float part[WAVES][RPB];
+  __shared__ __attribute__((aligned(16))) float acts[MAX_ENTRIES][I];  // gathered act rows
+  __shared__ TopkScratch topk;
   __shared__ uint32_t epoch_s;
   __shared__ int fail_s;
 
   const int b = blockIdx.x, tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const Layout L = layout(p.experts, I);
   uint64_t* logit_words = reinterpret_cast<uint64_t*>(p.state + L.logits);
-  float* act = reinterpret_cast<float*>(p.state + L.act);
-  uint32_t* counter = reinterpret_cast<uint32_t*>(p.state + L.counter);
+  uint64_t* act_words = reinterpret_cast<uint64_t*>(p.state + L.act);
   uint32_t* epochs = reinterpret_cast<uint32_t*>(p.state + L.epoch);
   uint32_t* status = reinterpret_cast<uint32_t*>(p.state + L.status);
   const int E = p.experts, K = p.k;
@@ -149,6 +155,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     epoch_s = epochs[b] + 1;
     fail_s = 0;
   }
+  WM_DS_TRACE((epochs[b] + 1) & 127, 0);
 
   // ---- x = bf16(rmsnorm(r) * w) (wm_norm_router's arithmetic): each thread H / 256 values
   static_assert(H % 512 == 0, "router rows of whole 1 KB chunks, an even share of r per thread");
@@ -179,6 +186,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     xs[(VPT * tid + q) / 2] = (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(c) << 16);
   }
   __syncthreads();
+  WM_DS_TRACE(epoch & 127, 1);
   if (b == 0 && p.x_out)
     for (int i = tid; i < H / 2; i += THREADS) reinterpret_cast<uint32_t*>(p.x_out)[i] = xs[i];
 
@@ -196,7 +204,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     }
     a = segment_sum<64>(a);
     if (lane == 0) {
-      put_word(&logit_words[e_row], __float_as_uint(a), epoch);
+      ll_put(&logit_words[e_row], __float_as_uint(a), epoch);
       if (p.logits_out) p.logits_out[e_row] = a;
     }
   }
@@ -216,53 +224,24 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     gate = 1.0f / (1.0f + __expf(-a));
   }
   if (gate_wave && lane == 0) red[4] = gate;
+  WM_DS_TRACE(epoch & 127, 2);
 
   // ---- wave 0 gathers every logit (bounded polls) and routes
   if (wave == 0) {
     bool ok = true;
-    constexpr int PER = MAX_EXPERTS / 64;
-    uint64_t v[PER];
-#pragma unroll
-    for (int m = 0; m < PER; ++m) {
-      const int e = lane + 64 * m;
-      v[m] = e < E ? __hip_atomic_load(&logit_words[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                   : (uint64_t)epoch << 32;
-    }
-    uint32_t spins = 0;
-    while (true) {
-      bool ready = true;
-#pragma unroll
-      for (int m = 0; m < PER; ++m) ready &= (uint32_t)(v[m] >> 32) == epoch;
-      if (__all(ready)) break;
-      if (++spins > SPIN_LIMIT) {
-        __hip_atomic_store(status, ST_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = false;
-        break;
-      }
-      if ((spins & 255) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-        ok = false;
-        break;
-      }
-#pragma unroll
-      for (int m = 0; m < PER; ++m) {
-        const int e = lane + 64 * m;
-        if (e < E && (uint32_t)(v[m] >> 32) != epoch)
-          v[m] = __hip_atomic_load(&logit_words[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < PER; ++m) {
-      const int e = lane + 64 * m;
-      if (e < E) lg[e] = __uint_as_float((uint32_t)v[m]);
-    }
+    ll_gather<MAX_EXPERTS / 64>(logit_words, lane, 64, E, epoch, status, ok,
+                                [&](int e, uint64_t v) { lg[e] = __uint_as_float((uint32_t)v); });
+    ok = __all(ok);
+    WM_DS_TRACE(epoch & 127, 3);
     if (!ok && lane == 0) fail_s = 1;
     if (ok) {
       int sel = 0;
-      float w = 0.0f;
+      float w = 0.0f, full;
       if (E <= 512)
-        wave_route_softmax<8>(lg, E, K, p.norm_topk != 0, lane, sel, w, nullptr);
+        wave_route_softmax<8>(lg, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
       else
-        wave_route_softmax<16>(lg, E, K, p.norm_topk != 0, lane, sel, w, nullptr);
+        wave_route_softmax<16>(lg, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
+      WM_DS_TRACE(epoch & 127, 8);
       // a selection outside [0, E) (fewer than k selectable logits, e.g. NaN) ends the call
       const bool bad = lane < K && (sel < 0 || sel >= E);
       if (__any(bad)) {
@@ -279,6 +258,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     }
   }
   __syncthreads();
+  WM_DS_TRACE(epoch & 127, 9);
   if (p.has_shared && tid == 0) {
     rid[K] = -1;
     rw[K] = p.gate_vec ? red[4] : 1.0f;
@@ -294,6 +274,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     rres[tid] = !t.slots || gload<int32_t>(t.slots + (e < 0 ? 0 : e)) >= 0;
   }
   __syncthreads();
+  WM_DS_TRACE(epoch & 127, 4);
 
   // regions of an entry (the routed expert rid[entry], or the shared one for rid < 0), each
   // field selected on its own so no table is copied to scratch memory
@@ -344,8 +325,8 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   // ---- gate_up: this wave's (entry, intermediate index) pairs
   {
     const int gw = b * WAVES + wave, nwaves = WGS * WAVES;
-    const int total = NE * I;
-    const int per = (total + nwaves - 1) / nwaves;
+    const int total = NE * I;  // even: I is
+    const int per = 2 * ((total + 2 * nwaves - 1) / (2 * nwaves));
     const int n0 = gw * per;
     uint32_t xr[CH][16];  // x values [1024 c + 32 lane, +32) of a row chunk (H / 2 bytes a row)
 #pragma unroll
@@ -360,6 +341,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     }
     uint4 wq[PMAX][2][CH];
     uint32_t sq[PMAX][2][CH];
+    float actv[PMAX];
 #pragma unroll
     for (int u = 0; u < PMAX; ++u) {
       const int n = n0 + u;
@@ -406,45 +388,50 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
         }
         g2[h] = segment_sum<64>(a);
       }
-      if (live && lane == 0) {
-        const float limit = rid[entry] < 0 ? p.shared.swiglu_limit : p.routed.swiglu_limit;
-        float g = g2[0], u2 = g2[1];
-        if (limit > 0.0f) {
-          g = fminf(g, limit);
-          u2 = fminf(fmaxf(u2, -limit), limit);
-        }
-        act[entry * I + i] = rres[entry] ? silu(g) * u2 : 0.0f;
+      const float limit = rid[entry] < 0 ? p.shared.swiglu_limit : p.routed.swiglu_limit;
+      float g = g2[0], u2 = g2[1];  // wave-uniform (segment_sum gives every lane the sum)
+      if (limit > 0.0f) {
+        g = fminf(g, limit);
+        u2 = fminf(fmaxf(u2, -limit), limit);
       }
+      actv[u] = live && rres[entry] ? silu(g) * u2 : 0.0f;
+    }
+    // lane q publishes the word of pairs n0 + 2q and n0 + 2q + 1 (same entry: I is even)
+#pragma unroll
+    for (int q = 0; q < PMAX / 2; ++q) {
+      const int n = n0 + 2 * q;
+      if (lane == q && 2 * q < per && n < total)
+        __hip_atomic_store(&act_words[n / 2], f24_pair_word(actv[2 * q], actv[2 * q + 1], epoch), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  // every wave releases its act stores at agent scope, then one increment of the counter
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (tid == 0) {
-    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // wait until every workgroup of this call has published (bounded)
-    const uint32_t target = epoch * (uint32_t)WGS;
-    uint32_t spins = 0;
-    while ((int32_t)(__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-      if (++spins > SPIN_LIMIT) {
-        __hip_atomic_store(status, ST_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        fail_s = 1;
-        break;
-      }
-      if ((spins & 255) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-        fail_s = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
+
+  WM_DS_TRACE(epoch & 127, 5);
+  // ---- gather the act rows of this wave's down entries (wave, wave + 4, ...) into LDS
+  {
+    constexpr int WPE = I / 2;             // act words an entry
+    constexpr int NPL = (WPE + 63) / 64;   // words a lane gathers per entry
+    bool ok = true;
+    ll_gather_at<EPW * NPL, 16>(
+        act_words,
+        [&](int m) {
+          const int entry = wave + WAVES * (m / NPL), w = (m % NPL) * 64 + lane;
+          return entry < NE && w < WPE ? entry * WPE + w : -1;
+        },
+        epoch, status, ok,
+        [&](int m, uint64_t v) {
+          const int entry = wave + WAVES * (m / NPL), w = (m % NPL) * 64 + lane;
+          acts[entry][2 * w] = f24_to_f32((uint32_t)v & 0xffffffu);
+          acts[entry][2 * w + 1] = f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
+        });
+    if (!ok) fail_s = 1;
   }
   __syncthreads();
+  WM_DS_TRACE(epoch & 127, 6);
   if (fail_s) {
     if (tid == 0) epochs[b] = epoch;
     return;
   }
-  // the other workgroups' act rows: read after an acquire at agent scope (every wave)
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
   // ---- down: y[o] = sum over the wave's entries of w act . Wd[o]
   float acc[STEPS];
@@ -455,7 +442,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     const int entry = wave + WAVES * j;
     const bool live = entry < NE && rres[entry < NE ? entry : 0];  // wave-uniform
     const float w = live ? rw[entry] : 0.0f;
-    const float* arow = act + (live ? entry : 0) * I;
+    const float* arow = acts[live ? entry : 0];
 #pragma unroll
     for (int gp = 0; gp < DS::GPL; ++gp) {
       const int g = gl + gp * DS::LPR;
@@ -504,6 +491,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     if (p.y) p.y[o] = yb;
     if (p.r_out) p.r_out[o] = p.r[o] + bf16_bits_to_f32(yb);
   }
+  WM_DS_TRACE(epoch & 127, 7);
   if (tid == 0) epochs[b] = epoch;
 }
 
@@ -525,7 +513,7 @@ size_t moe_layer_state_size(int experts, int inter) { return dl::layout(experts,
 void moe_layer_fused(const dl::Params& p, int hidden, int inter, hipStream_t s) {
 #define WM_DL_RUN(HH, II)                                                                                     \
   if (hidden == HH && inter == II) {                                                                           \
-    constexpr int PMAX = (dl::MAX_ENTRIES * II + dl::WGS * dl::WAVES - 1) / (dl::WGS * dl::WAVES);            \
+    constexpr int PMAX = 2 * ((dl::MAX_ENTRIES * II + 2 * dl::WGS * dl::WAVES - 1) / (2 * dl::WGS * dl::WAVES)); \
     hipLaunchKernelGGL((dl::moe_layer_kernel<HH, II, PMAX>), dim3(dl::WGS), dim3(dl::THREADS), 0, s, p);       \
     check_launch("moe_layer_kernel");                                                                          \
     return;                                                                                                    \

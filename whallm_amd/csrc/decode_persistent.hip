@@ -36,6 +36,7 @@
 #include <cmath>
 #include <mutex>
 
+#include "messages.h"
 #include "moe_internal.h"
 #include "route_device.h"
 
@@ -50,10 +51,11 @@ constexpr int DS_SLICE = DS_I / DS_X; // 64 intermediate columns per XCD
 constexpr int DS_ROWS = DS_H / DS_J;  // 64 output rows per workgroup
 constexpr int DS_NE_MAX = 12;         // routed + shared experts per layer
 constexpr int DS_KB = DS_H / 128;     // K-steps of a phase-A tile (128 per MFMA)
-constexpr uint32_t DS_SPIN_LIMIT = 1u << 20;
+constexpr uint32_t DS_SPIN_LIMIT = MSG_SPIN_LIMIT;
 // Status word values (0 = healthy): a message wait ran out, the caller's cancel word was
 // set, a selected expert is not resident (its slot map entry is negative).
 constexpr uint32_t DS_STALLED = 1, DS_CANCELLED = 2, DS_NOT_RESIDENT = 3, DS_NO_ROUTE = 4;
+static_assert(DS_STALLED == MSG_STALLED, "the message waits raise DS_STALLED");
 constexpr int DS_MAX_LAYERS = 128;    // layer descriptors kept in LDS
 constexpr int DS_CW = 3;                      // compute waves (prefetch weights and compute)
 constexpr int DS_THREADS = (DS_CW + 1) * 64;  // + one message wave (polls and publishes)
@@ -80,10 +82,6 @@ __host__ __device__ inline DSLayout ds_layout(int layers) {
   return d;
 }
 
-__device__ __forceinline__ void ll_put(uint64_t* p, uint32_t bits, uint32_t epoch) {
-  __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Store of a message word read only by workgroups of the writer's own XCD. With
 // LOCAL, a workgroup-scope store: it is written through the CU's L1 into the XCD's
 // L2, where the readers' agent-scope loads find it, and goes no further (measured
@@ -93,54 +91,6 @@ template <bool LOCAL>
 __device__ __forceinline__ void ll_put_xcd(uint64_t* p, uint64_t word) {
   if constexpr (LOCAL) __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   else __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Reads base[first + m * stride] (m < N, index < limit) with all N loads in flight,
-// re-polls only the words whose top EBITS bits do not equal `epoch` (mod 2^EBITS)
-// yet, then hands each word to store(index, word). Bounded: after DS_SPIN_LIMIT
-// rounds it raises the status word.
-template <int N, int EBITS = 32, typename Store>
-__device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int stride, int limit, uint32_t epoch,
-                                          uint32_t* status, bool& ok, Store store, uint32_t* rounds = nullptr) {
-  const uint32_t want = EBITS == 32 ? epoch : (epoch & ((1u << EBITS) - 1));
-  auto tag = [](uint64_t v) { return (uint32_t)(v >> (64 - EBITS)); };
-  uint64_t v[N];
-#pragma unroll
-  for (int m = 0; m < N; ++m) {
-    int i = first + m * stride;
-    v[m] = i < limit ? __hip_atomic_load(&base[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                     : (uint64_t)want << (64 - EBITS);
-  }
-  uint32_t spins = 0;
-  while (ok) {
-    bool ready = true;
-#pragma unroll
-    for (int m = 0; m < N; ++m) ready &= tag(v[m]) == want;
-    if (ready) break;
-    if (++spins > DS_SPIN_LIMIT) {
-      __hip_atomic_store(status, DS_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = false;
-      break;
-    }
-    if ((spins & 255) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-      ok = false;
-      break;
-    }
-    // no sleep between rounds: each round already waits for its loads to return (a 64- or
-    // 128-clock pause there measured the same or up to 3% slower)
-#pragma unroll
-    for (int m = 0; m < N; ++m) {
-      int i = first + m * stride;
-      if (i < limit && tag(v[m]) != want)
-        v[m] = __hip_atomic_load(&base[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-#pragma unroll
-  for (int m = 0; m < N; ++m) {
-    int i = first + m * stride;
-    if (i < limit) store(i, v[m]);
-  }
-  if (rounds) *rounds = spins;
 }
 
 // Phase timestamps and notes for the profiling build of whallm_amd.phase_trace (both expand
@@ -166,15 +116,6 @@ __device__ __forceinline__ uint32_t ds_bf16_pair(float a, float b) {
 }
 __device__ __forceinline__ uint16_t ds_bf16_bits(float v) { return (uint16_t)ds_bf16_pair(v, 0.0f); }
 __device__ __forceinline__ float bf16_round_f(float v) { return __uint_as_float(ds_bf16_pair(v, 0.0f) << 16); }
-
-// Act values travel two to a message word as 24-bit floats (sign, exponent, 15 mantissa
-// bits, rounded to nearest even) under a 16-bit epoch; phase B uses 12 significant bits
-// of w act (three E4M3 terms), so the shortened mantissa changes nothing it reads.
-__device__ __forceinline__ uint32_t f32_to_f24(float v) {
-  const uint32_t u = __float_as_uint(v);
-  return (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
-}
-__device__ __forceinline__ float f24_to_f32(uint32_t b) { return __uint_as_float(b << 8); }
 
 // ---- E4M3 term splitting -------------------------------------------------------
 // E8M0 exponent s that puts amax / 2^(s-127) in [128, 256) (E4M3's largest finite is
@@ -213,6 +154,7 @@ struct DSShared {
   int r_go;      // layers whose r rows this workgroup has published (the compute waves' r polls wait for it)
   int gate_l;    // layers whose shared gate is in sh.gate (the wave with the shared expert waits for it)
   int failures;
+  TopkScratch topk;  // the prologue's routing (the message wave)
 };
 
 // Per-launch constants of one workgroup.
@@ -740,9 +682,9 @@ __global__ void __launch_bounds__(DS_THREADS, 1) decode_persistent_kernel(
   // routes layer b while every wave copies the descriptors and r_0 and the epoch arrives.
   static_assert(DS_MAX_LAYERS <= DS_WGS, "a workgroup routes one layer at most");
   int sel = 0;
-  float w = 0.0f;
+  float w = 0.0f, full;
   if (msg && b < L)
-    wave_route_softmax<PER_LANE>(logits + (size_t)b * E, E, K, norm_topk != 0, c.lane, sel, w, nullptr);
+    wave_route_softmax<PER_LANE>(logits + (size_t)b * E, E, K, norm_topk != 0, c.lane, sh.topk, sel, w, false, full);
   for (int i = tid; i < L * (int)(sizeof(wm_decode_layer) / 8); i += DS_THREADS)
     reinterpret_cast<uint64_t*>(sh.desc)[i] = reinterpret_cast<const uint64_t*>(layers)[i];
   for (int i = tid; i < DS_H; i += DS_THREADS) sh.r[i] = residual[i];

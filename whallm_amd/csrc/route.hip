@@ -20,12 +20,14 @@ __global__ void __launch_bounds__(256) route_softmax_topk_kernel(const float* __
                                                                 int32_t* __restrict__ indices,
                                                                 float* __restrict__ weights,
                                                                 float* __restrict__ probabilities) {
+  __shared__ TopkScratch topk[4];
   const int t = blockIdx.x * 4 + threadIdx.x / 64, lane = threadIdx.x % 64;
   if (t >= tokens) return;
   const float* row = logits + (int64_t)t * experts;
   int sel;
   float w, full;
-  wave_route_softmax<PER_LANE>(row, experts, k, norm != 0, lane, sel, w, probabilities ? &full : nullptr);
+  wave_route_softmax<PER_LANE>(row, experts, k, norm != 0, lane, topk[threadIdx.x / 64], sel, w,
+                               probabilities != nullptr, full);
   if (lane < k) {
     indices[(int64_t)t * k + lane] = sel;
     weights[(int64_t)t * k + lane] = w;
@@ -57,6 +59,7 @@ __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restri
   constexpr int func = FUNC;
   __shared__ float biased_all[4][64 * PER_LANE];
   __shared__ float score_all[4][64 * PER_LANE];
+  __shared__ TopkScratch topk[4];
   const int wave = threadIdx.x / 64, t = blockIdx.x * 4 + wave, lane = threadIdx.x % 64;
   if (t >= tokens) return;
   float* biased_lds = biased_all[wave];  // each wave's own rows: LDS is shared only within the wave
@@ -142,7 +145,7 @@ __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restri
     }
     int gsel;
     float gval;
-    wave_topk<1>(gs, n_groups, topk_groups, lane, gsel, gval);
+    wave_topk<1>(gs, n_groups, topk_groups, lane, topk[wave], gsel, gval);
     uint64_t keep = 0;
     for (int j = 0; j < topk_groups; ++j) keep |= 1ull << __builtin_amdgcn_readlane(gsel, j);
 #pragma unroll
@@ -153,7 +156,7 @@ __global__ void __launch_bounds__(256) route_scored_kernel(const float* __restri
   }
   int sel;
   float sel_val;
-  wave_topk<PER_LANE>(vals, experts, k, lane, sel, sel_val);
+  wave_topk<PER_LANE>(vals, experts, k, lane, topk[wave], sel, sel_val);
   float mine = lane < k ? score_lds[lane < k ? sel : 0] : 0.0f;
   float sum = segment_sum<64>(mine);
   if (lane < k) {

@@ -2,9 +2,9 @@
 //
 // One wave64 holds a row of up to 64 * PER_LANE scores: expert e in lane e % 64,
 // register e / 64. Every per-lane array is indexed only with unrolled, compile-time
-// indices, so the row stays in registers. Top-k is k rounds of a wave-wide
-// arg-max, value descending and ties to the lower index (the rule fixed for this
-// build; Native/DeepSeekNative/engine.mm:1881 breaks ties the same way).
+// indices, so the row stays in registers. Top-k is a radix select on order-preserving
+// keys, value descending and ties to the lower index (the rule fixed for this build;
+// Native/DeepSeekNative/engine.mm:1881 breaks ties the same way).
 #pragma once
 
 #include <cmath>
@@ -124,85 +124,124 @@ __device__ __forceinline__ float topk_value(uint32_t key) {
   return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
-// Wave-wide max / min; every lane gets the result (rows through DPP, then the four rows'
-// results through scalar registers).
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
-  v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
-  v = max(v, (uint32_t)dpp_i<0x141>((int)v));
-  v = max(v, (uint32_t)dpp_i<0x140>((int)v));
-  const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
-  const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
-  return max(a, b);
-}
-__device__ __forceinline__ int wave_min_i32(int v) {
-  v = min(v, dpp_i<0xB1>(v));
-  v = min(v, dpp_i<0x4E>(v));
-  v = min(v, dpp_i<0x141>(v));
-  v = min(v, dpp_i<0x140>(v));
-  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+// LDS a wave's top-k uses to put its selections in order: the selected (key, expert) pairs
+// in expert order, then in selection order. One per wave that routes at a time.
+struct TopkScratch {
+  uint2 cand[64];
+  uint2 sorted[64];
+};
+
+// Orders this wave's LDS accesses around it (lgkmcnt 0; no hardware barrier: one wave).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// k rounds of arg-max over vals (entries with e >= experts are ignored). Lane j < k
-// receives the j-th selection in (sel, sel_val); a round with nothing left to select
-// gives (0x7fffffff, -inf). Each lane keeps its best remaining entry (the lowest register
-// among equal keys, so the lowest expert id); a round takes the wave max of those keys, and
-// only when several lanes hold it the lowest expert id among them. The winner's lane drops
-// the entry and finds its next best. Values are compared as keys, so -0 and +0 tie and a
-// selected zero is reported as +0.
+// Top-k of vals (entries with e >= experts ignored; k <= 64), value descending and ties to
+// the lower expert id. Lane j < k receives the j-th selection in (sel, sel_val); when fewer
+// than k entries are selectable (NaN never is), the lanes past them get (0x7fffffff, -inf);
+// lanes >= k get (-1, -inf). Values are compared as keys, so -0 and +0 tie and a selected
+// zero is reported as +0.
+//
+// Radix select on the keys, most significant bit first: the k-th largest key K is the
+// largest t with #{key >= t} >= k, found one bit at a time from ballot counts (a v_cmp and a
+// scalar popcount per register, no cross-lane reduction); the walk stops early once
+// #{key >= prefix} == k, when that set is the selection. Otherwise the selection is every key
+// above K plus the lowest-id entries equal to K. The (at most k) selections are compacted
+// into LDS in expert order, each ranks itself against the others, and lane j reads rank j.
 template <int PER_LANE>
-__device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int experts, int k, int lane, int& sel,
-                                          float& sel_val) {
+__device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int experts, int k, int lane,
+                                          TopkScratch& sc, int& sel, float& sel_val) {
   uint32_t key[PER_LANE];
 #pragma unroll
   for (int r = 0; r < PER_LANE; ++r) key[r] = r * 64 + lane < experts ? topk_key(vals[r]) : 0u;
-  uint32_t hk;
-  int hr;
-  auto best = [&]() {
-    hk = key[0];
-    hr = 0;
+  auto count_ge = [&](uint32_t t) {
+    int c = 0;
 #pragma unroll
-    for (int r = 1; r < PER_LANE; ++r) {  // strict: the lowest register wins a tie
-      const bool t = key[r] > hk;
-      hk = t ? key[r] : hk;
-      hr = t ? r : hr;
-    }
+    for (int r = 0; r < PER_LANE; ++r) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[r] >= t));
+    return c;
   };
-  best();
+  uint32_t prefix = 0;
+  bool exact = false;  // #{key >= prefix} == k
+  // kept rolled: a launch starts with a cold instruction cache, and an unrolled walk is
+  // ~30 cache lines of straight-line code fetched one after another
+#pragma nounroll
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = prefix | (1u << bit);
+    const int c = count_ge(cand);
+    if (c >= k) {
+      prefix = cand;
+      if (c == k) {
+        exact = true;
+        break;
+      }
+    }
+  }
+  // selection masks, register by register (expert order: register, then lane)
+  uint64_t m[PER_LANE];
+  if (exact || prefix == 0u) {  // prefix 0: fewer than k selectable keys, take them all
+    const uint32_t lo = exact ? prefix : 1u;
+#pragma unroll
+    for (int r = 0; r < PER_LANE; ++r) m[r] = __builtin_amdgcn_ballot_w64(key[r] >= lo);
+  } else {
+    int need = k - count_ge(prefix + 1u);  // ties at K to take, lowest expert id first
+#pragma unroll
+    for (int r = 0; r < PER_LANE; ++r) {
+      uint64_t eq = __builtin_amdgcn_ballot_w64(key[r] == prefix);
+      uint64_t take = 0;
+      for (; need > 0 && eq != 0; --need) {
+        const uint64_t low = eq & (~eq + 1);
+        take |= low;
+        eq ^= low;
+      }
+      m[r] = __builtin_amdgcn_ballot_w64(key[r] > prefix) | take;
+    }
+  }
+  wave_lds_sync();  // a previous call's reads of sc are done
+  int n = 0;
+#pragma unroll
+  for (int r = 0; r < PER_LANE; ++r) {
+    const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m[r] >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m[r], 0u));
+    if ((m[r] >> lane) & 1ull) sc.cand[pos] = make_uint2(key[r], (uint32_t)(r * 64 + lane));
+    n += __builtin_popcountll(m[r]);
+  }
+  wave_lds_sync();
+  if (lane < n) {
+    const uint2 me = sc.cand[lane];
+    int rank = 0;
+    for (int i0 = 0; i0 < n; i0 += 8) {  // eight candidates a batch, all reads issued together
+      uint2 o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = sc.cand[i0 + j < n ? i0 + j : 0];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        rank += (i0 + j < n) & ((o[j].x > me.x) | ((o[j].x == me.x) & (o[j].y < me.y)));
+    }
+    sc.sorted[rank] = me;
+  }
+  wave_lds_sync();
   sel = -1;
   sel_val = -INFINITY;
-  for (int j = 0; j < k; ++j) {
-    const uint32_t m = wave_max_u32(hk);
-    int ew = 0x7fffffff;
-    float vw = -INFINITY;
-    if (m != 0u) {
-      const uint64_t tied = __builtin_amdgcn_ballot_w64(hk == m);
-      if (__builtin_popcountll(tied) == 1) {
-        const int wl = (int)__builtin_ctzll(tied);
-        ew = __builtin_amdgcn_readlane(hr, wl) * 64 + wl;
-      } else {
-        ew = wave_min_i32(hk == m ? hr * 64 + lane : 0x7fffffff);
-      }
-      vw = topk_value(m);
-      const bool win = lane == (ew & 63);
-      const int rw = ew >> 6;
-#pragma unroll
-      for (int r = 0; r < PER_LANE; ++r) key[r] = (win & (r == rw)) ? 0u : key[r];
-      best();
-    }
-    if (lane == j) {
-      sel = ew;
-      sel_val = vw;
+  if (lane < k) {
+    if (lane < n) {
+      const uint2 s = sc.sorted[lane];
+      sel = (int)s.y;
+      sel_val = topk_value(s.x);
+    } else {
+      sel = 0x7fffffff;
     }
   }
 }
 
 // Softmax routing of one row (logits, `experts` long) by one wave: lane j < k gets the
-// j-th expert and its weight exp(l_j - l_max) / sum (kept logits when `norm`, else all).
+// j-th expert and its weight exp(l_j - l_max) / sum (kept logits when `norm`, else all);
+// with `want_full`, `full` receives the sum over all logits.
 template <int PER_LANE>
 __device__ __forceinline__ void wave_route_softmax(const float* __restrict__ row, int experts, int k, bool norm,
-                                                   int lane, int& sel, float& weight, float* full_denominator) {
+                                                   int lane, TopkScratch& sc, int& sel, float& weight,
+                                                   bool want_full, float& full) {
   float vals[PER_LANE];
 #pragma unroll
   for (int r = 0; r < PER_LANE; ++r) {  // every load in bounds, so all are issued together
@@ -211,20 +250,19 @@ __device__ __forceinline__ void wave_route_softmax(const float* __restrict__ row
     vals[r] = e < experts ? v : -INFINITY;
   }
   float sel_val;
-  wave_topk<PER_LANE>(vals, experts, k, lane, sel, sel_val);
+  wave_topk<PER_LANE>(vals, experts, k, lane, sc, sel, sel_val);
   // the first selection (lane 0) is the row maximum
   float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sel_val), 0));
   float mine = lane < k ? __expf(sel_val - top) : 0.0f;
   float denom;
-  float full = 0.0f;
-  if (!norm || full_denominator) {
+  full = 0.0f;
+  if (!norm || want_full) {
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) {
       int e = r * 64 + lane;
       if (e < experts) full += __expf(vals[r] - top);
     }
     full = segment_sum<64>(full);
-    if (full_denominator) *full_denominator = full;
   }
   denom = norm ? segment_sum<64>(mine) : full;
   weight = mine / denom;

@@ -1,15 +1,19 @@
-"""Per-layer phase trace of the persistent decode kernel (a profiling tool, not on the path).
+"""Phase traces of the decode kernels (a profiling tool, not on the path).
 
-    python -m whallm_amd.phase_trace [--tokens N]
+    python -m whallm_amd.phase_trace [--kernel persistent|layer] [--tokens N]
 
-Builds an instrumented copy of libwhallm_moe.so in whallm_amd/_build/trace/: the kernel source
+Builds an instrumented copy of libwhallm_moe.so in whallm_amd/lib/trace/: the kernel source
 is compiled with phase_trace.h first, which turns the kernel's WM_DS_TRACE / WM_DS_NOTE
 hooks into stores of s_memrealtime (100 MHz, one clock for the whole chip) or of a value
-into a device buffer [workgroup 256][layer 128][wave 4][point 16]; every other object is
-the library's own. It then runs the C2 stack (48 layers x 512 MXFP4 experts, hidden 2048,
-intermediate 512, top-10 + shared, synthetic weights) for a few tokens and prints, per
-phase point, the min / median / max over the 256 workgroups of its time after the layer's
-first S0, averaged over layers 2..45, and the mean re-poll rounds of each gather.
+into a device buffer [workgroup 256][layer or call 128][wave 4][point 16]; every other
+object is the library's own.
+- persistent: runs the C2 stack (48 layers x 512 MXFP4 experts, hidden 2048, intermediate
+  512, top-10 + shared, synthetic weights) for a few tokens and prints, per phase point, the
+  min / median / max over the 256 workgroups of its time after the layer's first S0,
+  averaged over layers 2..45, and the mean re-poll rounds of each gather;
+- layer: runs the one-launch decode layer (wm_moe_layer_decode) at the C2 shape for a few
+  calls and prints, per phase point, the min / median / max over the workgroups of its time
+  after the call's first start, averaged over the calls after the first.
 """
 from __future__ import annotations
 
@@ -23,7 +27,7 @@ import numpy as np
 from . import build as hip_build
 
 PACKAGE = Path(__file__).resolve().parent
-TRACE_DIR = hip_build.BUILD / "trace"
+TRACE_DIR = PACKAGE / "lib" / "trace"   # beside the library, so a prebuilt copy travels with it
 TRACE_LIB = TRACE_DIR / "libwhallm_moe_trace.so"
 HEADER = hip_build.CSRC / "phase_trace.h"
 
@@ -35,19 +39,24 @@ POINTS = [(0, 0, "compute: S0 (r and its norm in LDS)"), (0, 3, "compute: phase 
 NOTES = [(15, "partial"), (7, "r")]
 
 
-def build_traced() -> Path:
-    """Compile the library's decode_persistent.hip with the trace hooks and link it with the
-    library's other objects."""
+SOURCES = {"persistent": "decode_persistent", "layer": "decode_layer"}
+
+
+def build_traced(kernel: str = "persistent") -> Path:
+    """Compile the kernel's source with the trace hooks and link it with the library's other
+    objects."""
     hip_build.build()
     TRACE_DIR.mkdir(parents=True, exist_ok=True)
-    src = hip_build.CSRC / "decode_persistent.hip"
-    obj = TRACE_DIR / "decode_persistent_trace.o"
+    stem = SOURCES[kernel]
+    src = hip_build.CSRC / f"{stem}.hip"
+    obj = hip_build.BUILD / "trace" / f"{stem}_trace.o"
+    obj.parent.mkdir(parents=True, exist_ok=True)
     cmd = [hip_build.hipcc(), *hip_build.HIP_FLAGS, f"-I{hip_build.INCLUDE}", f"-I{hip_build.CSRC}", "-include",
            str(HEADER), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"hipcc failed on the traced kernel:\n{r.stderr}")
-    objs = [str(o) for o in sorted(hip_build.BUILD.glob("*.o")) if o.stem != "decode_persistent"]
+    objs = [str(o) for o in sorted(hip_build.BUILD.glob("*.o")) if o.stem != stem]
     r = subprocess.run([hip_build.hipcc(), f"--offload-arch={hip_build.ARCH}", "-shared", "-fPIC", *objs, str(obj),
                         "-o", str(TRACE_LIB)], capture_output=True, text=True)
     if r.returncode:
@@ -88,6 +97,54 @@ def run(tokens: int = 30, seed: int = 0) -> np.ndarray:
     return trace.cpu().numpy().reshape(256, 128, 4, 16)[:, :L].astype(np.float64) / 100.0
 
 
+LAYER_POINTS = [(0, 0, "start"), (0, 1, "x in LDS"), (0, 2, "logits published"), (0, 3, "logits gathered (wave 0)"),
+                (0, 8, "top-k done (wave 0)"), (0, 9, "routes in LDS"), (0, 4, "routed"), (0, 5, "gate_up published"), (0, 6, "act gathered"), (0, 7, "done")]
+
+
+def run_layer(calls: int = 40, seed: int = 0) -> np.ndarray:
+    """Trace `calls` launches of the decode layer at C2; returns the trace [256, calls, 4, 16]
+    in us (call c at slot (c + 1) % 128)."""
+    import torch
+
+    from . import _lib
+    _lib.LIB_PATH = TRACE_LIB
+    lib = _lib.load()
+    lib.wm_trace_set.argtypes = [ctypes.c_void_p]
+    lib.wm_trace_set.restype = ctypes.c_int
+    from . import synthetic as S
+    from .ops import DecodeLayer
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    H, E, I, K = 2048, 512, 512, 10
+    experts = S.mxfp4_experts_device(E, H, I, dev, g)
+    shared = S.mxfp4_experts_device(1, H, I, dev, g)
+    gate = (torch.randn(H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    router = (torch.randn(E, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    layer = DecodeLayer(experts, router, shared, gate, k=K)
+    trace = torch.zeros(256 * 128 * 4 * 16, dtype=torch.int64, device=dev)
+    if lib.wm_trace_set(ctypes.c_void_p(trace.data_ptr())) != 0:
+        raise RuntimeError("wm_trace_set failed")
+    r = torch.randn(H, device=dev, generator=g)
+    for _ in range(min(calls, 126)):
+        layer(r)
+    torch.cuda.synchronize()
+    layer.raise_for_status()
+    t = trace.cpu().numpy().reshape(256, 128, 4, 16)[:, 1:min(calls, 126) + 1].astype(np.float64) / 100.0
+    return t
+
+
+def summary_layer(t: np.ndarray) -> str:
+    calls = range(1, t.shape[1])
+    out = ["time after the call's first start, us: min / median / max over the 256 workgroups (wave 0), "
+           f"averaged over calls {calls.start}..{calls.stop - 1}"]
+    for w, p, name in LAYER_POINTS:
+        d = np.array([[f(t[:, c, w, p] - t[:, c, 0, 0].min()) for f in (np.min, np.median, np.max)]
+                      for c in calls]).mean(0)
+        out.append(f"  {name:40s} {d[0]:6.2f} {d[1]:6.2f} {d[2]:6.2f}")
+    return "\n".join(out)
+
+
 def summary(t: np.ndarray) -> str:
     layers = range(2, t.shape[1] - 2)
     starts = [t[:, l, 3, 8].min() for l in range(t.shape[1])]
@@ -107,14 +164,17 @@ def summary(t: np.ndarray) -> str:
 
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--tokens", type=int, default=30)
+    ap.add_argument("--kernel", default="persistent", choices=sorted(SOURCES))
+    ap.add_argument("--tokens", type=int, default=30, help="tokens (persistent) or calls (layer)")
     ap.add_argument("--save", default=None, help="also save the raw trace (.npy)")
+    ap.add_argument("--prebuilt", action="store_true", help="use the traced library built beforehand")
     args = ap.parse_args()
-    build_traced()
-    t = run(args.tokens)
+    if not args.prebuilt:
+        build_traced(args.kernel)
+    t = run(args.tokens) if args.kernel == "persistent" else run_layer(args.tokens)
     if args.save:
         np.save(args.save, t)
-    print(summary(t))
+    print(summary(t) if args.kernel == "persistent" else summary_layer(t))
 
 
 if __name__ == "__main__":
