@@ -97,6 +97,29 @@ def test_route_softmax_topk_signed_zero_and_masked_logits(device, experts, k):
         np.testing.assert_allclose(_np(w), want_w, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("experts,k", [(512, 10), (1000, 16), (128, 4)])
+def test_route_topk_candidate_set_edges(device, experts, k):
+    """Rows around the top-k's prefilter (the candidates are the keys at or above the k-th
+    largest per-lane maximum, ranked among themselves when at most 64, else a full radix
+    walk): exactly 64 and 65 copies of the maximum, 100 copies, the k-th value tied 20 times
+    after k - 1 distinct larger ones, and copies placed in one lane (ids 64 apart)."""
+    rng = np.random.default_rng(experts * 7 + k)
+    logits = rng.standard_normal((7, experts)).astype(np.float32)
+    for row, copies in ((0, 64), (1, 65), (2, 100)):
+        logits[row, rng.choice(experts, copies, replace=False)] = 5.0
+    logits[3, :] = rng.standard_normal(experts).astype(np.float32) - 3.0
+    logits[3, :k - 1] = np.arange(k - 1, 0, -1, dtype=np.float32) + 10.0
+    logits[3, rng.choice(np.arange(k, experts), 20, replace=False)] = 5.0
+    logits[4, ::64] = 7.0                    # the maxima share one lane
+    logits[5, 1::64] = logits[5, 1::64] + 9.0
+    logits[6, :] = np.float32(0.5)           # every key equal
+    for norm in (True, False):
+        idx, w = wa.route_softmax_topk(torch.from_numpy(logits).to(device), k, norm)
+        want_idx, want_w = M.route_softmax_topk(logits, k, norm)
+        np.testing.assert_array_equal(_np(idx), want_idx)
+        np.testing.assert_allclose(_np(w), want_w, rtol=2e-6, atol=1e-7)
+
+
 def test_route_softmax_c1_router_linear(device):
     # C1: router weight bf16 N(0, 0.02) [64, 1024], x bf16 N(0, 1) [16, 1024], seed 0.
     rng = np.random.default_rng(0)

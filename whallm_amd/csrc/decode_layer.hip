@@ -9,7 +9,7 @@
 // The per-layer path launches norm_router, route, gate_up and down (four dependent kernels,
 // ~31 us a layer at C2); here 256 workgroups of 4 waves, all resident, run the whole layer
 // with two grid-wide exchanges, both in message words (messages.h: value and epoch in one
-// 64-bit word, agent-scope relaxed atomics, no fences or counters):
+// 64-bit word, agent-scope relaxed atomics, no L2-wide fences):
 //   1. every workgroup normalises r into LDS (x, bf16) and computes its share of the router
 //      logits (one wave per expert row, rows loaded before the norm) and publishes them
 //      (fp32 | 32-bit epoch); every workgroup gathers all E logits and routes redundantly (the
@@ -20,9 +20,11 @@
 //      gate and up rows (64 lanes x 16 bytes a row chunk), dots them with x held in registers
 //      and publishes act two values to a word (24-bit floats | 16-bit epoch);
 //   3. down: workgroup b owns output rows [H/256 b, H/256 (b + 1)); its waves split the layer's
-//      entries and load their down rows into registers right after routing, then gather those
-//      entries' act words into LDS and reduce y = sum_k w_k act_k . Wd_k[o] + gate act_s .
-//      Wd_s[o] in fp32 (lanes, then waves).
+//      entries and load their down rows into registers right after routing. Each workgroup
+//      counts on one of eight counters once its act words are acknowledged; one wave polls the
+//      counters (a few words a round) and only then do the waves gather their entries' act
+//      words into LDS, so no wave polls act words while others still stream weights. Then
+//      y = sum_k w_k act_k . Wd_k[o] + gate act_s . Wd_s[o] in fp32 (lanes, then waves).
 //
 // Exchanges use per-call epochs kept in the state buffer (each workgroup's own word), so the
 // same launch can be replayed from a graph; every wait is bounded and raises the status word.
@@ -34,12 +36,16 @@
 #include "route_device.h"
 #include "wm_common.h"
 
-// Phase timestamps of the profiling build (phase_trace.h; nothing in the library): slot
+// Phase timestamps of the profiling build (phase_trace_lds.h; nothing in the library): slot
 // epoch % 128, points 0 start, 1 x in LDS, 2 logits published, 3 logits gathered (wave 0),
 // 4 routed, 5 gate_up computed and published, 6 act gathered, 7 done; 8 top-k done (wave 0),
-// 9 routes in LDS.
+// 9 routes in LDS, 10 act counters complete, 11 down rows issued, 12 gate_up rows issued,
+// 13 first pair computed.
 #ifndef WM_DS_TRACE
 #define WM_DS_TRACE(layer, point)
+#endif
+#ifndef WM_DS_TRACE_FLUSH
+#define WM_DS_TRACE_FLUSH(layer)
 #endif
 
 namespace wm {
@@ -50,18 +56,20 @@ constexpr int WAVES = 4;
 constexpr int THREADS = 64 * WAVES;
 constexpr int MAX_ENTRIES = 12;          // routed (k <= 11) + shared
 constexpr int MAX_EXPERTS = 1024;        // router rows: 4 per workgroup
+constexpr int GROUPS = 8;                // act completion counters (workgroup b counts on b % 8)
 constexpr uint32_t ST_STALLED = MSG_STALLED, ST_NO_ROUTE = 4;
 
 // State buffer (zero-filled once by the caller): logit words, act words, per-workgroup
 // epochs and the status word.
 struct Layout {
-  size_t logits, act, epoch, status, total;
+  size_t logits, act, counters, epoch, status, total;
 };
 __host__ __device__ inline Layout layout(int experts, int inter) {
   Layout d;
   size_t at = 0;
   d.logits = at;  at += (size_t)MAX_EXPERTS * 8;
   d.act = at;     at += (size_t)MAX_ENTRIES * (inter / 2) * 8;
+  d.counters = at; at += (size_t)GROUPS * 256;
   d.epoch = at;   at += (size_t)WGS * 4;
   d.status = at;  at += 256;
   d.total = at;
@@ -87,6 +95,48 @@ struct Params {
   float* w_out;              // [k] fp32, nullable
   uint8_t* state;
 };
+
+// The fields of an expert table the kernel reads, staged in LDS once per launch, and the
+// regions of each entry of the call: per-entry selections then read LDS, never the kernel
+// arguments through a lane-dependent address (a vector load of the argument segment whose
+// latency each later weight load would wait for).
+struct TableDesc {
+  const uint8_t* gate_up;
+  const uint8_t* gate_up_scales;
+  const uint8_t* down;
+  const uint8_t* down_scales;
+  int64_t gate_up_stride, gate_up_scales_stride, down_stride, down_scales_stride;
+  const int32_t* slots;
+  int up_first;
+  float limit;
+};
+__device__ __forceinline__ void stage_table(TableDesc& d, const wm_mxfp4_experts& t) {
+  d.gate_up = (const uint8_t*)t.gate_up;
+  d.gate_up_scales = (const uint8_t*)t.gate_up_scales;
+  d.down = (const uint8_t*)t.down;
+  d.down_scales = (const uint8_t*)t.down_scales;
+  d.gate_up_stride = t.gate_up_stride;
+  d.gate_up_scales_stride = t.gate_up_scales_stride;
+  d.down_stride = t.down_stride;
+  d.down_scales_stride = t.down_scales_stride;
+  d.slots = t.slots;
+  d.up_first = t.up_first;
+  d.limit = t.swiglu_limit;
+}
+struct EntryRegions {
+  const uint8_t* gate_up;
+  const uint8_t* gate_up_scales;
+  const uint8_t* down;
+  const uint8_t* down_scales;
+  int up_first;
+  float limit;
+};
+
+// Workgroup b's count on its group's act counter: once per call on every path, so the
+// counters stay at epoch * (WGS / GROUPS) after each call.
+__device__ __forceinline__ void count_done(uint32_t* counters, int b) {
+  __hip_atomic_fetch_add(&counters[(b % GROUPS) * 64], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Row chunks of 1 KB (64 lanes x 16 bytes): a gate_up row of H / 2 bytes spans CH chunks; the
 // lanes past the row's end in the last chunk load nothing.
@@ -116,7 +166,6 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   constexpr int EPW = (MAX_ENTRIES + WAVES - 1) / WAVES;  // down entries per wave
 
   __shared__ __attribute__((aligned(16))) uint32_t xs[H / 2];  // x as bf16 pairs
-  __shared__ float lg[MAX_EXPERTS];
   __shared__ float red[2 * WAVES];
   __shared__ int rid[MAX_ENTRIES];
   __shared__ float rw[MAX_ENTRIES];
@@ -124,6 +173,8 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   __shared__ float part[WAVES][RPB];
   __shared__ __attribute__((aligned(16))) float acts[MAX_ENTRIES][I];  // gathered act rows
   __shared__ TopkScratch topk;
+  __shared__ TableDesc tdesc[2];  // 0 routed, 1 shared
+  __shared__ EntryRegions ent[MAX_ENTRIES];
   __shared__ uint32_t epoch_s;
   __shared__ int fail_s;
 
@@ -131,6 +182,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   const Layout L = layout(p.experts, I);
   uint64_t* logit_words = reinterpret_cast<uint64_t*>(p.state + L.logits);
   uint64_t* act_words = reinterpret_cast<uint64_t*>(p.state + L.act);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(p.state + L.counters);  // one per 256 bytes
   uint32_t* epochs = reinterpret_cast<uint32_t*>(p.state + L.epoch);
   uint32_t* status = reinterpret_cast<uint32_t*>(p.state + L.status);
   const int E = p.experts, K = p.k;
@@ -154,7 +206,11 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   if (tid == 0) {
     epoch_s = epochs[b] + 1;
     fail_s = 0;
+    stage_table(tdesc[0], p.routed);
+    stage_table(tdesc[1], p.shared);
   }
+  // this workgroup's residual rows, for the residual add at the end
+  const float r_rows = tid < RPB ? p.r[RPB * b + tid] : 0.0f;
   WM_DS_TRACE((epochs[b] + 1) & 127, 0);
 
   // ---- x = bf16(rmsnorm(r) * w) (wm_norm_router's arithmetic): each thread H / 256 values
@@ -229,18 +285,25 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   // ---- wave 0 gathers every logit (bounded polls) and routes
   if (wave == 0) {
     bool ok = true;
-    ll_gather<MAX_EXPERTS / 64>(logit_words, lane, 64, E, epoch, status, ok,
-                                [&](int e, uint64_t v) { lg[e] = __uint_as_float((uint32_t)v); });
+    constexpr int PER = MAX_EXPERTS / 64;
+    float lv[PER];  // logit of expert lane + 64 m in lv[m], kept in registers
+    ll_gather_at<PER>(
+        logit_words, [&](int m) { return lane + 64 * m < E ? lane + 64 * m : -1; }, epoch, status, ok,
+        [&](int m, uint64_t v) { lv[m] = __uint_as_float((uint32_t)v); });
     ok = __all(ok);
     WM_DS_TRACE(epoch & 127, 3);
     if (!ok && lane == 0) fail_s = 1;
     if (ok) {
       int sel = 0;
       float w = 0.0f, full;
-      if (E <= 512)
-        wave_route_softmax<8>(lg, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
-      else
-        wave_route_softmax<16>(lg, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
+      if (E <= 512) {
+        float v8[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) v8[m] = lv[m];
+        wave_route_softmax_vals<8>(v8, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
+      } else {
+        wave_route_softmax_vals<PER>(lv, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
+      }
       WM_DS_TRACE(epoch & 127, 8);
       // a selection outside [0, E) (fewer than k selectable logits, e.g. NaN) ends the call
       const bool bad = lane < K && (sel < 0 || sel >= E);
@@ -264,37 +327,39 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     rw[K] = p.gate_vec ? red[4] : 1.0f;
   }
   if (fail_s) {  // every workgroup routes the same logits, so all leave here
-    if (tid == 0) epochs[b] = epoch;
+    if (tid == 0) {
+      count_done(counters, b);
+      epochs[b] = epoch;
+    }
     return;
   }
   __syncthreads();
-  if (tid < NE) {  // residency of the entries (a non-resident expert contributes nothing)
+  if (tid < NE) {  // the entries' regions and residency (a non-resident expert contributes nothing)
     const int e = rid[tid];
-    const wm_mxfp4_experts& t = e < 0 ? p.shared : p.routed;
-    rres[tid] = !t.slots || gload<int32_t>(t.slots + (e < 0 ? 0 : e)) >= 0;
+    const TableDesc& t = tdesc[e < 0 ? 1 : 0];
+    int64_t slot = e < 0 ? 0 : e;
+    bool resident = true;
+    if (t.slots) {
+      const int32_t s = gload<int32_t>(t.slots + slot);
+      resident = s >= 0;
+      slot = s < 0 ? 0 : s;  // not resident: slot 0 keeps every address inside the pool
+    }
+    rres[tid] = resident;
+    EntryRegions r;
+    r.gate_up = t.gate_up + slot * t.gate_up_stride;
+    r.gate_up_scales = t.gate_up_scales + slot * t.gate_up_scales_stride;
+    r.down = t.down + slot * t.down_stride;
+    r.down_scales = t.down_scales + slot * t.down_scales_stride;
+    r.up_first = t.up_first;
+    r.limit = t.limit;
+    ent[tid] = r;
   }
   __syncthreads();
   WM_DS_TRACE(epoch & 127, 4);
 
-  // regions of an entry (the routed expert rid[entry], or the shared one for rid < 0), each
-  // field selected on its own so no table is copied to scratch memory
-  auto regions = [&](int entry) {
-    const int e = rid[entry];
-    const bool sh = e < 0;
-    int64_t slot = sh ? 0 : (p.routed.slots ? (int64_t)gload<int32_t>(p.routed.slots + e) : e);
-    slot = slot < 0 ? 0 : slot;  // not resident: the entry is skipped, slot 0 keeps addresses valid
-    ExpertRegions r;
-    r.gate_up = (const uint8_t*)(sh ? p.shared.gate_up : p.routed.gate_up) +
-                slot * (sh ? p.shared.gate_up_stride : p.routed.gate_up_stride);
-    r.gate_up_scales = (const uint8_t*)(sh ? p.shared.gate_up_scales : p.routed.gate_up_scales) +
-                       slot * (sh ? p.shared.gate_up_scales_stride : p.routed.gate_up_scales_stride);
-    r.down = (const uint8_t*)(sh ? p.shared.down : p.routed.down) + slot * (sh ? p.shared.down_stride : p.routed.down_stride);
-    r.down_scales = (const uint8_t*)(sh ? p.shared.down_scales : p.routed.down_scales) +
-                    slot * (sh ? p.shared.down_scales_stride : p.routed.down_scales_stride);
-    return r;
-  };
-
-  // ---- down prefetch: this wave's entries (wave, wave + 4, ...) for the workgroup's rows
+  // ---- down prefetch: this wave's entries (wave, wave + 4, ...) for the workgroup's rows.
+  // Every load is issued (lanes and entries past the end read entry 0's first row, in
+  // bounds) so none waits for another; their values are masked where they are used.
   const int o0 = RPB * b;
   const int slot = lane / DS::LPR, gl = lane % DS::LPR;
   uint4 dq[EPW][STEPS][DS::GPL];
@@ -302,26 +367,22 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
 #pragma unroll
   for (int j = 0; j < EPW; ++j) {
     const int entry = wave + WAVES * j;
-    const bool live = entry < NE && rres[entry < NE ? entry : 0];
-    ExpertRegions r = regions(live ? entry : 0);
+    const EntryRegions& r = ent[entry < NE ? entry : 0];
 #pragma unroll
     for (int st = 0; st < STEPS; ++st) {
       const int row = st * DS::NS + slot;
-      const int o = o0 + row;
+      const int o = o0 + (row < RPB ? row : 0);
 #pragma unroll
       for (int gp = 0; gp < DS::GPL; ++gp) {
         const int g = gl + gp * DS::LPR;
-        if (live && row < RPB && g < DS::G) {
-          dq[j][st][gp] = reinterpret_cast<const uint4*>(r.down + (int64_t)o * (I / 2))[g];
-          ds_[j][st][gp] = r.down_scales[(int64_t)o * DS::G + g];
-        } else {
-          dq[j][st][gp] = make_uint4(0, 0, 0, 0);
-          ds_[j][st][gp] = 127;
-        }
+        const int gc = g < DS::G ? g : 0;
+        dq[j][st][gp] = gload16(r.down + (int64_t)o * (I / 2) + 16 * gc);
+        ds_[j][st][gp] = gload<uint8_t>(r.down_scales + (int64_t)o * DS::G + gc);
       }
     }
   }
 
+  WM_DS_TRACE(epoch & 127, 11);
   // ---- gate_up: this wave's (entry, intermediate index) pairs
   {
     const int gw = b * WAVES + wave, nwaves = WGS * WAVES;
@@ -342,31 +403,30 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     uint4 wq[PMAX][2][CH];
     uint32_t sq[PMAX][2][CH];
     float actv[PMAX];
+    // every load issued (dead pairs read entry 0's row 0, lanes past a row's end its first
+    // chunk); the values are masked where they are used
 #pragma unroll
     for (int u = 0; u < PMAX; ++u) {
       const int n = n0 + u;
       const bool live = u < per && n < total;
       const int entry = live ? n / I : 0, i = live ? n % I : 0;
-      const ExpertRegions r = regions(entry);
-      const int up_first = rid[entry] < 0 ? p.shared.up_first : p.routed.up_first;
+      const EntryRegions& r = ent[entry];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {  // h 0: gate row, 1: up row
-        const int row = (h ^ up_first) ? I + i : i;
+        const int row = (h ^ r.up_first) ? I + i : i;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
           const int off = 1024 * c + 16 * lane;
-          if (live && off < H / 2) {
-            wq[u][h][c] = gload16(r.gate_up + (int64_t)row * (H / 2) + off);
-            sq[u][h][c] = r.gate_up_scales[(int64_t)row * (H / 32) + off / 16];
-          } else {
-            wq[u][h][c] = make_uint4(0, 0, 0, 0);
-            sq[u][h][c] = 127;
-          }
+          const int offc = off < H / 2 ? off : 0;
+          wq[u][h][c] = gload16(r.gate_up + (int64_t)row * (H / 2) + offc);
+          sq[u][h][c] = gload<uint8_t>(r.gate_up_scales + (int64_t)row * (H / 32) + offc / 16);
         }
       }
     }
+    WM_DS_TRACE(epoch & 127, 12);
 #pragma unroll
     for (int u = 0; u < PMAX; ++u) {
+      if (u == 1) WM_DS_TRACE(epoch & 127, 13);
       const int n = n0 + u;
       const bool live = u < per && n < total;  // wave-uniform
       const int entry = live ? n / I : 0, i = live ? n % I : 0;
@@ -377,7 +437,8 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
           const uint32_t words[4] = {wq[u][h][c].x, wq[u][h][c].y, wq[u][h][c].z, wq[u][h][c].w};
-          const float sc = e8m0_scale_operand(sq[u][h][c]);
+          // lanes past the row's end: scale 0 (a 255 byte would be inf, inf x 0 NaN)
+          const float sc = 1024 * c + 16 * lane < H / 2 ? e8m0_scale_operand(sq[u][h][c]) : 0.0f;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             wm_bf16x2 wv[4];
@@ -388,7 +449,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
         }
         g2[h] = segment_sum<64>(a);
       }
-      const float limit = rid[entry] < 0 ? p.shared.swiglu_limit : p.routed.swiglu_limit;
+      const float limit = ent[entry].limit;
       float g = g2[0], u2 = g2[1];  // wave-uniform (segment_sum gives every lane the sum)
       if (limit > 0.0f) {
         g = fminf(g, limit);
@@ -407,7 +468,40 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   }
 
   WM_DS_TRACE(epoch & 127, 5);
-  // ---- gather the act rows of this wave's down entries (wave, wave + 4, ...) into LDS
+  // ---- wait for every workgroup's act words: the barrier waits for this workgroup's stores
+  // to be acknowledged, then it counts once on its group's counter; lanes 0..7 of wave 0
+  // poll the eight counters (a few words a round, with a pause between rounds) instead of
+  // every wave polling its act words while other workgroups still stream their weights
+  __syncthreads();
+  if (tid == 0) count_done(counters, b);
+  if (wave == 0) {
+    bool ok = true;
+    if (lane < GROUPS) {
+      const uint32_t target = epoch * (uint32_t)(WGS / GROUPS);
+      uint32_t spins = 0;
+      while ((int32_t)(__hip_atomic_load(&counters[lane * 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+        if (++spins > MSG_SPIN_LIMIT) {
+          __hip_atomic_store(status, ST_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = false;
+          break;
+        }
+        if ((spins & 63) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    if (!__all(ok) && lane == 0) fail_s = 1;
+  }
+  __syncthreads();
+  WM_DS_TRACE(epoch & 127, 10);
+  if (fail_s) {
+    if (tid == 0) epochs[b] = epoch;
+    return;
+  }
+  // ---- gather the act rows of this wave's down entries (wave, wave + 4, ...) into LDS (every
+  // word still checked against the epoch: the counters order nothing)
   {
     constexpr int WPE = I / 2;             // act words an entry
     constexpr int NPL = (WPE + 63) / 64;   // words a lane gathers per entry
@@ -455,7 +549,9 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
       }
 #pragma unroll
       for (int st = 0; st < STEPS; ++st) {
-        const float scale = e8m0_scale_operand(ds_[j][st][gp]);
+        // rows past the block, groups past the row and dead entries: scale 0
+        const bool valid = live && st * DS::NS + slot < RPB && g < DS::G;
+        const float scale = valid ? e8m0_scale_operand(ds_[j][st][gp]) : 0.0f;
         const uint32_t words[4] = {dq[j][st][gp].x, dq[j][st][gp].y, dq[j][st][gp].z, dq[j][st][gp].w};
         float s = 0.0f;
 #pragma unroll
@@ -489,9 +585,10 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     const float v = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
     const uint16_t yb = f32_to_bf16_bits(v);
     if (p.y) p.y[o] = yb;
-    if (p.r_out) p.r_out[o] = p.r[o] + bf16_bits_to_f32(yb);
+    if (p.r_out) p.r_out[o] = r_rows + bf16_bits_to_f32(yb);
   }
   WM_DS_TRACE(epoch & 127, 7);
+  WM_DS_TRACE_FLUSH(epoch & 127);
   if (tid == 0) epochs[b] = epoch;
 }
 

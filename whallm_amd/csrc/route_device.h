@@ -138,18 +138,46 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The largest t with #{key >= t} >= k over a wave's keys (the k-th largest key, or 0 when
+// fewer than k keys are above 0): a radix walk from the most significant bit, one bit a
+// round from ballot counts (a v_cmp and a scalar popcount per register, no cross-lane
+// reduction). It stops early once #{key >= t} == k (`exact`: that set is the top k).
+template <int N>
+__device__ __forceinline__ uint32_t radix_kth_key(const uint32_t (&key)[N], int k, bool& exact) {
+  uint32_t prefix = 0;
+  exact = false;
+  // kept rolled: the round is short, and an unrolled walk is ~30 cache lines of code
+#pragma nounroll
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = prefix | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int r = 0; r < N; ++r) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[r] >= cand));
+    if (c >= k) {
+      prefix = cand;
+      if (c == k) {
+        exact = true;
+        break;
+      }
+    }
+  }
+  return prefix;
+}
+
 // Top-k of vals (entries with e >= experts ignored; k <= 64), value descending and ties to
 // the lower expert id. Lane j < k receives the j-th selection in (sel, sel_val); when fewer
 // than k entries are selectable (NaN never is), the lanes past them get (0x7fffffff, -inf);
 // lanes >= k get (-1, -inf). Values are compared as keys, so -0 and +0 tie and a selected
 // zero is reported as +0.
 //
-// Radix select on the keys, most significant bit first: the k-th largest key K is the
-// largest t with #{key >= t} >= k, found one bit at a time from ballot counts (a v_cmp and a
-// scalar popcount per register, no cross-lane reduction); the walk stops early once
-// #{key >= prefix} == k, when that set is the selection. Otherwise the selection is every key
-// above K plus the lowest-id entries equal to K. The (at most k) selections are compacted
-// into LDS in expert order, each ranks itself against the others, and lane j reads rank j.
+// A prefilter first: the k-th largest of the 64 per-lane maximum keys, T, has at least k
+// keys at or above it, so the top k are among the keys >= T, and the rank of such a key among
+// them (the keys better than it: larger, or equal with a lower id) is its rank in the row.
+// When there are at most 64 of them (T > 0), they are compacted into LDS in expert order,
+// each ranks itself against the others, and the first k ranks are the selection. Otherwise
+// (heavy ties, or fewer than k selectable keys) a radix walk over every key finds the k-th
+// largest key K, and the selection is every key above K plus the lowest-id entries equal
+// to K, ranked the same way.
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int experts, int k, int lane,
                                           TopkScratch& sc, int& sel, float& sel_val) {
@@ -162,44 +190,38 @@ __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int exp
     for (int r = 0; r < PER_LANE; ++r) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[r] >= t));
     return c;
   };
-  uint32_t prefix = 0;
-  bool exact = false;  // #{key >= prefix} == k
-  // kept rolled: a launch starts with a cold instruction cache, and an unrolled walk is
-  // ~30 cache lines of straight-line code fetched one after another
-#pragma nounroll
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = prefix | (1u << bit);
-    const int c = count_ge(cand);
-    if (c >= k) {
-      prefix = cand;
-      if (c == k) {
-        exact = true;
-        break;
-      }
-    }
-  }
-  // selection masks, register by register (expert order: register, then lane)
-  uint64_t m[PER_LANE];
-  if (exact || prefix == 0u) {  // prefix 0: fewer than k selectable keys, take them all
-    const uint32_t lo = exact ? prefix : 1u;
+  uint64_t m[PER_LANE];  // selection masks, register by register (expert order: register, then lane)
+  bool exact;
+  uint32_t lane_max[1] = {key[0]};
 #pragma unroll
-    for (int r = 0; r < PER_LANE; ++r) m[r] = __builtin_amdgcn_ballot_w64(key[r] >= lo);
+  for (int r = 1; r < PER_LANE; ++r) lane_max[0] = max(lane_max[0], key[r]);
+  const uint32_t t = PER_LANE == 1 ? 0u : radix_kth_key<1>(lane_max, k, exact);
+  if (t != 0u && count_ge(t) <= 64) {
+#pragma unroll
+    for (int r = 0; r < PER_LANE; ++r) m[r] = __builtin_amdgcn_ballot_w64(key[r] >= t);
   } else {
-    int need = k - count_ge(prefix + 1u);  // ties at K to take, lowest expert id first
+    const uint32_t kth = radix_kth_key<PER_LANE>(key, k, exact);
+    if (exact || kth == 0u) {  // kth 0: fewer than k selectable keys, take them all
+      const uint32_t lo = exact ? kth : 1u;
 #pragma unroll
-    for (int r = 0; r < PER_LANE; ++r) {
-      uint64_t eq = __builtin_amdgcn_ballot_w64(key[r] == prefix);
-      uint64_t take = 0;
-      for (; need > 0 && eq != 0; --need) {
-        const uint64_t low = eq & (~eq + 1);
-        take |= low;
-        eq ^= low;
+      for (int r = 0; r < PER_LANE; ++r) m[r] = __builtin_amdgcn_ballot_w64(key[r] >= lo);
+    } else {
+      int need = k - count_ge(kth + 1u);  // ties at K to take, lowest expert id first
+#pragma unroll
+      for (int r = 0; r < PER_LANE; ++r) {
+        uint64_t eq = __builtin_amdgcn_ballot_w64(key[r] == kth);
+        uint64_t take = 0;
+        for (; need > 0 && eq != 0; --need) {
+          const uint64_t low = eq & (~eq + 1);
+          take |= low;
+          eq ^= low;
+        }
+        m[r] = __builtin_amdgcn_ballot_w64(key[r] > kth) | take;
       }
-      m[r] = __builtin_amdgcn_ballot_w64(key[r] > prefix) | take;
     }
   }
   wave_lds_sync();  // a previous call's reads of sc are done
-  int n = 0;
+  int n = 0;        // selected or candidate keys (at most 64)
 #pragma unroll
   for (int r = 0; r < PER_LANE; ++r) {
     const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m[r] >> 32),
@@ -219,36 +241,30 @@ __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int exp
       for (int j = 0; j < 8; ++j)
         rank += (i0 + j < n) & ((o[j].x > me.x) | ((o[j].x == me.x) & (o[j].y < me.y)));
     }
-    sc.sorted[rank] = me;
+    if (rank < k) sc.sorted[rank] = me;
   }
   wave_lds_sync();
   sel = -1;
   sel_val = -INFINITY;
   if (lane < k) {
     if (lane < n) {
-      const uint2 s = sc.sorted[lane];
-      sel = (int)s.y;
-      sel_val = topk_value(s.x);
+      const uint2 s2 = sc.sorted[lane];
+      sel = (int)s2.y;
+      sel_val = topk_value(s2.x);
     } else {
       sel = 0x7fffffff;
     }
   }
 }
 
-// Softmax routing of one row (logits, `experts` long) by one wave: lane j < k gets the
-// j-th expert and its weight exp(l_j - l_max) / sum (kept logits when `norm`, else all);
-// with `want_full`, `full` receives the sum over all logits.
+// Softmax routing of one row held in registers (vals, expert e in lane e % 64, register
+// e / 64; entries past `experts` ignored) by one wave: lane j < k gets the j-th expert and its
+// weight exp(l_j - l_max) / sum (kept logits when `norm`, else all); with `want_full`, `full`
+// receives the sum over all logits.
 template <int PER_LANE>
-__device__ __forceinline__ void wave_route_softmax(const float* __restrict__ row, int experts, int k, bool norm,
-                                                   int lane, TopkScratch& sc, int& sel, float& weight,
-                                                   bool want_full, float& full) {
-  float vals[PER_LANE];
-#pragma unroll
-  for (int r = 0; r < PER_LANE; ++r) {  // every load in bounds, so all are issued together
-    const int e = r * 64 + lane;
-    const float v = row[e < experts ? e : experts - 1];
-    vals[r] = e < experts ? v : -INFINITY;
-  }
+__device__ __forceinline__ void wave_route_softmax_vals(const float (&vals)[PER_LANE], int experts, int k, bool norm,
+                                                        int lane, TopkScratch& sc, int& sel, float& weight,
+                                                        bool want_full, float& full) {
   float sel_val;
   wave_topk<PER_LANE>(vals, experts, k, lane, sc, sel, sel_val);
   // the first selection (lane 0) is the row maximum
@@ -266,6 +282,21 @@ __device__ __forceinline__ void wave_route_softmax(const float* __restrict__ row
   }
   denom = norm ? segment_sum<64>(mine) : full;
   weight = mine / denom;
+}
+
+// The same for a row in memory (`experts` long).
+template <int PER_LANE>
+__device__ __forceinline__ void wave_route_softmax(const float* __restrict__ row, int experts, int k, bool norm,
+                                                   int lane, TopkScratch& sc, int& sel, float& weight,
+                                                   bool want_full, float& full) {
+  float vals[PER_LANE];
+#pragma unroll
+  for (int r = 0; r < PER_LANE; ++r) {  // every load in bounds, so all are issued together
+    const int e = r * 64 + lane;
+    const float v = row[e < experts ? e : experts - 1];
+    vals[r] = e < experts ? v : -INFINITY;
+  }
+  wave_route_softmax_vals<PER_LANE>(vals, experts, k, norm, lane, sc, sel, weight, want_full, full);
 }
 
 }  // namespace wm

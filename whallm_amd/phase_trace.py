@@ -30,6 +30,7 @@ PACKAGE = Path(__file__).resolve().parent
 TRACE_DIR = PACKAGE / "lib" / "trace"   # beside the library, so a prebuilt copy travels with it
 TRACE_LIB = TRACE_DIR / "libwhallm_moe_trace.so"
 HEADER = hip_build.CSRC / "phase_trace.h"
+HEADERS = {"persistent": HEADER, "layer": hip_build.CSRC / "phase_trace_lds.h"}
 
 # point -> (wave role, name); compute waves 0..2, message wave 3
 POINTS = [(0, 0, "compute: S0 (r and its norm in LDS)"), (0, 3, "compute: phase A done, own act gathered"),
@@ -52,7 +53,7 @@ def build_traced(kernel: str = "persistent") -> Path:
     obj = hip_build.BUILD / "trace" / f"{stem}_trace.o"
     obj.parent.mkdir(parents=True, exist_ok=True)
     cmd = [hip_build.hipcc(), *hip_build.HIP_FLAGS, f"-I{hip_build.INCLUDE}", f"-I{hip_build.CSRC}", "-include",
-           str(HEADER), "-c", str(src), "-o", str(obj)]
+           str(HEADERS[kernel]), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"hipcc failed on the traced kernel:\n{r.stderr}")
@@ -98,7 +99,10 @@ def run(tokens: int = 30, seed: int = 0) -> np.ndarray:
 
 
 LAYER_POINTS = [(0, 0, "start"), (0, 1, "x in LDS"), (0, 2, "logits published"), (0, 3, "logits gathered (wave 0)"),
-                (0, 8, "top-k done (wave 0)"), (0, 9, "routes in LDS"), (0, 4, "routed"), (0, 5, "gate_up published"), (0, 6, "act gathered"), (0, 7, "done")]
+                (0, 8, "top-k done (wave 0)"), (0, 9, "routes in LDS"), (0, 4, "routed"),
+                (0, 11, "down rows issued"), (0, 12, "gate_up rows issued"), (0, 13, "first pair computed"),
+                (0, 5, "gate_up published"), (0, 10, "act counters complete"), (0, 6, "act gathered"),
+                (0, 7, "done")]
 
 
 def run_layer(calls: int = 40, seed: int = 0) -> np.ndarray:
