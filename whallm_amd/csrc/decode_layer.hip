@@ -171,7 +171,9 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   __shared__ float rw[MAX_ENTRIES];
   __shared__ int rres[MAX_ENTRIES];  // entry resident (its slot map entry, if any, >= 0)
   __shared__ float part[WAVES][RPB];
-  __shared__ __attribute__((aligned(16))) float acts[MAX_ENTRIES][I];  // gathered act rows
+  // gathered act rows, value v of a row at 4 (G q + g) + c for v = 32 g + 4 q + c (G = I / 32):
+  // the down lanes reading four values of groups g, g + 1, ... hit consecutive 16 bytes
+  __shared__ __attribute__((aligned(16))) float acts[MAX_ENTRIES][I];
   __shared__ TopkScratch topk;
   __shared__ TableDesc tdesc[2];  // 0 routed, 1 shared
   __shared__ EntryRegions ent[MAX_ENTRIES];
@@ -515,8 +517,9 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
         epoch, status, ok,
         [&](int m, uint64_t v) {
           const int entry = wave + WAVES * (m / NPL), w = (m % NPL) * 64 + lane;
-          acts[entry][2 * w] = f24_to_f32((uint32_t)v & 0xffffffu);
-          acts[entry][2 * w + 1] = f24_to_f32((uint32_t)(v >> 24) & 0xffffffu);
+          const int v0 = 2 * w, at = 4 * (DS::G * ((v0 % 32) / 4) + v0 / 32) + v0 % 4;
+          *reinterpret_cast<float2*>(&acts[entry][at]) =
+              make_float2(f24_to_f32((uint32_t)v & 0xffffffu), f24_to_f32((uint32_t)(v >> 24) & 0xffffffu));
         });
     if (!ok) fail_s = 1;
   }
@@ -543,7 +546,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
       float av[32];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const float4 v = live && g < DS::G ? *reinterpret_cast<const float4*>(arow + 32 * g + 4 * q)
+        const float4 v = live && g < DS::G ? *reinterpret_cast<const float4*>(arow + 4 * (DS::G * q + g))
                                             : make_float4(0, 0, 0, 0);
         av[4 * q] = v.x; av[4 * q + 1] = v.y; av[4 * q + 2] = v.z; av[4 * q + 3] = v.w;
       }
