@@ -470,11 +470,12 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   }
 
   WM_DS_TRACE(epoch & 127, 5);
-  // ---- wait for every workgroup's act words: the barrier waits for this workgroup's stores
-  // to be acknowledged, then it counts once on its group's counter; lanes 0..7 of wave 0
-  // poll the eight counters (a few words a round, with a pause between rounds) instead of
-  // every wave polling its act words while other workgroups still stream their weights
-  __syncthreads();
+  // ---- wait for every workgroup's act words: once its four waves have issued their act
+  // stores, the workgroup counts once on its group's counter (without waiting for the stores'
+  // acknowledgements: the gather below checks every word's epoch and re-polls a late one);
+  // lanes 0..7 of wave 0 poll the eight counters (a few words a round, with a pause between
+  // rounds) instead of every wave polling its act words while others still stream weights
+  ds_barrier();
   if (tid == 0) count_done(counters, b);
   if (wave == 0) {
     bool ok = true;
@@ -496,7 +497,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     }
     if (!__all(ok) && lane == 0) fail_s = 1;
   }
-  __syncthreads();
+  ds_barrier();
   WM_DS_TRACE(epoch & 127, 10);
   if (fail_s) {
     if (tid == 0) epochs[b] = epoch;

@@ -167,17 +167,6 @@ struct DSCtx {
   float* trace;           // nullable: [L][H] fp32 residual after each layer
 };
 
-// Workgroup barrier over LDS only: this wave's LDS operations complete (lgkmcnt 0),
-// then the hardware barrier. __syncthreads() would also wait for this wave's global
-// stores, and since the vector memory counter drains in order, for every weight load
-// still in flight; message words need no such wait (their epochs order them).
-__device__ __forceinline__ void ds_barrier() {
-  __asm__ __volatile__("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
-  __builtin_amdgcn_s_barrier();
-  __asm__ __volatile__("" ::: "memory");
-}
-
 // x = bf16(r * inv) as two E4M3 terms: hi = e4m3(x / 2^(s-127)), lo = e4m3((x / 2^(s-127)
 // - hi) * 16) under scale 2^(s-131). Thread t handles x[8t .. 8t+7]; x[n] with
 // n = 128 kb + 64 h + 16 g + e sits at byte 16 h + e of xb[term][kb][g], the order in

@@ -74,6 +74,17 @@ __device__ __forceinline__ void ll_gather(const uint64_t* base, int first, int s
       [&](int m, uint64_t v) { store(first + m * stride, v); }, rounds);
 }
 
+// Workgroup barrier over LDS only: this wave's LDS operations complete (lgkmcnt 0),
+// then the hardware barrier. __syncthreads() would also wait for this wave's global
+// stores, and since the vector memory counter drains in order, for every weight load
+// still in flight; message words need no such wait (their epochs order them).
+__device__ __forceinline__ void ds_barrier() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
+
 // Values that travel two to a message word as 24-bit floats (sign, exponent, 15 mantissa
 // bits, rounded to nearest even) under a 16-bit epoch: bits 0-23 the first value, 24-47
 // the second, 48-63 the epoch.
