@@ -33,17 +33,21 @@ namespace wm {
 
 // ---------------------------------------------------------------------------------
 // The input row of a decode token as bf16 pairs: lane group `g` needs values
-// [32 g, 32 g + 32) = 16 words; groups at or past `groups` (the row's end) read as zero.
+// [32 g, 32 g + 32) = 16 words; groups at or past `groups` (the row's end) read group 0.
+// Every load in these kernels is issued unconditionally at an in-bounds address and its
+// value masked where it is used (a scale of 0 for groups past a row's end): a load under a
+// condition makes the compiler wait for it where the branches join, before the loads after
+// it are issued.
 template <int GPL, int LPR>
 __device__ __forceinline__ void load_x_groups(const uint32_t* __restrict__ xrow, int gl, int groups,
                                               uint32_t (&xw)[GPL][16]) {
 #pragma unroll
   for (int gp = 0; gp < GPL; ++gp) {
     const int g = gl + gp * LPR;
-    const uint4* src = reinterpret_cast<const uint4*>(xrow + g * 16);
+    const uint4* src = reinterpret_cast<const uint4*>(xrow + (g < groups ? g : 0) * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      uint4 v = g < groups ? src[q] : make_uint4(0, 0, 0, 0);
+      uint4 v = src[q];
       xw[gp][4 * q + 0] = v.x;
       xw[gp][4 * q + 1] = v.y;
       xw[gp][4 * q + 2] = v.z;
@@ -134,23 +138,23 @@ __global__ void __launch_bounds__(256) gate_up_act_kernel(const uint16_t* __rest
     int row = ((q & 1) ^ up_first) ? I + i : i;
 #pragma unroll
     for (int gp = 0; gp < GPL; ++gp) {
-      int g = gl + gp * LPR;
-      if (ok && g < G) {
-        wq[st][gp] = reinterpret_cast<const uint4*>(r.gate_up + (int64_t)row * (H / 2))[g];
-        sb[st][gp] = r.gate_up_scales[(int64_t)row * G + g];
-      } else {
-        wq[st][gp] = make_uint4(0, 0, 0, 0);
-        sb[st][gp] = 127;
-      }
+      const int g = gl + gp * LPR;
+      const int rc = ok ? row : 0, gc = g < G ? g : 0;
+      wq[st][gp] = gload16(r.gate_up + (int64_t)rc * (H / 2) + 16 * gc);
+      sb[st][gp] = gload<uint8_t>(r.gate_up_scales + (int64_t)rc * G + gc);
     }
   }
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
+    const int q = st * NS + slot;
+    const bool ok = q < ROWS && i_base + q / 2 < I;
     float acc = 0.0f;
 #pragma unroll
-    for (int gp = 0; gp < GPL; ++gp) acc = group_dot_bf16(wq[st][gp], e8m0_scale_operand(sb[st][gp]), xw[gp], acc);
+    for (int gp = 0; gp < GPL; ++gp) {
+      const bool valid = ok && gl + gp * LPR < G;
+      acc = group_dot_bf16(wq[st][gp], valid ? e8m0_scale_operand(sb[st][gp]) : 0.0f, xw[gp], acc);
+    }
     acc = segment_sum<LPR>(acc);
-    int q = st * NS + slot;
     if (gl == 0 && q < ROWS) sums[wave][q] = acc;
   }
   __syncthreads();
@@ -260,29 +264,26 @@ __global__ void __launch_bounds__(256) down_kernel(const float* __restrict__ act
       int o = o_base + st * NS + slot;
 #pragma unroll
       for (int gp = 0; gp < GPL; ++gp) {
-        int g = gl + gp * LPR;
-        if (o < H && g < G) {
-          wq[st][gp] = reinterpret_cast<const uint4*>(r.down + (int64_t)o * (I / 2))[g];
-          sb[st][gp] = r.down_scales[(int64_t)o * G + g];
-        } else {
-          wq[st][gp] = make_uint4(0, 0, 0, 0);
-          sb[st][gp] = 127;
-        }
+        const int g = gl + gp * LPR;
+        const int oc = o < H ? o : 0, gc = g < G ? g : 0;
+        wq[st][gp] = gload16(r.down + (int64_t)oc * (I / 2) + 16 * gc);
+        sb[st][gp] = gload<uint8_t>(r.down_scales + (int64_t)oc * G + gc);
       }
     }
 #pragma unroll
     for (int gp = 0; gp < GPL; ++gp) {
       const int g = gl + gp * LPR;
-      const float4* a4 = reinterpret_cast<const float4*>(arow + g * 32);
+      const float4* a4 = reinterpret_cast<const float4*>(arow + (g < G ? g : 0) * 32);
       float av[32];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        float4 v = g < G ? a4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 v = a4[q];
         av[4 * q] = v.x; av[4 * q + 1] = v.y; av[4 * q + 2] = v.z; av[4 * q + 3] = v.w;
       }
 #pragma unroll
       for (int st = 0; st < STEPS; ++st) {
-        float scale = e8m0_scale_operand(sb[st][gp]);
+        const bool valid = o_base + st * NS + slot < H && g < G;
+        float scale = valid ? e8m0_scale_operand(sb[st][gp]) : 0.0f;
         uint32_t words[4] = {wq[st][gp].x, wq[st][gp].y, wq[st][gp].z, wq[st][gp].w};
         float s = 0.0f;
 #pragma unroll

@@ -84,11 +84,20 @@ constexpr int FP8_RPW = 2;  // intermediate rows per wave (4 weight rows: gate a
 // The block scale of the 16 columns [c, c + 16) of row `row` in a matrix of `cols` columns:
 // SF 0, fp32 128 x 128 blocks; SF 1, E8M0 32 x 32 blocks (2^(b - 127)).
 template <int SF>
-__device__ __forceinline__ float fp8_block_scale(const uint8_t* scales, int row, int cols, int c) {
+__device__ __forceinline__ uint32_t fp8_block_scale_raw(const uint8_t* scales, int row, int cols, int c) {
   if constexpr (SF == 0)
-    return gload<float>(reinterpret_cast<const float*>(scales) + (int64_t)(row / 128) * (cols / 128) + c / 128);
+    return gload<uint32_t>(reinterpret_cast<const uint32_t*>(scales) + (int64_t)(row / 128) * (cols / 128) + c / 128);
   else
-    return e8m0_value(gload<uint8_t>(scales + (int64_t)(row / 32) * (cols / 32) + c / 32));
+    return gload<uint8_t>(scales + (int64_t)(row / 32) * (cols / 32) + c / 32);
+}
+// The scale value of a raw load, converted where it is used (a conversion next to the load
+// would make the lane wait for it before issuing the loads after it).
+template <int SF>
+__device__ __forceinline__ float fp8_scale_value(uint32_t raw) {
+  if constexpr (SF == 0)
+    return __uint_as_float(raw);
+  else
+    return e8m0_value(raw);
 }
 
 // grid: (I / (4 * FP8_RPW), pairs). CPL = ceil(H / 1024) chunks of 16 bytes per lane per row;
@@ -117,41 +126,54 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
   const float limit = tab.swiglu_limit;
   const int i_base = blockIdx.x * 4 * FP8_RPW + wave * FP8_RPW;
 
-  uint32_t xw[CPL][8];  // x[1024 m + 16 lane .. +15] as bf16 pairs (zero past the row)
+  // Every load is issued unconditionally (lanes past a row's end read its first chunk) and
+  // masked where it is used, through the chunk's scale: a load under a condition makes the
+  // compiler wait for it where the branches join, before the loads after it are issued.
+  uint32_t xw[CPL][8];  // x[1024 m + 16 lane .. +15] as bf16 pairs
+  float inm[CPL];       // 1 for chunks inside the row, 0 past its end
   const uint16_t* xr = x + (int64_t)t * H;
 #pragma unroll
   for (int m = 0; m < CPL; ++m) {
-    const bool in = 1024 * m + 16 * lane < H;
-    const uint4* src = reinterpret_cast<const uint4*>(xr + 1024 * m + 16 * lane);
-    const uint4 a = in ? src[0] : make_uint4(0, 0, 0, 0), b = in ? src[1] : make_uint4(0, 0, 0, 0);
+    const int off = 1024 * m + 16 * lane;
+    inm[m] = off < H ? 1.0f : 0.0f;
+    const uint4* src = reinterpret_cast<const uint4*>(xr + (off < H ? off : 0));
+    const uint4 a = src[0], b = src[1];
     xw[m][0] = a.x; xw[m][1] = a.y; xw[m][2] = a.z; xw[m][3] = a.w;
     xw[m][4] = b.x; xw[m][5] = b.y; xw[m][6] = b.z; xw[m][7] = b.w;
   }
   // a wave's FP8_RPW gate rows lie in one scale block (128 or 32 rows), and so do its up rows
   static_assert(32 % (4 * FP8_RPW) == 0, "a workgroup's rows lie in one scale block");
   uint4 wq[ROWS][CPL];
-  float sc[2][CPL];
+  uint32_t sc[2][CPL];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int row = (h ^ up_first) ? I + i_base : i_base;  // h 0: gate, 1: up
 #pragma unroll
-    for (int m = 0; m < CPL; ++m)
-      sc[h][m] = 1024 * m + 16 * lane < H ? fp8_block_scale<SF>(r.w13_scales, row, H, 1024 * m + 16 * lane) : 0.0f;
+    for (int m = 0; m < CPL; ++m) {
+      const int off = 1024 * m + 16 * lane;
+      sc[h][m] = fp8_block_scale_raw<SF>(r.w13_scales, row, H, off < H ? off : 0);
+    }
   }
 #pragma unroll
   for (int q = 0; q < ROWS; ++q) {
     const int i = i_base + q / 2;  // I is a multiple of 8: always in range
     const int row = ((q & 1) ^ up_first) ? I + i : i;  // q even: gate, odd: up
 #pragma unroll
-    for (int m = 0; m < CPL; ++m)
-      wq[q][m] = 1024 * m + 16 * lane < H ? gload16_nt(r.w13 + (int64_t)row * H + 1024 * m + 16 * lane)
-                                           : make_uint4(0, 0, 0, 0);
+    for (int m = 0; m < CPL; ++m) {
+      const int off = 1024 * m + 16 * lane;
+      wq[q][m] = gload16_nt(r.w13 + (int64_t)row * H + (off < H ? off : 0));
+    }
   }
+  float scv[2][CPL];  // the scales' values, masked (every load above is issued by now)
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) scv[h][m] = fp8_scale_value<SF>(sc[h][m]) * inm[m];
 #pragma unroll
   for (int q = 0; q < ROWS; ++q) {
     float acc = 0.0f;
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) acc = fmaf(sc[q & 1][m], e4m3x16_dot_bf16(wq[q][m], xw[m], 0.0f), acc);
+    for (int m = 0; m < CPL; ++m) acc = fmaf(scv[q & 1][m], e4m3x16_dot_bf16(wq[q][m], xw[m], 0.0f), acc);
     acc = segment_sum<64>(acc);
     if (lane == 0) sums[wave][q] = acc;
   }
@@ -240,15 +262,18 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
       if (!resident) break;  // zero row
       w = 1.0f;
     }
+    // loads unconditional (lanes past the row read its first chunk), masked through the scale
     float av[CPL][16];
+    float inm[CPL];
     const float* arow = act + (int64_t)p * I;
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
-      const bool in = 1024 * m + 16 * lane < I;
-      const float4* a4 = reinterpret_cast<const float4*>(arow + 1024 * m + 16 * lane);
+      const int off = 1024 * m + 16 * lane;
+      inm[m] = off < I ? 1.0f : 0.0f;
+      const float4* a4 = reinterpret_cast<const float4*>(arow + (off < I ? off : 0));
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float4 v = in ? a4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 v = a4[q];
         av[m][4 * q] = v.x; av[m][4 * q + 1] = v.y; av[m][4 * q + 2] = v.z; av[m][4 * q + 3] = v.w;
       }
     }
@@ -256,23 +281,29 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
     // (128 or 32 rows): one scale load per 1024-wide chunk
     static_assert(32 % FP8_OPW == 0, "a step's rows lie in one scale block");
     uint4 wq[FP8_OPW][CPL];
-    float sc[CPL];
+    uint32_t sc[CPL];
 #pragma unroll
-    for (int m = 0; m < CPL; ++m)
-      sc[m] = 1024 * m + 16 * lane < I ? fp8_block_scale<SF>(r.w2_scales, o_base, I, 1024 * m + 16 * lane) : 0.0f;
+    for (int m = 0; m < CPL; ++m) {
+      const int off = 1024 * m + 16 * lane;
+      sc[m] = fp8_block_scale_raw<SF>(r.w2_scales, o_base, I, off < I ? off : 0);
+    }
 #pragma unroll
     for (int q = 0; q < FP8_OPW; ++q) {
       const int o = o_base + q;  // H is a multiple of 32: always in range
 #pragma unroll
-      for (int m = 0; m < CPL; ++m)
-        wq[q][m] = 1024 * m + 16 * lane < I ? gload16_nt(r.w2 + (int64_t)o * I + 1024 * m + 16 * lane)
-                                             : make_uint4(0, 0, 0, 0);
+      for (int m = 0; m < CPL; ++m) {
+        const int off = 1024 * m + 16 * lane;
+        wq[q][m] = gload16_nt(r.w2 + (int64_t)o * I + (off < I ? off : 0));
+      }
     }
+    float scv[CPL];  // the scales' values, masked (every load above is issued by now)
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) scv[m] = fp8_scale_value<SF>(sc[m]) * inm[m];
 #pragma unroll
     for (int q = 0; q < FP8_OPW; ++q) {
       float s = 0.0f;
 #pragma unroll
-      for (int m = 0; m < CPL; ++m) s = fmaf(sc[m], e4m3x16_dot_f32(wq[q][m], av[m], 0.0f), s);
+      for (int m = 0; m < CPL; ++m) s = fmaf(scv[m], e4m3x16_dot_f32(wq[q][m], av[m], 0.0f), s);
       acc[q] = fmaf(w, s, acc[q]);
     }
   }

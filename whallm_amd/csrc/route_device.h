@@ -3,8 +3,9 @@
 // One wave64 holds a row of up to 64 * PER_LANE scores: expert e in lane e % 64,
 // register e / 64. Every per-lane array is indexed only with unrolled, compile-time
 // indices, so the row stays in registers. Top-k is a radix select on order-preserving
-// keys, value descending and ties to the lower index (the rule fixed for this build;
-// Native/DeepSeekNative/engine.mm:1881 breaks ties the same way).
+// keys (k rounds of a wave arg-max when a lane holds one value), value descending and ties
+// to the lower index (the rule fixed for this build; Native/DeepSeekNative/engine.mm:1881
+// breaks ties the same way).
 #pragma once
 
 #include <cmath>
@@ -138,6 +139,81 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Wave-wide max / min; every lane gets the result (rows through DPP, then the four rows'
+// results through scalar registers).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x141>((int)v));
+  v = max(v, (uint32_t)dpp_i<0x140>((int)v));
+  const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+  const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+  return max(a, b);
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  v = min(v, dpp_i<0xB1>(v));
+  v = min(v, dpp_i<0x4E>(v));
+  v = min(v, dpp_i<0x141>(v));
+  v = min(v, dpp_i<0x140>(v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Top-k by k rounds of arg-max over vals (entries with e >= experts are ignored), for short
+// selections (one value a lane: the group stage of the scored router). Lane j < k receives
+// the j-th selection in (sel, sel_val); a round with nothing left to select gives
+// (0x7fffffff, -inf). Each lane keeps its best remaining entry (the lowest register
+// among equal keys, so the lowest expert id); a round takes the wave max of those keys, and
+// only when several lanes hold it the lowest expert id among them. The winner's lane drops
+// the entry and finds its next best. Values are compared as keys, so -0 and +0 tie and a
+// selected zero is reported as +0.
+template <int PER_LANE>
+__device__ __forceinline__ void wave_topk_rounds(const float (&vals)[PER_LANE], int experts, int k, int lane,
+                                                 int& sel, float& sel_val) {
+  uint32_t key[PER_LANE];
+#pragma unroll
+  for (int r = 0; r < PER_LANE; ++r) key[r] = r * 64 + lane < experts ? topk_key(vals[r]) : 0u;
+  uint32_t hk;
+  int hr;
+  auto best = [&]() {
+    hk = key[0];
+    hr = 0;
+#pragma unroll
+    for (int r = 1; r < PER_LANE; ++r) {  // strict: the lowest register wins a tie
+      const bool t = key[r] > hk;
+      hk = t ? key[r] : hk;
+      hr = t ? r : hr;
+    }
+  };
+  best();
+  sel = -1;
+  sel_val = -INFINITY;
+  for (int j = 0; j < k; ++j) {
+    const uint32_t m = wave_max_u32(hk);
+    int ew = 0x7fffffff;
+    float vw = -INFINITY;
+    if (m != 0u) {
+      const uint64_t tied = __builtin_amdgcn_ballot_w64(hk == m);
+      if (__builtin_popcountll(tied) == 1) {
+        const int wl = (int)__builtin_ctzll(tied);
+        ew = __builtin_amdgcn_readlane(hr, wl) * 64 + wl;
+      } else {
+        ew = wave_min_i32(hk == m ? hr * 64 + lane : 0x7fffffff);
+      }
+      vw = topk_value(m);
+      const bool win = lane == (ew & 63);
+      const int rw = ew >> 6;
+#pragma unroll
+      for (int r = 0; r < PER_LANE; ++r) key[r] = (win & (r == rw)) ? 0u : key[r];
+      best();
+    }
+    if (lane == j) {
+      sel = ew;
+      sel_val = vw;
+    }
+  }
+}
+
 // The largest t with #{key >= t} >= k over a wave's keys (the k-th largest key, or 0 when
 // fewer than k keys are above 0): a radix walk from the most significant bit, one bit a
 // round from ballot counts (a v_cmp and a scalar popcount per register, no cross-lane
@@ -181,6 +257,10 @@ __device__ __forceinline__ uint32_t radix_kth_key(const uint32_t (&key)[N], int 
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int experts, int k, int lane,
                                           TopkScratch& sc, int& sel, float& sel_val) {
+  if constexpr (PER_LANE == 1) {  // a few values a wave: k rounds are the shorter chain
+    wave_topk_rounds<1>(vals, experts, k, lane, sel, sel_val);
+    return;
+  }
   uint32_t key[PER_LANE];
 #pragma unroll
   for (int r = 0; r < PER_LANE; ++r) key[r] = r * 64 + lane < experts ? topk_key(vals[r]) : 0u;
@@ -195,7 +275,7 @@ __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int exp
   uint32_t lane_max[1] = {key[0]};
 #pragma unroll
   for (int r = 1; r < PER_LANE; ++r) lane_max[0] = max(lane_max[0], key[r]);
-  const uint32_t t = PER_LANE == 1 ? 0u : radix_kth_key<1>(lane_max, k, exact);
+  const uint32_t t = radix_kth_key<1>(lane_max, k, exact);
   if (t != 0u && count_ge(t) <= 64) {
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) m[r] = __builtin_amdgcn_ballot_w64(key[r] >= t);
