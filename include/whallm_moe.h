@@ -456,15 +456,20 @@ WM_EXPORT int wm_slot_cache_acquire_ready(wm_slot_cache* cache, int32_t file, co
  * are submitted before the reads, Native/QwenNative/engine.mm:2204-2230): plans `experts`
  * (the call's unique ids, host), then on compute_stream splits the device pair ids
  * indices [pairs] into ready_indices (the id where its expert is ready, else -1) and
- * late_indices (the rest; device arrays of `pairs`), with no host -> device copy, and only
- * then enqueues the fills, which wait for the split but not for later work on
- * compute_stream. A slot filled by an earlier acquire_ready that no wait_fills has covered
- * is not ready. Run the ready pairs at once, wm_slot_cache_wait_fills, then the late pairs.
- * At most 1024 experts. */
+ * late_indices (the rest; device arrays of `pairs`), with no host -> device copy. The copy
+ * stream is ordered after compute_stream's work up to the split, but the fills are held
+ * back until wm_slot_cache_start_fills, so the caller enqueues its ready-pair kernels
+ * first and they run under the copies; any later call on the cache (wm_slot_cache_wait_fills
+ * included) starts held fills the caller has not started. A slot filled by an earlier
+ * acquire_ready that no wait_fills has covered is not ready. Order: acquire_split, the
+ * ready pairs, start_fills, wait_fills, the late pairs. At most 1024 experts. */
 WM_EXPORT int wm_slot_cache_acquire_split(wm_slot_cache* cache, int32_t file, const int32_t* experts, int32_t n,
                                           int32_t* out_slots, int32_t* out_ready, const int32_t* indices,
                                           int64_t pairs, int32_t* ready_indices, int32_t* late_indices,
                                           void* compute_stream);
+/* Enqueues the fills wm_slot_cache_acquire_split held back (no-op when there are none): the
+ * reads the native engine submits after the ready pairs (engine.mm:2225-2231). */
+WM_EXPORT int wm_slot_cache_start_fills(wm_slot_cache* cache);
 WM_EXPORT int wm_slot_cache_wait_fills(wm_slot_cache* cache, void* compute_stream);
 /* Route mode (ExpertCache with eviction_policy "route", expert_cache.py:1131-1181): scores
  * [files * experts] (host, the route policy's retention scores) and quotas [files] (its

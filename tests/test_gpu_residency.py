@@ -162,22 +162,24 @@ def test_cached_first_at_decode_shape(device):
     # The C2 expert shape (H 2048, I 512; 1.6 MB blobs). After a warm-up call, 20 of the
     # step's experts are copied in from pinned host memory while the pairs of the resident
     # ones run (the rocprofv3 trace of this test shows those kernels inside the copy's span).
+    # Three fresh caches in a row, so the last round runs with every code path warm.
     files, experts, slots, K, tokens = 1, 48, 40, 10, 16
     arrays, pool = make_pool(files, experts, 21, hidden=2048, inter=512)
-    cache = SlotCache(slots, 2048, 512, files, experts, pool, device)
     table = S.experts_to_device(arrays[0], device)
-    cache.acquire(0, list(range(12)))
     rng = np.random.default_rng(22)
-    for lo, hi in ((12, 18), (18, 38)):    # 6 missing experts, then 20
-        idx = np.stack([np.concatenate([rng.choice(12, 4, replace=False), rng.choice(np.arange(lo, hi), K - 4,
-                                                                                    replace=False)])
-                        for _ in range(tokens)]).astype(np.int32)
-        x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, 2048)), device)
-        it = torch.from_numpy(idx).to(device)
-        got = cache.experts_ready_first(0, x, it)
-        want = wa.experts_mxfp4(x, it, table)
-        assert torch.equal(got.cpu(), want.cpu())
-    assert cache.stats()["copies"] > 0
+    for _ in range(3):
+        cache = SlotCache(slots, 2048, 512, files, experts, pool, device)
+        cache.acquire(0, list(range(12)))
+        for lo, hi in ((12, 18), (18, 38)):    # 6 missing experts, then 20
+            idx = np.stack([np.concatenate([rng.choice(12, 4, replace=False),
+                                            rng.choice(np.arange(lo, hi), K - 4, replace=False)])
+                            for _ in range(tokens)]).astype(np.int32)
+            x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, 2048)), device)
+            it = torch.from_numpy(idx).to(device)
+            got = cache.experts_ready_first(0, x, it)
+            want = wa.experts_mxfp4(x, it, table)
+            assert torch.equal(got.cpu(), want.cpu())
+        assert cache.stats()["copies"] > 0
 
 
 def test_hits_on_slots_still_filling_wait_for_their_fills(device):
@@ -214,6 +216,30 @@ def test_hits_on_slots_still_filling_wait_for_their_fills(device):
     assert all(ready)
     ready_idx, late_idx, any_late = cache.acquire_split(0, it)
     assert not any_late and torch.equal(ready_idx, it) and bool((late_idx == -1).all())
+
+
+def test_held_fills_start_on_the_next_cache_call(device):
+    """acquire_split holds its copies back until start_fills; a caller that goes on to another
+    cache call (here acquire, or wait_fills) without start_fills still gets them: the kernel
+    after that call reads the filled weights (equal to the all-resident table bit for bit)."""
+    files, experts, slots, K, tokens = 1, 48, 40, 10, 4
+    arrays, pool = make_pool(files, experts, 33, hidden=2048, inter=512)
+    table = S.experts_to_device(arrays[0], device)
+    rng = np.random.default_rng(34)
+    idx = np.stack([rng.choice(experts, K, replace=False) for _ in range(tokens)]).astype(np.int32)
+    it = torch.from_numpy(idx).to(device)
+    x = S.bf16_bits_to_tensor(S.bf16_normal_np(rng, (tokens, 2048)), device)
+    want = wa.experts_mxfp4(x, it, table)
+    for follow in ("acquire", "wait_fills"):
+        cache = SlotCache(slots, 2048, 512, files, experts, pool, device)
+        _, _, any_late = cache.acquire_split(0, it)
+        assert any_late
+        if follow == "acquire":
+            cache.acquire(0, sorted(set(idx.reshape(-1).tolist())))   # every expert a hit of the held plan
+        else:
+            cache.wait_fills()
+        got = wa.experts_mxfp4(x, it, cache.table(0))
+        assert torch.equal(got.cpu(), want.cpu()), follow
 
 
 def test_combine_pairs_matches_oracle(device):

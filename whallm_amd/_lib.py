@@ -105,6 +105,7 @@ _SIGNATURES = {
     "wm_slot_cache_route_record_read": (c_int, [_P, c_int32, ctypes.c_double]),
     "wm_slot_cache_route_rebalance": (c_int, [_P]),
     "wm_slot_cache_route_state": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "wm_slot_cache_start_fills": (c_int, [_P]),
     "wm_slot_cache_wait_fills": (c_int, [_P, _P]),
     "wm_slot_cache_set_route": (c_int, [_P, _P, _P]),
     "wm_slot_cache_read_layer": (c_int, [_P, c_int32, _P, _P]),

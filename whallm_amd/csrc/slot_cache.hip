@@ -135,6 +135,10 @@ class SlotCache {
   }
   ~SlotCache() {
     if (!dev_) return;
+    try {
+      start_fills();  // held copies were planned: the map and the arena already count them
+    } catch (...) {
+    }
     (void)hipStreamSynchronize(copy_);
     for (auto& kv : layer_done_) (void)hipEventDestroy(kv.second);
     for (auto& st : staging_) {
@@ -174,6 +178,7 @@ class SlotCache {
   }
 
   void plan(int file, const int32_t* experts, int n, int32_t* out_slots, int32_t* filled) {
+    start_fills();
     std::vector<int32_t> own(filled ? 0 : n);
     const Request r{file, experts, n, out_slots, filled ? filled : own.data()};
     plan_requests(&r, 1);
@@ -182,6 +187,7 @@ class SlotCache {
   // In route mode with the cache's own policy, the requested ids count as routes of `file`
   // in the current phase (ExpertCache.get_many observes them, expert_cache.py:1483).
   void acquire(int file, const int32_t* experts, int n, int32_t* out_slots, hipStream_t compute) {
+    start_fills();
     observe_request(file, experts, n);
     std::vector<int32_t> filled(n);
     const Request r{file, experts, n, out_slots, filled.data()};
@@ -190,6 +196,7 @@ class SlotCache {
 
   // One plan over several files (see plan_requests), filled like acquire.
   void acquire_files(const Request* req, int m, hipStream_t compute) {
+    start_fills();
     for (int r = 0; r < m; ++r) observe_request(req[r].file, req[r].experts, req[r].n);
     fill(req, m, compute, nullptr, true);
   }
@@ -203,6 +210,7 @@ class SlotCache {
   // for yet is not ready either: its copy may still be in flight.
   void acquire_ready(int file, const int32_t* experts, int n, int32_t* out_slots, int32_t* out_ready,
                      hipStream_t compute) {
+    start_fills();
     observe_request(file, experts, n);
     std::vector<int32_t> filled(n);
     const Request r{file, experts, n, out_slots, filled.data()};
@@ -210,6 +218,7 @@ class SlotCache {
     for (int i = 0; i < n; ++i) out_ready[i] = filled[i] || fill_pending_[out_slots[i]] ? 0 : 1;
   }
   void wait_fills(hipStream_t compute) {
+    start_fills();
     if (pending_) check(hipStreamWaitEvent(compute, fills_done_, 0), "hipStreamWaitEvent");
     pending_ = false;
     std::fill(fill_pending_.begin(), fill_pending_.end(), 0);
@@ -217,12 +226,15 @@ class SlotCache {
 
   // acquire_ready for one call's pairs, in the reference's order (engine.mm:2204-2230: the
   // ready pairs are submitted, then the reads): plan, then split the pairs on compute_stream
-  // into ready and late index arrays (split_ready_kernel, the ready set passed by value),
-  // then enqueue the fills, whose copy stream waits for the split but not for work enqueued
-  // after this call, so the caller's ready-pair kernels overlap the fills.
+  // into ready and late index arrays (split_ready_kernel, the ready set passed by value).
+  // The copy stream is made to wait for compute_stream's work up to here (which may still
+  // read the slots being refilled), but the copies themselves are held back until
+  // start_fills, so the caller can enqueue its ready-pair kernels first; any later call on
+  // the cache (wait_fills included) starts them if the caller has not.
   void acquire_split(int file, const int32_t* experts, int n, int32_t* out_slots, int32_t* out_ready,
                      const int32_t* indices, int64_t pairs, int32_t* ready_idx, int32_t* late_idx,
                      hipStream_t compute) {
+    start_fills();
     if (!dev_) throw std::runtime_error("slot cache: opened without device memory (policy only)");
     if (experts_ > 1024) throw std::runtime_error("slot cache: the pair split takes at most 1024 experts");
     observe_request(file, experts, n);
@@ -239,7 +251,22 @@ class SlotCache {
                          pairs, bits, experts_, ready_idx, late_idx);
       check(hipGetLastError(), "split_ready_kernel");
     }
-    enqueue_fills(&r, 1, compute, nullptr, false);
+    if (!any_filled(&r, 1)) return;
+    order_copies_after(compute);
+    held_file_ = file;
+    held_experts_.assign(experts, experts + n);
+    held_slots_.assign(out_slots, out_slots + n);
+    held_filled_ = filled;
+    held_ = true;
+  }
+
+  // The copies acquire_split held back, now (a no-op when there are none).
+  void start_fills() {
+    if (!held_) return;
+    held_ = false;
+    const Request r{held_file_, held_experts_.data(), (int)held_experts_.size(), held_slots_.data(),
+                    held_filled_.data()};
+    issue_fills(&r, 1, nullptr);
   }
 
   // plan + copies of the misses: from the host pool, or with `layer` (a device copy of the
@@ -250,20 +277,33 @@ class SlotCache {
     plan_requests(req, m);
     enqueue_fills(req, m, compute, layer, compute_waits);
   }
+  static bool any_filled(const Request* req, int m) {
+    for (int r = 0; r < m; ++r)
+      for (int i = 0; i < req[r].n; ++i)
+        if (req[r].filled[i]) return true;
+    return false;
+  }
+  // The slots being refilled may still be read by work already on the compute stream: the
+  // copy stream's next work waits for it.
+  void order_copies_after(hipStream_t compute) {
+    check(hipEventRecord(compute_done_, compute), "hipEventRecord");
+    check(hipStreamWaitEvent(copy_, compute_done_, 0), "hipStreamWaitEvent");
+  }
   // The copies of a planned request's misses (fill after plan_requests).
   void enqueue_fills(const Request* req, int m, hipStream_t compute, const uint8_t* layer, bool compute_waits) {
-    bool any = false;
-    for (int r = 0; r < m; ++r)
-      for (int i = 0; i < req[r].n; ++i) any |= req[r].filled[i] != 0;
-    if (!any) {
+    if (!any_filled(req, m)) {
       // every expert is a hit, but some may be slots an earlier acquire_ready is still
       // filling: work enqueued after an acquire must see them resident
       if (compute_waits) wait_fills(compute);
       return;
     }
-    // the slots being refilled may still be read by work already on the compute stream
-    check(hipEventRecord(compute_done_, compute), "hipEventRecord");
-    check(hipStreamWaitEvent(copy_, compute_done_, 0), "hipStreamWaitEvent");
+    order_copies_after(compute);
+    issue_fills(req, m, layer);
+    if (compute_waits) wait_fills(compute);
+  }
+  // The copies themselves (the copy stream already ordered after the compute stream), the
+  // expert -> slot map refresh, and the event wait_fills waits for.
+  void issue_fills(const Request* req, int m, const uint8_t* layer) {
     // one copy per run of misses whose experts and slots both follow each other (free slots
     // are handed out in order, so a cold cache fills consecutive experts in one copy)
     for (int r = 0; r < m; ++r) {
@@ -307,7 +347,6 @@ class SlotCache {
     }
     check(hipEventRecord(fills_done_, copy_), "hipEventRecord");
     pending_ = true;
-    if (compute_waits) wait_fills(compute);
   }
 
   // ExpertArena::seed (engine.mm:1664-1678): plan `experts` of `file` (least valuable
@@ -315,6 +354,7 @@ class SlotCache {
   // whole file.
   void seed(int file, const int32_t* experts, const int32_t* uses, int n, const uint8_t* layer, int32_t* out_slots,
             hipStream_t compute) {
+    start_fills();
     std::vector<int32_t> filled(n);
     const Request r{file, experts, n, out_slots, filled.data()};
     fill(&r, 1, compute, layer, true);
@@ -328,6 +368,7 @@ class SlotCache {
   // at most kMaxReadBatch blobs per copy (the reference's prefill expert reads,
   // expert_cache.py:2062-2085 with contiguous_batches, qwen_streaming_policy.py:7-20).
   void read_layer(int file, uint8_t* dst, hipStream_t compute, const int32_t* experts = nullptr, int n = -1) {
+    start_fills();
     if (!dev_) throw std::runtime_error("slot cache: opened without device memory (policy only)");
     if (file < 0 || file >= files_) throw std::runtime_error("slot cache: file out of range");
     if (!dst) throw std::runtime_error("slot cache: null layer buffer");
@@ -372,6 +413,7 @@ class SlotCache {
   // Returns how many were seeded; out_experts / out_slots (host, >= limit entries) list them.
   int seed_tail(int file, const int32_t* routes, int64_t rows, int k, int limit, const uint8_t* layer,
                 int32_t* out_experts, int32_t* out_slots, hipStream_t compute) {
+    start_fills();
     if (!dev_) throw std::runtime_error("slot cache: opened without device memory (policy only)");
     if (file < 0 || file >= files_) throw std::runtime_error("slot cache: file out of range");
     if (rows < 0 || k < 1 || limit < 0 || experts_ > 1024)
@@ -588,7 +630,11 @@ class SlotCache {
   hipStream_t copy_ = nullptr;
   hipEvent_t compute_done_ = nullptr, fills_done_ = nullptr;
   bool pending_ = false;  // fills recorded in fills_done_ that no compute stream waited for yet
-  std::vector<uint8_t> fill_pending_;  // per slot: filled by a copy behind pending_
+  std::vector<uint8_t> fill_pending_;
+  // the copies of the last acquire_split, held back until start_fills
+  bool held_ = false;
+  int held_file_ = 0;
+  std::vector<int32_t> held_experts_, held_slots_, held_filled_;  // per slot: filled by a copy behind pending_
   std::vector<Staging> staging_;
   unsigned next_staging_ = 0;
 };
@@ -687,6 +733,11 @@ WM_EXPORT int wm_slot_cache_acquire_split(wm_slot_cache* cache, int32_t file, co
     c->acquire_split(file, experts, n, out_slots, out_ready, indices, pairs, ready_indices, late_indices,
                      as_stream(compute_stream));
   });
+}
+
+WM_EXPORT int wm_slot_cache_start_fills(wm_slot_cache* cache) {
+  SlotCache* c = reinterpret_cast<SlotCache*>(cache);
+  return with_cache(c, [&] { c->start_fills(); });
 }
 
 WM_EXPORT int wm_slot_cache_wait_fills(wm_slot_cache* cache, void* compute_stream) {

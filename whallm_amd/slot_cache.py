@@ -125,6 +125,11 @@ class SlotCache:
                                                             ctypes.c_void_p(stream)), "acquire_ready")
         return out.tolist(), [bool(r) for r in ready]
 
+    def start_fills(self) -> None:
+        """Enqueues the fills ``acquire_split`` held back (engine.mm:2225-2231: the reads
+        follow the ready pairs' submission)."""
+        self._check(_lib.load().wm_slot_cache_start_fills(self._handle), "start_fills")
+
     def wait_fills(self) -> None:
         """The current stream waits for the fills of earlier ``acquire_ready`` calls."""
         stream = torch.cuda.current_stream(self.device).cuda_stream
@@ -132,10 +137,11 @@ class SlotCache:
 
     def acquire_split(self, file: int, indices: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, bool]:
         """The cached-first acquire of one call's pairs (engine.mm:2204-2230): plans the call's
-        experts, splits ``indices`` on the current stream into (ready, late) id tensors (-1
-        where a pair is in the other set) with no host -> device copy, then enqueues the fills.
-        Returns (ready, late, whether any pair is late). ``indices`` is read on the host, as the
-        reference's acquire is."""
+        experts and splits ``indices`` on the current stream into (ready, late) id tensors (-1
+        where a pair is in the other set) with no host -> device copy. The fills are held back
+        until ``start_fills`` (or the next call on the cache), so the ready pairs can be
+        enqueued first. Returns (ready, late, whether any pair is late). ``indices`` is read on
+        the host, as the reference's acquire is."""
         if self.device is None:
             raise SlotCacheError("policy-only cache")
         idx = indices.to(torch.int32).contiguous()
@@ -160,6 +166,7 @@ class SlotCache:
         ready_idx, late_idx, any_late = self.acquire_split(file, indices)
         table = self.table(file)
         out = experts_mxfp4(x, ready_idx, table, out=out)
+        self.start_fills()
         self.wait_fills()
         if any_late:
             experts_mxfp4(x, late_idx, table, out=out)
