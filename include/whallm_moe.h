@@ -570,6 +570,29 @@ WM_EXPORT int wm_mtp_verify_rejection(const float* target_logp, const float* dra
                                       int32_t n_drafts, int32_t vocab, const float* uniforms, int32_t* out,
                                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- the verify round's expert half -----------------------------------------
+ * The MTP verify call (wq_verify, Native/QwenNative/capi.h:57; native_qwen.py:604-656) for
+ * the part on the expert path: `rows` = the accepted token and its drafts (<= 16) through
+ * `layers` FP8 MoE layers, each x_l = bf16(rmsnorm(r_l)), scored routing of
+ * router_logits[l] (fp32 [layers, rows, experts]) with biases[l] (host array of device
+ * pointers, nullable; nullable entries), r_{l+1} = r_l + MoE_l(x_l) (tables[l] and
+ * shared[l]: host arrays of `layers` tables; shared nullable), then logits = x_L . head^T
+ * (bf16 head [vocab, hidden] -> fp32 [rows, vocab]) and greedy acceptance of drafts[rows - 1]
+ * into acceptance (device int32[2] = accepted drafts, next token; Sampler.verify,
+ * native_qwen.py:389-408). residual (fp32 [rows, hidden]) is updated in place. Routing:
+ * k, func (0 softmax, 1 sigmoid, 2 sqrt-softplus), route_scale, n_groups / topk_groups as
+ * wm_route_scored with normalised weights. Every step is a library kernel on `stream`, with
+ * no host synchronisation. The attention half, the KV state, wq_draft and wq_commit are not
+ * on the expert path. workspace: wm_verify_step_fp8_workspace_size bytes, 256-byte aligned. */
+WM_EXPORT size_t wm_verify_step_fp8_workspace_size(int32_t rows, int32_t k, int32_t vocab,
+                                                   const wm_fp8_experts* experts);
+WM_EXPORT int wm_verify_step_fp8(int32_t layers, const float* router_logits, float* residual, int32_t rows,
+                                 const wm_fp8_experts* tables, const wm_fp8_experts* shared,
+                                 const float* const* biases, int32_t k, int32_t func, float route_scale,
+                                 int32_t n_groups, int32_t topk_groups, float eps, const void* head, int32_t vocab,
+                                 const int32_t* drafts, float* logits, int32_t* acceptance, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

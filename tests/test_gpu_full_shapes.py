@@ -223,3 +223,7 @@ def test_c5_verify_step(device):
     rows = np.unique(np.concatenate([rng.choice(V, 8192, replace=False), top.cpu().numpy()]))
     want = x_last @ head[torch.from_numpy(rows).to(device)].float().cpu().numpy().astype(np.float64).T
     close(logits.cpu().numpy()[:, rows], want, "C5 LM head logits")
+    # the library's one C entry for the same step (wm_verify_step_fp8) equals the composition bit for bit
+    residual_n = r0.clone()
+    accept_n, logits_n = step.native(router, residual_n, drafts)
+    assert torch.equal(accept_n, accept) and torch.equal(logits_n, logits) and torch.equal(residual_n, residual)

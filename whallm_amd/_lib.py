@@ -117,6 +117,9 @@ _SIGNATURES = {
     "wm_experts_fp8": (c_int, [_P, c_int32, _P, c_int32, POINTER(FP8ExpertsC), _P, _P, c_size_t, _P]),
     "wm_mtp_workspace_size": (c_size_t, [c_int32, c_int32]),
     "wm_mtp_verify_greedy": (c_int, [_P, _P, c_int32, c_int32, _P, _P, c_size_t, _P]),
+    "wm_verify_step_fp8_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, _P]),
+    "wm_verify_step_fp8": (c_int, [c_int32, _P, _P, c_int32, _P, _P, _P, c_int32, c_int32, c_float, c_int32, c_int32,
+                                   c_float, _P, c_int32, _P, _P, _P, _P, c_size_t, _P]),
     "wm_mtp_verify_rejection": (c_int, [_P, _P, _P, c_int32, c_int32, _P, _P, _P, c_size_t, _P]),
     "wm_split_rows_e2m3": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "wm_split_rows_e4m3": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),

@@ -19,7 +19,11 @@ from __future__ import annotations
 
 import torch
 
-from .ops import (FP8Experts, linear_bf16, moe_fp8, mtp_verify_greedy, residual_rmsnorm, route_scored)
+import ctypes
+
+from . import _lib
+from .ops import (SCORE_FUNCS, FP8Experts, _ptr, _stream, linear_bf16, moe_fp8, mtp_verify_greedy, residual_rmsnorm,
+                  route_scored)
 
 
 class VerifyStep:
@@ -36,6 +40,11 @@ class VerifyStep:
         self.layers, self.shared, self.biases, self.head = layers, shared, biases, head
         self.k, self.score_func, self.route_scale = k, score_func, route_scale
         self.n_groups, self.topk_groups, self.eps = n_groups, topk_groups, eps
+        # the C entry's host arrays: the layer tables, the shared tables, the bias pointers
+        self._tables = (_lib.FP8ExpertsC * len(layers))(*[t.c_struct() for t in layers])
+        self._shared = (_lib.FP8ExpertsC * len(shared))(*[t.c_struct() for t in shared])
+        self._biases = (ctypes.c_void_p * len(biases))(*[b.data_ptr() if b is not None else None for b in biases])
+        self._ws = None
 
     def moe_layers(self, router_logits: torch.Tensor, residual: torch.Tensor, trace: list | None = None):
         """router_logits fp32 [L, M, E]; residual fp32 [M, H], updated in place. Returns the
@@ -57,3 +66,26 @@ class VerifyStep:
         x = self.moe_layers(router_logits, residual, trace)
         logits = linear_bf16(x, self.head)
         return mtp_verify_greedy(logits, drafts), logits
+
+    def native(self, router_logits: torch.Tensor, residual: torch.Tensor, drafts: torch.Tensor):
+        """The same step through the library's one C entry (wm_verify_step_fp8): the calls a
+        native caller binds instead of composing them. Returns (acceptance, logits) as
+        __call__ does; residual is updated in place."""
+        L, M = len(self.layers), residual.shape[0]
+        H, E, V = self.layers[0].hidden, self.layers[0].count, self.head.shape[0]
+        if router_logits.shape != (L, M, E) or router_logits.dtype != torch.float32 or not router_logits.is_contiguous():
+            raise ValueError("router_logits must be contiguous fp32 [layers, rows, experts]")
+        if residual.dtype != torch.float32 or not residual.is_contiguous() or residual.shape != (M, H):
+            raise ValueError("residual must be contiguous fp32 [rows, hidden]")
+        lib = _lib.load()
+        need = lib.wm_verify_step_fp8_workspace_size(M, self.k, V, ctypes.byref(self._tables[0]))
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=residual.device)
+        logits = torch.empty(M, V, dtype=torch.float32, device=residual.device)
+        acceptance = torch.empty(2, dtype=torch.int32, device=residual.device)
+        d = drafts.to(torch.int32).contiguous()
+        _lib.call("wm_verify_step_fp8", L, _ptr(router_logits), _ptr(residual), M, self._tables, self._shared,
+                  self._biases, self.k, SCORE_FUNCS[self.score_func], float(self.route_scale), self.n_groups,
+                  self.topk_groups, float(self.eps), _ptr(self.head), V, _ptr(d), _ptr(logits), _ptr(acceptance),
+                  _ptr(self._ws), self._ws.numel(), _stream(residual.device))
+        return acceptance, logits
