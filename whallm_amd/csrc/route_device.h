@@ -125,10 +125,19 @@ __device__ __forceinline__ float topk_value(uint32_t key) {
   return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
-// LDS a wave's top-k uses to put its selections in order: the selected (key, expert) pairs
-// in expert order, then in selection order. One per wave that routes at a time.
+// LDS a wave's top-k uses to put its selections in order (2 KB). One per wave that routes
+// at a time.
+//   cand[0, 64):    the candidates in expert order, each as a 64-bit composite (low word
+//                   63 - position, high word the key): a larger composite is a better
+//                   candidate (a larger key, or an equal key with a lower expert id);
+//   cand[64, 128):  one spare slot per lane, which takes the stores of lanes with nothing to
+//                   store (so no store needs a branch around it);
+//   expert[]:       the candidates' expert ids, with the same spare slots;
+//   sorted[]:       the selections in selection order, (key, expert); before that, the 64
+//                   words of the threshold's rank pass.
 struct TopkScratch {
-  uint2 cand[64];
+  uint2 cand[128];
+  uint32_t expert[128];
   uint2 sorted[64];
 };
 
@@ -240,20 +249,45 @@ __device__ __forceinline__ uint32_t radix_kth_key(const uint32_t (&key)[N], int 
   return prefix;
 }
 
+// A lower bound T of the k-th largest of the wave's 64 keys (one a lane, 1 <= k <= 64)
+// with at least k keys >= T: each lane ranks u = ((key >> 1) & ~63) | lane (31 bits, unique)
+// against the 64 values read back from LDS in one pass of independent counts (o > u exactly
+// when bit 31 of u - o is set, as both are below 2^31), and the lane of rank k - 1 gives
+// T = its key with the low 7 bits cleared. 0 when fewer than k keys are nonzero (a nonzero
+// key is at least 0x007fffff, the key of -inf). `lds` holds 64 words; the caller orders it
+// against its other uses.
+__device__ __forceinline__ uint32_t wave_kth_key_floor(uint32_t key, int k, int lane, uint32_t* lds) {
+  const uint32_t u = ((key >> 1) & ~63u) | (uint32_t)lane;
+  lds[lane] = u;
+  wave_lds_sync();
+  uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;  // values above u
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint4 o = reinterpret_cast<const uint4*>(lds)[j];
+    a0 += (u - o.x) >> 31;
+    a1 += (u - o.y) >> 31;
+    a2 += (u - o.z) >> 31;
+    a3 += (u - o.w) >> 31;
+  }
+  const uint64_t at = __builtin_amdgcn_ballot_w64((int)(a0 + a1 + a2 + a3) == k - 1);  // exactly one lane
+  return ((uint32_t)__builtin_amdgcn_readlane((int)u, (int)__builtin_ctzll(at)) & ~63u) << 1;
+}
+
 // Top-k of vals (entries with e >= experts ignored; k <= 64), value descending and ties to
 // the lower expert id. Lane j < k receives the j-th selection in (sel, sel_val); when fewer
 // than k entries are selectable (NaN never is), the lanes past them get (0x7fffffff, -inf);
 // lanes >= k get (-1, -inf). Values are compared as keys, so -0 and +0 tie and a selected
 // zero is reported as +0.
 //
-// A prefilter first: the k-th largest of the 64 per-lane maximum keys, T, has at least k
-// keys at or above it, so the top k are among the keys >= T, and the rank of such a key among
-// them (the keys better than it: larger, or equal with a lower id) is its rank in the row.
-// When there are at most 64 of them (T > 0), they are compacted into LDS in expert order,
-// each ranks itself against the others, and the first k ranks are the selection. Otherwise
-// (heavy ties, or fewer than k selectable keys) a radix walk over every key finds the k-th
-// largest key K, and the selection is every key above K plus the lowest-id entries equal
-// to K, ranked the same way.
+// A prefilter first: a lower bound T of the k-th largest of the 64 per-lane maximum keys
+// (wave_kth_key_floor) has at least k keys at or above it, so the top k are among the keys
+// >= T, and the rank of such a key among them (the keys better than it: larger, or equal with
+// a lower id) is its rank in the row. When there are at most 64 of them (T > 0), they are
+// compacted into LDS in expert order, each ranks itself against the others in one pass of
+// 64-bit composite compares, and the first k ranks are the selection. Otherwise (heavy ties,
+// or fewer than k selectable keys) a radix walk over every key finds the k-th largest key K,
+// and the selection is every key above K plus the lowest-id entries equal to K, ranked the
+// same way. No store sits under a branch (lanes with nothing to store write a spare slot).
 template <int PER_LANE>
 __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int experts, int k, int lane,
                                           TopkScratch& sc, int& sel, float& sel_val) {
@@ -263,78 +297,84 @@ __device__ __forceinline__ void wave_topk(const float (&vals)[PER_LANE], int exp
   }
   uint32_t key[PER_LANE];
 #pragma unroll
-  for (int r = 0; r < PER_LANE; ++r) key[r] = r * 64 + lane < experts ? topk_key(vals[r]) : 0u;
+  for (int r = 0; r < PER_LANE; ++r) {
+    uint32_t kk = topk_key(vals[r]);
+    asm volatile("" : "+v"(kk));  // computed on every lane, not under a branch
+    key[r] = r * 64 + lane < experts ? kk : 0u;
+  }
   auto count_ge = [&](uint32_t t) {
     int c = 0;
 #pragma unroll
     for (int r = 0; r < PER_LANE; ++r) c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(key[r] >= t));
     return c;
   };
-  uint64_t m[PER_LANE];  // selection masks, register by register (expert order: register, then lane)
-  bool exact;
-  uint32_t lane_max[1] = {key[0]};
+  bool take[PER_LANE];  // this lane's entry of register r is a candidate
+  uint32_t lane_max = key[0];
 #pragma unroll
-  for (int r = 1; r < PER_LANE; ++r) lane_max[0] = max(lane_max[0], key[r]);
-  const uint32_t t = radix_kth_key<1>(lane_max, k, exact);
+  for (int r = 1; r < PER_LANE; ++r) lane_max = max(lane_max, key[r]);
+  wave_lds_sync();  // a previous call's reads of sc are done
+  const uint32_t t = wave_kth_key_floor(lane_max, k, lane, reinterpret_cast<uint32_t*>(sc.sorted));
   if (t != 0u && count_ge(t) <= 64) {
 #pragma unroll
-    for (int r = 0; r < PER_LANE; ++r) m[r] = __builtin_amdgcn_ballot_w64(key[r] >= t);
+    for (int r = 0; r < PER_LANE; ++r) take[r] = key[r] >= t;
   } else {
+    bool exact;
     const uint32_t kth = radix_kth_key<PER_LANE>(key, k, exact);
     if (exact || kth == 0u) {  // kth 0: fewer than k selectable keys, take them all
       const uint32_t lo = exact ? kth : 1u;
 #pragma unroll
-      for (int r = 0; r < PER_LANE; ++r) m[r] = __builtin_amdgcn_ballot_w64(key[r] >= lo);
+      for (int r = 0; r < PER_LANE; ++r) take[r] = key[r] >= lo;
     } else {
       int need = k - count_ge(kth + 1u);  // ties at K to take, lowest expert id first
 #pragma unroll
       for (int r = 0; r < PER_LANE; ++r) {
         uint64_t eq = __builtin_amdgcn_ballot_w64(key[r] == kth);
-        uint64_t take = 0;
+        uint64_t low_ids = 0;
         for (; need > 0 && eq != 0; --need) {
           const uint64_t low = eq & (~eq + 1);
-          take |= low;
+          low_ids |= low;
           eq ^= low;
         }
-        m[r] = __builtin_amdgcn_ballot_w64(key[r] > kth) | take;
+        take[r] = (key[r] > kth) | (((low_ids >> lane) & 1ull) != 0);
       }
     }
   }
-  wave_lds_sync();  // a previous call's reads of sc are done
-  int n = 0;        // selected or candidate keys (at most 64)
+  wave_lds_sync();
+  int n = 0;  // candidates (at most 64)
 #pragma unroll
   for (int r = 0; r < PER_LANE; ++r) {
-    const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m[r] >> 32),
-                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m[r], 0u));
-    if ((m[r] >> lane) & 1ull) sc.cand[pos] = make_uint2(key[r], (uint32_t)(r * 64 + lane));
-    n += __builtin_popcountll(m[r]);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(take[r]);
+    const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    const int slot = take[r] ? pos : 64 + lane;
+    sc.cand[slot] = make_uint2(63u - (uint32_t)pos, key[r]);
+    sc.expert[slot] = (uint32_t)(r * 64 + lane);
+    n += __builtin_popcountll(m);
   }
+  // zero composites after the last candidate, to the end of its batch of 16 (a zero is never
+  // better than a candidate: a candidate's key is nonzero)
+  sc.cand[lane < 16 && n + lane < 64 ? n + lane : 64 + lane] = make_uint2(0u, 0u);
   wave_lds_sync();
-  if (lane < n) {
-    const uint2 me = sc.cand[lane];
-    int rank = 0;
-    for (int i0 = 0; i0 < n; i0 += 8) {  // eight candidates a batch, all reads issued together
-      uint2 o[8];
+  const uint2 mine = sc.cand[lane];
+  const uint64_t me = lane < n ? ((uint64_t)mine.y << 32 | mine.x) : ~0ull;
+  const uint32_t me_expert = sc.expert[lane];
+  int r0 = 0, r1 = 0;  // better candidates
+  for (int i0 = 0; i0 < n; i0 += 16) {  // sixteen candidates a batch, all reads issued together
+    uint4 o[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = sc.cand[i0 + j < n ? i0 + j : 0];
+    for (int q = 0; q < 8; ++q) o[q] = reinterpret_cast<const uint4*>(sc.cand)[i0 / 2 + q];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        rank += (i0 + j < n) & ((o[j].x > me.x) | ((o[j].x == me.x) & (o[j].y < me.y)));
-    }
-    if (rank < k) sc.sorted[rank] = me;
-  }
-  wave_lds_sync();
-  sel = -1;
-  sel_val = -INFINITY;
-  if (lane < k) {
-    if (lane < n) {
-      const uint2 s2 = sc.sorted[lane];
-      sel = (int)s2.y;
-      sel_val = topk_value(s2.x);
-    } else {
-      sel = 0x7fffffff;
+    for (int q = 0; q < 8; ++q) {
+      r0 += (int)(((uint64_t)o[q].y << 32 | o[q].x) > me);
+      r1 += (int)(((uint64_t)o[q].w << 32 | o[q].z) > me);
     }
   }
+  const int rank = r0 + r1;
+  wave_lds_sync();
+  *(lane < n && rank < k ? &sc.sorted[rank] : &sc.cand[64 + lane]) = make_uint2((uint32_t)(me >> 32), me_expert);
+  wave_lds_sync();
+  const uint2 s2 = sc.sorted[lane];
+  sel = lane < k ? (lane < n ? (int)s2.y : 0x7fffffff) : -1;
+  sel_val = lane < k && lane < n ? topk_value(s2.x) : -INFINITY;
 }
 
 // Softmax routing of one row held in registers (vals, expert e in lane e % 64, register

@@ -1,6 +1,6 @@
 """Phase traces of the decode kernels (a profiling tool, not on the path).
 
-    python -m whallm_amd.phase_trace [--kernel persistent|layer] [--tokens N]
+    python -m whallm_amd.phase_trace [--kernel persistent|layer] [--tokens N] [--layers L]
 
 Builds an instrumented copy of libwhallm_moe.so in whallm_amd/lib/trace/: the kernel source
 is compiled with phase_trace.h first, which turns the kernel's WM_DS_TRACE / WM_DS_NOTE
@@ -13,7 +13,8 @@ object is the library's own.
   averaged over layers 2..45, and the mean re-poll rounds of each gather;
 - layer: runs the one-launch decode layer (wm_moe_layer_decode) at the C2 shape for a few
   calls and prints, per phase point, the min / median / max over the workgroups of its time
-  after the call's first start, averaged over the calls after the first.
+  after the call's first start, averaged over the calls after the first; with --layers L the
+  calls cycle over L layers of distinct weights, as a stack runs them.
 """
 from __future__ import annotations
 
@@ -105,9 +106,11 @@ LAYER_POINTS = [(0, 0, "start"), (0, 1, "x in LDS"), (0, 2, "logits published"),
                 (0, 7, "done")]
 
 
-def run_layer(calls: int = 40, seed: int = 0) -> np.ndarray:
+def run_layer(calls: int = 40, seed: int = 0, layers: int = 1) -> np.ndarray:
     """Trace `calls` launches of the decode layer at C2; returns the trace [256, calls, 4, 16]
-    in us (call c at slot (c + 1) % 128)."""
+    in us (call c at slot (c + 1) % 128). With `layers` > 1 the calls cycle over that many
+    layers of distinct weights (as a stack runs them: each call's experts cold in the caches
+    and TLBs), else one layer's weights serve every call."""
     import torch
 
     from . import _lib
@@ -121,19 +124,24 @@ def run_layer(calls: int = 40, seed: int = 0) -> np.ndarray:
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     H, E, I, K = 2048, 512, 512, 10
-    experts = S.mxfp4_experts_device(E, H, I, dev, g)
-    shared = S.mxfp4_experts_device(1, H, I, dev, g)
-    gate = (torch.randn(H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    router = (torch.randn(E, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
-    layer = DecodeLayer(experts, router, shared, gate, k=K)
+    stack = []
+    for _ in range(max(layers, 1)):
+        experts = S.mxfp4_experts_device(E, H, I, dev, g)
+        shared = S.mxfp4_experts_device(1, H, I, dev, g)
+        gate = (torch.randn(H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        router = (torch.randn(E, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+        stack.append(DecodeLayer(experts, router, shared, gate, k=K))
+    for layer in stack[1:]:  # one state: the epoch (the trace slot) counts every call
+        layer.state = stack[0].state
     trace = torch.zeros(256 * 128 * 4 * 16, dtype=torch.int64, device=dev)
     if lib.wm_trace_set(ctypes.c_void_p(trace.data_ptr())) != 0:
         raise RuntimeError("wm_trace_set failed")
     r = torch.randn(H, device=dev, generator=g)
-    for _ in range(min(calls, 126)):
-        layer(r)
+    for c in range(min(calls, 126)):
+        stack[c % len(stack)](r)
     torch.cuda.synchronize()
-    layer.raise_for_status()
+    for layer in stack:
+        layer.raise_for_status()
     t = trace.cpu().numpy().reshape(256, 128, 4, 16)[:, 1:min(calls, 126) + 1].astype(np.float64) / 100.0
     return t
 
@@ -172,10 +180,12 @@ def main() -> None:
     ap.add_argument("--tokens", type=int, default=30, help="tokens (persistent) or calls (layer)")
     ap.add_argument("--save", default=None, help="also save the raw trace (.npy)")
     ap.add_argument("--prebuilt", action="store_true", help="use the traced library built beforehand")
+    ap.add_argument("--layers", type=int, default=1,
+                    help="layer: cycle the calls over this many layers of distinct weights")
     args = ap.parse_args()
     if not args.prebuilt:
         build_traced(args.kernel)
-    t = run(args.tokens) if args.kernel == "persistent" else run_layer(args.tokens)
+    t = run(args.tokens) if args.kernel == "persistent" else run_layer(args.tokens, layers=args.layers)
     if args.save:
         np.save(args.save, t)
     print(summary(t) if args.kernel == "persistent" else summary_layer(t))
