@@ -21,10 +21,12 @@
 //      and publishes act two values to a word (24-bit floats | 16-bit epoch);
 //   3. down: workgroup b owns output rows [H/256 b, H/256 (b + 1)); its waves split the layer's
 //      entries and load their down rows into registers right after routing. Each workgroup
-//      counts on one of eight counters once its act words are acknowledged; one wave polls the
-//      counters (a few words a round) and only then do the waves gather their entries' act
-//      words into LDS, so no wave polls act words while others still stream weights. Then
-//      y = sum_k w_k act_k . Wd_k[o] + gate act_s . Wd_s[o] in fp32 (lanes, then waves).
+//      stores the epoch into its own flag word (256 bytes apart, so no two workgroups write
+//      one line: shared counters serialise their atomics) once its waves have issued their act
+//      stores; one wave polls the 256 flags (four words a lane a round) and only then do the
+//      waves gather their entries' act words into LDS, so no wave polls act words while others
+//      still stream weights. Then y = sum_k w_k act_k . Wd_k[o] + gate act_s . Wd_s[o] in fp32
+//      (lanes, then waves).
 //
 // Exchanges use per-call epochs kept in the state buffer (each workgroup's own word), so the
 // same launch can be replayed from a graph; every wait is bounded and raises the status word.
@@ -39,7 +41,7 @@
 // Phase timestamps of the profiling build (phase_trace_lds.h; nothing in the library): slot
 // epoch % 128, points 0 start, 1 x in LDS, 2 logits published, 3 logits gathered (wave 0),
 // 4 routed, 5 gate_up computed and published, 6 act gathered, 7 done; 8 top-k done (wave 0),
-// 9 routes in LDS, 10 act counters complete, 11 down rows issued, 12 gate_up rows issued,
+// 9 routes in LDS, 10 act flags complete, 11 down rows issued, 12 gate_up rows issued,
 // 13 first pair computed.
 #ifndef WM_DS_TRACE
 #define WM_DS_TRACE(layer, point)
@@ -56,20 +58,19 @@ constexpr int WAVES = 4;
 constexpr int THREADS = 64 * WAVES;
 constexpr int MAX_ENTRIES = 12;          // routed (k <= 11) + shared
 constexpr int MAX_EXPERTS = 1024;        // router rows: 4 per workgroup
-constexpr int GROUPS = 8;                // act completion counters (workgroup b counts on b % 8)
 constexpr uint32_t ST_STALLED = MSG_STALLED, ST_NO_ROUTE = 4;
 
 // State buffer (zero-filled once by the caller): logit words, act words, per-workgroup
 // epochs and the status word.
 struct Layout {
-  size_t logits, act, counters, epoch, status, total;
+  size_t logits, act, flags, epoch, status, total;
 };
 __host__ __device__ inline Layout layout(int experts, int inter) {
   Layout d;
   size_t at = 0;
   d.logits = at;  at += (size_t)MAX_EXPERTS * 8;
   d.act = at;     at += (size_t)MAX_ENTRIES * (inter / 2) * 8;
-  d.counters = at; at += (size_t)GROUPS * 256;
+  d.flags = at;   at += (size_t)WGS * 256;
   d.epoch = at;   at += (size_t)WGS * 4;
   d.status = at;  at += 256;
   d.total = at;
@@ -132,10 +133,10 @@ struct EntryRegions {
   float limit;
 };
 
-// Workgroup b's count on its group's act counter: once per call on every path, so the
-// counters stay at epoch * (WGS / GROUPS) after each call.
-__device__ __forceinline__ void count_done(uint32_t* counters, int b) {
-  __hip_atomic_fetch_add(&counters[(b % GROUPS) * 64], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Workgroup b's act flag (its word, 256 bytes from the next): the call's epoch, stored once
+// per call on every path.
+__device__ __forceinline__ void mark_done(uint32_t* flags, int b, uint32_t epoch) {
+  __hip_atomic_store(&flags[b * 64], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Row chunks of 1 KB (64 lanes x 16 bytes): a gate_up row of H / 2 bytes spans CH chunks; the
@@ -184,7 +185,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   const Layout L = layout(p.experts, I);
   uint64_t* logit_words = reinterpret_cast<uint64_t*>(p.state + L.logits);
   uint64_t* act_words = reinterpret_cast<uint64_t*>(p.state + L.act);
-  uint32_t* counters = reinterpret_cast<uint32_t*>(p.state + L.counters);  // one per 256 bytes
+  uint32_t* flags = reinterpret_cast<uint32_t*>(p.state + L.flags);  // one per 256 bytes
   uint32_t* epochs = reinterpret_cast<uint32_t*>(p.state + L.epoch);
   uint32_t* status = reinterpret_cast<uint32_t*>(p.state + L.status);
   const int E = p.experts, K = p.k;
@@ -330,7 +331,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   }
   if (fail_s) {  // every workgroup routes the same logits, so all leave here
     if (tid == 0) {
-      count_done(counters, b);
+      mark_done(flags, b, epoch);
       epochs[b] = epoch;
     }
     return;
@@ -471,29 +472,37 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
 
   WM_DS_TRACE(epoch & 127, 5);
   // ---- wait for every workgroup's act words: once its four waves have issued their act
-  // stores, the workgroup counts once on its group's counter (without waiting for the stores'
+  // stores, the workgroup stores the epoch into its flag (without waiting for the stores'
   // acknowledgements: the gather below checks every word's epoch and re-polls a late one);
-  // lanes 0..7 of wave 0 poll the eight counters (a few words a round, with a pause between
-  // rounds) instead of every wave polling its act words while others still stream weights
+  // wave 0 polls the 256 flags, four a lane (with a pause between rounds), instead of every
+  // wave polling its act words while others still stream weights
   ds_barrier();
-  if (tid == 0) count_done(counters, b);
+  if (tid == 0) mark_done(flags, b, epoch);
   if (wave == 0) {
+    static_assert(WGS == 4 * 64, "four flags a lane");
     bool ok = true;
-    if (lane < GROUPS) {
-      const uint32_t target = epoch * (uint32_t)(WGS / GROUPS);
-      uint32_t spins = 0;
-      while ((int32_t)(__hip_atomic_load(&counters[lane * 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-        if (++spins > MSG_SPIN_LIMIT) {
-          __hip_atomic_store(status, ST_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = false;
-          break;
-        }
-        if ((spins & 63) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-          ok = false;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
+    auto behind = [&]() {
+      uint32_t f[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        f[j] = __hip_atomic_load(&flags[(lane + 64 * j) * 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bool late = false;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) late |= (int32_t)(f[j] - epoch) < 0;
+      return late;
+    };
+    uint32_t spins = 0;
+    while (behind()) {
+      if (++spins > MSG_SPIN_LIMIT) {
+        __hip_atomic_store(status, ST_STALLED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = false;
+        break;
       }
+      if ((spins & 63) == 0 && __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
     }
     if (!__all(ok) && lane == 0) fail_s = 1;
   }
@@ -504,7 +513,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     return;
   }
   // ---- gather the act rows of this wave's down entries (wave, wave + 4, ...) into LDS (every
-  // word still checked against the epoch: the counters order nothing)
+  // word still checked against the epoch: the flags order nothing)
   {
     constexpr int WPE = I / 2;             // act words an entry
     constexpr int NPL = (WPE + 63) / 64;   // words a lane gathers per entry

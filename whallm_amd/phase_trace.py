@@ -102,7 +102,7 @@ def run(tokens: int = 30, seed: int = 0) -> np.ndarray:
 LAYER_POINTS = [(0, 0, "start"), (0, 1, "x in LDS"), (0, 2, "logits published"), (0, 3, "logits gathered (wave 0)"),
                 (0, 8, "top-k done (wave 0)"), (0, 9, "routes in LDS"), (0, 4, "routed"),
                 (0, 11, "down rows issued"), (0, 12, "gate_up rows issued"), (0, 13, "first pair computed"),
-                (0, 5, "gate_up published"), (0, 10, "act counters complete"), (0, 6, "act gathered"),
+                (0, 5, "gate_up published"), (0, 10, "act flags complete"), (0, 6, "act gathered"),
                 (0, 7, "done")]
 
 
