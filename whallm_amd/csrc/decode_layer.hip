@@ -12,21 +12,24 @@
 // 64-bit word, agent-scope relaxed atomics, no L2-wide fences):
 //   1. every workgroup normalises r into LDS (x, bf16) and computes its share of the router
 //      logits (one wave per expert row, rows loaded before the norm) and publishes them
-//      (fp32 | 32-bit epoch); every workgroup gathers all E logits and routes redundantly (the
-//      wave top-k of route_device.h: same selections as wm_route_softmax_topk on the same
-//      logits);
+//      (fp32 | 32-bit epoch); in every workgroup wave 0 gathers all E logits into LDS and all
+//      four waves route them redundantly (the wave top-k of route_device.h: same selections as
+//      wm_route_softmax_topk on the same logits), each into its own copy of the entries, so no
+//      workgroup barrier stands between the top-k and a wave's weight loads;
 //   2. gate_up: the (entry, intermediate index) pairs of the K routed experts and the shared one
 //      are spread evenly over the 1024 waves, an even number to a wave; each wave streams its
 //      gate and up rows (64 lanes x 16 bytes a row chunk), dots them with x held in registers
 //      and publishes act two values to a word (24-bit floats | 16-bit epoch);
 //   3. down: workgroup b owns output rows [H/256 b, H/256 (b + 1)); its waves split the layer's
-//      entries and load their down rows into registers right after routing. Each workgroup
-//      stores the epoch into its own flag word (256 bytes apart, so no two workgroups write
-//      one line: shared counters serialise their atomics) once its waves have issued their act
-//      stores; one wave polls the 256 flags (four words a lane a round) and only then do the
-//      waves gather their entries' act words into LDS, so no wave polls act words while others
-//      still stream weights. Then y = sum_k w_k act_k . Wd_k[o] + gate act_s . Wd_s[o] in fp32
-//      (lanes, then waves).
+//      entries. Each workgroup stores the epoch into its own flag word (256 bytes apart, so no
+//      two workgroups write one line: shared counters serialise their atomics) once its waves
+//      have issued their act stores; one wave polls the 256 flags (four words a lane a round)
+//      and only then do the waves gather their entries' act words into LDS, so no wave polls
+//      act words while others still stream weights. The down rows are loaded into registers
+//      after the flag store (waves 1-3) or after the flag polls (wave 0): issued earlier, they
+//      share the CU's memory queue with the gate_up rows, the flag store and the polls, and
+//      the vector memory counter drains in order. Then y = sum_k w_k act_k . Wd_k[o] +
+//      gate act_s . Wd_s[o] in fp32 (lanes, then waves).
 //
 // Exchanges use per-call epochs kept in the state buffer (each workgroup's own word), so the
 // same launch can be replayed from a graph; every wait is bounded and raises the status word.
@@ -39,10 +42,10 @@
 #include "wm_common.h"
 
 // Phase timestamps of the profiling build (phase_trace_lds.h; nothing in the library): slot
-// epoch % 128, points 0 start, 1 x in LDS, 2 logits published, 3 logits gathered (wave 0),
-// 4 routed, 5 gate_up computed and published, 6 act gathered, 7 done; 8 top-k done (wave 0),
-// 9 routes in LDS, 10 act flags complete, 11 down rows issued, 12 gate_up rows issued,
-// 13 first pair computed.
+// epoch % 128, points 0 start, 1 x in LDS, 2 logits published, 3 logits in LDS (every wave),
+// 4 routed (the wave's entries in LDS), 5 gate_up computed and published, 6 act gathered,
+// 7 done; 8 top-k done, 10 act flags complete, 11 flag stored and (waves 1-3) down rows
+// issued, 12 gate_up rows issued, 13 first pair computed.
 #ifndef WM_DS_TRACE
 #define WM_DS_TRACE(layer, point)
 #endif
@@ -168,16 +171,17 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
 
   __shared__ __attribute__((aligned(16))) uint32_t xs[H / 2];  // x as bf16 pairs
   __shared__ float red[2 * WAVES];
-  __shared__ int rid[MAX_ENTRIES];
-  __shared__ float rw[MAX_ENTRIES];
-  __shared__ int rres[MAX_ENTRIES];  // entry resident (its slot map entry, if any, >= 0)
+  // every wave routes the same logits and keeps its own copy of the entries
+  __shared__ float rw_w[WAVES][MAX_ENTRIES];
+  __shared__ int rres_w[WAVES][MAX_ENTRIES];  // entry resident (its slot map entry, if any, >= 0)
+  __shared__ __attribute__((aligned(16))) float lg[MAX_EXPERTS];
   __shared__ float part[WAVES][RPB];
   // gathered act rows, value v of a row at 4 (G q + g) + c for v = 32 g + 4 q + c (G = I / 32):
   // the down lanes reading four values of groups g, g + 1, ... hit consecutive 16 bytes
   __shared__ __attribute__((aligned(16))) float acts[MAX_ENTRIES][I];
-  __shared__ TopkScratch topk;
+  __shared__ TopkScratch topk[WAVES];
   __shared__ TableDesc tdesc[2];  // 0 routed, 1 shared
-  __shared__ EntryRegions ent[MAX_ENTRIES];
+  __shared__ EntryRegions ent_w[WAVES][MAX_ENTRIES];
   __shared__ uint32_t epoch_s;
   __shared__ int fail_s;
 
@@ -285,107 +289,92 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   if (gate_wave && lane == 0) red[4] = gate;
   WM_DS_TRACE(epoch & 127, 2);
 
-  // ---- wave 0 gathers every logit (bounded polls) and routes
+  // ---- wave 0 gathers every logit (bounded polls) into LDS; every wave routes them (the same
+  // selections: one function of the same values) and sets up its own copy of the entries, so
+  // no barrier separates the top-k from the weight loads
+  constexpr int PER = MAX_EXPERTS / 64;
   if (wave == 0) {
     bool ok = true;
-    constexpr int PER = MAX_EXPERTS / 64;
-    float lv[PER];  // logit of expert lane + 64 m in lv[m], kept in registers
+    float lv[PER];  // logit of expert lane + 64 m in lv[m]
     ll_gather_at<PER>(
         logit_words, [&](int m) { return lane + 64 * m < E ? lane + 64 * m : -1; }, epoch, status, ok,
         [&](int m, uint64_t v) { lv[m] = __uint_as_float((uint32_t)v); });
     ok = __all(ok);
-    WM_DS_TRACE(epoch & 127, 3);
     if (!ok && lane == 0) fail_s = 1;
-    if (ok) {
-      int sel = 0;
-      float w = 0.0f, full;
-      if (E <= 512) {
-        float v8[8];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) v8[m] = lv[m];
-        wave_route_softmax_vals<8>(v8, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
-      } else {
-        wave_route_softmax_vals<PER>(lv, E, K, p.norm_topk != 0, lane, topk, sel, w, false, full);
-      }
-      WM_DS_TRACE(epoch & 127, 8);
-      // a selection outside [0, E) (fewer than k selectable logits, e.g. NaN) ends the call
-      const bool bad = lane < K && (sel < 0 || sel >= E);
-      if (__any(bad)) {
-        if (lane == 0) {
-          fail_s = 1;
-          __hip_atomic_store(status, ST_NO_ROUTE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else if (lane < K) {
-        rid[lane] = sel;
-        rw[lane] = w;
-        if (b == 0 && p.idx_out) p.idx_out[lane] = sel;
-        if (b == 0 && p.w_out) p.w_out[lane] = w;
-      }
-    }
+    for (int m = 0; m < PER; ++m) lg[lane + 64 * m] = lv[m];
   }
-  __syncthreads();
-  WM_DS_TRACE(epoch & 127, 9);
-  if (p.has_shared && tid == 0) {
-    rid[K] = -1;
-    rw[K] = p.gate_vec ? red[4] : 1.0f;
-  }
-  if (fail_s) {  // every workgroup routes the same logits, so all leave here
+  ds_barrier();
+  WM_DS_TRACE(epoch & 127, 3);
+  if (fail_s) {  // every workgroup gathers the same words, so all leave here
     if (tid == 0) {
       mark_done(flags, b, epoch);
       epochs[b] = epoch;
     }
     return;
   }
-  __syncthreads();
-  if (tid < NE) {  // the entries' regions and residency (a non-resident expert contributes nothing)
-    const int e = rid[tid];
-    const TableDesc& t = tdesc[e < 0 ? 1 : 0];
-    int64_t slot = e < 0 ? 0 : e;
-    bool resident = true;
-    if (t.slots) {
-      const int32_t s = gload<int32_t>(t.slots + slot);
-      resident = s >= 0;
-      slot = s < 0 ? 0 : s;  // not resident: slot 0 keeps every address inside the pool
+  float* rw = rw_w[wave];
+  int* rres = rres_w[wave];
+  EntryRegions* ent = ent_w[wave];
+  {
+    int sel = 0;
+    float w = 0.0f, full;
+    if (E <= 512) {
+      float v8[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) v8[m] = lg[lane + 64 * m];
+      wave_route_softmax_vals<8>(v8, E, K, p.norm_topk != 0, lane, topk[wave], sel, w, false, full);
+    } else {
+      float lv[PER];
+#pragma unroll
+      for (int m = 0; m < PER; ++m) lv[m] = lg[lane + 64 * m];
+      wave_route_softmax_vals<PER>(lv, E, K, p.norm_topk != 0, lane, topk[wave], sel, w, false, full);
     }
-    rres[tid] = resident;
-    EntryRegions r;
-    r.gate_up = t.gate_up + slot * t.gate_up_stride;
-    r.gate_up_scales = t.gate_up_scales + slot * t.gate_up_scales_stride;
-    r.down = t.down + slot * t.down_stride;
-    r.down_scales = t.down_scales + slot * t.down_scales_stride;
-    r.up_first = t.up_first;
-    r.limit = t.limit;
-    ent[tid] = r;
+    WM_DS_TRACE(epoch & 127, 8);
+    // a selection outside [0, E) (fewer than k selectable logits, e.g. NaN) ends the call
+    if (__any(lane < K && (sel < 0 || sel >= E))) {  // the same in every wave and workgroup
+      if (tid == 0) {
+        __hip_atomic_store(status, ST_NO_ROUTE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mark_done(flags, b, epoch);
+        epochs[b] = epoch;
+      }
+      return;
+    }
+    if (wave == 0 && b == 0 && lane < K) {
+      if (p.idx_out) p.idx_out[lane] = sel;
+      if (p.w_out) p.w_out[lane] = w;
+    }
+    if (lane < NE) {  // the entries' regions and residency (a non-resident expert contributes nothing)
+      const int e = lane < K ? sel : -1;  // -1: the shared expert
+      const TableDesc& t = tdesc[e < 0 ? 1 : 0];
+      int64_t slot = e < 0 ? 0 : e;
+      bool resident = true;
+      if (t.slots) {
+        const int32_t s = gload<int32_t>(t.slots + slot);
+        resident = s >= 0;
+        slot = s < 0 ? 0 : s;  // not resident: slot 0 keeps every address inside the pool
+      }
+      rres[lane] = resident;
+      rw[lane] = e < 0 ? (p.gate_vec ? red[4] : 1.0f) : w;
+      EntryRegions r;
+      r.gate_up = t.gate_up + slot * t.gate_up_stride;
+      r.gate_up_scales = t.gate_up_scales + slot * t.gate_up_scales_stride;
+      r.down = t.down + slot * t.down_stride;
+      r.down_scales = t.down_scales + slot * t.down_scales_stride;
+      r.up_first = t.up_first;
+      r.limit = t.limit;
+      ent[lane] = r;
+    }
+    wave_lds_sync();
   }
-  __syncthreads();
   WM_DS_TRACE(epoch & 127, 4);
 
-  // ---- down prefetch: this wave's entries (wave, wave + 4, ...) for the workgroup's rows.
-  // Every load is issued (lanes and entries past the end read entry 0's first row, in
-  // bounds) so none waits for another; their values are masked where they are used.
+  // down rows of this wave's entries (wave, wave + 4, ...) for the workgroup's rows, loaded
+  // into registers after the act publish (issue_down)
   const int o0 = RPB * b;
   const int slot = lane / DS::LPR, gl = lane % DS::LPR;
   uint4 dq[EPW][STEPS][DS::GPL];
   uint32_t ds_[EPW][STEPS][DS::GPL];
-#pragma unroll
-  for (int j = 0; j < EPW; ++j) {
-    const int entry = wave + WAVES * j;
-    const EntryRegions& r = ent[entry < NE ? entry : 0];
-#pragma unroll
-    for (int st = 0; st < STEPS; ++st) {
-      const int row = st * DS::NS + slot;
-      const int o = o0 + (row < RPB ? row : 0);
-#pragma unroll
-      for (int gp = 0; gp < DS::GPL; ++gp) {
-        const int g = gl + gp * DS::LPR;
-        const int gc = g < DS::G ? g : 0;
-        dq[j][st][gp] = gload16(r.down + (int64_t)o * (I / 2) + 16 * gc);
-        ds_[j][st][gp] = gload<uint8_t>(r.down_scales + (int64_t)o * DS::G + gc);
-      }
-    }
-  }
-
-  WM_DS_TRACE(epoch & 127, 11);
   // ---- gate_up: this wave's (entry, intermediate index) pairs
   {
     const int gw = b * WAVES + wave, nwaves = WGS * WAVES;
@@ -471,6 +460,27 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   }
 
   WM_DS_TRACE(epoch & 127, 5);
+  // Every down load is issued (lanes and entries past the end read entry 0's first row, in
+  // bounds) so none waits for another; their values are masked where they are used.
+  auto issue_down = [&]() {
+#pragma unroll
+    for (int j = 0; j < EPW; ++j) {
+      const int entry = wave + WAVES * j;
+      const EntryRegions& r = ent[entry < NE ? entry : 0];
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        const int row = st * DS::NS + slot;
+        const int o = o0 + (row < RPB ? row : 0);
+#pragma unroll
+        for (int gp = 0; gp < DS::GPL; ++gp) {
+          const int g = gl + gp * DS::LPR;
+          const int gc = g < DS::G ? g : 0;
+          dq[j][st][gp] = gload16(r.down + (int64_t)o * (I / 2) + 16 * gc);
+          ds_[j][st][gp] = gload<uint8_t>(r.down_scales + (int64_t)o * DS::G + gc);
+        }
+      }
+    }
+  };
   // ---- wait for every workgroup's act words: once its four waves have issued their act
   // stores, the workgroup stores the epoch into its flag (without waiting for the stores'
   // acknowledgements: the gather below checks every word's epoch and re-polls a late one);
@@ -478,6 +488,8 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
   // wave polling its act words while others still stream weights
   ds_barrier();
   if (tid == 0) mark_done(flags, b, epoch);
+  if (wave != 0) issue_down();  // after the flag store, which would queue behind them
+  WM_DS_TRACE(epoch & 127, 11);
   if (wave == 0) {
     static_assert(WGS == 4 * 64, "four flags a lane");
     bool ok = true;
@@ -506,6 +518,7 @@ __global__ void __launch_bounds__(THREADS) moe_layer_kernel(Params p) {
     }
     if (!__all(ok) && lane == 0) fail_s = 1;
   }
+  if (wave == 0) issue_down();  // after the polls, which would wait for these loads
   ds_barrier();
   WM_DS_TRACE(epoch & 127, 10);
   if (fail_s) {

@@ -99,11 +99,11 @@ def run(tokens: int = 30, seed: int = 0) -> np.ndarray:
     return trace.cpu().numpy().reshape(256, 128, 4, 16)[:, :L].astype(np.float64) / 100.0
 
 
-LAYER_POINTS = [(0, 0, "start"), (0, 1, "x in LDS"), (0, 2, "logits published"), (0, 3, "logits gathered (wave 0)"),
-                (0, 8, "top-k done (wave 0)"), (0, 9, "routes in LDS"), (0, 4, "routed"),
-                (0, 11, "down rows issued"), (0, 12, "gate_up rows issued"), (0, 13, "first pair computed"),
-                (0, 5, "gate_up published"), (0, 10, "act flags complete"), (0, 6, "act gathered"),
-                (0, 7, "done")]
+LAYER_POINTS = [(0, 0, "start"), (0, 1, "x in LDS"), (0, 2, "logits published"), (0, 3, "logits in LDS"),
+                (0, 8, "top-k done (wave 0)"), (0, 4, "routed"), (0, 12, "gate_up rows issued"),
+                (0, 13, "first pair computed"), (0, 5, "gate_up published"),
+                (1, 11, "flag stored, down rows issued (wave 1)"), (0, 10, "act flags complete"),
+                (0, 6, "act gathered"), (0, 7, "done")]
 
 
 def run_layer(calls: int = 40, seed: int = 0, layers: int = 1) -> np.ndarray:
