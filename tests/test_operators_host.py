@@ -57,6 +57,41 @@ def test_get_many_gathers_a_compact_table_and_records_the_sync():
     assert [int(table.gate_up[i, 0, 0]) for i in range(3)] == [1, 4, 5]
 
 
+def _pooled_experts(n=6, H=64, I=32):
+    """n experts handed out as [i] views of region-major tensors (the reference's get_many,
+    expert_cache.py:488-497), each expert's regions filled with its id."""
+    gu = torch.arange(n, dtype=torch.int32).repeat_interleave(2 * I * H // 8).reshape(n, 2 * I, H // 8)
+    gus = torch.full((n, 2 * I, H // 32), 127, dtype=torch.uint8)
+    dn = torch.arange(n, dtype=torch.int32).repeat_interleave(H * I // 8).reshape(n, H, I // 8)
+    dns = torch.full((n, H, I // 32), 127, dtype=torch.uint8)
+    return [O.QwenExpertWeights(gu[e], gus[e], dn[e], dns[e]) for e in range(n)]
+
+
+def test_get_many_addresses_pooled_experts_in_place():
+    experts = _pooled_experts()
+    cache = SimpleNamespace(get_many=lambda _l, ids: O.ResidentExperts(
+        tuple(experts[e] for e in sorted(set(ids))), {e: i for i, e in enumerate(sorted(set(ids)))}))
+    idx = torch.tensor([[[5, 1], [1, 4]]], dtype=torch.int32)
+    table, compact = O.resolve_table(cache, 0, idx)
+    # no copy: views from the lowest expert's regions on, and a slot map relative to it
+    assert table.slots.tolist() == [0, 3, 4] and table.count == 3
+    assert table.gate_up.data_ptr() == experts[1].gate_up.data_ptr()
+    assert compact.tolist() == [[[2, 0], [0, 1]]]
+    for i, e in enumerate([1, 4, 5]):
+        s = int(table.slots[i])
+        assert torch.equal(table.gate_up[s], experts[e].gate_up) and torch.equal(table.down[s], experts[e].down)
+
+
+def test_get_many_copies_experts_outside_one_pool():
+    pooled = _pooled_experts(3)
+    experts = [pooled[0], _qwen_expert(7), pooled[2]]  # one expert from another allocation
+    cache = SimpleNamespace(get_many=lambda _l, ids: O.ResidentExperts(tuple(experts), {0: 0, 1: 1, 2: 2}))
+    table, compact = O.resolve_table(cache, 0, torch.tensor([[2, 0, 1]], dtype=torch.int32))
+    assert table.slots is None and table.gate_up.shape[0] == 3
+    assert [int(table.gate_up[i, 0, 0]) for i in range(3)] == [0, 7, 2]
+    assert compact.tolist() == [[2, 0, 1]]
+
+
 def test_current_batched_needs_no_host_ids_and_records_the_call():
     batched = O.QwenBatchedExperts(*(torch.zeros(4, 2, 2, dtype=d) for d in (torch.int32, torch.uint8,
                                                                             torch.int32, torch.uint8)))

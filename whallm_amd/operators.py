@@ -142,22 +142,34 @@ def _stack_tables(tables: list):
     return type(first)(*fields, up_first=first.up_first, swiglu_limit=first.swiglu_limit)
 
 
-def _pool_table(tables: list):
-    """One table over single-expert tables whose regions are views of shared storages at one
-    stride per region (the slot views of a pool, or [i] of region-major tensors, which is how
-    the reference's get_many hands out resident experts, expert_cache.py:488-497): the
-    library addresses them as base + slot * stride through a slot map, so nothing is copied.
-    None when the regions lie otherwise."""
-    n = len(tables)
-    regions = [[t.tensors()[r] for t in tables] for r in range(4)]
+def _pool_regions(regs: list):
+    """For single experts (``regs``: each expert's four region tensors) whose regions are
+    views of shared storages at one stride per region (the slot views of a pool, or [i] of
+    region-major tensors, which is how the reference's get_many hands out resident experts,
+    expert_cache.py:488-497): the four regions as slot-major views over those storages and
+    each expert's slot in them, so the library addresses the experts as base + slot * stride
+    and nothing is copied. None when the regions lie otherwise."""
+    n = len(regs)
     slot_of = None
     fields = []
-    for ts in regions:
-        t0 = ts[0]
-        if any(t.dim() != 2 or t.shape != t0.shape or t.stride() != t0.stride() or t.dtype != t0.dtype
-               or t.untyped_storage().data_ptr() != t0.untyped_storage().data_ptr() for t in ts):
+    for r in range(4):
+        t0 = regs[0][r]
+        if t0.dim() != 2:
             return None
-        offs = [t.storage_offset() for t in ts]
+        shape, stride, dtype = t0.shape, t0.stride(), t0.dtype
+        size = t0.element_size()
+        storage = t0.untyped_storage()
+        base = storage.data_ptr()
+        end = base + storage.nbytes()
+        offs = []
+        for reg in regs:  # one address per view: inside t0's storage means a view of it
+            t = reg[r]
+            if t.shape != shape or t.stride() != stride or t.dtype != dtype:
+                return None
+            at = t.data_ptr() - base
+            if at < 0 or base + at >= end or at % size:
+                return None
+            offs.append(at // size)
         lo = min(offs)
         if slot_of is None:       # slot numbers from the first region's offsets
             unit = 0
@@ -167,40 +179,100 @@ def _pool_table(tables: list):
             slot_of = [(o - lo) // unit for o in offs]
             if len(set(slot_of)) != n:
                 return None
-        top = max(range(n), key=lambda i: slot_of[i])
-        step = (offs[top] - lo) // slot_of[top] if slot_of[top] else t0.numel()
-        if step < t0.numel() or any(o - lo != s * step for o, s in zip(offs, slot_of)):
+        top_slot = max(slot_of)
+        top = slot_of.index(top_slot)
+        step = (offs[top] - lo) // top_slot if top_slot else t0.numel()
+        if step < t0.numel():
             return None
-        fields.append(t0.as_strided((slot_of[top] + 1, *t0.shape), (step, *t0.stride()), lo))
-    first = tables[0]
-    slots = torch.tensor(slot_of, dtype=torch.int32).to(fields[0].device, non_blocking=True)
-    return type(first)(*fields, slots=slots, experts=n, up_first=first.up_first, swiglu_limit=first.swiglu_limit)
+        for o, sl in zip(offs, slot_of):
+            if o - lo != sl * step:
+                return None
+        fields.append(t0.as_strided((top_slot + 1, *shape), (step, *stride), lo))
+    return fields, slot_of
 
 
-def _resident_table(resident: ResidentExperts, experts: list[int], limit: float):
-    """The individual experts of ``experts`` (unique ids) as one compact table: addressed in
-    place when their regions share a pool (_pool_table), else gathered by a copy."""
-    singles = []
+class _PinnedRing:
+    """Small int32 host-to-device copies through pinned memory: each copy is queued on the
+    current stream and the host does not wait for it. A ring of slots; a slot is written
+    again only after the event recorded behind its last copy has completed."""
+    SLOTS, WORDS = 32, 4096
+
+    def __init__(self):
+        self.host = torch.empty(self.SLOTS * self.WORDS, dtype=torch.int32, pin_memory=True)
+        self.view = self.host.numpy()
+        self.events = [None] * self.SLOTS
+        self.next = 0
+
+    def to_device(self, values: list, device: torch.device) -> torch.Tensor:
+        n = len(values)
+        if n > self.WORDS:
+            return torch.tensor(values, dtype=torch.int32, device=device)
+        slot = self.next
+        self.next = (slot + 1) % self.SLOTS
+        if self.events[slot] is not None:
+            self.events[slot].synchronize()
+        lo = slot * self.WORDS
+        self.view[lo:lo + n] = values
+        out = torch.empty(n, dtype=torch.int32, device=device)
+        out.copy_(self.host[lo:lo + n], non_blocking=True)
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream(device))
+        self.events[slot] = event
+        return out
+
+
+_ring: _PinnedRing | None = None
+
+
+def _device_i32(values: list, device: torch.device) -> torch.Tensor:
+    """int32 [len(values)] on ``device``, copied without a host wait (_PinnedRing)."""
+    global _ring
+    if device.type != "cuda":  # host tensors (the CPU tests of this module's logic)
+        return torch.tensor(values, dtype=torch.int32, device=device)
+    if _ring is None:
+        _ring = _PinnedRing()
+    return _ring.to_device(values, device)
+
+
+def _resident_table(resident: ResidentExperts, experts: list[int], limit: float, ids: list[int],
+                    indices: torch.Tensor):
+    """(table, indices into it) for the individual experts of ``experts`` (sorted unique ids)
+    and the call's ids (``ids``, host ints in ``indices``' order): the table addresses the
+    experts in place when their regions share a pool (_pool_regions), else gathers them by a
+    copy. The ids are mapped to table positions on the host (they are there already), and the
+    slot map and those positions reach the device in one copy."""
+    weights = []
     for e in experts:
         if e not in resident.slots:
             raise ValueError(f"expert {e} is not resident")
-        singles.append(_as_table(resident.individual_weights[resident.slots[e]], limit))
-    return _pool_table(singles) or _stack_tables(singles)
+        weights.append(resident.individual_weights[resident.slots[e]])
+    singles = None
+    if all(type(w) is QwenExpertWeights for w in weights):  # the regions as they are (_as_table)
+        regs = [(w.gate_up, w.gate_up_scales, w.down, w.down_scales) for w in weights]
+        cls, up_first, lim = MXFP4Experts, False, limit
+    else:
+        singles = [_as_table(w, limit) for w in weights]
+        regs = [t.tensors()[:4] for t in singles]
+        cls, up_first, lim = type(singles[0]), singles[0].up_first, singles[0].swiglu_limit
+    pos = {e: i for i, e in enumerate(experts)}
+    compact = [pos[e] for e in ids]
+    pool = _pool_regions(regs)
+    if pool is None:
+        if singles is None:
+            singles = [_as_table(w, limit) for w in weights]
+        return _stack_tables(singles), _device_i32(compact, indices.device).reshape(indices.shape)
+    fields, slot_of = pool
+    n = len(slot_of)
+    buf = _device_i32(slot_of + compact, fields[0].device)
+    return cls(*fields, slots=buf[:n], experts=n, up_first=up_first, swiglu_limit=lim), buf[n:].reshape(indices.shape)
 
 
-def _compact(indices: torch.Tensor, experts: list[int]) -> torch.Tensor:
-    """Expert ids -> positions in ``experts`` (sorted unique ids), on the device."""
-    lut = torch.full((max(experts) + 1,), -1, dtype=torch.int32, device=indices.device)
-    lut[torch.tensor(experts, dtype=torch.long, device=indices.device)] = torch.arange(
-        len(experts), dtype=torch.int32, device=indices.device)
-    return lut[indices.long()]
-
-
-def _host_ids(indices: torch.Tensor, expert_count: int | None):
-    flat = indices.reshape(-1).to("cpu", torch.int64)
-    if flat.numel() and (int(flat.min()) < 0 or (expert_count is not None and int(flat.max()) >= expert_count)):
+def _host_ids(indices: torch.Tensor, expert_count: int | None) -> list[int]:
+    """The call's expert ids as host ints (one device read), checked against the model."""
+    ids = indices.reshape(-1).to("cpu").tolist()
+    if ids and (min(ids) < 0 or (expert_count is not None and max(ids) >= expert_count)):
         raise ValueError("expert ID is outside the model")
-    return flat
+    return ids
 
 
 def _generic_experts(x: torch.Tensor, indices: torch.Tensor, table, activation) -> torch.Tensor:
@@ -254,11 +326,10 @@ def resolve_table(cache, layer: int, indices: torch.Tensor, limit: float = 0.0):
         return replace(_as_table(batched), swiglu_limit=limit), indices
     started = time.perf_counter()
     model = getattr(cache, "model", None)
-    flat = _host_ids(indices, getattr(model, "expert_count", None))
+    ids = _host_ids(indices, getattr(model, "expert_count", None))
     record_sync = getattr(cache, "record_routing_sync", None)
     if record_sync is not None:
         record_sync(time.perf_counter() - started)
-    ids = flat.tolist()
     unique = sorted(set(ids))
     rows = indices.numel() // indices.shape[-1]
     if rows == 1 and getattr(cache, "ready_expert_decode", False) and hasattr(cache, "iter_ready"):
@@ -272,7 +343,7 @@ def resolve_table(cache, layer: int, indices: torch.Tensor, limit: float = 0.0):
         resident = ResidentExperts(tuple(got[e] for e in unique), {e: i for i, e in enumerate(unique)})
     else:
         resident = cache.get_many(layer, ids)
-    return _resident_table(resident, unique, limit), _compact(indices, unique)
+    return _resident_table(resident, unique, limit, ids, indices)
 
 
 # ----------------------------------------------------------------------------- Qwen operators
@@ -460,11 +531,10 @@ class _StreamingSwitchGLU:
 
     def forward_with_resident(self, x: torch.Tensor, indices: torch.Tensor, resident: ResidentExperts):
         """Token-shaped expert math from one pre-acquired union (model.py:387-395)."""
-        flat = _host_ids(indices, None)
-        unique = sorted(set(flat.tolist()))
+        ids = _host_ids(indices, None)
+        unique = sorted(set(ids))
         limit = _fused_limit(self.activation)
-        table = _resident_table(resident, unique, 0.0 if limit is None else limit)
-        idx = _compact(indices, unique)
+        table, idx = _resident_table(resident, unique, 0.0 if limit is None else limit, ids, indices)
         if limit is None:
             H = x.shape[-1]
             T = x.numel() // H
