@@ -1,4 +1,4 @@
-"""GPU parity at the full shapes the benchmark times (C4 prefill, C5).
+"""GPU parity at the full shapes the benchmark times (C4 prefill and decode, C5).
 
 The oracle cannot afford every token at these sizes, so each test checks a seeded sample
 of tokens against the oracle's fp32 dequant-then-matmul (relative L2 <= 1e-2, max |err|
@@ -179,6 +179,42 @@ def test_c4_prefill_full_size(device):
     rel_rows = float(np.linalg.norm(got - want_rows) / np.linalg.norm(want_rows))
     print(f"C4 E4M3 against the oracle with bf16 rows: rel L2 {rel_rows:.2e}", flush=True)
     assert rel_rows <= 2.5e-3
+
+
+def fp8_expert_any(tab, e):
+    """One FP8 expert of a device table as the oracle's FP8Expert, either scale format."""
+    I, fmt = tab.inter, tab.scale_format
+    b = I // (32 if fmt else 128)
+    w13, s13 = tab.w13[e].cpu().numpy(), tab.w13_scales[e].cpu().numpy()
+    return M.FP8Expert(w13[:I], s13[:b], w13[I:], s13[b:], tab.w2[e].cpu().numpy(), tab.w2_scales[e].cpu().numpy(),
+                       scale_format=fmt)
+
+
+@pytest.mark.parametrize("fmt", [0, 1], ids=["fp32-128", "e8m0-32"])
+def test_c4_decode_full_size(device, fmt):
+    """The C4 decode layer at its full shape (H 7168, I 2048, 256 experts, top-8 over 8 groups /
+    top 4, sigmoid scores with bias, the ungated shared expert), one token a call through the
+    fused GEMV path, as the bench runs it: routes bit-exact and every output element against
+    the oracle (each token's 8 experts and the shared one dequantized), for two tokens."""
+    H, E, I, K = 7168, 256, 2048, 8
+    g = torch.Generator(device=device)
+    g.manual_seed(13 + fmt)
+    experts = S.fp8_experts_device(E, H, I, device, g, scale_format=fmt)
+    shared = S.fp8_experts_device(1, H, I, device, g, scale_format=fmt)
+    bias = torch.randn(E, device=device, generator=g) * 0.1
+    sh = fp8_expert_any(shared, 0)
+    for t in range(2):
+        logits = torch.randn(1, E, device=device, generator=g)
+        x = torch.randn(1, H, device=device, generator=g).to(torch.bfloat16)
+        idx, w = wa.route_scored(logits, bias, K, "sigmoid", 2.5, True, 8, 4)
+        want_idx, want_w = M.route_scored(logits.cpu().numpy(), bias.cpu().numpy(), K, "sigmoid", 2.5, True, 8, 4)
+        np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+        y = wa.moe_fp8(x, idx, w, experts, shared, None)
+        xs = x.float().cpu().numpy()
+        ex = {int(e): fp8_expert_any(experts, int(e)) for e in np.unique(want_idx)}
+        want = M.combine(M.routed_outputs(xs, want_idx, ex, ffn=M.fp8_expert_ffn), w.cpu().numpy(),
+                         M.fp8_expert_ffn(xs, sh), None)
+        close(y.float().cpu().numpy(), want, f"C4 decode token {t}, scale format {fmt}")
 
 
 def test_c5_verify_step(device):
