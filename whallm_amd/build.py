@@ -66,7 +66,8 @@ def build(force: bool = False, jobs: int | None = None) -> Path:
     newest = max(o.stat().st_mtime for o in objects)
     if force or not LIB.exists() or LIB.stat().st_mtime < newest:
         tmp = LIB.with_suffix(".so.tmp")
-        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+        # -z defs: an undefined symbol (a declaration without its definition) fails the link
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objects), "-o", str(tmp)]
         result = subprocess.run(cmd, capture_output=True, text=True)
         if result.returncode != 0:
             raise RuntimeError(f"link of {LIB.name} failed:\n{result.stderr}")

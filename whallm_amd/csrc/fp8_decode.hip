@@ -15,12 +15,18 @@
 //                     input (v_dot2_f32_bf16) and multiplies the 16-column partial by the
 //                     scale of its block (fp32, or 2^(b-127) of its E8M0 byte, both exact
 //                     powers or floats applied once per partial); silu(gate) * up (clamped when the
-//                     table sets a SwiGLU limit) -> act (fp32).
+//                     table sets a SwiGLU limit) in fp32 -> act, stored as bf16. The reference
+//                     rounds the gate and up projections to bf16 before the SwiGLU and feeds the
+//                     shared expert's act to w2 as bf16 (deepseek_v41/moe.py:86-93), so rounding
+//                     act once is an error of the size it already carries; the bf16 rows halve the
+//                     down kernel's act reads and take the bf16 dot.
 //   fp8_down        : one workgroup = (token, 8 output rows); the four waves split the
 //                     token's experts (routed + shared) and keep routing-weighted partial
 //                     sums per row, reduced once: y[t, o] = sum_k w_k act_k . Wd_k[o]
-//                     (+ gate(t) act_s . Wd_s[o]). The per-pair mode writes each pair's
-//                     row unweighted (router order, the StreamingExperts contract).
+//                     (+ gate(t) act_s . Wd_s[o]), each 16-column partial a v_dot2_f32_bf16
+//                     chain of the exactly converted weights with the bf16 act. The per-pair
+//                     mode writes each pair's row unweighted (router order, the
+//                     StreamingExperts contract).
 //
 // Weight rows are streamed once per call, so their loads carry the non-temporal hint (4%
 // faster C4 decode steps than plain loads).
@@ -40,21 +46,6 @@ __device__ __forceinline__ float e4m3x16_dot_bf16(uint4 w, const uint32_t* xw, f
     const wm_bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(words[j], 1.0f, true);
     acc = dot2_bf16(lo, bits_to_bf16x2(xw[2 * j]), acc);
     acc = dot2_bf16(hi, bits_to_bf16x2(xw[2 * j + 1]), acc);
-  }
-  return acc;
-}
-
-// 16 E4M3 bytes dotted with 16 fp32 values.
-__device__ __forceinline__ float e4m3x16_dot_f32(uint4 w, const float* a, float acc) {
-  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const wm_f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[j], false);
-    const wm_f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[j], true);
-    acc = fmaf(lo[0], a[4 * j], acc);
-    acc = fmaf(lo[1], a[4 * j + 1], acc);
-    acc = fmaf(hi[0], a[4 * j + 2], acc);
-    acc = fmaf(hi[1], a[4 * j + 3], acc);
   }
   return acc;
 }
@@ -106,7 +97,7 @@ template <int CPL, int SF>
 __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __restrict__ x, int tokens, int k,
                                                               const int32_t* __restrict__ indices,
                                                               wm_fp8_experts routed, wm_fp8_experts shared,
-                                                              int has_shared, float* __restrict__ act) {
+                                                              int has_shared, uint16_t* __restrict__ act) {
   constexpr int ROWS = 2 * FP8_RPW;
   __shared__ float sums[4][ROWS];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -118,7 +109,7 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
   if (!fp8_pair(p, tokens, k, indices, routed, has_shared != 0, shared, t, r, is_shared)) {
     // unknown or non-resident expert: its act rows are zero and the down kernels skip the pair
     for (int i = blockIdx.x * 4 * FP8_RPW + threadIdx.x; i < (int)(blockIdx.x + 1) * 4 * FP8_RPW; i += 256)
-      act[(int64_t)p * I + i] = 0.0f;
+      act[(int64_t)p * I + i] = 0;
     return;
   }
   const wm_fp8_experts& tab = is_shared ? shared : routed;
@@ -184,7 +175,7 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
       g = fminf(g, limit);
       u = fminf(fmaxf(u, -limit), limit);
     }
-    act[(int64_t)p * I + i_base + lane] = silu(g) * u;
+    act[(int64_t)p * I + i_base + lane] = f32_to_bf16_bits(silu(g) * u);
   }
 }
 
@@ -192,7 +183,7 @@ constexpr int FP8_OPW = 8;  // output rows per wave step
 
 // grid: combine (H / FP8_OPW, tokens); per pair (H / (4 * FP8_OPW), pairs). CPL = ceil(I / 1024).
 template <int CPL, int SF, bool COMBINE>
-__global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__ act, int tokens, int k,
+__global__ void __launch_bounds__(256) fp8_down_kernel(const uint16_t* __restrict__ act, int tokens, int k,
                                                        const int32_t* __restrict__ indices,
                                                        const float* __restrict__ weights, wm_fp8_experts routed,
                                                        wm_fp8_experts shared, int has_shared,
@@ -263,17 +254,17 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
       w = 1.0f;
     }
     // loads unconditional (lanes past the row read its first chunk), masked through the scale
-    float av[CPL][16];
+    uint32_t av[CPL][8];
     float inm[CPL];
-    const float* arow = act + (int64_t)p * I;
+    const uint16_t* arow = act + (int64_t)p * I;
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
       const int off = 1024 * m + 16 * lane;
       inm[m] = off < I ? 1.0f : 0.0f;
-      const float4* a4 = reinterpret_cast<const float4*>(arow + (off < I ? off : 0));
+      const uint4* a4 = reinterpret_cast<const uint4*>(arow + (off < I ? off : 0));
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 v = a4[q];
+      for (int q = 0; q < 2; ++q) {
+        const uint4 v = a4[q];
         av[m][4 * q] = v.x; av[m][4 * q + 1] = v.y; av[m][4 * q + 2] = v.z; av[m][4 * q + 3] = v.w;
       }
     }
@@ -303,7 +294,7 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
     for (int q = 0; q < FP8_OPW; ++q) {
       float s = 0.0f;
 #pragma unroll
-      for (int m = 0; m < CPL; ++m) s = fmaf(scv[m], e4m3x16_dot_f32(wq[q][m], av[m], 0.0f), s);
+      for (int m = 0; m < CPL; ++m) s = fmaf(scv[m], e4m3x16_dot_bf16(wq[q][m], av[m], 0.0f), s);
       acc[q] = fmaf(w, s, acc[q]);
     }
   }
@@ -327,7 +318,7 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const float* __restrict__
 template <int SF>
 static void launch_decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                               const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
-                              uint16_t* y, bool combine, float* act, hipStream_t s) {
+                              uint16_t* y, bool combine, uint16_t* act, hipStream_t s) {
   const int H = routed.hidden, I = routed.inter;
   const int pairs = tokens * k + (shared ? tokens : 0);
   const wm_fp8_experts sh = shared ? *shared : routed;
@@ -361,7 +352,7 @@ static void launch_decode_fp8(const uint16_t* x, int tokens, const int32_t* indi
 
 void decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                 const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
-                uint16_t* y, bool combine, float* act, hipStream_t s) {
+                uint16_t* y, bool combine, uint16_t* act, hipStream_t s) {
   const int H = routed.hidden, I = routed.inter;
   if (H % 128 || I % 128 || H > 8192 || I > 8192)
     fail("FP8 decode: hidden and intermediate must be multiples of 128 up to 8192");

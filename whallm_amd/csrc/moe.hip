@@ -193,7 +193,8 @@ WM_EXPORT int wm_experts_mxfp4(const void* x, int32_t tokens, const int32_t* ind
 
 WM_EXPORT size_t wm_moe_fp8_workspace_size(int32_t tokens, int32_t k, const wm_fp8_experts* experts) {
   if (!experts || tokens < 0 || k < 1) return 0;
-  if (use_decode_fp8(tokens, k, *experts)) return sizeof(float) * (size_t)(tokens * k + tokens) * experts->inter + 256;
+  if (use_decode_fp8(tokens, k, *experts))  // act rows, bf16
+    return sizeof(uint16_t) * (size_t)(tokens * k + tokens) * experts->inter + 256;
   return prefill_fp8_workspace_size(tokens, k, *experts, true) + 256;
 }
 
@@ -211,7 +212,7 @@ WM_EXPORT int wm_moe_fp8(const void* x, int32_t tokens, const int32_t* indices, 
     hipStream_t s = as_stream(stream);
     if (use_decode_fp8(tokens, k, *experts))
       decode_fp8((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
-                 (uint16_t*)y, true, (float*)workspace, s);
+                 (uint16_t*)y, true, (uint16_t*)workspace, s);
     else
       prefill_fp8((const uint16_t*)x, tokens, indices, weights, k, *experts, shared, (const uint16_t*)shared_gate,
                   (uint16_t*)y, true, workspace, workspace_bytes, s);
@@ -232,7 +233,7 @@ WM_EXPORT int wm_experts_fp8(const void* x, int32_t tokens, const int32_t* indic
     hipStream_t s = as_stream(stream);
     if (use_decode_fp8(tokens, k, *experts))
       decode_fp8((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out, false,
-                 (float*)workspace, s);
+                 (uint16_t*)workspace, s);
     else
       prefill_fp8((const uint16_t*)x, tokens, indices, nullptr, k, *experts, nullptr, nullptr, (uint16_t*)out, false,
                   workspace, workspace_bytes, s);

@@ -70,7 +70,7 @@ void prefill_mxfp4(const uint16_t* x, int tokens, const int32_t* indices, const 
 // FP8 expert FFN (hidden and intermediate multiples of 128; up to 8192 for decode).
 void decode_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                 const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
-                uint16_t* y, bool combine, float* act, hipStream_t s);
+                uint16_t* y, bool combine, uint16_t* act, hipStream_t s);  // act: bf16 [pairs, I]
 size_t prefill_fp8_workspace_size(int tokens, int k, const wm_fp8_experts& e, bool has_shared);
 void prefill_fp8(const uint16_t* x, int tokens, const int32_t* indices, const float* weights, int k,
                  const wm_fp8_experts& routed, const wm_fp8_experts* shared, const uint16_t* shared_gate,
