@@ -602,6 +602,10 @@ struct RingMx {
 // piece p ^ (row & 15); its scale dword is written by the loader at position
 // 16 w + 4 i + d for row 4 (w + 8 i) + d (the wave that loads the row's terms).
 __device__ __forceinline__ uint32_t e4_piece(int row, int p) { return (uint32_t)(row * XSTEP8 + 16 * (p ^ (row & 15))); }
+// The gate_up epilogue stages the tile's E4M3 act rows at a 512-byte pitch (two steps), so
+// the 16 rows one ds_write_b128 cycle serves would all hit the same 16 bytes of banks:
+// piece q (0..15) of a row's staged step goes to q ^ (row & 15) instead.
+__device__ __forceinline__ int e4_stage_piece(int row, int q) { return q ^ (row & 15); }
 __device__ __forceinline__ uint32_t e4_scale(int row) {
   return (uint32_t)(BM * XSTEP8 + 4 * (16 * ((row / 4) % 8) + 4 * (row / 32) + row % 4));
 }
@@ -1171,12 +1175,13 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
           uint32_t hi[8], lo8[8];
           int s_hi;
           fp8_terms32(full, hi, lo8, s_hi);
-          uint4* dh = reinterpret_cast<uint4*>(step + (kb % 4) * 32);
-          uint4* dl = reinterpret_cast<uint4*>(step + 128 + (kb % 4) * 32);
-          dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-          dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-          dl[0] = make_uint4(lo8[0], lo8[1], lo8[2], lo8[3]);
-          dl[1] = make_uint4(lo8[4], lo8[5], lo8[6], lo8[7]);
+          // 16-byte piece q of a staged step at q ^ (lr & 15) (see e4_stage_piece)
+          const int q0 = 2 * (kb % 4);
+          auto piece = [&](int q) { return reinterpret_cast<uint4*>(step + 16 * e4_stage_piece(lr, q)); };
+          *piece(q0) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+          *piece(q0 + 1) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+          *piece(8 + q0) = make_uint4(lo8[0], lo8[1], lo8[2], lo8[3]);
+          *piece(8 + q0 + 1) = make_uint4(lo8[4], lo8[5], lo8[6], lo8[7]);
           sscale(lr)[kb] = (uint8_t)s_hi;  // byte kb % 4 of the row's dword kb / 4
         } else {
           v6u_t hi, lo6;
@@ -1196,7 +1201,8 @@ __global__ void __launch_bounds__(64 * F::WAVES, F::WAVES / 4) gate_up_mx_kernel
     const int n = (t.end - t.begin) * chunks;
     for (int idx = threadIdx.x; idx < n; idx += 64 * F::WAVES) {
       const int lr = idx / chunks, c = idx - lr * chunks;
-      const uint4 v4 = *reinterpret_cast<const uint4*>(srow(lr) + 16 * c);
+      const int cs = F::Terms::E4 ? (c & ~15) | e4_stage_piece(lr, c & 15) : c;
+      const uint4 v4 = *reinterpret_cast<const uint4*>(srow(lr) + 16 * cs);
       *reinterpret_cast<uint4*>(a6 + (int64_t)(t.begin + lr) * a_row + (int64_t)(t.nt * TG / 128) * XS + 16 * c) = v4;
     }
     if constexpr (F::Terms::E4) {
