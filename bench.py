@@ -948,7 +948,9 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # untimed: the kernels settle over their first ~15 back-to-back launches (clock ramp,
+    # cold caches; the per-dispatch durations in profiles/)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2-decode", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-impl", default="persistent", choices=["persistent", "layers"],
