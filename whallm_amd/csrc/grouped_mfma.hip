@@ -965,8 +965,8 @@ __device__ __forceinline__ void ring_wait_keep<10>() {
 // Step g reads weight slot g % DA and split-row slot g % DB. At the top of step g every
 // wave has step g's loads landed and is done with step g - 1's slots; the shallower ring
 // then loads step g + 1 into its freed slot and the deeper ring (depth D) step g + D - 1
-// (a tile's later step, or the next tile's first steps), each in two halves issued
-// between the step's MFMA groups, the deeper ring's last. With K steps fewer than D the
+// (a tile's later step, or the next tile's first steps), each in two halves issued at the
+// top of the step or between its MFMA groups, the deeper ring's last. With K steps fewer than D the
 // deeper ring also loads one step ahead. The next tile is set up (index loads, load
 // offsets) after the MFMAs of the step before its first loads; after an epilogue (whose
 // stores may complete out of order with loads) the top waits for everything.
@@ -1017,19 +1017,30 @@ __device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps,
     const int td = kd < steps ? (cur_ok ? 1 : 0) : (more ? 2 : 0);
     const int ks_s = k + 1 < steps ? k + 1 : 0, ks_d = kd < steps ? kd : kd - steps;
     const int sl_s = (g + 1) % DS, sl_d = (g + la) % D;
+    // half h of the deeper (deep) or shallower ring's loads of this step
+    auto part = [&](bool deep, int h) {
+      const int t = deep ? td : ts;
+      if (t == 1)
+        issue(cur, deep, deep ? sl_d : sl_s, deep ? ks_d : ks_s, h);
+      else if (t == 2)
+        issue(nxt, deep, deep ? sl_d : sl_s, deep ? ks_d : ks_s, h);
+    };
+    // Rings of equal depth (the shallower one is then the weight ring): the weight halves at
+    // the top of the step, the split-row halves after MFMA groups 0 and 1. Otherwise the
+    // shallower ring's halves after groups 0 and 1 and the deeper ring's after groups 2 and
+    // 3, so the deeper ring's loads are the last ones the ring wait leaves in flight.
+    constexpr bool EQUAL = DA == DB;
     auto load_part = [&](int p) {
-      if (p < 2) {
-        if (ts == 1)
-          issue(cur, false, sl_s, ks_s, p);
-        else if (ts == 2)
-          issue(nxt, false, sl_s, ks_s, p);
+      if (EQUAL && cur_ok) {
+        if (p < 2) part(true, p);
       } else {
-        if (td == 1)
-          issue(cur, true, sl_d, ks_d, p - 2);
-        else if (td == 2)
-          issue(nxt, true, sl_d, ks_d, p - 2);
+        part(p >= 2, p & 1);
       }
     };
+    if (EQUAL && cur_ok) {
+      part(false, 0);
+      part(false, 1);
+    }
     if (cur_ok) {
       mfma(cur, wslot(g % DA), rslot(g % DB), k, load_part);
     } else {
