@@ -134,22 +134,6 @@ class DecodeStack:
         if self.impl == "persistent":
             self.stack.raise_for_status()
 
-    def kernel_ms(self, launches: int) -> float:
-        """Average duration of the persistent kernel itself: HIP events recorded on the
-        replay stream around each replay of a step's graph, whose one node is the kernel
-        (the timed steps replay the same graphs back to back)."""
-        stream = torch.cuda.current_stream(self.device)
-        total = 0.0
-        for i in range(launches):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            self.graphs[i % len(self.graphs)].replay()
-            b.record(stream)
-            b.synchronize()
-            total += a.elapsed_time(b)
-        self.check()
-        return total / launches
-
     def _body_at(self, j):
         if self.impl == "persistent":
             self.stack(self.step_logits[j], self.step_embed[j].view(-1), self.x_out.view(-1), check=False)
@@ -296,9 +280,6 @@ class LayerCalls(DecodeStack):
     def check(self):
         for call in self.calls:
             call.raise_for_status()
-
-    def kernel_ms(self, launches: int) -> float:
-        return None
 
     def config(self):
         c = super().config()
@@ -870,11 +851,12 @@ def measure(wl, steps: int, warmup: int):
                     "layer_call_us": round(per_layer_ms * 1e3, 3),
                     "algorithmic_bytes_per_launch": wl.algorithmic_bytes() // wl.L}
     elif isinstance(wl, DecodeStack):
+        # the HIP events over the timed region (graphs replayed back to back on this stream):
+        # for the persistent kernel, one launch a step, its duration plus the gap to the next
+        k_ms = ms_per_step
         if wl.impl == "persistent":
-            k_ms = wl.kernel_ms(steps)
             kernel = "decode_persistent_kernel (one launch = one token through 48 layers)"
         else:
-            k_ms = ms_per_step
             kernel = "decode step: 48 x (route, gate_up_act, down_combine, residual_rmsnorm)"
         achieved = wl.algorithmic_bytes() / (k_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
