@@ -23,6 +23,7 @@ SwiGLU hot path.
 from __future__ import annotations
 
 import math
+import threading
 import time
 from dataclasses import dataclass, replace
 
@@ -194,7 +195,8 @@ def _pool_regions(regs: list):
 class _PinnedRing:
     """Small int32 host-to-device copies through pinned memory: each copy is queued on the
     current stream and the host does not wait for it. A ring of slots; a slot is written
-    again only after the event recorded behind its last copy has completed."""
+    again only after the event recorded behind its last copy has completed. Calls from
+    several threads take the ring one at a time."""
     SLOTS, WORDS = 32, 4096
 
     def __init__(self):
@@ -202,22 +204,24 @@ class _PinnedRing:
         self.view = self.host.numpy()
         self.events = [None] * self.SLOTS
         self.next = 0
+        self.lock = threading.Lock()
 
     def to_device(self, values: list, device: torch.device) -> torch.Tensor:
         n = len(values)
         if n > self.WORDS:
             return torch.tensor(values, dtype=torch.int32, device=device)
-        slot = self.next
-        self.next = (slot + 1) % self.SLOTS
-        if self.events[slot] is not None:
-            self.events[slot].synchronize()
-        lo = slot * self.WORDS
-        self.view[lo:lo + n] = values
-        out = torch.empty(n, dtype=torch.int32, device=device)
-        out.copy_(self.host[lo:lo + n], non_blocking=True)
-        event = torch.cuda.Event()
-        event.record(torch.cuda.current_stream(device))
-        self.events[slot] = event
+        with self.lock:
+            slot = self.next
+            self.next = (slot + 1) % self.SLOTS
+            if self.events[slot] is not None:
+                self.events[slot].synchronize()
+            lo = slot * self.WORDS
+            self.view[lo:lo + n] = values
+            out = torch.empty(n, dtype=torch.int32, device=device)
+            out.copy_(self.host[lo:lo + n], non_blocking=True)
+            event = torch.cuda.Event()
+            event.record(torch.cuda.current_stream(device))
+            self.events[slot] = event
         return out
 
 
