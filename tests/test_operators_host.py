@@ -149,3 +149,44 @@ def test_activation_descriptors():
     got = O.ClampedSwiGLU(10)(up, gate)
     want = torch.nn.functional.silu(torch.tensor([10.0, 1.0])) * torch.tensor([10.0, -10.0])
     assert torch.allclose(got, want)
+
+
+def _same_pool(a, b):
+    if a is None or b is None:
+        return a is None and b is None
+    (fa, sa), (fb, sb) = a, b
+    return list(sa) == list(sb) and all(
+        x.shape == y.shape and x.stride() == y.stride() and x.storage_offset() == y.storage_offset()
+        and x.data_ptr() == y.data_ptr() and x.dtype == y.dtype for x, y in zip(fa, fb))
+
+
+@pytest.mark.skipif(O._host_meta is None, reason="csrc/host_meta.cpp is not built (python -m whallm_amd.build)")
+def test_compiled_pool_check_equals_the_python_rules():
+    rng = torch.Generator().manual_seed(0)
+    experts = _pooled_experts(8)
+    regs = lambda ws: [(w.gate_up, w.gate_up_scales, w.down, w.down_scales) for w in ws]  # noqa: E731
+    cases = [regs(experts), regs(experts[3:4]), regs([experts[i] for i in (6, 1, 4)])]
+    for _ in range(20):  # random subsets in random order
+        perm = torch.randperm(8, generator=rng)[:int(torch.randint(1, 9, (1,), generator=rng))]
+        cases.append(regs([experts[int(i)] for i in perm]))
+    # padded slots: [i, :rows] of a region-major tensor with two spare rows per slot
+    pad = torch.zeros(4, 66, 8, dtype=torch.int32)
+    padded = [O.QwenExpertWeights(pad[e, :64], experts[e].gate_up_scales, experts[e].down, experts[e].down_scales)
+              for e in range(4)]
+    cases.append(regs(padded))
+    # not one pool: another allocation, a shape or dtype that differs, a repeated expert,
+    # a 3-D region, offsets that are not slot multiples of one step
+    other = _qwen_expert(7)
+    cases.append(regs([experts[0], other]))
+    cases.append(regs([experts[0], O.QwenExpertWeights(experts[1].gate_up[:, :4], *regs([experts[1]])[0][1:])]))
+    cases.append(regs([experts[0], O.QwenExpertWeights(experts[1].gate_up.view(torch.float32),
+                                                       *regs([experts[1]])[0][1:])]))
+    cases.append(regs([experts[2], experts[2]]))
+    cases.append([(experts[0].gate_up[None], *regs([experts[0]])[0][1:])])
+    flat = torch.zeros(1000, dtype=torch.int32)
+    odd = [O.QwenExpertWeights(flat[o:o + 64 * 8].view(64, 8), *regs([experts[e]])[0][1:]) for e, o in ((0, 0), (1, 3))]
+    cases.append(regs(odd))
+    for regs_case in cases:
+        assert _same_pool(O._host_meta.pool_regions([t for r in regs_case for t in r], len(regs_case)),
+                          O._pool_regions(regs_case))
+    assert O._host_meta.pool_regions([], 0) is None

@@ -75,6 +75,41 @@ def build(force: bool = False, jobs: int | None = None) -> Path:
     return LIB
 
 
+HOST_META_SRC = CSRC / "host_meta.cpp"
+
+
+def host_meta_path() -> Path:
+    """Where the operator mirrors' host helper (csrc/host_meta.cpp) is built."""
+    import sysconfig
+    return LIB.parent / ("_host_meta" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_host_meta(force: bool = False) -> Path:
+    """Compile csrc/host_meta.cpp into a CPython extension against the installed torch (host
+    code only, g++); returns its path."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    out = host_meta_path()
+    if not force and out.exists() and out.stat().st_mtime >= HOST_META_SRC.stat().st_mtime:
+        return out
+    LIB.parent.mkdir(exist_ok=True)
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = ["g++", "-O2", "-shared", "-fPIC", "-std=c++17", "-DTORCH_EXTENSION_NAME=_host_meta",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-I{p}" for p in cpp_extension.include_paths()], f"-I{sysconfig.get_paths()['include']}",
+           str(HOST_META_SRC), "-o", str(tmp),
+           *[f"-L{p}" for p in cpp_extension.library_paths()], "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"g++ failed on {HOST_META_SRC.name}:\n{result.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     path = build(force="--force" in sys.argv)
     print(path)
+    print(build_host_meta(force="--force" in sys.argv))

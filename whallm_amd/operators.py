@@ -192,6 +192,37 @@ def _pool_regions(regs: list):
     return fields, slot_of
 
 
+def _load_host_meta():
+    """The compiled form of _pool_regions (csrc/host_meta.cpp, built beside the library by
+    whallm_amd.build), or None when it is not built."""
+    import importlib.util
+    import warnings
+
+    from .build import host_meta_path
+    path = host_meta_path()
+    if not path.exists():
+        return None
+    try:
+        spec = importlib.util.spec_from_file_location("_host_meta", path)
+        module = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(module)
+        return module
+    except ImportError as exc:
+        warnings.warn(f"{path.name} did not load ({exc}); the pool check runs in Python")
+        return None
+
+
+_host_meta = _load_host_meta()
+
+
+def _pool_fields(regs: list):
+    """_pool_regions through the compiled helper when it is built (the same rules; reading
+    tensor metadata from Python is most of a resident-expert call's host time)."""
+    if _host_meta is not None:
+        return _host_meta.pool_regions([t for reg in regs for t in reg], len(regs))
+    return _pool_regions(regs)
+
+
 class _PinnedRing:
     """Small int32 host-to-device copies through pinned memory: each copy is queued on the
     current stream and the host does not wait for it. A ring of slots; a slot is written
@@ -260,7 +291,7 @@ def _resident_table(resident: ResidentExperts, experts: list[int], limit: float,
         cls, up_first, lim = type(singles[0]), singles[0].up_first, singles[0].swiglu_limit
     pos = {e: i for i, e in enumerate(experts)}
     compact = [pos[e] for e in ids]
-    pool = _pool_regions(regs)
+    pool = _pool_fields(regs)
     if pool is None:
         if singles is None:
             singles = [_as_table(w, limit) for w in weights]
