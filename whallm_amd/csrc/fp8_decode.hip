@@ -70,6 +70,24 @@ __device__ __forceinline__ bool fp8_pair(int p, int tokens, int k, const int32_t
   return resident;
 }
 
+// The block's (row block x, pair or token p). One token: a 2-D grid (X, P), the row blocks
+// of a pair in launch order. Several tokens: a 1-D grid of X * P blocks in which the P blocks
+// of one row block lie 8 apart (block b runs on XCD b % 8), so they run on one XCD at about
+// the same time and its L2 serves the rows they share: the shared expert's, read once per
+// token, and any routed expert two tokens picked (C5 verify 1.24-1.26 ms against 1.31 ms;
+// one token keeps the row-block order, whose reads each XCD spreads over fewer experts).
+// X is a multiple of 8 (widths are multiples of 128).
+__device__ __forceinline__ void block_order(int X, int P, bool interleave, int& x, int& p) {
+  if (!interleave) {
+    x = blockIdx.x;
+    p = blockIdx.y;
+    return;
+  }
+  const int b = blockIdx.x, lo = b % 8, q = b / 8;
+  p = q % P;
+  x = 8 * (q / P) + lo;
+}
+
 constexpr int FP8_RPW = 2;  // intermediate rows per wave (4 weight rows: gate and up of each)
 
 // The block scale of the 16 columns [c, c + 16) of row `row` in a matrix of `cols` columns:
@@ -91,7 +109,8 @@ __device__ __forceinline__ float fp8_scale_value(uint32_t raw) {
     return e8m0_value(raw);
 }
 
-// grid: (I / (4 * FP8_RPW), pairs). CPL = ceil(H / 1024) chunks of 16 bytes per lane per row;
+// grid: (I / (4 * FP8_RPW), pairs), one 1-D grid of as many blocks with several tokens
+// (block_order). CPL = ceil(H / 1024) chunks of 16 bytes per lane per row;
 // SF the scale format.
 template <int CPL, int SF>
 __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __restrict__ x, int tokens, int k,
@@ -101,21 +120,22 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
   constexpr int ROWS = 2 * FP8_RPW;
   __shared__ float sums[4][ROWS];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int p = blockIdx.y;
   const int H = routed.hidden, I = routed.inter;
+  int bx, p;
+  block_order(I / (4 * FP8_RPW), tokens * k + (has_shared ? tokens : 0), tokens > 1, bx, p);
   int t;
   Fp8Regions r;
   bool is_shared;
   if (!fp8_pair(p, tokens, k, indices, routed, has_shared != 0, shared, t, r, is_shared)) {
     // unknown or non-resident expert: its act rows are zero and the down kernels skip the pair
-    for (int i = blockIdx.x * 4 * FP8_RPW + threadIdx.x; i < (int)(blockIdx.x + 1) * 4 * FP8_RPW; i += 256)
+    for (int i = bx * 4 * FP8_RPW + threadIdx.x; i < (bx + 1) * 4 * FP8_RPW; i += 256)
       act[(int64_t)p * I + i] = 0;
     return;
   }
   const wm_fp8_experts& tab = is_shared ? shared : routed;
   const int up_first = tab.up_first;
   const float limit = tab.swiglu_limit;
-  const int i_base = blockIdx.x * 4 * FP8_RPW + wave * FP8_RPW;
+  const int i_base = bx * 4 * FP8_RPW + wave * FP8_RPW;
 
   // Every load is issued unconditionally (lanes past a row's end read its first chunk) and
   // masked where it is used, through the chunk's scale: a load under a condition makes the
@@ -181,7 +201,8 @@ __global__ void __launch_bounds__(256) fp8_gate_up_act_kernel(const uint16_t* __
 
 constexpr int FP8_OPW = 8;  // output rows per wave step
 
-// grid: combine (H / FP8_OPW, tokens); per pair (H / (4 * FP8_OPW), pairs). CPL = ceil(I / 1024).
+// grid: combine (H / FP8_OPW, tokens), one 1-D grid of as many blocks with several tokens
+// (block_order); per pair (H / (4 * FP8_OPW), pairs). CPL = ceil(I / 1024).
 template <int CPL, int SF, bool COMBINE>
 __global__ void __launch_bounds__(256) fp8_down_kernel(const uint16_t* __restrict__ act, int tokens, int k,
                                                        const int32_t* __restrict__ indices,
@@ -196,8 +217,9 @@ __global__ void __launch_bounds__(256) fp8_down_kernel(const uint16_t* __restric
   const int H = routed.hidden, I = routed.inter;
   int t, o_base, first, step, n_entries;
   if (COMBINE) {
-    t = blockIdx.y;
-    o_base = blockIdx.x * FP8_OPW;
+    int bx;
+    block_order(H / FP8_OPW, tokens, tokens > 1, bx, t);
+    o_base = bx * FP8_OPW;
     n_entries = k + (has_shared ? 1 : 0);
     first = wave;
     step = 4;
@@ -322,7 +344,7 @@ static void launch_decode_fp8(const uint16_t* x, int tokens, const int32_t* indi
   const int H = routed.hidden, I = routed.inter;
   const int pairs = tokens * k + (shared ? tokens : 0);
   const wm_fp8_experts sh = shared ? *shared : routed;
-  const dim3 g1(I / (4 * FP8_RPW), pairs);
+  const dim3 g1 = tokens > 1 ? dim3(I / (4 * FP8_RPW) * pairs) : dim3(I / (4 * FP8_RPW), pairs);
   switch ((H + 1023) / 1024) {
 #define WM_F8GU(C) case C: hipLaunchKernelGGL((fp8_gate_up_act_kernel<C, SF>), g1, dim3(256), 0, s, x, tokens, k, \
                                               indices, routed, sh, shared ? 1 : 0, act); break;
@@ -331,7 +353,7 @@ static void launch_decode_fp8(const uint16_t* x, int tokens, const int32_t* indi
   }
   check_launch("fp8_gate_up_act");
   if (combine) {
-    const dim3 g2(H / FP8_OPW, tokens);
+    const dim3 g2 = tokens > 1 ? dim3(H / FP8_OPW * tokens) : dim3(H / FP8_OPW, tokens);
     switch ((I + 1023) / 1024) {
 #define WM_F8DN(C) case C: hipLaunchKernelGGL((fp8_down_kernel<C, SF, true>), g2, dim3(256), 0, s, act, tokens, k, \
                                               indices, weights, routed, sh, shared ? 1 : 0, x, shared_gate, y); break;
