@@ -1025,21 +1025,23 @@ __device__ __forceinline__ void persistent_tiles(const TileRange& tr, int steps,
       else if (t == 2)
         issue(nxt, deep, deep ? sl_d : sl_s, deep ? ks_d : ks_s, h);
     };
-    // Rings of equal depth (the shallower one is then the weight ring): the weight halves at
-    // the top of the step, the split-row halves after MFMA groups 0 and 1. Otherwise the
-    // shallower ring's halves after groups 0 and 1 and the deeper ring's after groups 2 and
-    // 3, so the deeper ring's loads are the last ones the ring wait leaves in flight.
-    constexpr bool EQUAL = DA == DB;
+    // Rings of equal depth (the shallower one is then the weight ring): one operand's halves
+    // at the top of the step and the other's after MFMA groups 0 and 1; FP8 weights (32 KB a
+    // step) go first, and with MXFP4 weights (16 KB and their scales) the split rows do.
+    // Otherwise the shallower ring's halves after groups 0 and 1 and the deeper ring's after
+    // groups 2 and 3, so the deeper ring's loads are the last ones the ring wait leaves in
+    // flight.
+    constexpr bool EQUAL = DA == DB, SPLIT_FIRST = !F::FP8;
     auto load_part = [&](int p) {
       if (EQUAL && cur_ok) {
-        if (p < 2) part(true, p);
+        if (p < 2) part(!SPLIT_FIRST, p);
       } else {
         part(p >= 2, p & 1);
       }
     };
     if (EQUAL && cur_ok) {
-      part(false, 0);
-      part(false, 1);
+      part(SPLIT_FIRST, 0);
+      part(SPLIT_FIRST, 1);
     }
     if (cur_ok) {
       mfma(cur, wslot(g % DA), rslot(g % DB), k, load_part);
