@@ -89,27 +89,29 @@ class MXFP4Experts:
         return self.gate_up.shape[0] if self.gate_up.dim() == 3 else 1
 
     def c_struct(self) -> MXFP4ExpertsC:
-        def stride(t: torch.Tensor) -> int:
-            return t.stride(0) * t.element_size() if t.dim() == 3 else 0
-
-        for name, t, dt in (("gate_up", self.gate_up, torch.int32), ("down", self.down, torch.int32)):
-            if t.dtype not in (torch.int32, torch.uint32):
+        # each region's shape and strides read once (this runs on every call of the
+        # resident-expert path)
+        regions = (self.gate_up, self.gate_up_scales, self.down, self.down_scales)
+        shapes = [t.shape for t in regions]
+        strides = [t.stride() for t in regions]
+        for name, t, shape, st in zip(("gate_up", "gate_up_scales", "down", "down_scales"), regions, shapes, strides):
+            if name.endswith("scales"):
+                if t.dtype != torch.uint8:
+                    raise ValueError(f"{name} must be uint8")
+            elif t.dtype not in (torch.int32, torch.uint32):
                 raise ValueError(f"{name} must hold 32-bit words, got {t.dtype}")
-            if t.stride(-1) != 1 or t.stride(-2) != t.shape[-1]:
+            if st[-1] != 1 or st[-2] != shape[-1]:
                 raise ValueError(f"{name} rows must be contiguous")
-        for name, t in (("gate_up_scales", self.gate_up_scales), ("down_scales", self.down_scales)):
-            if t.dtype != torch.uint8:
-                raise ValueError(f"{name} must be uint8")
-            if t.stride(-1) != 1 or t.stride(-2) != t.shape[-1]:
-                raise ValueError(f"{name} rows must be contiguous")
-        H, I = self.hidden, self.inter
-        if self.down.shape[-2:] != (H, I // 8) or self.gate_up_scales.shape[-2:] != (2 * I, H // 32) \
-                or self.down_scales.shape[-2:] != (H, I // 32):
+        H, I = shapes[0][-1] * 8, shapes[0][-2] // 2
+        if shapes[2][-2:] != (H, I // 8) or shapes[1][-2:] != (2 * I, H // 32) or shapes[3][-2:] != (H, I // 32):
             raise ValueError("expert region shapes do not agree")
+        # bytes between experts: a leading expert axis, or none for a single expert
+        step = [st[0] * (4 if i % 2 == 0 else 1) if len(st) == 3 else 0 for i, st in enumerate(strides)]
+        count = self.experts if self.experts is not None else (shapes[0][0] if len(shapes[0]) == 3 else 1)
         return MXFP4ExpertsC(
-            self.gate_up.data_ptr(), self.gate_up_scales.data_ptr(), self.down.data_ptr(), self.down_scales.data_ptr(),
-            stride(self.gate_up), stride(self.gate_up_scales), stride(self.down), stride(self.down_scales),
-            0 if self.slots is None else self.slots.data_ptr(), self.count, H, I, int(self.up_first),
+            regions[0].data_ptr(), regions[1].data_ptr(), regions[2].data_ptr(), regions[3].data_ptr(),
+            step[0], step[1], step[2], step[3],
+            0 if self.slots is None else self.slots.data_ptr(), count, H, I, int(self.up_first),
             float(self.swiglu_limit), int(self.tiled), _act_terms(self.act_terms))
 
     def tensors(self):
